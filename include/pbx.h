@@ -1,0 +1,160 @@
+/*
+ * pbx.h -- C ABI of the MI355X (gfx950) backend for PureBee's quantized
+ * matmul / matvec instruction.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, and
+ * returns an int status (PBX_OK == 0, negative PBX_E* on failure).  The
+ * message for the last failure is returned by pbx_last_error(ctx)
+ * (pbx_last_error(NULL) for failures that happen before a context exists).
+ * Arguments are validated on the host before any HIP call, so every error
+ * path can be exercised without a GPU.
+ *
+ * Weight orientation is GGUF's: a weight is N rows (output features) of K
+ * columns (input features), row n holding K/32 consecutive blocks
+ * (gguf.js:36-49; streaming-loader.js:257-259 reads N = dims[1], K = dims[0]).
+ *
+ * The reference interface each entry point replaces is cited beside it
+ * (file:line in sammcj/purebee).  The reference is JavaScript: its "ABI" is
+ * the JS module surface of wasm-q4.js, engine.js and purebee.js, which the
+ * N-API addon (purebee_amd/napi) and the JS modules (purebee_amd/js) expose
+ * on top of this header.
+ */
+#ifndef PBX_H
+#define PBX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------- */
+#define PBX_OK        0
+#define PBX_EINVAL   -1   /* bad argument (shape, size, null pointer, type) */
+#define PBX_ENODEV   -2   /* no HIP device / device index out of range      */
+#define PBX_ENOMEM   -3   /* device or pinned host allocation failed         */
+#define PBX_EHIP     -4   /* a HIP runtime call failed                       */
+#define PBX_ENOTSUP  -5   /* shape or type not supported by any kernel       */
+#define PBX_ELOAD    -6   /* code object missing or not loadable (hipModuleLoad) */
+
+/* ---- weight types ----------------------------------------------------
+ * GGML numbering, as gguf.js:30-33 (GGML_TYPE).  PBX_TYPE_Q8_REF is the
+ * reference's own in-memory Q8 tensor (quantize.js:30-50, QuantizedTensor
+ * 'q8_0'): int8 values of a [K,N] matrix laid out flat, one f32 scale per
+ * 32 consecutive flat elements, consumed by matmul_q8 (quantize.js:224-266).
+ */
+#define PBX_TYPE_F32     0
+#define PBX_TYPE_Q4_0    2
+#define PBX_TYPE_Q8_0    8
+#define PBX_TYPE_Q8_REF  100
+
+typedef struct pbx_ctx pbx_ctx;
+typedef struct pbx_weight pbx_weight;
+
+/* ---- context ----------------------------------------------------------
+ * Replaces wasmQ4.init() (wasm-q4.js:647-668) / engine.initWasm()
+ * (engine.js:28-31): selects the device, creates the context's stream and
+ * loads the gfx950 code object with hipModuleLoad.  A context is used from
+ * one host thread at a time (the reference calls everything from the main
+ * JS thread, thread-pool.js:3-7).
+ */
+int         pbx_init(int device, pbx_ctx **out);
+void        pbx_shutdown(pbx_ctx *ctx);
+const char *pbx_last_error(const pbx_ctx *ctx);
+/* Device name (NUL-terminated, truncated to cap) and compute-unit count. */
+int         pbx_device_info(pbx_ctx *ctx, char *name, size_t cap, int *cu_count);
+
+/* ---- resident weights ------------------------------------------------
+ * Replaces the per-call copy of the raw block bytes into WASM memory
+ * (wasm-q4.js:735-738) and wasmSimd.allocWeights / engine.cacheWeight
+ * (wasm-simd.js:406-414, engine.js:39-42): the bytes are copied to the GPU
+ * once through pinned staging buffers and repacked there into the layout
+ * the kernels read; the handle stays valid until pbx_weight_free.
+ *
+ * host/nbytes hold GGUF row-major blocks: N rows of K/32 blocks of
+ * 18 B (Q4_0: fp16 d + 16 nibble bytes) or 34 B (Q8_0: fp16 d + 32 int8),
+ * gguf.js:36-49 and 239-286; for PBX_TYPE_F32, N*K little-endian floats.
+ * K must be a multiple of 32 for every type.
+ */
+int pbx_weight_upload(pbx_ctx *ctx, int type, int64_t N, int64_t K,
+                      const void *host, size_t nbytes, pbx_weight **out);
+/* The reference's QuantizedTensor 'q8_0' of shape [K,N] (quantize.js:30-50):
+ * q = K*N int8 values, scales = ceil(K*N/32) f32 values. */
+int pbx_weight_upload_q8ref(pbx_ctx *ctx, int64_t K, int64_t N,
+                            const int8_t *q, const float *scales,
+                            int64_t n_scales, pbx_weight **out);
+/* Replaces wasmSimd.resetWeights (wasm-simd.js:511-513) / PureBee.FREE
+ * (purebee.js:200-202) for a resident weight. */
+int pbx_weight_free(pbx_ctx *ctx, pbx_weight *w);
+int pbx_weight_info(const pbx_weight *w, int *type, int64_t *N, int64_t *K,
+                    size_t *device_bytes);
+
+/* ---- the instruction -------------------------------------------------
+ * Y[M,N] = X[M,K] . W^T (+ bias[N]), fp32 in and out.
+ *   M == 1   -> fused unpack/dequant/dot GEMV (one wavefront per row group)
+ *   M >= 2   -> dequant -> LDS -> fp16 MFMA GEMM (quantized types)
+ * Replaces, with the same arithmetic meaning:
+ *   wasmQ4.q4_0_matvec(x, rawBuf, N, K)           wasm-q4.js:716-747
+ *   quantizedMatvec(x, rawBuf, type, N, K)        llama-streaming.js:168-177
+ *   AtomicsThreadPool.matvec(...)                 thread-pool.js:165-246
+ *   wasmQ4.lmHead(hidden, emb, vocab, dim) (F32)  wasm-q4.js:798-839
+ *   engine.tensorMulAdd(x, W, b)  (F32)           engine.js:180-244
+ *   engine.tensorMulAddQ8(x, Wq, b) (Q8_REF)      engine.js:259-269,
+ *                                                 quantize.js:224-266
+ * pbx_linear takes host pointers and blocks until Y is written (the
+ * reference's synchronous convention, wasm-q4.js:744-746).  pbx_linear_dev
+ * takes device pointers and only enqueues on the context's stream.
+ * bias may be NULL.
+ */
+int pbx_linear(pbx_ctx *ctx, const pbx_weight *W, const float *X, int64_t M,
+               const float *bias, float *Y);
+int pbx_linear_dev(pbx_ctx *ctx, const pbx_weight *W, const float *dX,
+                   int64_t M, const float *dBias, float *dY);
+
+/* Exact dequantisation of a resident weight to fp32, row-major [N,K]
+ * (for PBX_TYPE_Q8_REF: [K,N], the reference's own orientation).
+ * Replaces loadTensorData's Q4_0/Q8_0 branches (gguf.js:239-286) and
+ * dequantize_q8 (quantize.js:170-181).  Bit-exact by construction. */
+int pbx_dequant(pbx_ctx *ctx, const pbx_weight *W, float *Y);
+int pbx_dequant_dev(pbx_ctx *ctx, const pbx_weight *W, float *dY);
+
+/* ---- host-side quantisers (CPU) ---------------------------------------
+ * Q8_0 with the numerics of quantize_q8 (quantize.js:79-109: absmax/127,
+ * ECMAScript Math.round of x*127/absmax in double) applied per 32-block
+ * along K of each row, the scale stored as fp16 (GGUF Q8_0 layout).
+ * Q4_0 with d = absmax/8 stored as fp16 and nibble = clamp(round(x*8/absmax),
+ * -8, 7) + 8, GGUF non-interleaved nibble order (gguf.js:259-286).
+ * out must hold N*K/32*34 (Q8_0) or N*K/32*18 (Q4_0) bytes. */
+int pbx_quantize_q8_0(const float *w, int64_t N, int64_t K, uint8_t *out);
+int pbx_quantize_q4_0(const float *w, int64_t N, int64_t K, uint8_t *out);
+/* quantize_q8 itself (quantize.js:79-109): flat, f32 scales (Q8_REF). */
+int pbx_quantize_q8_ref(const float *w, int64_t n, int8_t *q, float *scales);
+
+/* Seeded synthetic data: element i of the stream is a pure function of
+ * (seed, i): SplitMix64 -> Box-Muller in double -> mean + std*z as float. */
+int pbx_synth_normal(uint64_t seed, int64_t n, double mean, double std,
+                     float *out);
+
+/* ---- device memory, streams, timing (for callers on device pointers) -- */
+int pbx_dev_alloc(pbx_ctx *ctx, size_t bytes, void **out);
+int pbx_dev_free(pbx_ctx *ctx, void *p);
+int pbx_memcpy_h2d(pbx_ctx *ctx, void *dst, const void *src, size_t bytes);
+int pbx_memcpy_d2h(pbx_ctx *ctx, void *dst, const void *src, size_t bytes);
+int pbx_memset_dev(pbx_ctx *ctx, void *dst, int value, size_t bytes);
+int pbx_sync(pbx_ctx *ctx);
+/* HIP events recorded on the context's stream: the kernels' own stream. */
+int pbx_timer_start(pbx_ctx *ctx);
+int pbx_timer_stop(pbx_ctx *ctx, double *elapsed_ms);
+/* Enqueue `reps` passes over n_ops (W[i], dX[i] -> dY[i]) linears at row
+ * count M and return the elapsed time between HIP events recorded on the
+ * context's stream around the whole sequence. */
+int pbx_bench_linear(pbx_ctx *ctx, int n_ops, const pbx_weight *const *W,
+                     const float *const *dX, float *const *dY, int64_t M,
+                     int reps, double *elapsed_ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PBX_H */

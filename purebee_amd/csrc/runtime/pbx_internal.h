@@ -1,0 +1,91 @@
+// pbx_internal.h -- shared definitions of the runtime's translation units.
+#ifndef PBX_INTERNAL_H
+#define PBX_INTERNAL_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "pbx.h"
+
+// Kernels of pbx_kernels.hsaco, looked up by name at pbx_init.
+#define PBX_KERNEL_LIST(X)                                   \
+  X(PBX_K_REPACK_Q4_0, "pbx_repack_q4_0")                    \
+  X(PBX_K_REPACK_Q8_0, "pbx_repack_q8_0")                    \
+  X(PBX_K_DEQUANT_Q4_0, "pbx_dequant_q4_0")                  \
+  X(PBX_K_DEQUANT_Q8_0, "pbx_dequant_q8_0")                  \
+  X(PBX_K_DEQUANT_Q8REF, "pbx_dequant_q8ref")                \
+  X(PBX_K_GEMV_Q4_0_WIDE_R4, "pbx_gemv_q4_0_wide_r4")        \
+  X(PBX_K_GEMV_Q4_0_WIDE_R8, "pbx_gemv_q4_0_wide_r8")        \
+  X(PBX_K_GEMV_Q4_0_WIDE_R16, "pbx_gemv_q4_0_wide_r16")      \
+  X(PBX_K_GEMV_Q8_0_WIDE_R4, "pbx_gemv_q8_0_wide_r4")        \
+  X(PBX_K_GEMV_Q8_0_WIDE_R8, "pbx_gemv_q8_0_wide_r8")        \
+  X(PBX_K_GEMV_F32_WIDE_R2, "pbx_gemv_f32_wide_r2")          \
+  X(PBX_K_GEMV_F32_WIDE_R4, "pbx_gemv_f32_wide_r4")          \
+  X(PBX_K_GEMV_Q4_0_SMALL, "pbx_gemv_q4_0_small")            \
+  X(PBX_K_GEMV_Q8_0_SMALL, "pbx_gemv_q8_0_small")            \
+  X(PBX_K_GEMV_F32_SMALL, "pbx_gemv_f32_small")              \
+  X(PBX_K_GEMV_Q8REF, "pbx_gemv_q8ref")
+
+enum {
+#define X(id, name) id,
+  PBX_KERNEL_LIST(X)
+#undef X
+  PBX_K_COUNT
+};
+
+// Row count from which quantized linears take the MFMA GEMM path.
+#define PBX_GEMM_MIN_M (1 << 30)
+
+#define PBX_MAX_MODULES 8
+
+#define PBX_WEIGHT_MAGIC 0x50425857u  // "PBXW"
+
+struct pbx_ctx {
+  int device = 0;
+  int cu_count = 256;
+  char name[256] = {0};
+  std::string code_object;
+  std::string err;
+  hipModule_t modules[PBX_MAX_MODULES] = {};
+  hipFunction_t fn[PBX_K_COUNT] = {};
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  hipEvent_t ev_stage[2] = {nullptr, nullptr};
+  // grow-only scratch
+  void *d_x = nullptr, *d_y = nullptr, *d_b = nullptr;
+  size_t d_x_cap = 0, d_y_cap = 0, d_b_cap = 0;
+  void *d_stage[2] = {nullptr, nullptr};
+  size_t d_stage_cap[2] = {0, 0};
+  void *h_io = nullptr;
+  size_t h_io_cap = 0;
+  void *h_stage[2] = {nullptr, nullptr};
+  size_t h_stage_cap[2] = {0, 0};
+  void *models = nullptr;  // decode-step models owned by this context
+};
+
+struct pbx_weight {
+  uint32_t magic = 0;
+  int type = 0;
+  int64_t N = 0, K = 0, B = 0, Npad = 0;
+  int64_t n_scales = 0;
+  void *qs = nullptr;  // nibble / int8 / f32 plane (Q8_REF: flat int8 [K,N])
+  void *d = nullptr;   // fp16 scale plane (Q8_REF: f32 scales)
+  size_t bytes = 0;
+};
+
+int pbx_fail(pbx_ctx *c, int code, const char *fmt, ...)
+    __attribute__((format(printf, 3, 4)));
+int pbx_launch(pbx_ctx *c, int kernel, dim3 grid, dim3 block, void **args,
+               hipStream_t stream = nullptr);
+int pbx_ensure_dev(pbx_ctx *c, void **p, size_t *cap, size_t need);
+int pbx_ensure_pinned(pbx_ctx *c, void **p, size_t *cap, size_t need);
+int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
+                       const float *dBias, float *dY, hipStream_t stream);
+int pbx_gemm_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
+                     const float *dBias, float *dY, hipStream_t stream);
+size_t pbx_type_block_bytes(int type);
+void pbx_model_release_all(pbx_ctx *c);
+
+#endif

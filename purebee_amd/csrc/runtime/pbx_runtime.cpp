@@ -1,0 +1,646 @@
+// pbx_runtime.cpp -- host side of the C ABI declared in include/pbx.h.
+//
+// Owns the HIP device context, the context's stream, the gfx950 code object
+// (loaded with hipModuleLoad, kernels launched with hipModuleLaunchKernel),
+// resident weights and the launch heuristics.  No torch, no CUDA shims: the
+// only dependency is the HIP runtime.
+
+#include "pbx_internal.h"
+
+#include <dlfcn.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+
+static thread_local std::string g_err;  // failures before a context exists
+
+int pbx_fail(pbx_ctx *c, int code, const char *fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (c) c->err = buf;
+  g_err = buf;
+  return code;
+}
+
+#define HIPCHK(ctx, call)                                                        \
+  do {                                                                           \
+    hipError_t e_ = (call);                                                      \
+    if (e_ != hipSuccess)                                                        \
+      return pbx_fail((ctx), PBX_EHIP, "%s failed: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+
+extern "C" const char *pbx_last_error(const pbx_ctx *ctx) {
+  return ctx ? ctx->err.c_str() : g_err.c_str();
+}
+
+// ---------------------------------------------------------------------------
+// Kernel table.
+// ---------------------------------------------------------------------------
+static const char *const kKernelNames[PBX_K_COUNT] = {
+#define X(id, name) name,
+    PBX_KERNEL_LIST(X)
+#undef X
+};
+
+// Code objects built from purebee_amd/csrc/kernels/*.hip, found next to this
+// library (or in the directory named by PBX_KERNEL_DIR).
+static const char *const kModuleFiles[] = {"pbx_gemv.hsaco"};
+static const int kModuleCount = (int)(sizeof kModuleFiles / sizeof kModuleFiles[0]);
+
+static std::string code_object_dir() {
+  const char *env = getenv("PBX_KERNEL_DIR");
+  if (env && *env) return env;
+  Dl_info info;
+  if (dladdr((void *)&pbx_init, &info) && info.dli_fname) {
+    std::string p = info.dli_fname;
+    size_t slash = p.rfind('/');
+    return slash == std::string::npos ? "." : p.substr(0, slash);
+  }
+  return ".";
+}
+
+static void unload_modules(pbx_ctx *c) {
+  for (int i = 0; i < PBX_MAX_MODULES; ++i)
+    if (c->modules[i]) {
+      hipModuleUnload(c->modules[i]);
+      c->modules[i] = nullptr;
+    }
+}
+
+extern "C" int pbx_init(int device, pbx_ctx **out) {
+  if (!out) return pbx_fail(nullptr, PBX_EINVAL, "pbx_init: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0)
+    return pbx_fail(nullptr, PBX_ENODEV, "pbx_init: no HIP device (%s)",
+                    e == hipSuccess ? "device count is 0" : hipGetErrorString(e));
+  if (device < 0 || device >= n)
+    return pbx_fail(nullptr, PBX_ENODEV, "pbx_init: device %d out of range [0, %d)", device, n);
+  const std::string dir = code_object_dir();
+  for (int m = 0; m < kModuleCount; ++m) {
+    std::string path = dir + "/" + kModuleFiles[m];
+    FILE *f = fopen(path.c_str(), "rb");
+    if (!f)
+      return pbx_fail(nullptr, PBX_ELOAD, "pbx_init: code object '%s' not found (build it first)",
+                      path.c_str());
+    fclose(f);
+  }
+
+  pbx_ctx *c = new pbx_ctx();
+  c->device = device;
+  c->code_object = dir;
+  if (hipSetDevice(device) != hipSuccess) {
+    delete c;
+    return pbx_fail(nullptr, PBX_EHIP, "pbx_init: hipSetDevice(%d) failed", device);
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+    snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
+    c->cu_count = prop.multiProcessorCount;
+  }
+  for (int m = 0; m < kModuleCount; ++m) {
+    std::string path = dir + "/" + kModuleFiles[m];
+    e = hipModuleLoad(&c->modules[m], path.c_str());
+    if (e != hipSuccess) {
+      c->modules[m] = nullptr;
+      unload_modules(c);
+      delete c;
+      return pbx_fail(nullptr, PBX_ELOAD, "pbx_init: hipModuleLoad('%s') failed: %s "
+                      "(the code objects are built for gfx950)", path.c_str(), hipGetErrorString(e));
+    }
+  }
+  for (int i = 0; i < PBX_K_COUNT; ++i) {
+    c->fn[i] = nullptr;
+    for (int m = 0; m < kModuleCount && !c->fn[i]; ++m) {
+      hipFunction_t f = nullptr;
+      if (hipModuleGetFunction(&f, c->modules[m], kKernelNames[i]) == hipSuccess) c->fn[i] = f;
+    }
+    if (!c->fn[i]) {
+      unload_modules(c);
+      delete c;
+      return pbx_fail(nullptr, PBX_ELOAD, "pbx_init: kernel '%s' missing from the code objects in '%s'",
+                      kKernelNames[i], dir.c_str());
+    }
+  }
+  (void)hipGetLastError();  // lookups that missed in earlier modules are not errors
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess ||
+      hipEventCreate(&c->ev_stage[0]) != hipSuccess ||
+      hipEventCreate(&c->ev_stage[1]) != hipSuccess) {
+    unload_modules(c);
+    delete c;
+    return pbx_fail(nullptr, PBX_EHIP, "pbx_init: stream/event creation failed");
+  }
+  *out = c;
+  return PBX_OK;
+}
+
+extern "C" void pbx_shutdown(pbx_ctx *c) {
+  if (!c) return;
+  hipSetDevice(c->device);
+  hipStreamSynchronize(c->stream);
+  pbx_model_release_all(c);
+  for (void *p : {c->d_x, c->d_y, c->d_b, c->d_stage[0], c->d_stage[1]})
+    if (p) hipFree(p);
+  for (void *p : {c->h_io, c->h_stage[0], c->h_stage[1]})
+    if (p) hipHostFree(p);
+  hipEventDestroy(c->ev0);
+  hipEventDestroy(c->ev1);
+  hipEventDestroy(c->ev_stage[0]);
+  hipEventDestroy(c->ev_stage[1]);
+  hipStreamDestroy(c->stream);
+  unload_modules(c);
+  delete c;
+}
+
+extern "C" int pbx_device_info(pbx_ctx *c, char *name, size_t cap, int *cu_count) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_device_info: ctx is NULL");
+  if (name && cap) {
+    strncpy(name, c->name, cap - 1);
+    name[cap - 1] = 0;
+  }
+  if (cu_count) *cu_count = c->cu_count;
+  return PBX_OK;
+}
+
+int pbx_launch(pbx_ctx *c, int kernel, dim3 grid, dim3 block, void **args,
+               hipStream_t stream) {
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return PBX_OK;
+  hipError_t e = hipModuleLaunchKernel(c->fn[kernel], grid.x, grid.y, grid.z, block.x,
+                                       block.y, block.z, 0, stream ? stream : c->stream,
+                                       args, nullptr);
+  if (e != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "launch of %s failed: %s", kKernelNames[kernel],
+                    hipGetErrorString(e));
+  return PBX_OK;
+}
+
+// Grow-only scratch buffers owned by the context.
+int pbx_ensure_dev(pbx_ctx *c, void **p, size_t *cap, size_t need) {
+  if (*cap >= need) return PBX_OK;
+  if (*p) {
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+  }
+  size_t sz = std::max<size_t>(need, 1 << 16);
+  if (hipMalloc(p, sz) != hipSuccess) {
+    *p = nullptr;
+    return pbx_fail(c, PBX_ENOMEM, "hipMalloc(%zu) failed", sz);
+  }
+  *cap = sz;
+  return PBX_OK;
+}
+
+int pbx_ensure_pinned(pbx_ctx *c, void **p, size_t *cap, size_t need) {
+  if (*cap >= need) return PBX_OK;
+  if (*p) {
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    hipHostFree(*p);
+    *p = nullptr;
+    *cap = 0;
+  }
+  size_t sz = std::max<size_t>(need, 1 << 16);
+  if (hipHostMalloc(p, sz, hipHostMallocDefault) != hipSuccess) {
+    *p = nullptr;
+    return pbx_fail(c, PBX_ENOMEM, "hipHostMalloc(%zu) failed", sz);
+  }
+  *cap = sz;
+  return PBX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Upload: host bytes -> pinned staging (2 x 32 MiB, double buffered) ->
+// hipMemcpyAsync -> device staging -> optional repack kernel.
+// ---------------------------------------------------------------------------
+static const size_t kStageBytes = 32u << 20;
+
+// Copies `bytes` from host to device memory dst through the pinned ring.
+static int stage_copy(pbx_ctx *c, void *dst, const void *src, size_t bytes) {
+  for (int i = 0; i < 2; ++i) {
+    int rc = pbx_ensure_pinned(c, &c->h_stage[i], &c->h_stage_cap[i], kStageBytes);
+    if (rc) return rc;
+  }
+  size_t off = 0;
+  int slot = 0;
+  while (off < bytes) {
+    size_t n = std::min(kStageBytes, bytes - off);
+    HIPCHK(c, hipEventSynchronize(c->ev_stage[slot]));
+    memcpy(c->h_stage[slot], (const char *)src + off, n);
+    HIPCHK(c, hipMemcpyAsync((char *)dst + off, c->h_stage[slot], n, hipMemcpyHostToDevice,
+                             c->stream));
+    HIPCHK(c, hipEventRecord(c->ev_stage[slot], c->stream));
+    off += n;
+    slot ^= 1;
+  }
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return PBX_OK;
+}
+
+// Raw GGUF rows -> planes, chunk by chunk through device staging.
+static int stage_repack(pbx_ctx *c, pbx_weight *w, const uint8_t *src, int kernel,
+                        size_t row_bytes) {
+  for (int i = 0; i < 2; ++i) {
+    int rc = pbx_ensure_pinned(c, &c->h_stage[i], &c->h_stage_cap[i], kStageBytes);
+    if (rc) return rc;
+    rc = pbx_ensure_dev(c, &c->d_stage[i], &c->d_stage_cap[i], kStageBytes);
+    if (rc) return rc;
+  }
+  const int64_t rows_per_chunk = std::max<int64_t>(1, (int64_t)(kStageBytes / row_bytes));
+  if ((size_t)rows_per_chunk * row_bytes > kStageBytes)
+    return pbx_fail(c, PBX_ENOTSUP, "row of %zu bytes exceeds the staging buffer", row_bytes);
+  int slot = 0;
+  for (int64_t r0 = 0; r0 < w->N; r0 += rows_per_chunk) {
+    const int64_t rows = std::min(rows_per_chunk, w->N - r0);
+    const size_t n = (size_t)rows * row_bytes;
+    HIPCHK(c, hipEventSynchronize(c->ev_stage[slot]));
+    memcpy(c->h_stage[slot], src + (size_t)r0 * row_bytes, n);
+    HIPCHK(c, hipMemcpyAsync(c->d_stage[slot], c->h_stage[slot], n, hipMemcpyHostToDevice,
+                             c->stream));
+    int B = (int)w->B;
+    int64_t row0 = r0, nrows = rows;
+    void *raw = c->d_stage[slot];
+    void *args[] = {&raw, &w->qs, &w->d, &row0, &nrows, &B};
+    const int64_t blocks = rows * w->B;
+    int rc = pbx_launch(c, kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), args);
+    if (rc) return rc;
+    HIPCHK(c, hipEventRecord(c->ev_stage[slot], c->stream));
+    slot ^= 1;
+  }
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return PBX_OK;
+}
+
+size_t pbx_type_block_bytes(int type) {
+  switch (type) {
+    case PBX_TYPE_Q4_0: return 18;
+    case PBX_TYPE_Q8_0: return 34;
+    case PBX_TYPE_F32: return 128;
+    default: return 0;
+  }
+}
+
+static bool weight_ok(const pbx_weight *w) { return w && w->magic == PBX_WEIGHT_MAGIC; }
+
+extern "C" int pbx_weight_upload(pbx_ctx *c, int type, int64_t N, int64_t K,
+                                 const void *host, size_t nbytes, pbx_weight **out) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_weight_upload: ctx is NULL");
+  if (!out) return pbx_fail(c, PBX_EINVAL, "pbx_weight_upload: out is NULL");
+  *out = nullptr;
+  if (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0 && type != PBX_TYPE_F32)
+    return pbx_fail(c, PBX_EINVAL, "pbx_weight_upload: unsupported weight type %d", type);
+  if (N <= 0 || K <= 0 || K % 32 != 0)
+    return pbx_fail(c, PBX_EINVAL,
+                    "pbx_weight_upload: bad shape N=%lld K=%lld (need N>0, K>0, K%%32==0)",
+                    (long long)N, (long long)K);
+  if (N > INT32_MAX || K / 32 > (1 << 20))
+    return pbx_fail(c, PBX_ENOTSUP, "pbx_weight_upload: shape N=%lld K=%lld too large",
+                    (long long)N, (long long)K);
+  const int64_t B = K / 32;
+  const size_t row_bytes = (size_t)B * pbx_type_block_bytes(type);
+  const size_t need = (size_t)N * row_bytes;
+  if (!host) return pbx_fail(c, PBX_EINVAL, "pbx_weight_upload: host buffer is NULL");
+  if (nbytes < need)
+    return pbx_fail(c, PBX_EINVAL,
+                    "pbx_weight_upload: buffer holds %zu bytes, N=%lld x K=%lld needs %zu",
+                    nbytes, (long long)N, (long long)K, need);
+  HIPCHK(c, hipSetDevice(c->device));
+
+  pbx_weight *w = new pbx_weight();
+  w->magic = PBX_WEIGHT_MAGIC;
+  w->type = type;
+  w->N = N;
+  w->K = K;
+  w->B = B;
+  w->Npad = (N + 63) / 64 * 64;
+  size_t qs_bytes, d_bytes = 0;
+  if (type == PBX_TYPE_F32) {
+    qs_bytes = (size_t)w->Npad * K * 4;
+  } else {
+    qs_bytes = (size_t)w->Npad * B * (type == PBX_TYPE_Q4_0 ? 16 : 32);
+    d_bytes = (size_t)w->Npad * B * 2;
+  }
+  if (hipMalloc(&w->qs, qs_bytes) != hipSuccess) {
+    delete w;
+    return pbx_fail(c, PBX_ENOMEM, "pbx_weight_upload: hipMalloc(%zu) failed", qs_bytes);
+  }
+  if (d_bytes && hipMalloc(&w->d, d_bytes) != hipSuccess) {
+    hipFree(w->qs);
+    delete w;
+    return pbx_fail(c, PBX_ENOMEM, "pbx_weight_upload: hipMalloc(%zu) failed", d_bytes);
+  }
+  w->bytes = qs_bytes + d_bytes;
+  int rc = PBX_OK;
+  // Pad rows read as zero weights with zero scales.
+  if (hipMemsetAsync(w->qs, 0, qs_bytes, c->stream) != hipSuccess ||
+      (d_bytes && hipMemsetAsync(w->d, 0, d_bytes, c->stream) != hipSuccess))
+    rc = pbx_fail(c, PBX_EHIP, "pbx_weight_upload: hipMemsetAsync failed");
+  if (!rc) {
+    if (type == PBX_TYPE_F32)
+      rc = stage_copy(c, w->qs, host, need);
+    else
+      rc = stage_repack(c, w, (const uint8_t *)host,
+                        type == PBX_TYPE_Q4_0 ? PBX_K_REPACK_Q4_0 : PBX_K_REPACK_Q8_0, row_bytes);
+  }
+  if (rc) {
+    hipStreamSynchronize(c->stream);
+    hipFree(w->qs);
+    if (w->d) hipFree(w->d);
+    delete w;
+    return rc;
+  }
+  *out = w;
+  return PBX_OK;
+}
+
+extern "C" int pbx_weight_upload_q8ref(pbx_ctx *c, int64_t K, int64_t N, const int8_t *q,
+                                       const float *scales, int64_t n_scales,
+                                       pbx_weight **out) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_weight_upload_q8ref: ctx is NULL");
+  if (!out) return pbx_fail(c, PBX_EINVAL, "pbx_weight_upload_q8ref: out is NULL");
+  *out = nullptr;
+  if (K <= 0 || N <= 0 || !q || !scales)
+    return pbx_fail(c, PBX_EINVAL, "pbx_weight_upload_q8ref: bad arguments K=%lld N=%lld",
+                    (long long)K, (long long)N);
+  if (N > INT32_MAX || K > INT32_MAX)
+    return pbx_fail(c, PBX_ENOTSUP, "pbx_weight_upload_q8ref: shape too large");
+  const int64_t need_scales = (K * N + 31) / 32;
+  if (n_scales < need_scales)
+    return pbx_fail(c, PBX_EINVAL,
+                    "pbx_weight_upload_q8ref: %lld scales given, [%lld,%lld] needs %lld",
+                    (long long)n_scales, (long long)K, (long long)N, (long long)need_scales);
+  HIPCHK(c, hipSetDevice(c->device));
+  pbx_weight *w = new pbx_weight();
+  w->magic = PBX_WEIGHT_MAGIC;
+  w->type = PBX_TYPE_Q8_REF;
+  w->N = N;
+  w->K = K;
+  w->B = 0;
+  w->Npad = N;
+  w->n_scales = need_scales;
+  const size_t qb = (size_t)K * N, sb = (size_t)need_scales * 4;
+  if (hipMalloc(&w->qs, qb) != hipSuccess || hipMalloc(&w->d, sb) != hipSuccess) {
+    if (w->qs) hipFree(w->qs);
+    delete w;
+    return pbx_fail(c, PBX_ENOMEM, "pbx_weight_upload_q8ref: hipMalloc failed");
+  }
+  w->bytes = qb + sb;
+  int rc = stage_copy(c, w->qs, q, qb);
+  if (!rc) rc = stage_copy(c, w->d, scales, sb);
+  if (rc) {
+    hipFree(w->qs);
+    hipFree(w->d);
+    delete w;
+    return rc;
+  }
+  *out = w;
+  return PBX_OK;
+}
+
+extern "C" int pbx_weight_free(pbx_ctx *c, pbx_weight *w) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_weight_free: ctx is NULL");
+  if (!w) return PBX_OK;
+  if (!weight_ok(w)) return pbx_fail(c, PBX_EINVAL, "pbx_weight_free: not a live weight handle");
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  w->magic = 0;
+  if (w->qs) hipFree(w->qs);
+  if (w->d) hipFree(w->d);
+  delete w;
+  return PBX_OK;
+}
+
+extern "C" int pbx_weight_info(const pbx_weight *w, int *type, int64_t *N, int64_t *K,
+                               size_t *device_bytes) {
+  if (!weight_ok(w)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_weight_info: not a live weight handle");
+  if (type) *type = w->type;
+  if (N) *N = w->N;
+  if (K) *K = w->K;
+  if (device_bytes) *device_bytes = w->bytes;
+  return PBX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// The instruction.
+// ---------------------------------------------------------------------------
+int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
+                       const float *dBias, float *dY, hipStream_t stream) {
+  if (M > 65535) return pbx_fail(c, PBX_ENOTSUP, "pbx_linear: M=%lld > 65535", (long long)M);
+  int N = (int)w->N;
+  const unsigned gy = (unsigned)M;
+  if (w->type == PBX_TYPE_Q8_REF) {
+    int K = (int)w->K;
+    void *args[] = {(void *)&w->qs, (void *)&w->d, &dX, &dBias, &dY, &N, &K};
+    return pbx_launch(c, PBX_K_GEMV_Q8REF, dim3((unsigned)((N + 63) / 64), gy), dim3(512),
+                      args, stream);
+  }
+  if (M >= PBX_GEMM_MIN_M && w->type != PBX_TYPE_F32)
+    return pbx_gemm_enqueue(c, w, dX, M, dBias, dY, stream);
+  int B = (int)w->B;
+  void *args[] = {(void *)&w->qs, (void *)&w->d, &dX, &dBias, &dY, &N, &B};
+  if (B <= 32) {
+    // Small-K path: 4 waves per workgroup, each wave a tile of P*(64/B) rows.
+    const int P = w->type == PBX_TYPE_Q4_0 ? 8 : w->type == PBX_TYPE_Q8_0 ? 4 : 2;
+    const int T = P * (64 / B);
+    const int k = w->type == PBX_TYPE_Q4_0   ? PBX_K_GEMV_Q4_0_SMALL
+                  : w->type == PBX_TYPE_Q8_0 ? PBX_K_GEMV_Q8_0_SMALL
+                                             : PBX_K_GEMV_F32_SMALL;
+    return pbx_launch(c, k, dim3((unsigned)((N + 4 * T - 1) / (4 * T)), gy), dim3(256), args,
+                      stream);
+  }
+  const int W = (B + 63) / 64;
+  if (W > 8)
+    return pbx_fail(c, PBX_ENOTSUP, "pbx_linear: K=%lld exceeds the GEMV limit of 16384",
+                    (long long)w->K);
+  // Rows per tile: the largest tile that still gives >= 4 workgroups per CU.
+  const int target = std::max(4 * c->cu_count, 256);
+  int R, k;
+  if (w->type == PBX_TYPE_Q4_0) {
+    if (N / 16 >= target) { R = 16; k = PBX_K_GEMV_Q4_0_WIDE_R16; }
+    else if (N / 8 >= target) { R = 8; k = PBX_K_GEMV_Q4_0_WIDE_R8; }
+    else { R = 4; k = PBX_K_GEMV_Q4_0_WIDE_R4; }
+  } else if (w->type == PBX_TYPE_Q8_0) {
+    if (N / 8 >= target) { R = 8; k = PBX_K_GEMV_Q8_0_WIDE_R8; }
+    else { R = 4; k = PBX_K_GEMV_Q8_0_WIDE_R4; }
+  } else {
+    if (N / 4 >= target) { R = 4; k = PBX_K_GEMV_F32_WIDE_R4; }
+    else { R = 2; k = PBX_K_GEMV_F32_WIDE_R2; }
+  }
+  return pbx_launch(c, k, dim3((unsigned)((N + R - 1) / R), gy), dim3(64 * W), args, stream);
+}
+
+static int check_linear_args(pbx_ctx *c, const pbx_weight *w, const void *X, int64_t M,
+                             const void *Y, const char *who) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "%s: ctx is NULL", who);
+  if (!weight_ok(w)) return pbx_fail(c, PBX_EINVAL, "%s: not a live weight handle", who);
+  if (!X || !Y) return pbx_fail(c, PBX_EINVAL, "%s: X or Y is NULL", who);
+  if (M <= 0) return pbx_fail(c, PBX_EINVAL, "%s: M=%lld must be positive", who, (long long)M);
+  return PBX_OK;
+}
+
+extern "C" int pbx_linear_dev(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
+                              const float *dBias, float *dY) {
+  int rc = check_linear_args(c, w, dX, M, dY, "pbx_linear_dev");
+  if (rc) return rc;
+  HIPCHK(c, hipSetDevice(c->device));
+  return pbx_linear_enqueue(c, w, dX, M, dBias, dY, c->stream);
+}
+
+extern "C" int pbx_linear(pbx_ctx *c, const pbx_weight *w, const float *X, int64_t M,
+                          const float *bias, float *Y) {
+  int rc = check_linear_args(c, w, X, M, Y, "pbx_linear");
+  if (rc) return rc;
+  HIPCHK(c, hipSetDevice(c->device));
+  const size_t xb = (size_t)M * w->K * 4, yb = (size_t)M * w->N * 4;
+  const size_t bb = bias ? (size_t)w->N * 4 : 0;
+  if ((rc = pbx_ensure_dev(c, &c->d_x, &c->d_x_cap, xb))) return rc;
+  if ((rc = pbx_ensure_dev(c, &c->d_y, &c->d_y_cap, yb))) return rc;
+  if (bias && (rc = pbx_ensure_dev(c, &c->d_b, &c->d_b_cap, bb))) return rc;
+  if ((rc = pbx_ensure_pinned(c, &c->h_io, &c->h_io_cap, std::max(xb + bb, yb)))) return rc;
+  memcpy(c->h_io, X, xb);
+  if (bias) memcpy((char *)c->h_io + xb, bias, bb);
+  HIPCHK(c, hipMemcpyAsync(c->d_x, c->h_io, xb, hipMemcpyHostToDevice, c->stream));
+  if (bias)
+    HIPCHK(c, hipMemcpyAsync(c->d_b, (char *)c->h_io + xb, bb, hipMemcpyHostToDevice, c->stream));
+  if ((rc = pbx_linear_enqueue(c, w, (const float *)c->d_x, M,
+                               bias ? (const float *)c->d_b : nullptr, (float *)c->d_y,
+                               c->stream)))
+    return rc;
+  HIPCHK(c, hipMemcpyAsync(c->h_io, c->d_y, yb, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  memcpy(Y, c->h_io, yb);
+  return PBX_OK;
+}
+
+extern "C" int pbx_dequant_dev(pbx_ctx *c, const pbx_weight *w, float *dY) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_dequant_dev: ctx is NULL");
+  if (!weight_ok(w)) return pbx_fail(c, PBX_EINVAL, "pbx_dequant_dev: not a live weight handle");
+  if (!dY) return pbx_fail(c, PBX_EINVAL, "pbx_dequant_dev: output is NULL");
+  HIPCHK(c, hipSetDevice(c->device));
+  if (w->type == PBX_TYPE_F32) {
+    HIPCHK(c, hipMemcpyAsync(dY, w->qs, (size_t)w->N * w->K * 4, hipMemcpyDeviceToDevice,
+                             c->stream));
+    return PBX_OK;
+  }
+  if (w->type == PBX_TYPE_Q8_REF) {
+    int64_t n = w->N * w->K;
+    void *args[] = {(void *)&w->qs, (void *)&w->d, &dY, &n};
+    return pbx_launch(c, PBX_K_DEQUANT_Q8REF, dim3((unsigned)((n + 255) / 256)), dim3(256), args);
+  }
+  int N = (int)w->N, B = (int)w->B;
+  void *args[] = {(void *)&w->qs, (void *)&w->d, &dY, &N, &B};
+  const int64_t blocks = (int64_t)N * B;
+  return pbx_launch(c, w->type == PBX_TYPE_Q4_0 ? PBX_K_DEQUANT_Q4_0 : PBX_K_DEQUANT_Q8_0,
+                    dim3((unsigned)((blocks + 255) / 256)), dim3(256), args);
+}
+
+extern "C" int pbx_dequant(pbx_ctx *c, const pbx_weight *w, float *Y) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_dequant: ctx is NULL");
+  if (!weight_ok(w)) return pbx_fail(c, PBX_EINVAL, "pbx_dequant: not a live weight handle");
+  if (!Y) return pbx_fail(c, PBX_EINVAL, "pbx_dequant: output is NULL");
+  HIPCHK(c, hipSetDevice(c->device));
+  const size_t bytes = (size_t)w->N * w->K * 4;
+  void *d = nullptr;
+  if (hipMalloc(&d, bytes) != hipSuccess)
+    return pbx_fail(c, PBX_ENOMEM, "pbx_dequant: hipMalloc(%zu) failed", bytes);
+  int rc = pbx_dequant_dev(c, w, (float *)d);
+  if (!rc && hipMemcpyAsync(Y, d, bytes, hipMemcpyDeviceToHost, c->stream) != hipSuccess)
+    rc = pbx_fail(c, PBX_EHIP, "pbx_dequant: copy back failed");
+  if (!rc && hipStreamSynchronize(c->stream) != hipSuccess)
+    rc = pbx_fail(c, PBX_EHIP, "pbx_dequant: synchronize failed");
+  hipFree(d);
+  return rc;
+}
+
+// ---------------------------------------------------------------------------
+// Device memory, timing.
+// ---------------------------------------------------------------------------
+extern "C" int pbx_dev_alloc(pbx_ctx *c, size_t bytes, void **out) {
+  if (!c || !out) return pbx_fail(c, PBX_EINVAL, "pbx_dev_alloc: NULL argument");
+  *out = nullptr;
+  HIPCHK(c, hipSetDevice(c->device));
+  if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess) {
+    *out = nullptr;
+    return pbx_fail(c, PBX_ENOMEM, "pbx_dev_alloc: hipMalloc(%zu) failed", bytes);
+  }
+  return PBX_OK;
+}
+
+extern "C" int pbx_dev_free(pbx_ctx *c, void *p) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_dev_free: ctx is NULL");
+  if (!p) return PBX_OK;
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  HIPCHK(c, hipFree(p));
+  return PBX_OK;
+}
+
+extern "C" int pbx_memcpy_h2d(pbx_ctx *c, void *dst, const void *src, size_t bytes) {
+  if (!c || !dst || !src) return pbx_fail(c, PBX_EINVAL, "pbx_memcpy_h2d: NULL argument");
+  HIPCHK(c, hipSetDevice(c->device));
+  return stage_copy(c, dst, src, bytes);
+}
+
+extern "C" int pbx_memcpy_d2h(pbx_ctx *c, void *dst, const void *src, size_t bytes) {
+  if (!c || !dst || !src) return pbx_fail(c, PBX_EINVAL, "pbx_memcpy_d2h: NULL argument");
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  HIPCHK(c, hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return PBX_OK;
+}
+
+extern "C" int pbx_memset_dev(pbx_ctx *c, void *dst, int value, size_t bytes) {
+  if (!c || !dst) return pbx_fail(c, PBX_EINVAL, "pbx_memset_dev: NULL argument");
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipMemsetAsync(dst, value, bytes, c->stream));
+  return PBX_OK;
+}
+
+extern "C" int pbx_sync(pbx_ctx *c) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_sync: ctx is NULL");
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return PBX_OK;
+}
+
+extern "C" int pbx_timer_start(pbx_ctx *c) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_timer_start: ctx is NULL");
+  HIPCHK(c, hipEventRecord(c->ev0, c->stream));
+  return PBX_OK;
+}
+
+extern "C" int pbx_timer_stop(pbx_ctx *c, double *ms) {
+  if (!c || !ms) return pbx_fail(c, PBX_EINVAL, "pbx_timer_stop: NULL argument");
+  HIPCHK(c, hipEventRecord(c->ev1, c->stream));
+  HIPCHK(c, hipEventSynchronize(c->ev1));
+  float f = 0.f;
+  HIPCHK(c, hipEventElapsedTime(&f, c->ev0, c->ev1));
+  *ms = f;
+  return PBX_OK;
+}
+
+extern "C" int pbx_bench_linear(pbx_ctx *c, int n_ops, const pbx_weight *const *W,
+                                const float *const *dX, float *const *dY, int64_t M, int reps,
+                                double *ms) {
+  if (!c || !W || !dX || !dY || !ms || n_ops <= 0 || reps <= 0 || M <= 0)
+    return pbx_fail(c, PBX_EINVAL, "pbx_bench_linear: bad arguments");
+  for (int i = 0; i < n_ops; ++i)
+    if (!weight_ok(W[i]) || !dX[i] || !dY[i])
+      return pbx_fail(c, PBX_EINVAL, "pbx_bench_linear: bad operand %d", i);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipEventRecord(c->ev0, c->stream));
+  for (int r = 0; r < reps; ++r)
+    for (int i = 0; i < n_ops; ++i) {
+      int rc = pbx_linear_enqueue(c, W[i], dX[i], M, nullptr, dY[i], c->stream);
+      if (rc) return rc;
+    }
+  return pbx_timer_stop(c, ms);
+}

@@ -1,0 +1,294 @@
+// pbx_napi.cc -- N-API addon exposing the C ABI (include/pbx.h) to Node.js.
+//
+// Thin on purpose: typed-array backing stores are handed to the C ABI
+// directly (no copies on the JS side), every non-zero status becomes a thrown
+// Error carrying pbx_last_error(), and results come back as fresh
+// Float32Arrays, the synchronous convention of wasm-q4.js:744-746.
+// N-API is ABI-stable, so the same binary loads in any Node >= 10.
+#include <node_api.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "pbx.h"
+
+namespace {
+
+pbx_ctx *g_ctx = nullptr;
+
+struct WeightRef {
+  pbx_weight *w;
+  int type;
+  int64_t N, K;
+};
+
+napi_value throw_pbx(napi_env env, int rc, const char *who) {
+  char msg[1200];
+  snprintf(msg, sizeof msg, "%s: %s (status %d)", who, pbx_last_error(g_ctx), rc);
+  napi_throw_error(env, nullptr, msg);
+  return nullptr;
+}
+
+napi_value throw_msg(napi_env env, const char *msg) {
+  napi_throw_error(env, nullptr, msg);
+  return nullptr;
+}
+
+bool get_args(napi_env env, napi_callback_info info, size_t want, napi_value *argv,
+              size_t *got = nullptr) {
+  size_t argc = want;
+  if (napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr) != napi_ok) return false;
+  for (size_t i = argc; i < want; ++i) napi_get_undefined(env, &argv[i]);
+  if (got) *got = argc;
+  return true;
+}
+
+bool is_nullish(napi_env env, napi_value v) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  return t == napi_undefined || t == napi_null;
+}
+
+bool get_i64(napi_env env, napi_value v, int64_t *out) {
+  return napi_get_value_int64(env, v, out) == napi_ok;
+}
+
+// Any typed array (or Buffer): returns data pointer and byte length.
+bool typed_bytes(napi_env env, napi_value v, void **data, size_t *bytes,
+                 napi_typedarray_type *ty = nullptr) {
+  bool is = false;
+  napi_is_typedarray(env, v, &is);
+  if (!is) return false;
+  napi_typedarray_type t;
+  size_t len = 0, off = 0;
+  napi_value ab;
+  if (napi_get_typedarray_info(env, v, &t, &len, data, &ab, &off) != napi_ok) return false;
+  size_t el = 1;
+  switch (t) {
+    case napi_int16_array: case napi_uint16_array: el = 2; break;
+    case napi_int32_array: case napi_uint32_array: case napi_float32_array: el = 4; break;
+    case napi_float64_array: el = 8; break;
+    default: el = 1;
+  }
+  *bytes = len * el;
+  if (ty) *ty = t;
+  return true;
+}
+
+bool get_f32(napi_env env, napi_value v, float **data, size_t *count) {
+  void *p;
+  size_t b;
+  napi_typedarray_type t;
+  if (!typed_bytes(env, v, &p, &b, &t) || t != napi_float32_array) return false;
+  *data = (float *)p;
+  *count = b / 4;
+  return true;
+}
+
+napi_value new_f32(napi_env env, size_t count, float **data) {
+  napi_value ab, arr;
+  void *p = nullptr;
+  if (napi_create_arraybuffer(env, count * 4, &p, &ab) != napi_ok) return nullptr;
+  if (napi_create_typedarray(env, napi_float32_array, count, ab, 0, &arr) != napi_ok) return nullptr;
+  *data = (float *)p;
+  return arr;
+}
+
+void finalize_weight(napi_env env, void *data, void *hint) {
+  WeightRef *r = (WeightRef *)data;
+  if (r->w && g_ctx) pbx_weight_free(g_ctx, r->w);
+  delete r;
+}
+
+WeightRef *get_weight(napi_env env, napi_value v) {
+  void *p = nullptr;
+  if (napi_get_value_external(env, v, &p) != napi_ok || !p) return nullptr;
+  return (WeightRef *)p;
+}
+
+bool need_ctx(napi_env env) {
+  if (g_ctx) return true;
+  throw_msg(env, "purebee_amd: call init() first");
+  return false;
+}
+
+// init(device = 0) -> true
+napi_value Init(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  int64_t dev = 0;
+  if (!is_nullish(env, argv[0]) && !get_i64(env, argv[0], &dev))
+    return throw_msg(env, "init: device must be a number");
+  if (!g_ctx) {
+    int rc = pbx_init((int)dev, &g_ctx);
+    if (rc) {
+      g_ctx = nullptr;
+      return throw_pbx(env, rc, "init");
+    }
+  }
+  napi_value t;
+  napi_get_boolean(env, true, &t);
+  return t;
+}
+
+napi_value DeviceInfo(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  char name[256];
+  int cus = 0;
+  int rc = pbx_device_info(g_ctx, name, sizeof name, &cus);
+  if (rc) return throw_pbx(env, rc, "deviceInfo");
+  napi_value o, n, c;
+  napi_create_object(env, &o);
+  napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &n);
+  napi_create_int32(env, cus, &c);
+  napi_set_named_property(env, o, "name", n);
+  napi_set_named_property(env, o, "computeUnits", c);
+  return o;
+}
+
+napi_value make_handle(napi_env env, pbx_weight *w, int type, int64_t N, int64_t K) {
+  WeightRef *r = new WeightRef{w, type, N, K};
+  napi_value h;
+  if (napi_create_external(env, r, finalize_weight, nullptr, &h) != napi_ok) {
+    pbx_weight_free(g_ctx, w);
+    delete r;
+    return throw_msg(env, "upload: could not create handle");
+  }
+  return h;
+}
+
+// upload(type, N, K, bytes: TypedArray) -> handle
+napi_value Upload(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[4];
+  get_args(env, info, 4, argv);
+  int64_t type, N, K;
+  if (!get_i64(env, argv[0], &type) || !get_i64(env, argv[1], &N) || !get_i64(env, argv[2], &K))
+    return throw_msg(env, "upload(type, N, K, data): type, N and K must be numbers");
+  void *data;
+  size_t bytes;
+  if (!typed_bytes(env, argv[3], &data, &bytes))
+    return throw_msg(env, "upload(type, N, K, data): data must be a TypedArray or Buffer");
+  pbx_weight *w = nullptr;
+  int rc = pbx_weight_upload(g_ctx, (int)type, N, K, data, bytes, &w);
+  if (rc) return throw_pbx(env, rc, "upload");
+  return make_handle(env, w, (int)type, N, K);
+}
+
+// uploadQ8Ref(K, N, q: Int8Array, scales: Float32Array) -> handle
+napi_value UploadQ8Ref(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[4];
+  get_args(env, info, 4, argv);
+  int64_t K, N;
+  if (!get_i64(env, argv[0], &K) || !get_i64(env, argv[1], &N))
+    return throw_msg(env, "uploadQ8Ref(K, N, q, scales): K and N must be numbers");
+  void *q;
+  size_t qb;
+  float *s;
+  size_t ns;
+  if (!typed_bytes(env, argv[2], &q, &qb) || !get_f32(env, argv[3], &s, &ns))
+    return throw_msg(env, "uploadQ8Ref: q must be an Int8Array and scales a Float32Array");
+  if ((int64_t)qb < K * N) return throw_msg(env, "uploadQ8Ref: q shorter than K*N");
+  pbx_weight *w = nullptr;
+  int rc = pbx_weight_upload_q8ref(g_ctx, K, N, (const int8_t *)q, s, (int64_t)ns, &w);
+  if (rc) return throw_pbx(env, rc, "uploadQ8Ref");
+  return make_handle(env, w, PBX_TYPE_Q8_REF, N, K);
+}
+
+napi_value Free(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  WeightRef *r = get_weight(env, argv[0]);
+  if (!r) return throw_msg(env, "free: not a weight handle");
+  if (r->w) {
+    int rc = pbx_weight_free(g_ctx, r->w);
+    r->w = nullptr;
+    if (rc) return throw_pbx(env, rc, "free");
+  }
+  return nullptr;
+}
+
+// linear(handle, x: Float32Array [M*K], M = 1, bias: Float32Array|null) -> Float32Array [M*N]
+napi_value Linear(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[4];
+  get_args(env, info, 4, argv);
+  WeightRef *r = get_weight(env, argv[0]);
+  if (!r || !r->w) return throw_msg(env, "linear: not a live weight handle");
+  float *x;
+  size_t nx;
+  if (!get_f32(env, argv[1], &x, &nx)) return throw_msg(env, "linear: x must be a Float32Array");
+  int64_t M = 1;
+  if (!is_nullish(env, argv[2]) && !get_i64(env, argv[2], &M))
+    return throw_msg(env, "linear: M must be a number");
+  if (M <= 0 || (int64_t)nx < M * r->K) {
+    char msg[200];
+    snprintf(msg, sizeof msg, "linear: x holds %zu values, M=%lld x K=%lld needed", nx,
+             (long long)M, (long long)r->K);
+    return throw_msg(env, msg);
+  }
+  float *bias = nullptr;
+  size_t nb = 0;
+  if (!is_nullish(env, argv[3])) {
+    if (!get_f32(env, argv[3], &bias, &nb) || (int64_t)nb < r->N)
+      return throw_msg(env, "linear: bias must be a Float32Array of length N");
+  }
+  float *y;
+  napi_value out = new_f32(env, (size_t)(M * r->N), &y);
+  if (!out) return throw_msg(env, "linear: out of memory");
+  int rc = pbx_linear(g_ctx, r->w, x, M, bias, y);
+  if (rc) return throw_pbx(env, rc, "linear");
+  return out;
+}
+
+napi_value Dequant(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  WeightRef *r = get_weight(env, argv[0]);
+  if (!r || !r->w) return throw_msg(env, "dequant: not a live weight handle");
+  float *y;
+  napi_value out = new_f32(env, (size_t)(r->N * r->K), &y);
+  if (!out) return throw_msg(env, "dequant: out of memory");
+  int rc = pbx_dequant(g_ctx, r->w, y);
+  if (rc) return throw_pbx(env, rc, "dequant");
+  return out;
+}
+
+napi_value Info(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  WeightRef *r = get_weight(env, argv[0]);
+  if (!r) return throw_msg(env, "info: not a weight handle");
+  napi_value o, v;
+  napi_create_object(env, &o);
+  napi_create_int32(env, r->type, &v);
+  napi_set_named_property(env, o, "type", v);
+  napi_create_int64(env, r->N, &v);
+  napi_set_named_property(env, o, "N", v);
+  napi_create_int64(env, r->K, &v);
+  napi_set_named_property(env, o, "K", v);
+  napi_get_boolean(env, r->w != nullptr, &v);
+  napi_set_named_property(env, o, "live", v);
+  return o;
+}
+
+napi_value ModuleInit(napi_env env, napi_value exports) {
+  struct {
+    const char *name;
+    napi_callback cb;
+  } fns[] = {{"init", Init},     {"deviceInfo", DeviceInfo}, {"upload", Upload},
+             {"uploadQ8Ref", UploadQ8Ref}, {"free", Free},  {"linear", Linear},
+             {"dequant", Dequant}, {"info", Info}};
+  for (auto &f : fns) {
+    napi_value fn;
+    napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn);
+    napi_set_named_property(env, exports, f.name, fn);
+  }
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, ModuleInit)

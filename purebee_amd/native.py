@@ -1,0 +1,274 @@
+"""ctypes binding of the C ABI in include/pbx.h (lib/libpbhip.so).
+
+Raises PbxError (with the library's own message) for every non-zero status;
+there is no fallback path: without the built library nothing here works.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(PKG, "lib")
+
+TYPE_F32 = 0
+TYPE_Q4_0 = 2
+TYPE_Q8_0 = 8
+TYPE_Q8_REF = 100
+
+STATUS = {0: "PBX_OK", -1: "PBX_EINVAL", -2: "PBX_ENODEV", -3: "PBX_ENOMEM",
+          -4: "PBX_EHIP", -5: "PBX_ENOTSUP", -6: "PBX_ELOAD"}
+
+# Every entry point declared in include/pbx.h.
+EXPORTS = (
+    "pbx_init", "pbx_shutdown", "pbx_last_error", "pbx_device_info",
+    "pbx_weight_upload", "pbx_weight_upload_q8ref", "pbx_weight_free", "pbx_weight_info",
+    "pbx_linear", "pbx_linear_dev", "pbx_dequant", "pbx_dequant_dev",
+    "pbx_quantize_q8_0", "pbx_quantize_q4_0", "pbx_quantize_q8_ref", "pbx_synth_normal",
+    "pbx_dev_alloc", "pbx_dev_free", "pbx_memcpy_h2d", "pbx_memcpy_d2h", "pbx_memset_dev",
+    "pbx_sync", "pbx_timer_start", "pbx_timer_stop", "pbx_bench_linear",
+)
+
+
+class PbxError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"{STATUS.get(code, code)}: {msg}")
+        self.code = code
+
+
+def library_path():
+    return os.path.join(LIB_DIR, "libpbhip.so")
+
+
+_lib = None
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+
+
+def load_library():
+    """Load lib/libpbhip.so; raises if it was not built (no silent fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not os.path.exists(path):
+        raise PbxError(-6, f"{path} not built: run `python -m purebee_amd.build`")
+    L = ctypes.CDLL(path)
+    sig = {
+        "pbx_init": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_vp)]),
+        "pbx_shutdown": (None, [_vp]),
+        "pbx_last_error": (ctypes.c_char_p, [_vp]),
+        "pbx_device_info": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_size_t,
+                                           ctypes.POINTER(ctypes.c_int)]),
+        "pbx_weight_upload": (ctypes.c_int, [_vp, ctypes.c_int, _i64, _i64, _vp,
+                                             ctypes.c_size_t, ctypes.POINTER(_vp)]),
+        "pbx_weight_upload_q8ref": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _i64,
+                                                   ctypes.POINTER(_vp)]),
+        "pbx_weight_free": (ctypes.c_int, [_vp, _vp]),
+        "pbx_weight_info": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int),
+                                           ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                                           ctypes.POINTER(ctypes.c_size_t)]),
+        "pbx_linear": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
+        "pbx_linear_dev": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
+        "pbx_dequant": (ctypes.c_int, [_vp, _vp, _vp]),
+        "pbx_dequant_dev": (ctypes.c_int, [_vp, _vp, _vp]),
+        "pbx_quantize_q8_0": (ctypes.c_int, [_f32p, _i64, _i64, _u8p]),
+        "pbx_quantize_q4_0": (ctypes.c_int, [_f32p, _i64, _i64, _u8p]),
+        "pbx_quantize_q8_ref": (ctypes.c_int, [_f32p, _i64, _i8p, _f32p]),
+        "pbx_synth_normal": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_double,
+                                            ctypes.c_double, _f32p]),
+        "pbx_dev_alloc": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.POINTER(_vp)]),
+        "pbx_dev_free": (ctypes.c_int, [_vp, _vp]),
+        "pbx_memcpy_h2d": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_size_t]),
+        "pbx_memcpy_d2h": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_size_t]),
+        "pbx_memset_dev": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_size_t]),
+        "pbx_sync": (ctypes.c_int, [_vp]),
+        "pbx_timer_start": (ctypes.c_int, [_vp]),
+        "pbx_timer_stop": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_double)]),
+        "pbx_bench_linear": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.POINTER(_vp),
+                                            ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i64,
+                                            ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc, ctx_ptr=None):
+    if rc != 0:
+        msg = load_library().pbx_last_error(ctx_ptr)
+        raise PbxError(rc, msg.decode() if msg else "")
+
+
+def block_bytes(t):
+    return {TYPE_Q4_0: 18, TYPE_Q8_0: 34, TYPE_F32: 128}[t]
+
+
+def quantize_q8_0(w):
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    out = np.empty(N * (K // 32) * 34, np.uint8)
+    _check(load_library().pbx_quantize_q8_0(w, N, K, out))
+    return out
+
+
+def quantize_q4_0(w):
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    out = np.empty(N * (K // 32) * 18, np.uint8)
+    _check(load_library().pbx_quantize_q4_0(w, N, K, out))
+    return out
+
+
+def quantize_q8_ref(w):
+    w = np.ascontiguousarray(w, np.float32).ravel()
+    q = np.empty(w.size, np.int8)
+    s = np.empty((w.size + 31) // 32, np.float32)
+    _check(load_library().pbx_quantize_q8_ref(w, w.size, q, s))
+    return q, s
+
+
+def synth_normal(seed, n, mean=0.0, std=1.0):
+    out = np.empty(n, np.float32)
+    _check(load_library().pbx_synth_normal(seed, n, mean, std, out))
+    return out
+
+
+class DeviceBuffer:
+    def __init__(self, ctx, nbytes):
+        self.ctx = ctx
+        self.nbytes = nbytes
+        p = _vp()
+        ctx._call("pbx_dev_alloc", ctx._p, nbytes, ctypes.byref(p))
+        self.ptr = p.value
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        self.ctx._call("pbx_memcpy_h2d", self.ctx._p, self.ptr, arr.ctypes.data, arr.nbytes)
+        return self
+
+    def download(self, dtype, count):
+        out = np.empty(count, dtype)
+        assert out.nbytes <= self.nbytes
+        self.ctx._call("pbx_memcpy_d2h", self.ctx._p, out.ctypes.data, self.ptr, out.nbytes)
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.ctx._call("pbx_dev_free", self.ctx._p, self.ptr)
+            self.ptr = None
+
+
+class Weight:
+    def __init__(self, ctx, ptr, type_, N, K):
+        self.ctx, self.ptr, self.type, self.N, self.K = ctx, ptr, type_, N, K
+
+    @property
+    def device_bytes(self):
+        t, n, k, b = ctypes.c_int(), _i64(), _i64(), ctypes.c_size_t()
+        _check(load_library().pbx_weight_info(self.ptr, ctypes.byref(t), ctypes.byref(n),
+                                              ctypes.byref(k), ctypes.byref(b)))
+        return b.value
+
+    def free(self):
+        if self.ptr:
+            self.ctx._call("pbx_weight_free", self.ctx._p, self.ptr)
+            self.ptr = None
+
+
+class Context:
+    """One pbx_ctx: a device, its stream and the loaded code objects."""
+
+    def __init__(self, device=0):
+        L = load_library()
+        p = _vp()
+        _check(L.pbx_init(device, ctypes.byref(p)))
+        self._p = p.value
+        self.L = L
+
+    def _call(self, name, *args):
+        rc = getattr(self.L, name)(*args)
+        if rc != 0:
+            msg = self.L.pbx_last_error(self._p)
+            raise PbxError(rc, msg.decode() if msg else "")
+
+    def close(self):
+        if self._p:
+            self.L.pbx_shutdown(self._p)
+            self._p = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def device_info(self):
+        buf = ctypes.create_string_buffer(256)
+        cu = ctypes.c_int()
+        self._call("pbx_device_info", self._p, buf, 256, ctypes.byref(cu))
+        return buf.value.decode(), cu.value
+
+    def upload(self, type_, N, K, data):
+        data = np.ascontiguousarray(data)
+        w = _vp()
+        self._call("pbx_weight_upload", self._p, type_, N, K, data.ctypes.data, data.nbytes,
+                   ctypes.byref(w))
+        return Weight(self, w.value, type_, N, K)
+
+    def upload_q8ref(self, K, N, q, scales):
+        q = np.ascontiguousarray(q, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        w = _vp()
+        self._call("pbx_weight_upload_q8ref", self._p, K, N, q.ctypes.data, scales.ctypes.data,
+                   scales.size, ctypes.byref(w))
+        return Weight(self, w.value, TYPE_Q8_REF, N, K)
+
+    def linear(self, w, X, bias=None):
+        X = np.ascontiguousarray(X, np.float32)
+        M = 1 if X.ndim == 1 else X.shape[0]
+        assert X.size == M * w.K, (X.shape, w.K)
+        Y = np.empty((M, w.N), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self._call("pbx_linear", self._p, w.ptr, X.ctypes.data, M,
+                   None if b is None else b.ctypes.data, Y.ctypes.data)
+        return Y[0] if X.ndim == 1 else Y
+
+    def linear_dev(self, w, dX, M, dY, dBias=None):
+        self._call("pbx_linear_dev", self._p, w.ptr, dX, M, dBias, dY)
+
+    def dequant(self, w):
+        shape = (w.K, w.N) if w.type == TYPE_Q8_REF else (w.N, w.K)
+        out = np.empty(shape, np.float32)
+        self._call("pbx_dequant", self._p, w.ptr, out.ctypes.data)
+        return out
+
+    def alloc(self, nbytes):
+        return DeviceBuffer(self, nbytes)
+
+    def sync(self):
+        self._call("pbx_sync", self._p)
+
+    def timer_start(self):
+        self._call("pbx_timer_start", self._p)
+
+    def timer_stop(self):
+        ms = ctypes.c_double()
+        self._call("pbx_timer_stop", self._p, ctypes.byref(ms))
+        return ms.value
+
+    def bench_linear(self, weights, dXs, dYs, M, reps):
+        n = len(weights)
+        W = (_vp * n)(*[w.ptr for w in weights])
+        X = (_vp * n)(*dXs)
+        Y = (_vp * n)(*dYs)
+        ms = ctypes.c_double()
+        self._call("pbx_bench_linear", self._p, n, W, X, Y, M, reps, ctypes.byref(ms))
+        return ms.value

@@ -1,0 +1,182 @@
+"""GPU parity of the quantized matvec instruction through the C ABI.
+
+Bars (stated per test):
+  * dequantised weights: bit-exact against the oracle (gguf.js:239-286);
+  * matvec / matmul outputs: relative L2 <= 1e-3 against the oracle's
+    double-accumulated restatement (llama-streaming.js:72-104 for Q4_0).
+"""
+import numpy as np
+import pytest
+
+import oracle
+import purebee_amd as pb
+from tests.conftest import rel_l2, synth_matrix
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # relative L2, matvec outputs
+
+# (N, K) shapes of the configurations: Llama-3.2-1B, SmolLM2-135M, stories15M
+LLAMA1B = [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192)]
+SMOLLM2 = [(576, 576), (192, 576), (1536, 576), (576, 1536)]
+STORIES = [(288, 288), (768, 288), (288, 768)]
+EDGE = [(1, 32), (7, 64), (65, 96), (1000, 1056), (129, 2080), (3, 16384), (63, 4064)]
+
+
+def quantize(t, w):
+    return oracle.quantize_q4_0(w) if t == pb.TYPE_Q4_0 else oracle.quantize_q8_0(w)
+
+
+def dequant(t, raw, n):
+    return oracle.dequant_q4_0(raw, n) if t == pb.TYPE_Q4_0 else oracle.dequant_q8_0(raw, n)
+
+
+@pytest.mark.parametrize("t", [pb.TYPE_Q4_0, pb.TYPE_Q8_0])
+@pytest.mark.parametrize("N,K", LLAMA1B[:2] + SMOLLM2[:2] + STORIES[:2] + EDGE[:4])
+def test_dequant_bit_exact(ctx, t, N, K):
+    print(f"[case] dequant type={t} N={N} K={K}", flush=True)
+    raw = quantize(t, synth_matrix(100 + N + K, N, K))
+    w = ctx.upload(t, N, K, raw)
+    got = ctx.dequant(w)
+    ref = dequant(t, raw, N * K).reshape(N, K)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    w.free()
+
+
+def test_reference_q4_kat(ctx):
+    """wasm-q4.js:673-704 on the GPU path: [32, 128] within 0.1."""
+    print("[case] q4 KAT", flush=True)
+    raw = np.zeros(36, np.uint8)
+    raw[0:2] = [0x00, 0x3C]
+    raw[2:18] = 0x99
+    raw[18:20] = [0x00, 0x40]
+    raw[20:36] = 0xAA
+    w = ctx.upload(pb.TYPE_Q4_0, 2, 32, raw)
+    y = ctx.linear(w, np.ones(32, np.float32))
+    assert abs(y[0] - 32.0) < 0.1 and abs(y[1] - 128.0) < 0.1
+    assert y[0] == 32.0 and y[1] == 128.0
+    w.free()
+
+
+@pytest.mark.parametrize("t", [pb.TYPE_Q4_0, pb.TYPE_Q8_0])
+@pytest.mark.parametrize("N,K", LLAMA1B + SMOLLM2 + STORIES + EDGE)
+def test_matvec_parity(ctx, t, N, K):
+    print(f"[case] matvec type={t} N={N} K={K}", flush=True)
+    raw = quantize(t, synth_matrix(7 * N + K, N, K))
+    x = pb.synth_normal(N ^ K, K)
+    w = ctx.upload(t, N, K, raw)
+    y = ctx.linear(w, x)
+    ref = oracle.matvec(t, x, raw, N, K)
+    assert y.shape == (N,)
+    assert rel_l2(y, ref) <= TOL, rel_l2(y, ref)
+    # fp32 accumulation in a different order: in practice far below the bar
+    assert rel_l2(y, ref) < 1e-5
+    w.free()
+
+
+def test_lm_head_q4_0_llama(ctx):
+    """The tied 128256 x 2048 Q4_0 embedding as LM head (the largest GEMV)."""
+    N, K = 128256, 2048
+    print(f"[case] lm head q4_0 N={N} K={K}", flush=True)
+    raw = pb.quantize_q4_0(synth_matrix(4242, N, K))
+    x = pb.synth_normal(17, K)
+    w = ctx.upload(pb.TYPE_Q4_0, N, K, raw)
+    y = ctx.linear(w, x)
+    ref = oracle.q4_0_matvec_js(x, raw, N, K)
+    assert rel_l2(y, ref) <= TOL
+    assert int(np.argmax(y)) == int(np.argmax(ref))
+    w.free()
+
+
+@pytest.mark.parametrize("N,K", [(32000, 288), (49152, 576), (300, 2048), (5, 64)])
+def test_f32_matvec_lm_head(ctx, N, K):
+    """f32 weights: the reference LM head of llama.js:359-367 / batch_dot."""
+    print(f"[case] f32 matvec N={N} K={K}", flush=True)
+    W = synth_matrix(N + 3 * K, N, K)
+    x = pb.synth_normal(5, K)
+    w = ctx.upload(pb.TYPE_F32, N, K, W)
+    y = ctx.linear(w, x)
+    assert rel_l2(y, oracle.f32_matvec(x, W)) <= TOL
+    assert rel_l2(y, oracle.batch_dot_wasm(x, W)) < 1e-5
+    assert np.array_equal(ctx.dequant(w), W)
+    w.free()
+
+
+@pytest.mark.parametrize("t", [pb.TYPE_Q4_0, pb.TYPE_Q8_0, pb.TYPE_F32])
+def test_bias_and_multi_row(ctx, t):
+    N, K, M = 576, 576, 5
+    print(f"[case] bias/multi-row type={t}", flush=True)
+    W = synth_matrix(31, N, K)
+    data = W if t == pb.TYPE_F32 else quantize(t, W)
+    X = pb.synth_normal(32, M * K).reshape(M, K)
+    bias = pb.synth_normal(33, N)
+    w = ctx.upload(t, N, K, data)
+    Y = ctx.linear(w, X, bias)
+    for m in range(M):
+        ref = (oracle.f32_matvec(X[m], W) if t == pb.TYPE_F32
+               else oracle.matvec(t, X[m], data, N, K)) + bias
+        assert rel_l2(Y[m], ref) <= TOL
+    w.free()
+
+
+@pytest.mark.parametrize("K,N,M", [(288, 288, 1), (288, 768, 1), (768, 288, 3), (64, 100, 2)])
+def test_q8_ref_tensor_matches_matmul_q8(ctx, K, N, M):
+    """The reference's own QuantizedTensor (quantize.js) through
+    tensorMulAddQ8 -> matmul_q8 (quantize.js:224-266)."""
+    print(f"[case] q8ref K={K} N={N} M={M}", flush=True)
+    Wkn = synth_matrix(K * 7 + N, K, N)
+    q, s = oracle.quantize_q8_ref(Wkn)
+    X = pb.synth_normal(M + 1, M * K).reshape(M, K)
+    X[0, 3] = 0.0  # the skipped-zero branch
+    bias = pb.synth_normal(9, N)
+    w = ctx.upload_q8ref(K, N, q, s)
+    Y = ctx.linear(w, X, bias)
+    ref = oracle.matmul_q8_ref(X, q, s, N, bias)
+    assert rel_l2(Y, ref) <= TOL
+    assert rel_l2(Y, ref) < 1e-5
+    assert np.array_equal(ctx.dequant(w).ravel(), oracle.dequant_q8_ref(q, s))
+    w.free()
+
+
+def test_device_pointer_path_and_reuse(ctx):
+    """pbx_linear_dev on device buffers; the same resident weight reused."""
+    N, K = 2048, 8192
+    print("[case] device-pointer path", flush=True)
+    raw = pb.quantize_q4_0(synth_matrix(77, N, K))
+    w = ctx.upload(pb.TYPE_Q4_0, N, K, raw)
+    dx = ctx.alloc(K * 4)
+    dy = ctx.alloc(N * 4)
+    for seed in (1, 2, 3):
+        x = pb.synth_normal(seed, K)
+        dx.upload(x)
+        ctx.linear_dev(w, dx.ptr, 1, dy.ptr)
+        ctx.sync()
+        y = dy.download(np.float32, N)
+        assert rel_l2(y, oracle.q4_0_matvec_js(x, raw, N, K)) <= TOL
+    dx.free()
+    dy.free()
+    w.free()
+
+
+def test_error_paths_on_device(ctx):
+    print("[case] error paths", flush=True)
+    with pytest.raises(pb.PbxError) as e:
+        ctx.upload(pb.TYPE_Q4_0, 4, 33, np.zeros(200, np.uint8))
+    assert e.value.code == -1 and "K%32" in str(e.value)
+    with pytest.raises(pb.PbxError) as e:
+        ctx.upload(pb.TYPE_Q4_0, 4, 64, np.zeros(10, np.uint8))
+    assert e.value.code == -1 and "needs 144" in str(e.value)
+    with pytest.raises(pb.PbxError) as e:
+        ctx.upload(5, 4, 64, np.zeros(1000, np.uint8))
+    assert e.value.code == -1
+    # K beyond the GEMV limit uploads but the launch reports ENOTSUP
+    w = ctx.upload(pb.TYPE_Q4_0, 2, 16416, np.zeros(2 * 513 * 18, np.uint8))
+    with pytest.raises(pb.PbxError) as e:
+        ctx.linear(w, np.zeros(16416, np.float32))
+    assert e.value.code == -5
+    w.free()
+    # a NULL handle is rejected before any HIP call
+    with pytest.raises(pb.PbxError) as e:
+        ctx._call("pbx_linear", ctx._p, None, np.zeros(32, np.float32).ctypes.data, 1, None,
+                  np.zeros(2, np.float32).ctypes.data)
+    assert e.value.code == -1
