@@ -153,6 +153,65 @@ int pbx_bench_linear(pbx_ctx *ctx, int n_ops, const pbx_weight *const *W,
                      const float *const *dX, float *const *dY, int64_t M,
                      int reps, double *elapsed_ms);
 
+/* ---- resident model and on-GPU decode step ----------------------------
+ * A Llama-family model held in device memory, replacing the reference's
+ * runtimes for decode: LlamaRuntime.forward (llama.js:204-371) and
+ * StreamingLlamaRuntime.forward/_runLayerQ4 (llama-streaming.js:505-606,
+ * 738-815): RMSNorm (eps), q/k/v, RoPE on adjacent pairs with theta,
+ * KV cache, grouped-query attention, output projection + residual, RMSNorm,
+ * SwiGLU FFN + residual; final RMSNorm, LM head, greedy argmax (first
+ * maximum, llama.js:432-442).  Activations and the KV cache are fp32.
+ */
+typedef struct pbx_model pbx_model;
+
+typedef struct pbx_model_config {
+  int32_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim;
+  int32_t vocab_size, max_seq;
+  int32_t weight_type;  /* every layer matrix: PBX_TYPE_Q4_0 / Q8_0 / F32  */
+  int32_t embed_type;   /* token_embd (row lookup and, when tied, LM head) */
+  int32_t output_type;  /* untied LM head type, or -1: tied to token_embd  */
+  float rms_eps;        /* 1e-5 in the reference (purebee.js:164)         */
+  double rope_theta;    /* 10000 (llama.js:33) or the GGUF rope.freq_base */
+} pbx_model_config;
+
+/* Tensor ids for pbx_model_set_tensor, named as the GGUF tensors they take
+ * (gguf.js:378-410).  Matrices are GGUF row-major blocks of their type,
+ * [N rows = out features][K = in features]; norms are f32. */
+#define PBX_T_TOKEN_EMBD   0   /* [vocab, dim]   embed_type            */
+#define PBX_T_OUTPUT       1   /* [vocab, dim]   output_type (untied)  */
+#define PBX_T_OUTPUT_NORM  2   /* [dim] f32                            */
+#define PBX_T_ATTN_NORM    3   /* per layer: [dim] f32                 */
+#define PBX_T_FFN_NORM     4   /* per layer: [dim] f32                 */
+#define PBX_T_ATTN_Q       5   /* per layer: [dim, dim]                */
+#define PBX_T_ATTN_K       6   /* per layer: [kv_dim, dim]             */
+#define PBX_T_ATTN_V       7   /* per layer: [kv_dim, dim]             */
+#define PBX_T_ATTN_OUTPUT  8   /* per layer: [dim, dim]                */
+#define PBX_T_FFN_GATE     9   /* per layer: [hidden, dim]   (w1)      */
+#define PBX_T_FFN_UP      10   /* per layer: [hidden, dim]   (w3)      */
+#define PBX_T_FFN_DOWN    11   /* per layer: [dim, hidden]   (w2)      */
+
+int pbx_model_create(pbx_ctx *ctx, const pbx_model_config *cfg, pbx_model **out);
+int pbx_model_free(pbx_model *m);
+/* Replaces the loaders' per-tensor reads (streaming-loader.js:245-299,
+ * loadResidentWeights 324-335): one upload, resident afterwards. */
+int pbx_model_set_tensor(pbx_model *m, int tensor, int layer, const void *data,
+                         size_t nbytes);
+/* forward(tokenIds, startPos) (llama.js:204, llama-streaming.js:738):
+ * runs tokens[0..n) at positions start_pos.., writing the KV cache; returns
+ * the last position's logits (if logits != NULL, [vocab]) and its argmax. */
+int pbx_model_forward(pbx_model *m, const int32_t *tokens, int n_tokens,
+                      int start_pos, float *logits, int32_t *next_token);
+/* The greedy decode loop of generate() (llama.js:475-489): feeds `token` at
+ * start_pos, then each step's argmax, n_steps times, entirely on the GPU;
+ * out_tokens[i] is the token chosen by step i. */
+int pbx_model_generate(pbx_model *m, int32_t token, int start_pos, int n_steps,
+                       int32_t *out_tokens, float *last_logits);
+/* resetCache / rollbackCache (llama-streaming.js:828-862): zero cache
+ * positions >= pos of every layer. */
+int pbx_model_reset_cache(pbx_model *m);
+int pbx_model_rollback(pbx_model *m, int pos);
+int pbx_model_info(const pbx_model *m, size_t *device_bytes, int *uses_graph);
+
 #ifdef __cplusplus
 }
 #endif

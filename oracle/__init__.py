@@ -16,6 +16,13 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 _lib = None
 
+
+class _PboCfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("dim", "hidden", "n_layers", "n_heads", "n_kv",
+                                            "head_dim", "vocab", "max_seq")] + \
+               [("theta", ctypes.c_double), ("eps", ctypes.c_double)]
+
+
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
@@ -54,6 +61,15 @@ def lib():
         L.pbo_pool_destroy.argtypes = [ctypes.c_void_p]
         L.pbo_pool_q4_0_matvec.argtypes = [ctypes.c_void_p, _f32p, _u8p, _i64, _i64, _f32p]
         L.pbo_cpu_lm_head.argtypes = [_f32p, _f32p, _i64, _i64, _f32p]
+        L.pbo_llama_create.restype = ctypes.c_void_p
+        L.pbo_llama_create.argtypes = [ctypes.POINTER(_PboCfg)]
+        L.pbo_llama_set.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _f32p]
+        L.pbo_llama_forward.argtypes = [ctypes.c_void_p, np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS"),
+                                        ctypes.c_int, ctypes.c_int, _f32p]
+        L.pbo_llama_rollback.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        L.pbo_llama_free.argtypes = [ctypes.c_void_p]
+        L.pbo_argmax.restype = ctypes.c_int
+        L.pbo_argmax.argtypes = [_f32p, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -230,3 +246,40 @@ def cpu_lm_head(hidden, emb, vocab, dim, out=None):
         out = np.empty(vocab, np.float32)
     lib().pbo_cpu_lm_head(_c(hidden, np.float32), emb, vocab, dim, out)
     return out
+
+
+def argmax(v):
+    """llama.js:432-442: first index of the maximum."""
+    return lib().pbo_argmax(_c(v, np.float32), len(v))
+
+
+class LlamaRef:
+    """llama.js forward restated (llama_ref.c) on fp32 weights in GGUF
+    orientation; tensor ids as the product's PBX_T_* constants."""
+
+    def __init__(self, dim, hidden, n_layers, n_heads, n_kv, head_dim, vocab, max_seq,
+                 theta=10000.0, eps=1e-5):
+        self.cfg = _PboCfg(dim, hidden, n_layers, n_heads, n_kv, head_dim, vocab, max_seq,
+                           theta, eps)
+        self.vocab = vocab
+        self._p = lib().pbo_llama_create(ctypes.byref(self.cfg))
+
+    def set(self, tensor, layer, data):
+        lib().pbo_llama_set(self._p, tensor, layer, _c(data, np.float32).ravel())
+
+    def forward(self, tokens, start_pos):
+        toks = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(self.vocab, np.float32)
+        lib().pbo_llama_forward(self._p, toks, len(toks), start_pos, out)
+        return out
+
+    def rollback(self, pos):
+        lib().pbo_llama_rollback(self._p, pos)
+
+    def close(self):
+        if self._p:
+            lib().pbo_llama_free(self._p)
+            self._p = None
+
+    def __del__(self):
+        self.close()

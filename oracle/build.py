@@ -16,7 +16,7 @@ def build(verbose=False):
     # -ffp-contract=off: the restated f32 kernels multiply and add separately,
     # as the reference's WebAssembly does.
     cmd = ["gcc", "-O2", "-g", "-fPIC", "-shared", "-std=c11", "-ffp-contract=off", "-mssse3",
-           "-pthread", "-Wall", *srcs, "-o", tmp, "-lm"]
+           "-pthread", "-fopenmp", "-Wall", *srcs, "-o", tmp, "-lm"]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)

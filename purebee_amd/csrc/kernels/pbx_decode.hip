@@ -1,0 +1,273 @@
+// pbx_decode.hip -- gfx950 kernels of the on-GPU Llama decode step.
+//
+// One decode token (llama.js:204-371 at seqLen 1; llama-streaming.js:505-606)
+// runs as, per layer:
+//   1. GEMV  x -> [q|k|v]           RMSNorm(x, attn_norm) fused as prologue
+//   2. attention                     RoPE, KV-cache append, softmax(q.K)V
+//   3. GEMV  attn -> x (+=)          residual add fused as epilogue
+//   4. GEMV  x -> [gate|up]          RMSNorm(x, ffn_norm) prologue
+//   5. GEMV  silu(gate)*up -> x (+=) SwiGLU prologue, residual epilogue
+// then the LM head GEMV (RMSNorm(x, output_norm) prologue, per-tile argmax
+// partials epilogue) and a one-workgroup argmax that also advances the
+// device-side position, so consecutive steps replay without the host.
+// Device state: state[0] = position, state[1] = current token, state[2] =
+// step counter (index into the generated-token history).
+
+#include "pbx_gemv_impl.h"
+
+using namespace pbx;
+
+// ---------------------------------------------------------------------------
+// Fused GEMV instantiations.  Name: pbx_dk_<type>_<shape>_<mode>
+//   shape: w<R> (gemv_wide, R rows per workgroup) or s (gemv_small)
+//   mode : qkv = RMSNorm prologue + store      add = plain + accumulate
+//          swa = SwiGLU prologue + accumulate  lmh = RMSNorm + argmax partials
+// ---------------------------------------------------------------------------
+#define DK_WIDE(T, TN, R, PRO, EPI, MN)                                             \
+  extern "C" __global__ void __launch_bounds__(512) pbx_dk_##TN##_w##R##_##MN(GemvArgs a) { \
+    gemv_wide<T, R, PRO, EPI>(a);                                                   \
+  }
+#define DK_SMALL(T, TN, P, PRO, EPI, MN)                                            \
+  extern "C" __global__ void __launch_bounds__(256) pbx_dk_##TN##_s_##MN(GemvArgs a) { \
+    gemv_small<T, P, PRO, EPI>(a);                                                  \
+  }
+#define DK_MODES_WIDE(T, TN, R)                     \
+  DK_WIDE(T, TN, R, PRO_RMSNORM, EPI_STORE, qkv)    \
+  DK_WIDE(T, TN, R, PRO_NONE, EPI_ADD, add)         \
+  DK_WIDE(T, TN, R, PRO_SWIGLU, EPI_ADD, swa)       \
+  DK_WIDE(T, TN, R, PRO_RMSNORM, EPI_ARGMAX, lmh)
+#define DK_MODES_SMALL(T, TN, P)                    \
+  DK_SMALL(T, TN, P, PRO_RMSNORM, EPI_STORE, qkv)   \
+  DK_SMALL(T, TN, P, PRO_NONE, EPI_ADD, add)        \
+  DK_SMALL(T, TN, P, PRO_SWIGLU, EPI_ADD, swa)      \
+  DK_SMALL(T, TN, P, PRO_RMSNORM, EPI_ARGMAX, lmh)
+
+DK_MODES_WIDE(PBX_Q4, q4, 4)
+DK_MODES_WIDE(PBX_Q4, q4, 8)
+DK_MODES_WIDE(PBX_Q4, q4, 16)
+DK_MODES_SMALL(PBX_Q4, q4, 8)
+DK_MODES_WIDE(PBX_Q8, q8, 4)
+DK_MODES_WIDE(PBX_Q8, q8, 8)
+DK_MODES_SMALL(PBX_Q8, q8, 4)
+DK_MODES_WIDE(PBX_F32, f32, 2)
+DK_MODES_WIDE(PBX_F32, f32, 4)
+DK_MODES_SMALL(PBX_F32, f32, 2)
+
+// ---------------------------------------------------------------------------
+// Block reductions for 256-thread workgroups.
+// ---------------------------------------------------------------------------
+namespace {
+
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float *scratch) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float o = __shfl_xor(v, off, 64);
+    v = is_max ? fmaxf(v, o) : v + o;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();  // scratch may still be read from a previous reduction
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float r = scratch[0];
+  for (int w = 1; w < nw; ++w) r = is_max ? fmaxf(r, scratch[w]) : r + scratch[w];
+  return r;
+}
+
+}  // namespace
+
+#define PBX_ATTN_MAX_SEQ 8192
+#define PBX_ATTN_MAX_HD 256
+
+struct AttnArgs {
+  const float *qkv;    // [dim | kv_dim | kv_dim] of this token, before RoPE
+  float *kcache;       // this layer: [max_seq][kv_dim]
+  float *vcache;
+  const float *rope;   // [max_seq][head_dim/2][cos, sin]
+  float *out;          // [dim]
+  const int *state;    // state[0] = position
+  int n_heads, n_kv_heads, head_dim;
+  float scale;         // 1/sqrt(head_dim)
+};
+
+// One workgroup per query head (llama.js:258-301 / llama-streaming.js:543-573):
+// rotate q and the new k (adjacent pairs, llama.js:163-190), append k and v
+// at `pos` (the first query head of each KV group writes), scores over
+// positions 0..pos, max-subtracted softmax, weighted sum of V.
+extern "C" __global__ void __launch_bounds__(256) pbx_attention_decode(AttnArgs a) {
+  __shared__ float qr[PBX_ATTN_MAX_HD], kn[PBX_ATTN_MAX_HD], vn[PBX_ATTN_MAX_HD];
+  __shared__ float sc[PBX_ATTN_MAX_SEQ];
+  __shared__ float part[8][PBX_ATTN_MAX_HD];
+  __shared__ float red[8];
+
+  const int h = blockIdx.x, hd = a.head_dim;
+  const int group = a.n_heads / a.n_kv_heads, kvh = h / group;
+  const int kvdim = a.n_kv_heads * hd, dim = a.n_heads * hd;
+  const int pos = a.state[0];
+  const float *q = a.qkv + (size_t)h * hd;
+  const float *k = a.qkv + dim + (size_t)kvh * hd;
+  const float *v = a.qkv + dim + kvdim + (size_t)kvh * hd;
+  const float *rp = a.rope + (size_t)pos * hd;
+
+  for (int i = threadIdx.x; i < hd / 2; i += blockDim.x) {
+    const float c = rp[2 * i], s = rp[2 * i + 1];
+    const float q0 = q[2 * i], q1 = q[2 * i + 1];
+    qr[2 * i] = q0 * c - q1 * s;
+    qr[2 * i + 1] = q0 * s + q1 * c;
+    const float k0 = k[2 * i], k1 = k[2 * i + 1];
+    kn[2 * i] = k0 * c - k1 * s;
+    kn[2 * i + 1] = k0 * s + k1 * c;
+    vn[2 * i] = v[2 * i];
+    vn[2 * i + 1] = v[2 * i + 1];
+  }
+  __syncthreads();
+  float *krow = a.kcache + (size_t)kvh * hd;
+  float *vrow = a.vcache + (size_t)kvh * hd;
+  if (h % group == 0) {
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+      krow[(size_t)pos * kvdim + d] = kn[d];
+      vrow[(size_t)pos * kvdim + d] = vn[d];
+    }
+  }
+
+  // scores: positions < pos from the cache, position pos from LDS
+  const int L = pos + 1;
+  for (int j = threadIdx.x; j < L; j += blockDim.x) {
+    float dot = 0.f;
+    if (j < pos) {
+      const float4 *kr = reinterpret_cast<const float4 *>(krow + (size_t)j * kvdim);
+      for (int d4 = 0; d4 < hd / 4; ++d4) {
+        const float4 t = kr[d4];
+        dot = fmaf(qr[4 * d4], t.x, dot);
+        dot = fmaf(qr[4 * d4 + 1], t.y, dot);
+        dot = fmaf(qr[4 * d4 + 2], t.z, dot);
+        dot = fmaf(qr[4 * d4 + 3], t.w, dot);
+      }
+    } else {
+      for (int d = 0; d < hd; ++d) dot = fmaf(qr[d], kn[d], dot);
+    }
+    sc[j] = dot * a.scale;
+  }
+  __syncthreads();
+  float m = -INFINITY;
+  for (int j = threadIdx.x; j < L; j += blockDim.x) m = fmaxf(m, sc[j]);
+  m = block_reduce(m, true, red);
+  float sum = 0.f;
+  for (int j = threadIdx.x; j < L; j += blockDim.x) {
+    const float e = expf(sc[j] - m);
+    sc[j] = e;
+    sum += e;
+  }
+  sum = block_reduce(sum, false, red);
+  for (int j = threadIdx.x; j < L; j += blockDim.x) sc[j] = sc[j] / sum;
+  __syncthreads();
+
+  // out[d] = sum_j p_j V[j][d]: G groups of hd threads split the positions
+  const int G = (int)blockDim.x / hd;
+  const int g = threadIdx.x / hd, d = threadIdx.x % hd;
+  if (g < G) {
+    float acc = 0.f;
+    for (int j = g; j < L; j += G) {
+      const float vv = (j < pos) ? vrow[(size_t)j * kvdim + d] : vn[d];
+      acc = fmaf(sc[j], vv, acc);
+    }
+    part[g][d] = acc;
+  }
+  __syncthreads();
+  if (threadIdx.x < hd) {
+    float s = 0.f;
+    for (int gg = 0; gg < G; ++gg) s += part[gg][threadIdx.x];
+    a.out[(size_t)h * hd + threadIdx.x] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Embedding row of the current token (llama.js:216-225), dequantised exactly
+// from the resident token_embd planes (gguf.js:239-286) or copied (F32).
+// ---------------------------------------------------------------------------
+struct EmbedArgs {
+  const uint8_t *qs;
+  const uint16_t *dsc;
+  float *x;
+  const int *state;  // state[1] = token
+  int type;          // PBX_Q4 / PBX_Q8 / PBX_F32
+  int dim, vocab;
+};
+
+extern "C" __global__ void __launch_bounds__(256) pbx_embed(EmbedArgs a) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.dim) return;
+  int tok = a.state[1];
+  if (tok < 0 || tok >= a.vocab) tok = 0;  // never read outside the table
+  const int B = a.dim / 32, b = i / 32, j = i % 32;
+  float val;
+  if (a.type == PBX_F32) {
+    val = reinterpret_cast<const float *>(a.qs)[(size_t)tok * a.dim + i];
+  } else {
+    const float d = f16_bits_to_f32(a.dsc[((size_t)(tok >> 3) * B + b) * 8 + (tok & 7)]);
+    if (a.type == PBX_Q4) {
+      const unsigned byte = a.qs[((size_t)tok * B + b) * 16 + (j & 15)];
+      const int nib = j < 16 ? (int)(byte & 15u) : (int)(byte >> 4);
+      val = (float)(nib - 8) * d;
+    } else {
+      val = (float)(int8_t)a.qs[((size_t)tok * B + b) * 32 + j] * d;
+    }
+  }
+  a.x[i] = val;
+}
+
+// ---------------------------------------------------------------------------
+// Final argmax over the LM head's per-tile partial keys; records the token,
+// appends it to the history and advances the position.
+// ---------------------------------------------------------------------------
+struct ArgmaxArgs {
+  const uint64_t *partials;
+  int *state;
+  int *hist;
+  int n_partials;
+  int hist_cap;
+};
+
+extern "C" __global__ void __launch_bounds__(1024) pbx_argmax_final(ArgmaxArgs a) {
+  __shared__ uint64_t red[16];
+  uint64_t best = 0;
+  for (int i = threadIdx.x; i < a.n_partials; i += blockDim.x) {
+    const uint64_t k = a.partials[i];
+    best = k > best ? k : best;
+  }
+  best = wave_max_u64(best);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) best = red[w] > best ? red[w] : best;
+    best = red[0] > best ? red[0] : best;
+    const int tok = best ? (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFu)) : 0;
+    a.state[1] = tok;
+    const int step = a.state[2];
+    if (a.hist && step >= 0 && step < a.hist_cap) a.hist[step] = tok;
+    a.state[2] = step + 1;
+    a.state[0] = a.state[0] + 1;
+  }
+}
+
+// Zero cache positions [from, max_seq) of every layer (resetCache /
+// rollbackCache, llama-streaming.js:828-862).  A kernel rather than a
+// memset so it can sit inside a captured graph.
+extern "C" __global__ void __launch_bounds__(256)
+pbx_kv_fill(float *kcache, float *vcache, int64_t layer_stride, int64_t from_off, int64_t count,
+            int n_layers) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count * n_layers) return;
+  const int64_t l = i / count, o = from_off + i % count;
+  kcache[l * layer_stride + o] = 0.f;
+  vcache[l * layer_stride + o] = 0.f;
+}
+
+// Writes the token and position of a host-driven step into the device state.
+extern "C" __global__ void pbx_set_state(int *state, int pos, int token, int step) {
+  if (threadIdx.x == 0) {
+    if (pos >= 0) state[0] = pos;
+    if (token >= 0) state[1] = token;
+    if (step >= 0) state[2] = step;
+  }
+}

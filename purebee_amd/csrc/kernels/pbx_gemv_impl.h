@@ -1,0 +1,445 @@
+// pbx_gemv_impl.h -- device implementation of the M=1 GEMV family, shared by
+// the plain instruction kernels (pbx_gemv.hip) and the fused decode-step
+// kernels (pbx_decode.hip).
+//
+// A GEMV computes y[n] = sum_k x[k] * W[n,k] for one activation row.  Two
+// templates cover every shape:
+//   gemv_wide  : B = K/32 >= 33.  W = ceil(B/64) waves per workgroup; lane l
+//                of wave w owns block b = 64w + l of every row and keeps that
+//                block's 32 activations in registers; R rows per workgroup.
+//   gemv_small : B <= 32.  Lane l owns (row slot l/B, block l%B); 64/B rows
+//                per pass, P passes per wave, partials summed through LDS.
+// Both take a prologue that builds the activation block the lane needs
+// (plain load, RMSNorm of x, or SwiGLU of gate/up) and an epilogue that
+// consumes each row's sum (store with optional bias, accumulate into y for
+// residual connections, or store plus per-tile argmax partials).
+#ifndef PBX_GEMV_IMPL_H
+#define PBX_GEMV_IMPL_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define PBX_Q4 0
+#define PBX_Q8 1
+#define PBX_F32 2
+
+#define PRO_NONE 0
+#define PRO_RMSNORM 1
+#define PRO_SWIGLU 2
+
+#define EPI_STORE 0
+#define EPI_ADD 1
+#define EPI_ARGMAX 2
+
+// Everything a fused GEMV launch needs; passed by value.
+struct GemvArgs {
+  const uint8_t *qs;    // weight plane (nibbles / int8 / f32)
+  const uint16_t *dsc;  // fp16 scale plane (quantised types)
+  const float *X;       // activation row(s) [M][K]; gate for PRO_SWIGLU
+  const float *X2;      // up for PRO_SWIGLU
+  const float *normw;   // RMSNorm weight [K] for PRO_RMSNORM
+  const float *bias;    // [N] or null (EPI_STORE)
+  float *Y;             // [M][N]
+  uint64_t *partials;   // EPI_ARGMAX: one key per tile
+  int N, B;
+  float eps;
+};
+
+namespace pbx {
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load of weight bytes that are read once per matvec
+// (nontemporal: they should not displace the activations in the caches).
+__device__ __forceinline__ uint4 ld_stream(const void *p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(unsigned bits) {
+  // IEEE binary16 -> binary32 (v_cvt_f32_f16): the conversion of
+  // gguf.js:55-70 including subnormals, +-inf and NaN.
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)(bits & 0xFFFFu));
+}
+
+// sum_j x[j] * nibble_j over one Q4_0 block (nibbles unsigned, 0..15); the
+// caller subtracts 8*sum(x) to obtain sum_j x[j] * (nibble_j - 8).  Byte j
+// holds element j (low nibble) and element j+16 (high nibble).
+__device__ __forceinline__ float dot_q4(const uint4 q, const float (&xr)[32]) {
+  const unsigned w[4] = {q.x, q.y, q.z, q.w};
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const unsigned lo = w[j] & 0x0F0F0F0Fu;
+    const unsigned hi = (w[j] >> 4) & 0x0F0F0F0Fu;
+    s0 = fmaf(xr[4 * j + 0], (float)(lo & 0xFFu), s0);
+    s0 = fmaf(xr[4 * j + 1], (float)((lo >> 8) & 0xFFu), s0);
+    s0 = fmaf(xr[4 * j + 2], (float)((lo >> 16) & 0xFFu), s0);
+    s0 = fmaf(xr[4 * j + 3], (float)(lo >> 24), s0);
+    s1 = fmaf(xr[16 + 4 * j + 0], (float)(hi & 0xFFu), s1);
+    s1 = fmaf(xr[16 + 4 * j + 1], (float)((hi >> 8) & 0xFFu), s1);
+    s1 = fmaf(xr[16 + 4 * j + 2], (float)((hi >> 16) & 0xFFu), s1);
+    s1 = fmaf(xr[16 + 4 * j + 3], (float)(hi >> 24), s1);
+  }
+  return s0 + s1;
+}
+
+// sum_j x[j] * (q_j + 128) over one Q8_0 block: flipping the sign bit of each
+// int8 gives the unsigned byte q+128, which converts in one instruction; the
+// caller subtracts 128*sum(x).
+__device__ __forceinline__ float dot_q8(const uint4 qa, const uint4 qb,
+                                        const float (&xr)[32]) {
+  const unsigned w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const unsigned u = w[j] ^ 0x80808080u;
+    float &s = (j & 1) ? s1 : s0;
+    s = fmaf(xr[4 * j + 0], (float)(u & 0xFFu), s);
+    s = fmaf(xr[4 * j + 1], (float)((u >> 8) & 0xFFu), s);
+    s = fmaf(xr[4 * j + 2], (float)((u >> 16) & 0xFFu), s);
+    s = fmaf(xr[4 * j + 3], (float)(u >> 24), s);
+  }
+  return s0 + s1;
+}
+
+__device__ __forceinline__ float dot_f32(const uint4 (&q)[8], const float (&xr)[32]) {
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float &s = (j & 1) ? s1 : s0;
+    s = fmaf(xr[4 * j + 0], __uint_as_float(q[j].x), s);
+    s = fmaf(xr[4 * j + 1], __uint_as_float(q[j].y), s);
+    s = fmaf(xr[4 * j + 2], __uint_as_float(q[j].z), s);
+    s = fmaf(xr[4 * j + 3], __uint_as_float(q[j].w), s);
+  }
+  return s0 + s1;
+}
+
+template <int TYPE> struct BlockTraits;
+template <> struct BlockTraits<PBX_Q4> { static constexpr int QB = 16; static constexpr float OFF = 8.f; };
+template <> struct BlockTraits<PBX_Q8> { static constexpr int QB = 32; static constexpr float OFF = 128.f; };
+template <> struct BlockTraits<PBX_F32> { static constexpr int QB = 128; static constexpr float OFF = 0.f; };
+
+__device__ __forceinline__ void load_block(const float *__restrict__ p, bool valid,
+                                           float (&v)[32]) {
+  if (valid) {
+    const float4 *xp = reinterpret_cast<const float4 *>(p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 t = xp[i];
+      v[4 * i + 0] = t.x; v[4 * i + 1] = t.y;
+      v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = 0.f;
+  }
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// Order-preserving key for argmax: larger value -> larger key; equal values
+// -> the smaller index wins (the first maximum, as llama.js:432-442 keeps
+// the first index on ties with its strict `>`).  NaN never wins.
+__device__ __forceinline__ uint64_t argmax_key(float v, unsigned idx) {
+  if (v != v) return 0;
+  unsigned b = __float_as_uint(v);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)b << 32) | (uint64_t)(0xFFFFFFFFu - idx);
+}
+
+// Activation block b (32 values) after the prologue.  `own` marks the lanes
+// whose block counts once toward the RMSNorm sum of squares.
+template <int PRO>
+__device__ __forceinline__ void prologue_block(const GemvArgs &a, const float *x,
+                                               const float *x2, int b, bool valid,
+                                               float (&xr)[32]) {
+  if constexpr (PRO == PRO_SWIGLU) {
+    float g[32], u[32];
+    load_block(x + (size_t)b * 32, valid, g);
+    load_block(x2 + (size_t)b * 32, valid, u);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) xr[j] = silu(g[j]) * u[j];
+  } else {
+    load_block(x + (size_t)b * 32, valid, xr);
+  }
+}
+
+// RMSNorm (engine.js:429-449): rms = sqrt(sum(x^2)/K + eps); x/rms * w.
+__device__ __forceinline__ void apply_rmsnorm(const GemvArgs &a, float ss, int K, int b,
+                                              bool valid, float (&xr)[32]) {
+  const float rms = sqrtf(ss / (float)K + a.eps);
+  if (valid) {
+    float w[32];
+    load_block(a.normw + (size_t)b * 32, true, w);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) xr[j] = xr[j] / rms * w[j];
+  }
+}
+
+template <int TYPE>
+__device__ __forceinline__ float block_term(const uint4 (&q)[BlockTraits<TYPE>::QB / 16],
+                                            const float (&xr)[32], float corr, float d) {
+  if constexpr (TYPE == PBX_Q4) {
+    return (dot_q4(q[0], xr) - corr) * d;
+  } else if constexpr (TYPE == PBX_Q8) {
+    return (dot_q8(q[0], q[1], xr) - corr) * d;
+  } else {
+    return dot_f32(q, xr);
+  }
+}
+
+// Transposed wavefront reduction: v[0..R) are 64-lane partial sums of R rows.
+// Each halving stage exchanges half of the remaining values with the lane
+// OFF away, so the stages move R/2, R/4, ... values instead of reducing each
+// row separately; lane l ends with row l / (64/R) summed over its group and
+// the remaining butterfly stages complete the 64-lane sum.
+template <int CNT, int OFF, int R>
+__device__ __forceinline__ void transpose_stage(float (&v)[R], int lane) {
+  if constexpr (CNT > 1) {
+    const bool up = (lane & OFF) != 0;
+#pragma unroll
+    for (int i = 0; i < CNT / 2; ++i) {
+      const float keep = up ? v[i + CNT / 2] : v[i];
+      const float send = up ? v[i] : v[i + CNT / 2];
+      v[i] = keep + __shfl_xor(send, OFF, 64);
+    }
+    transpose_stage<CNT / 2, OFF / 2, R>(v, lane);
+  }
+}
+
+template <int R>
+__device__ __forceinline__ float wave_transpose_reduce(float (&v)[R], int lane) {
+  transpose_stage<R, 32, R>(v, lane);
+  float r = v[0];
+#pragma unroll
+  for (int off = (64 / R) / 2; off >= 1; off >>= 1) r += __shfl_xor(r, off, 64);
+  return r;
+}
+
+template <int EPI>
+__device__ __forceinline__ void epilogue_row(const GemvArgs &a, float *y, int n, float s) {
+  if constexpr (EPI == EPI_ADD) {
+    y[n] += s;
+  } else {
+    y[n] = s + (a.bias ? a.bias[n] : 0.f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <int TYPE, int R, int PRO, int EPI>
+__device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
+  constexpr int QB = BlockTraits<TYPE>::QB;
+  constexpr int NV = QB / 16;
+  constexpr int MAXW = 8;
+  __shared__ float red[MAXW][R];
+  __shared__ float ssw[MAXW];
+
+  const int N = a.N, B = a.B;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int b = wave * 64 + lane;
+  const bool valid = b < B;
+  const int K = B * 32;
+  const float *x = a.X + (size_t)blockIdx.y * K;
+  const float *x2 = a.X2 ? a.X2 + (size_t)blockIdx.y * K : nullptr;
+  float *y = a.Y + (size_t)blockIdx.y * N;
+  const int r0 = blockIdx.x * R;
+
+  // Issue the weight loads first: they do not depend on the activations.
+  uint4 q[R][NV];
+  const uint8_t *base = a.qs + ((size_t)r0 * B + b) * QB;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+      q[i][v] = valid ? ld_stream(base + (size_t)i * B * QB + v * 16)
+                      : make_uint4(0u, 0u, 0u, 0u);
+  }
+  float dsf[R];
+  if constexpr (TYPE != PBX_F32) {
+    if constexpr (R >= 8) {
+#pragma unroll
+      for (int g = 0; g < R / 8; ++g) {
+        const uint4 dv = valid ? *reinterpret_cast<const uint4 *>(
+                                     a.dsc + ((size_t)(r0 / 8 + g) * B + b) * 8)
+                               : make_uint4(0u, 0u, 0u, 0u);
+        const unsigned dw[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          dsf[g * 8 + 2 * j] = f16_bits_to_f32(dw[j]);
+          dsf[g * 8 + 2 * j + 1] = f16_bits_to_f32(dw[j] >> 16);
+        }
+      }
+    } else {
+      // R = 2 or 4 rows inside one 8-row group (r0 % R == 0).
+      const uint16_t *dp = a.dsc + ((size_t)(r0 / 8) * B + b) * 8 + (r0 & 7);
+#pragma unroll
+      for (int i = 0; i < R; ++i) dsf[i] = valid ? f16_bits_to_f32(dp[i]) : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < R; ++i) dsf[i] = 1.f;
+  }
+
+  float xr[32];
+  prologue_block<PRO>(a, x, x2, b, valid, xr);
+  if constexpr (PRO == PRO_RMSNORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) ss = fmaf(xr[j], xr[j], ss);
+    ss = wave_sum(ss);
+    if (nwaves > 1) {
+      if (lane == 0) ssw[wave] = ss;
+      __syncthreads();
+      ss = 0.f;
+      for (int w = 0; w < nwaves; ++w) ss += ssw[w];
+    }
+    apply_rmsnorm(a, ss, K, b, valid, xr);
+  }
+  float xs = 0.f;
+  if constexpr (TYPE != PBX_F32) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) xs += xr[i];
+  }
+  const float corr = BlockTraits<TYPE>::OFF * xs;
+
+  float acc[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) acc[i] = block_term<TYPE>(q[i], xr, corr, dsf[i]);
+
+  const float tot = wave_transpose_reduce<R>(acc, lane);
+  const int lanes_per_row = 64 / R;
+  const int row = lane / lanes_per_row;
+  uint64_t key = 0;
+  if (nwaves == 1) {
+    if ((lane % lanes_per_row) == 0) {
+      const int n = r0 + row;
+      if (n < N) {
+        epilogue_row<EPI>(a, y, n, tot);
+        if constexpr (EPI == EPI_ARGMAX) key = argmax_key(tot, (unsigned)n);
+      }
+    }
+  } else {
+    if ((lane % lanes_per_row) == 0) red[wave][row] = tot;
+    __syncthreads();
+    if (threadIdx.x < R) {
+      float s = 0.f;
+      for (int w = 0; w < nwaves; ++w) s += red[w][threadIdx.x];
+      const int n = r0 + threadIdx.x;
+      if (n < N) {
+        epilogue_row<EPI>(a, y, n, s);
+        if constexpr (EPI == EPI_ARGMAX) key = argmax_key(s, (unsigned)n);
+      }
+    }
+  }
+  if constexpr (EPI == EPI_ARGMAX) {
+    if (wave == 0) {
+      key = wave_max_u64(key);
+      if (lane == 0) a.partials[blockIdx.x] = key;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <int TYPE, int P, int PRO, int EPI>
+__device__ __forceinline__ void gemv_small(const GemvArgs &a) {
+  constexpr int QB = BlockTraits<TYPE>::QB;
+  constexpr int NV = QB / 16;
+  __shared__ float part[4][P][64];
+
+  const int N = a.N, B = a.B;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rpw = 64 / B;
+  const bool active = lane < rpw * B;
+  const int rs = active ? lane / B : 0;
+  const int b = active ? lane % B : 0;
+  const int K = B * 32;
+  const float *x = a.X + (size_t)blockIdx.y * K;
+  const float *x2 = a.X2 ? a.X2 + (size_t)blockIdx.y * K : nullptr;
+  float *y = a.Y + (size_t)blockIdx.y * N;
+
+  const int T = P * rpw;
+  const int r0 = (blockIdx.x * 4 + wave) * T;
+
+  uint4 q[P][NV];
+  float d[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int rw = r0 + p * rpw + rs;
+    const bool ok = active && rw < N;
+    const uint8_t *src = a.qs + ((size_t)rw * B + b) * QB;
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+      q[p][v] = ok ? ld_stream(src + v * 16) : make_uint4(0u, 0u, 0u, 0u);
+    d[p] = 1.f;
+    if constexpr (TYPE != PBX_F32)
+      d[p] = ok ? f16_bits_to_f32(a.dsc[((size_t)(rw >> 3) * B + b) * 8 + (rw & 7)]) : 0.f;
+  }
+
+  float xr[32];
+  prologue_block<PRO>(a, x, x2, b, active, xr);
+  if constexpr (PRO == PRO_RMSNORM) {
+    float ss = 0.f;
+    if (active && rs == 0) {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) ss = fmaf(xr[j], xr[j], ss);
+    }
+    ss = wave_sum(ss);
+    apply_rmsnorm(a, ss, K, b, active, xr);
+  }
+  float xs = 0.f;
+  if constexpr (TYPE != PBX_F32) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) xs += xr[i];
+  }
+  const float corr = BlockTraits<TYPE>::OFF * xs;
+
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int rw = r0 + p * rpw + rs;
+    const bool ok = active && rw < N;
+    part[wave][p][lane] = ok ? block_term<TYPE>(q[p], xr, corr, d[p]) : 0.f;
+  }
+  __syncthreads();
+  uint64_t key = 0;
+  for (int t = lane; t < T; t += 64) {
+    const int p = t / rpw, r = t % rpw;
+    float s = 0.f;
+    for (int j = 0; j < B; ++j) s += part[wave][p][r * B + j];
+    const int n = r0 + t;
+    if (n < N) {
+      epilogue_row<EPI>(a, y, n, s);
+      if constexpr (EPI == EPI_ARGMAX) {
+        const uint64_t k = argmax_key(s, (unsigned)n);
+        key = k > key ? k : key;
+      }
+    }
+  }
+  if constexpr (EPI == EPI_ARGMAX) {
+    key = wave_max_u64(key);
+    if (lane == 0) a.partials[blockIdx.x * 4 + wave] = key;
+  }
+}
+
+}  // namespace pbx
+
+#endif

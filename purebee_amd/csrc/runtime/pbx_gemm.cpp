@@ -6,5 +6,3 @@ int pbx_gemm_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M
   (void)w; (void)dX; (void)M; (void)dBias; (void)dY; (void)stream;
   return pbx_fail(c, PBX_ENOTSUP, "pbx_linear: MFMA GEMM path not built");
 }
-
-void pbx_model_release_all(pbx_ctx *c) { (void)c; }

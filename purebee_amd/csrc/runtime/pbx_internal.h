@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <unordered_map>
 
 #include "pbx.h"
 
@@ -63,6 +64,7 @@ struct pbx_ctx {
   void *h_stage[2] = {nullptr, nullptr};
   size_t h_stage_cap[2] = {0, 0};
   void *models = nullptr;  // decode-step models owned by this context
+  std::unordered_map<std::string, hipFunction_t> named;  // kernels looked up by name
 };
 
 struct pbx_weight {
@@ -79,6 +81,13 @@ int pbx_fail(pbx_ctx *c, int code, const char *fmt, ...)
     __attribute__((format(printf, 3, 4)));
 int pbx_launch(pbx_ctx *c, int kernel, dim3 grid, dim3 block, void **args,
                hipStream_t stream = nullptr);
+hipFunction_t pbx_kernel_by_name(pbx_ctx *c, const std::string &name);
+int pbx_launch_fn(pbx_ctx *c, hipFunction_t f, const char *name, dim3 grid, dim3 block,
+                  void **args, hipStream_t stream);
+int pbx_weight_alloc(pbx_ctx *c, int type, int64_t N, int64_t K, pbx_weight **out);
+int pbx_weight_write_rows(pbx_ctx *c, pbx_weight *w, int64_t row0, int64_t rows,
+                          const void *host);
+void pbx_weight_release(pbx_weight *w);
 int pbx_ensure_dev(pbx_ctx *c, void **p, size_t *cap, size_t need);
 int pbx_ensure_pinned(pbx_ctx *c, void **p, size_t *cap, size_t need);
 int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,

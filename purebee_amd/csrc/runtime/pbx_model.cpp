@@ -1,0 +1,616 @@
+// pbx_model.cpp -- resident Llama-family model and its on-GPU decode step.
+//
+// The reference's decode layer (_runLayerQ4, llama-streaming.js:505-606; the
+// same math as LlamaRuntime.forward, llama.js:204-371) runs here as 5 kernels
+// per layer plus embedding, LM head and argmax (see pbx_decode.hip).  One
+// step is captured once into a HIP graph and replayed: the token and the
+// position live in device memory, the argmax kernel writes the next token and
+// advances the position, so greedy decoding never returns to the host between
+// tokens.  Weights are uploaded once; q|k|v and gate|up are stored as one
+// matrix each so a single GEMV reads them.
+
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "pbx_internal.h"
+
+#define PBX_MODEL_MAGIC 0x5042584Du  // "PBXM"
+
+namespace {
+
+struct GemvArgsHost {  // layout of GemvArgs in pbx_gemv_impl.h
+  const void *qs;
+  const void *dsc;
+  const float *X;
+  const float *X2;
+  const float *normw;
+  const float *bias;
+  float *Y;
+  uint64_t *partials;
+  int N, B;
+  float eps;
+};
+
+struct AttnArgsHost {  // AttnArgs in pbx_decode.hip
+  const float *qkv;
+  float *kcache, *vcache;
+  const float *rope;
+  float *out;
+  const int *state;
+  int n_heads, n_kv_heads, head_dim;
+  float scale;
+};
+
+struct EmbedArgsHost {  // EmbedArgs in pbx_decode.hip
+  const void *qs;
+  const void *dsc;
+  float *x;
+  const int *state;
+  int type;
+  int dim, vocab;
+};
+
+struct ArgmaxArgsHost {  // ArgmaxArgs in pbx_decode.hip
+  const uint64_t *partials;
+  int *state;
+  int *hist;
+  int n_partials;
+  int hist_cap;
+};
+
+enum ArgKind { ARG_GEMV, ARG_ATTN, ARG_EMBED, ARG_ARGMAX };
+
+struct Op {
+  hipFunction_t f = nullptr;
+  std::string name;
+  dim3 grid, block;
+  ArgKind kind;
+  GemvArgsHost gemv;
+  AttnArgsHost attn;
+  EmbedArgsHost embed;
+  ArgmaxArgsHost amax;
+};
+
+struct Layer {
+  pbx_weight *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wd = nullptr;
+  float *attn_norm = nullptr, *ffn_norm = nullptr;
+  unsigned set_mask = 0;
+};
+
+const char *type_tag(int t) {
+  return t == PBX_TYPE_Q4_0 ? "q4" : t == PBX_TYPE_Q8_0 ? "q8" : "f32";
+}
+
+int kernel_type(int t) { return t == PBX_TYPE_Q4_0 ? 0 : t == PBX_TYPE_Q8_0 ? 1 : 2; }
+
+}  // namespace
+
+struct pbx_model {
+  uint32_t magic = 0;
+  pbx_ctx *c = nullptr;
+  pbx_model_config cfg;
+  int kvdim = 0, qkv_rows = 0;
+  std::vector<Layer> layers;
+  pbx_weight *embd = nullptr, *output = nullptr;
+  float *out_norm = nullptr;
+  unsigned global_mask = 0;
+  float *kcache = nullptr, *vcache = nullptr, *rope = nullptr;
+  float *x = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
+  uint64_t *partials = nullptr;
+  int n_partials_cap = 0;
+  int *state = nullptr;
+  int *hist = nullptr;
+  int hist_cap = 0;
+  std::vector<Op> ops;
+  bool ops_ready = false;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  bool graph_tried = false, graph_ok = false;
+  size_t bytes = 0;
+};
+
+static bool model_ok(const pbx_model *m) { return m && m->magic == PBX_MODEL_MAGIC; }
+
+// Kernel shape for a GEMV of N rows x B blocks (the same rules as the plain
+// instruction): small-K kernel for B <= 32, otherwise ceil(B/64) waves per
+// workgroup and the largest row tile that keeps >= 4 workgroups per CU.
+static void plan_gemv(pbx_ctx *c, int type, int N, int B, std::string *shape, dim3 *grid,
+                      dim3 *block, int *n_tiles) {
+  if (B <= 32) {
+    const int P = type == PBX_TYPE_Q4_0 ? 8 : type == PBX_TYPE_Q8_0 ? 4 : 2;
+    const int T = P * (64 / B);
+    const int gx = (N + 4 * T - 1) / (4 * T);
+    *shape = "s";
+    *grid = dim3(gx);
+    *block = dim3(256);
+    *n_tiles = gx * 4;
+    return;
+  }
+  const int W = (B + 63) / 64;
+  const int target = std::max(4 * c->cu_count, 256);
+  int R;
+  if (type == PBX_TYPE_Q4_0)
+    R = (N / 16 >= target) ? 16 : (N / 8 >= target) ? 8 : 4;
+  else if (type == PBX_TYPE_Q8_0)
+    R = (N / 8 >= target) ? 8 : 4;
+  else
+    R = (N / 4 >= target) ? 4 : 2;
+  *shape = "w" + std::to_string(R);
+  *grid = dim3((N + R - 1) / R);
+  *block = dim3(64 * W);
+  *n_tiles = (int)grid->x;
+}
+
+static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const float *X,
+                    const float *X2, const float *normw, float *Y, int *n_tiles_out) {
+  pbx_ctx *c = m->c;
+  Op op;
+  op.kind = ARG_GEMV;
+  std::string shape;
+  int n_tiles = 0;
+  plan_gemv(c, w->type, (int)w->N, (int)w->B, &shape, &op.grid, &op.block, &n_tiles);
+  if (w->B > 32 && (w->B + 63) / 64 > 8)
+    return pbx_fail(c, PBX_ENOTSUP, "model: K=%lld exceeds the GEMV limit of 16384",
+                    (long long)w->K);
+  op.name = std::string("pbx_dk_") + type_tag(w->type) + "_" + shape + "_" + mode;
+  op.f = pbx_kernel_by_name(c, op.name);
+  if (!op.f) return pbx_fail(c, PBX_ELOAD, "model: kernel %s not found", op.name.c_str());
+  op.gemv = GemvArgsHost{w->qs, w->d, X, X2, normw, nullptr, Y, m->partials, (int)w->N,
+                         (int)w->B, m->cfg.rms_eps};
+  if (n_tiles_out) *n_tiles_out = n_tiles;
+  m->ops.push_back(op);
+  return PBX_OK;
+}
+
+static int build_ops(pbx_model *m) {
+  pbx_ctx *c = m->c;
+  const pbx_model_config &g = m->cfg;
+  m->ops.clear();
+  Op e;
+  e.kind = ARG_EMBED;
+  e.name = "pbx_embed";
+  e.f = pbx_kernel_by_name(c, e.name);
+  if (!e.f) return pbx_fail(c, PBX_ELOAD, "model: kernel pbx_embed not found");
+  e.grid = dim3((g.dim + 255) / 256);
+  e.block = dim3(256);
+  e.embed = EmbedArgsHost{m->embd->qs, m->embd->d, m->x, m->state, kernel_type(m->embd->type),
+                          g.dim, g.vocab_size};
+  m->ops.push_back(e);
+  hipFunction_t fattn = pbx_kernel_by_name(c, "pbx_attention_decode");
+  if (!fattn) return pbx_fail(c, PBX_ELOAD, "model: kernel pbx_attention_decode not found");
+  const size_t layer_kv = (size_t)g.max_seq * m->kvdim;
+  for (int l = 0; l < g.n_layers; ++l) {
+    Layer &L = m->layers[l];
+    int rc;
+    if ((rc = add_gemv(m, L.wqkv, "qkv", m->x, nullptr, L.attn_norm, m->qkv, nullptr))) return rc;
+    Op a;
+    a.kind = ARG_ATTN;
+    a.name = "pbx_attention_decode";
+    a.f = fattn;
+    a.grid = dim3(g.n_heads);
+    a.block = dim3(256);
+    a.attn = AttnArgsHost{m->qkv, m->kcache + l * layer_kv, m->vcache + l * layer_kv, m->rope,
+                          m->attn, m->state, g.n_heads, g.n_kv_heads, g.head_dim,
+                          (float)(1.0 / sqrt((double)g.head_dim))};
+    m->ops.push_back(a);
+    if ((rc = add_gemv(m, L.wo, "add", m->attn, nullptr, nullptr, m->x, nullptr))) return rc;
+    if ((rc = add_gemv(m, L.wgu, "qkv", m->x, nullptr, L.ffn_norm, m->gu, nullptr))) return rc;
+    if ((rc = add_gemv(m, L.wd, "swa", m->gu, m->gu + g.hidden_dim, nullptr, m->x, nullptr)))
+      return rc;
+  }
+  int n_tiles = 0;
+  const pbx_weight *head = m->output ? m->output : m->embd;
+  int rc = add_gemv(m, head, "lmh", m->x, nullptr, m->out_norm, m->logits, &n_tiles);
+  if (rc) return rc;
+  if (n_tiles > m->n_partials_cap)
+    return pbx_fail(c, PBX_EINVAL, "model: %d argmax partials exceed capacity %d", n_tiles,
+                    m->n_partials_cap);
+  Op am;
+  am.kind = ARG_ARGMAX;
+  am.name = "pbx_argmax_final";
+  am.f = pbx_kernel_by_name(c, am.name);
+  if (!am.f) return pbx_fail(c, PBX_ELOAD, "model: kernel pbx_argmax_final not found");
+  am.grid = dim3(1);
+  am.block = dim3(1024);
+  am.amax = ArgmaxArgsHost{m->partials, m->state, m->hist, n_tiles, m->hist_cap};
+  m->ops.push_back(am);
+  m->ops_ready = true;
+  return PBX_OK;
+}
+
+static int enqueue_ops(pbx_model *m) {
+  for (Op &op : m->ops) {
+    void *arg;
+    switch (op.kind) {
+      case ARG_GEMV: arg = &op.gemv; break;
+      case ARG_ATTN: arg = &op.attn; break;
+      case ARG_EMBED: arg = &op.embed; break;
+      default: arg = &op.amax; break;
+    }
+    void *args[] = {arg};
+    int rc = pbx_launch_fn(m->c, op.f, op.name.c_str(), op.grid, op.block, args, m->c->stream);
+    if (rc) return rc;
+  }
+  return PBX_OK;
+}
+
+static void drop_graph(pbx_model *m) {
+  if (m->exec) hipGraphExecDestroy(m->exec);
+  if (m->graph) hipGraphDestroy(m->graph);
+  m->exec = nullptr;
+  m->graph = nullptr;
+  m->graph_tried = m->graph_ok = false;
+}
+
+static bool use_graphs() {
+  const char *e = getenv("PBX_GRAPHS");
+  return !(e && e[0] == '0');
+}
+
+// One decode step on the context's stream: graph replay when capture worked.
+static int run_step(pbx_model *m) {
+  if (!m->ops_ready) {
+    int rc = build_ops(m);
+    if (rc) return rc;
+  }
+  if (use_graphs() && !m->graph_tried) {
+    m->graph_tried = true;
+    hipStream_t s = m->c->stream;
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+      int rc = enqueue_ops(m);
+      hipGraph_t g = nullptr;
+      hipError_t e = hipStreamEndCapture(s, &g);
+      if (!rc && e == hipSuccess && g &&
+          hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0) == hipSuccess) {
+        m->graph = g;
+        m->graph_ok = true;
+      } else if (g) {
+        hipGraphDestroy(g);
+      }
+    }
+    (void)hipGetLastError();
+  }
+  if (m->graph_ok) {
+    if (hipGraphLaunch(m->exec, m->c->stream) != hipSuccess)
+      return pbx_fail(m->c, PBX_EHIP, "model: hipGraphLaunch failed");
+    return PBX_OK;
+  }
+  return enqueue_ops(m);
+}
+
+static int set_state(pbx_model *m, int pos, int token, int step) {
+  hipFunction_t f = pbx_kernel_by_name(m->c, "pbx_set_state");
+  if (!f) return pbx_fail(m->c, PBX_ELOAD, "model: kernel pbx_set_state not found");
+  int *st = m->state;
+  void *args[] = {&st, &pos, &token, &step};
+  return pbx_launch_fn(m->c, f, "pbx_set_state", dim3(1), dim3(64), args, m->c->stream);
+}
+
+static int kv_fill(pbx_model *m, int from) {
+  hipFunction_t f = pbx_kernel_by_name(m->c, "pbx_kv_fill");
+  if (!f) return pbx_fail(m->c, PBX_ELOAD, "model: kernel pbx_kv_fill not found");
+  int64_t stride = (int64_t)m->cfg.max_seq * m->kvdim;
+  int64_t off = (int64_t)from * m->kvdim;
+  int64_t count = stride - off;
+  int nl = m->cfg.n_layers;
+  if (count <= 0) return PBX_OK;
+  float *k = m->kcache, *v = m->vcache;
+  void *args[] = {&k, &v, &stride, &off, &count, &nl};
+  const int64_t total = count * nl;
+  return pbx_launch_fn(m->c, f, "pbx_kv_fill", dim3((unsigned)((total + 255) / 256)), dim3(256),
+                       args, m->c->stream);
+}
+
+static int dalloc(pbx_model *m, void **p, size_t bytes) {
+  if (hipMalloc(p, bytes) != hipSuccess) {
+    *p = nullptr;
+    return pbx_fail(m->c, PBX_ENOMEM, "model: hipMalloc(%zu) failed", bytes);
+  }
+  m->bytes += bytes;
+  return PBX_OK;
+}
+
+static void model_release(pbx_model *m) {
+  if (!m) return;
+  drop_graph(m);
+  for (Layer &L : m->layers) {
+    pbx_weight_release(L.wqkv);
+    pbx_weight_release(L.wo);
+    pbx_weight_release(L.wgu);
+    pbx_weight_release(L.wd);
+    if (L.attn_norm) hipFree(L.attn_norm);
+    if (L.ffn_norm) hipFree(L.ffn_norm);
+  }
+  pbx_weight_release(m->embd);
+  pbx_weight_release(m->output);
+  for (void *p : {(void *)m->out_norm, (void *)m->kcache, (void *)m->vcache, (void *)m->rope,
+                  (void *)m->x, (void *)m->qkv, (void *)m->attn, (void *)m->gu, (void *)m->logits,
+                  (void *)m->partials, (void *)m->state, (void *)m->hist})
+    if (p) hipFree(p);
+  m->magic = 0;
+  delete m;
+}
+
+void pbx_model_release_all(pbx_ctx *c) {
+  auto *list = (std::vector<pbx_model *> *)c->models;
+  if (!list) return;
+  for (pbx_model *m : *list) model_release(m);
+  delete list;
+  c->models = nullptr;
+}
+
+static bool is_weight_type(int t) {
+  return t == PBX_TYPE_Q4_0 || t == PBX_TYPE_Q8_0 || t == PBX_TYPE_F32;
+}
+
+extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_model **out) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_create: ctx is NULL");
+  if (!cfg || !out) return pbx_fail(c, PBX_EINVAL, "pbx_model_create: NULL argument");
+  *out = nullptr;
+  const pbx_model_config &g = *cfg;
+  if (g.dim <= 0 || g.hidden_dim <= 0 || g.n_layers <= 0 || g.n_heads <= 0 ||
+      g.n_kv_heads <= 0 || g.head_dim <= 0 || g.vocab_size <= 0 || g.max_seq <= 0)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_create: every size must be positive");
+  if (g.dim % 32 || g.hidden_dim % 32)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_create: dim and hidden_dim must be multiples of 32");
+  if (g.n_heads * g.head_dim != g.dim || g.n_heads % g.n_kv_heads)
+    return pbx_fail(c, PBX_EINVAL,
+                    "pbx_model_create: need n_heads*head_dim == dim and n_kv_heads | n_heads");
+  if (g.head_dim % 4 || g.head_dim < 32 || g.head_dim > 256)
+    return pbx_fail(c, PBX_ENOTSUP, "pbx_model_create: head_dim %d unsupported (32..256, %%4)",
+                    g.head_dim);
+  if (g.max_seq > 8192)
+    return pbx_fail(c, PBX_ENOTSUP, "pbx_model_create: max_seq %d > 8192", g.max_seq);
+  if (!is_weight_type(g.weight_type) || !is_weight_type(g.embed_type) ||
+      (g.output_type >= 0 && !is_weight_type(g.output_type)))
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_create: unsupported weight type");
+  if (g.rope_theta <= 0 || !(g.rms_eps >= 0))
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_create: bad rope_theta / rms_eps");
+  if (hipSetDevice(c->device) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_create: hipSetDevice failed");
+
+  pbx_model *m = new pbx_model();
+  m->magic = PBX_MODEL_MAGIC;
+  m->c = c;
+  m->cfg = g;
+  m->kvdim = g.n_kv_heads * g.head_dim;
+  m->qkv_rows = g.dim + 2 * m->kvdim;
+  m->layers.resize(g.n_layers);
+  int rc = PBX_OK;
+  for (int l = 0; l < g.n_layers && !rc; ++l) {
+    Layer &L = m->layers[l];
+    if (!rc) rc = pbx_weight_alloc(c, g.weight_type, m->qkv_rows, g.dim, &L.wqkv);
+    if (!rc) rc = pbx_weight_alloc(c, g.weight_type, g.dim, g.dim, &L.wo);
+    if (!rc) rc = pbx_weight_alloc(c, g.weight_type, 2 * (int64_t)g.hidden_dim, g.dim, &L.wgu);
+    if (!rc) rc = pbx_weight_alloc(c, g.weight_type, g.dim, g.hidden_dim, &L.wd);
+    if (!rc) rc = dalloc(m, (void **)&L.attn_norm, (size_t)g.dim * 4);
+    if (!rc) rc = dalloc(m, (void **)&L.ffn_norm, (size_t)g.dim * 4);
+    if (!rc)
+      m->bytes += L.wqkv->bytes + L.wo->bytes + L.wgu->bytes + L.wd->bytes;
+  }
+  if (!rc) rc = pbx_weight_alloc(c, g.embed_type, g.vocab_size, g.dim, &m->embd);
+  if (!rc) m->bytes += m->embd->bytes;
+  if (!rc && g.output_type >= 0) {
+    rc = pbx_weight_alloc(c, g.output_type, g.vocab_size, g.dim, &m->output);
+    if (!rc) m->bytes += m->output->bytes;
+  }
+  const size_t kv_bytes = (size_t)g.n_layers * g.max_seq * m->kvdim * 4;
+  if (!rc) rc = dalloc(m, (void **)&m->out_norm, (size_t)g.dim * 4);
+  if (!rc) rc = dalloc(m, (void **)&m->kcache, kv_bytes);
+  if (!rc) rc = dalloc(m, (void **)&m->vcache, kv_bytes);
+  if (!rc) rc = dalloc(m, (void **)&m->rope, (size_t)g.max_seq * g.head_dim * 4);
+  if (!rc) rc = dalloc(m, (void **)&m->x, (size_t)g.dim * 4);
+  if (!rc) rc = dalloc(m, (void **)&m->qkv, (size_t)m->qkv_rows * 4);
+  if (!rc) rc = dalloc(m, (void **)&m->attn, (size_t)g.dim * 4);
+  if (!rc) rc = dalloc(m, (void **)&m->gu, (size_t)g.hidden_dim * 2 * 4);
+  if (!rc) rc = dalloc(m, (void **)&m->logits, (size_t)g.vocab_size * 4);
+  m->n_partials_cap = g.vocab_size + 256;  // at most one tile per row (+ small-kernel slack)
+  if (!rc) rc = dalloc(m, (void **)&m->partials, (size_t)m->n_partials_cap * 8);
+  if (!rc) rc = dalloc(m, (void **)&m->state, 64);
+  m->hist_cap = g.max_seq;
+  if (!rc) rc = dalloc(m, (void **)&m->hist, (size_t)m->hist_cap * 4);
+  if (!rc) {
+    // RoPE table, llama.js:163-190: pair i of a head rotates by
+    // pos / theta^(2i/head_dim), evaluated in double as the reference does.
+    std::vector<float> tab((size_t)g.max_seq * g.head_dim);
+    for (int p = 0; p < g.max_seq; ++p)
+      for (int i = 0; i < g.head_dim; i += 2) {
+        const double freq = 1.0 / pow(g.rope_theta, (double)i / g.head_dim);
+        const double ang = p * freq;
+        tab[(size_t)p * g.head_dim + i] = (float)cos(ang);
+        tab[(size_t)p * g.head_dim + i + 1] = (float)sin(ang);
+      }
+    if (hipMemcpy(m->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemsetAsync(m->kcache, 0, kv_bytes, c->stream) != hipSuccess ||
+        hipMemsetAsync(m->vcache, 0, kv_bytes, c->stream) != hipSuccess ||
+        hipMemsetAsync(m->state, 0, 64, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+      rc = pbx_fail(c, PBX_EHIP, "pbx_model_create: initialisation copies failed");
+  }
+  if (rc) {
+    hipStreamSynchronize(c->stream);
+    model_release(m);
+    return rc;
+  }
+  auto *list = (std::vector<pbx_model *> *)c->models;
+  if (!list) c->models = list = new std::vector<pbx_model *>();
+  list->push_back(m);
+  *out = m;
+  return PBX_OK;
+}
+
+extern "C" int pbx_model_free(pbx_model *m) {
+  if (!m) return PBX_OK;
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_free: not a live model");
+  pbx_ctx *c = m->c;
+  hipStreamSynchronize(c->stream);
+  auto *list = (std::vector<pbx_model *> *)c->models;
+  if (list) list->erase(std::remove(list->begin(), list->end(), m), list->end());
+  model_release(m);
+  return PBX_OK;
+}
+
+static size_t expect_bytes(int type, int64_t N, int64_t K) {
+  return (size_t)N * (size_t)(K / 32) * pbx_type_block_bytes(type);
+}
+
+extern "C" int pbx_model_set_tensor(pbx_model *m, int tensor, int layer, const void *data,
+                                    size_t nbytes) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_set_tensor: not a live model");
+  pbx_ctx *c = m->c;
+  const pbx_model_config &g = m->cfg;
+  if (!data) return pbx_fail(c, PBX_EINVAL, "pbx_model_set_tensor: data is NULL");
+  if (hipSetDevice(c->device) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_set_tensor: hipSetDevice failed");
+  const bool per_layer = tensor >= PBX_T_ATTN_NORM;
+  if (per_layer && (layer < 0 || layer >= g.n_layers))
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_set_tensor: layer %d out of range [0, %d)", layer,
+                    g.n_layers);
+  auto copy_f32 = [&](float *dst, int64_t n) -> int {
+    if (nbytes < (size_t)n * 4)
+      return pbx_fail(c, PBX_EINVAL, "pbx_model_set_tensor: %zu bytes, tensor %d needs %lld",
+                      nbytes, tensor, (long long)n * 4);
+    if (hipMemcpy(dst, data, (size_t)n * 4, hipMemcpyHostToDevice) != hipSuccess)
+      return pbx_fail(c, PBX_EHIP, "pbx_model_set_tensor: copy failed");
+    return PBX_OK;
+  };
+  auto rows = [&](pbx_weight *w, int64_t row0, int64_t n) -> int {
+    const size_t need = expect_bytes(w->type, n, w->K);
+    if (nbytes < need)
+      return pbx_fail(c, PBX_EINVAL, "pbx_model_set_tensor: %zu bytes, tensor %d needs %zu",
+                      nbytes, tensor, need);
+    return pbx_weight_write_rows(c, w, row0, n, data);
+  };
+  int rc;
+  unsigned bit = 1u << tensor;
+  switch (tensor) {
+    case PBX_T_TOKEN_EMBD: rc = rows(m->embd, 0, g.vocab_size); break;
+    case PBX_T_OUTPUT:
+      if (!m->output)
+        return pbx_fail(c, PBX_EINVAL, "pbx_model_set_tensor: LM head is tied to token_embd");
+      rc = rows(m->output, 0, g.vocab_size);
+      break;
+    case PBX_T_OUTPUT_NORM: rc = copy_f32(m->out_norm, g.dim); break;
+    case PBX_T_ATTN_NORM: rc = copy_f32(m->layers[layer].attn_norm, g.dim); break;
+    case PBX_T_FFN_NORM: rc = copy_f32(m->layers[layer].ffn_norm, g.dim); break;
+    case PBX_T_ATTN_Q: rc = rows(m->layers[layer].wqkv, 0, g.dim); break;
+    case PBX_T_ATTN_K: rc = rows(m->layers[layer].wqkv, g.dim, m->kvdim); break;
+    case PBX_T_ATTN_V: rc = rows(m->layers[layer].wqkv, g.dim + m->kvdim, m->kvdim); break;
+    case PBX_T_ATTN_OUTPUT: rc = rows(m->layers[layer].wo, 0, g.dim); break;
+    case PBX_T_FFN_GATE: rc = rows(m->layers[layer].wgu, 0, g.hidden_dim); break;
+    case PBX_T_FFN_UP: rc = rows(m->layers[layer].wgu, g.hidden_dim, g.hidden_dim); break;
+    case PBX_T_FFN_DOWN: rc = rows(m->layers[layer].wd, 0, g.dim); break;
+    default:
+      return pbx_fail(c, PBX_EINVAL, "pbx_model_set_tensor: unknown tensor id %d", tensor);
+  }
+  if (rc) return rc;
+  if (per_layer)
+    m->layers[layer].set_mask |= bit;
+  else
+    m->global_mask |= bit;
+  return PBX_OK;
+}
+
+static int check_complete(pbx_model *m) {
+  const unsigned layer_all = (1u << PBX_T_ATTN_NORM) | (1u << PBX_T_FFN_NORM) |
+                             (1u << PBX_T_ATTN_Q) | (1u << PBX_T_ATTN_K) | (1u << PBX_T_ATTN_V) |
+                             (1u << PBX_T_ATTN_OUTPUT) | (1u << PBX_T_FFN_GATE) |
+                             (1u << PBX_T_FFN_UP) | (1u << PBX_T_FFN_DOWN);
+  unsigned global_all = (1u << PBX_T_TOKEN_EMBD) | (1u << PBX_T_OUTPUT_NORM);
+  if (m->output) global_all |= 1u << PBX_T_OUTPUT;
+  if ((m->global_mask & global_all) != global_all)
+    return pbx_fail(m->c, PBX_EINVAL, "model: token_embd/output_norm%s not set",
+                    m->output ? "/output" : "");
+  for (int l = 0; l < m->cfg.n_layers; ++l)
+    if ((m->layers[l].set_mask & layer_all) != layer_all)
+      return pbx_fail(m->c, PBX_EINVAL, "model: layer %d is missing tensors (mask 0x%x)", l,
+                      m->layers[l].set_mask);
+  return PBX_OK;
+}
+
+extern "C" int pbx_model_forward(pbx_model *m, const int32_t *tokens, int n_tokens,
+                                 int start_pos, float *logits, int32_t *next_token) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_forward: not a live model");
+  pbx_ctx *c = m->c;
+  const pbx_model_config &g = m->cfg;
+  if (!tokens || n_tokens <= 0)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_forward: need at least one token");
+  if (start_pos < 0 || (int64_t)start_pos + n_tokens > g.max_seq)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_forward: positions [%d, %lld) exceed max_seq %d",
+                    start_pos, (long long)start_pos + n_tokens, g.max_seq);
+  for (int t = 0; t < n_tokens; ++t)
+    if (tokens[t] < 0 || tokens[t] >= g.vocab_size)
+      return pbx_fail(c, PBX_EINVAL, "pbx_model_forward: token %d out of range [0, %d)",
+                      tokens[t], g.vocab_size);
+  int rc = check_complete(m);
+  if (rc) return rc;
+  if (hipSetDevice(c->device) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_forward: hipSetDevice failed");
+  for (int t = 0; t < n_tokens; ++t) {
+    if ((rc = set_state(m, start_pos + t, tokens[t], 0))) return rc;
+    if ((rc = run_step(m))) return rc;
+  }
+  if (logits && hipMemcpyAsync(logits, m->logits, (size_t)g.vocab_size * 4,
+                               hipMemcpyDeviceToHost, c->stream) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_forward: logits copy failed");
+  int st[3] = {0, 0, 0};
+  if (hipMemcpyAsync(st, m->state, sizeof st, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_forward: step failed on the device");
+  if (next_token) *next_token = st[1];
+  return PBX_OK;
+}
+
+extern "C" int pbx_model_generate(pbx_model *m, int32_t token, int start_pos, int n_steps,
+                                  int32_t *out_tokens, float *last_logits) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_generate: not a live model");
+  pbx_ctx *c = m->c;
+  const pbx_model_config &g = m->cfg;
+  if (n_steps <= 0 || !out_tokens)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_generate: need n_steps > 0 and an output array");
+  if (token < 0 || token >= g.vocab_size)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_generate: token %d out of range", token);
+  if (start_pos < 0 || (int64_t)start_pos + n_steps > g.max_seq)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_generate: positions [%d, %lld) exceed max_seq %d",
+                    start_pos, (long long)start_pos + n_steps, g.max_seq);
+  int rc = check_complete(m);
+  if (rc) return rc;
+  if (hipSetDevice(c->device) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_generate: hipSetDevice failed");
+  if ((rc = set_state(m, start_pos, token, 0))) return rc;
+  for (int i = 0; i < n_steps; ++i)
+    if ((rc = run_step(m))) return rc;
+  if (hipMemcpyAsync(out_tokens, m->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost,
+                     c->stream) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_generate: token copy failed");
+  if (last_logits && hipMemcpyAsync(last_logits, m->logits, (size_t)g.vocab_size * 4,
+                                    hipMemcpyDeviceToHost, c->stream) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_generate: logits copy failed");
+  if (hipStreamSynchronize(c->stream) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_generate: step failed on the device");
+  return PBX_OK;
+}
+
+extern "C" int pbx_model_reset_cache(pbx_model *m) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_reset_cache: not a live model");
+  return kv_fill(m, 0);
+}
+
+extern "C" int pbx_model_rollback(pbx_model *m, int pos) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_rollback: not a live model");
+  if (pos < 0 || pos > m->cfg.max_seq)
+    return pbx_fail(m->c, PBX_EINVAL, "pbx_model_rollback: pos %d outside [0, %d]", pos,
+                    m->cfg.max_seq);
+  return kv_fill(m, pos);
+}
+
+extern "C" int pbx_model_info(const pbx_model *m, size_t *device_bytes, int *uses_graph) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_info: not a live model");
+  if (device_bytes) *device_bytes = m->bytes;
+  if (uses_graph) *uses_graph = m->graph_ok ? 1 : 0;
+  return PBX_OK;
+}

@@ -50,7 +50,7 @@ static const char *const kKernelNames[PBX_K_COUNT] = {
 
 // Code objects built from purebee_amd/csrc/kernels/*.hip, found next to this
 // library (or in the directory named by PBX_KERNEL_DIR).
-static const char *const kModuleFiles[] = {"pbx_gemv.hsaco"};
+static const char *const kModuleFiles[] = {"pbx_gemv.hsaco", "pbx_decode.hsaco"};
 static const int kModuleCount = (int)(sizeof kModuleFiles / sizeof kModuleFiles[0]);
 
 static std::string code_object_dir() {
@@ -170,6 +170,29 @@ extern "C" int pbx_device_info(pbx_ctx *c, char *name, size_t cap, int *cu_count
   return PBX_OK;
 }
 
+hipFunction_t pbx_kernel_by_name(pbx_ctx *c, const std::string &name) {
+  auto it = c->named.find(name);
+  if (it != c->named.end()) return it->second;
+  hipFunction_t f = nullptr;
+  for (int m = 0; m < PBX_MAX_MODULES && !f; ++m) {
+    hipFunction_t g = nullptr;
+    if (c->modules[m] && hipModuleGetFunction(&g, c->modules[m], name.c_str()) == hipSuccess) f = g;
+  }
+  (void)hipGetLastError();
+  if (f) c->named[name] = f;
+  return f;
+}
+
+int pbx_launch_fn(pbx_ctx *c, hipFunction_t f, const char *name, dim3 grid, dim3 block,
+                  void **args, hipStream_t stream) {
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return PBX_OK;
+  hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0,
+                                       stream ? stream : c->stream, args, nullptr);
+  if (e != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "launch of %s failed: %s", name, hipGetErrorString(e));
+  return PBX_OK;
+}
+
 int pbx_launch(pbx_ctx *c, int kernel, dim3 grid, dim3 block, void **args,
                hipStream_t stream) {
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return PBX_OK;
@@ -246,8 +269,8 @@ static int stage_copy(pbx_ctx *c, void *dst, const void *src, size_t bytes) {
 }
 
 // Raw GGUF rows -> planes, chunk by chunk through device staging.
-static int stage_repack(pbx_ctx *c, pbx_weight *w, const uint8_t *src, int kernel,
-                        size_t row_bytes) {
+static int stage_repack(pbx_ctx *c, pbx_weight *w, int64_t first_row, int64_t n_rows,
+                        const uint8_t *src, int kernel, size_t row_bytes) {
   for (int i = 0; i < 2; ++i) {
     int rc = pbx_ensure_pinned(c, &c->h_stage[i], &c->h_stage_cap[i], kStageBytes);
     if (rc) return rc;
@@ -258,15 +281,15 @@ static int stage_repack(pbx_ctx *c, pbx_weight *w, const uint8_t *src, int kerne
   if ((size_t)rows_per_chunk * row_bytes > kStageBytes)
     return pbx_fail(c, PBX_ENOTSUP, "row of %zu bytes exceeds the staging buffer", row_bytes);
   int slot = 0;
-  for (int64_t r0 = 0; r0 < w->N; r0 += rows_per_chunk) {
-    const int64_t rows = std::min(rows_per_chunk, w->N - r0);
+  for (int64_t r0 = 0; r0 < n_rows; r0 += rows_per_chunk) {
+    const int64_t rows = std::min(rows_per_chunk, n_rows - r0);
     const size_t n = (size_t)rows * row_bytes;
     HIPCHK(c, hipEventSynchronize(c->ev_stage[slot]));
     memcpy(c->h_stage[slot], src + (size_t)r0 * row_bytes, n);
     HIPCHK(c, hipMemcpyAsync(c->d_stage[slot], c->h_stage[slot], n, hipMemcpyHostToDevice,
                              c->stream));
     int B = (int)w->B;
-    int64_t row0 = r0, nrows = rows;
+    int64_t row0 = first_row + r0, nrows = rows;
     void *raw = c->d_stage[slot];
     void *args[] = {&raw, &w->qs, &w->d, &row0, &nrows, &B};
     const int64_t blocks = rows * w->B;
@@ -290,6 +313,72 @@ size_t pbx_type_block_bytes(int type) {
 
 static bool weight_ok(const pbx_weight *w) { return w && w->magic == PBX_WEIGHT_MAGIC; }
 
+int pbx_weight_alloc(pbx_ctx *c, int type, int64_t N, int64_t K, pbx_weight **out) {
+  *out = nullptr;
+  if (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0 && type != PBX_TYPE_F32)
+    return pbx_fail(c, PBX_EINVAL, "unsupported weight type %d", type);
+  if (N <= 0 || K <= 0 || K % 32 != 0)
+    return pbx_fail(c, PBX_EINVAL, "bad shape N=%lld K=%lld (need N>0, K>0, K%%32==0)",
+                    (long long)N, (long long)K);
+  if (N > INT32_MAX || K / 32 > (1 << 20))
+    return pbx_fail(c, PBX_ENOTSUP, "shape N=%lld K=%lld too large", (long long)N, (long long)K);
+  HIPCHK(c, hipSetDevice(c->device));
+  pbx_weight *w = new pbx_weight();
+  w->magic = PBX_WEIGHT_MAGIC;
+  w->type = type;
+  w->N = N;
+  w->K = K;
+  w->B = K / 32;
+  w->Npad = (N + 63) / 64 * 64;
+  size_t qs_bytes, d_bytes = 0;
+  if (type == PBX_TYPE_F32) {
+    qs_bytes = (size_t)w->Npad * K * 4;
+  } else {
+    qs_bytes = (size_t)w->Npad * w->B * (type == PBX_TYPE_Q4_0 ? 16 : 32);
+    d_bytes = (size_t)w->Npad * w->B * 2;
+  }
+  if (hipMalloc(&w->qs, qs_bytes) != hipSuccess) {
+    delete w;
+    return pbx_fail(c, PBX_ENOMEM, "hipMalloc(%zu) failed", qs_bytes);
+  }
+  if (d_bytes && hipMalloc(&w->d, d_bytes) != hipSuccess) {
+    hipFree(w->qs);
+    delete w;
+    return pbx_fail(c, PBX_ENOMEM, "hipMalloc(%zu) failed", d_bytes);
+  }
+  w->bytes = qs_bytes + d_bytes;
+  // Pad rows read as zero weights with zero scales.
+  if (hipMemsetAsync(w->qs, 0, qs_bytes, c->stream) != hipSuccess ||
+      (d_bytes && hipMemsetAsync(w->d, 0, d_bytes, c->stream) != hipSuccess)) {
+    hipFree(w->qs);
+    if (w->d) hipFree(w->d);
+    delete w;
+    return pbx_fail(c, PBX_EHIP, "hipMemsetAsync failed");
+  }
+  *out = w;
+  return PBX_OK;
+}
+
+void pbx_weight_release(pbx_weight *w) {
+  if (!w) return;
+  w->magic = 0;
+  if (w->qs) hipFree(w->qs);
+  if (w->d) hipFree(w->d);
+  delete w;
+}
+
+int pbx_weight_write_rows(pbx_ctx *c, pbx_weight *w, int64_t row0, int64_t rows,
+                          const void *host) {
+  if (row0 < 0 || rows <= 0 || row0 + rows > w->N)
+    return pbx_fail(c, PBX_EINVAL, "rows [%lld, %lld) outside a weight of %lld rows",
+                    (long long)row0, (long long)(row0 + rows), (long long)w->N);
+  const size_t row_bytes = (size_t)w->B * pbx_type_block_bytes(w->type);
+  if (w->type == PBX_TYPE_F32)
+    return stage_copy(c, (char *)w->qs + (size_t)row0 * row_bytes, host, (size_t)rows * row_bytes);
+  return stage_repack(c, w, row0, rows, (const uint8_t *)host,
+                      w->type == PBX_TYPE_Q4_0 ? PBX_K_REPACK_Q4_0 : PBX_K_REPACK_Q8_0, row_bytes);
+}
+
 extern "C" int pbx_weight_upload(pbx_ctx *c, int type, int64_t N, int64_t K,
                                  const void *host, size_t nbytes, pbx_weight **out) {
   if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_weight_upload: ctx is NULL");
@@ -301,60 +390,19 @@ extern "C" int pbx_weight_upload(pbx_ctx *c, int type, int64_t N, int64_t K,
     return pbx_fail(c, PBX_EINVAL,
                     "pbx_weight_upload: bad shape N=%lld K=%lld (need N>0, K>0, K%%32==0)",
                     (long long)N, (long long)K);
-  if (N > INT32_MAX || K / 32 > (1 << 20))
-    return pbx_fail(c, PBX_ENOTSUP, "pbx_weight_upload: shape N=%lld K=%lld too large",
-                    (long long)N, (long long)K);
-  const int64_t B = K / 32;
-  const size_t row_bytes = (size_t)B * pbx_type_block_bytes(type);
-  const size_t need = (size_t)N * row_bytes;
   if (!host) return pbx_fail(c, PBX_EINVAL, "pbx_weight_upload: host buffer is NULL");
+  const size_t need = (size_t)N * (size_t)(K / 32) * pbx_type_block_bytes(type);
   if (nbytes < need)
     return pbx_fail(c, PBX_EINVAL,
                     "pbx_weight_upload: buffer holds %zu bytes, N=%lld x K=%lld needs %zu",
                     nbytes, (long long)N, (long long)K, need);
-  HIPCHK(c, hipSetDevice(c->device));
-
-  pbx_weight *w = new pbx_weight();
-  w->magic = PBX_WEIGHT_MAGIC;
-  w->type = type;
-  w->N = N;
-  w->K = K;
-  w->B = B;
-  w->Npad = (N + 63) / 64 * 64;
-  size_t qs_bytes, d_bytes = 0;
-  if (type == PBX_TYPE_F32) {
-    qs_bytes = (size_t)w->Npad * K * 4;
-  } else {
-    qs_bytes = (size_t)w->Npad * B * (type == PBX_TYPE_Q4_0 ? 16 : 32);
-    d_bytes = (size_t)w->Npad * B * 2;
-  }
-  if (hipMalloc(&w->qs, qs_bytes) != hipSuccess) {
-    delete w;
-    return pbx_fail(c, PBX_ENOMEM, "pbx_weight_upload: hipMalloc(%zu) failed", qs_bytes);
-  }
-  if (d_bytes && hipMalloc(&w->d, d_bytes) != hipSuccess) {
-    hipFree(w->qs);
-    delete w;
-    return pbx_fail(c, PBX_ENOMEM, "pbx_weight_upload: hipMalloc(%zu) failed", d_bytes);
-  }
-  w->bytes = qs_bytes + d_bytes;
-  int rc = PBX_OK;
-  // Pad rows read as zero weights with zero scales.
-  if (hipMemsetAsync(w->qs, 0, qs_bytes, c->stream) != hipSuccess ||
-      (d_bytes && hipMemsetAsync(w->d, 0, d_bytes, c->stream) != hipSuccess))
-    rc = pbx_fail(c, PBX_EHIP, "pbx_weight_upload: hipMemsetAsync failed");
-  if (!rc) {
-    if (type == PBX_TYPE_F32)
-      rc = stage_copy(c, w->qs, host, need);
-    else
-      rc = stage_repack(c, w, (const uint8_t *)host,
-                        type == PBX_TYPE_Q4_0 ? PBX_K_REPACK_Q4_0 : PBX_K_REPACK_Q8_0, row_bytes);
-  }
+  pbx_weight *w = nullptr;
+  int rc = pbx_weight_alloc(c, type, N, K, &w);
+  if (rc) return rc;
+  rc = pbx_weight_write_rows(c, w, 0, N, host);
   if (rc) {
     hipStreamSynchronize(c->stream);
-    hipFree(w->qs);
-    if (w->d) hipFree(w->d);
-    delete w;
+    pbx_weight_release(w);
     return rc;
   }
   *out = w;
@@ -411,10 +459,7 @@ extern "C" int pbx_weight_free(pbx_ctx *c, pbx_weight *w) {
   if (!weight_ok(w)) return pbx_fail(c, PBX_EINVAL, "pbx_weight_free: not a live weight handle");
   HIPCHK(c, hipSetDevice(c->device));
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  w->magic = 0;
-  if (w->qs) hipFree(w->qs);
-  if (w->d) hipFree(w->d);
-  delete w;
+  pbx_weight_release(w);
   return PBX_OK;
 }
 

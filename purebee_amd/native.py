@@ -27,7 +27,21 @@ EXPORTS = (
     "pbx_quantize_q8_0", "pbx_quantize_q4_0", "pbx_quantize_q8_ref", "pbx_synth_normal",
     "pbx_dev_alloc", "pbx_dev_free", "pbx_memcpy_h2d", "pbx_memcpy_d2h", "pbx_memset_dev",
     "pbx_sync", "pbx_timer_start", "pbx_timer_stop", "pbx_bench_linear",
+    "pbx_model_create", "pbx_model_free", "pbx_model_set_tensor", "pbx_model_forward",
+    "pbx_model_generate", "pbx_model_reset_cache", "pbx_model_rollback", "pbx_model_info",
 )
+
+# Tensor ids of pbx_model_set_tensor (GGUF tensor names, gguf.js:378-410).
+T_TOKEN_EMBD, T_OUTPUT, T_OUTPUT_NORM, T_ATTN_NORM, T_FFN_NORM = 0, 1, 2, 3, 4
+T_ATTN_Q, T_ATTN_K, T_ATTN_V, T_ATTN_OUTPUT = 5, 6, 7, 8
+T_FFN_GATE, T_FFN_UP, T_FFN_DOWN = 9, 10, 11
+
+
+class ModelConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab_size",
+        "max_seq", "weight_type", "embed_type", "output_type")] + \
+        [("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_double)]
 
 
 class PbxError(RuntimeError):
@@ -91,6 +105,15 @@ def load_library():
         "pbx_bench_linear": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.POINTER(_vp),
                                             ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i64,
                                             ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
+        "pbx_model_create": (ctypes.c_int, [_vp, ctypes.POINTER(ModelConfig), ctypes.POINTER(_vp)]),
+        "pbx_model_free": (ctypes.c_int, [_vp]),
+        "pbx_model_set_tensor": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t]),
+        "pbx_model_forward": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+        "pbx_model_generate": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+        "pbx_model_reset_cache": (ctypes.c_int, [_vp]),
+        "pbx_model_rollback": (ctypes.c_int, [_vp, ctypes.c_int]),
+        "pbx_model_info": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_size_t),
+                                          ctypes.POINTER(ctypes.c_int)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -272,3 +295,60 @@ class Context:
         ms = ctypes.c_double()
         self._call("pbx_bench_linear", self._p, n, W, X, Y, M, reps, ctypes.byref(ms))
         return ms.value
+
+
+class Model:
+    """A resident Llama-family model with the on-GPU decode step (pbx_model_*)."""
+
+    def __init__(self, ctx, dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, max_seq,
+                 weight_type, embed_type, output_type=-1, head_dim=None, rms_eps=1e-5,
+                 rope_theta=10000.0):
+        self.ctx = ctx
+        hd = head_dim or dim // n_heads
+        self.cfg = ModelConfig(dim, hidden_dim, n_layers, n_heads, n_kv_heads, hd, vocab_size,
+                               max_seq, weight_type, embed_type, output_type, rms_eps, rope_theta)
+        p = _vp()
+        ctx._call("pbx_model_create", ctx._p, ctypes.byref(self.cfg), ctypes.byref(p))
+        self._m = p.value
+        self.vocab = vocab_size
+
+    def _mcall(self, name, *args):
+        rc = getattr(self.ctx.L, name)(self._m, *args)
+        if rc != 0:
+            msg = self.ctx.L.pbx_last_error(self.ctx._p)
+            raise PbxError(rc, msg.decode() if msg else "")
+
+    def set_tensor(self, tensor, layer, data):
+        data = np.ascontiguousarray(data)
+        self._mcall("pbx_model_set_tensor", tensor, layer, data.ctypes.data, data.nbytes)
+
+    def forward(self, tokens, start_pos, want_logits=True):
+        toks = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.vocab, np.float32) if want_logits else None
+        nxt = ctypes.c_int32()
+        self._mcall("pbx_model_forward", toks.ctypes.data, len(toks), start_pos,
+                    None if logits is None else logits.ctypes.data, ctypes.byref(nxt))
+        return logits, nxt.value
+
+    def generate(self, token, start_pos, n_steps, want_logits=False):
+        out = np.empty(n_steps, np.int32)
+        logits = np.empty(self.vocab, np.float32) if want_logits else None
+        self._mcall("pbx_model_generate", int(token), start_pos, n_steps, out.ctypes.data,
+                    None if logits is None else logits.ctypes.data)
+        return (out, logits) if want_logits else out
+
+    def reset_cache(self):
+        self._mcall("pbx_model_reset_cache")
+
+    def rollback(self, pos):
+        self._mcall("pbx_model_rollback", pos)
+
+    def info(self):
+        b, g = ctypes.c_size_t(), ctypes.c_int()
+        self._mcall("pbx_model_info", ctypes.byref(b), ctypes.byref(g))
+        return {"device_bytes": b.value, "graph": bool(g.value)}
+
+    def free(self):
+        if self._m:
+            self._mcall("pbx_model_free")
+            self._m = None

@@ -1,0 +1,66 @@
+"""Pins the oracle's Llama forward (oracle/llama_ref.c) against the
+reference's own LlamaRuntime outputs (tests/golden/llama_tiny.json, written
+by tests/golden/make_llama_fixture.js from llama.js), plus the invariants the
+reference's two forward modes imply."""
+import numpy as np
+import pytest
+
+import oracle
+from tests.golden import llama_fixture as lf
+
+
+@pytest.fixture(scope="module")
+def fixture():
+    return lf.load()
+
+
+def oracle_model(fx):
+    c = fx["config"]
+    ref = oracle.LlamaRef(c["dim"], c["hiddenDim"], c["nLayers"], c["nHeads"], c["nKvHeads"],
+                          c["dim"] // c["nHeads"], c["vocabSize"], c["seqLen"], c["ropeTheta"])
+    for tid, layer, w in lf.weights(fx):
+        ref.set(tid, layer, w)
+    return ref
+
+
+def test_oracle_matches_reference_llama_js(fixture):
+    ref = oracle_model(fixture)
+    for st in fixture["steps"]:
+        got = ref.forward(st["tokens"], st["pos"])
+        want = np.asarray(st["logits"], np.float32)
+        # the reference accumulates LINEAR in f32 (engine.js:222-240), the
+        # oracle in double: they agree far inside the 2e-3 logit bar
+        assert np.abs(got - want).max() < 1e-4, (st["pos"], np.abs(got - want).max())
+        assert oracle.argmax(got) == st["argmax"]
+    ref.close()
+
+
+def test_prefill_equals_sequential_decode(fixture):
+    """llama.js forward over a prompt at once (causal mask) and token by token
+    must agree: the reference's prefill and decode modes."""
+    a = oracle_model(fixture)
+    b = oracle_model(fixture)
+    prompt = fixture["steps"][0]["tokens"]
+    la = a.forward(prompt, 0)
+    for p, t in enumerate(prompt):
+        lb = b.forward([t], p)
+    assert np.abs(la - lb).max() < 1e-5
+    a.close()
+    b.close()
+
+
+def test_position_zero_attention_is_v(fixture):
+    """With one cached position, softmax over a single score is 1 and the
+    attention output equals V: zeroing wq and wk changes nothing at pos 0."""
+    c = fixture["config"]
+    base = oracle_model(fixture)
+    alt = oracle_model(fixture)
+    for tid, layer, w in lf.weights(fixture):
+        if tid in (lf.T_Q, lf.T_K):
+            alt.set(tid, layer, np.zeros_like(w))
+    tok = [7]
+    assert np.array_equal(base.forward(tok, 0), alt.forward(tok, 0))
+    # ... but not at pos 1, where the scores matter
+    assert not np.array_equal(base.forward([8], 1), alt.forward([8], 1))
+    base.close()
+    alt.close()

@@ -1,0 +1,167 @@
+"""End-to-end parity of the on-GPU decode step against the llama.js forward
+restated in the oracle (llama.js:204-371, llama-streaming.js:505-606).
+
+Bars: logits within 2e-3 max-abs of the oracle at every checked position;
+greedy tokens identical to the oracle's argmax (a mismatch is accepted only
+where the oracle's own top logits are closer than that tolerance).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from purebee_amd import PbxError, synth
+from purebee_amd.native import TYPE_F32, TYPE_Q4_0, TYPE_Q8_0
+from tests.e2e_util import LOGIT_TOL, check_greedy, make_pair
+
+pytestmark = pytest.mark.gpu
+
+
+def tiny(weight_type, embed_type, **kw):
+    cfg = dict(dim=256, hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=1000,
+               max_seq=64, weight_type=weight_type, embed_type=embed_type, rope_theta=10000.0)
+    cfg.update(kw)
+    return cfg
+
+
+def run_prompt_then_greedy(ctx, cfg, n_prompt, n_gen, seed):
+    model, ref, cfg = make_pair(ctx, cfg, seed)
+    prompt = synth.random_tokens(seed + 1, n_prompt, cfg["vocab_size"])
+    # prefill: the reference processes the prompt in one forward (llama.js:465)
+    ref_logits = ref.forward(prompt, 0)
+    logits, nxt = model.forward(prompt, 0)
+    err = float(np.abs(logits - ref_logits).max())
+    assert err <= LOGIT_TOL, f"prefill logits max-abs {err:.2e}"
+    assert nxt == int(np.argmax(logits))
+    first = oracle.argmax(ref_logits)
+    if nxt != first:
+        assert ref_logits[first] - ref_logits[nxt] < LOGIT_TOL
+    # greedy decode on the GPU, then walk it through the oracle
+    toks, last = model.generate(nxt, n_prompt, n_gen, want_logits=True)
+    exact, ties = check_greedy(ref, toks, nxt, n_prompt)
+    # the oracle has now consumed the same tokens: compare the final logits
+    ref_last = ref.forward([int(toks[-1])], n_prompt + n_gen)
+    gpu_last, _ = model.forward([int(toks[-1])], n_prompt + n_gen)
+    err2 = float(np.abs(gpu_last - ref_last).max())
+    assert err2 <= LOGIT_TOL, f"final logits max-abs {err2:.2e}"
+    model.free()
+    ref.close()
+    return exact, ties, err, err2
+
+
+@pytest.mark.parametrize("wt,et", [(TYPE_Q4_0, TYPE_Q4_0), (TYPE_Q8_0, TYPE_Q8_0),
+                                   (TYPE_Q8_0, TYPE_F32), (TYPE_F32, TYPE_F32)])
+def test_tiny_model_prefill_and_greedy(ctx, wt, et):
+    print(f"[case] tiny model weights={wt} embed={et}", flush=True)
+    exact, ties, e1, e2 = run_prompt_then_greedy(ctx, tiny(wt, et), 8, 24, seed=50 + wt)
+    print(f"  exact={exact} ties={ties} prefill_err={e1:.1e} final_err={e2:.1e}")
+    assert exact >= 22
+
+
+def test_untied_head_and_small_head_dim(ctx):
+    print("[case] untied head, head_dim 48", flush=True)
+    cfg = tiny(TYPE_Q8_0, TYPE_F32, dim=288, hidden_dim=768, n_heads=6, n_kv_heads=6,
+               output_type=TYPE_Q4_0)
+    exact, ties, e1, e2 = run_prompt_then_greedy(ctx, cfg, 5, 12, seed=77)
+    assert exact >= 10
+
+
+def test_stories15m_shape(ctx):
+    """config: stories15M-shaped, Q8_0 layers, f32 embedding / LM head."""
+    print("[case] stories15m 16-token prompt + 64 greedy", flush=True)
+    exact, ties, e1, e2 = run_prompt_then_greedy(ctx, "stories15m", 16, 64, seed=1000)
+    print(f"  exact={exact} ties={ties} prefill_err={e1:.1e} final_err={e2:.1e}")
+    assert exact >= 62
+
+
+def test_smollm2_shape(ctx):
+    """config: SmolLM2-135M-shaped, GQA 9/3, tied Q8_0 embedding."""
+    print("[case] smollm2 32-token prompt + 64 greedy", flush=True)
+    exact, ties, e1, e2 = run_prompt_then_greedy(ctx, "smollm2_135m", 32, 64, seed=2000)
+    print(f"  exact={exact} ties={ties} prefill_err={e1:.1e} final_err={e2:.1e}")
+    assert exact >= 62
+
+
+def test_llama1b_shape(ctx):
+    """config: Llama-3.2-1B-shaped Q4_0 (tied 128256x2048 Q4_0 head, theta 5e5)."""
+    print("[case] llama32_1b 8-token prompt + 16 greedy", flush=True)
+    exact, ties, e1, e2 = run_prompt_then_greedy(ctx, "llama32_1b", 8, 16, seed=3000)
+    print(f"  exact={exact} ties={ties} prefill_err={e1:.1e} final_err={e2:.1e}")
+    assert exact >= 15
+
+
+def test_teacher_forced_logits_every_step(ctx):
+    print("[case] teacher-forced per-step logits", flush=True)
+    model, ref, cfg = make_pair(ctx, tiny(TYPE_Q4_0, TYPE_Q4_0, n_layers=3), 91)
+    toks = synth.random_tokens(92, 20, cfg["vocab_size"])
+    worst = 0.0
+    for p, t in enumerate(toks):
+        g, _ = model.forward([int(t)], p)
+        r = ref.forward([int(t)], p)
+        worst = max(worst, float(np.abs(g - r).max()))
+    assert worst <= LOGIT_TOL, worst
+    model.free()
+    ref.close()
+
+
+def test_cache_rollback_and_reset(ctx):
+    """rollbackCache / resetCache semantics (llama-streaming.js:828-862):
+    after rolling back to p, re-running positions >= p reproduces the logits."""
+    print("[case] rollback/reset", flush=True)
+    model, ref, cfg = make_pair(ctx, tiny(TYPE_Q8_0, TYPE_Q8_0), 93)
+    toks = [int(t) for t in synth.random_tokens(94, 12, cfg["vocab_size"])]
+    a, _ = model.forward(toks, 0)
+    model.forward([5, 6, 7], 12)          # extend past 12 ...
+    model.rollback(12)                    # ... and drop it again
+    b, _ = model.forward([toks[-1]], 11)  # re-run position 11
+    assert np.array_equal(a, b)
+    model.reset_cache()
+    c, _ = model.forward(toks, 0)
+    assert np.array_equal(a, c)
+    # a prompt fed in one call equals the same tokens fed one at a time
+    model.reset_cache()
+    for p, t in enumerate(toks):
+        d, _ = model.forward([t], p)
+    assert np.array_equal(a, d)
+    model.free()
+    ref.close()
+
+
+def test_model_argument_errors(ctx):
+    print("[case] model errors", flush=True)
+    cfg = tiny(TYPE_Q4_0, TYPE_Q4_0)
+    m = synth.Model(ctx, cfg["dim"], cfg["hidden_dim"], cfg["n_layers"], cfg["n_heads"],
+                    cfg["n_kv_heads"], cfg["vocab_size"], cfg["max_seq"], TYPE_Q4_0, TYPE_Q4_0)
+    with pytest.raises(PbxError) as e:
+        m.forward([1, 2], 0)  # nothing uploaded yet
+    assert "not set" in str(e.value)
+    m.free()
+    model, ref, cfg = make_pair(ctx, cfg, 95)
+    with pytest.raises(PbxError):
+        model.forward([cfg["vocab_size"]], 0)
+    with pytest.raises(PbxError):
+        model.forward([1], cfg["max_seq"])
+    with pytest.raises(PbxError):
+        model.generate(1, cfg["max_seq"] - 2, 5)
+    with pytest.raises(PbxError):
+        synth.Model(ctx, 100, 512, 1, 4, 2, 1000, 64, TYPE_Q4_0, TYPE_Q4_0)  # dim % 32
+    model.free()
+    ref.close()
+
+
+def test_gpu_matches_reference_llama_js_fixture(ctx):
+    """The GPU decode step against logits the reference's own LlamaRuntime
+    produced (tests/golden/llama_tiny.json), f32 weights."""
+    from tests.golden import llama_fixture as lf
+    print("[case] llama.js golden fixture", flush=True)
+    fx = lf.load()
+    c = fx["config"]
+    m = synth.Model(ctx, c["dim"], c["hiddenDim"], c["nLayers"], c["nHeads"], c["nKvHeads"],
+                    c["vocabSize"], c["seqLen"], TYPE_F32, TYPE_F32, rope_theta=c["ropeTheta"])
+    for tid, layer, w in lf.weights(fx):
+        m.set_tensor(tid, layer, w)
+    for st in fx["steps"]:
+        logits, nxt = m.forward(st["tokens"], st["pos"])
+        want = np.asarray(st["logits"], np.float32)
+        assert np.abs(logits - want).max() <= LOGIT_TOL, (st["pos"], np.abs(logits - want).max())
+        assert nxt == st["argmax"]
+    m.free()
