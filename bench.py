@@ -1,18 +1,21 @@
 #!/usr/bin/env python3
-"""Benchmark: Llama-3.2-1B-shaped Q4_0 decode matvecs on one MI355X.
+"""Benchmark: Llama-3.2-1B-shaped Q4_0 decode at batch 1 on one MI355X.
 
-Workload "matvec" (default): one step is the quantized-matvec pass of one
-Llama-3.2-1B decode token at batch 1: for each of 16 layers the seven
-projections q/k/v/o (2048x2048, 512x2048 x2, 2048x2048), gate/up
-(8192x2048 x2) and down (2048x8192), then the tied 128256x2048 LM head, all
-Q4_0, every layer with its own synthetic weights (SplitMix64/Box-Muller
-N(0, 0.02), quantised d = absmax/8) so the 695 MB per step stream from HBM
-rather than from the 256 MB MALL.  Activations are N(0,1).  Inputs are
-resident in HBM before the timed region.
+Default workload ("decode"): a Llama-3.2-1B-shaped model (dim 2048, 16
+layers, 32/8 heads, head_dim 64, FFN 8192 SwiGLU, vocab 128256, tied Q4_0
+embedding, RoPE theta 5e5) with seeded N(0, 0.02) weights quantised to Q4_0,
+resident in HBM.  A 128-token random prompt is run, then one timed step is one
+greedy decode token (every layer's matvecs, attention over the KV cache,
+LM head, argmax) replayed on the GPU from a captured graph; the default 256
+steps take the KV cache from 128 to 384 positions.
 
-Prints one JSON line (the bench contract) with a roofline entry for the
-kernel that takes the largest share of a step (HIP events on the context's
-stream) and the restated reference CPU path timed on a bounded sample.
+Workload "matvec": the per-token quantized-matvec pass alone (16 layers x
+q/k/v/o/gate/up/down + LM head) through the plain instruction.
+
+Prints one JSON line: the bench contract plus `roofline` (the kernel with the
+largest share of a step; HIP events on the model's stream), `kernels` (per
+role) and `cpu_baseline` (the restated reference CPU path on a bounded sample
+of the same work, timed on this host's cores).
 """
 import argparse
 import json
@@ -26,138 +29,203 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
-
-DIM, HIDDEN, LAYERS, KV_DIM, VOCAB = 2048, 8192, 16, 512, 128256
-LAYER_SHAPES = [("q", DIM, DIM), ("k", KV_DIM, DIM), ("v", KV_DIM, DIM), ("o", DIM, DIM),
-                ("gate", HIDDEN, DIM), ("up", HIDDEN, DIM), ("down", DIM, HIDDEN)]
-
-
-def q4_bytes(N, K):
-    """Algorithmic bytes of one Q4_0 matvec: weights + x + y."""
-    return N * K // 32 * 18 + 4 * K + 4 * N
+METRIC = "Llama-3.2-1B Q4 decode tok/s @1 GPU; Q4 matvec HBM GB/s vs peak"
+PROMPT = 128
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_model(pb, ctx, seed=1000):
-    """Quantised weights for every layer, uploaded once; host copies kept
-    for the CPU baseline."""
-    ops, host = [], {}
-    t0 = time.time()
-    for layer in range(LAYERS):
-        for i, (name, N, K) in enumerate(LAYER_SHAPES):
-            w = pb.synth_normal(seed + layer * 16 + i, N * K, 0.0, 0.02).reshape(N, K)
-            raw = pb.quantize_q4_0(w)
-            ops.append((name, N, K, ctx.upload(pb.TYPE_Q4_0, N, K, raw)))
-            host[(layer, name)] = raw
-    w = pb.synth_normal(seed + 999, VOCAB * DIM, 0.0, 0.02).reshape(VOCAB, DIM)
-    raw = pb.quantize_q4_0(w)
-    del w
-    ops.append(("lm_head", VOCAB, DIM, ctx.upload(pb.TYPE_Q4_0, VOCAB, DIM, raw)))
-    host["lm_head"] = raw
-    log(f"weights generated+uploaded in {time.time() - t0:.1f}s")
-    return ops, host
+def q4_bytes(N, K):
+    return N * K // 32 * 18
 
 
-def cpu_baseline(host, seconds):
-    """Restated reference CPU path (wasm-q4.js kernel in SSE + thread-pool.js
-    row split, f32 LM head through wasmQ4.lmHead on the exactly dequantised
-    embedding) on the same per-token matvec pass, for a bounded sample."""
+def cpu_baseline(host, cfg, seconds):
+    """Restated reference CPU path on the same weights: wasm-q4.js Q4_0 kernel
+    in SSE under the thread-pool.js row split for the 7 matvecs of each layer,
+    and the single-threaded f32 LM head (wasmQ4.lmHead) over the exactly
+    dequantised tied embedding.  Attention and norms (<1% of the reference's
+    per-token time) are left out of the sample."""
     import oracle
+    from purebee_amd import native as N_
     threads = min(16, os.cpu_count() or 1)
     pool = oracle.CpuPool(threads)
-    emb = oracle.dequant_q4_0(host["lm_head"], VOCAB * DIM)
-    xs = {K: np.asarray(np.random.default_rng(K).normal(0, 1, K), np.float32) for K in (DIM, HIDDEN)}
-    outs = {}
+    d, h, L, V = cfg["dim"], cfg["hidden_dim"], cfg["n_layers"], cfg["vocab_size"]
+    emb = oracle.dequant_q4_0(host[(N_.T_TOKEN_EMBD, -1)], V * d)
+    x = {d: np.random.default_rng(1).normal(0, 1, d).astype(np.float32),
+         h: np.random.default_rng(2).normal(0, 1, h).astype(np.float32)}
+    mats = [(N_.T_ATTN_Q, d, d), (N_.T_ATTN_K, -1, d), (N_.T_ATTN_V, -1, d),
+            (N_.T_ATTN_OUTPUT, d, d), (N_.T_FFN_GATE, h, d), (N_.T_FFN_UP, h, d),
+            (N_.T_FFN_DOWN, d, h)]
+    kv = cfg["n_kv_heads"] * (d // cfg["n_heads"])
 
     def one_token():
-        for layer in range(LAYERS):
-            for name, N, K in LAYER_SHAPES:
-                outs[name] = pool.q4_0_matvec(xs[K], host[(layer, name)], N, K,
-                                              outs.get(name) if name in outs else None)
-        oracle.cpu_lm_head(xs[DIM], emb, VOCAB, DIM)
+        for l in range(L):
+            for tid, n, k in mats:
+                n = kv if n < 0 else n
+                pool.q4_0_matvec(x[k], host[(tid, l)], n, k)
+        oracle.cpu_lm_head(x[d], emb, V, d)
 
-    one_token()  # warm-up
+    one_token()
     t0 = time.perf_counter()
     one_token()
     per = time.perf_counter() - t0
-    n = max(1, min(60, int(seconds / max(per, 1e-3))))
+    n = max(2, min(60, int(seconds / max(per, 1e-3))))
     t0 = time.perf_counter()
     for _ in range(n):
         one_token()
     dt = time.perf_counter() - t0
     pool.close()
-    return {"value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} tokens of the per-token Q4_0 matvec pass (16 layers x 7 matvecs on "
-                      f"{threads} threads + single-threaded f32 LM head), {dt:.1f}s"}
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} decode tokens of Q4_0 matvec work (16 layers x 7 matvecs, "
+                      f"{threads} threads) + single-threaded f32 LM head, {dt:.1f}s"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py: this backend runs on one GPU; multi-GPU runs are not part of this "
-              "build (see DESIGN.md for how the path would shard)", file=sys.stderr)
-        sys.exit(2)
+COPY_BYTES = 256 << 20
 
-    import purebee_amd as pb
+
+def measure_copy(ctx, reps=8):
+    """Achievable HBM bandwidth of a plain copy kernel (pbx_dev_copy) over
+    buffers larger than the 256 MB MALL; counted as read + write bytes.  The
+    same launches calibrate the FETCH_SIZE / WRITE_SIZE counters."""
+    a, b = ctx.alloc(COPY_BYTES), ctx.alloc(COPY_BYTES)
+    ctx.dev_copy(b.ptr, a.ptr, COPY_BYTES)
+    ctx.sync()
+    ctx.timer_start()
+    for i in range(reps):
+        src, dst = (a, b) if i % 2 == 0 else (b, a)
+        ctx.dev_copy(dst.ptr, src.ptr, COPY_BYTES)
+    ms = ctx.timer_stop()
+    a.free()
+    b.free()
+    return {"bytes": COPY_BYTES, "GBps": 2 * COPY_BYTES * reps / ms / 1e6}
+
+
+def load_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed PMC summary
+    (profiles/traffic_decode.json, written by --summarize-pmc), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic_decode.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    k = t.get("kernels", {}).get(kernel)
+    return None if k is None else k.get("hbm_bytes_per_launch")
+
+
+def summarize_pmc(fetch_csv, write_csv, out_path):
+    """Mean FETCH_SIZE / WRITE_SIZE per dispatch and kernel from two
+    rocprofv3 --pmc counter_collection CSVs, scaled by the factor that makes
+    the plain copy kernel read and write exactly its known bytes."""
+    import csv
+
+    def per_kernel(path, counter):
+        acc = {}
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r.get("Counter_Name") != counter:
+                    continue
+                name = r["Kernel_Name"].split("(")[0].strip()
+                key = (name, r.get("Dispatch_Id"))
+                acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"])
+        out = {}
+        for (name, _), v in acc.items():
+            s = out.setdefault(name, [0.0, 0])
+            s[0] += v
+            s[1] += 1
+        return {k: v[0] / v[1] for k, v in out.items()}
+
+    fetch = per_kernel(fetch_csv, "FETCH_SIZE")
+    write = per_kernel(write_csv, "WRITE_SIZE")
+    copy_kib = COPY_BYTES / 1024.0
+    f_scale = copy_kib / fetch["pbx_copy16"] if fetch.get("pbx_copy16") else None
+    w_scale = copy_kib / write["pbx_copy16"] if write.get("pbx_copy16") else None
+    kernels = {}
+    for k in sorted(set(fetch) | set(write)):
+        fk, wk = fetch.get(k), write.get(k)
+        entry = {"fetch_kib_raw": fk, "write_kib_raw": wk}
+        if fk is not None and wk is not None and f_scale and w_scale:
+            entry["hbm_bytes_per_launch"] = round((fk * f_scale + wk * w_scale) * 1024)
+        kernels[k] = entry
+    res = {"copy_kernel_bytes_each_way": COPY_BYTES, "fetch_scale": f_scale,
+           "write_scale": w_scale, "kernels": kernels}
+    with open(out_path, "w") as f:
+        json.dump(res, f, indent=1)
+    return res
+
+
+def run_decode(args, pb, synth):
+    cfg = synth.CONFIGS["llama32_1b"]
     ctx = pb.Context(0)
     dev, cus = ctx.device_info()
     log(f"device {dev}, {cus} CUs")
-    ops, host = build_model(pb, ctx)
-    xbuf = {K: ctx.alloc(K * 4).upload(np.random.default_rng(K).normal(0, 1, K).astype(np.float32))
-            for K in (DIM, HIDDEN)}
-    ybuf = ctx.alloc(VOCAB * 4)
-    W = [w for (_, _, _, w) in ops]
-    X = [xbuf[K].ptr for (_, _, K, _) in ops]
-    Y = [ybuf.ptr for _ in ops]
+    host = {}
+    t0 = time.time()
 
-    # warm-up, then the timed steps: HIP events on the context's stream
-    ctx.bench_linear(W, X, Y, 1, args.warmup)
+    def keep(spec, data):
+        tid, layer, N, K, t = spec
+        if t == pb.TYPE_Q4_0:
+            host[(tid, layer)] = data
+
+    model = synth.build(ctx, cfg, seed=1000, keep=keep if not args.no_cpu_baseline else None)
+    info = model.info()
+    log(f"model built + uploaded in {time.time() - t0:.1f}s, {info['device_bytes'] / 1e9:.2f} GB resident")
+
+    copy = measure_copy(ctx)
+    log(f"plain copy kernel: {copy['GBps']:.0f} GB/s ({copy['bytes'] / 2**20:.0f} MiB read + written)")
+
+    prompt = synth.random_tokens(7, PROMPT, cfg["vocab_size"])
+    t0 = time.perf_counter()
+    _, nxt = model.forward(prompt, 0, want_logits=False)
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill {PROMPT} tokens (token-by-token decode steps): {prefill_s * 1e3:.1f} ms")
+
+    model.generate(nxt, PROMPT, args.warmup)
+    model.rollback(PROMPT)
     ctx.sync()
-    ms = ctx.bench_linear(W, X, Y, 1, args.steps)
+    ctx.timer_start()
+    toks = model.generate(nxt, PROMPT, args.steps)
+    ms = ctx.timer_stop()
     ms_per_step = ms / args.steps
-    step_bytes = sum(q4_bytes(N, K) for (_, N, K, _) in ops)
-    log(f"step {ms_per_step * 1e3:.1f} us, {step_bytes / ms_per_step / 1e6:.0f} GB/s aggregate")
+    log(f"decode {args.steps} steps: {ms_per_step * 1e3:.1f} us/token, {1e3 / ms_per_step:.1f} tok/s "
+        f"(graph={model.info()['graph']})")
+    model.rollback(PROMPT)
 
-    # per-kernel timing: each shape class over all its instances (distinct buffers)
-    kernels = {}
-    for cls, names in (("qo_2048x2048", ("q", "o")), ("kv_512x2048", ("k", "v")),
-                       ("gateup_8192x2048", ("gate", "up")), ("down_2048x8192", ("down",)),
-                       ("lmhead_128256x2048", ("lm_head",))):
-        sel = [(N, K, w) for (n, N, K, w) in ops if n in names]
-        Ws = [w for (_, _, w) in sel]
-        Xs = [xbuf[K].ptr for (_, K, _) in sel]
-        reps = max(1, 400 // len(sel))
-        ctx.bench_linear(Ws, Xs, [ybuf.ptr] * len(sel), 1, 3)
-        t = ctx.bench_linear(Ws, Xs, [ybuf.ptr] * len(sel), 1, reps)
-        per_launch_us = t * 1e3 / (reps * len(sel))
-        N, K, _ = sel[0]
-        b = q4_bytes(N, K)
-        kernels[cls] = {"N": N, "K": K, "launches_per_step": len(sel), "us_per_launch": per_launch_us,
-                        "bytes_per_launch": b, "GBps": b / per_launch_us / 1e3,
-                        "us_per_step": per_launch_us * len(sel)}
-        log(f"{cls}: {per_launch_us:.2f} us/launch, {b / per_launch_us / 1e3:.0f} GB/s")
-    dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["us_per_step"])
-    roofline = {"bound": "hbm", "kernel": dom_name, "achieved": round(dom["GBps"], 1),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
-                "traffic": None}
-
+    # per-kernel attribution: the same steps launched kernel by kernel with
+    # an event after each kernel
+    prof = model.profile(nxt, PROMPT, 8)
+    model.rollback(PROMPT)
+    roles = {}
+    for role, kern, us, by in prof:
+        r = roles.setdefault(role, {"kernel": kern, "launches_per_step": 0, "us_per_step": 0.0,
+                                    "bytes_per_step": 0.0})
+        r["launches_per_step"] += 1
+        r["us_per_step"] += us
+        r["bytes_per_step"] += by
+    for role, r in roles.items():
+        n = r["launches_per_step"]
+        r["us_per_launch"] = r["us_per_step"] / n
+        r["bytes_per_launch"] = r["bytes_per_step"] / n
+        r["GBps"] = r["bytes_per_step"] / r["us_per_step"] / 1e3 if r["us_per_step"] else 0.0
+        log(f"{role:8s} {r['kernel']:24s} x{n:3d}: {r['us_per_launch']:7.2f} us/launch, "
+            f"{r['GBps']:7.0f} GB/s, {r['us_per_step']:7.1f} us/step")
+    gemv_roles = {k: v for k, v in roles.items() if k in ("qkv", "o", "gate_up", "down", "lm_head")}
+    dom_name, dom = max(gemv_roles.items(), key=lambda kv: kv[1]["us_per_step"])
+    roofline = {"bound": "hbm", "kernel": f"{dom['kernel']} ({dom_name})",
+                "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
+                "traffic": load_traffic(dom["kernel"]),
+                "bytes_per_launch": round(dom["bytes_per_launch"]),
+                "us_per_launch": round(dom["us_per_launch"], 3)}
+    step_bytes = sum(r["bytes_per_step"] for r in roles.values())
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the restated reference CPU path ...")
-        cpu = cpu_baseline(host, args.cpu_seconds)
-        log(f"cpu baseline {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
-
+        cpu = cpu_baseline(host, cfg, args.cpu_seconds)
+        log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
     out = {
-        "metric": "Llama-3.2-1B Q4 decode tok/s @1 GPU; Q4 matvec HBM GB/s vs peak",
+        "metric": METRIC,
         "value": round(1e3 / ms_per_step, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -167,19 +235,123 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 weights, fp32 activations/accumulation",
-        "data": "synthetic (seeded N(0,0.02) weights quantised to Q4_0, N(0,1) activations)",
-        "config": {"workload": "llama-3.2-1b q4_0 decode matvec pass: 16 layers x "
-                               "(q,k,v,o,gate,up,down) + tied 128256x2048 lm head, batch 1",
-                   "bytes_per_step": step_bytes,
-                   "aggregate_GBps": round(step_bytes / ms_per_step / 1e6, 1),
-                   "device": dev},
+        "dtype": "q4_0 weights; fp32 activations, accumulation and KV cache",
+        "data": "synthetic: seeded N(0,0.02) weights quantised to Q4_0, random prompt tokens",
+        "config": {"workload": "llama-3.2-1b-shaped q4_0 greedy decode, batch 1, "
+                               f"{PROMPT}-token prompt then {args.steps} steps "
+                               f"(KV {PROMPT}->{PROMPT + args.steps})",
+                   "model": "llama-3.2-1b-shaped (random init)",
+                   "global_batch": 1, "seq_len": PROMPT + args.steps,
+                   "bytes_per_step": round(step_bytes),
+                   "effective_GBps": round(step_bytes / ms_per_step / 1e6, 1),
+                   "prefill_ms": round(prefill_s * 1e3, 2), "device": dev,
+                   "copy_kernel_GBps": round(copy["GBps"], 1),
+                   "first_tokens": [int(t) for t in toks[:8]]},
         "roofline": roofline,
-        "kernels": kernels,
+        "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in roles.items()},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
+    model.free()
     ctx.close()
+    return out
+
+
+def run_pmc_probe(args, pb, synth):
+    """A short run for hardware-counter passes (rocprofv3 --pmc serialises
+    every dispatch): the calibration copies and two decode steps of the same
+    model.  Prints its progress."""
+    cfg = synth.CONFIGS["llama32_1b"]
+    ctx = pb.Context(0)
+    log("probe: building model")
+    model = synth.build(ctx, cfg, seed=1000)
+    log("probe: calibration copies")
+    measure_copy(ctx, reps=2)
+    log("probe: prompt + 2 decode steps")
+    _, nxt = model.forward(synth.random_tokens(7, 4, cfg["vocab_size"]), 0, want_logits=False)
+    model.generate(nxt, 4, 2)
+    ctx.sync()
+    log("probe: done")
+    model.free()
+    ctx.close()
+    return None
+
+
+def run_matvec(args, pb, synth):
+    """Per-token Q4_0 matvec pass through the plain instruction."""
+    cfg = synth.CONFIGS["llama32_1b"]
+    d, h, L, V = cfg["dim"], cfg["hidden_dim"], cfg["n_layers"], cfg["vocab_size"]
+    kv = cfg["n_kv_heads"] * (d // cfg["n_heads"])
+    shapes = [("q", d, d), ("k", kv, d), ("v", kv, d), ("o", d, d), ("gate", h, d), ("up", h, d),
+              ("down", d, h)]
+    ctx = pb.Context(0)
+    dev, _ = ctx.device_info()
+    ops = []
+    seed = 1000
+    for l in range(L):
+        for i, (name, N, K) in enumerate(shapes):
+            raw = pb.quantize_q4_0(pb.synth_normal(seed + 16 * l + i, N * K, 0, 0.02).reshape(N, K))
+            ops.append((name, N, K, ctx.upload(pb.TYPE_Q4_0, N, K, raw)))
+    raw = pb.quantize_q4_0(pb.synth_normal(seed + 999, V * d, 0, 0.02).reshape(V, d))
+    ops.append(("lm_head", V, d, ctx.upload(pb.TYPE_Q4_0, V, d, raw)))
+    xb = {K: ctx.alloc(K * 4).upload(np.random.default_rng(K).normal(0, 1, K).astype(np.float32))
+          for K in (d, h)}
+    yb = ctx.alloc(V * 4)
+    W = [w for (_, _, _, w) in ops]
+    X = [xb[K].ptr for (_, _, K, _) in ops]
+    Y = [yb.ptr] * len(ops)
+    ctx.bench_linear(W, X, Y, 1, args.warmup)
+    ms = ctx.bench_linear(W, X, Y, 1, args.steps)
+    ms_per_step = ms / args.steps
+    step_bytes = sum(q4_bytes(N, K) + 4 * (N + K) for (_, N, K, _) in ops)
+    # the LM head alone, its launches separated by the 547 MB of layer weights
+    sel = [w for (n, _, _, w) in ops if n == "lm_head"]
+    t = ctx.bench_linear(sel, [xb[d].ptr], [yb.ptr], 1, 20) / 20
+    b = q4_bytes(V, d) + 4 * (V + d)
+    roofline = {"bound": "hbm", "kernel": "pbx_gemv_q4_0_wide_r16 (lm head)",
+                "achieved": round(b / t / 1e6, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4), "traffic": None}
+    ctx.close()
+    return {"metric": METRIC, "value": round(1e3 / ms_per_step, 2), "unit": "tok/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "q4_0 weights; fp32 activations and accumulation",
+            "data": "synthetic: seeded N(0,0.02) weights quantised to Q4_0",
+            "config": {"workload": "llama-3.2-1b-shaped q4_0 decode matvec pass only",
+                       "bytes_per_step": step_bytes, "device": dev},
+            "roofline": roofline, "cpu_baseline": None}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--workload", choices=("decode", "matvec", "pmc-probe"), default="decode")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/traffic_decode.json from two rocprofv3 --pmc runs")
+    args = ap.parse_args()
+    if args.summarize_pmc:
+        res = summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1],
+                            os.path.join(ROOT, "profiles", "traffic_decode.json"))
+        print(json.dumps(res, indent=1))
+        return
+    if args.gpus != 1:
+        print("bench.py: this backend runs on one GPU; multi-GPU runs are not part of this "
+              "build (DESIGN.md describes how the path would shard)", file=sys.stderr)
+        sys.exit(2)
+    if args.workload == "decode" and PROMPT + args.steps > 1024:
+        print("bench.py: --steps must keep the KV cache within 1024 positions", file=sys.stderr)
+        sys.exit(2)
+    import purebee_amd as pb
+    from purebee_amd import synth
+    if args.workload == "pmc-probe":
+        run_pmc_probe(args, pb, synth)
+        return
+    out = run_decode(args, pb, synth) if args.workload == "decode" else run_matvec(args, pb, synth)
+    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

@@ -142,6 +142,10 @@ int pbx_dev_free(pbx_ctx *ctx, void *p);
 int pbx_memcpy_h2d(pbx_ctx *ctx, void *dst, const void *src, size_t bytes);
 int pbx_memcpy_d2h(pbx_ctx *ctx, void *dst, const void *src, size_t bytes);
 int pbx_memset_dev(pbx_ctx *ctx, void *dst, int value, size_t bytes);
+/* Device-to-device copy by a plain kernel (bytes and both addresses 16-byte
+ * aligned): a known-traffic kernel for calibrating hardware byte counters.
+ * No reference counterpart. */
+int pbx_dev_copy(pbx_ctx *ctx, void *dst, const void *src, size_t bytes);
 int pbx_sync(pbx_ctx *ctx);
 /* HIP events recorded on the context's stream: the kernels' own stream. */
 int pbx_timer_start(pbx_ctx *ctx);
@@ -211,6 +215,16 @@ int pbx_model_generate(pbx_model *m, int32_t token, int start_pos, int n_steps,
 int pbx_model_reset_cache(pbx_model *m);
 int pbx_model_rollback(pbx_model *m, int pos);
 int pbx_model_info(const pbx_model *m, size_t *device_bytes, int *uses_graph);
+/* Measurement: n_steps greedy decode steps launched kernel by kernel (no
+ * graph) with a HIP event on the model's stream after every kernel.
+ * op_us[i] is the mean time from the end of kernel i-1 to the end of
+ * kernel i, op_bytes[i] its mean algorithmic bytes (may be NULL); *n_ops is
+ * the kernel count per step (arrays hold min(cap, *n_ops) entries).
+ * pbx_model_op_name gives "role:kernel" of kernel i (no reference
+ * counterpart: the reference has no GPU kernels to profile). */
+int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int n_steps,
+                      double *op_us, double *op_bytes, int cap, int *n_ops);
+int pbx_model_op_name(const pbx_model *m, int i, char *buf, size_t cap);
 
 #ifdef __cplusplus
 }

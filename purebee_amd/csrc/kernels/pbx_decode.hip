@@ -5,8 +5,9 @@
 //   1. GEMV  x -> [q|k|v]           RMSNorm(x, attn_norm) fused as prologue
 //   2. attention                     RoPE, KV-cache append, softmax(q.K)V
 //   3. GEMV  attn -> x (+=)          residual add fused as epilogue
-//   4. GEMV  x -> [gate|up]          RMSNorm(x, ffn_norm) prologue
-//   5. GEMV  silu(gate)*up -> x (+=) SwiGLU prologue, residual epilogue
+//   4. GEMV  x -> silu(gate)*up      RMSNorm(x, ffn_norm) prologue; each
+//                                    workgroup pairs gate and up rows
+//   5. GEMV  h -> x (+=)             residual epilogue
 // then the LM head GEMV (RMSNorm(x, output_norm) prologue, per-tile argmax
 // partials epilogue) and a one-workgroup argmax that also advances the
 // device-side position, so consecutive steps replay without the host.
@@ -21,7 +22,8 @@ using namespace pbx;
 // Fused GEMV instantiations.  Name: pbx_dk_<type>_<shape>_<mode>
 //   shape: w<R> (gemv_wide, R rows per workgroup) or s (gemv_small)
 //   mode : qkv = RMSNorm prologue + store      add = plain + accumulate
-//          swa = SwiGLU prologue + accumulate  lmh = RMSNorm + argmax partials
+//          gu  = RMSNorm + paired gate/up rows, stores silu(gate)*up
+//          lmh = RMSNorm + argmax partials
 // ---------------------------------------------------------------------------
 #define DK_WIDE(T, TN, R, PRO, EPI, MN)                                             \
   extern "C" __global__ void __launch_bounds__(512) pbx_dk_##TN##_w##R##_##MN(GemvArgs a) { \
@@ -34,12 +36,12 @@ using namespace pbx;
 #define DK_MODES_WIDE(T, TN, R)                     \
   DK_WIDE(T, TN, R, PRO_RMSNORM, EPI_STORE, qkv)    \
   DK_WIDE(T, TN, R, PRO_NONE, EPI_ADD, add)         \
-  DK_WIDE(T, TN, R, PRO_SWIGLU, EPI_ADD, swa)       \
+  DK_WIDE(T, TN, R, PRO_RMSNORM, EPI_SWIGLU, gu)    \
   DK_WIDE(T, TN, R, PRO_RMSNORM, EPI_ARGMAX, lmh)
 #define DK_MODES_SMALL(T, TN, P)                    \
   DK_SMALL(T, TN, P, PRO_RMSNORM, EPI_STORE, qkv)   \
   DK_SMALL(T, TN, P, PRO_NONE, EPI_ADD, add)        \
-  DK_SMALL(T, TN, P, PRO_SWIGLU, EPI_ADD, swa)      \
+  DK_SMALL(T, TN, P, PRO_RMSNORM, EPI_SWIGLU, gu)   \
   DK_SMALL(T, TN, P, PRO_RMSNORM, EPI_ARGMAX, lmh)
 
 DK_MODES_WIDE(PBX_Q4, q4, 4)
@@ -93,10 +95,14 @@ struct AttnArgs {
 // rotate q and the new k (adjacent pairs, llama.js:163-190), append k and v
 // at `pos` (the first query head of each KV group writes), scores over
 // positions 0..pos, max-subtracted softmax, weighted sum of V.
+// Loads are arranged for memory-level parallelism: a thread scores whole
+// positions (head_dim/4 independent 16-B loads of one K row), and the V sum
+// splits the head_dim/4 float4 columns x (256 / (head_dim/4)) position groups
+// over the threads, four positions per iteration.
 extern "C" __global__ void __launch_bounds__(256) pbx_attention_decode(AttnArgs a) {
   __shared__ float qr[PBX_ATTN_MAX_HD], kn[PBX_ATTN_MAX_HD], vn[PBX_ATTN_MAX_HD];
   __shared__ float sc[PBX_ATTN_MAX_SEQ];
-  __shared__ float part[8][PBX_ATTN_MAX_HD];
+  __shared__ float4 part[256];
   __shared__ float red[8];
 
   const int h = blockIdx.x, hd = a.head_dim;
@@ -131,21 +137,44 @@ extern "C" __global__ void __launch_bounds__(256) pbx_attention_decode(AttnArgs 
 
   // scores: positions < pos from the cache, position pos from LDS
   const int L = pos + 1;
+  const int hd4 = hd / 4;
   for (int j = threadIdx.x; j < L; j += blockDim.x) {
     float dot = 0.f;
     if (j < pos) {
       const float4 *kr = reinterpret_cast<const float4 *>(krow + (size_t)j * kvdim);
-      for (int d4 = 0; d4 < hd / 4; ++d4) {
+      float d0 = 0.f, d1 = 0.f;
+      for (int d4 = 0; d4 < hd4; d4 += 2) {
         const float4 t = kr[d4];
-        dot = fmaf(qr[4 * d4], t.x, dot);
-        dot = fmaf(qr[4 * d4 + 1], t.y, dot);
-        dot = fmaf(qr[4 * d4 + 2], t.z, dot);
-        dot = fmaf(qr[4 * d4 + 3], t.w, dot);
+        d0 = fmaf(qr[4 * d4], t.x, d0);
+        d0 = fmaf(qr[4 * d4 + 1], t.y, d0);
+        d0 = fmaf(qr[4 * d4 + 2], t.z, d0);
+        d0 = fmaf(qr[4 * d4 + 3], t.w, d0);
+        if (d4 + 1 < hd4) {
+          const float4 u = kr[d4 + 1];
+          d1 = fmaf(qr[4 * d4 + 4], u.x, d1);
+          d1 = fmaf(qr[4 * d4 + 5], u.y, d1);
+          d1 = fmaf(qr[4 * d4 + 6], u.z, d1);
+          d1 = fmaf(qr[4 * d4 + 7], u.w, d1);
+        }
       }
+      dot = d0 + d1;
     } else {
       for (int d = 0; d < hd; ++d) dot = fmaf(qr[d], kn[d], dot);
     }
     sc[j] = dot * a.scale;
+  }
+  // The first V rows this thread will need do not depend on the softmax:
+  // issue their loads before the reductions so the latency overlaps.
+  const int G = (int)blockDim.x / hd4;
+  const int c = threadIdx.x % hd4, g = threadIdx.x / hd4;
+  const float4 *vb = reinterpret_cast<const float4 *>(vrow) + c;
+  const size_t stride4 = (size_t)kvdim / 4;
+  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 vp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int j = g + i * G;
+    vp[i] = (g < G && j < pos) ? vb[(size_t)j * stride4] : zero4;
   }
   __syncthreads();
   float m = -INFINITY;
@@ -161,22 +190,52 @@ extern "C" __global__ void __launch_bounds__(256) pbx_attention_decode(AttnArgs 
   for (int j = threadIdx.x; j < L; j += blockDim.x) sc[j] = sc[j] / sum;
   __syncthreads();
 
-  // out[d] = sum_j p_j V[j][d]: G groups of hd threads split the positions
-  const int G = (int)blockDim.x / hd;
-  const int g = threadIdx.x / hd, d = threadIdx.x % hd;
+  // out[d] = sum_j p_j V[j][d]: thread = (float4 column c, position group g)
+  float4 acc = zero4;
   if (g < G) {
-    float acc = 0.f;
-    for (int j = g; j < L; j += G) {
-      const float vv = (j < pos) ? vrow[(size_t)j * kvdim + d] : vn[d];
-      acc = fmaf(sc[j], vv, acc);
+    const float4 vnew = make_float4(vn[4 * c], vn[4 * c + 1], vn[4 * c + 2], vn[4 * c + 3]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = g + i * G;
+      if (j < L) {
+        const float4 vv = j < pos ? vp[i] : vnew;
+        const float p = sc[j];
+        acc.x = fmaf(p, vv.x, acc.x); acc.y = fmaf(p, vv.y, acc.y);
+        acc.z = fmaf(p, vv.z, acc.z); acc.w = fmaf(p, vv.w, acc.w);
+      }
     }
-    part[g][d] = acc;
+    int j = g + 4 * G;
+    for (; j + 3 * G < pos; j += 4 * G) {
+      const float4 v0 = vb[(size_t)j * stride4];
+      const float4 v1 = vb[(size_t)(j + G) * stride4];
+      const float4 v2 = vb[(size_t)(j + 2 * G) * stride4];
+      const float4 v3 = vb[(size_t)(j + 3 * G) * stride4];
+      const float p0 = sc[j], p1 = sc[j + G], p2 = sc[j + 2 * G], p3 = sc[j + 3 * G];
+      acc.x = fmaf(p0, v0.x, acc.x); acc.y = fmaf(p0, v0.y, acc.y);
+      acc.z = fmaf(p0, v0.z, acc.z); acc.w = fmaf(p0, v0.w, acc.w);
+      acc.x = fmaf(p1, v1.x, acc.x); acc.y = fmaf(p1, v1.y, acc.y);
+      acc.z = fmaf(p1, v1.z, acc.z); acc.w = fmaf(p1, v1.w, acc.w);
+      acc.x = fmaf(p2, v2.x, acc.x); acc.y = fmaf(p2, v2.y, acc.y);
+      acc.z = fmaf(p2, v2.z, acc.z); acc.w = fmaf(p2, v2.w, acc.w);
+      acc.x = fmaf(p3, v3.x, acc.x); acc.y = fmaf(p3, v3.y, acc.y);
+      acc.z = fmaf(p3, v3.z, acc.z); acc.w = fmaf(p3, v3.w, acc.w);
+    }
+    for (; j < L; j += G) {
+      const float4 vv = (j < pos) ? vb[(size_t)j * stride4] : vnew;
+      const float p = sc[j];
+      acc.x = fmaf(p, vv.x, acc.x); acc.y = fmaf(p, vv.y, acc.y);
+      acc.z = fmaf(p, vv.z, acc.z); acc.w = fmaf(p, vv.w, acc.w);
+    }
   }
+  part[threadIdx.x] = acc;
   __syncthreads();
-  if (threadIdx.x < hd) {
-    float s = 0.f;
-    for (int gg = 0; gg < G; ++gg) s += part[gg][threadIdx.x];
-    a.out[(size_t)h * hd + threadIdx.x] = s;
+  if (threadIdx.x < hd4) {
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int gg = 0; gg < G; ++gg) {
+      const float4 t = part[gg * hd4 + threadIdx.x];
+      s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+    }
+    reinterpret_cast<float4 *>(a.out + (size_t)h * hd)[threadIdx.x] = s;
   }
 }
 
@@ -203,7 +262,7 @@ extern "C" __global__ void __launch_bounds__(256) pbx_embed(EmbedArgs a) {
   if (a.type == PBX_F32) {
     val = reinterpret_cast<const float *>(a.qs)[(size_t)tok * a.dim + i];
   } else {
-    const float d = f16_bits_to_f32(a.dsc[((size_t)(tok >> 3) * B + b) * 8 + (tok & 7)]);
+    const float d = f16_bits_to_f32(a.dsc[dsc_index(tok, b, B)]);
     if (a.type == PBX_Q4) {
       const unsigned byte = a.qs[((size_t)tok * B + b) * 16 + (j & 15)];
       const int nib = j < 16 ? (int)(byte & 15u) : (int)(byte >> 4);

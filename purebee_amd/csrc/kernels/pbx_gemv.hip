@@ -8,9 +8,9 @@
 // Device layout of a resident weight (N rows, K columns, B = K/32 blocks/row,
 // Npad = N rounded up to 64 so row tiles never need a load guard):
 //   Q4_0 : qs plane  [Npad][B][16] bytes   (the 16 nibble bytes of each block)
-//          d  plane  [Npad/8][B][8] fp16   (8 rows' scales of one block are
-//                                           contiguous: one 16-B load serves
-//                                           an 8-row group)
+//          d  plane  [Npad/4][B][4] fp16   (4 rows' scales of one block are
+//                                           contiguous: one 8-B load serves
+//                                           a 4-row group)
 //   Q8_0 : qs plane  [Npad][B][32] int8, d plane as Q4_0
 //   F32  : plane     [Npad][K] float
 // The GGUF block formats these come from are gguf.js:36-49 (sizes) and
@@ -112,7 +112,7 @@ pbx_repack_q4_0(const uint16_t *raw, uint8_t *qs, uint16_t *dsc, int64_t row0,
   v.x = h[0] | (h[1] << 16); v.y = h[2] | (h[3] << 16);
   v.z = h[4] | (h[5] << 16); v.w = h[6] | (h[7] << 16);
   *reinterpret_cast<uint4 *>(qs + ((size_t)n * B + b) * 16) = v;
-  dsc[((size_t)(n >> 3) * B + b) * 8 + (n & 7)] = src[0];
+  dsc[dsc_index((int)n, b, B)] = src[0];
 }
 
 extern "C" __global__ void __launch_bounds__(256)
@@ -134,7 +134,7 @@ pbx_repack_q8_0(const uint16_t *raw, uint8_t *qs, uint16_t *dsc, int64_t row0,
   uint4 *dst = reinterpret_cast<uint4 *>(qs + ((size_t)n * B + b) * 32);
   dst[0] = v0;
   dst[1] = v1;
-  dsc[((size_t)(n >> 3) * B + b) * 8 + (n & 7)] = src[0];
+  dsc[dsc_index((int)n, b, B)] = src[0];
 }
 
 // ---------------------------------------------------------------------------
@@ -147,7 +147,7 @@ pbx_dequant_q4_0(const uint8_t *qs, const uint16_t *dsc, float *out, int N, int 
   if (i >= (int64_t)N * B) return;
   const int n = (int)(i / B), b = (int)(i % B);
   const uint4 q = *reinterpret_cast<const uint4 *>(qs + i * 16);
-  const float d = f16_bits_to_f32(dsc[((size_t)(n >> 3) * B + b) * 8 + (n & 7)]);
+  const float d = f16_bits_to_f32(dsc[dsc_index((int)n, b, B)]);
   const unsigned w[4] = {q.x, q.y, q.z, q.w};
   float v[32];
 #pragma unroll
@@ -167,7 +167,7 @@ pbx_dequant_q8_0(const uint8_t *qs, const uint16_t *dsc, float *out, int N, int 
   if (i >= (int64_t)N * B) return;
   const int n = (int)(i / B), b = (int)(i % B);
   const int8_t *q = reinterpret_cast<const int8_t *>(qs + i * 32);
-  const float d = f16_bits_to_f32(dsc[((size_t)(n >> 3) * B + b) * 8 + (n & 7)]);
+  const float d = f16_bits_to_f32(dsc[dsc_index((int)n, b, B)]);
   float4 *dst = reinterpret_cast<float4 *>(out + i * 32);
 #pragma unroll
   for (int j = 0; j < 8; ++j)
@@ -181,4 +181,13 @@ pbx_dequant_q8ref(const int8_t *q, const float *scales, float *out, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   out[i] = (float)q[i] * scales[i / 32];
+}
+
+// Plain 16-byte copy (pbx_dev_copy): a kernel of known traffic, n16 * 16 bytes
+// read and written, used to calibrate hardware byte counters.
+extern "C" __global__ void __launch_bounds__(256)
+pbx_copy16(const uint4 *src, uint4 *dst, int64_t n16) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
 }

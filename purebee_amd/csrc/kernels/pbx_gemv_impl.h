@@ -30,6 +30,9 @@
 #define EPI_STORE 0
 #define EPI_ADD 1
 #define EPI_ARGMAX 2
+// Paired rows: the weight holds N/2 gate rows then N/2 up rows; a workgroup
+// reads matching gate and up rows and stores silu(gate)*up (N/2 outputs).
+#define EPI_SWIGLU 3
 
 // Everything a fused GEMV launch needs; passed by value.
 struct GemvArgs {
@@ -54,6 +57,13 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_stream(const void *p) {
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Scale plane: 4-row groups, [Npad/4][B][4] fp16, so the scales of 4
+// consecutive rows at one block are one 8-byte load and a tile of >= 4 rows
+// uses whole cache lines.
+__device__ __forceinline__ size_t dsc_index(int n, int b, int B) {
+  return ((size_t)(n >> 2) * B + b) * 4 + (n & 3);
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(unsigned bits) {
@@ -181,15 +191,16 @@ __device__ __forceinline__ void prologue_block(const GemvArgs &a, const float *x
   }
 }
 
-// RMSNorm (engine.js:429-449): rms = sqrt(sum(x^2)/K + eps); x/rms * w.
+// RMSNorm (engine.js:429-449): rms = sqrt(sum(x^2)/K + eps); x/rms * w,
+// here as x * (1/rms) * w (one reciprocal instead of 32 divisions).
 __device__ __forceinline__ void apply_rmsnorm(const GemvArgs &a, float ss, int K, int b,
                                               bool valid, float (&xr)[32]) {
-  const float rms = sqrtf(ss / (float)K + a.eps);
+  const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
   if (valid) {
     float w[32];
     load_block(a.normw + (size_t)b * 32, true, w);
 #pragma unroll
-    for (int j = 0; j < 32; ++j) xr[j] = xr[j] / rms * w[j];
+    for (int j = 0; j < 32; ++j) xr[j] = xr[j] * inv * w[j];
   }
 }
 
@@ -260,39 +271,46 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
   const int K = B * 32;
   const float *x = a.X + (size_t)blockIdx.y * K;
   const float *x2 = a.X2 ? a.X2 + (size_t)blockIdx.y * K : nullptr;
-  float *y = a.Y + (size_t)blockIdx.y * N;
-  const int r0 = blockIdx.x * R;
+  constexpr bool PAIR = EPI == EPI_SWIGLU;
+  const int NO = PAIR ? N / 2 : N;  // output rows
+  float *y = a.Y + (size_t)blockIdx.y * NO;
+  // Row i of the tile: R consecutive rows, or (PAIR) R/2 gate rows starting
+  // at r0 and the matching R/2 up rows starting at N/2 + r0.
+  const int r0 = blockIdx.x * (PAIR ? R / 2 : R);
+  auto tile_row = [&](int i) -> int {
+    return PAIR ? (i < R / 2 ? r0 + i : N / 2 + r0 + i - R / 2) : r0 + i;
+  };
 
   // Issue the weight loads first: they do not depend on the activations.
   uint4 q[R][NV];
-  const uint8_t *base = a.qs + ((size_t)r0 * B + b) * QB;
 #pragma unroll
   for (int i = 0; i < R; ++i) {
+    const uint8_t *src = a.qs + ((size_t)tile_row(i) * B + b) * QB;
 #pragma unroll
     for (int v = 0; v < NV; ++v)
-      q[i][v] = valid ? ld_stream(base + (size_t)i * B * QB + v * 16)
-                      : make_uint4(0u, 0u, 0u, 0u);
+      q[i][v] = valid ? ld_stream(src + v * 16) : make_uint4(0u, 0u, 0u, 0u);
   }
   float dsf[R];
   if constexpr (TYPE != PBX_F32) {
-    if constexpr (R >= 8) {
+    constexpr int SEG = PAIR ? R / 2 : R;  // rows contiguous in the scale plane
+    if constexpr (SEG >= 4) {
 #pragma unroll
-      for (int g = 0; g < R / 8; ++g) {
-        const uint4 dv = valid ? *reinterpret_cast<const uint4 *>(
-                                     a.dsc + ((size_t)(r0 / 8 + g) * B + b) * 8)
-                               : make_uint4(0u, 0u, 0u, 0u);
-        const unsigned dw[4] = {dv.x, dv.y, dv.z, dv.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          dsf[g * 8 + 2 * j] = f16_bits_to_f32(dw[j]);
-          dsf[g * 8 + 2 * j + 1] = f16_bits_to_f32(dw[j] >> 16);
-        }
+      for (int g = 0; g < R / 4; ++g) {
+        const int rg = tile_row(g * 4);
+        const uint2 dv = valid ? *reinterpret_cast<const uint2 *>(a.dsc + dsc_index(rg, b, B))
+                               : make_uint2(0u, 0u);
+        dsf[g * 4 + 0] = f16_bits_to_f32(dv.x);
+        dsf[g * 4 + 1] = f16_bits_to_f32(dv.x >> 16);
+        dsf[g * 4 + 2] = f16_bits_to_f32(dv.y);
+        dsf[g * 4 + 3] = f16_bits_to_f32(dv.y >> 16);
       }
     } else {
-      // R = 2 or 4 rows inside one 8-row group (r0 % R == 0).
-      const uint16_t *dp = a.dsc + ((size_t)(r0 / 8) * B + b) * 8 + (r0 & 7);
+      // segments of 1 or 2 rows inside one 4-row group
 #pragma unroll
-      for (int i = 0; i < R; ++i) dsf[i] = valid ? f16_bits_to_f32(dp[i]) : 0.f;
+      for (int i = 0; i < R; ++i) {
+        const int rw = tile_row(i);
+        dsf[i] = valid ? f16_bits_to_f32(a.dsc[dsc_index(rw, b, B)]) : 0.f;
+      }
     }
   } else {
 #pragma unroll
@@ -329,6 +347,29 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
   const int lanes_per_row = 64 / R;
   const int row = lane / lanes_per_row;
   uint64_t key = 0;
+  if constexpr (PAIR) {
+    // gate row i sits in lane i*lpr, its up row in lane i*lpr + 32
+    if (nwaves == 1) {
+      const float up = __shfl_xor(tot, 32, 64);
+      if (lane < 32 && (lane % lanes_per_row) == 0) {
+        const int n = r0 + row;
+        if (n < NO) y[n] = silu(tot) * up;
+      }
+    } else {
+      if ((lane % lanes_per_row) == 0) red[wave][row] = tot;
+      __syncthreads();
+      if (threadIdx.x < R / 2) {
+        float g = 0.f, u = 0.f;
+        for (int w = 0; w < nwaves; ++w) {
+          g += red[w][threadIdx.x];
+          u += red[w][threadIdx.x + R / 2];
+        }
+        const int n = r0 + threadIdx.x;
+        if (n < NO) y[n] = silu(g) * u;
+      }
+    }
+    return;
+  }
   if (nwaves == 1) {
     if ((lane % lanes_per_row) == 0) {
       const int n = r0 + row;
@@ -377,22 +418,31 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
   const float *x2 = a.X2 ? a.X2 + (size_t)blockIdx.y * K : nullptr;
   float *y = a.Y + (size_t)blockIdx.y * N;
 
-  const int T = P * rpw;
-  const int r0 = (blockIdx.x * 4 + wave) * T;
+  constexpr bool PAIR = EPI == EPI_SWIGLU;
+  const int NO = PAIR ? N / 2 : N;
+  float *yo = a.Y + (size_t)blockIdx.y * NO;
+  const int T = P * rpw;  // tile rows (PAIR: T/2 gate + T/2 up, T is even)
+  const int r0 = (blockIdx.x * 4 + wave) * (PAIR ? T / 2 : T);
+  auto tile_row = [&](int t) -> int {
+    return PAIR ? (t < T / 2 ? r0 + t : N / 2 + r0 + t - T / 2) : r0 + t;
+  };
+  auto row_ok = [&](int t) -> bool {
+    return PAIR ? (r0 + (t < T / 2 ? t : t - T / 2)) < NO : (r0 + t) < N;
+  };
 
   uint4 q[P][NV];
   float d[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
-    const int rw = r0 + p * rpw + rs;
-    const bool ok = active && rw < N;
+    const int rw = tile_row(p * rpw + rs);
+    const bool ok = active && row_ok(p * rpw + rs);
     const uint8_t *src = a.qs + ((size_t)rw * B + b) * QB;
 #pragma unroll
     for (int v = 0; v < NV; ++v)
       q[p][v] = ok ? ld_stream(src + v * 16) : make_uint4(0u, 0u, 0u, 0u);
     d[p] = 1.f;
     if constexpr (TYPE != PBX_F32)
-      d[p] = ok ? f16_bits_to_f32(a.dsc[((size_t)(rw >> 3) * B + b) * 8 + (rw & 7)]) : 0.f;
+      d[p] = ok ? f16_bits_to_f32(a.dsc[dsc_index(rw, b, B)]) : 0.f;
   }
 
   float xr[32];
@@ -415,11 +465,23 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
 
 #pragma unroll
   for (int p = 0; p < P; ++p) {
-    const int rw = r0 + p * rpw + rs;
-    const bool ok = active && rw < N;
+    const bool ok = active && row_ok(p * rpw + rs);
     part[wave][p][lane] = ok ? block_term<TYPE>(q[p], xr, corr, d[p]) : 0.f;
   }
   __syncthreads();
+  if constexpr (PAIR) {
+    for (int t = lane; t < T / 2; t += 64) {
+      const int tu = t + T / 2;
+      float g = 0.f, u = 0.f;
+      for (int j = 0; j < B; ++j) {
+        g += part[wave][t / rpw][(t % rpw) * B + j];
+        u += part[wave][tu / rpw][(tu % rpw) * B + j];
+      }
+      const int n = r0 + t;
+      if (n < NO) yo[n] = silu(g) * u;
+    }
+    return;
+  }
   uint64_t key = 0;
   for (int t = lane; t < T; t += 64) {
     const int p = t / rpw, r = t % rpw;

@@ -27,7 +27,8 @@
   X(PBX_K_GEMV_Q4_0_SMALL, "pbx_gemv_q4_0_small")            \
   X(PBX_K_GEMV_Q8_0_SMALL, "pbx_gemv_q8_0_small")            \
   X(PBX_K_GEMV_F32_SMALL, "pbx_gemv_f32_small")              \
-  X(PBX_K_GEMV_Q8REF, "pbx_gemv_q8ref")
+  X(PBX_K_GEMV_Q8REF, "pbx_gemv_q8ref")                      \
+  X(PBX_K_COPY16, "pbx_copy16")
 
 enum {
 #define X(id, name) id,

@@ -10,6 +10,7 @@
 // matrix each so a single GEMV reads them.
 
 #include <math.h>
+#include <stdio.h>
 #include <string.h>
 
 #include <algorithm>
@@ -67,6 +68,8 @@ enum ArgKind { ARG_GEMV, ARG_ATTN, ARG_EMBED, ARG_ARGMAX };
 struct Op {
   hipFunction_t f = nullptr;
   std::string name;
+  std::string role;      // embed / qkv / attn / o / gate_up / down / lm_head / argmax
+  double bytes = 0;      // algorithmic bytes per launch (attention: per cached position)
   dim3 grid, block;
   ArgKind kind;
   GemvArgsHost gemv;
@@ -145,8 +148,9 @@ static void plan_gemv(pbx_ctx *c, int type, int N, int B, std::string *shape, di
   *n_tiles = (int)grid->x;
 }
 
-static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const float *X,
-                    const float *X2, const float *normw, float *Y, int *n_tiles_out) {
+static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const char *role,
+                    const float *X, const float *X2, const float *normw, float *Y,
+                    int *n_tiles_out) {
   pbx_ctx *c = m->c;
   Op op;
   op.kind = ARG_GEMV;
@@ -161,6 +165,12 @@ static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const f
   if (!op.f) return pbx_fail(c, PBX_ELOAD, "model: kernel %s not found", op.name.c_str());
   op.gemv = GemvArgsHost{w->qs, w->d, X, X2, normw, nullptr, Y, m->partials, (int)w->N,
                          (int)w->B, m->cfg.rms_eps};
+  op.role = role;
+  // weights + activation reads (+ up for SwiGLU, + norm weight) + output
+  // (read and written for the residual epilogue)
+  op.bytes = (double)w->N * w->B * pbx_type_block_bytes(w->type) + 4.0 * w->K * (X2 ? 2 : 1) +
+             (normw ? 4.0 * w->K : 0.0) +
+             (strcmp(mode, "add") == 0 ? 8.0 * w->N : strcmp(mode, "gu") == 0 ? 2.0 * w->N : 4.0 * w->N);
   if (n_tiles_out) *n_tiles_out = n_tiles;
   m->ops.push_back(op);
   return PBX_OK;
@@ -177,6 +187,8 @@ static int build_ops(pbx_model *m) {
   if (!e.f) return pbx_fail(c, PBX_ELOAD, "model: kernel pbx_embed not found");
   e.grid = dim3((g.dim + 255) / 256);
   e.block = dim3(256);
+  e.role = "embed";
+  e.bytes = (double)g.dim / 32 * pbx_type_block_bytes(m->embd->type) + 4.0 * g.dim;
   e.embed = EmbedArgsHost{m->embd->qs, m->embd->d, m->x, m->state, kernel_type(m->embd->type),
                           g.dim, g.vocab_size};
   m->ops.push_back(e);
@@ -186,25 +198,26 @@ static int build_ops(pbx_model *m) {
   for (int l = 0; l < g.n_layers; ++l) {
     Layer &L = m->layers[l];
     int rc;
-    if ((rc = add_gemv(m, L.wqkv, "qkv", m->x, nullptr, L.attn_norm, m->qkv, nullptr))) return rc;
+    if ((rc = add_gemv(m, L.wqkv, "qkv", "qkv", m->x, nullptr, L.attn_norm, m->qkv, nullptr))) return rc;
     Op a;
     a.kind = ARG_ATTN;
     a.name = "pbx_attention_decode";
     a.f = fattn;
     a.grid = dim3(g.n_heads);
     a.block = dim3(256);
+    a.role = "attn";
+    a.bytes = 2.0 * 4.0 * m->kvdim;  // K and V of one cached position, all KV heads
     a.attn = AttnArgsHost{m->qkv, m->kcache + l * layer_kv, m->vcache + l * layer_kv, m->rope,
                           m->attn, m->state, g.n_heads, g.n_kv_heads, g.head_dim,
                           (float)(1.0 / sqrt((double)g.head_dim))};
     m->ops.push_back(a);
-    if ((rc = add_gemv(m, L.wo, "add", m->attn, nullptr, nullptr, m->x, nullptr))) return rc;
-    if ((rc = add_gemv(m, L.wgu, "qkv", m->x, nullptr, L.ffn_norm, m->gu, nullptr))) return rc;
-    if ((rc = add_gemv(m, L.wd, "swa", m->gu, m->gu + g.hidden_dim, nullptr, m->x, nullptr)))
-      return rc;
+    if ((rc = add_gemv(m, L.wo, "add", "o", m->attn, nullptr, nullptr, m->x, nullptr))) return rc;
+    if ((rc = add_gemv(m, L.wgu, "gu", "gate_up", m->x, nullptr, L.ffn_norm, m->gu, nullptr))) return rc;
+    if ((rc = add_gemv(m, L.wd, "add", "down", m->gu, nullptr, nullptr, m->x, nullptr))) return rc;
   }
   int n_tiles = 0;
   const pbx_weight *head = m->output ? m->output : m->embd;
-  int rc = add_gemv(m, head, "lmh", m->x, nullptr, m->out_norm, m->logits, &n_tiles);
+  int rc = add_gemv(m, head, "lmh", "lm_head", m->x, nullptr, m->out_norm, m->logits, &n_tiles);
   if (rc) return rc;
   if (n_tiles > m->n_partials_cap)
     return pbx_fail(c, PBX_EINVAL, "model: %d argmax partials exceed capacity %d", n_tiles,
@@ -216,10 +229,24 @@ static int build_ops(pbx_model *m) {
   if (!am.f) return pbx_fail(c, PBX_ELOAD, "model: kernel pbx_argmax_final not found");
   am.grid = dim3(1);
   am.block = dim3(1024);
+  am.role = "argmax";
+  am.bytes = 8.0 * n_tiles;
   am.amax = ArgmaxArgsHost{m->partials, m->state, m->hist, n_tiles, m->hist_cap};
   m->ops.push_back(am);
   m->ops_ready = true;
   return PBX_OK;
+}
+
+static int enqueue_op(pbx_model *m, Op &op) {
+  void *arg;
+  switch (op.kind) {
+    case ARG_GEMV: arg = &op.gemv; break;
+    case ARG_ATTN: arg = &op.attn; break;
+    case ARG_EMBED: arg = &op.embed; break;
+    default: arg = &op.amax; break;
+  }
+  void *args[] = {arg};
+  return pbx_launch_fn(m->c, op.f, op.name.c_str(), op.grid, op.block, args, m->c->stream);
 }
 
 static int enqueue_ops(pbx_model *m) {
@@ -612,5 +639,67 @@ extern "C" int pbx_model_info(const pbx_model *m, size_t *device_bytes, int *use
   if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_info: not a live model");
   if (device_bytes) *device_bytes = m->bytes;
   if (uses_graph) *uses_graph = m->graph_ok ? 1 : 0;
+  return PBX_OK;
+}
+
+extern "C" int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int n_steps,
+                                 double *op_us, double *op_bytes, int cap, int *n_ops) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_profile: not a live model");
+  pbx_ctx *c = m->c;
+  if (!op_us || !n_ops || cap <= 0 || n_steps <= 0)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_profile: bad arguments");
+  if (token < 0 || token >= m->cfg.vocab_size || start_pos < 0 ||
+      (int64_t)start_pos + n_steps > m->cfg.max_seq)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_profile: token/positions out of range");
+  int rc = check_complete(m);
+  if (rc) return rc;
+  if (!m->ops_ready && (rc = build_ops(m))) return rc;
+  const int n = (int)m->ops.size();
+  std::vector<hipEvent_t> ev(n + 1, nullptr);
+  for (auto &e : ev)
+    if (hipEventCreate(&e) != hipSuccess) {
+      for (auto &f : ev)
+        if (f) hipEventDestroy(f);
+      return pbx_fail(c, PBX_EHIP, "pbx_model_profile: hipEventCreate failed");
+    }
+  std::vector<double> acc(n, 0.0), bytes(n, 0.0);
+  if ((rc = set_state(m, start_pos, token, 0))) goto out;
+  for (int s = 0; s < n_steps && !rc; ++s) {
+    if (hipEventRecord(ev[0], c->stream) != hipSuccess) { rc = pbx_fail(c, PBX_EHIP, "event"); break; }
+    for (int i = 0; i < n && !rc; ++i) {
+      rc = enqueue_op(m, m->ops[i]);
+      if (!rc && hipEventRecord(ev[i + 1], c->stream) != hipSuccess)
+        rc = pbx_fail(c, PBX_EHIP, "pbx_model_profile: hipEventRecord failed");
+    }
+    if (rc || hipEventSynchronize(ev[n]) != hipSuccess) {
+      if (!rc) rc = pbx_fail(c, PBX_EHIP, "pbx_model_profile: step failed on the device");
+      break;
+    }
+    for (int i = 0; i < n; ++i) {
+      float ms = 0.f;
+      hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+      acc[i] += ms * 1e3;
+      const Op &op = m->ops[i];
+      bytes[i] += op.kind == ARG_ATTN ? op.bytes * (start_pos + s + 1) : op.bytes;
+    }
+  }
+  if (!rc) {
+    const int k = std::min(n, cap);
+    for (int i = 0; i < k; ++i) {
+      op_us[i] = acc[i] / n_steps;
+      if (op_bytes) op_bytes[i] = bytes[i] / n_steps;
+    }
+    *n_ops = n;
+  }
+out:
+  for (auto &e : ev) hipEventDestroy(e);
+  return rc;
+}
+
+extern "C" int pbx_model_op_name(const pbx_model *m, int i, char *buf, size_t cap) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_op_name: not a live model");
+  if (i < 0 || i >= (int)m->ops.size() || !buf || !cap)
+    return pbx_fail(m->c, PBX_EINVAL, "pbx_model_op_name: op %d out of range", i);
+  snprintf(buf, cap, "%s:%s", m->ops[i].role.c_str(), m->ops[i].name.c_str());
   return PBX_OK;
 }

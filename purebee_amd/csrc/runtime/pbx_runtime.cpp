@@ -649,6 +649,17 @@ extern "C" int pbx_memset_dev(pbx_ctx *c, void *dst, int value, size_t bytes) {
   return PBX_OK;
 }
 
+extern "C" int pbx_dev_copy(pbx_ctx *c, void *dst, const void *src, size_t bytes) {
+  if (!c || !dst || !src) return pbx_fail(c, PBX_EINVAL, "pbx_dev_copy: NULL argument");
+  if (bytes % 16 || ((uintptr_t)dst | (uintptr_t)src) % 16)
+    return pbx_fail(c, PBX_EINVAL, "pbx_dev_copy: size and addresses must be 16-byte aligned");
+  HIPCHK(c, hipSetDevice(c->device));
+  int64_t n16 = (int64_t)(bytes / 16);
+  const unsigned grid = (unsigned)std::min<int64_t>((n16 + 255) / 256, 4 * 1024);
+  void *args[] = {(void *)&src, &dst, &n16};
+  return pbx_launch(c, PBX_K_COPY16, dim3(grid ? grid : 1), dim3(256), args);
+}
+
 extern "C" int pbx_sync(pbx_ctx *c) {
   if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_sync: ctx is NULL");
   HIPCHK(c, hipSetDevice(c->device));

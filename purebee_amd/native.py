@@ -26,9 +26,10 @@ EXPORTS = (
     "pbx_linear", "pbx_linear_dev", "pbx_dequant", "pbx_dequant_dev",
     "pbx_quantize_q8_0", "pbx_quantize_q4_0", "pbx_quantize_q8_ref", "pbx_synth_normal",
     "pbx_dev_alloc", "pbx_dev_free", "pbx_memcpy_h2d", "pbx_memcpy_d2h", "pbx_memset_dev",
-    "pbx_sync", "pbx_timer_start", "pbx_timer_stop", "pbx_bench_linear",
+    "pbx_dev_copy", "pbx_sync", "pbx_timer_start", "pbx_timer_stop", "pbx_bench_linear",
     "pbx_model_create", "pbx_model_free", "pbx_model_set_tensor", "pbx_model_forward",
     "pbx_model_generate", "pbx_model_reset_cache", "pbx_model_rollback", "pbx_model_info",
+    "pbx_model_profile", "pbx_model_op_name",
 )
 
 # Tensor ids of pbx_model_set_tensor (GGUF tensor names, gguf.js:378-410).
@@ -99,6 +100,7 @@ def load_library():
         "pbx_memcpy_h2d": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_size_t]),
         "pbx_memcpy_d2h": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_size_t]),
         "pbx_memset_dev": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_size_t]),
+        "pbx_dev_copy": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_size_t]),
         "pbx_sync": (ctypes.c_int, [_vp]),
         "pbx_timer_start": (ctypes.c_int, [_vp]),
         "pbx_timer_stop": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_double)]),
@@ -114,6 +116,9 @@ def load_library():
         "pbx_model_rollback": (ctypes.c_int, [_vp, ctypes.c_int]),
         "pbx_model_info": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_size_t),
                                           ctypes.POINTER(ctypes.c_int)]),
+        "pbx_model_profile": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int, ctypes.c_int,
+                                             _vp, _vp, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]),
+        "pbx_model_op_name": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -279,6 +284,9 @@ class Context:
     def sync(self):
         self._call("pbx_sync", self._p)
 
+    def dev_copy(self, dst, src, nbytes):
+        self._call("pbx_dev_copy", self._p, dst, src, nbytes)
+
     def timer_start(self):
         self._call("pbx_timer_start", self._p)
 
@@ -347,6 +355,22 @@ class Model:
         b, g = ctypes.c_size_t(), ctypes.c_int()
         self._mcall("pbx_model_info", ctypes.byref(b), ctypes.byref(g))
         return {"device_bytes": b.value, "graph": bool(g.value)}
+
+    def profile(self, token, start_pos, n_steps):
+        """[(role, kernel, mean us, mean algorithmic bytes)] per kernel of a step."""
+        cap = 4096
+        us = np.zeros(cap, np.float64)
+        by = np.zeros(cap, np.float64)
+        n = ctypes.c_int()
+        self._mcall("pbx_model_profile", int(token), start_pos, n_steps, us.ctypes.data,
+                    by.ctypes.data, cap, ctypes.byref(n))
+        out = []
+        buf = ctypes.create_string_buffer(256)
+        for i in range(min(n.value, cap)):
+            self._mcall("pbx_model_op_name", i, buf, 256)
+            role, kern = buf.value.decode().split(":", 1)
+            out.append((role, kern, float(us[i]), float(by[i])))
+        return out
 
     def free(self):
         if self._m:
