@@ -225,6 +225,14 @@ int pbx_model_info(const pbx_model *m, size_t *device_bytes, int *uses_graph);
 int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int n_steps,
                       double *op_us, double *op_bytes, int cap, int *n_ops);
 int pbx_model_op_name(const pbx_model *m, int i, char *buf, size_t cap);
+/* Measurement: the GEMV kernels of one role ("qkv", "o", "gate_up", "down",
+ * "lm_head") launched back to back over every layer's weights, `reps`
+ * passes between two HIP events on the model's stream; returns the mean
+ * time and algorithmic bytes per launch.  Leaves the activations in an
+ * unspecified state (the next forward re-embeds its token). */
+int pbx_model_bench_role(pbx_model *m, const char *role, int reps,
+                         double *us_per_launch, double *bytes_per_launch,
+                         int *launches_per_rep);
 
 #ifdef __cplusplus
 }

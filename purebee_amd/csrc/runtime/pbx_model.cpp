@@ -703,3 +703,37 @@ extern "C" int pbx_model_op_name(const pbx_model *m, int i, char *buf, size_t ca
   snprintf(buf, cap, "%s:%s", m->ops[i].role.c_str(), m->ops[i].name.c_str());
   return PBX_OK;
 }
+
+extern "C" int pbx_model_bench_role(pbx_model *m, const char *role, int reps,
+                                    double *us_per_launch, double *bytes_per_launch,
+                                    int *launches_per_rep) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_bench_role: not a live model");
+  pbx_ctx *c = m->c;
+  if (!role || reps <= 0 || !us_per_launch)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_bench_role: bad arguments");
+  int rc = check_complete(m);
+  if (rc) return rc;
+  if (!m->ops_ready && (rc = build_ops(m))) return rc;
+  std::vector<Op *> sel;
+  double bytes = 0;
+  for (Op &op : m->ops)
+    if (op.kind == ARG_GEMV && op.role == role) {
+      sel.push_back(&op);
+      bytes += op.bytes;
+    }
+  if (sel.empty())
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_bench_role: no GEMV with role '%s'", role);
+  for (Op *op : sel)  // warm-up pass
+    if ((rc = enqueue_op(m, *op))) return rc;
+  if (hipEventRecord(c->ev0, c->stream) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_bench_role: hipEventRecord failed");
+  for (int r = 0; r < reps; ++r)
+    for (Op *op : sel)
+      if ((rc = enqueue_op(m, *op))) return rc;
+  double ms = 0;
+  if ((rc = pbx_timer_stop(c, &ms))) return rc;
+  *us_per_launch = ms * 1e3 / ((double)reps * sel.size());
+  if (bytes_per_launch) *bytes_per_launch = bytes / sel.size();
+  if (launches_per_rep) *launches_per_rep = (int)sel.size();
+  return PBX_OK;
+}

@@ -29,7 +29,7 @@ EXPORTS = (
     "pbx_dev_copy", "pbx_sync", "pbx_timer_start", "pbx_timer_stop", "pbx_bench_linear",
     "pbx_model_create", "pbx_model_free", "pbx_model_set_tensor", "pbx_model_forward",
     "pbx_model_generate", "pbx_model_reset_cache", "pbx_model_rollback", "pbx_model_info",
-    "pbx_model_profile", "pbx_model_op_name",
+    "pbx_model_profile", "pbx_model_op_name", "pbx_model_bench_role",
 )
 
 # Tensor ids of pbx_model_set_tensor (GGUF tensor names, gguf.js:378-410).
@@ -119,6 +119,10 @@ def load_library():
         "pbx_model_profile": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int, ctypes.c_int,
                                              _vp, _vp, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]),
         "pbx_model_op_name": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]),
+        "pbx_model_bench_role": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int,
+                                                ctypes.POINTER(ctypes.c_double),
+                                                ctypes.POINTER(ctypes.c_double),
+                                                ctypes.POINTER(ctypes.c_int)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -371,6 +375,13 @@ class Model:
             role, kern = buf.value.decode().split(":", 1)
             out.append((role, kern, float(us[i]), float(by[i])))
         return out
+
+    def bench_role(self, role, reps):
+        """(us per launch, algorithmic bytes per launch, launches per pass)."""
+        us, by, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int()
+        self._mcall("pbx_model_bench_role", role.encode(), reps, ctypes.byref(us),
+                    ctypes.byref(by), ctypes.byref(n))
+        return us.value, by.value, n.value
 
     def free(self):
         if self._m:
