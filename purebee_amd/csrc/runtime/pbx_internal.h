@@ -38,7 +38,7 @@ enum {
 };
 
 // Row count from which quantized linears take the MFMA GEMM path.
-#define PBX_GEMM_MIN_M (1 << 30)
+#define PBX_GEMM_MIN_M 4
 
 #define PBX_MAX_MODULES 8
 
@@ -58,6 +58,8 @@ struct pbx_ctx {
   // grow-only scratch
   void *d_x = nullptr, *d_y = nullptr, *d_b = nullptr;
   size_t d_x_cap = 0, d_y_cap = 0, d_b_cap = 0;
+  void *d_gemm = nullptr;  // GEMM workspace: fp16 activations, row scales, split-K partials
+  size_t d_gemm_cap = 0;
   void *d_stage[2] = {nullptr, nullptr};
   size_t d_stage_cap[2] = {0, 0};
   void *h_io = nullptr;
@@ -95,6 +97,8 @@ int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t
                        const float *dBias, float *dY, hipStream_t stream);
 int pbx_gemm_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
                      const float *dBias, float *dY, hipStream_t stream);
+int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
+                    const float *dBias, float *dY, int accumulate, hipStream_t stream);
 size_t pbx_type_block_bytes(int type);
 void pbx_model_release_all(pbx_ctx *c);
 

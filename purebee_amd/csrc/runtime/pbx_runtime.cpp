@@ -50,7 +50,7 @@ static const char *const kKernelNames[PBX_K_COUNT] = {
 
 // Code objects built from purebee_amd/csrc/kernels/*.hip, found next to this
 // library (or in the directory named by PBX_KERNEL_DIR).
-static const char *const kModuleFiles[] = {"pbx_gemv.hsaco", "pbx_decode.hsaco"};
+static const char *const kModuleFiles[] = {"pbx_gemv.hsaco", "pbx_decode.hsaco", "pbx_gemm.hsaco"};
 static const int kModuleCount = (int)(sizeof kModuleFiles / sizeof kModuleFiles[0]);
 
 static std::string code_object_dir() {
@@ -147,7 +147,7 @@ extern "C" void pbx_shutdown(pbx_ctx *c) {
   hipSetDevice(c->device);
   hipStreamSynchronize(c->stream);
   pbx_model_release_all(c);
-  for (void *p : {c->d_x, c->d_y, c->d_b, c->d_stage[0], c->d_stage[1]})
+  for (void *p : {c->d_x, c->d_y, c->d_b, c->d_gemm, c->d_stage[0], c->d_stage[1]})
     if (p) hipFree(p);
   for (void *p : {c->h_io, c->h_stage[0], c->h_stage[1]})
     if (p) hipHostFree(p);

@@ -180,3 +180,45 @@ def test_error_paths_on_device(ctx):
         ctx._call("pbx_linear", ctx._p, None, np.zeros(32, np.float32).ctypes.data, 1, None,
                   np.zeros(2, np.float32).ctypes.data)
     assert e.value.code == -1
+
+
+GEMM_SHAPES = [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192), (576, 576), (1536, 576),
+               (576, 1536), (288, 288), (768, 288), (288, 768), (100, 64)]
+
+
+@pytest.mark.parametrize("t", [pb.TYPE_Q4_0, pb.TYPE_Q8_0])
+@pytest.mark.parametrize("M", [4, 5, 17, 64, 130])
+@pytest.mark.parametrize("N,K", GEMM_SHAPES)
+def test_mfma_gemm_parity(ctx, t, M, N, K):
+    """M >= 4 takes the MFMA path (fp16 operands, fp32 accumulation): every
+    row within 1e-3 relative L2 of the oracle's double-accumulated matvec."""
+    print(f"[case] gemm type={t} M={M} N={N} K={K}", flush=True)
+    raw = quantize(t, synth_matrix(11 * N + K + M, N, K))
+    X = pb.synth_normal(M * 7 + K, M * K).reshape(M, K)
+    X[1] *= 1e-3   # rows of very different magnitude: per-row scaling
+    X[2] *= 300.0
+    bias = pb.synth_normal(3, N)
+    w = ctx.upload(t, N, K, raw)
+    Y = ctx.linear(w, X, bias)
+    assert Y.shape == (M, N)
+    rows = range(M) if M <= 17 else [0, 1, 2, M // 2, M - 1]
+    for m in rows:
+        ref = oracle.matvec(t, X[m], raw, N, K) + bias
+        assert rel_l2(Y[m], ref) <= TOL, (m, rel_l2(Y[m], ref))
+    # every row against the M=1 GEMV (fp32 path)
+    for m in range(M):
+        assert rel_l2(Y[m], ctx.linear(w, X[m]) + bias) <= TOL
+    w.free()
+
+
+def test_mfma_gemm_prefill_shape(ctx):
+    """The prefill shape of the M>1 config: M = 512 on the gate/up matrix."""
+    N, K, M = 16384, 2048, 512
+    print(f"[case] gemm prefill M={M} N={N} K={K}", flush=True)
+    raw = pb.quantize_q4_0(synth_matrix(99, N, K))
+    X = pb.synth_normal(98, M * K).reshape(M, K)
+    w = ctx.upload(pb.TYPE_Q4_0, N, K, raw)
+    Y = ctx.linear(w, X)
+    for m in (0, 255, 511):
+        assert rel_l2(Y[m], oracle.q4_0_matvec_js(X[m], raw, N, K)) <= TOL
+    w.free()
