@@ -205,6 +205,14 @@ int pbx_model_set_tensor(pbx_model *m, int tensor, int layer, const void *data,
  * the last position's logits (if logits != NULL, [vocab]) and its argmax. */
 int pbx_model_forward(pbx_model *m, const int32_t *tokens, int n_tokens,
                       int start_pos, float *logits, int32_t *next_token);
+/* forward() over n tokens in ONE batched pass that keeps every position's
+ * output (the reference computes them inside forward, llama.js:204-371, and
+ * keeps only the last): logits [n][vocab] (or NULL) and next_tokens[n], the
+ * argmax of each row (or NULL).  Quantized matrices run on the MFMA GEMM
+ * with all n rows; this is the speculative verify of speculative.js:131-185
+ * done as one forward instead of one forward per draft token. */
+int pbx_model_forward_batch(pbx_model *m, const int32_t *tokens, int n_tokens,
+                            int start_pos, float *logits, int32_t *next_tokens);
 /* The greedy decode loop of generate() (llama.js:475-489): feeds `token` at
  * start_pos, then each step's argmax, n_steps times, entirely on the GPU;
  * out_tokens[i] is the token chosen by step i. */
@@ -233,6 +241,30 @@ int pbx_model_op_name(const pbx_model *m, int i, char *buf, size_t cap);
 int pbx_model_bench_role(pbx_model *m, const char *role, int reps,
                          double *us_per_launch, double *bytes_per_launch,
                          int *launches_per_rep);
+
+/* ---- speculative decoding ----------------------------------------------
+ * SelfSpeculativeDecoder.generate (speculative.js:58-204) in its greedy
+ * mode, with the draft taken from a separate (smaller) model instead of the
+ * target's first layers.  Both caches are reset, the prompt is prefilled
+ * into both, then each round drafts up to draft_count tokens with `draft`,
+ * verifies them with `target`, accepts the longest agreeing prefix, emits
+ * the target's own token at the first disagreement (or a bonus token when
+ * every draft agrees) and rolls the target's cache back past the rejected
+ * positions.  batched_verify = 1 verifies a round's drafts in one
+ * pbx_model_forward_batch (M = drafts + 1); 0 verifies them one forward at
+ * a time as the reference does.  Token ids outside a model's vocabulary are
+ * taken modulo it (draft and target vocabularies may differ).
+ * out_tokens receives the generated tokens (not the prompt): at most
+ * max_tokens + 1 of them (the reference's bound), *n_out of them. */
+typedef struct pbx_spec_stats {
+  int32_t rounds, drafted, accepted;
+  double prefill_ms, decode_ms;  /* host wall clock around the two phases */
+} pbx_spec_stats;
+
+int pbx_speculative_generate(pbx_model *target, pbx_model *draft, const int32_t *prompt,
+                             int n_prompt, int max_tokens, int draft_count,
+                             const int32_t *eos_ids, int n_eos, int batched_verify,
+                             int32_t *out_tokens, int *n_out, pbx_spec_stats *stats);
 
 #ifdef __cplusplus
 }

@@ -4,8 +4,9 @@
 //
 // One v_mfma_f32_16x16x32_f16 consumes exactly one 32-wide quantisation
 // block: the A operand is 16 activation rows x 32 k (fp16), the B operand is
-// 16 weight rows x 32 k dequantised on the fly, the 16x16 fp32 accumulator
-// sums over blocks.  Operand lane layout (checked on the device):
+// the 16 x 32 integer codes of 16 weight rows unpacked on the fly, and the
+// 16x16 block product, times each row's block scale, is summed over blocks
+// in fp32.  Operand lane layout (checked on the device):
 //   A: lane l holds A[l%16][8*(l/16) + e], e = 0..7
 //   B: lane l holds B[8*(l/16) + e][l%16]
 //   D: lane l holds D[4*(l/16) + r][l%16], r = 0..3
@@ -13,58 +14,78 @@
 // of bytes 0..7 (g=0), of bytes 8..15 (g=1), high nibbles of bytes 0..7
 // (g=2) and of bytes 8..15 (g=3), the element order of gguf.js:259-286.
 //
-// Precision: activations are scaled per row by a power of two so the row's
-// largest magnitude sits just below 2^15, then rounded to fp16 (relative
-// error <= 2^-11); weights are (q - 8) * d rounded once to fp16 (the product
-// is exact in fp32).  Accumulation is fp32; the power of two is undone
-// exactly in the epilogue.
+// Precision: weights enter the MFMA as their integer codes (q - 8 for Q4_0,
+// q for Q8_0), which fp16 holds exactly; the block scale d multiplies the
+// block's 16x16 partial product in fp32 afterwards, so the weight side adds
+// no rounding at all.  Activations are scaled per row by a power of two so
+// the row's largest magnitude sits just below 2^15 and split into two fp16
+// operands, hi = fp16(x) and lo = fp16(x - hi), each multiplied by the same
+// weight codes (two MFMAs per tile and block): ~22 significant bits instead
+// of fp16's 11.  A single fp16 (or bf16) activation operand is not accurate
+// enough for the end-to-end bar: on the Llama-3.2-1B shape a 512-token
+// prefill with fp16 activations ends 6.4e-3 (max-abs) away from the fp32
+// decode path's logits, against a 2e-3 tolerance.  Accumulation is fp32;
+// the power of two is undone exactly in the epilogue.
 
 #include "pbx_gemv_impl.h"
 
 using namespace pbx;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 struct GemmArgs {
-  const uint8_t *qs;    // weight plane
-  const uint16_t *dsc;  // fp16 scale plane (4-row groups)
-  const _Float16 *X16;  // [Mpad][K] scaled fp16 activations
-  const float *inv;     // [Mpad] power of two undoing the row scale
-  const float *bias;    // [N] or null (single split only)
-  float *Y;             // KS == 1: [M][N]; else partials [KS][M][N]
+  const uint8_t *qs;      // weight plane
+  const uint16_t *dsc;    // fp16 scale plane (4-row groups)
+  const _Float16 *X16;    // [Mpad][K] scaled fp16 activations
+  const _Float16 *X16lo;  // [Mpad][K] rounding residual of X16
+  const float *inv;       // [Mpad] power of two undoing the row scale
+  const float *bias;      // [N] or null (single split only)
+  float *Y;               // KS == 1: [M][N]; else partials [KS][M][N]
   int M, N, Npad, B, KS;
-  int accumulate;       // 1: Y[m][n] += result (residual), single split only
+  int accumulate;         // 1: Y[m][n] += result (residual), single split only
 };
 
 namespace {
 
+// Two byte-sized codes c0, c1 (< 256, in bits 0-7 and 8-15 of v) as fp16
+// 1024 + c (exact: fp16 spacing is 1 on [1024, 2048)), minus `bias`.
+__device__ __forceinline__ half2v codes_to_half2(unsigned v, _Float16 bias) {
+  const unsigned p = (v & 0xFFu) | ((v & 0xFF00u) << 8) | 0x64006400u;
+  return __builtin_bit_cast(half2v, p) - half2v{bias, bias};
+}
+
+// Lane group g's 8 integer weight codes of row n, block b, and the block
+// scale (0 for padding rows).
 template <int TYPE>
-__device__ __forceinline__ half8 weight_operand(const GemmArgs &a, int n, int b, int g) {
+__device__ __forceinline__ half8 weight_codes(const GemmArgs &a, int n, int b, int g, float *d) {
   half8 v;
   if (n >= a.Npad) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = (_Float16)0.f;
+    *d = 0.f;
     return v;
   }
-  const float d = f16_bits_to_f32(a.dsc[dsc_index(n, b, a.B)]);
+  *d = f16_bits_to_f32(a.dsc[dsc_index(n, b, a.B)]);
+  unsigned x, y;
+  _Float16 bias;
   if constexpr (TYPE == PBX_Q4) {
     const uint2 w = *reinterpret_cast<const uint2 *>(a.qs + ((size_t)n * a.B + b) * 16 + (g & 1) * 8);
     const unsigned sh = (g >> 1) * 4;  // low nibbles for g < 2, high for g >= 2
-    const unsigned lo = (w.x >> sh) & 0x0F0F0F0Fu, hi = (w.y >> sh) & 0x0F0F0F0Fu;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = (_Float16)((float)((int)((lo >> (8 * e)) & 0xFu) - 8) * d);
-      v[e + 4] = (_Float16)((float)((int)((hi >> (8 * e)) & 0xFu) - 8) * d);
-    }
+    x = (w.x >> sh) & 0x0F0F0F0Fu;
+    y = (w.y >> sh) & 0x0F0F0F0Fu;
+    bias = (_Float16)1032.f;  // 1024 + 8
   } else {
     const uint2 w = *reinterpret_cast<const uint2 *>(a.qs + ((size_t)n * a.B + b) * 32 + g * 8);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = (_Float16)((float)(int8_t)((w.x >> (8 * e)) & 0xFFu) * d);
-      v[e + 4] = (_Float16)((float)(int8_t)((w.y >> (8 * e)) & 0xFFu) * d);
-    }
+    x = w.x ^ 0x80808080u;  // int8 q -> q + 128
+    y = w.y ^ 0x80808080u;
+    bias = (_Float16)1152.f;  // 1024 + 128
   }
+  const half2v p0 = codes_to_half2(x, bias), p1 = codes_to_half2(x >> 16, bias);
+  const half2v p2 = codes_to_half2(y, bias), p3 = codes_to_half2(y >> 16, bias);
+  v[0] = p0[0]; v[1] = p0[1]; v[2] = p1[0]; v[3] = p1[1];
+  v[4] = p2[0]; v[5] = p2[1]; v[6] = p3[0]; v[7] = p3[1];
   return v;
 }
 
@@ -80,25 +101,34 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a) {
   const int per = (a.B + a.KS - 1) / a.KS;
   const int b0 = blockIdx.z * per;
   const int b1 = min(a.B, b0 + per);
+  const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
 
   floatx4 acc[MT][NT];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int u = 0; u < NT; ++u) acc[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < NT; ++u) acc[t][u] = zero;
 
   for (int b = b0; b < b1; ++b) {
-    half8 A[MT], W[NT];
+    half8 A[MT], Alo[MT], W[NT];
+    float d[NT];
 #pragma unroll
-    for (int u = 0; u < NT; ++u) W[u] = weight_operand<TYPE>(a, n0 + 16 * u + li, b, g);
+    for (int u = 0; u < NT; ++u) W[u] = weight_codes<TYPE>(a, n0 + 16 * u + li, b, g, &d[u]);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const size_t off = (size_t)(m0 + 16 * t + li) * K + b * 32 + 8 * g;
+      A[t] = *reinterpret_cast<const half8 *>(a.X16 + off);
+      Alo[t] = *reinterpret_cast<const half8 *>(a.X16lo + off);
+    }
 #pragma unroll
     for (int t = 0; t < MT; ++t)
-      A[t] = *reinterpret_cast<const half8 *>(a.X16 + (size_t)(m0 + 16 * t + li) * K + b * 32 + 8 * g);
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+      for (int u = 0; u < NT; ++u) {
+        floatx4 blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t], W[u], zero, 0, 0, 0);
+        blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(Alo[t], W[u], blk, 0, 0, 0);
 #pragma unroll
-      for (int u = 0; u < NT; ++u)
-        acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t], W[u], acc[t][u], 0, 0, 0);
+        for (int r = 0; r < 4; ++r) acc[t][u][r] = fmaf(blk[r], d[u], acc[t][u][r]);
+      }
   }
 
 #pragma unroll
@@ -146,14 +176,19 @@ GEMM_KERNEL(pbx_gemm_q8_m4_n4, PBX_Q8, 4, 4)
 
 // Row scaling to fp16: one workgroup per (padded) row.  The scale is
 // 2^(15 - e) with 2^(e-1) <= max|x| < 2^e, so every scaled value is below
-// 2^15 in magnitude (fp16 max 65504); padding rows are zero.
+// 2^15 in magnitude (fp16 max 65504); padding rows are zero.  X16lo gets
+// the residual x*scale - X16 rounded to fp16.
 extern "C" __global__ void __launch_bounds__(256)
-pbx_gemm_prep_x(const float *X, _Float16 *X16, float *inv, int M, int K) {
+pbx_gemm_prep_x(const float *X, _Float16 *X16, _Float16 *X16lo, float *inv, int M, int K) {
   __shared__ float red[4];
   const int m = blockIdx.x;
   _Float16 *dst = X16 + (size_t)m * K;
+  _Float16 *lo = X16lo + (size_t)m * K;
   if (m >= M) {
-    for (int k = threadIdx.x; k < K; k += blockDim.x) dst[k] = (_Float16)0.f;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+      dst[k] = (_Float16)0.f;
+      lo[k] = (_Float16)0.f;
+    }
     if (threadIdx.x == 0) inv[m] = 0.f;
     return;
   }
@@ -168,7 +203,12 @@ pbx_gemm_prep_x(const float *X, _Float16 *X16, float *inv, int M, int K) {
   int e = 0;
   if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
   const float scale = mx > 0.f ? ldexpf(1.f, 15 - e) : 1.f;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) dst[k] = (_Float16)(src[k] * scale);
+  for (int k = threadIdx.x; k < K; k += blockDim.x) {
+    const float v = src[k] * scale;  // exact: scale is a power of two
+    const _Float16 h = (_Float16)v;
+    dst[k] = h;
+    lo[k] = (_Float16)(v - (float)h);
+  }
   if (threadIdx.x == 0) inv[m] = mx > 0.f ? ldexpf(1.f, e - 15) : 1.f;
 }
 

@@ -13,6 +13,7 @@ struct GemmArgsHost {  // GemmArgs in pbx_gemm.hip
   const void *qs;
   const void *dsc;
   const void *X16;
+  const void *X16lo;
   const float *inv;
   const float *bias;
   float *Y;
@@ -45,15 +46,19 @@ int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M6
   const int waves = nwg * mtiles * 4;
   int KS = 1;
   if (waves < 8 * c->cu_count) KS = std::min({B, 8, (8 * c->cu_count + waves - 1) / waves});
+  // fp16 activations and their fp16 rounding residuals
   const size_t x16_bytes = ((size_t)Mpad * K * 2 + 255) / 256 * 256;
+  const size_t lo_bytes = x16_bytes;
   const size_t inv_bytes = ((size_t)Mpad * 4 + 255) / 256 * 256;
   const size_t part_bytes = KS > 1 ? (size_t)KS * M * N * 4 : 0;
-  int rc = pbx_ensure_dev(c, &c->d_gemm, &c->d_gemm_cap, x16_bytes + inv_bytes + part_bytes);
+  int rc = pbx_ensure_dev(c, &c->d_gemm, &c->d_gemm_cap,
+                          x16_bytes + lo_bytes + inv_bytes + part_bytes);
   if (rc) return rc;
   char *ws = (char *)c->d_gemm;
   void *x16 = ws;
-  float *inv = (float *)(ws + x16_bytes);
-  float *part = (float *)(ws + x16_bytes + inv_bytes);
+  void *x16lo = ws + x16_bytes;
+  float *inv = (float *)(ws + x16_bytes + lo_bytes);
+  float *part = (float *)(ws + x16_bytes + lo_bytes + inv_bytes);
 
   hipFunction_t fprep = pbx_kernel_by_name(c, "pbx_gemm_prep_x");
   const std::string name = std::string("pbx_gemm_") + (w->type == PBX_TYPE_Q4_0 ? "q4" : "q8") +
@@ -63,11 +68,11 @@ int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M6
   if (!fprep || !fg || !fred) return pbx_fail(c, PBX_ELOAD, "pbx_gemm: kernel %s missing", name.c_str());
   {
     int m = M, k = K;
-    void *args[] = {(void *)&dX, &x16, &inv, &m, &k};
+    void *args[] = {(void *)&dX, &x16, &x16lo, &inv, &m, &k};
     if ((rc = pbx_launch_fn(c, fprep, "pbx_gemm_prep_x", dim3(Mpad), dim3(256), args, stream)))
       return rc;
   }
-  GemmArgsHost g{w->qs, w->d, x16, inv, KS == 1 ? dBias : nullptr, KS == 1 ? dY : part,
+  GemmArgsHost g{w->qs, w->d, x16, x16lo, inv, KS == 1 ? dBias : nullptr, KS == 1 ? dY : part,
                  M, N, (int)w->Npad, B, KS, KS == 1 ? accumulate : 0};
   {
     void *args[] = {&g};

@@ -101,5 +101,8 @@ int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
                     const float *dBias, float *dY, int accumulate, hipStream_t stream);
 size_t pbx_type_block_bytes(int type);
 void pbx_model_release_all(pbx_ctx *c);
+int pbx_model_clear_range(pbx_model *m, int from, int to);
+const pbx_model_config *pbx_model_cfg(const pbx_model *m);
+pbx_ctx *pbx_model_ctx(const pbx_model *m);
 
 #endif

@@ -114,6 +114,12 @@ struct pbx_model {
   hipGraphExec_t exec = nullptr;
   bool graph_tried = false, graph_ok = false;
   size_t bytes = 0;
+  // Row-batched forward (prefill / verify): activations of up to batch_cap
+  // rows, grown on demand; logits of every row up to logits_cap rows.
+  int batch_cap = 0, logits_cap = 0;
+  float *bx = nullptr, *bxn = nullptr, *bqkv = nullptr, *battn = nullptr, *bgu = nullptr,
+        *bh = nullptr, *btmp = nullptr, *blogits = nullptr;
+  int *btok = nullptr, *bnext = nullptr;
 };
 
 static bool model_ok(const pbx_model *m) { return m && m->magic == PBX_MODEL_MAGIC; }
@@ -358,6 +364,10 @@ static void model_release(pbx_model *m) {
                   (void *)m->x, (void *)m->qkv, (void *)m->attn, (void *)m->gu, (void *)m->logits,
                   (void *)m->partials, (void *)m->state, (void *)m->hist})
     if (p) hipFree(p);
+  for (void *p : {(void *)m->bx, (void *)m->bxn, (void *)m->bqkv, (void *)m->battn,
+                  (void *)m->bgu, (void *)m->bh, (void *)m->btmp, (void *)m->blogits,
+                  (void *)m->btok, (void *)m->bnext})
+    if (p) hipFree(p);
   m->magic = 0;
   delete m;
 }
@@ -559,6 +569,157 @@ static int check_complete(pbx_model *m) {
   return PBX_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Row-batched forward: llama.js:204-371 with seqLen = n > 1.  Every linear
+// takes all n rows at once (the MFMA GEMM for Q4_0/Q8_0, the multi-row GEMV
+// for f32), so each weight is read once per forward instead of once per
+// token.  The KV rows of all n positions are appended before attention, and
+// attention row t sees positions 0..start+t (the causal mask of
+// llama.js:274-286).
+// ---------------------------------------------------------------------------
+
+static int grow(pbx_model *m, void **p, size_t bytes) {
+  if (*p) {
+    hipStreamSynchronize(m->c->stream);
+    hipFree(*p);
+    *p = nullptr;
+  }
+  if (hipMalloc(p, bytes) != hipSuccess) {
+    *p = nullptr;
+    return pbx_fail(m->c, PBX_ENOMEM, "model: hipMalloc(%zu) for the batch failed", bytes);
+  }
+  return PBX_OK;
+}
+
+static int ensure_batch(pbx_model *m, int rows, bool all_logits) {
+  const pbx_model_config &g = m->cfg;
+  int rc = PBX_OK;
+  if (rows > m->batch_cap) {
+    const size_t R = (size_t)rows;
+    const size_t tmp_cols = std::max({(size_t)g.dim, (size_t)m->qkv_rows, 2 * (size_t)g.hidden_dim});
+    if (!rc) rc = grow(m, (void **)&m->bx, R * g.dim * 4);
+    if (!rc) rc = grow(m, (void **)&m->bxn, R * g.dim * 4);
+    if (!rc) rc = grow(m, (void **)&m->bqkv, R * m->qkv_rows * 4);
+    if (!rc) rc = grow(m, (void **)&m->battn, R * g.dim * 4);
+    if (!rc) rc = grow(m, (void **)&m->bgu, R * 2 * g.hidden_dim * 4);
+    if (!rc) rc = grow(m, (void **)&m->bh, R * g.hidden_dim * 4);
+    if (!rc && g.weight_type == PBX_TYPE_F32) rc = grow(m, (void **)&m->btmp, R * tmp_cols * 4);
+    if (!rc) rc = grow(m, (void **)&m->btok, R * 4);
+    if (!rc) rc = grow(m, (void **)&m->bnext, R * 4);
+    if (rc) {
+      m->batch_cap = 0;
+      return rc;
+    }
+    m->batch_cap = rows;
+  }
+  if (all_logits && rows > m->logits_cap) {
+    if ((rc = grow(m, (void **)&m->blogits, (size_t)rows * g.vocab_size * 4))) {
+      m->logits_cap = 0;
+      return rc;
+    }
+    m->logits_cap = rows;
+  }
+  return PBX_OK;
+}
+
+static int launch_k(pbx_model *m, const char *name, dim3 grid, dim3 block, void **args) {
+  hipFunction_t f = pbx_kernel_by_name(m->c, name);
+  if (!f) return pbx_fail(m->c, PBX_ELOAD, "model: kernel %s not found", name);
+  return pbx_launch_fn(m->c, f, name, grid, block, args, m->c->stream);
+}
+
+// Y[n][N] (+)= X[n][K] . W^T over all rows.
+static int linear_rows(pbx_model *m, const pbx_weight *w, const float *X, int n, float *Y,
+                       bool accumulate) {
+  pbx_ctx *c = m->c;
+  if (w->type != PBX_TYPE_F32) return pbx_gemm_launch(c, w, X, n, nullptr, Y, accumulate ? 1 : 0, c->stream);
+  if (!accumulate) return pbx_linear_enqueue(c, w, X, n, nullptr, Y, c->stream);
+  int rc = pbx_linear_enqueue(c, w, X, n, nullptr, m->btmp, c->stream);
+  if (rc) return rc;
+  int64_t count = (int64_t)n * w->N;
+  float *y = Y, *t = m->btmp;
+  void *args[] = {&y, &t, &count};
+  return launch_k(m, "pbx_add_inplace", dim3((unsigned)((count + 255) / 256)), dim3(256), args);
+}
+
+static int rmsnorm_rows(pbx_model *m, const float *x, const float *w, float *out, int n) {
+  int dim = m->cfg.dim;
+  float eps = m->cfg.rms_eps;
+  void *args[] = {(void *)&x, (void *)&w, &out, &dim, &eps};
+  return launch_k(m, "pbx_rmsnorm_rows", dim3(n), dim3(256), args);
+}
+
+// Runs the layer stack over n rows; leaves the residual stream in m->bx.
+static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
+  pbx_ctx *c = m->c;
+  const pbx_model_config &g = m->cfg;
+  if (hipMemcpyAsync(m->btok, tokens, (size_t)n * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "model: token upload failed");
+  int rc;
+  {
+    const void *qs = m->embd->qs, *dsc = m->embd->d;
+    int *tok = m->btok;
+    float *x = m->bx;
+    int type = kernel_type(m->embd->type), dim = g.dim, vocab = g.vocab_size;
+    void *args[] = {(void *)&qs, (void *)&dsc, &tok, &x, &type, &dim, &vocab};
+    if ((rc = launch_k(m, "pbx_embed_rows", dim3((g.dim + 255) / 256, n), dim3(256), args))) return rc;
+  }
+  const size_t layer_kv = (size_t)g.max_seq * m->kvdim;
+  for (int l = 0; l < g.n_layers; ++l) {
+    Layer &L = m->layers[l];
+    float *kc = m->kcache + l * layer_kv, *vc = m->vcache + l * layer_kv;
+    if ((rc = rmsnorm_rows(m, m->bx, L.attn_norm, m->bxn, n))) return rc;
+    if ((rc = linear_rows(m, L.wqkv, m->bxn, n, m->bqkv, false))) return rc;
+    {
+      float *qkv = m->bqkv, *rope = m->rope;
+      int st = start, nh = g.n_heads, nkv = g.n_kv_heads, hd = g.head_dim;
+      void *args[] = {&qkv, &kc, &vc, &rope, &st, &nh, &nkv, &hd};
+      if ((rc = launch_k(m, "pbx_rope_append_rows", dim3(n), dim3(256), args))) return rc;
+    }
+    {
+      float *qkv = m->bqkv, *out = m->battn;
+      int st = start, nh = g.n_heads, nkv = g.n_kv_heads, hd = g.head_dim;
+      float scale = (float)(1.0 / sqrt((double)g.head_dim));
+      void *args[] = {&qkv, &kc, &vc, &out, &st, &nh, &nkv, &hd, &scale};
+      if ((rc = launch_k(m, "pbx_attention_rows", dim3(g.n_heads, n), dim3(256), args))) return rc;
+    }
+    if ((rc = linear_rows(m, L.wo, m->battn, n, m->bx, true))) return rc;
+    if ((rc = rmsnorm_rows(m, m->bx, L.ffn_norm, m->bxn, n))) return rc;
+    if ((rc = linear_rows(m, L.wgu, m->bxn, n, m->bgu, false))) return rc;
+    {
+      float *gu = m->bgu, *h = m->bh;
+      int hidden = g.hidden_dim;
+      void *args[] = {&gu, &h, &hidden};
+      if ((rc = launch_k(m, "pbx_swiglu_rows", dim3((g.hidden_dim + 255) / 256, n), dim3(256), args)))
+        return rc;
+    }
+    if ((rc = linear_rows(m, L.wd, m->bh, n, m->bx, true))) return rc;
+  }
+  return PBX_OK;
+}
+
+// Prefill: the layer stack over n rows, then the decode step's own LM head
+// and argmax on the last row, which leave the device state at
+// (start + n, next token) as n sequential steps would.
+static int prefill_batched(pbx_model *m, const int32_t *tokens, int n, int start) {
+  int rc = ensure_batch(m, n, false);
+  if (rc) return rc;
+  if (!m->ops_ready && (rc = build_ops(m))) return rc;
+  if ((rc = batch_layers(m, tokens, n, start))) return rc;
+  if ((rc = set_state(m, start + n - 1, tokens[n - 1], 0))) return rc;
+  if (hipMemcpyAsync(m->x, m->bx + (size_t)(n - 1) * m->cfg.dim, (size_t)m->cfg.dim * 4,
+                     hipMemcpyDeviceToDevice, m->c->stream) != hipSuccess)
+    return pbx_fail(m->c, PBX_EHIP, "model: residual copy failed");
+  const size_t k = m->ops.size();
+  if ((rc = enqueue_op(m, m->ops[k - 2]))) return rc;  // lm_head
+  return enqueue_op(m, m->ops[k - 1]);                 // argmax
+}
+
+static bool batched_prefill_enabled() {
+  const char *e = getenv("PBX_BATCHED_PREFILL");
+  return !(e && e[0] == '0');
+}
+
 extern "C" int pbx_model_forward(pbx_model *m, const int32_t *tokens, int n_tokens,
                                  int start_pos, float *logits, int32_t *next_token) {
   if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_forward: not a live model");
@@ -577,9 +738,13 @@ extern "C" int pbx_model_forward(pbx_model *m, const int32_t *tokens, int n_toke
   if (rc) return rc;
   if (hipSetDevice(c->device) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward: hipSetDevice failed");
-  for (int t = 0; t < n_tokens; ++t) {
-    if ((rc = set_state(m, start_pos + t, tokens[t], 0))) return rc;
-    if ((rc = run_step(m))) return rc;
+  if (n_tokens >= PBX_GEMM_MIN_M && batched_prefill_enabled()) {
+    if ((rc = prefill_batched(m, tokens, n_tokens, start_pos))) return rc;
+  } else {
+    for (int t = 0; t < n_tokens; ++t) {
+      if ((rc = set_state(m, start_pos + t, tokens[t], 0))) return rc;
+      if ((rc = run_step(m))) return rc;
+    }
   }
   if (logits && hipMemcpyAsync(logits, m->logits, (size_t)g.vocab_size * 4,
                                hipMemcpyDeviceToHost, c->stream) != hipSuccess)
@@ -589,6 +754,52 @@ extern "C" int pbx_model_forward(pbx_model *m, const int32_t *tokens, int n_toke
       hipStreamSynchronize(c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward: step failed on the device");
   if (next_token) *next_token = st[1];
+  return PBX_OK;
+}
+
+extern "C" int pbx_model_forward_batch(pbx_model *m, const int32_t *tokens, int n_tokens,
+                                       int start_pos, float *logits, int32_t *next_tokens) {
+  if (!model_ok(m))
+    return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_forward_batch: not a live model");
+  pbx_ctx *c = m->c;
+  const pbx_model_config &g = m->cfg;
+  if (!tokens || n_tokens <= 0)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_forward_batch: need at least one token");
+  if (n_tokens > 65535)
+    return pbx_fail(c, PBX_ENOTSUP, "pbx_model_forward_batch: %d rows exceed 65535", n_tokens);
+  if (start_pos < 0 || (int64_t)start_pos + n_tokens > g.max_seq)
+    return pbx_fail(c, PBX_EINVAL,
+                    "pbx_model_forward_batch: positions [%d, %lld) exceed max_seq %d", start_pos,
+                    (long long)start_pos + n_tokens, g.max_seq);
+  for (int t = 0; t < n_tokens; ++t)
+    if (tokens[t] < 0 || tokens[t] >= g.vocab_size)
+      return pbx_fail(c, PBX_EINVAL, "pbx_model_forward_batch: token %d out of range [0, %d)",
+                      tokens[t], g.vocab_size);
+  int rc = check_complete(m);
+  if (rc) return rc;
+  if (hipSetDevice(c->device) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_forward_batch: hipSetDevice failed");
+  const int n = n_tokens;
+  if ((rc = ensure_batch(m, n, true))) return rc;
+  if ((rc = batch_layers(m, tokens, n, start_pos))) return rc;
+  if ((rc = rmsnorm_rows(m, m->bx, m->out_norm, m->bxn, n))) return rc;
+  const pbx_weight *head = m->output ? m->output : m->embd;
+  if ((rc = linear_rows(m, head, m->bxn, n, m->blogits, false))) return rc;
+  {
+    const float *lg = m->blogits;
+    int vocab = g.vocab_size;
+    int *out = m->bnext;
+    void *args[] = {(void *)&lg, &vocab, &out};
+    if ((rc = launch_k(m, "pbx_argmax_rows", dim3(n), dim3(256), args))) return rc;
+  }
+  if (logits && hipMemcpyAsync(logits, m->blogits, (size_t)n * g.vocab_size * 4,
+                               hipMemcpyDeviceToHost, c->stream) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_forward_batch: logits copy failed");
+  if (next_tokens && hipMemcpyAsync(next_tokens, m->bnext, (size_t)n * 4, hipMemcpyDeviceToHost,
+                                    c->stream) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_forward_batch: token copy failed");
+  if (hipStreamSynchronize(c->stream) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_forward_batch: forward failed on the device");
   return PBX_OK;
 }
 
@@ -634,6 +845,33 @@ extern "C" int pbx_model_rollback(pbx_model *m, int pos) {
                     m->cfg.max_seq);
   return kv_fill(m, pos);
 }
+
+// Zeroes cache positions [from, to) of every layer: the part of
+// rollbackCache (llama-streaming.js:845-862) that a verify round can have
+// written, without touching the never-written tail.
+int pbx_model_clear_range(pbx_model *m, int from, int to) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "model: not a live model");
+  from = std::max(from, 0);
+  to = std::min(to, m->cfg.max_seq);
+  if (to <= from) return PBX_OK;
+  hipFunction_t f = pbx_kernel_by_name(m->c, "pbx_kv_fill");
+  if (!f) return pbx_fail(m->c, PBX_ELOAD, "model: kernel pbx_kv_fill not found");
+  int64_t stride = (int64_t)m->cfg.max_seq * m->kvdim;
+  int64_t off = (int64_t)from * m->kvdim;
+  int64_t count = (int64_t)(to - from) * m->kvdim;
+  int nl = m->cfg.n_layers;
+  float *k = m->kcache, *v = m->vcache;
+  void *args[] = {&k, &v, &stride, &off, &count, &nl};
+  const int64_t total = count * nl;
+  return pbx_launch_fn(m->c, f, "pbx_kv_fill", dim3((unsigned)((total + 255) / 256)), dim3(256),
+                       args, m->c->stream);
+}
+
+const pbx_model_config *pbx_model_cfg(const pbx_model *m) {
+  return model_ok(m) ? &m->cfg : nullptr;
+}
+
+pbx_ctx *pbx_model_ctx(const pbx_model *m) { return model_ok(m) ? m->c : nullptr; }
 
 extern "C" int pbx_model_info(const pbx_model *m, size_t *device_bytes, int *uses_graph) {
   if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_info: not a live model");

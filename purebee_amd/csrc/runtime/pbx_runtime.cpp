@@ -50,7 +50,8 @@ static const char *const kKernelNames[PBX_K_COUNT] = {
 
 // Code objects built from purebee_amd/csrc/kernels/*.hip, found next to this
 // library (or in the directory named by PBX_KERNEL_DIR).
-static const char *const kModuleFiles[] = {"pbx_gemv.hsaco", "pbx_decode.hsaco", "pbx_gemm.hsaco"};
+static const char *const kModuleFiles[] = {"pbx_gemv.hsaco", "pbx_decode.hsaco", "pbx_gemm.hsaco",
+                                          "pbx_prefill.hsaco"};
 static const int kModuleCount = (int)(sizeof kModuleFiles / sizeof kModuleFiles[0]);
 
 static std::string code_object_dir() {

@@ -28,8 +28,9 @@ EXPORTS = (
     "pbx_dev_alloc", "pbx_dev_free", "pbx_memcpy_h2d", "pbx_memcpy_d2h", "pbx_memset_dev",
     "pbx_dev_copy", "pbx_sync", "pbx_timer_start", "pbx_timer_stop", "pbx_bench_linear",
     "pbx_model_create", "pbx_model_free", "pbx_model_set_tensor", "pbx_model_forward",
-    "pbx_model_generate", "pbx_model_reset_cache", "pbx_model_rollback", "pbx_model_info",
+    "pbx_model_forward_batch", "pbx_model_generate", "pbx_model_reset_cache", "pbx_model_rollback", "pbx_model_info",
     "pbx_model_profile", "pbx_model_op_name", "pbx_model_bench_role",
+    "pbx_speculative_generate",
 )
 
 # Tensor ids of pbx_model_set_tensor (GGUF tensor names, gguf.js:378-410).
@@ -43,6 +44,12 @@ class ModelConfig(ctypes.Structure):
         "dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab_size",
         "max_seq", "weight_type", "embed_type", "output_type")] + \
         [("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_double)]
+
+
+class SpecStats(ctypes.Structure):
+    _fields_ = [("rounds", ctypes.c_int32), ("drafted", ctypes.c_int32),
+                ("accepted", ctypes.c_int32), ("prefill_ms", ctypes.c_double),
+                ("decode_ms", ctypes.c_double)]
 
 
 class PbxError(RuntimeError):
@@ -111,6 +118,7 @@ def load_library():
         "pbx_model_free": (ctypes.c_int, [_vp]),
         "pbx_model_set_tensor": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t]),
         "pbx_model_forward": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+        "pbx_model_forward_batch": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
         "pbx_model_generate": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int, ctypes.c_int, _vp, _vp]),
         "pbx_model_reset_cache": (ctypes.c_int, [_vp]),
         "pbx_model_rollback": (ctypes.c_int, [_vp, ctypes.c_int]),
@@ -123,6 +131,10 @@ def load_library():
                                                 ctypes.POINTER(ctypes.c_double),
                                                 ctypes.POINTER(ctypes.c_double),
                                                 ctypes.POINTER(ctypes.c_int)]),
+        "pbx_speculative_generate": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int,
+                                                    ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int,
+                                                    _vp, ctypes.POINTER(ctypes.c_int),
+                                                    ctypes.POINTER(SpecStats)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -342,6 +354,15 @@ class Model:
                     None if logits is None else logits.ctypes.data, ctypes.byref(nxt))
         return logits, nxt.value
 
+    def forward_batch(self, tokens, start_pos, want_logits=True):
+        """One batched forward over all tokens: (logits [n, vocab] or None, argmax [n])."""
+        toks = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty((len(toks), self.vocab), np.float32) if want_logits else None
+        nxt = np.empty(len(toks), np.int32)
+        self._mcall("pbx_model_forward_batch", toks.ctypes.data, len(toks), start_pos,
+                    None if logits is None else logits.ctypes.data, nxt.ctypes.data)
+        return logits, nxt
+
     def generate(self, token, start_pos, n_steps, want_logits=False):
         out = np.empty(n_steps, np.int32)
         logits = np.empty(self.vocab, np.float32) if want_logits else None
@@ -387,3 +408,24 @@ class Model:
         if self._m:
             self._mcall("pbx_model_free")
             self._m = None
+
+
+def speculative_generate(target, draft, prompt, max_tokens, draft_count=4, eos_ids=(2,),
+                         batched_verify=True):
+    """Greedy speculative decoding (speculative.js:58-204) with `draft` proposing
+    and `target` verifying.  Returns (generated tokens, stats dict)."""
+    ctx = target.ctx
+    p = np.ascontiguousarray(prompt, np.int32)
+    eos = np.ascontiguousarray(list(eos_ids), np.int32)
+    out = np.empty(max_tokens + 1, np.int32)
+    n = ctypes.c_int()
+    st = SpecStats()
+    rc = ctx.L.pbx_speculative_generate(target._m, draft._m, p.ctypes.data, len(p), max_tokens,
+                                        draft_count, eos.ctypes.data if len(eos) else None,
+                                        len(eos), 1 if batched_verify else 0, out.ctypes.data,
+                                        ctypes.byref(n), ctypes.byref(st))
+    if rc != 0:
+        msg = ctx.L.pbx_last_error(ctx._p)
+        raise PbxError(rc, msg.decode() if msg else "")
+    stats = {k: getattr(st, k) for k, _ in SpecStats._fields_}
+    return out[:n.value].copy(), stats

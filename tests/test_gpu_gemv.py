@@ -190,9 +190,12 @@ GEMM_SHAPES = [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192), (576, 576)
 @pytest.mark.parametrize("M", [4, 5, 17, 64, 130])
 @pytest.mark.parametrize("N,K", GEMM_SHAPES)
 def test_mfma_gemm_parity(ctx, t, M, N, K):
-    """M >= 4 takes the MFMA path (fp16 operands, fp32 accumulation): every
-    row within 1e-3 relative L2 of the oracle's double-accumulated matvec."""
+    """M >= 4 takes the MFMA path (exact integer weight codes, activations as
+    an fp16 pair hi + lo, fp32 accumulation): every row within 1e-5 relative
+    L2 of the oracle's double-accumulated matvec and of the M=1 GEMV (the
+    matvec bar is 1e-3; single-fp16 activations would sit near 2e-4)."""
     print(f"[case] gemm type={t} M={M} N={N} K={K}", flush=True)
+    tol = 1e-5
     raw = quantize(t, synth_matrix(11 * N + K + M, N, K))
     X = pb.synth_normal(M * 7 + K, M * K).reshape(M, K)
     X[1] *= 1e-3   # rows of very different magnitude: per-row scaling
@@ -202,12 +205,15 @@ def test_mfma_gemm_parity(ctx, t, M, N, K):
     Y = ctx.linear(w, X, bias)
     assert Y.shape == (M, N)
     rows = range(M) if M <= 17 else [0, 1, 2, M // 2, M - 1]
+    worst = 0.0
     for m in rows:
         ref = oracle.matvec(t, X[m], raw, N, K) + bias
-        assert rel_l2(Y[m], ref) <= TOL, (m, rel_l2(Y[m], ref))
+        worst = max(worst, rel_l2(Y[m], ref))
+    print(f"  worst rel L2 vs oracle {worst:.2e}")
+    assert worst <= tol
     # every row against the M=1 GEMV (fp32 path)
     for m in range(M):
-        assert rel_l2(Y[m], ctx.linear(w, X[m]) + bias) <= TOL
+        assert rel_l2(Y[m], ctx.linear(w, X[m]) + bias) <= tol
     w.free()
 
 

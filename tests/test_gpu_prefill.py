@@ -1,0 +1,260 @@
+"""The M > 1 path: batched prefill and speculative verify through the MFMA
+GEMM (llama.js:204-371 with seqLen > 1; speculative.js:58-204).
+
+Bars:
+* batched prefill logits within 2e-3 max-abs of the oracle's forward;
+* every row of a batched forward within 2e-3 of the same position's
+  single-token (decode-step) forward, with the same argmax unless the two
+  top logits are closer than that tolerance;
+* speculative decoding emits exactly the target's greedy tokens, and the
+  batched verify (one forward of drafts + 1 rows) takes exactly the accept /
+  reject decisions of the reference's one-forward-per-draft verify.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from purebee_amd import PbxError, synth
+from purebee_amd.native import TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, speculative_generate
+from tests.e2e_util import LOGIT_TOL, make_pair
+
+pytestmark = pytest.mark.gpu
+
+
+def tiny(weight_type, embed_type, **kw):
+    cfg = dict(dim=256, hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=1000,
+               max_seq=128, weight_type=weight_type, embed_type=embed_type, rope_theta=10000.0)
+    cfg.update(kw)
+    return cfg
+
+
+def top_gap(logits, a, b):
+    return abs(float(logits[a]) - float(logits[b]))
+
+
+@pytest.mark.parametrize("wt,et", [(TYPE_Q4_0, TYPE_Q4_0), (TYPE_Q8_0, TYPE_Q8_0),
+                                   (TYPE_Q8_0, TYPE_F32), (TYPE_F32, TYPE_F32)])
+def test_batched_rows_match_oracle_positions(ctx, wt, et):
+    """forward_batch row t == the oracle's logits at position start + t."""
+    print(f"[case] forward_batch rows vs oracle weights={wt} embed={et}", flush=True)
+    model, ref, cfg = make_pair(ctx, tiny(wt, et), 300 + wt)
+    prompt = [int(t) for t in synth.random_tokens(301, 6, cfg["vocab_size"])]
+    model.forward(prompt, 0)
+    ref.forward(prompt, 0)
+    rows = [int(t) for t in synth.random_tokens(302, 9, cfg["vocab_size"])]
+    logits, nxt = model.forward_batch(rows, len(prompt))
+    worst = 0.0
+    for t, tok in enumerate(rows):
+        r = ref.forward([tok], len(prompt) + t)
+        worst = max(worst, float(np.abs(logits[t] - r).max()))
+        assert nxt[t] == int(np.argmax(logits[t]))
+        best = oracle.argmax(r)
+        if nxt[t] != best:
+            assert top_gap(r, best, nxt[t]) < LOGIT_TOL
+    print(f"  worst max-abs {worst:.2e}")
+    assert worst <= LOGIT_TOL
+    model.free()
+    ref.close()
+
+
+@pytest.mark.parametrize("n", [4, 5, 31, 64])
+def test_batched_prefill_vs_oracle(ctx, n):
+    print(f"[case] batched prefill n={n}", flush=True)
+    model, ref, cfg = make_pair(ctx, tiny(TYPE_Q4_0, TYPE_Q4_0, n_layers=3), 310 + n)
+    prompt = [int(t) for t in synth.random_tokens(311, n, cfg["vocab_size"])]
+    g, nxt = model.forward(prompt, 0)
+    r = ref.forward(prompt, 0)
+    err = float(np.abs(g - r).max())
+    print(f"  max-abs {err:.2e}")
+    assert err <= LOGIT_TOL
+    assert nxt == int(np.argmax(g))
+    # the state left by the batched prefill continues like a decode: the
+    # next greedy step sees all n cached positions
+    toks = model.generate(nxt, n, 3)
+    r2 = ref.forward([nxt], n)
+    best = oracle.argmax(r2)
+    assert toks[0] == best or top_gap(r2, best, toks[0]) < LOGIT_TOL
+    model.free()
+    ref.close()
+
+
+def test_prefill_gqa_untied_head(ctx):
+    print("[case] batched prefill, GQA 6/2, untied Q8_0 head, head_dim 48", flush=True)
+    cfg = tiny(TYPE_Q8_0, TYPE_F32, dim=288, hidden_dim=768, n_heads=6, n_kv_heads=2,
+               output_type=TYPE_Q8_0)
+    model, ref, cfg = make_pair(ctx, cfg, 320)
+    prompt = [int(t) for t in synth.random_tokens(321, 17, cfg["vocab_size"])]
+    g, _ = model.forward(prompt, 0)
+    r = ref.forward(prompt, 0)
+    assert float(np.abs(g - r).max()) <= LOGIT_TOL
+    # continue with a second batched chunk at a non-zero start position
+    more = [int(t) for t in synth.random_tokens(322, 8, cfg["vocab_size"])]
+    g2, _ = model.forward(more, 17)
+    r2 = ref.forward(more, 17)
+    assert float(np.abs(g2 - r2).max()) <= LOGIT_TOL
+    model.free()
+    ref.close()
+
+
+def _sequential_logits(model, tokens, start):
+    out = []
+    for i, t in enumerate(tokens):
+        lg, _ = model.forward([int(t)], start + i)
+        out.append(lg)
+    return np.stack(out)
+
+
+def test_llama1b_verify_rows_equal_sequential(ctx):
+    """Verify invariant of the M>1 config: one M=5 forward == 5 single-token
+    forwards (the reference's verify loop, speculative.js:131-137), on the
+    Llama-3.2-1B-shaped Q4_0 model after a 128-token prompt."""
+    print("[case] llama32_1b M=5 verify vs sequential", flush=True)
+    model = synth.build(ctx, "llama32_1b", 3000)
+    vocab = synth.CONFIGS["llama32_1b"]["vocab_size"]
+    prompt = [int(t) for t in synth.random_tokens(3001, 128, vocab)]
+    rows = [int(t) for t in synth.random_tokens(3002, 5, vocab)]
+    worst, flips = 0.0, 0
+    for rep in range(3):
+        model.reset_cache()
+        model.forward(prompt, 0)
+        start = 128 + 5 * rep
+        if rep:
+            model.forward(synth.random_tokens(3003 + rep, 5 * rep, vocab), 128)
+        lb, nb = model.forward_batch(rows, start)
+        ls = _sequential_logits(model, rows, start)
+        worst = max(worst, float(np.abs(lb - ls).max()))
+        for t in range(5):
+            s = int(np.argmax(ls[t]))
+            if nb[t] != s:
+                flips += 1
+                assert top_gap(ls[t], s, nb[t]) < LOGIT_TOL
+    print(f"  worst max-abs {worst:.2e} argmax near-tie flips {flips}")
+    assert worst <= LOGIT_TOL
+    model.free()
+
+
+def test_llama1b_prefill_512_equals_sequential(ctx):
+    """Batched prefill of a 512-token prompt (M = 512 through the MFMA GEMM)
+    against the same prompt fed one decode step at a time."""
+    print("[case] llama32_1b prefill 512 batched vs sequential", flush=True)
+    model = synth.build(ctx, "llama32_1b", 3100)
+    vocab = synth.CONFIGS["llama32_1b"]["vocab_size"]
+    prompt = [int(t) for t in synth.random_tokens(3101, 512, vocab)]
+    lb, nb = model.forward(prompt, 0)
+    follow_b = model.generate(nb, 512, 8)
+    model.reset_cache()
+    ls = None
+    for i, t in enumerate(prompt):
+        ls, ns = model.forward([t], i)
+    err = float(np.abs(lb - ls).max())
+    print(f"  last-position max-abs {err:.2e}, argmax {nb} vs {ns}")
+    assert err <= LOGIT_TOL
+    assert nb == ns or top_gap(ls, ns, nb) < LOGIT_TOL
+    # the decode that followed the batched prefill is a greedy walk over the
+    # sequentially written cache too (teacher forcing on its own tokens)
+    tok, pos = nb, 512
+    for g in follow_b:
+        L, best = model.forward([int(tok)], pos)
+        assert g == best or top_gap(L, best, g) < LOGIT_TOL
+        tok, pos = int(g), pos + 1
+    model.free()
+
+
+def _greedy(model, prompt, n_gen):
+    model.reset_cache()
+    _, nxt = model.forward(prompt, 0)
+    rest = model.generate(nxt, len(prompt), n_gen - 1)
+    return [nxt] + [int(t) for t in rest]
+
+
+@pytest.mark.parametrize("draft_kind", ["other", "same"])
+def test_speculative_equals_greedy(ctx, draft_kind):
+    """Greedy speculative decoding emits the target's own greedy tokens,
+    whatever the draft proposes; the batched verify and the reference's
+    one-by-one verify take the same decisions."""
+    print(f"[case] speculative draft={draft_kind}", flush=True)
+    tcfg = tiny(TYPE_Q4_0, TYPE_Q4_0, n_layers=3, max_seq=200)
+    target = synth.build(ctx, tcfg, 400)
+    if draft_kind == "same":
+        draft = synth.build(ctx, tcfg, 400)  # identical weights: every draft agrees
+    else:
+        draft = synth.build(ctx, tiny(TYPE_Q8_0, TYPE_F32, dim=128, hidden_dim=256,
+                                      n_heads=2, n_kv_heads=2, vocab_size=700, max_seq=200), 401)
+    prompt = [int(t) for t in synth.random_tokens(402, 16, tcfg["vocab_size"])]
+    n_gen = 48
+    ref = _greedy(target, prompt, n_gen)
+    out_b, st_b = speculative_generate(target, draft, prompt, n_gen, 4, eos_ids=(),
+                                       batched_verify=True)
+    out_s, st_s = speculative_generate(target, draft, prompt, n_gen, 4, eos_ids=(),
+                                       batched_verify=False)
+    print(f"  batched {st_b}\n  sequential {st_s}")
+    assert list(out_s[:n_gen]) == ref
+    assert list(out_b) == list(out_s)
+    assert (st_b["rounds"], st_b["drafted"], st_b["accepted"]) == \
+           (st_s["rounds"], st_s["drafted"], st_s["accepted"])
+    assert len(out_b) in (n_gen, n_gen + 1)
+    if draft_kind == "same":
+        assert st_b["accepted"] == st_b["drafted"]
+    target.free()
+    draft.free()
+
+
+def test_speculative_eos_and_budget(ctx):
+    """EOS stops decoding at the first emitted EOS (speculative.js:148-166);
+    max_tokens bounds the drafts (speculative.js:94)."""
+    print("[case] speculative eos/budget", flush=True)
+    tcfg = tiny(TYPE_Q8_0, TYPE_Q8_0, max_seq=128)
+    target = synth.build(ctx, tcfg, 410)
+    draft = synth.build(ctx, tcfg, 410)
+    prompt = [int(t) for t in synth.random_tokens(411, 8, tcfg["vocab_size"])]
+    ref = _greedy(target, prompt, 20)
+    eos = ref[9]
+    stop = ref.index(eos)
+    for batched in (True, False):
+        out, _ = speculative_generate(target, draft, prompt, 20, 4, eos_ids=(eos,),
+                                      batched_verify=batched)
+        assert list(out) == ref[:stop + 1]
+    out, _ = speculative_generate(target, draft, prompt, 3, 4, eos_ids=())
+    assert list(out[:3]) == ref[:3] and len(out) <= 4
+    target.free()
+    draft.free()
+
+
+def test_speculative_config_shapes(ctx):
+    """The M>1 config: Llama-3.2-1B-shaped Q4_0 target, stories15M-shaped
+    draft (vocabulary 32000: target tokens enter the draft modulo 32000),
+    draft_count 4, verify M = 5."""
+    print("[case] speculative llama32_1b target, stories15m draft", flush=True)
+    target = synth.build(ctx, "llama32_1b", 3200)
+    draft = synth.build(ctx, "stories15m", 3201)
+    vocab = synth.CONFIGS["llama32_1b"]["vocab_size"]
+    prompt = [int(t) for t in synth.random_tokens(3202, 32, vocab)]
+    n_gen = 24
+    ref = _greedy(target, prompt, n_gen)
+    out_b, st_b = speculative_generate(target, draft, prompt, n_gen, 4, eos_ids=())
+    out_s, st_s = speculative_generate(target, draft, prompt, n_gen, 4, eos_ids=(),
+                                       batched_verify=False)
+    print(f"  batched {st_b}\n  sequential {st_s}")
+    assert list(out_s[:n_gen]) == ref
+    assert list(out_b) == list(out_s)
+    target.free()
+    draft.free()
+
+
+def test_speculative_errors(ctx):
+    print("[case] speculative errors", flush=True)
+    cfg = tiny(TYPE_Q4_0, TYPE_Q4_0, max_seq=64)
+    a = synth.build(ctx, cfg, 420)
+    b = synth.build(ctx, cfg, 421)
+    with pytest.raises(PbxError):
+        speculative_generate(a, a, [1, 2, 3], 4)            # shared cache
+    with pytest.raises(PbxError):
+        speculative_generate(a, b, [1, 2, 3], 4, draft_count=0)
+    with pytest.raises(PbxError):
+        speculative_generate(a, b, [1, 2, 3], 60)           # beyond max_seq
+    with pytest.raises(PbxError):
+        a.forward_batch([1, cfg["vocab_size"]], 0)
+    with pytest.raises(PbxError):
+        a.forward_batch([1, 2], cfg["max_seq"] - 1)
+    a.free()
+    b.free()
