@@ -179,7 +179,7 @@ def run_decode(args, pb, synth):
     t0 = time.perf_counter()
     _, nxt = model.forward(prompt, 0, want_logits=False)
     prefill_s = time.perf_counter() - t0
-    log(f"prefill {PROMPT} tokens (token-by-token decode steps): {prefill_s * 1e3:.1f} ms")
+    log(f"prefill {PROMPT} tokens (one batched forward): {prefill_s * 1e3:.1f} ms")
 
     model.generate(nxt, PROMPT, args.warmup)
     model.rollback(PROMPT)
@@ -226,6 +226,7 @@ def run_decode(args, pb, synth):
                 "bytes_per_launch": round(by), "us_per_launch": round(us, 3),
                 "us_per_launch_in_step": round(dom["us_per_launch"], 3)}
     step_bytes = sum(r["bytes_per_step"] for r in roles.values())
+    m_gt_1 = None if args.no_m_gt_1 else run_m_gt_1(ctx, model, cfg, pb, synth)
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the restated reference CPU path ...")
@@ -257,11 +258,91 @@ def run_decode(args, pb, synth):
         "roofline": roofline,
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in roles.items()},
+        "m_gt_1": m_gt_1,
         "cpu_baseline": cpu,
     }
     model.free()
     ctx.close()
     return out
+
+
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA, vendor figure
+
+
+def run_m_gt_1(ctx, model, cfg, pb, synth):
+    """The M>1 path on the same model: a 512-token batched prefill, the MFMA
+    GEMM alone at the prefill shape, and speculative decoding with M=5
+    verifies (4 drafts from a stories15M-shaped Q8_0 model + 1)."""
+    d, h, V = cfg["dim"], cfg["hidden_dim"], cfg["vocab_size"]
+    res = {}
+    prompt = synth.random_tokens(11, 512, V)
+    times = []
+    for _ in range(3):
+        model.reset_cache()
+        ctx.sync()
+        t0 = time.perf_counter()
+        model.forward(prompt, 0, want_logits=False)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    # useful FLOPs of a prefill: 2 * params per token for the layer matrices,
+    # the LM head on the last row only, attention 4 * hd per (query, key) pair
+    L, kvd = cfg["n_layers"], cfg["n_kv_heads"] * (d // cfg["n_heads"])
+    layer_params = L * (d * (d + 2 * kvd) + d * d + 2 * h * d + d * h)
+    flops = 2.0 * 512 * layer_params + 2.0 * V * d + L * cfg["n_heads"] * 4 * (d // cfg["n_heads"]) * 512 * 513 / 2
+    res["prefill"] = {"tokens": 512, "ms": round(t * 1e3, 3), "tok_per_s": round(512 / t, 1),
+                      "useful_TFLOPs": round(flops / t / 1e12, 2)}
+    log(f"prefill 512 tokens (batched, MFMA): {t * 1e3:.2f} ms, {512 / t:.0f} tok/s, "
+        f"{flops / t / 1e12:.1f} TFLOP/s useful")
+    # the GEMM alone: gate|up (16384 x 2048, Q4_0) at M = 512, prep + MFMA
+    N, K, M = 2 * h, d, 512
+    raw = pb.quantize_q4_0(pb.synth_normal(77, N * K, 0, 0.02).reshape(N, K))
+    w = ctx.upload(pb.TYPE_Q4_0, N, K, raw)
+    dx = ctx.alloc(M * K * 4).upload(np.random.default_rng(5).normal(0, 1, M * K).astype(np.float32))
+    dy = ctx.alloc(M * N * 4)
+    ctx.bench_linear([w], [dx.ptr], [dy.ptr], M, 3)
+    reps = 20
+    ms = ctx.bench_linear([w], [dx.ptr], [dy.ptr], M, reps) / reps
+    tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    res["gemm"] = {"shape": f"M={M} N={N} K={K} q4_0 (gate|up)", "kernel": "pbx_gemm_q4_m4_n4",
+                   "us_per_launch": round(ms * 1e3, 2), "achieved": round(tf, 2),
+                   "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                   "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                   "note": "useful 2*M*N*K; the kernel issues two fp16 MFMAs (activation hi + lo) "
+                           "per useful product"}
+    log(f"gemm {res['gemm']['shape']}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s useful "
+        f"({100 * tf / MFMA_F16_PEAK_TFLOPS:.1f}% of {MFMA_F16_PEAK_TFLOPS:.0f})")
+    w.free(), dx.free(), dy.free()
+    # verify: M = 5 forward after a 128-token prompt, then speculative decoding
+    draft = synth.build(ctx, "stories15m", seed=2000)
+    vp = synth.random_tokens(12, PROMPT, V)
+    model.reset_cache()
+    model.forward(vp, 0, want_logits=False)
+    rows = synth.random_tokens(13, 5, V)
+    model.forward_batch(rows, PROMPT, want_logits=False)
+    ctx.sync()
+    n_ver = 64
+    t0 = time.perf_counter()
+    for i in range(n_ver):
+        model.forward_batch(rows, PROMPT, want_logits=False)
+    tv = (time.perf_counter() - t0) / n_ver
+    wbytes = model.info()["device_bytes"]  # resident weights + caches: an upper bound
+    step_bytes = sum(q4_bytes(*s[2:4]) for s in synth.tensor_specs(cfg) if s[4] == pb.TYPE_Q4_0)
+    res["verify"] = {"M": 5, "ms": round(tv * 1e3, 3),
+                     "weight_GBps": round(step_bytes / tv / 1e9, 1),
+                     "frac_hbm": round(step_bytes / tv / 1e9 / HBM_PEAK_GBS, 4),
+                     "weight_bytes": step_bytes, "resident_bytes": wbytes}
+    log(f"verify M=5: {tv * 1e3:.3f} ms per forward, {step_bytes / tv / 1e9:.0f} GB/s of weights")
+    out, st = pb.speculative_generate(model, draft, vp, 64, 4, eos_ids=())
+    res["speculative"] = {"draft": "stories15m-shaped q8_0 (vocab 32000)", "draft_count": 4,
+                          "tokens": int(len(out)), "rounds": st["rounds"],
+                          "accepted": st["accepted"], "drafted": st["drafted"],
+                          "decode_ms": round(st["decode_ms"], 2),
+                          "tok_per_s": round((len(out) - 1) / (st["decode_ms"] / 1e3), 1)}
+    log(f"speculative: {len(out)} tokens in {st['rounds']} rounds, accepted {st['accepted']}/"
+        f"{st['drafted']}, {res['speculative']['tok_per_s']} tok/s")
+    draft.free()
+    model.reset_cache()
+    return res
 
 
 def run_pmc_probe(args, pb, synth):
@@ -337,6 +418,8 @@ def main():
     ap.add_argument("--workload", choices=("decode", "matvec", "pmc-probe"), default="decode")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-m-gt-1", action="store_true",
+                    help="skip the prefill / verify / speculative measurements")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write profiles/traffic_decode.json from two rocprofv3 --pmc runs")
     args = ap.parse_args()

@@ -10,4 +10,5 @@ from .native import (  # noqa: F401
     PbxError, Context, Weight, Model, ModelConfig, load_library, library_path,
     TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, TYPE_Q8_REF,
     quantize_q4_0, quantize_q8_0, quantize_q8_ref, synth_normal, block_bytes,
+    speculative_generate,
 )

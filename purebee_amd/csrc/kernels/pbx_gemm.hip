@@ -56,42 +56,52 @@ __device__ __forceinline__ half2v codes_to_half2(unsigned v, _Float16 bias) {
   return __builtin_bit_cast(half2v, p) - half2v{bias, bias};
 }
 
-// Lane group g's 8 integer weight codes of row n, block b, and the block
-// scale (0 for padding rows).
+// Raw bytes of lane group g's 8 weight codes of row n, block b (8 bytes of
+// the row's block) and the block's scale bits; zero for padding rows.
 template <int TYPE>
-__device__ __forceinline__ half8 weight_codes(const GemmArgs &a, int n, int b, int g, float *d) {
-  half8 v;
+__device__ __forceinline__ void load_codes(const GemmArgs &a, int n, int b, int g, uint2 *raw,
+                                           unsigned *dbits) {
   if (n >= a.Npad) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = (_Float16)0.f;
-    *d = 0.f;
-    return v;
+    *raw = make_uint2(0u, 0u);
+    *dbits = 0u;
+    return;
   }
-  *d = f16_bits_to_f32(a.dsc[dsc_index(n, b, a.B)]);
+  *dbits = a.dsc[dsc_index(n, b, a.B)];
+  if constexpr (TYPE == PBX_Q4)
+    *raw = *reinterpret_cast<const uint2 *>(a.qs + ((size_t)n * a.B + b) * 16 + (g & 1) * 8);
+  else
+    *raw = *reinterpret_cast<const uint2 *>(a.qs + ((size_t)n * a.B + b) * 32 + g * 8);
+}
+
+// The 8 integer codes as an fp16 MFMA operand: q - 8 (Q4_0, low nibbles for
+// g < 2, high for g >= 2) or q (Q8_0).
+template <int TYPE>
+__device__ __forceinline__ half8 codes_operand(uint2 w, int g) {
   unsigned x, y;
   _Float16 bias;
   if constexpr (TYPE == PBX_Q4) {
-    const uint2 w = *reinterpret_cast<const uint2 *>(a.qs + ((size_t)n * a.B + b) * 16 + (g & 1) * 8);
-    const unsigned sh = (g >> 1) * 4;  // low nibbles for g < 2, high for g >= 2
+    const unsigned sh = (g >> 1) * 4;
     x = (w.x >> sh) & 0x0F0F0F0Fu;
     y = (w.y >> sh) & 0x0F0F0F0Fu;
     bias = (_Float16)1032.f;  // 1024 + 8
   } else {
-    const uint2 w = *reinterpret_cast<const uint2 *>(a.qs + ((size_t)n * a.B + b) * 32 + g * 8);
     x = w.x ^ 0x80808080u;  // int8 q -> q + 128
     y = w.y ^ 0x80808080u;
     bias = (_Float16)1152.f;  // 1024 + 128
   }
   const half2v p0 = codes_to_half2(x, bias), p1 = codes_to_half2(x >> 16, bias);
   const half2v p2 = codes_to_half2(y, bias), p3 = codes_to_half2(y >> 16, bias);
+  half8 v;
   v[0] = p0[0]; v[1] = p0[1]; v[2] = p1[0]; v[3] = p1[1];
   v[4] = p2[0]; v[5] = p2[1]; v[6] = p3[0]; v[7] = p3[1];
   return v;
 }
 
 // Workgroup = 4 waves side by side along n.  Wave tile: 16*MT rows of X by
-// 16*NT rows of W; blockIdx.z splits the K blocks.
-template <int TYPE, int MT, int NT>
+// 16*NT rows of W; blockIdx.z splits the K blocks.  The block loop runs in
+// steps of U blocks whose loads are all issued before the first MFMA, so a
+// wave keeps U blocks of weights in flight.
+template <int TYPE, int MT, int NT, int U>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 15, g = lane >> 4;
@@ -109,26 +119,41 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a) {
 #pragma unroll
     for (int u = 0; u < NT; ++u) acc[t][u] = zero;
 
-  for (int b = b0; b < b1; ++b) {
-    half8 A[MT], Alo[MT], W[NT];
-    float d[NT];
+  for (int b = b0; b < b1; b += U) {
+    uint2 raw[U][NT];
+    unsigned dbits[U][NT];
+    half8 A[U][MT], Alo[U][MT];
 #pragma unroll
-    for (int u = 0; u < NT; ++u) W[u] = weight_codes<TYPE>(a, n0 + 16 * u + li, b, g, &d[u]);
+    for (int j = 0; j < U; ++j) {
+      const int bb = b + j;
+      if (bb < b1) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const size_t off = (size_t)(m0 + 16 * t + li) * K + b * 32 + 8 * g;
-      A[t] = *reinterpret_cast<const half8 *>(a.X16 + off);
-      Alo[t] = *reinterpret_cast<const half8 *>(a.X16lo + off);
+        for (int u = 0; u < NT; ++u) load_codes<TYPE>(a, n0 + 16 * u + li, bb, g, &raw[j][u], &dbits[j][u]);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const size_t off = (size_t)(m0 + 16 * t + li) * K + bb * 32 + 8 * g;
+          A[j][t] = *reinterpret_cast<const half8 *>(a.X16 + off);
+          Alo[j][t] = *reinterpret_cast<const half8 *>(a.X16lo + off);
+        }
+      }
     }
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+    for (int j = 0; j < U; ++j) {
+      if (b + j < b1) {
 #pragma unroll
-      for (int u = 0; u < NT; ++u) {
-        floatx4 blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t], W[u], zero, 0, 0, 0);
-        blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(Alo[t], W[u], blk, 0, 0, 0);
+        for (int u = 0; u < NT; ++u) {
+          const half8 W = codes_operand<TYPE>(raw[j][u], g);
+          const float d = f16_bits_to_f32(dbits[j][u]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][u][r] = fmaf(blk[r], d[u], acc[t][u][r]);
+          for (int t = 0; t < MT; ++t) {
+            floatx4 blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[j][t], W, zero, 0, 0, 0);
+            blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(Alo[j][t], W, blk, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[t][u][r] = fmaf(blk[r], d, acc[t][u][r]);
+          }
+        }
       }
+    }
   }
 
 #pragma unroll
@@ -159,7 +184,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a) {
 
 #define GEMM_KERNEL(NAME, TYPE, MT, NT)                                            \
   extern "C" __global__ void __launch_bounds__(256) NAME(GemmArgs a) {             \
-    gemm_tile<TYPE, MT, NT>(a);                                                    \
+    gemm_tile<TYPE, MT, NT, (MT == 1 ? 8 : 2)>(a);                                  \
   }
 GEMM_KERNEL(pbx_gemm_q4_m1_n1, PBX_Q4, 1, 1)
 GEMM_KERNEL(pbx_gemm_q4_m1_n2, PBX_Q4, 1, 2)

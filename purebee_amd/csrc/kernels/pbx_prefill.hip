@@ -181,13 +181,17 @@ pbx_add_inplace(float *y, const float *x, int64_t n) {
 }
 
 // Argmax of each row of logits [M][vocab] (first maximum wins,
-// llama.js:432-442).  One workgroup per row.
+// llama.js:432-442), in two passes so a row is scanned by many workgroups:
+// workgroup (p, row) reduces columns [p*chunk, (p+1)*chunk) to one key,
+// then one wave per row reduces the P keys.
 extern "C" __global__ void __launch_bounds__(256)
-pbx_argmax_rows(const float *logits, int vocab, int *out) {
+pbx_argmax_rows_partial(const float *logits, int vocab, int chunk, uint64_t *keys, int P) {
   __shared__ uint64_t red[4];
-  const float *r = logits + (size_t)blockIdx.x * vocab;
+  const int row = blockIdx.y, p = blockIdx.x;
+  const float *r = logits + (size_t)row * vocab;
+  const int lo = p * chunk, hi = min(vocab, lo + chunk);
   uint64_t best = 0;
-  for (int i = threadIdx.x; i < vocab; i += blockDim.x) {
+  for (int i = lo + threadIdx.x; i < hi; i += blockDim.x) {
     const uint64_t k = argmax_key(r[i], (unsigned)i);
     best = k > best ? k : best;
   }
@@ -197,6 +201,16 @@ pbx_argmax_rows(const float *logits, int vocab, int *out) {
   if (threadIdx.x == 0) {
     for (int w = 1; w < 4; ++w) best = red[w] > best ? red[w] : best;
     best = red[0] > best ? red[0] : best;
-    out[blockIdx.x] = best ? (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFu)) : 0;
+    keys[(size_t)row * P + p] = best;
   }
+}
+
+extern "C" __global__ void __launch_bounds__(64)
+pbx_argmax_rows_final(const uint64_t *keys, int P, int *out) {
+  const uint64_t *k = keys + (size_t)blockIdx.x * P;
+  uint64_t best = 0;
+  for (int i = threadIdx.x; i < P; i += 64) best = k[i] > best ? k[i] : best;
+  best = wave_max_u64(best);
+  if (threadIdx.x == 0)
+    out[blockIdx.x] = best ? (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFu)) : 0;
 }

@@ -120,6 +120,7 @@ struct pbx_model {
   float *bx = nullptr, *bxn = nullptr, *bqkv = nullptr, *battn = nullptr, *bgu = nullptr,
         *bh = nullptr, *btmp = nullptr, *blogits = nullptr;
   int *btok = nullptr, *bnext = nullptr;
+  uint64_t *bkeys = nullptr;  // [logits_cap][64] partial argmax keys
 };
 
 static bool model_ok(const pbx_model *m) { return m && m->magic == PBX_MODEL_MAGIC; }
@@ -366,7 +367,7 @@ static void model_release(pbx_model *m) {
     if (p) hipFree(p);
   for (void *p : {(void *)m->bx, (void *)m->bxn, (void *)m->bqkv, (void *)m->battn,
                   (void *)m->bgu, (void *)m->bh, (void *)m->btmp, (void *)m->blogits,
-                  (void *)m->btok, (void *)m->bnext})
+                  (void *)m->btok, (void *)m->bnext, (void *)m->bkeys})
     if (p) hipFree(p);
   m->magic = 0;
   delete m;
@@ -613,7 +614,8 @@ static int ensure_batch(pbx_model *m, int rows, bool all_logits) {
     m->batch_cap = rows;
   }
   if (all_logits && rows > m->logits_cap) {
-    if ((rc = grow(m, (void **)&m->blogits, (size_t)rows * g.vocab_size * 4))) {
+    if ((rc = grow(m, (void **)&m->blogits, (size_t)rows * g.vocab_size * 4)) ||
+        (rc = grow(m, (void **)&m->bkeys, (size_t)rows * 64 * 8))) {
       m->logits_cap = 0;
       return rc;
     }
@@ -786,11 +788,17 @@ extern "C" int pbx_model_forward_batch(pbx_model *m, const int32_t *tokens, int 
   const pbx_weight *head = m->output ? m->output : m->embd;
   if ((rc = linear_rows(m, head, m->bxn, n, m->blogits, false))) return rc;
   {
+    // P partial keys per row (<= 64, the bkeys row stride), ~2048 columns each
     const float *lg = m->blogits;
     int vocab = g.vocab_size;
+    int P = std::min(64, (g.vocab_size + 2047) / 2048);
+    int chunk = (g.vocab_size + P - 1) / P;
+    uint64_t *keys = m->bkeys;
     int *out = m->bnext;
-    void *args[] = {(void *)&lg, &vocab, &out};
-    if ((rc = launch_k(m, "pbx_argmax_rows", dim3(n), dim3(256), args))) return rc;
+    void *a1[] = {(void *)&lg, &vocab, &chunk, &keys, &P};
+    if ((rc = launch_k(m, "pbx_argmax_rows_partial", dim3(P, n), dim3(256), a1))) return rc;
+    void *a2[] = {&keys, &P, &out};
+    if ((rc = launch_k(m, "pbx_argmax_rows_final", dim3(n), dim3(64), a2))) return rc;
   }
   if (logits && hipMemcpyAsync(logits, m->blogits, (size_t)n * g.vocab_size * 4,
                                hipMemcpyDeviceToHost, c->stream) != hipSuccess)
