@@ -240,6 +240,207 @@ extern "C" __global__ void __launch_bounds__(256) pbx_attention_decode(AttnArgs 
 }
 
 // ---------------------------------------------------------------------------
+// Split-position attention (flash-decoding) for head_dim <= 128: grid
+// (n_kv_heads, S); workgroup (g, s) serves the Gq = n_heads/n_kv_heads query
+// heads of KV group g (one wave each) over positions [s*C, (s+1)*C) of
+// 0..pos, C = ceil((pos+1)/S).  K/V tiles of up to 32 positions are staged
+// once in LDS for all Gq heads; each wave keeps a running max / sum / weighted V sum
+// (online softmax) and writes its partial; pbx_attention_combine then merges
+// the S partials of every head:
+//   out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,
+// the softmax(q.K)V of llama.js:258-301 evaluated in S pieces.  The split
+// holding `pos` rotates the new k, appends k and v to the cache and uses them
+// from LDS; no other split reads position pos.
+// ---------------------------------------------------------------------------
+#define PBX_SPLIT_TILE 32
+#define PBX_SPLIT_MAX_HD 128
+#define PBX_SPLIT_MAX_GQ 16
+
+struct AttnSplitArgs {
+  const float *qkv;    // [dim | kv_dim | kv_dim] of this token, before RoPE
+  float *kcache;       // this layer: [max_seq][kv_dim]
+  float *vcache;
+  const float *rope;   // [max_seq][head_dim/2][cos, sin]
+  float *out;          // [dim]
+  const int *state;    // state[0] = position
+  float *part;         // [n_heads][S][head_dim + 2]: m, l, acc[head_dim]
+  int n_heads, n_kv_heads, head_dim, S;
+  float scale;         // 1/sqrt(head_dim)
+};
+
+extern "C" __global__ void __launch_bounds__(1024) pbx_attention_split(AttnSplitArgs a) {
+  __shared__ float qs[PBX_SPLIT_MAX_GQ][PBX_SPLIT_MAX_HD];
+  __shared__ float kt[PBX_SPLIT_TILE][PBX_SPLIT_MAX_HD + 1];  // +1: conflict-free column reads
+  __shared__ float vt[PBX_SPLIT_TILE][PBX_SPLIT_MAX_HD];
+  __shared__ float knew[PBX_SPLIT_MAX_HD], vnew[PBX_SPLIT_MAX_HD];
+  const int g = blockIdx.x, s = blockIdx.y;
+  const int hd = a.head_dim, Gq = a.n_heads / a.n_kv_heads, half = hd / 2;
+  const int dim = a.n_heads * hd, kvdim = a.n_kv_heads * hd;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int pos = a.state[0], L = pos + 1;
+  const int C = (L + a.S - 1) / a.S;
+  const int p0 = min(s * C, L), p1 = min(p0 + C, L);
+  const bool has_pos = p0 <= pos && pos < p1;
+  const float *rp = a.rope + (size_t)pos * hd;
+  float *kbase = a.kcache + (size_t)g * hd, *vbase = a.vcache + (size_t)g * hd;
+  const int hd4 = hd / 4;
+  // A tile is T positions such that each thread loads at most TL float4 of
+  // K and of V: T = min(32, TL * threads / (head_dim / 4)) >= 8.
+  constexpr int TL = 4;
+  const int T = min(PBX_SPLIT_TILE, TL * (int)blockDim.x / hd4);
+  float4 kreg[TL], vreg[TL];
+  auto load_tile = [&](int t0, int n) {
+#pragma unroll
+    for (int r = 0; r < TL; ++r) {
+      const int i = threadIdx.x + r * blockDim.x;
+      const int j = i / hd4, c4 = 4 * (i % hd4), p = t0 + j;
+      if (i < n * hd4 && p != pos) {
+        kreg[r] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvdim + c4);
+        vreg[r] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvdim + c4);
+      }
+    }
+  };
+  auto store_tile = [&](int t0, int n) {
+#pragma unroll
+    for (int r = 0; r < TL; ++r) {
+      const int i = threadIdx.x + r * blockDim.x;
+      const int j = i / hd4, c4 = 4 * (i % hd4), p = t0 + j;
+      if (i < n * hd4) {
+        float4 kv = kreg[r], vv = vreg[r];
+        if (p == pos) {
+          kv = make_float4(knew[c4], knew[c4 + 1], knew[c4 + 2], knew[c4 + 3]);
+          vv = make_float4(vnew[c4], vnew[c4 + 1], vnew[c4 + 2], vnew[c4 + 3]);
+        }
+        kt[j][c4] = kv.x; kt[j][c4 + 1] = kv.y; kt[j][c4 + 2] = kv.z; kt[j][c4 + 3] = kv.w;
+        *reinterpret_cast<float4 *>(&vt[j][c4]) = vv;
+      }
+    }
+  };
+  // The first tile's K/V loads do not depend on q: issue them first.
+  if (p0 < p1) load_tile(p0, min(T, p1 - p0));
+
+  // q pairs of the group's heads: Gq * hd/2 <= 64 * Gq = threads, so one
+  // pair per thread; the new k, v pair (hd/2 <= 64) likewise.
+  {
+    const int i = threadIdx.x;
+    const bool qok = i < Gq * half, kok = has_pos && i < half;
+    const int hh = i / half, k = i % half;
+    const float2 cs = (qok || kok) ? *reinterpret_cast<const float2 *>(rp + 2 * k) : make_float2(0.f, 0.f);
+    const float2 qv = qok ? *reinterpret_cast<const float2 *>(a.qkv + (size_t)(g * Gq + hh) * hd + 2 * k)
+                          : make_float2(0.f, 0.f);
+    const float *kp = a.qkv + dim + (size_t)g * hd;
+    const float2 kv = kok ? *reinterpret_cast<const float2 *>(kp + 2 * i) : make_float2(0.f, 0.f);
+    const float2 vv = kok ? *reinterpret_cast<const float2 *>(kp + kvdim + 2 * i) : make_float2(0.f, 0.f);
+    if (qok) {
+      qs[hh][2 * k] = qv.x * cs.x - qv.y * cs.y;
+      qs[hh][2 * k + 1] = qv.x * cs.y + qv.y * cs.x;
+    }
+    if (kok) {
+      knew[2 * i] = kv.x * cs.x - kv.y * cs.y;
+      knew[2 * i + 1] = kv.x * cs.y + kv.y * cs.x;
+      vnew[2 * i] = vv.x;
+      vnew[2 * i + 1] = vv.y;
+    }
+  }
+  __syncthreads();
+  if (has_pos)
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+      kbase[(size_t)pos * kvdim + d] = knew[d];
+      vbase[(size_t)pos * kvdim + d] = vnew[d];
+    }
+
+  float m = -INFINITY, l = 0.f, acc0 = 0.f, acc1 = 0.f;
+  for (int t0 = p0; t0 < p1; t0 += T) {
+    const int n = min(T, p1 - t0);
+    if (t0 != p0) load_tile(t0, n);
+    store_tile(t0, n);
+    __syncthreads();
+    if (w < Gq) {
+      float sc = -INFINITY;
+      if (lane < n) {
+        float d0 = 0.f, d1 = 0.f;
+        for (int d = 0; d < hd; d += 2) {
+          d0 = fmaf(qs[w][d], kt[lane][d], d0);
+          d1 = fmaf(qs[w][d + 1], kt[lane][d + 1], d1);
+        }
+        sc = (d0 + d1) * a.scale;
+      }
+      float mt = sc;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
+      const float mn = fmaxf(m, mt);
+      const float f = expf(m - mn);  // 0 on the first tile (m = -inf)
+      const float p = lane < n ? expf(sc - mn) : 0.f;
+      l = fmaf(l, f, wave_sum(p));
+      acc0 *= f;
+      acc1 *= f;
+      for (int j = 0; j < n; ++j) {
+        const float pj = __shfl(p, j, 64);
+        if (lane < hd) acc0 = fmaf(pj, vt[j][lane], acc0);
+        if (lane + 64 < hd) acc1 = fmaf(pj, vt[j][lane + 64], acc1);
+      }
+      m = mn;
+    }
+    __syncthreads();
+  }
+  if (w < Gq) {
+    float *pp = a.part + ((size_t)(g * Gq + w) * a.S + s) * (hd + 2);
+    if (lane == 0) {
+      pp[0] = m;
+      pp[1] = l;
+    }
+    if (lane < hd) pp[2 + lane] = acc0;
+    if (lane + 64 < hd) pp[2 + 64 + lane] = acc1;
+  }
+}
+
+// One wave per query head: merge the S split partials (m_s, l_s, acc_s),
+// S <= 64.  Lane t reads split t's (m, l); the weights e^(m_t - M) are then
+// broadcast from lane t while every lane sums its head_dim column over the
+// splits, 32 splits' loads in flight at a time.  Empty splits carry m = -inf
+// and weigh e^-inf = 0; split 0 always holds position 0, so M is finite.
+extern "C" __global__ void __launch_bounds__(64)
+pbx_attention_combine(const float *part, float *out, int head_dim, int S) {
+  const int h = blockIdx.x, lane = threadIdx.x, hd = head_dim, st = hd + 2;
+  const float *pb = part + (size_t)h * S * st;
+  // every load of the first 32 splits is issued before any reduction
+  float v0[32], v1[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const bool ok = i < S;
+    v0[i] = (ok && lane < hd) ? pb[(size_t)i * st + 2 + lane] : 0.f;
+    v1[i] = (ok && lane + 64 < hd) ? pb[(size_t)i * st + 2 + 64 + lane] : 0.f;
+  }
+  const float mt = lane < S ? pb[(size_t)lane * st] : -INFINITY;
+  const float lt = lane < S ? pb[(size_t)lane * st + 1] : 0.f;
+  float mx = mt;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  const float wt = expf(mt - mx);
+  const float lsum = wave_sum(wt * lt);
+  float o0 = 0.f, o1 = 0.f;
+  for (int t0 = 0; t0 < S; t0 += 32) {
+    if (t0 > 0) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const bool ok = t0 + i < S;
+        v0[i] = (ok && lane < hd) ? pb[(size_t)(t0 + i) * st + 2 + lane] : 0.f;
+        v1[i] = (ok && lane + 64 < hd) ? pb[(size_t)(t0 + i) * st + 2 + 64 + lane] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const float w = __shfl(wt, (t0 + i) & 63, 64);
+      o0 = fmaf(w, v0[i], o0);
+      o1 = fmaf(w, v1[i], o1);
+    }
+  }
+  const float inv = 1.0f / lsum;
+  if (lane < hd) out[(size_t)h * hd + lane] = o0 * inv;
+  if (lane + 64 < hd) out[(size_t)h * hd + 64 + lane] = o1 * inv;
+}
+
+// ---------------------------------------------------------------------------
 // Embedding row of the current token (llama.js:216-225), dequantised exactly
 // from the resident token_embd planes (gguf.js:239-286) or copied (F32).
 // ---------------------------------------------------------------------------

@@ -244,10 +244,12 @@ __device__ __forceinline__ float wave_transpose_reduce(float (&v)[R], int lane) 
   return r;
 }
 
+// Store of output row n; `res` is the residual y[n] read at kernel start
+// (EPI_ADD), so the epilogue does not wait on a second round trip.
 template <int EPI>
-__device__ __forceinline__ void epilogue_row(const GemvArgs &a, float *y, int n, float s) {
+__device__ __forceinline__ void epilogue_row(const GemvArgs &a, float *y, int n, float s, float res) {
   if constexpr (EPI == EPI_ADD) {
-    y[n] += s;
+    y[n] = res + s;
   } else {
     y[n] = s + (a.bias ? a.bias[n] : 0.f);
   }
@@ -280,6 +282,15 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
   auto tile_row = [&](int i) -> int {
     return PAIR ? (i < R / 2 ? r0 + i : N / 2 + r0 + i - R / 2) : r0 + i;
   };
+
+  // The residual rows this thread will store (EPI_ADD), read up front.
+  const int lanes_per_row = 64 / R;
+  float res = 0.f;
+  if constexpr (EPI == EPI_ADD) {
+    const int rr = nwaves == 1 ? ((lane % lanes_per_row) == 0 ? lane / lanes_per_row : R)
+                               : (int)threadIdx.x;
+    if (rr < R && r0 + rr < N) res = y[r0 + rr];
+  }
 
   // Issue the weight loads first: they do not depend on the activations.
   uint4 q[R][NV];
@@ -344,7 +355,6 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
   for (int i = 0; i < R; ++i) acc[i] = block_term<TYPE>(q[i], xr, corr, dsf[i]);
 
   const float tot = wave_transpose_reduce<R>(acc, lane);
-  const int lanes_per_row = 64 / R;
   const int row = lane / lanes_per_row;
   uint64_t key = 0;
   if constexpr (PAIR) {
@@ -374,7 +384,7 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
     if ((lane % lanes_per_row) == 0) {
       const int n = r0 + row;
       if (n < N) {
-        epilogue_row<EPI>(a, y, n, tot);
+        epilogue_row<EPI>(a, y, n, tot, res);
         if constexpr (EPI == EPI_ARGMAX) key = argmax_key(tot, (unsigned)n);
       }
     }
@@ -386,7 +396,7 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
       for (int w = 0; w < nwaves; ++w) s += red[w][threadIdx.x];
       const int n = r0 + threadIdx.x;
       if (n < N) {
-        epilogue_row<EPI>(a, y, n, s);
+        epilogue_row<EPI>(a, y, n, s, res);
         if constexpr (EPI == EPI_ARGMAX) key = argmax_key(s, (unsigned)n);
       }
     }
@@ -429,6 +439,11 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
   auto row_ok = [&](int t) -> bool {
     return PAIR ? (r0 + (t < T / 2 ? t : t - T / 2)) < NO : (r0 + t) < N;
   };
+
+  // residual of the first row this lane stores (EPI_ADD), read up front
+  float res = 0.f;
+  if constexpr (EPI == EPI_ADD)
+    if (lane < T && r0 + lane < N) res = y[r0 + lane];
 
   uint4 q[P][NV];
   float d[P];
@@ -489,7 +504,7 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
     for (int j = 0; j < B; ++j) s += part[wave][p][r * B + j];
     const int n = r0 + t;
     if (n < N) {
-      epilogue_row<EPI>(a, y, n, s);
+      epilogue_row<EPI>(a, y, n, s, t == lane ? res : y[n]);
       if constexpr (EPI == EPI_ARGMAX) {
         const uint64_t k = argmax_key(s, (unsigned)n);
         key = k > key ? k : key;

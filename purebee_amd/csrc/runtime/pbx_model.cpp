@@ -46,6 +46,23 @@ struct AttnArgsHost {  // AttnArgs in pbx_decode.hip
   float scale;
 };
 
+struct AttnSplitArgsHost {  // AttnSplitArgs in pbx_decode.hip
+  const float *qkv;
+  float *kcache, *vcache;
+  const float *rope;
+  float *out;
+  const int *state;
+  float *part;
+  int n_heads, n_kv_heads, head_dim, S;
+  float scale;
+};
+
+struct CombineArgsHost {  // pbx_attention_combine's parameters
+  const float *part;
+  float *out;
+  int head_dim, S;
+};
+
 struct EmbedArgsHost {  // EmbedArgs in pbx_decode.hip
   const void *qs;
   const void *dsc;
@@ -63,7 +80,7 @@ struct ArgmaxArgsHost {  // ArgmaxArgs in pbx_decode.hip
   int hist_cap;
 };
 
-enum ArgKind { ARG_GEMV, ARG_ATTN, ARG_EMBED, ARG_ARGMAX };
+enum ArgKind { ARG_GEMV, ARG_ATTN, ARG_ATTN_SPLIT, ARG_COMBINE, ARG_EMBED, ARG_ARGMAX };
 
 struct Op {
   hipFunction_t f = nullptr;
@@ -74,6 +91,8 @@ struct Op {
   ArgKind kind;
   GemvArgsHost gemv;
   AttnArgsHost attn;
+  AttnSplitArgsHost split;
+  CombineArgsHost comb;
   EmbedArgsHost embed;
   ArgmaxArgsHost amax;
 };
@@ -105,6 +124,9 @@ struct pbx_model {
   float *x = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
   uint64_t *partials = nullptr;
   int n_partials_cap = 0;
+  // split-position attention: S splits per KV head and their partials
+  int attn_splits = 0;
+  float *attn_part = nullptr;
   int *state = nullptr;
   int *hist = nullptr;
   int hist_cap = 0;
@@ -201,23 +223,50 @@ static int build_ops(pbx_model *m) {
   m->ops.push_back(e);
   hipFunction_t fattn = pbx_kernel_by_name(c, "pbx_attention_decode");
   if (!fattn) return pbx_fail(c, PBX_ELOAD, "model: kernel pbx_attention_decode not found");
+  hipFunction_t fsplit = pbx_kernel_by_name(c, "pbx_attention_split");
+  hipFunction_t fcomb = pbx_kernel_by_name(c, "pbx_attention_combine");
+  if (!fsplit || !fcomb)
+    return pbx_fail(c, PBX_ELOAD, "model: split attention kernels not found");
   const size_t layer_kv = (size_t)g.max_seq * m->kvdim;
   for (int l = 0; l < g.n_layers; ++l) {
     Layer &L = m->layers[l];
     int rc;
     if ((rc = add_gemv(m, L.wqkv, "qkv", "qkv", m->x, nullptr, L.attn_norm, m->qkv, nullptr))) return rc;
     Op a;
-    a.kind = ARG_ATTN;
-    a.name = "pbx_attention_decode";
-    a.f = fattn;
-    a.grid = dim3(g.n_heads);
-    a.block = dim3(256);
     a.role = "attn";
     a.bytes = 2.0 * 4.0 * m->kvdim;  // K and V of one cached position, all KV heads
-    a.attn = AttnArgsHost{m->qkv, m->kcache + l * layer_kv, m->vcache + l * layer_kv, m->rope,
-                          m->attn, m->state, g.n_heads, g.n_kv_heads, g.head_dim,
-                          (float)(1.0 / sqrt((double)g.head_dim))};
-    m->ops.push_back(a);
+    a.block = dim3(256);
+    if (m->attn_splits > 0) {
+      a.kind = ARG_ATTN_SPLIT;
+      a.name = "pbx_attention_split";
+      a.f = fsplit;
+      a.grid = dim3(g.n_kv_heads, m->attn_splits);
+      a.block = dim3(64 * (g.n_heads / g.n_kv_heads));
+      a.split = AttnSplitArgsHost{m->qkv, m->kcache + l * layer_kv, m->vcache + l * layer_kv,
+                                  m->rope, m->attn, m->state, m->attn_part,
+                                  g.n_heads, g.n_kv_heads, g.head_dim, m->attn_splits,
+                                  (float)(1.0 / sqrt((double)g.head_dim))};
+      m->ops.push_back(a);
+      Op cb;  // merges the S partials of every head into m->attn
+      cb.kind = ARG_COMBINE;
+      cb.name = "pbx_attention_combine";
+      cb.f = fcomb;
+      cb.role = "attn_combine";
+      cb.grid = dim3(g.n_heads);
+      cb.block = dim3(64);
+      cb.bytes = (double)g.n_heads * m->attn_splits * (g.head_dim + 2) * 4 + 4.0 * g.dim;
+      cb.comb = CombineArgsHost{m->attn_part, m->attn, g.head_dim, m->attn_splits};
+      m->ops.push_back(cb);
+    } else {
+      a.kind = ARG_ATTN;
+      a.name = "pbx_attention_decode";
+      a.f = fattn;
+      a.grid = dim3(g.n_heads);
+      a.attn = AttnArgsHost{m->qkv, m->kcache + l * layer_kv, m->vcache + l * layer_kv, m->rope,
+                            m->attn, m->state, g.n_heads, g.n_kv_heads, g.head_dim,
+                            (float)(1.0 / sqrt((double)g.head_dim))};
+      m->ops.push_back(a);
+    }
     if ((rc = add_gemv(m, L.wo, "add", "o", m->attn, nullptr, nullptr, m->x, nullptr))) return rc;
     if ((rc = add_gemv(m, L.wgu, "gu", "gate_up", m->x, nullptr, L.ffn_norm, m->gu, nullptr))) return rc;
     if ((rc = add_gemv(m, L.wd, "add", "down", m->gu, nullptr, nullptr, m->x, nullptr))) return rc;
@@ -249,6 +298,11 @@ static int enqueue_op(pbx_model *m, Op &op) {
   switch (op.kind) {
     case ARG_GEMV: arg = &op.gemv; break;
     case ARG_ATTN: arg = &op.attn; break;
+    case ARG_ATTN_SPLIT: arg = &op.split; break;
+    case ARG_COMBINE: {
+      void *args[] = {&op.comb.part, &op.comb.out, &op.comb.head_dim, &op.comb.S};
+      return pbx_launch_fn(m->c, op.f, op.name.c_str(), op.grid, op.block, args, m->c->stream);
+    }
     case ARG_EMBED: arg = &op.embed; break;
     default: arg = &op.amax; break;
   }
@@ -258,15 +312,7 @@ static int enqueue_op(pbx_model *m, Op &op) {
 
 static int enqueue_ops(pbx_model *m) {
   for (Op &op : m->ops) {
-    void *arg;
-    switch (op.kind) {
-      case ARG_GEMV: arg = &op.gemv; break;
-      case ARG_ATTN: arg = &op.attn; break;
-      case ARG_EMBED: arg = &op.embed; break;
-      default: arg = &op.amax; break;
-    }
-    void *args[] = {arg};
-    int rc = pbx_launch_fn(m->c, op.f, op.name.c_str(), op.grid, op.block, args, m->c->stream);
+    int rc = enqueue_op(m, op);
     if (rc) return rc;
   }
   return PBX_OK;
@@ -363,7 +409,8 @@ static void model_release(pbx_model *m) {
   pbx_weight_release(m->output);
   for (void *p : {(void *)m->out_norm, (void *)m->kcache, (void *)m->vcache, (void *)m->rope,
                   (void *)m->x, (void *)m->qkv, (void *)m->attn, (void *)m->gu, (void *)m->logits,
-                  (void *)m->partials, (void *)m->state, (void *)m->hist})
+                  (void *)m->partials, (void *)m->state, (void *)m->hist,
+                  (void *)m->attn_part})
     if (p) hipFree(p);
   for (void *p : {(void *)m->bx, (void *)m->bxn, (void *)m->bqkv, (void *)m->battn,
                   (void *)m->bgu, (void *)m->bh, (void *)m->btmp, (void *)m->blogits,
@@ -379,6 +426,12 @@ void pbx_model_release_all(pbx_ctx *c) {
   for (pbx_model *m : *list) model_release(m);
   delete list;
   c->models = nullptr;
+}
+
+// PBX_SPLIT_ATTENTION=0 selects the one-workgroup-per-head attention kernel.
+static bool split_attention_disabled() {
+  const char *e = getenv("PBX_SPLIT_ATTENTION");
+  return e && e[0] == '0';
 }
 
 static bool is_weight_type(int t) {
@@ -451,6 +504,14 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
   if (!rc) rc = dalloc(m, (void **)&m->state, 64);
   m->hist_cap = g.max_seq;
   if (!rc) rc = dalloc(m, (void **)&m->hist, (size_t)m->hist_cap * 4);
+  // Split-position attention when its tiles fit (head_dim <= 128, <= 16
+  // query heads per KV head): about 256 workgroups per layer, at most 64
+  // splits, never more splits than positions.
+  if (!rc && g.head_dim <= 128 && g.n_heads / g.n_kv_heads <= 16 && !split_attention_disabled()) {
+    m->attn_splits = std::min({64, g.max_seq, std::max(4, (256 + g.n_kv_heads - 1) / g.n_kv_heads)});
+    rc = dalloc(m, (void **)&m->attn_part,
+                (size_t)g.n_heads * m->attn_splits * (g.head_dim + 2) * 4);
+  }
   if (!rc) {
     // RoPE table, llama.js:163-190: pair i of a head rotates by
     // pos / theta^(2i/head_dim), evaluated in double as the reference does.
@@ -926,7 +987,8 @@ extern "C" int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int
       hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
       acc[i] += ms * 1e3;
       const Op &op = m->ops[i];
-      bytes[i] += op.kind == ARG_ATTN ? op.bytes * (start_pos + s + 1) : op.bytes;
+      bytes[i] += (op.kind == ARG_ATTN || op.kind == ARG_ATTN_SPLIT) ? op.bytes * (start_pos + s + 1)
+                                                                      : op.bytes;
     }
   }
   if (!rc) {

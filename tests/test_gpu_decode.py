@@ -131,6 +131,34 @@ def test_cache_rollback_and_reset(ctx):
     ref.close()
 
 
+def test_split_attention_matches_one_workgroup_per_head(ctx, monkeypatch):
+    """The split-position attention (KV group x position split, online
+    softmax over 32-position tiles, last-workgroup combine) against the
+    one-workgroup-per-head kernel and the oracle.  64 KV heads give 4 splits,
+    so 160 positions take two tiles per split."""
+    print("[case] split attention vs per-head attention, 64 heads, 160 positions", flush=True)
+    cfg = tiny(TYPE_Q8_0, TYPE_Q8_0, dim=2048, hidden_dim=256, n_layers=1, n_heads=64,
+               n_kv_heads=64, vocab_size=512, max_seq=256)
+    split, ref, cfg = make_pair(ctx, cfg, 97)
+    monkeypatch.setenv("PBX_SPLIT_ATTENTION", "0")
+    one = synth.build(ctx, cfg, 97)
+    monkeypatch.delenv("PBX_SPLIT_ATTENTION")
+    toks = [int(t) for t in synth.random_tokens(98, 160, cfg["vocab_size"])]
+    worst = 0.0
+    for p, t in enumerate(toks):
+        a, _ = split.forward([t], p)
+        b, _ = one.forward([t], p)
+        worst = max(worst, float(np.abs(a - b).max()))
+    r = ref.forward(toks, 0)
+    err = float(np.abs(a - r).max())
+    print(f"  split vs per-head max-abs {worst:.2e}, vs oracle {err:.2e}")
+    assert worst <= 1e-4
+    assert err <= LOGIT_TOL
+    split.free()
+    one.free()
+    ref.close()
+
+
 def test_model_argument_errors(ctx):
     print("[case] model errors", flush=True)
     cfg = tiny(TYPE_Q4_0, TYPE_Q4_0)
