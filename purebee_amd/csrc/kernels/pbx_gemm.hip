@@ -190,14 +190,141 @@ GEMM_KERNEL(pbx_gemm_q4_m1_n1, PBX_Q4, 1, 1)
 GEMM_KERNEL(pbx_gemm_q4_m1_n2, PBX_Q4, 1, 2)
 GEMM_KERNEL(pbx_gemm_q4_m1_n4, PBX_Q4, 1, 4)
 GEMM_KERNEL(pbx_gemm_q4_m2_n2, PBX_Q4, 2, 2)
-GEMM_KERNEL(pbx_gemm_q4_m4_n2, PBX_Q4, 4, 2)
-GEMM_KERNEL(pbx_gemm_q4_m4_n4, PBX_Q4, 4, 4)
 GEMM_KERNEL(pbx_gemm_q8_m1_n1, PBX_Q8, 1, 1)
 GEMM_KERNEL(pbx_gemm_q8_m1_n2, PBX_Q8, 1, 2)
 GEMM_KERNEL(pbx_gemm_q8_m1_n4, PBX_Q8, 1, 4)
 GEMM_KERNEL(pbx_gemm_q8_m2_n2, PBX_Q8, 2, 2)
-GEMM_KERNEL(pbx_gemm_q8_m4_n2, PBX_Q8, 4, 2)
-GEMM_KERNEL(pbx_gemm_q8_m4_n4, PBX_Q8, 4, 4)
+
+// ---------------------------------------------------------------------------
+// Large-M kernel (M > 32): workgroup tile 128 (M) x 128 (N), four waves in
+// a 2 x 2 arrangement, each wave 64 x 64 (4 x 4 MFMA tiles).  The activation
+// tile of a block (128 rows x 32 k, hi and lo, 16 KB) is loaded once per
+// workgroup into LDS (double buffered: block b+1 is read from global while
+// block b is multiplied) and read by the two waves that share it; each wave
+// reads its 64 weight rows' codes one block ahead.  LDS rows are padded to
+// 40 halves so the 16 rows of an operand read fall in distinct banks.
+// Needs X16 / X16lo padded to a multiple of 128 rows.
+// ---------------------------------------------------------------------------
+#define BIG_TM 128
+#define BIG_LDSR 40  // halves per LDS row (32 + 8 padding)
+
+template <int TYPE>
+__device__ __forceinline__ void gemm_big(const GemmArgs &a) {
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][2][BIG_TM * BIG_LDSR];  // [buf][hi/lo]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, g = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n0 = blockIdx.x * 128 + wn * 64;
+  const int mblk = blockIdx.y * BIG_TM;
+  const int m0 = wm * 64;  // within the workgroup tile
+  const int K = a.B * 32;
+  const int per = (a.B + a.KS - 1) / a.KS;
+  const int b0 = blockIdx.z * per;
+  const int b1 = min(a.B, b0 + per);
+  const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+
+  // global -> LDS staging: 1024 16-byte chunks per block (2 planes x 128
+  // rows x 4 chunks), four per thread: chunk c = tid + 256 i is plane i / 2,
+  // row (c & 511) / 4, 8-half quarter c & 3
+  uint4 st0, st1, st2, st3;
+  const int srow = (tid & 511) >> 2, sq = tid & 3;
+  const int srow2 = ((tid + 256) & 511) >> 2;
+  const _Float16 *gsrc[4] = {a.X16 + (size_t)(mblk + srow) * K + sq * 8,
+                             a.X16 + (size_t)(mblk + srow2) * K + sq * 8,
+                             a.X16lo + (size_t)(mblk + srow) * K + sq * 8,
+                             a.X16lo + (size_t)(mblk + srow2) * K + sq * 8};
+  const int ldst[4] = {srow * BIG_LDSR + sq * 8, srow2 * BIG_LDSR + sq * 8,
+                       srow * BIG_LDSR + sq * 8, srow2 * BIG_LDSR + sq * 8};
+#define BIG_LOAD_A(b)                                                              \
+  do {                                                                             \
+    st0 = *reinterpret_cast<const uint4 *>(gsrc[0] + (b) * 32);                    \
+    st1 = *reinterpret_cast<const uint4 *>(gsrc[1] + (b) * 32);                    \
+    st2 = *reinterpret_cast<const uint4 *>(gsrc[2] + (b) * 32);                    \
+    st3 = *reinterpret_cast<const uint4 *>(gsrc[3] + (b) * 32);                    \
+  } while (0)
+#define BIG_STORE_A(buf)                                                           \
+  do {                                                                             \
+    *reinterpret_cast<uint4 *>(&As[buf][0][ldst[0]]) = st0;                        \
+    *reinterpret_cast<uint4 *>(&As[buf][0][ldst[1]]) = st1;                        \
+    *reinterpret_cast<uint4 *>(&As[buf][1][ldst[2]]) = st2;                        \
+    *reinterpret_cast<uint4 *>(&As[buf][1][ldst[3]]) = st3;                        \
+  } while (0)
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[t][u] = zero;
+
+  uint2 raw[4];
+  unsigned dbits[4];
+  if (b0 < b1) {
+    BIG_LOAD_A(b0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_codes<TYPE>(a, n0 + 16 * u + li, b0, g, &raw[u], &dbits[u]);
+    BIG_STORE_A(0);
+  }
+  __syncthreads();
+  for (int b = b0; b < b1; ++b) {
+    const int buf = (b - b0) & 1;
+    const bool more = b + 1 < b1;
+    if (more) BIG_LOAD_A(b + 1);
+    half8 W[4];
+    float d[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      W[u] = codes_operand<TYPE>(raw[u], g);
+      d[u] = f16_bits_to_f32(dbits[u]);
+    }
+    if (more) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) load_codes<TYPE>(a, n0 + 16 * u + li, b + 1, g, &raw[u], &dbits[u]);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = m0 + 16 * t + li;
+      const half8 Ah = *reinterpret_cast<const half8 *>(&As[buf][0][r * BIG_LDSR + 8 * g]);
+      const half8 Al = *reinterpret_cast<const half8 *>(&As[buf][1][r * BIG_LDSR + 8 * g]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        floatx4 blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, W[u], zero, 0, 0, 0);
+        blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, W[u], blk, 0, 0, 0);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) acc[t][u][rr] = fmaf(blk[rr], d[u], acc[t][u][rr]);
+      }
+    }
+    if (more) BIG_STORE_A(buf ^ 1);
+    __syncthreads();
+  }
+#undef BIG_LOAD_A
+#undef BIG_STORE_A
+
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int n = n0 + 16 * u + li;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int m = mblk + m0 + 16 * t + 4 * g + rr;
+        if (m < a.M && n < a.N) {
+          const float v = acc[t][u][rr] * a.inv[m];
+          if (a.KS == 1) {
+            float *y = a.Y + (size_t)m * a.N + n;
+            if (a.accumulate)
+              *y += v;
+            else
+              *y = v + (a.bias ? a.bias[n] : 0.f);
+          } else {
+            a.Y[((size_t)blockIdx.z * a.M + m) * a.N + n] = v;
+          }
+        }
+      }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_big(GemmArgs a) { gemm_big<PBX_Q4>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q8_big(GemmArgs a) { gemm_big<PBX_Q8>(a); }
 
 // Row scaling to fp16: one workgroup per (padded) row.  The scale is
 // 2^(15 - e) with 2^(e-1) <= max|x| < 2^e, so every scaled value is below

@@ -162,6 +162,143 @@ pbx_attention_rows(const float *qkv, const float *kcache, const float *vcache, f
   }
 }
 
+// Tiled causal attention for head_dim <= 64 (llama.js:258-301 over a block
+// of query rows): workgroup (head h, query tile of 64 rows).  K and V of 64
+// positions at a time are staged in LDS and shared by the 64 rows; thread
+// (qi, j) holds rows 4qi..4qi+3 and, for the scores, keys 4j..4j+3 of the
+// tile, for the weighted V sum dims 4j..4j+3.  A running max, sum and
+// accumulator per row (online softmax) carry across key tiles; the rows of a
+// thread group are reduced with lane shuffles (the 16 threads of a row group
+// are consecutive lanes).  Keys after a row's own position are masked.
+#define PF_QT 64
+#define PF_KT 64
+#define PF_LD 68  // padded row stride (floats): 16-byte rows, distinct banks
+
+extern "C" __global__ void __launch_bounds__(256)
+pbx_attention_tiled(const float *qkv, const float *kcache, const float *vcache, float *out,
+                    int start, int n_rows, int n_heads, int n_kv_heads, int head_dim,
+                    float scale) {
+  __shared__ __attribute__((aligned(16))) float Qs[PF_QT * PF_LD];
+  __shared__ __attribute__((aligned(16))) float Ks[PF_KT * PF_LD];
+  __shared__ __attribute__((aligned(16))) float Vs[PF_KT * PF_LD];
+  __shared__ float Ps[PF_QT * (PF_KT + 1)];
+  const int h = blockIdx.x, t0 = blockIdx.y * PF_QT, hd = head_dim, hd4 = hd / 4;
+  const int group = n_heads / n_kv_heads, kvh = h / group;
+  const int dim = n_heads * hd, kvdim = n_kv_heads * hd, rs = dim + 2 * kvdim;
+  const int tid = threadIdx.x, qi = tid >> 4, j = tid & 15;
+  const int nq = min(PF_QT, n_rows - t0);
+  // queries of this tile (already rotated by pbx_rope_append_rows)
+  for (int i = tid; i < PF_QT * hd4; i += 256) {
+    const int r = i / hd4, c = 4 * (i % hd4);
+    const float4 v = r < nq ? *reinterpret_cast<const float4 *>(qkv + (size_t)(t0 + r) * rs + (size_t)h * hd + c)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+    *reinterpret_cast<float4 *>(&Qs[r * PF_LD + c]) = v;
+  }
+  float m[4], l[4], acc[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[r][e] = 0.f;
+  }
+  const int last_key = start + t0 + nq - 1;  // the tile's last row sees keys 0..last_key
+  const float *kb = kcache + (size_t)kvh * hd, *vb = vcache + (size_t)kvh * hd;
+  for (int k0 = 0; k0 <= last_key; k0 += PF_KT) {
+    const int nk = min(PF_KT, last_key + 1 - k0);
+    __syncthreads();  // previous tile's K/V/P reads are done
+    for (int i = tid; i < PF_KT * hd4; i += 256) {
+      const int r = i / hd4, c = 4 * (i % hd4);
+      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+      if (r < nk) {
+        kv = *reinterpret_cast<const float4 *>(kb + (size_t)(k0 + r) * kvdim + c);
+        vv = *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + r) * kvdim + c);
+      }
+      *reinterpret_cast<float4 *>(&Ks[r * PF_LD + c]) = kv;
+      *reinterpret_cast<float4 *>(&Vs[r * PF_LD + c]) = vv;
+    }
+    __syncthreads();
+    float sc[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sc[r][c] = 0.f;
+    for (int d = 0; d < hd; d += 4) {
+      float4 q[4], k[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) q[r] = *reinterpret_cast<const float4 *>(&Qs[(4 * qi + r) * PF_LD + d]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) k[c] = *reinterpret_cast<const float4 *>(&Ks[(4 * j + c) * PF_LD + d]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          sc[r][c] = fmaf(q[r].x, k[c].x, sc[r][c]);
+          sc[r][c] = fmaf(q[r].y, k[c].y, sc[r][c]);
+          sc[r][c] = fmaf(q[r].z, k[c].z, sc[r][c]);
+          sc[r][c] = fmaf(q[r].w, k[c].w, sc[r][c]);
+        }
+    }
+    float f[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int qpos = start + t0 + 4 * qi + r;
+      float mt = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int kpos = k0 + 4 * j + c;
+        sc[r][c] = (4 * j + c < nk && kpos <= qpos) ? sc[r][c] * scale : -INFINITY;
+        mt = fmaxf(mt, sc[r][c]);
+      }
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
+      const float mn = fmaxf(m[r], mt);
+      // rows past the end of the tile or with no visible key yet keep -inf
+      f[r] = mn == -INFINITY ? 1.f : expf(m[r] - mn);
+      float ps = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float p = mn == -INFINITY ? 0.f : expf(sc[r][c] - mn);
+        Ps[(4 * qi + r) * (PF_KT + 1) + 4 * j + c] = p;
+        ps += p;
+      }
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1) ps += __shfl_xor(ps, off, 64);
+      l[r] = fmaf(l[r], f[r], ps);
+      m[r] = mn;
+    }
+    __syncthreads();
+    if (4 * j < hd) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[r][e] *= f[r];
+      for (int k = 0; k < nk; ++k) {
+        const float4 v = *reinterpret_cast<const float4 *>(&Vs[k * PF_LD + 4 * j]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = Ps[(4 * qi + r) * (PF_KT + 1) + k];
+          acc[r][0] = fmaf(p, v.x, acc[r][0]);
+          acc[r][1] = fmaf(p, v.y, acc[r][1]);
+          acc[r][2] = fmaf(p, v.z, acc[r][2]);
+          acc[r][3] = fmaf(p, v.w, acc[r][3]);
+        }
+      }
+    }
+  }
+  if (4 * j < hd) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 4 * qi + r;
+      if (row < nq) {
+        const float inv = 1.0f / l[r];
+        *reinterpret_cast<float4 *>(out + (size_t)(t0 + row) * dim + (size_t)h * hd + 4 * j) =
+            make_float4(acc[r][0] * inv, acc[r][1] * inv, acc[r][2] * inv, acc[r][3] * inv);
+      }
+    }
+  }
+}
+
 // SwiGLU rows (llama.js:329-333): h[t][i] = silu(gate[t][i]) * up[t][i],
 // gate and up side by side in gu[t] = [gate | up].
 extern "C" __global__ void __launch_bounds__(256)

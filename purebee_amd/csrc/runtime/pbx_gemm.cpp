@@ -29,23 +29,35 @@ int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M6
     return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: weight type %d has no MFMA path", w->type);
   if (M64 > 65535) return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: M=%lld too large", (long long)M64);
   const int M = (int)M64, N = (int)w->N, B = (int)w->B, K = B * 32;
-  const int MT = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  // M > 32: the LDS-tiled 128 x 128 kernel; otherwise one wave per 16*MT
+  // rows x 16*NT weight rows.
+  const bool big = M > 32;
+  const int MT = big ? 8 : M <= 16 ? 1 : 2;
   const int Mpad = (M + 16 * MT - 1) / (16 * MT) * (16 * MT);
   const int mtiles = Mpad / (16 * MT);
-  // Largest n tile that still gives two workgroups per CU; then split K so
-  // at least ~8 waves per CU are in flight.
   const int want_wg = 2 * c->cu_count;
-  int NT;
-  if (MT == 1)
-    NT = ((N + 255) / 256) * mtiles >= want_wg ? 4 : ((N + 127) / 128) * mtiles >= want_wg ? 2 : 1;
-  else if (MT == 2)
-    NT = 2;
-  else
-    NT = ((N + 255) / 256) * mtiles >= want_wg ? 4 : 2;
-  const int nwg = (N + 64 * NT - 1) / (64 * NT);
-  const int waves = nwg * mtiles * 4;
+  int NT, nwg;
+  if (big) {
+    NT = 8;
+    nwg = (N + 127) / 128;
+  } else {
+    // Largest n tile that still gives two workgroups per CU.
+    if (MT == 1)
+      NT = ((N + 255) / 256) * mtiles >= want_wg ? 4 : ((N + 127) / 128) * mtiles >= want_wg ? 2 : 1;
+    else
+      NT = 2;
+    nwg = (N + 64 * NT - 1) / (64 * NT);
+  }
+  // Split K so the grid has about two workgroups (big) or eight waves
+  // (small) per CU.
   int KS = 1;
-  if (waves < 8 * c->cu_count) KS = std::min({B, 8, (8 * c->cu_count + waves - 1) / waves});
+  if (big) {
+    const int wgs = nwg * mtiles;
+    if (wgs < want_wg) KS = std::min({B, 8, (want_wg + wgs - 1) / wgs});
+  } else {
+    const int waves = nwg * mtiles * 4;
+    if (waves < 8 * c->cu_count) KS = std::min({B, 8, (8 * c->cu_count + waves - 1) / waves});
+  }
   // fp16 activations and their fp16 rounding residuals
   const size_t x16_bytes = ((size_t)Mpad * K * 2 + 255) / 256 * 256;
   const size_t lo_bytes = x16_bytes;
@@ -62,7 +74,8 @@ int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M6
 
   hipFunction_t fprep = pbx_kernel_by_name(c, "pbx_gemm_prep_x");
   const std::string name = std::string("pbx_gemm_") + (w->type == PBX_TYPE_Q4_0 ? "q4" : "q8") +
-                           "_m" + std::to_string(MT) + "_n" + std::to_string(NT);
+                           (big ? std::string("_big")
+                                : "_m" + std::to_string(MT) + "_n" + std::to_string(NT));
   hipFunction_t fg = pbx_kernel_by_name(c, name);
   hipFunction_t fred = pbx_kernel_by_name(c, "pbx_gemm_reduce");
   if (!fprep || !fg || !fred) return pbx_fail(c, PBX_ELOAD, "pbx_gemm: kernel %s missing", name.c_str());

@@ -741,10 +741,18 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
     }
     {
       float *qkv = m->bqkv, *out = m->battn;
-      int st = start, nh = g.n_heads, nkv = g.n_kv_heads, hd = g.head_dim;
+      int st = start, nh = g.n_heads, nkv = g.n_kv_heads, hd = g.head_dim, rows = n;
       float scale = (float)(1.0 / sqrt((double)g.head_dim));
-      void *args[] = {&qkv, &kc, &vc, &out, &st, &nh, &nkv, &hd, &scale};
-      if ((rc = launch_k(m, "pbx_attention_rows", dim3(g.n_heads, n), dim3(256), args))) return rc;
+      // 64-row query tiles sharing K/V tiles in LDS pay off from 16 rows; a
+      // few rows (speculative verify) spread better one workgroup per row.
+      if (g.head_dim <= 64 && n >= 16) {
+        void *args[] = {&qkv, &kc, &vc, &out, &st, &rows, &nh, &nkv, &hd, &scale};
+        rc = launch_k(m, "pbx_attention_tiled", dim3(g.n_heads, (n + 63) / 64), dim3(256), args);
+      } else {
+        void *args[] = {&qkv, &kc, &vc, &out, &st, &nh, &nkv, &hd, &scale};
+        rc = launch_k(m, "pbx_attention_rows", dim3(g.n_heads, n), dim3(256), args);
+      }
+      if (rc) return rc;
     }
     if ((rc = linear_rows(m, L.wo, m->battn, n, m->bx, true))) return rc;
     if ((rc = rmsnorm_rows(m, m->bx, L.ffn_norm, m->bxn, n))) return rc;
