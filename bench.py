@@ -12,6 +12,9 @@ steps take the KV cache from 128 to 384 positions.
 Workload "matvec": the per-token quantized-matvec pass alone (16 layers x
 q/k/v/o/gate/up/down + LM head) through the plain instruction.
 
+Workload "m-gt-1": only the M>1 measurements of the default line (batched
+512-token prefill, the MFMA GEMM at M=512, M=5 verify, speculative decoding).
+
 Prints one JSON line: the bench contract plus `roofline` (the kernel with the
 largest share of a step; HIP events on the model's stream), `kernels` (per
 role) and `cpu_baseline` (the restated reference CPU path on a bounded sample
@@ -303,7 +306,7 @@ def run_m_gt_1(ctx, model, cfg, pb, synth):
     reps = 20
     ms = ctx.bench_linear([w], [dx.ptr], [dy.ptr], M, reps) / reps
     tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-    res["gemm"] = {"shape": f"M={M} N={N} K={K} q4_0 (gate|up)", "kernel": "pbx_gemm_q4_m4_n4",
+    res["gemm"] = {"shape": f"M={M} N={N} K={K} q4_0 (gate|up)", "kernel": "pbx_gemm_q4_big",
                    "us_per_launch": round(ms * 1e3, 2), "achieved": round(tf, 2),
                    "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                    "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
@@ -415,7 +418,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--workload", choices=("decode", "matvec", "pmc-probe"), default="decode")
+    ap.add_argument("--workload", choices=("decode", "matvec", "pmc-probe", "m-gt-1"),
+                    default="decode")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-m-gt-1", action="store_true",
@@ -439,6 +443,15 @@ def main():
     from purebee_amd import synth
     if args.workload == "pmc-probe":
         run_pmc_probe(args, pb, synth)
+        return
+    if args.workload == "m-gt-1":
+        cfg = synth.CONFIGS["llama32_1b"]
+        ctx = pb.Context(0)
+        model = synth.build(ctx, cfg, seed=1000)
+        res = run_m_gt_1(ctx, model, cfg, pb, synth)
+        model.free()
+        ctx.close()
+        print(json.dumps({"workload": "llama-3.2-1b-shaped q4_0, M>1 path", "m_gt_1": res}), flush=True)
         return
     out = run_decode(args, pb, synth) if args.workload == "decode" else run_matvec(args, pb, synth)
     print(json.dumps(out), flush=True)
