@@ -9,6 +9,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <vector>
+
 #include "pbx.h"
 
 namespace {
@@ -274,13 +276,301 @@ napi_value Info(napi_env env, napi_callback_info info) {
   return o;
 }
 
+// ---- resident model (pbx_model_*) ----------------------------------------
+
+struct ModelRef {
+  pbx_model *m;
+  int vocab, max_seq;
+};
+
+void finalize_model(napi_env env, void *data, void *hint) {
+  ModelRef *r = (ModelRef *)data;
+  if (r->m && g_ctx) pbx_model_free(r->m);
+  delete r;
+}
+
+ModelRef *get_model(napi_env env, napi_value v) {
+  void *p = nullptr;
+  if (napi_get_value_external(env, v, &p) != napi_ok || !p) return nullptr;
+  ModelRef *r = (ModelRef *)p;
+  return r->m ? r : nullptr;
+}
+
+bool prop_num(napi_env env, napi_value o, const char *k, double *out, bool required) {
+  bool has = false;
+  napi_has_named_property(env, o, k, &has);
+  if (!has) return !required;
+  napi_value v;
+  napi_get_named_property(env, o, k, &v);
+  return napi_get_value_double(env, v, out) == napi_ok;
+}
+
+// Int32Array, or an Array of numbers, copied into `out`.
+bool get_tokens(napi_env env, napi_value v, std::vector<int32_t> *out) {
+  void *p;
+  size_t b;
+  napi_typedarray_type t;
+  if (typed_bytes(env, v, &p, &b, &t)) {
+    if (t != napi_int32_array) return false;
+    out->assign((int32_t *)p, (int32_t *)p + b / 4);
+    return true;
+  }
+  bool arr = false;
+  napi_is_array(env, v, &arr);
+  if (!arr) return false;
+  uint32_t n = 0;
+  napi_get_array_length(env, v, &n);
+  out->resize(n);
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value e;
+    int32_t x;
+    napi_get_element(env, v, i, &e);
+    if (napi_get_value_int32(env, e, &x) != napi_ok) return false;
+    (*out)[i] = x;
+  }
+  return true;
+}
+
+napi_value new_i32(napi_env env, size_t count, int32_t **data) {
+  napi_value ab, arr;
+  void *p = nullptr;
+  if (napi_create_arraybuffer(env, count * 4, &p, &ab) != napi_ok) return nullptr;
+  if (napi_create_typedarray(env, napi_int32_array, count, ab, 0, &arr) != napi_ok) return nullptr;
+  *data = (int32_t *)p;
+  return arr;
+}
+
+// modelCreate({dim, hiddenDim, nLayers, nHeads, nKvHeads, headDim?, vocabSize, maxSeq,
+//              weightType, embedType, outputType = -1, rmsEps = 1e-5, ropeTheta = 10000})
+napi_value ModelCreate(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  double dim, hid, nl, nh, nkv, voc, ms, wt, et, hd = 0, ot = -1, eps = 1e-5, theta = 10000;
+  napi_value o = argv[0];
+  if (!prop_num(env, o, "dim", &dim, true) || !prop_num(env, o, "hiddenDim", &hid, true) ||
+      !prop_num(env, o, "nLayers", &nl, true) || !prop_num(env, o, "nHeads", &nh, true) ||
+      !prop_num(env, o, "nKvHeads", &nkv, true) || !prop_num(env, o, "vocabSize", &voc, true) ||
+      !prop_num(env, o, "maxSeq", &ms, true) || !prop_num(env, o, "weightType", &wt, true) ||
+      !prop_num(env, o, "embedType", &et, true) || !prop_num(env, o, "headDim", &hd, false) ||
+      !prop_num(env, o, "outputType", &ot, false) || !prop_num(env, o, "rmsEps", &eps, false) ||
+      !prop_num(env, o, "ropeTheta", &theta, false))
+    return throw_msg(env, "modelCreate: config needs dim, hiddenDim, nLayers, nHeads, nKvHeads, "
+                          "vocabSize, maxSeq, weightType, embedType (numbers)");
+  pbx_model_config c;
+  c.dim = (int32_t)dim;
+  c.hidden_dim = (int32_t)hid;
+  c.n_layers = (int32_t)nl;
+  c.n_heads = (int32_t)nh;
+  c.n_kv_heads = (int32_t)nkv;
+  c.head_dim = hd > 0 ? (int32_t)hd : (nh > 0 ? (int32_t)(dim / nh) : 0);
+  c.vocab_size = (int32_t)voc;
+  c.max_seq = (int32_t)ms;
+  c.weight_type = (int32_t)wt;
+  c.embed_type = (int32_t)et;
+  c.output_type = (int32_t)ot;
+  c.rms_eps = (float)eps;
+  c.rope_theta = theta;
+  pbx_model *m = nullptr;
+  int rc = pbx_model_create(g_ctx, &c, &m);
+  if (rc) return throw_pbx(env, rc, "modelCreate");
+  ModelRef *r = new ModelRef{m, c.vocab_size, c.max_seq};
+  napi_value h;
+  if (napi_create_external(env, r, finalize_model, nullptr, &h) != napi_ok) {
+    pbx_model_free(m);
+    delete r;
+    return throw_msg(env, "modelCreate: could not create handle");
+  }
+  return h;
+}
+
+// modelSetTensor(model, tensorId, layer, data: TypedArray)
+napi_value ModelSetTensor(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[4];
+  get_args(env, info, 4, argv);
+  ModelRef *r = get_model(env, argv[0]);
+  int64_t tid, layer;
+  void *data;
+  size_t bytes;
+  if (!r || !get_i64(env, argv[1], &tid) || !get_i64(env, argv[2], &layer) ||
+      !typed_bytes(env, argv[3], &data, &bytes))
+    return throw_msg(env, "modelSetTensor(model, tensorId, layer, data): bad arguments");
+  int rc = pbx_model_set_tensor(r->m, (int)tid, (int)layer, data, bytes);
+  if (rc) return throw_pbx(env, rc, "modelSetTensor");
+  return nullptr;
+}
+
+// modelForward(model, tokens, startPos) -> {logits: Float32Array [vocab], next}
+napi_value ModelForward(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[3];
+  get_args(env, info, 3, argv);
+  ModelRef *r = get_model(env, argv[0]);
+  std::vector<int32_t> toks;
+  int64_t start;
+  if (!r || !get_tokens(env, argv[1], &toks) || !get_i64(env, argv[2], &start))
+    return throw_msg(env, "modelForward(model, tokens, startPos): bad arguments");
+  float *lg;
+  napi_value logits = new_f32(env, (size_t)r->vocab, &lg);
+  if (!logits) return throw_msg(env, "modelForward: out of memory");
+  int32_t next = 0;
+  int rc = pbx_model_forward(r->m, toks.data(), (int)toks.size(), (int)start, lg, &next);
+  if (rc) return throw_pbx(env, rc, "modelForward");
+  napi_value o, nv;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "logits", logits);
+  napi_create_int32(env, next, &nv);
+  napi_set_named_property(env, o, "next", nv);
+  return o;
+}
+
+// modelForwardBatch(model, tokens, startPos) -> {logits: Float32Array [n*vocab], next: Int32Array}
+napi_value ModelForwardBatch(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[3];
+  get_args(env, info, 3, argv);
+  ModelRef *r = get_model(env, argv[0]);
+  std::vector<int32_t> toks;
+  int64_t start;
+  if (!r || !get_tokens(env, argv[1], &toks) || !get_i64(env, argv[2], &start) || toks.empty())
+    return throw_msg(env, "modelForwardBatch(model, tokens, startPos): bad arguments");
+  float *lg;
+  int32_t *nx;
+  napi_value logits = new_f32(env, toks.size() * (size_t)r->vocab, &lg);
+  napi_value next = new_i32(env, toks.size(), &nx);
+  if (!logits || !next) return throw_msg(env, "modelForwardBatch: out of memory");
+  int rc = pbx_model_forward_batch(r->m, toks.data(), (int)toks.size(), (int)start, lg, nx);
+  if (rc) return throw_pbx(env, rc, "modelForwardBatch");
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "logits", logits);
+  napi_set_named_property(env, o, "next", next);
+  return o;
+}
+
+// modelGenerate(model, token, startPos, nSteps) -> Int32Array [nSteps]
+napi_value ModelGenerate(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[4];
+  get_args(env, info, 4, argv);
+  ModelRef *r = get_model(env, argv[0]);
+  int64_t tok, start, n;
+  if (!r || !get_i64(env, argv[1], &tok) || !get_i64(env, argv[2], &start) ||
+      !get_i64(env, argv[3], &n) || n <= 0 || n > r->max_seq)
+    return throw_msg(env, "modelGenerate(model, token, startPos, nSteps): bad arguments");
+  int32_t *out;
+  napi_value arr = new_i32(env, (size_t)n, &out);
+  if (!arr) return throw_msg(env, "modelGenerate: out of memory");
+  int rc = pbx_model_generate(r->m, (int32_t)tok, (int)start, (int)n, out, nullptr);
+  if (rc) return throw_pbx(env, rc, "modelGenerate");
+  return arr;
+}
+
+// modelRollback(model, pos) / modelReset(model) / modelFree(model)
+napi_value ModelRollback(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  ModelRef *r = get_model(env, argv[0]);
+  int64_t pos;
+  if (!r || !get_i64(env, argv[1], &pos)) return throw_msg(env, "modelRollback(model, pos): bad arguments");
+  int rc = pbx_model_rollback(r->m, (int)pos);
+  if (rc) return throw_pbx(env, rc, "modelRollback");
+  return nullptr;
+}
+
+napi_value ModelReset(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  ModelRef *r = get_model(env, argv[0]);
+  if (!r) return throw_msg(env, "modelReset(model): not a live model");
+  int rc = pbx_model_reset_cache(r->m);
+  if (rc) return throw_pbx(env, rc, "modelReset");
+  return nullptr;
+}
+
+napi_value ModelFree(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  void *p = nullptr;
+  if (napi_get_value_external(env, argv[0], &p) != napi_ok || !p)
+    return throw_msg(env, "modelFree(model): not a model handle");
+  ModelRef *r = (ModelRef *)p;
+  if (r->m) {
+    int rc = pbx_model_free(r->m);
+    r->m = nullptr;
+    if (rc) return throw_pbx(env, rc, "modelFree");
+  }
+  return nullptr;
+}
+
+// speculative(target, draft, prompt, maxTokens, draftCount = 4, eosIds = [2], batched = true)
+//   -> {tokens: Int32Array, rounds, drafted, accepted, prefillMs, decodeMs}
+napi_value Speculative(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[7];
+  get_args(env, info, 7, argv);
+  ModelRef *t = get_model(env, argv[0]), *d = get_model(env, argv[1]);
+  std::vector<int32_t> prompt, eos = {2};
+  int64_t maxTok, dc = 4;
+  if (!t || !d || !get_tokens(env, argv[2], &prompt) || !get_i64(env, argv[3], &maxTok) ||
+      maxTok <= 0 || (!is_nullish(env, argv[4]) && !get_i64(env, argv[4], &dc)) ||
+      (!is_nullish(env, argv[5]) && !get_tokens(env, argv[5], &eos)))
+    return throw_msg(env, "speculative(target, draft, prompt, maxTokens, draftCount, eosIds, "
+                          "batched): bad arguments");
+  bool batched = true;
+  if (!is_nullish(env, argv[6])) napi_get_value_bool(env, argv[6], &batched);
+  std::vector<int32_t> out((size_t)maxTok + 1);
+  int n = 0;
+  pbx_spec_stats st;
+  int rc = pbx_speculative_generate(t->m, d->m, prompt.data(), (int)prompt.size(), (int)maxTok,
+                                    (int)dc, eos.empty() ? nullptr : eos.data(), (int)eos.size(),
+                                    batched ? 1 : 0, out.data(), &n, &st);
+  if (rc) return throw_pbx(env, rc, "speculative");
+  int32_t *tk;
+  napi_value toks = new_i32(env, (size_t)n, &tk);
+  if (!toks) return throw_msg(env, "speculative: out of memory");
+  memcpy(tk, out.data(), (size_t)n * 4);
+  napi_value o, v;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "tokens", toks);
+  napi_create_int32(env, st.rounds, &v);
+  napi_set_named_property(env, o, "rounds", v);
+  napi_create_int32(env, st.drafted, &v);
+  napi_set_named_property(env, o, "drafted", v);
+  napi_create_int32(env, st.accepted, &v);
+  napi_set_named_property(env, o, "accepted", v);
+  napi_create_double(env, st.prefill_ms, &v);
+  napi_set_named_property(env, o, "prefillMs", v);
+  napi_create_double(env, st.decode_ms, &v);
+  napi_set_named_property(env, o, "decodeMs", v);
+  return o;
+}
+
 napi_value ModuleInit(napi_env env, napi_value exports) {
   struct {
     const char *name;
     napi_callback cb;
-  } fns[] = {{"init", Init},     {"deviceInfo", DeviceInfo}, {"upload", Upload},
-             {"uploadQ8Ref", UploadQ8Ref}, {"free", Free},  {"linear", Linear},
-             {"dequant", Dequant}, {"info", Info}};
+  } fns[] = {{"init", Init},
+             {"deviceInfo", DeviceInfo},
+             {"upload", Upload},
+             {"uploadQ8Ref", UploadQ8Ref},
+             {"free", Free},
+             {"linear", Linear},
+             {"dequant", Dequant},
+             {"info", Info},
+             {"modelCreate", ModelCreate},
+             {"modelSetTensor", ModelSetTensor},
+             {"modelForward", ModelForward},
+             {"modelForwardBatch", ModelForwardBatch},
+             {"modelGenerate", ModelGenerate},
+             {"modelRollback", ModelRollback},
+             {"modelReset", ModelReset},
+             {"modelFree", ModelFree},
+             {"speculative", Speculative}};
   for (auto &f : fns) {
     napi_value fn;
     napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn);

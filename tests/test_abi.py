@@ -84,7 +84,9 @@ def test_napi_addon_loads_and_exports():
     r = subprocess.run(["node", "-e", js], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stderr
     keys = set(__import__("json").loads(r.stdout))
-    for k in ("init", "upload", "linear", "dequant", "free", "deviceInfo"):
+    for k in ("init", "upload", "linear", "dequant", "free", "deviceInfo", "modelCreate",
+              "modelSetTensor", "modelForward", "modelForwardBatch", "modelGenerate",
+              "modelRollback", "modelReset", "modelFree", "speculative"):
         assert k in keys, keys
 
 

@@ -1,0 +1,208 @@
+"""The JavaScript drop-ins on the GPU, driven through Node.js exactly as the
+reference's callers would use them:
+
+* js/hip-q4.js      -- wasm-q4.js surface (q4_0_matvec, matvec dispatch,
+                       lmHead) on raw GGUF Q4_0 / Q8_0 blocks;
+* js/engine-hip.js  -- ExecutionEngine.tensorMulAdd / tensorMulAddQ8 /
+                       tensorMul (f32 [K,N] Tensors and quantize.js's
+                       QuantizedTensor);
+* js/llama-hip.js   -- the resident model: forward / generate / rollback and
+                       the greedy speculative decoder.
+
+Inputs and expected outputs are computed here (the oracle, or the C ABI's
+own model for end-to-end tokens), passed to Node through files, and the
+results read back.  Bars as elsewhere: matvec 1e-3 relative L2, logits 2e-3.
+"""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+import purebee_amd as pb
+from purebee_amd import synth
+from purebee_amd.native import TYPE_Q4_0, TYPE_Q8_0, speculative_generate
+from tests.conftest import rel_l2
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(shutil.which("node") is None, reason="node not installed")]
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+JS = os.path.join(ROOT, "purebee_amd", "js")
+
+PRELUDE = """
+const fs = require('fs');
+const path = require('path');
+const dir = process.argv[2];
+const rd = (n, T) => { const b = fs.readFileSync(path.join(dir, n));
+  return new T(b.buffer.slice(b.byteOffset, b.byteOffset + b.length)); };
+const wr = (n, a) => fs.writeFileSync(path.join(dir, n), Buffer.from(a.buffer, a.byteOffset, a.byteLength));
+const meta = JSON.parse(fs.readFileSync(path.join(dir, 'meta.json')));
+"""
+
+
+def run_node(tmp_path, script, meta):
+    (tmp_path / "meta.json").write_text(json.dumps(meta))
+    (tmp_path / "t.js").write_text(PRELUDE + script)
+    r = subprocess.run(["node", str(tmp_path / "t.js"), str(tmp_path)], capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return r.stdout
+
+
+def test_hip_q4_module_matvec_and_dispatch(tmp_path):
+    print("[case] js hip-q4 q4_0_matvec / matvec / lmHead", flush=True)
+    N, K = 2048, 2048
+    w = pb.synth_normal(501, N * K, 0, 0.02).reshape(N, K)
+    raw4 = pb.quantize_q4_0(w)
+    raw8 = pb.quantize_q8_0(w)
+    x = pb.synth_normal(502, K)
+    emb = pb.synth_normal(503, 1000 * K, 0, 0.02)
+    raw4.tofile(tmp_path / "w4.bin")
+    raw8.tofile(tmp_path / "w8.bin")
+    x.tofile(tmp_path / "x.bin")
+    emb.tofile(tmp_path / "emb.bin")
+    out = run_node(tmp_path, f"""
+const q = require({os.path.join(JS, 'hip-q4.js')!r});
+if (!q.init()) throw new Error('init failed');
+const x = rd('x.bin', Float32Array), w4 = rd('w4.bin', Uint8Array), w8 = rd('w8.bin', Uint8Array);
+const xcopy = Float32Array.from(x);
+const y4 = q.q4_0_matvec(x, w4, meta.N, meta.K);
+const y4b = q.q4_0_matvec(x, w4, meta.N, meta.K);   // resident second call
+const y8 = q.matvec(x, w8, 8, meta.N, meta.K);
+const lm = q.lmHead(x, rd('emb.bin', Float32Array), 1000, meta.K);
+wr('y4.bin', y4); wr('y8.bin', y8); wr('lm.bin', lm);
+let errs = [];
+try {{ q.matvec(x, w4, 3, meta.N, meta.K); }} catch (e) {{ errs.push(e.message); }}
+try {{ q.matvec(x, w4, 6, meta.N, meta.K); }} catch (e) {{ errs.push(e.message); }}
+let same = true; for (let i = 0; i < x.length; i++) if (x[i] !== xcopy[i]) same = false;
+let rep = true; for (let i = 0; i < y4.length; i++) if (y4[i] !== y4b[i]) rep = false;
+console.log(JSON.stringify({{errs, same, rep, supported: q.supported}}));
+""", {"N": N, "K": K})
+    res = json.loads(out.strip().splitlines()[-1])
+    assert res["same"], "input mutated"
+    assert res["rep"], "second (resident) call differs"
+    assert len(res["errs"]) == 2 and all(res["errs"]), res["errs"]
+    y4 = np.fromfile(tmp_path / "y4.bin", np.float32)
+    y8 = np.fromfile(tmp_path / "y8.bin", np.float32)
+    lm = np.fromfile(tmp_path / "lm.bin", np.float32)
+    assert rel_l2(y4, oracle.q4_0_matvec_js(x, raw4, N, K)) <= 1e-3
+    assert rel_l2(y8, oracle.matvec(TYPE_Q8_0, x, raw8, N, K)) <= 1e-3
+    ref_lm = emb.reshape(1000, K).astype(np.float64) @ x.astype(np.float64)
+    assert rel_l2(lm, ref_lm) <= 1e-3
+
+
+def test_engine_adapter_linear_ops(tmp_path):
+    """tensorMulAdd / tensorMul on f32 [K,N] Tensors and tensorMulAddQ8 on a
+    quantize.js QuantizedTensor, through HipEngine and install()."""
+    print("[case] js engine-hip tensorMulAdd / tensorMulAddQ8", flush=True)
+    M, K, N = 5, 288, 768
+    rng = np.random.default_rng(7)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    W = rng.normal(0, 0.02, (K, N)).astype(np.float32)    # reference [K,N]
+    b = rng.normal(0, 1, N).astype(np.float32)
+    q, sc = pb.quantize_q8_ref(W)                           # quantize.js layout
+    x.tofile(tmp_path / "x.bin")
+    W.tofile(tmp_path / "W.bin")
+    b.tofile(tmp_path / "b.bin")
+    q.tofile(tmp_path / "q.bin")
+    sc.tofile(tmp_path / "s.bin")
+    run_node(tmp_path, f"""
+const eng = require({os.path.join(JS, 'engine-hip.js')!r});
+const T = eng.PlainTensor;
+const fake = {{ engine: {{}} }};
+const hip = eng.install(fake);
+const x = new T('x', [meta.M, meta.K], rd('x.bin', Float32Array));
+const W = new T('W', [meta.K, meta.N], rd('W.bin', Float32Array));
+const b = new T('b', [meta.N], rd('b.bin', Float32Array));
+fake.engine.cacheWeight(W);
+const y = fake.engine.tensorMulAdd(x, W, b, 'y');
+const z = fake.engine.tensorMul(x, W, 'z');
+const Wq = {{ type: 'q8_0', shape: [meta.K, meta.N], data: rd('q.bin', Int8Array), scales: rd('s.bin', Float32Array) }};
+const yq = fake.engine.tensorMulAddQ8(x, Wq, b, 'yq');
+if (y.shape[0] !== meta.M || y.shape[1] !== meta.N || y.name !== 'y') throw new Error('bad tensor');
+let threw = false;
+try {{ fake.engine.tensorMulAdd(new T('bad', [meta.M, meta.K + 1]), W, null, 'o'); }} catch (e) {{ threw = true; }}
+if (!threw) throw new Error('dimension mismatch not thrown');
+wr('y.bin', y.data); wr('z.bin', z.data); wr('yq.bin', yq.data);
+console.log(JSON.stringify(hip.stats));
+""", {"M": M, "K": K, "N": N})
+    y = np.fromfile(tmp_path / "y.bin", np.float32).reshape(M, N)
+    z = np.fromfile(tmp_path / "z.bin", np.float32).reshape(M, N)
+    yq = np.fromfile(tmp_path / "yq.bin", np.float32).reshape(M, N)
+    ref = x.astype(np.float64) @ W.astype(np.float64)
+    assert rel_l2(z, ref) <= 1e-5
+    assert rel_l2(y, ref + b) <= 1e-5
+    refq = oracle.matmul_q8_ref(x, q, sc, N, b)
+    assert rel_l2(yq, refq) <= 1e-3
+
+
+def test_llama_runtime_and_speculative_decoder(ctx, tmp_path):
+    """HipLlamaRuntime loaded tensor by tensor under GGUF names: forward
+    logits and greedy tokens match the same weights through the C ABI, and
+    HipSpeculativeDecoder emits the greedy tokens."""
+    print("[case] js llama-hip forward / generate / speculative", flush=True)
+    cfg = dict(dim=256, hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=1000,
+               max_seq=128, weight_type=TYPE_Q4_0, embed_type=TYPE_Q4_0, rope_theta=10000.0)
+    names = {0: "token_embd.weight", 2: "output_norm.weight", 3: "attn_norm.weight",
+             4: "ffn_norm.weight", 5: "attn_q.weight", 6: "attn_k.weight", 7: "attn_v.weight",
+             8: "attn_output.weight", 9: "ffn_gate.weight", 10: "ffn_up.weight",
+             11: "ffn_down.weight"}
+    files = []
+
+    def keep(spec, data):
+        tid, layer, N, K, t = spec
+        nm = names[tid] if layer < 0 else f"blk.{layer}.{names[tid]}"
+        fn = f"t{len(files)}.bin"
+        np.ascontiguousarray(data).tofile(tmp_path / fn)
+        files.append([nm, fn, "f32" if data.dtype == np.float32 else "u8"])
+
+    model = synth.build(ctx, cfg, 600, keep)
+    prompt = [int(t) for t in synth.random_tokens(601, 12, cfg["vocab_size"])]
+    logits, nxt = model.forward(prompt, 0)
+    greedy = [nxt] + [int(t) for t in model.generate(nxt, 12, 19)]
+    model.reset_cache()
+    draft = synth.build(ctx, cfg, 600)
+    spec, _ = speculative_generate(model, draft, prompt, 20, 4, eos_ids=())
+    assert list(spec[:20]) == greedy
+    model.free()
+    draft.free()
+    out = run_node(tmp_path, f"""
+const {{ HipLlamaRuntime, HipSpeculativeDecoder }} = require({os.path.join(JS, 'llama-hip.js')!r});
+const c = meta.cfg;
+const mk = () => {{
+  const rt = new HipLlamaRuntime({{ dim: c.dim, hiddenDim: c.hidden_dim, nLayers: c.n_layers, nHeads: c.n_heads,
+    nKvHeads: c.n_kv_heads, vocabSize: c.vocab_size, seqLen: c.max_seq, ropeTheta: c.rope_theta,
+    weightType: 'q4_0', embedType: 'q4_0' }});
+  for (const [nm, fn, ty] of meta.files) rt.loadTensor(nm, rd(fn, ty === 'f32' ? Float32Array : Uint8Array));
+  return rt;
+}};
+const rt = mk();
+const logits = rt.forward(meta.prompt, 0);
+wr('logits.bin', logits);
+const gen = rt.generate(meta.prompt, 20, {{ greedy: true, eosId: -1 }});
+rt.rollbackCache(5);
+const all = rt.forwardAll(meta.prompt.slice(5), 5);
+wr('all.bin', all.logits);
+const dr = mk();
+const sd = new HipSpeculativeDecoder(rt, dr, {{ draftCount: 4 }});
+const sp = sd.generate(meta.prompt, 20, {{ eosIds: [] }});
+let threw = false;
+try {{ rt.generate(meta.prompt, 4, {{}}); }} catch (e) {{ threw = true; }}
+console.log(JSON.stringify({{ gen: gen.tokens.slice(meta.prompt.length), spec: sp.tokens.slice(meta.prompt.length),
+  acc: sp.acceptanceRate, threw, argmax: rt.argmax(logits) }}));
+rt.free(); dr.free();
+""", {"cfg": cfg, "files": files, "prompt": prompt})
+    res = json.loads(out.strip().splitlines()[-1])
+    lj = np.fromfile(tmp_path / "logits.bin", np.float32)
+    assert float(np.abs(lj - logits).max()) <= 2e-3
+    assert res["argmax"] == int(np.argmax(lj))
+    assert res["gen"] == greedy
+    assert res["spec"][:20] == greedy
+    assert res["threw"], "non-greedy generate must throw"
+    allj = np.fromfile(tmp_path / "all.bin", np.float32).reshape(-1, cfg["vocab_size"])
+    assert allj.shape[0] == len(prompt) - 5
+    assert float(np.abs(allj[-1] - logits).max()) <= 2e-3
