@@ -51,6 +51,24 @@ DK_MODES_SMALL(PBX_Q4, q4, 8)
 DK_MODES_WIDE(PBX_Q8, q8, 4)
 DK_MODES_WIDE(PBX_Q8, q8, 8)
 DK_MODES_SMALL(PBX_Q8, q8, 4)
+// Integer-limb kernels for the gate|up GEMV (RMSNorm + SwiGLU pair), the
+// largest matrix of a layer; for the smaller GEMVs the activation prologue
+// costs more than the dot products save (measured).
+// Name: pbx_dk_<type>_i<WV>x<RT>b<IB>_gu.
+#define DK_INT_GU(T, TN, WV, RT, IB)                                                      \
+  extern "C" __global__ void __launch_bounds__(WV * 64)                                   \
+      pbx_dk_##TN##_i##WV##x##RT##b##IB##_gu(GemvArgs a) {                                \
+    gemv_int<T, WV, RT, IB, PRO_RMSNORM, EPI_SWIGLU>(a);                                  \
+  }
+DK_INT_GU(PBX_Q4, q4, 8, 4, 1)
+DK_INT_GU(PBX_Q4, q4, 16, 4, 1)
+DK_INT_GU(PBX_Q4, q4, 8, 4, 2)
+DK_INT_GU(PBX_Q4, q4, 16, 4, 2)
+DK_INT_GU(PBX_Q8, q8, 8, 4, 1)
+DK_INT_GU(PBX_Q8, q8, 16, 4, 1)
+DK_INT_GU(PBX_Q8, q8, 8, 4, 2)
+DK_INT_GU(PBX_Q8, q8, 16, 4, 2)
+
 DK_MODES_WIDE(PBX_F32, f32, 2)
 DK_MODES_WIDE(PBX_F32, f32, 4)
 DK_MODES_SMALL(PBX_F32, f32, 2)

@@ -517,6 +517,216 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Integer-limb GEMV for Q4_0 / Q8_0 with K >= 2048 (decode).  The workgroup
+// first turns the (normalised) activation vector into fixed point with one
+// power-of-two scale for the whole vector,
+//   x_q = rint(x * 2^(22 - e)),  2^(e-1) <= max|x| < 2^e,  |x_q| < 2^22,
+// held in LDS as three signed-byte limbs x_q = x2*65536 + x1*256 + x0 (with
+// x0, x1 the sign-extended low bytes) plus the exact per-block sums of x_q.
+// A block-row dot is then 8 (Q4_0: nibble words) or 8 (Q8_0: int8 words)
+// v_dot4_i32_i8 per limb, exact in int32, combined once in fp32 and scaled
+// by the block's d; 2^(e-22) is applied after the reduction.  Rounding x to
+// x_q costs at most 2^-23 of max|x| per element (~1e-6 relative to the
+// output for these vectors), against the ~75 VALU operations per block-row
+// of the float unpack the other kernels use.
+// Workgroup: WV waves x RT rows each (PAIR: RT/2 gate + RT/2 up rows); lane
+// l owns blocks l, l+64, ... (IB of them).
+// ---------------------------------------------------------------------------
+#define PBX_INT_MAXK 4096
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) {
+  return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+template <int TYPE, int WV, int RT, int IB, int PRO, int EPI>
+__device__ __forceinline__ void gemv_int(const GemvArgs &a) {
+  static_assert(TYPE == PBX_Q4 || TYPE == PBX_Q8, "quantised weights only");
+  constexpr int QB = BlockTraits<TYPE>::QB;
+  constexpr int NV = QB / 16;
+  constexpr int T = WV * 64;
+  constexpr bool PAIR = EPI == EPI_SWIGLU;
+  __shared__ __attribute__((aligned(16))) int limb[3][PBX_INT_MAXK / 4];
+  __shared__ int bsum[PBX_INT_MAXK / 32];
+  __shared__ float red[2][WV];
+  __shared__ uint64_t kred[WV];
+
+  const int N = a.N, B = a.B, K = B * 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
+  const int NO = PAIR ? N / 2 : N;
+  const int r0 = (blockIdx.x * WV + wave) * (PAIR ? RT / 2 : RT);
+  auto tile_row = [&](int i) -> int {
+    return PAIR ? (i < RT / 2 ? r0 + i : N / 2 + r0 + i - RT / 2) : r0 + i;
+  };
+  auto row_ok = [&](int i) -> bool {
+    return PAIR ? (r0 + (i < RT / 2 ? i : i - RT / 2)) < NO : (r0 + i) < N;
+  };
+  constexpr int LPR = 64 / RT;  // lanes per row after the transposed reduction
+  float *y = a.Y;
+  float res = 0.f;
+  if constexpr (EPI == EPI_ADD) {
+    const int rr = (lane % LPR) == 0 ? lane / LPR : RT;
+    if (rr < RT && r0 + rr < N) res = y[r0 + rr];
+  }
+
+  // weights first: they do not depend on the activations
+  uint4 q[RT][IB][NV];
+  float dsf[RT][IB];
+#pragma unroll
+  for (int i = 0; i < RT; ++i) {
+    const int rw = tile_row(i);
+    const bool rok = row_ok(i);
+#pragma unroll
+    for (int j = 0; j < IB; ++j) {
+      const int b = lane + 64 * j;
+      const bool ok = rok && b < B;
+      const uint8_t *src = a.qs + ((size_t)rw * B + b) * QB;
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        q[i][j][v] = ok ? ld_stream(src + v * 16) : make_uint4(0u, 0u, 0u, 0u);
+      dsf[i][j] = ok ? f16_bits_to_f32(a.dsc[dsc_index(rw, b, B)]) : 0.f;
+    }
+  }
+
+  // pass 1: sum of squares (RMSNorm) and max |x * w|
+  float ss = 0.f, mw = 0.f;
+  for (int i = tid * 4; i < K; i += T * 4) {
+    const float4 v = *reinterpret_cast<const float4 *>(a.X + i);
+    float4 w = make_float4(1.f, 1.f, 1.f, 1.f);
+    if constexpr (PRO == PRO_RMSNORM) {
+      w = *reinterpret_cast<const float4 *>(a.normw + i);
+      ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+    }
+    mw = fmaxf(mw, fmaxf(fmaxf(fabsf(v.x * w.x), fabsf(v.y * w.y)),
+                         fmaxf(fabsf(v.z * w.z), fabsf(v.w * w.w))));
+  }
+  if constexpr (PRO == PRO_RMSNORM) ss = wave_sum(ss);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mw = fmaxf(mw, __shfl_xor(mw, off, 64));
+  if (lane == 0) {
+    red[0][wave] = ss;
+    red[1][wave] = mw;
+  }
+  __syncthreads();
+  ss = 0.f;
+  mw = 0.f;
+#pragma unroll
+  for (int w = 0; w < WV; ++w) {
+    ss += red[0][w];
+    mw = fmaxf(mw, red[1][w]);
+  }
+  const float inv = PRO == PRO_RMSNORM ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.f;
+  int e = 0;
+  const float mx = mw * inv;
+  if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
+  const float c = inv * ldexpf(1.f, 22 - e);  // x_q = rint(x * w * c)
+  const float unscale = ldexpf(1.f, e - 22);
+
+  // pass 2: limbs and per-block sums (8 consecutive threads cover a block)
+  for (int i = tid * 4; i < K; i += T * 4) {
+    const float4 v = *reinterpret_cast<const float4 *>(a.X + i);
+    float4 w = make_float4(1.f, 1.f, 1.f, 1.f);
+    if constexpr (PRO == PRO_RMSNORM) w = *reinterpret_cast<const float4 *>(a.normw + i);
+    const int xq[4] = {(int)rintf(v.x * w.x * c), (int)rintf(v.y * w.y * c),
+                       (int)rintf(v.z * w.z * c), (int)rintf(v.w * w.w * c)};
+    unsigned l0 = 0, l1 = 0, l2 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int x0 = (int)(int8_t)(xq[k] & 0xFF);
+      const int r1 = (xq[k] - x0) >> 8;
+      const int x1 = (int)(int8_t)(r1 & 0xFF);
+      const int x2 = (r1 - x1) >> 8;
+      l0 |= (unsigned)(x0 & 0xFF) << (8 * k);
+      l1 |= (unsigned)(x1 & 0xFF) << (8 * k);
+      l2 |= (unsigned)(x2 & 0xFF) << (8 * k);
+    }
+    limb[0][i >> 2] = (int)l0;
+    limb[1][i >> 2] = (int)l1;
+    limb[2][i >> 2] = (int)l2;
+    int s4 = xq[0] + xq[1] + xq[2] + xq[3];
+    s4 += __shfl_xor(s4, 1, 64);
+    s4 += __shfl_xor(s4, 2, 64);
+    s4 += __shfl_xor(s4, 4, 64);
+    if ((tid & 7) == 0) bsum[i >> 5] = s4;
+  }
+  __syncthreads();
+
+  float acc[RT];
+#pragma unroll
+  for (int i = 0; i < RT; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int j = 0; j < IB; ++j) {
+    const int b = lane + 64 * j;
+    if (b >= B) continue;
+    int xl[3][8];
+#pragma unroll
+    for (int L = 0; L < 3; ++L) {
+      const int4 t0 = *reinterpret_cast<const int4 *>(&limb[L][b * 8]);
+      const int4 t1 = *reinterpret_cast<const int4 *>(&limb[L][b * 8 + 4]);
+      xl[L][0] = t0.x; xl[L][1] = t0.y; xl[L][2] = t0.z; xl[L][3] = t0.w;
+      xl[L][4] = t1.x; xl[L][5] = t1.y; xl[L][6] = t1.z; xl[L][7] = t1.w;
+    }
+    const float corr = TYPE == PBX_Q4 ? 8.f * (float)bsum[b] : 0.f;
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      int s0 = 0, s1 = 0, s2 = 0;
+      if constexpr (TYPE == PBX_Q4) {
+        // byte t holds element t (low nibble) and t+16 (high): word k covers
+        // elements 4k..4k+3 (limb word k) and 16+4k.. (limb word 4+k)
+        const unsigned w[4] = {q[i][j][0].x, q[i][j][0].y, q[i][j][0].z, q[i][j][0].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int lo = (int)(w[k] & 0x0F0F0F0Fu), hi = (int)((w[k] >> 4) & 0x0F0F0F0Fu);
+          s0 = sdot4(lo, xl[0][k], s0); s0 = sdot4(hi, xl[0][4 + k], s0);
+          s1 = sdot4(lo, xl[1][k], s1); s1 = sdot4(hi, xl[1][4 + k], s1);
+          s2 = sdot4(lo, xl[2][k], s2); s2 = sdot4(hi, xl[2][4 + k], s2);
+        }
+      } else {
+        const unsigned w[8] = {q[i][j][0].x, q[i][j][0].y, q[i][j][0].z, q[i][j][0].w,
+                               q[i][j][1].x, q[i][j][1].y, q[i][j][1].z, q[i][j][1].w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          s0 = sdot4((int)w[k], xl[0][k], s0);
+          s1 = sdot4((int)w[k], xl[1][k], s1);
+          s2 = sdot4((int)w[k], xl[2][k], s2);
+        }
+      }
+      const float f = fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0)) - corr;
+      acc[i] = fmaf(f, dsf[i][j], acc[i]);
+    }
+  }
+
+  const float tot = wave_transpose_reduce<RT>(acc, lane) * unscale;
+  const int row = lane / LPR;
+  if constexpr (PAIR) {
+    const float up = __shfl_xor(tot, 32, 64);
+    if (lane < 32 && (lane % LPR) == 0) {
+      const int n = r0 + row;
+      if (n < NO) y[n] = silu(tot) * up;
+    }
+    return;
+  }
+  uint64_t key = 0;
+  if ((lane % LPR) == 0) {
+    const int n = r0 + row;
+    if (n < N) {
+      epilogue_row<EPI>(a, y, n, tot, res);
+      if constexpr (EPI == EPI_ARGMAX) key = argmax_key(tot, (unsigned)n);
+    }
+  }
+  if constexpr (EPI == EPI_ARGMAX) {
+    key = wave_max_u64(key);
+    if (lane == 0) kred[wave] = key;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t best = kred[0];
+#pragma unroll
+      for (int w = 1; w < WV; ++w) best = kred[w] > best ? kred[w] : best;
+      a.partials[blockIdx.x] = best;
+    }
+  }
+}
+
 }  // namespace pbx
 
 #endif

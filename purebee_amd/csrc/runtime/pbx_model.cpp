@@ -124,6 +124,7 @@ struct pbx_model {
   float *x = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
   uint64_t *partials = nullptr;
   int n_partials_cap = 0;
+  bool gemv_int = true;  // integer-limb gate|up GEMV where it applies
   // split-position attention: S splits per KV head and their partials
   int attn_splits = 0;
   float *attn_part = nullptr;
@@ -147,11 +148,41 @@ struct pbx_model {
 
 static bool model_ok(const pbx_model *m) { return m && m->magic == PBX_MODEL_MAGIC; }
 
+// Integer-limb kernel for the gate|up GEMV (K = 2048..4096, Q4_0 / Q8_0):
+// 16 waves x 4 rows per workgroup when that still gives >= 256 workgroups,
+// else 8 x 4.  PBX_GEMV_INT=0 at model creation selects the float-unpack
+// kernel instead.
+static bool int_gemv_disabled() {
+  const char *e = getenv("PBX_GEMV_INT");
+  return e && e[0] == '0';
+}
+
+static bool int_shape(bool enabled, const char *mode, int type, int N, int B, int *wv, int *rt,
+                      int *ib) {
+  if (!enabled) return false;
+  if (strcmp(mode, "gu") != 0 || (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0) || B < 64 ||
+      B > 128)
+    return false;
+  *ib = B <= 64 ? 1 : 2;
+  *rt = 4;
+  *wv = N / 64 >= 256 ? 16 : 8;
+  return true;
+}
+
 // Kernel shape for a GEMV of N rows x B blocks (the same rules as the plain
-// instruction): small-K kernel for B <= 32, otherwise ceil(B/64) waves per
-// workgroup and the largest row tile that keeps >= 4 workgroups per CU.
-static void plan_gemv(pbx_ctx *c, int type, int N, int B, std::string *shape, dim3 *grid,
-                      dim3 *block, int *n_tiles) {
+// instruction): the integer-limb kernel for the gate|up GEMV where it
+// applies; else the small-K kernel for B <= 32, otherwise ceil(B/64) waves
+// per workgroup and the largest row tile that keeps >= 4 workgroups per CU.
+static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, int type, int N, int B,
+                      std::string *shape, dim3 *grid, dim3 *block, int *n_tiles) {
+  int wv, rt, ib;
+  if (int_shape(int_ok, mode, type, N, B, &wv, &rt, &ib)) {
+    *shape = "i" + std::to_string(wv) + "x" + std::to_string(rt) + "b" + std::to_string(ib);
+    *grid = dim3((N + wv * rt - 1) / (wv * rt));
+    *block = dim3(64 * wv);
+    *n_tiles = (int)grid->x;
+    return;
+  }
   if (B <= 32) {
     const int P = type == PBX_TYPE_Q4_0 ? 8 : type == PBX_TYPE_Q8_0 ? 4 : 2;
     const int T = P * (64 / B);
@@ -185,7 +216,8 @@ static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const c
   op.kind = ARG_GEMV;
   std::string shape;
   int n_tiles = 0;
-  plan_gemv(c, w->type, (int)w->N, (int)w->B, &shape, &op.grid, &op.block, &n_tiles);
+  plan_gemv(c, m->gemv_int, mode, w->type, (int)w->N, (int)w->B, &shape, &op.grid, &op.block,
+            &n_tiles);
   if (w->B > 32 && (w->B + 63) / 64 > 8)
     return pbx_fail(c, PBX_ENOTSUP, "model: K=%lld exceeds the GEMV limit of 16384",
                     (long long)w->K);
@@ -470,6 +502,7 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
   m->cfg = g;
   m->kvdim = g.n_kv_heads * g.head_dim;
   m->qkv_rows = g.dim + 2 * m->kvdim;
+  m->gemv_int = !int_gemv_disabled();
   m->layers.resize(g.n_layers);
   int rc = PBX_OK;
   for (int l = 0; l < g.n_layers && !rc; ++l) {

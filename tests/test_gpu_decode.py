@@ -159,6 +159,33 @@ def test_split_attention_matches_one_workgroup_per_head(ctx, monkeypatch):
     ref.close()
 
 
+@pytest.mark.parametrize("wt", [TYPE_Q4_0, TYPE_Q8_0])
+def test_integer_limb_gate_up_matches_float_kernel(ctx, monkeypatch, wt):
+    """The gate|up GEMV on integer limbs (v_dot4 over a fixed-point activation)
+    against the float-unpack kernel and the oracle, K = 2048."""
+    print(f"[case] integer-limb gate|up vs float kernel, type {wt}", flush=True)
+    cfg = tiny(wt, wt, dim=2048, hidden_dim=1024, n_layers=1, n_heads=16, n_kv_heads=4,
+               vocab_size=512, max_seq=64)
+    fast, ref, cfg = make_pair(ctx, cfg, 99)
+    monkeypatch.setenv("PBX_GEMV_INT", "0")
+    slow = synth.build(ctx, cfg, 99)
+    monkeypatch.delenv("PBX_GEMV_INT")
+    toks = [int(t) for t in synth.random_tokens(100, 20, cfg["vocab_size"])]
+    worst = 0.0
+    for p, t in enumerate(toks):
+        a, _ = fast.forward([t], p)
+        b, _ = slow.forward([t], p)
+        worst = max(worst, float(np.abs(a - b).max()))
+    r = ref.forward(toks, 0)
+    err = float(np.abs(a - r).max())
+    print(f"  int vs float max-abs {worst:.2e}, vs oracle {err:.2e}")
+    assert worst <= 1e-4
+    assert err <= LOGIT_TOL
+    fast.free()
+    slow.free()
+    ref.close()
+
+
 def test_model_argument_errors(ctx):
     print("[case] model errors", flush=True)
     cfg = tiny(TYPE_Q4_0, TYPE_Q4_0)
