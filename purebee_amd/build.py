@@ -23,6 +23,9 @@ ARCH = "gfx950"
 # Packed-FP32 VALU forms are kept out of every code object.
 HIP_FLAGS = ["-O3", "-std=c++17", f"--offload-arch={ARCH}",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Per-file additions: the GEMM keeps MFMA accumulators in VGPRs, so the
+# per-block scale FMAs read them without v_accvgpr moves.
+KERNEL_FLAGS = {"pbx_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 HOST_FLAGS = ["-O2", "-g", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-Wno-unused-parameter",
               "-D__HIP_PLATFORM_AMD__"]
 
@@ -47,7 +50,8 @@ def build_kernels(verbose=False):
     def one(src):
         out = os.path.join(LIB, os.path.basename(src)[:-4] + ".hsaco")
         tmp = out + ".tmp"
-        _run([HIPCC, "--genco", *HIP_FLAGS, src, "-o", tmp], verbose)
+        extra = KERNEL_FLAGS.get(os.path.basename(src), [])
+        _run([HIPCC, "--genco", *HIP_FLAGS, *extra, src, "-o", tmp], verbose)
         os.replace(tmp, out)
         return out
 

@@ -74,23 +74,32 @@ __device__ __forceinline__ void load_codes(const GemmArgs &a, int n, int b, int 
 }
 
 // The 8 integer codes as an fp16 MFMA operand: q - 8 (Q4_0, low nibbles for
-// g < 2, high for g >= 2) or q (Q8_0).
+// g < 2, high for g >= 2) or q (Q8_0).  One v_perm_b32 builds the fp16 pair
+// [0x64 | byte e, 0x64 | byte e+1] = 1024 + c (exact: fp16 spacing is 1 on
+// [1024, 2048)) from the code bytes and the constant 0x64 bytes, and one
+// packed-fp16 subtract removes 1024 + bias.  Q4_0 nibbles are isolated in
+// their bytes first; Q8_0 int8 codes are made unsigned (q + 128).
 template <int TYPE>
 __device__ __forceinline__ half8 codes_operand(uint2 w, int g) {
-  unsigned x, y;
+  unsigned x = w.x, y = w.y;
   _Float16 bias;
   if constexpr (TYPE == PBX_Q4) {
     const unsigned sh = (g >> 1) * 4;
-    x = (w.x >> sh) & 0x0F0F0F0Fu;
-    y = (w.y >> sh) & 0x0F0F0F0Fu;
+    x = (x >> sh) & 0x0F0F0F0Fu;
+    y = (y >> sh) & 0x0F0F0F0Fu;
     bias = (_Float16)1032.f;  // 1024 + 8
   } else {
-    x = w.x ^ 0x80808080u;  // int8 q -> q + 128
-    y = w.y ^ 0x80808080u;
+    x ^= 0x80808080u;
+    y ^= 0x80808080u;
     bias = (_Float16)1152.f;  // 1024 + 128
   }
-  const half2v p0 = codes_to_half2(x, bias), p1 = codes_to_half2(x >> 16, bias);
-  const half2v p2 = codes_to_half2(y, bias), p3 = codes_to_half2(y >> 16, bias);
+  auto pair = [&](unsigned v, unsigned sel) -> half2v {
+    // selector bytes 0..3 pick v's bytes, 4 picks a 0x64 byte of the constant
+    const unsigned h = __builtin_amdgcn_perm(0x64646464u, v, sel);
+    return __builtin_bit_cast(half2v, h) - half2v{bias, bias};
+  };
+  const half2v p0 = pair(x, 0x04010400u), p1 = pair(x, 0x04030402u);
+  const half2v p2 = pair(y, 0x04010400u), p3 = pair(y, 0x04030402u);
   half8 v;
   v[0] = p0[0]; v[1] = p0[1]; v[2] = p1[0]; v[3] = p1[1];
   v[4] = p2[0]; v[5] = p2[1]; v[6] = p3[0]; v[7] = p3[1];
@@ -202,19 +211,22 @@ GEMM_KERNEL(pbx_gemm_q8_m2_n2, PBX_Q8, 2, 2)
 // workgroup into LDS (double buffered: block b+1 is read from global while
 // block b is multiplied) and read by the two waves that share it; each wave
 // reads its 64 weight rows' codes one block ahead.  LDS rows are padded to
-// 40 halves so the 16 rows of an operand read fall in distinct banks.
+// 48 halves (measured against 32, 36 and 40).
 // Needs X16 / X16lo padded to a multiple of 128 rows.
 // ---------------------------------------------------------------------------
 #define BIG_TM 128
-#define BIG_LDSR 40  // halves per LDS row (32 + 8 padding)
+#define BIG_LDSR 48  // halves per LDS row (32 + 16 padding: fewest bank conflicts measured)
 
-template <int TYPE>
+// WN waves along N: 2 (128 x 128 tile, 256 threads).  A 128 x 256 tile
+// (WN = 4, 512 threads) measured 35% slower at M = 512 and is not built.
+template <int TYPE, int WN>
 __device__ __forceinline__ void gemm_big(const GemmArgs &a) {
+  constexpr int NTH = 128 * WN;  // threads
   __shared__ __attribute__((aligned(16))) _Float16 As[2][2][BIG_TM * BIG_LDSR];  // [buf][hi/lo]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, g = lane >> 4;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int n0 = blockIdx.x * 128 + wn * 64;
+  const int wm = wave / WN, wn = wave % WN;
+  const int n0 = blockIdx.x * (64 * WN) + wn * 64;
   const int mblk = blockIdx.y * BIG_TM;
   const int m0 = wm * 64;  // within the workgroup tile
   const int K = a.B * 32;
@@ -224,30 +236,35 @@ __device__ __forceinline__ void gemm_big(const GemmArgs &a) {
   const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
 
   // global -> LDS staging: 1024 16-byte chunks per block (2 planes x 128
-  // rows x 4 chunks), four per thread: chunk c = tid + 256 i is plane i / 2,
-  // row (c & 511) / 4, 8-half quarter c & 3
+  // rows x 4 chunks), CH = 1024 / NTH per thread: chunk c = tid + NTH i is
+  // plane c / 512, row (c & 511) / 4, 8-half quarter c & 3
+  // Thread tid stages chunks c = tid + NTH * i (i < 1024 / NTH): plane c / 512,
+  // row (c & 511) / 4, quarter c & 3.  With NTH = 256 the four chunks are
+  // (hi, row r), (hi, r + 64), (lo, r), (lo, r + 64); with 512 they are
+  // (hi, r) and (lo, r), r = tid / 4.
+  const int sq = tid & 3, sr = (tid & 511) >> 2;
+  const _Float16 *ghi = a.X16 + (size_t)(mblk + sr) * K + sq * 8;
+  const _Float16 *glo = a.X16lo + (size_t)(mblk + sr) * K + sq * 8;
+  const size_t g64 = (size_t)64 * K;  // 64 rows further down
+  const int lofs = sr * BIG_LDSR + sq * 8, l64 = 64 * BIG_LDSR;
   uint4 st0, st1, st2, st3;
-  const int srow = (tid & 511) >> 2, sq = tid & 3;
-  const int srow2 = ((tid + 256) & 511) >> 2;
-  const _Float16 *gsrc[4] = {a.X16 + (size_t)(mblk + srow) * K + sq * 8,
-                             a.X16 + (size_t)(mblk + srow2) * K + sq * 8,
-                             a.X16lo + (size_t)(mblk + srow) * K + sq * 8,
-                             a.X16lo + (size_t)(mblk + srow2) * K + sq * 8};
-  const int ldst[4] = {srow * BIG_LDSR + sq * 8, srow2 * BIG_LDSR + sq * 8,
-                       srow * BIG_LDSR + sq * 8, srow2 * BIG_LDSR + sq * 8};
 #define BIG_LOAD_A(b)                                                              \
   do {                                                                             \
-    st0 = *reinterpret_cast<const uint4 *>(gsrc[0] + (b) * 32);                    \
-    st1 = *reinterpret_cast<const uint4 *>(gsrc[1] + (b) * 32);                    \
-    st2 = *reinterpret_cast<const uint4 *>(gsrc[2] + (b) * 32);                    \
-    st3 = *reinterpret_cast<const uint4 *>(gsrc[3] + (b) * 32);                    \
+    st0 = *reinterpret_cast<const uint4 *>(ghi + (b) * 32);                        \
+    st2 = *reinterpret_cast<const uint4 *>(glo + (b) * 32);                        \
+    if constexpr (NTH == 256) {                                                    \
+      st1 = *reinterpret_cast<const uint4 *>(ghi + g64 + (b) * 32);                \
+      st3 = *reinterpret_cast<const uint4 *>(glo + g64 + (b) * 32);                \
+    }                                                                              \
   } while (0)
 #define BIG_STORE_A(buf)                                                           \
   do {                                                                             \
-    *reinterpret_cast<uint4 *>(&As[buf][0][ldst[0]]) = st0;                        \
-    *reinterpret_cast<uint4 *>(&As[buf][0][ldst[1]]) = st1;                        \
-    *reinterpret_cast<uint4 *>(&As[buf][1][ldst[2]]) = st2;                        \
-    *reinterpret_cast<uint4 *>(&As[buf][1][ldst[3]]) = st3;                        \
+    *reinterpret_cast<uint4 *>(&As[buf][0][lofs]) = st0;                           \
+    *reinterpret_cast<uint4 *>(&As[buf][1][lofs]) = st2;                           \
+    if constexpr (NTH == 256) {                                                    \
+      *reinterpret_cast<uint4 *>(&As[buf][0][lofs + l64]) = st1;                   \
+      *reinterpret_cast<uint4 *>(&As[buf][1][lofs + l64]) = st3;                   \
+    }                                                                              \
   } while (0)
 
   floatx4 acc[4][4];
@@ -323,8 +340,8 @@ __device__ __forceinline__ void gemm_big(const GemmArgs &a) {
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_big(GemmArgs a) { gemm_big<PBX_Q4>(a); }
-extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q8_big(GemmArgs a) { gemm_big<PBX_Q8>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_big(GemmArgs a) { gemm_big<PBX_Q4, 2>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q8_big(GemmArgs a) { gemm_big<PBX_Q8, 2>(a); }
 
 // Row scaling to fp16: one workgroup per (padded) row.  The scale is
 // 2^(15 - e) with 2^(e-1) <= max|x| < 2^e, so every scaled value is below
