@@ -230,6 +230,7 @@ def run_decode(args, pb, synth):
                 "us_per_launch_in_step": round(dom["us_per_launch"], 3)}
     step_bytes = sum(r["bytes_per_step"] for r in roles.values())
     m_gt_1 = None if args.no_m_gt_1 else run_m_gt_1(ctx, model, cfg, pb, synth)
+    q4_1 = None if args.no_m_gt_1 else run_q4_1(ctx, pb)
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the restated reference CPU path ...")
@@ -262,6 +263,7 @@ def run_decode(args, pb, synth):
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in roles.items()},
         "m_gt_1": m_gt_1,
+        "q4_1_matvec": q4_1,
         "cpu_baseline": cpu,
     }
     model.free()
@@ -345,6 +347,40 @@ def run_m_gt_1(ctx, model, cfg, pb, synth):
         f"{st['drafted']}, {res['speculative']['tok_per_s']} tok/s")
     draft.free()
     model.reset_cache()
+    return res
+
+
+def run_q4_1(ctx, pb):
+    """The Q4_1 matvec (quantizedMatvec type 3) through the plain
+    instruction at the Llama-3.2-1B FFN shapes, beside Q4_0 on the same
+    shapes.  Each timed pass rotates through 32 distinct weights (over 300 MB,
+    more than the last-level cache), so every launch streams its weight from
+    HBM.  Algorithmic bytes per launch: the GGUF blocks (20 B per 32 weights
+    for Q4_1, 18 B for Q4_0) plus the fp32 activation and output vectors."""
+    res = {}
+    rng = np.random.default_rng(41)
+    for name, N, K in (("ffn_gate", 8192, 2048), ("ffn_down", 2048, 8192)):
+        base = pb.synth_normal(4100 + N, N * K, 0, 0.02).reshape(N, K)
+        dx = ctx.alloc(K * 4).upload(rng.normal(0, 1, K).astype(np.float32))
+        dy = ctx.alloc(N * 4)
+        for t, qname, bpb, quant in ((pb.TYPE_Q4_1, "q4_1", 20, pb.quantize_q4_1),
+                                     (pb.TYPE_Q4_0, "q4_0", 18, pb.quantize_q4_0)):
+            ws = []
+            for i in range(32):
+                # distinct weights: roll the columns of one quantised base
+                ws.append(ctx.upload(t, N, K, quant(np.roll(base, 32 * i, axis=1))))
+            ctx.bench_linear(ws, [dx.ptr] * 32, [dy.ptr] * 32, 1, 2)
+            reps = 10
+            us = ctx.bench_linear(ws, [dx.ptr] * 32, [dy.ptr] * 32, 1, reps) / reps / 32 * 1e3
+            b = N * K // 32 * bpb + 4 * (N + K)
+            res[f"{name}_{qname}"] = {"N": N, "K": K, "us_per_launch": round(us, 2),
+                                      "achieved_GBps": round(b / us / 1e3, 1),
+                                      "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                                      "algorithmic_bytes": b}
+            log(f"{qname} matvec {name} {N}x{K}: {us:.2f} us, {b / us / 1e3:.0f} GB/s")
+            for w in ws:
+                w.free()
+        dx.free(), dy.free()
     return res
 
 

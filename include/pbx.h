@@ -46,6 +46,7 @@ extern "C" {
  */
 #define PBX_TYPE_F32     0
 #define PBX_TYPE_Q4_0    2
+#define PBX_TYPE_Q4_1    3
 #define PBX_TYPE_Q8_0    8
 #define PBX_TYPE_Q8_REF  100
 
@@ -73,8 +74,9 @@ int         pbx_device_info(pbx_ctx *ctx, char *name, size_t cap, int *cu_count)
  * the kernels read; the handle stays valid until pbx_weight_free.
  *
  * host/nbytes hold GGUF row-major blocks: N rows of K/32 blocks of
- * 18 B (Q4_0: fp16 d + 16 nibble bytes) or 34 B (Q8_0: fp16 d + 32 int8),
- * gguf.js:36-49 and 239-286; for PBX_TYPE_F32, N*K little-endian floats.
+ * 18 B (Q4_0: fp16 d + 16 nibble bytes), 20 B (Q4_1: fp16 d, fp16 m +
+ * 16 nibble bytes) or 34 B (Q8_0: fp16 d + 32 int8), gguf.js:36-49 and
+ * 239-314; for PBX_TYPE_F32, N*K little-endian floats.
  * K must be a multiple of 32 for every type.
  */
 int pbx_weight_upload(pbx_ctx *ctx, int type, int64_t N, int64_t K,
@@ -125,9 +127,14 @@ int pbx_dequant_dev(pbx_ctx *ctx, const pbx_weight *W, float *dY);
  * along K of each row, the scale stored as fp16 (GGUF Q8_0 layout).
  * Q4_0 with d = absmax/8 stored as fp16 and nibble = clamp(round(x*8/absmax),
  * -8, 7) + 8, GGUF non-interleaved nibble order (gguf.js:259-286).
- * out must hold N*K/32*34 (Q8_0) or N*K/32*18 (Q4_0) bytes. */
+ * Q4_1 with d = (max-min)/15 and m = min stored as fp16 and nibble =
+ * clamp(round((x-m)/d), 0, 15) against the stored values (GGUF Q4_1 layout,
+ * gguf.js:288-314).  The reference reads Q4_1 but has no quantiser for it.
+ * out must hold N*K/32*34 (Q8_0), N*K/32*18 (Q4_0) or N*K/32*20 (Q4_1)
+ * bytes. */
 int pbx_quantize_q8_0(const float *w, int64_t N, int64_t K, uint8_t *out);
 int pbx_quantize_q4_0(const float *w, int64_t N, int64_t K, uint8_t *out);
+int pbx_quantize_q4_1(const float *w, int64_t N, int64_t K, uint8_t *out);
 /* quantize_q8 itself (quantize.js:79-109): flat, f32 scales (Q8_REF). */
 int pbx_quantize_q8_ref(const float *w, int64_t n, int8_t *q, float *scales);
 

@@ -42,18 +42,18 @@ def lib():
         L.pbo_f16_to_f32_wasm.argtypes = [ctypes.c_uint16]
         L.pbo_f64_to_f16.restype = ctypes.c_uint16
         L.pbo_f64_to_f16.argtypes = [ctypes.c_double]
-        for name in ("pbo_dequant_q4_0", "pbo_dequant_q8_0"):
+        for name in ("pbo_dequant_q4_0", "pbo_dequant_q8_0", "pbo_dequant_q4_1"):
             getattr(L, name).argtypes = [_u8p, _i64, _f32p]
         L.pbo_dequant_q8_ref.argtypes = [_i8p, _f32p, _i64, _f32p]
         for name in ("pbo_q4_0_matvec_js", "pbo_q4_0_matvec_wasm", "pbo_q8_0_matvec_f64",
-                     "pbo_cpu_q4_0_matvec"):
+                     "pbo_cpu_q4_0_matvec", "pbo_q4_1_matvec_js", "pbo_q4_1_matvec_wasm"):
             getattr(L, name).argtypes = [_f32p, _u8p, _i64, _i64, _f32p]
         for name in ("pbo_f32_matvec_f64", "pbo_batch_dot_wasm"):
             getattr(L, name).argtypes = [_f32p, _f32p, _i64, _i64, _f32p]
         L.pbo_matmul_f32_axpy.argtypes = [_f32p, _i64, _i64, _f32p, _i64, ctypes.c_void_p, _f32p]
         L.pbo_matmul_q8_ref.argtypes = [_f32p, _i64, _i64, _i8p, _f32p, _i64, ctypes.c_void_p, _f32p]
         L.pbo_quantize_q8_ref.argtypes = [_f32p, _i64, _i8p, _f32p]
-        for name in ("pbo_quantize_q8_0", "pbo_quantize_q4_0"):
+        for name in ("pbo_quantize_q8_0", "pbo_quantize_q4_0", "pbo_quantize_q4_1"):
             getattr(L, name).argtypes = [_f32p, _i64, _i64, _u8p]
         L.pbo_synth_normal.argtypes = [ctypes.c_uint64, _i64, ctypes.c_double, ctypes.c_double, _f32p]
         L.pbo_pool_create.restype = ctypes.c_void_p
@@ -91,12 +91,18 @@ def f64_to_f16(v):
 
 
 def block_bytes(ggml_type):
-    return {2: 18, 8: 34}[ggml_type]
+    return {2: 18, 3: 20, 8: 34}[ggml_type]
 
 
 def dequant_q4_0(raw, n):
     out = np.empty(n, np.float32)
     lib().pbo_dequant_q4_0(_c(raw, np.uint8), n, out)
+    return out
+
+
+def dequant_q4_1(raw, n):
+    out = np.empty(n, np.float32)
+    lib().pbo_dequant_q4_1(_c(raw, np.uint8), n, out)
     return out
 
 
@@ -129,6 +135,16 @@ def q4_0_matvec_wasm(x, raw, N, K):
     return _mv(lib().pbo_q4_0_matvec_wasm, x, raw, N, K)
 
 
+def q4_1_matvec_js(x, raw, N, K):
+    """llama-streaming.js:115-151 (double accumulation)."""
+    return _mv(lib().pbo_q4_1_matvec_js, x, raw, N, K)
+
+
+def q4_1_matvec_wasm(x, raw, N, K):
+    """wasm-q4.js:275-435 replayed in f32, lane by lane."""
+    return _mv(lib().pbo_q4_1_matvec_wasm, x, raw, N, K)
+
+
 def q4_0_matvec_cpu_sse(x, raw, N, K):
     """The SSE restatement used as the timed CPU baseline."""
     return _mv(lib().pbo_cpu_q4_0_matvec, x, raw, N, K)
@@ -155,9 +171,12 @@ def batch_dot_wasm(x, W):
 
 
 def matvec(ggml_type, x, raw, N, K):
-    """Oracle for one quantized matvec on GGUF bytes (type 2 = Q4_0, 8 = Q8_0)."""
+    """Oracle for one quantized matvec on GGUF bytes (type 2 = Q4_0,
+    3 = Q4_1, 8 = Q8_0)."""
     if ggml_type == 2:
         return q4_0_matvec_js(x, raw, N, K)
+    if ggml_type == 3:
+        return q4_1_matvec_js(x, raw, N, K)
     if ggml_type == 8:
         return q8_0_matvec(x, raw, N, K)
     if ggml_type == 0:
@@ -210,6 +229,14 @@ def quantize_q4_0(w):
     N, K = w.shape
     out = np.empty(N * K // 32 * 18, np.uint8)
     lib().pbo_quantize_q4_0(w, N, K, out)
+    return out
+
+
+def quantize_q4_1(w):
+    w = _c(w, np.float32)
+    N, K = w.shape
+    out = np.empty(N * K // 32 * 20, np.uint8)
+    lib().pbo_quantize_q4_1(w, N, K, out)
     return out
 
 

@@ -16,6 +16,9 @@
  * Parity pins (see tests/test_oracle.py):
  *   - f16 conversions: all 65,536 bit patterns against numpy float16.
  *   - Q4_0 matvec: the reference's own known-answer test, wasm-q4.js:673-704.
+ *   - Q4_1 matvec: no reference KAT; pinned by the Q4_0 KAT through the
+ *     identity Q4_1(d, m = -8d) == Q4_0(d), by the dequantised product, and
+ *     by closed forms on constant blocks.
  *   - f32 matmul: the reference KATs wasm-simd.js:367-385 and main.js:65-74.
  *   - dequant: closed forms (gguf.js:239-286) on every byte value.
  *   - quantizers: ECMAScript Math.round tie cases and invariants.
@@ -133,6 +136,27 @@ void pbo_dequant_q8_0(const uint8_t *raw, int64_t n, float *out) {
   }
 }
 
+/* loadTensorData Q4_1 branch, gguf.js:288-314: per 20-byte block, fp16 d,
+ * fp16 m, 16 bytes; element j = lo(byte j) * d + m, element j+16 =
+ * hi(byte j) * d + m, each a double expression rounded once to f32. */
+void pbo_dequant_q4_1(const uint8_t *raw, int64_t n, float *out) {
+  int64_t o = 0;
+  const uint8_t *p = raw;
+  while (o < n) {
+    const double d = pbo_f16_to_f32(rd16(p));
+    const double m = pbo_f16_to_f32(rd16(p + 2));
+    const int64_t remaining = (n - o) < 32 ? (n - o) : 32;
+    const int64_t half = remaining < 16 ? remaining : 16;
+    for (int64_t j = 0; j < half; ++j) {
+      const int byte = p[4 + j];
+      out[o + j] = (float)((byte & 0x0f) * d + m);
+      if (j + 16 < remaining) out[o + j + 16] = (float)((byte >> 4) * d + m);
+    }
+    o += remaining;
+    p += 20;
+  }
+}
+
 /* dequantize_q8, quantize.js:170-181: out[i] = q[i] * scales[floor(i/32)]. */
 void pbo_dequant_q8_ref(const int8_t *q, const float *scales, int64_t n, float *out) {
   for (int64_t i = 0; i < n; ++i) out[i] = (float)((double)q[i] * (double)scales[i / 32]);
@@ -189,6 +213,69 @@ void pbo_q4_0_matvec_wasm(const float *x, const uint8_t *raw, int64_t N, int64_t
         }
       for (int i = 0; i < 4; ++i) {
         const float t = ba[i] * scale;
+        acc[i] = t + acc[i];
+      }
+    }
+    const float t0 = acc[0] + acc[2], t1 = acc[1] + acc[3];
+    out[n] = t1 + t0;
+  }
+}
+
+/* q4_1_matvec JS version, llama-streaming.js:115-151: per block, in double,
+ * nibbleSum += x[j]*lo(j) then += x[j+16]*hi(j); xBlockSum += (x[j] +
+ * x[j+16]); sum += delta*nibbleSum + min*xBlockSum; f32 store. */
+void pbo_q4_1_matvec_js(const float *x, const uint8_t *raw, int64_t N, int64_t K, float *out) {
+  const int64_t bpr = K >> 5, row_bytes = bpr * 20;
+  for (int64_t n = 0; n < N; ++n) {
+    double sum = 0;
+    const uint8_t *row = raw + n * row_bytes;
+    for (int64_t b = 0; b < bpr; ++b) {
+      const uint8_t *blk = row + b * 20;
+      const double delta = pbo_f16_to_f32(rd16(blk));
+      const double mn = pbo_f16_to_f32(rd16(blk + 2));
+      const float *xb = x + b * 32;
+      double nib_sum = 0, x_sum = 0;
+      for (int j = 0; j < 16; ++j) {
+        const int byte = blk[4 + j];
+        nib_sum += (double)xb[j] * (byte & 0x0f);
+        nib_sum += (double)xb[j + 16] * (byte >> 4);
+        x_sum += (double)xb[j] + (double)xb[j + 16];
+      }
+      sum += delta * nib_sum + mn * x_sum;
+    }
+    out[n] = (float)sum;
+  }
+}
+
+/* q4_1_matvec WebAssembly kernel, wasm-q4.js:275-435, replayed lane by lane
+ * in f32: for byte groups g = 0,4,8,12 lane i adds lo(g+i) * x[g+i] to its
+ * nibble accumulator and x[g+i] to its x accumulator, then the same for
+ * hi(g+i) and x[g+16+i]; per block acc += (nib*delta + xs*min); horizontal
+ * sum (a1+a3) + (a0+a2).  delta and min use the WASM f16 decode. */
+void pbo_q4_1_matvec_wasm(const float *x, const uint8_t *raw, int64_t N, int64_t K, float *out) {
+  const int64_t bpr = K >> 5, row_bytes = bpr * 20;
+  for (int64_t n = 0; n < N; ++n) {
+    float acc[4] = {0, 0, 0, 0};
+    const uint8_t *row = raw + n * row_bytes;
+    for (int64_t b = 0; b < bpr; ++b) {
+      const uint8_t *blk = row + b * 20;
+      const float delta = pbo_f16_to_f32_wasm(rd16(blk));
+      const float mn = pbo_f16_to_f32_wasm(rd16(blk + 2));
+      const float *xb = x + b * 32;
+      float na[4] = {0, 0, 0, 0}, xa[4] = {0, 0, 0, 0};
+      for (int g = 0; g < 16; g += 4)
+        for (int i = 0; i < 4; ++i) {
+          const int byte = blk[4 + g + i];
+          float t = (float)(byte & 0x0f) * xb[g + i];
+          na[i] = t + na[i];
+          xa[i] = xa[i] + xb[g + i];
+          t = (float)(byte >> 4) * xb[g + 16 + i];
+          na[i] = t + na[i];
+          xa[i] = xa[i] + xb[g + 16 + i];
+        }
+      for (int i = 0; i < 4; ++i) {
+        const float t1 = na[i] * delta, t2 = xa[i] * mn;
+        const float t = t1 + t2;
         acc[i] = t + acc[i];
       }
     }
@@ -358,6 +445,38 @@ void pbo_quantize_q4_0(const float *w, int64_t N, int64_t K, uint8_t *raw) {
       nib[i] = (int)r + 8;
     }
     for (int j = 0; j < 16; ++j) o[2 + j] = (uint8_t)(nib[j] | (nib[j + 16] << 4));
+  }
+}
+
+/* Q4_1 of synthetic workloads (no producer in the reference: parity
+ * unpinned, invariants only): per block d = (max - min)/15 and m = min, both
+ * stored as fp16; nibble = clamp(Math.round((x - m16) / d16), 0, 15) with
+ * the stored values, so the rounding sees the scale the reader will use. */
+void pbo_quantize_q4_1(const float *w, int64_t N, int64_t K, uint8_t *raw) {
+  const int64_t nb = N * (K / 32);
+  for (int64_t b = 0; b < nb; ++b) {
+    const float *x = w + b * 32;
+    uint8_t *o = raw + b * 20;
+    double lo = x[0], hi = x[0];
+    for (int i = 1; i < 32; ++i) {
+      if (x[i] < lo) lo = x[i];
+      if (x[i] > hi) hi = x[i];
+    }
+    const uint16_t hd = pbo_f64_to_f16((hi - lo) / 15);
+    const uint16_t hm = pbo_f64_to_f16(lo);
+    o[0] = (uint8_t)hd;
+    o[1] = (uint8_t)(hd >> 8);
+    o[2] = (uint8_t)hm;
+    o[3] = (uint8_t)(hm >> 8);
+    const double d = pbo_f16_to_f32(hd), m = pbo_f16_to_f32(hm);
+    int nib[32];
+    for (int i = 0; i < 32; ++i) {
+      double r = d > 0 ? js_round(((double)x[i] - m) / d) : 0;
+      if (r < 0) r = 0;
+      if (r > 15) r = 15;
+      nib[i] = (int)r;
+    }
+    for (int j = 0; j < 16; ++j) o[4 + j] = (uint8_t)(nib[j] | (nib[j + 16] << 4));
   }
 }
 

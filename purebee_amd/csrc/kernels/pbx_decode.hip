@@ -51,6 +51,10 @@ DK_MODES_SMALL(PBX_Q4, q4, 8)
 DK_MODES_WIDE(PBX_Q8, q8, 4)
 DK_MODES_WIDE(PBX_Q8, q8, 8)
 DK_MODES_SMALL(PBX_Q8, q8, 4)
+DK_MODES_WIDE(PBX_Q41, q41, 4)
+DK_MODES_WIDE(PBX_Q41, q41, 8)
+DK_MODES_WIDE(PBX_Q41, q41, 16)
+DK_MODES_SMALL(PBX_Q41, q41, 8)
 // Integer-limb kernels for the gate|up GEMV (RMSNorm + SwiGLU pair), the
 // largest matrix of a layer; for the smaller GEMVs the activation prologue
 // costs more than the dot products save (measured).
@@ -460,15 +464,16 @@ pbx_attention_combine(const float *part, float *out, int head_dim, int S) {
 
 // ---------------------------------------------------------------------------
 // Embedding row of the current token (llama.js:216-225), dequantised exactly
-// from the resident token_embd planes (gguf.js:239-286) or copied (F32).
+// from the resident token_embd planes (gguf.js:239-314) or copied (F32).
 // ---------------------------------------------------------------------------
 struct EmbedArgs {
   const uint8_t *qs;
   const uint16_t *dsc;
   float *x;
   const int *state;  // state[1] = token
-  int type;          // PBX_Q4 / PBX_Q8 / PBX_F32
+  int type;          // PBX_Q4 / PBX_Q8 / PBX_F32 / PBX_Q41
   int dim, vocab;
+  const uint16_t *msc;  // Q4_1 minima
 };
 
 extern "C" __global__ void __launch_bounds__(256) pbx_embed(EmbedArgs a) {
@@ -476,21 +481,7 @@ extern "C" __global__ void __launch_bounds__(256) pbx_embed(EmbedArgs a) {
   if (i >= a.dim) return;
   int tok = a.state[1];
   if (tok < 0 || tok >= a.vocab) tok = 0;  // never read outside the table
-  const int B = a.dim / 32, b = i / 32, j = i % 32;
-  float val;
-  if (a.type == PBX_F32) {
-    val = reinterpret_cast<const float *>(a.qs)[(size_t)tok * a.dim + i];
-  } else {
-    const float d = f16_bits_to_f32(a.dsc[dsc_index(tok, b, B)]);
-    if (a.type == PBX_Q4) {
-      const unsigned byte = a.qs[((size_t)tok * B + b) * 16 + (j & 15)];
-      const int nib = j < 16 ? (int)(byte & 15u) : (int)(byte >> 4);
-      val = (float)(nib - 8) * d;
-    } else {
-      val = (float)(int8_t)a.qs[((size_t)tok * B + b) * 32 + j] * d;
-    }
-  }
-  a.x[i] = val;
+  a.x[i] = row_value(a.qs, a.dsc, a.msc, a.type, tok, i, a.dim);
 }
 
 // ---------------------------------------------------------------------------

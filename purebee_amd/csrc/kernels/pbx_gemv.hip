@@ -12,10 +12,13 @@
 //                                           contiguous: one 8-B load serves
 //                                           a 4-row group)
 //   Q8_0 : qs plane  [Npad][B][32] int8, d plane as Q4_0
+//   Q4_1 : qs plane as Q4_0; d plane as Q4_0 and an m plane of the same
+//          layout (fp16 minima), value = nibble * d + m
 //   F32  : plane     [Npad][K] float
 // The GGUF block formats these come from are gguf.js:36-49 (sizes) and
 // gguf.js:239-286 (element order: Q4_0 byte j holds element j in its low
-// nibble and element j+16 in its high nibble; value = (nibble - 8) * d).
+// nibble and element j+16 in its high nibble; value = (nibble - 8) * d;
+// Q4_1 is gguf.js:288-314: 20-byte blocks, fp16 d, fp16 m, the same nibbles).
 
 #include "pbx_gemv_impl.h"
 
@@ -25,23 +28,27 @@
 using namespace pbx;
 
 __device__ __forceinline__ GemvArgs plain_args(const uint8_t *qs, const uint16_t *dsc,
-                                               const float *X, const float *bias, float *Y,
-                                               int N, int B) {
+                                               const uint16_t *msc, const float *X,
+                                               const float *bias, float *Y, int N, int B) {
   GemvArgs a;
   a.qs = qs; a.dsc = dsc; a.X = X; a.X2 = nullptr; a.normw = nullptr;
   a.bias = bias; a.Y = Y; a.partials = nullptr; a.N = N; a.B = B; a.eps = 0.f;
+  a.msc = msc;
   return a;
 }
 
 #define PBX_WIDE(NAME, TYPE, R)                                               \
   extern "C" __global__ void __launch_bounds__(512)                           \
-  NAME(const uint8_t *qs, const uint16_t *dsc, const float *X,                \
-       const float *bias, float *Y, int N, int B) {                           \
-    gemv_wide<TYPE, R, PRO_NONE, EPI_STORE>(plain_args(qs, dsc, X, bias, Y, N, B)); \
+  NAME(const uint8_t *qs, const uint16_t *dsc, const uint16_t *msc,          \
+       const float *X, const float *bias, float *Y, int N, int B) {           \
+    gemv_wide<TYPE, R, PRO_NONE, EPI_STORE>(plain_args(qs, dsc, msc, X, bias, Y, N, B)); \
   }
 PBX_WIDE(pbx_gemv_q4_0_wide_r4, PBX_Q4, 4)
 PBX_WIDE(pbx_gemv_q4_0_wide_r8, PBX_Q4, 8)
 PBX_WIDE(pbx_gemv_q4_0_wide_r16, PBX_Q4, 16)
+PBX_WIDE(pbx_gemv_q4_1_wide_r4, PBX_Q41, 4)
+PBX_WIDE(pbx_gemv_q4_1_wide_r8, PBX_Q41, 8)
+PBX_WIDE(pbx_gemv_q4_1_wide_r16, PBX_Q41, 16)
 PBX_WIDE(pbx_gemv_q8_0_wide_r4, PBX_Q8, 4)
 PBX_WIDE(pbx_gemv_q8_0_wide_r8, PBX_Q8, 8)
 PBX_WIDE(pbx_gemv_f32_wide_r2, PBX_F32, 2)
@@ -49,11 +56,12 @@ PBX_WIDE(pbx_gemv_f32_wide_r4, PBX_F32, 4)
 
 #define PBX_SMALL(NAME, TYPE, P)                                              \
   extern "C" __global__ void __launch_bounds__(256)                           \
-  NAME(const uint8_t *qs, const uint16_t *dsc, const float *X,                \
-       const float *bias, float *Y, int N, int B) {                           \
-    gemv_small<TYPE, P, PRO_NONE, EPI_STORE>(plain_args(qs, dsc, X, bias, Y, N, B)); \
+  NAME(const uint8_t *qs, const uint16_t *dsc, const uint16_t *msc,          \
+       const float *X, const float *bias, float *Y, int N, int B) {           \
+    gemv_small<TYPE, P, PRO_NONE, EPI_STORE>(plain_args(qs, dsc, msc, X, bias, Y, N, B)); \
   }
 PBX_SMALL(pbx_gemv_q4_0_small, PBX_Q4, 8)
+PBX_SMALL(pbx_gemv_q4_1_small, PBX_Q41, 8)
 PBX_SMALL(pbx_gemv_q8_0_small, PBX_Q8, 4)
 PBX_SMALL(pbx_gemv_f32_small, PBX_F32, 2)
 
@@ -137,6 +145,24 @@ pbx_repack_q8_0(const uint16_t *raw, uint8_t *qs, uint16_t *dsc, int64_t row0,
   dsc[dsc_index((int)n, b, B)] = src[0];
 }
 
+// Q4_1: 20-byte blocks (fp16 d, fp16 m, 16 nibble bytes) are 4-byte aligned
+// in the staged rows, so each block is five 32-bit loads.
+extern "C" __global__ void __launch_bounds__(256)
+pbx_repack_q4_1(const uint32_t *raw, uint8_t *qs, uint16_t *dsc, uint16_t *msc, int64_t row0,
+                int64_t rows, int B) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * B) return;
+  const int64_t n = row0 + i / B;
+  const int b = (int)(i % B);
+  const uint32_t *src = raw + i * 5;
+  const uint32_t dm = src[0];
+  *reinterpret_cast<uint4 *>(qs + ((size_t)n * B + b) * 16) =
+      make_uint4(src[1], src[2], src[3], src[4]);
+  const size_t di = dsc_index((int)n, b, B);
+  dsc[di] = (uint16_t)(dm & 0xFFFFu);
+  msc[di] = (uint16_t)(dm >> 16);
+}
+
 // ---------------------------------------------------------------------------
 // Exact dequantisation to fp32 row-major [N,K] (gguf.js:239-286): the
 // product of an fp16 scale and a small integer is exact in fp32.
@@ -173,6 +199,32 @@ pbx_dequant_q8_0(const uint8_t *qs, const uint16_t *dsc, float *out, int N, int 
   for (int j = 0; j < 8; ++j)
     dst[j] = make_float4((float)q[4 * j] * d, (float)q[4 * j + 1] * d,
                          (float)q[4 * j + 2] * d, (float)q[4 * j + 3] * d);
+}
+
+// Q4_1 (gguf.js:288-314): nibble * d + m.  nibble * d is exact in fp32, so
+// the fused multiply-add rounds once, as the reference's double expression
+// rounds once into its Float32Array.
+extern "C" __global__ void __launch_bounds__(256)
+pbx_dequant_q4_1(const uint8_t *qs, const uint16_t *dsc, const uint16_t *msc, float *out, int N,
+                 int B) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)N * B) return;
+  const int n = (int)(i / B), b = (int)(i % B);
+  const uint4 q = *reinterpret_cast<const uint4 *>(qs + i * 16);
+  const size_t di = dsc_index(n, b, B);
+  const float d = f16_bits_to_f32(dsc[di]);
+  const float m = f16_bits_to_f32(msc[di]);
+  const unsigned w[4] = {q.x, q.y, q.z, q.w};
+  float v[32];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const unsigned byte = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+    v[j] = fmaf((float)(byte & 0xFu), d, m);
+    v[j + 16] = fmaf((float)(byte >> 4), d, m);
+  }
+  float4 *dst = reinterpret_cast<float4 *>(out + i * 32);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
 }
 
 // dequantize_q8 (quantize.js:170-181): out[i] = q[i] * scales[i/32].

@@ -22,6 +22,7 @@
 #define PBX_Q4 0
 #define PBX_Q8 1
 #define PBX_F32 2
+#define PBX_Q41 3
 
 #define PRO_NONE 0
 #define PRO_RMSNORM 1
@@ -46,6 +47,7 @@ struct GemvArgs {
   uint64_t *partials;   // EPI_ARGMAX: one key per tile
   int N, B;
   float eps;
+  const uint16_t *msc;  // fp16 min plane (Q4_1), same layout as dsc
 };
 
 namespace pbx {
@@ -130,6 +132,7 @@ template <int TYPE> struct BlockTraits;
 template <> struct BlockTraits<PBX_Q4> { static constexpr int QB = 16; static constexpr float OFF = 8.f; };
 template <> struct BlockTraits<PBX_Q8> { static constexpr int QB = 32; static constexpr float OFF = 128.f; };
 template <> struct BlockTraits<PBX_F32> { static constexpr int QB = 128; static constexpr float OFF = 0.f; };
+template <> struct BlockTraits<PBX_Q41> { static constexpr int QB = 16; static constexpr float OFF = 0.f; };
 
 __device__ __forceinline__ void load_block(const float *__restrict__ p, bool valid,
                                            float (&v)[32]) {
@@ -145,6 +148,22 @@ __device__ __forceinline__ void load_block(const float *__restrict__ p, bool val
 #pragma unroll
     for (int i = 0; i < 32; ++i) v[i] = 0.f;
   }
+}
+
+// Element i of row `tok` of a resident [rows][dim] weight, dequantised
+// exactly as gguf.js:239-314 (Q8_0, Q4_0, Q4_1) or read (F32).
+__device__ __forceinline__ float row_value(const uint8_t *qs, const uint16_t *dsc,
+                                          const uint16_t *msc, int type, int tok, int i,
+                                          int dim) {
+  if (type == PBX_F32) return reinterpret_cast<const float *>(qs)[(size_t)tok * dim + i];
+  const int B = dim / 32, b = i / 32, j = i % 32;
+  const size_t di = dsc_index(tok, b, B);
+  const float d = f16_bits_to_f32(dsc[di]);
+  if (type == PBX_Q8) return (float)(int8_t)qs[((size_t)tok * B + b) * 32 + j] * d;
+  const unsigned byte = qs[((size_t)tok * B + b) * 16 + (j & 15)];
+  const int nib = j < 16 ? (int)(byte & 15u) : (int)(byte >> 4);
+  if (type == PBX_Q41) return fmaf((float)nib, d, f16_bits_to_f32(msc[di]));
+  return (float)(nib - 8) * d;
 }
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
@@ -204,15 +223,46 @@ __device__ __forceinline__ void apply_rmsnorm(const GemvArgs &a, float ss, int K
   }
 }
 
+// One block-row term.  corr = OFF * sum(x) removes the code offset (Q4_0,
+// Q8_0); Q4_1 (gguf.js:288-314: value = nibble * d + m) instead adds
+// m * sum(x) with corr = sum(x), the split of llama-streaming.js:138-145.
 template <int TYPE>
 __device__ __forceinline__ float block_term(const uint4 (&q)[BlockTraits<TYPE>::QB / 16],
-                                            const float (&xr)[32], float corr, float d) {
+                                            const float (&xr)[32], float corr, float d,
+                                            float mn) {
   if constexpr (TYPE == PBX_Q4) {
     return (dot_q4(q[0], xr) - corr) * d;
+  } else if constexpr (TYPE == PBX_Q41) {
+    return fmaf(dot_q4(q[0], xr), d, mn * corr);
   } else if constexpr (TYPE == PBX_Q8) {
     return (dot_q8(q[0], q[1], xr) - corr) * d;
   } else {
     return dot_f32(q, xr);
+  }
+}
+
+// fp16 scales (or Q4_1 minima) of tile rows 0..R) at block b.  SEG is the
+// number of rows of the tile that are consecutive in the plane (R, or R/2
+// for paired gate/up tiles); 4-row groups are one 8-byte load.
+template <int R, int SEG, typename RowFn>
+__device__ __forceinline__ void load_scales(const uint16_t *plane, RowFn tile_row, int b, int B,
+                                            bool valid, float (&out)[R]) {
+  if constexpr (SEG >= 4) {
+#pragma unroll
+    for (int g = 0; g < R / 4; ++g) {
+      const int rg = tile_row(g * 4);
+      const uint2 dv = valid ? *reinterpret_cast<const uint2 *>(plane + dsc_index(rg, b, B))
+                             : make_uint2(0u, 0u);
+      out[g * 4 + 0] = f16_bits_to_f32(dv.x);
+      out[g * 4 + 1] = f16_bits_to_f32(dv.x >> 16);
+      out[g * 4 + 2] = f16_bits_to_f32(dv.y);
+      out[g * 4 + 3] = f16_bits_to_f32(dv.y >> 16);
+    }
+  } else {
+    // segments of 1 or 2 rows inside one 4-row group
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      out[i] = valid ? f16_bits_to_f32(plane[dsc_index(tile_row(i), b, B)]) : 0.f;
   }
 }
 
@@ -301,28 +351,11 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
     for (int v = 0; v < NV; ++v)
       q[i][v] = valid ? ld_stream(src + v * 16) : make_uint4(0u, 0u, 0u, 0u);
   }
-  float dsf[R];
+  float dsf[R], msf[R];
   if constexpr (TYPE != PBX_F32) {
     constexpr int SEG = PAIR ? R / 2 : R;  // rows contiguous in the scale plane
-    if constexpr (SEG >= 4) {
-#pragma unroll
-      for (int g = 0; g < R / 4; ++g) {
-        const int rg = tile_row(g * 4);
-        const uint2 dv = valid ? *reinterpret_cast<const uint2 *>(a.dsc + dsc_index(rg, b, B))
-                               : make_uint2(0u, 0u);
-        dsf[g * 4 + 0] = f16_bits_to_f32(dv.x);
-        dsf[g * 4 + 1] = f16_bits_to_f32(dv.x >> 16);
-        dsf[g * 4 + 2] = f16_bits_to_f32(dv.y);
-        dsf[g * 4 + 3] = f16_bits_to_f32(dv.y >> 16);
-      }
-    } else {
-      // segments of 1 or 2 rows inside one 4-row group
-#pragma unroll
-      for (int i = 0; i < R; ++i) {
-        const int rw = tile_row(i);
-        dsf[i] = valid ? f16_bits_to_f32(a.dsc[dsc_index(rw, b, B)]) : 0.f;
-      }
-    }
+    load_scales<R, SEG>(a.dsc, tile_row, b, B, valid, dsf);
+    if constexpr (TYPE == PBX_Q41) load_scales<R, SEG>(a.msc, tile_row, b, B, valid, msf);
   } else {
 #pragma unroll
     for (int i = 0; i < R; ++i) dsf[i] = 1.f;
@@ -348,11 +381,12 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) xs += xr[i];
   }
-  const float corr = BlockTraits<TYPE>::OFF * xs;
+  const float corr = TYPE == PBX_Q41 ? xs : BlockTraits<TYPE>::OFF * xs;
 
   float acc[R];
 #pragma unroll
-  for (int i = 0; i < R; ++i) acc[i] = block_term<TYPE>(q[i], xr, corr, dsf[i]);
+  for (int i = 0; i < R; ++i)
+    acc[i] = block_term<TYPE>(q[i], xr, corr, dsf[i], TYPE == PBX_Q41 ? msf[i] : 0.f);
 
   const float tot = wave_transpose_reduce<R>(acc, lane);
   const int row = lane / lanes_per_row;
@@ -446,7 +480,7 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
     if (lane < T && r0 + lane < N) res = y[r0 + lane];
 
   uint4 q[P][NV];
-  float d[P];
+  float d[P], mn[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int rw = tile_row(p * rpw + rs);
@@ -456,8 +490,11 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
     for (int v = 0; v < NV; ++v)
       q[p][v] = ok ? ld_stream(src + v * 16) : make_uint4(0u, 0u, 0u, 0u);
     d[p] = 1.f;
+    mn[p] = 0.f;
     if constexpr (TYPE != PBX_F32)
       d[p] = ok ? f16_bits_to_f32(a.dsc[dsc_index(rw, b, B)]) : 0.f;
+    if constexpr (TYPE == PBX_Q41)
+      mn[p] = ok ? f16_bits_to_f32(a.msc[dsc_index(rw, b, B)]) : 0.f;
   }
 
   float xr[32];
@@ -476,12 +513,12 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) xs += xr[i];
   }
-  const float corr = BlockTraits<TYPE>::OFF * xs;
+  const float corr = TYPE == PBX_Q41 ? xs : BlockTraits<TYPE>::OFF * xs;
 
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const bool ok = active && row_ok(p * rpw + rs);
-    part[wave][p][lane] = ok ? block_term<TYPE>(q[p], xr, corr, d[p]) : 0.f;
+    part[wave][p][lane] = ok ? block_term<TYPE>(q[p], xr, corr, d[p], mn[p]) : 0.f;
   }
   __syncthreads();
   if constexpr (PAIR) {

@@ -31,27 +31,14 @@ __device__ __forceinline__ float block_reduce256(float v, bool is_max, float *sc
 
 // Embedding rows (llama.js:216-225): x[t] = dequantised row tokens[t].
 extern "C" __global__ void __launch_bounds__(256)
-pbx_embed_rows(const uint8_t *qs, const uint16_t *dsc, const int *tokens, float *x, int type,
-               int dim, int vocab) {
+pbx_embed_rows(const uint8_t *qs, const uint16_t *dsc, const uint16_t *msc, const int *tokens,
+               float *x, int type, int dim, int vocab) {
   const int t = blockIdx.y;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= dim) return;
   int tok = tokens[t];
   if (tok < 0 || tok >= vocab) tok = 0;
-  const int B = dim / 32, b = i / 32, j = i % 32;
-  float v;
-  if (type == PBX_F32) {
-    v = reinterpret_cast<const float *>(qs)[(size_t)tok * dim + i];
-  } else {
-    const float d = f16_bits_to_f32(dsc[dsc_index(tok, b, B)]);
-    if (type == PBX_Q4) {
-      const unsigned byte = qs[((size_t)tok * B + b) * 16 + (j & 15)];
-      v = (float)((int)(j < 16 ? (byte & 15u) : (byte >> 4)) - 8) * d;
-    } else {
-      v = (float)(int8_t)qs[((size_t)tok * B + b) * 32 + j] * d;
-    }
-  }
-  x[(size_t)t * dim + i] = v;
+  x[(size_t)t * dim + i] = row_value(qs, dsc, msc, type, tok, i, dim);
 }
 
 // RMSNorm of rows (engine.js:429-449): out[t] = x[t] * (1/rms) * w.

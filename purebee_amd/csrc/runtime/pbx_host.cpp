@@ -56,6 +56,14 @@ inline uint64_t splitmix64(uint64_t x) {
   return x ^ (x >> 31);
 }
 
+// binary16 bits -> double (finite values only; the quantisers never store
+// inf or NaN for finite inputs below 65504).
+double f16_bits_to_f64(uint16_t h) {
+  const int e = (h >> 10) & 0x1f, f = h & 0x3ff;
+  const double v = e == 0 ? ldexp((double)f, -24) : ldexp(1024.0 + f, e - 25);
+  return (h & 0x8000) ? -v : v;
+}
+
 }  // namespace
 
 extern "C" int pbx_quantize_q8_0(const float *w, int64_t N, int64_t K, uint8_t *out) {
@@ -109,6 +117,37 @@ extern "C" int pbx_quantize_q4_0(const float *w, int64_t N, int64_t K, uint8_t *
       for (int i = 0; i < 32; ++i) q[i] = 8;
     }
     for (int j = 0; j < 16; ++j) dst[2 + j] = (uint8_t)((q[j] & 0xF) | ((q[j + 16] & 0xF) << 4));
+  }
+  return PBX_OK;
+}
+
+extern "C" int pbx_quantize_q4_1(const float *w, int64_t N, int64_t K, uint8_t *out) {
+  if (!w || !out || N <= 0 || K <= 0 || K % 32 != 0)
+    return pbx_fail(nullptr, PBX_EINVAL, "pbx_quantize_q4_1: bad arguments (N=%lld K=%lld)",
+                    (long long)N, (long long)K);
+  const int64_t blocks = N * (K / 32);
+#pragma omp parallel for schedule(static)
+  for (int64_t blk = 0; blk < blocks; ++blk) {
+    const float *x = w + blk * 32;
+    uint8_t *dst = out + blk * 20;
+    double lo = x[0], hi = x[0];
+    for (int i = 1; i < 32; ++i) {
+      lo = std::min(lo, (double)x[i]);
+      hi = std::max(hi, (double)x[i]);
+    }
+    const uint16_t hd = f64_to_f16_bits((hi - lo) / 15.0);
+    const uint16_t hm = f64_to_f16_bits(lo);
+    dst[0] = (uint8_t)(hd & 0xFF);
+    dst[1] = (uint8_t)(hd >> 8);
+    dst[2] = (uint8_t)(hm & 0xFF);
+    dst[3] = (uint8_t)(hm >> 8);
+    const double d = f16_bits_to_f64(hd), m = f16_bits_to_f64(hm);
+    int q[32];
+    for (int i = 0; i < 32; ++i) {
+      const double r = d > 0 ? js_round(((double)x[i] - m) / d) : 0.0;
+      q[i] = (int)std::min(15.0, std::max(0.0, r));
+    }
+    for (int j = 0; j < 16; ++j) dst[4 + j] = (uint8_t)(q[j] | (q[j + 16] << 4));
   }
   return PBX_OK;
 }

@@ -14,6 +14,12 @@
 #define PBX_KERNEL_LIST(X)                                   \
   X(PBX_K_REPACK_Q4_0, "pbx_repack_q4_0")                    \
   X(PBX_K_REPACK_Q8_0, "pbx_repack_q8_0")                    \
+  X(PBX_K_REPACK_Q4_1, "pbx_repack_q4_1")                    \
+  X(PBX_K_DEQUANT_Q4_1, "pbx_dequant_q4_1")                  \
+  X(PBX_K_GEMV_Q4_1_WIDE_R4, "pbx_gemv_q4_1_wide_r4")        \
+  X(PBX_K_GEMV_Q4_1_WIDE_R8, "pbx_gemv_q4_1_wide_r8")        \
+  X(PBX_K_GEMV_Q4_1_WIDE_R16, "pbx_gemv_q4_1_wide_r16")      \
+  X(PBX_K_GEMV_Q4_1_SMALL, "pbx_gemv_q4_1_small")            \
   X(PBX_K_DEQUANT_Q4_0, "pbx_dequant_q4_0")                  \
   X(PBX_K_DEQUANT_Q8_0, "pbx_dequant_q8_0")                  \
   X(PBX_K_DEQUANT_Q8REF, "pbx_dequant_q8ref")                \
@@ -77,6 +83,7 @@ struct pbx_weight {
   int64_t n_scales = 0;
   void *qs = nullptr;  // nibble / int8 / f32 plane (Q8_REF: flat int8 [K,N])
   void *d = nullptr;   // fp16 scale plane (Q8_REF: f32 scales)
+  void *m = nullptr;   // Q4_1: fp16 min plane (inside the d allocation)
   size_t bytes = 0;
 };
 

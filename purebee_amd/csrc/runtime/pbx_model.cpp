@@ -34,6 +34,7 @@ struct GemvArgsHost {  // layout of GemvArgs in pbx_gemv_impl.h
   uint64_t *partials;
   int N, B;
   float eps;
+  const void *msc;
 };
 
 struct AttnArgsHost {  // AttnArgs in pbx_decode.hip
@@ -70,6 +71,7 @@ struct EmbedArgsHost {  // EmbedArgs in pbx_decode.hip
   const int *state;
   int type;
   int dim, vocab;
+  const void *msc;
 };
 
 struct ArgmaxArgsHost {  // ArgmaxArgs in pbx_decode.hip
@@ -104,10 +106,13 @@ struct Layer {
 };
 
 const char *type_tag(int t) {
-  return t == PBX_TYPE_Q4_0 ? "q4" : t == PBX_TYPE_Q8_0 ? "q8" : "f32";
+  return t == PBX_TYPE_Q4_0 ? "q4" : t == PBX_TYPE_Q4_1 ? "q41" : t == PBX_TYPE_Q8_0 ? "q8" : "f32";
 }
 
-int kernel_type(int t) { return t == PBX_TYPE_Q4_0 ? 0 : t == PBX_TYPE_Q8_0 ? 1 : 2; }
+// PBX_Q4 / PBX_Q8 / PBX_F32 / PBX_Q41 of pbx_gemv_impl.h
+int kernel_type(int t) {
+  return t == PBX_TYPE_Q4_0 ? 0 : t == PBX_TYPE_Q8_0 ? 1 : t == PBX_TYPE_Q4_1 ? 3 : 2;
+}
 
 }  // namespace
 
@@ -183,8 +188,9 @@ static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, int type, int N
     *n_tiles = (int)grid->x;
     return;
   }
+  const bool q4 = type == PBX_TYPE_Q4_0 || type == PBX_TYPE_Q4_1;
   if (B <= 32) {
-    const int P = type == PBX_TYPE_Q4_0 ? 8 : type == PBX_TYPE_Q8_0 ? 4 : 2;
+    const int P = q4 ? 8 : type == PBX_TYPE_Q8_0 ? 4 : 2;
     const int T = P * (64 / B);
     const int gx = (N + 4 * T - 1) / (4 * T);
     *shape = "s";
@@ -196,7 +202,7 @@ static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, int type, int N
   const int W = (B + 63) / 64;
   const int target = std::max(4 * c->cu_count, 256);
   int R;
-  if (type == PBX_TYPE_Q4_0)
+  if (q4)
     R = (N / 16 >= target) ? 16 : (N / 8 >= target) ? 8 : 4;
   else if (type == PBX_TYPE_Q8_0)
     R = (N / 8 >= target) ? 8 : 4;
@@ -225,7 +231,7 @@ static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const c
   op.f = pbx_kernel_by_name(c, op.name);
   if (!op.f) return pbx_fail(c, PBX_ELOAD, "model: kernel %s not found", op.name.c_str());
   op.gemv = GemvArgsHost{w->qs, w->d, X, X2, normw, nullptr, Y, m->partials, (int)w->N,
-                         (int)w->B, m->cfg.rms_eps};
+                         (int)w->B, m->cfg.rms_eps, w->m};
   op.role = role;
   // weights + activation reads (+ up for SwiGLU, + norm weight) + output
   // (read and written for the residual epilogue)
@@ -251,7 +257,7 @@ static int build_ops(pbx_model *m) {
   e.role = "embed";
   e.bytes = (double)g.dim / 32 * pbx_type_block_bytes(m->embd->type) + 4.0 * g.dim;
   e.embed = EmbedArgsHost{m->embd->qs, m->embd->d, m->x, m->state, kernel_type(m->embd->type),
-                          g.dim, g.vocab_size};
+                          g.dim, g.vocab_size, m->embd->m};
   m->ops.push_back(e);
   hipFunction_t fattn = pbx_kernel_by_name(c, "pbx_attention_decode");
   if (!fattn) return pbx_fail(c, PBX_ELOAD, "model: kernel pbx_attention_decode not found");
@@ -467,7 +473,7 @@ static bool split_attention_disabled() {
 }
 
 static bool is_weight_type(int t) {
-  return t == PBX_TYPE_Q4_0 || t == PBX_TYPE_Q8_0 || t == PBX_TYPE_F32;
+  return t == PBX_TYPE_Q4_0 || t == PBX_TYPE_Q4_1 || t == PBX_TYPE_Q8_0 || t == PBX_TYPE_F32;
 }
 
 extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_model **out) {
@@ -698,7 +704,9 @@ static int ensure_batch(pbx_model *m, int rows, bool all_logits) {
     if (!rc) rc = grow(m, (void **)&m->battn, R * g.dim * 4);
     if (!rc) rc = grow(m, (void **)&m->bgu, R * 2 * g.hidden_dim * 4);
     if (!rc) rc = grow(m, (void **)&m->bh, R * g.hidden_dim * 4);
-    if (!rc && g.weight_type == PBX_TYPE_F32) rc = grow(m, (void **)&m->btmp, R * tmp_cols * 4);
+    // accumulating linears without an MFMA path go through a temporary
+    if (!rc && g.weight_type != PBX_TYPE_Q4_0 && g.weight_type != PBX_TYPE_Q8_0)
+      rc = grow(m, (void **)&m->btmp, R * tmp_cols * 4);
     if (!rc) rc = grow(m, (void **)&m->btok, R * 4);
     if (!rc) rc = grow(m, (void **)&m->bnext, R * 4);
     if (rc) {
@@ -728,7 +736,8 @@ static int launch_k(pbx_model *m, const char *name, dim3 grid, dim3 block, void 
 static int linear_rows(pbx_model *m, const pbx_weight *w, const float *X, int n, float *Y,
                        bool accumulate) {
   pbx_ctx *c = m->c;
-  if (w->type != PBX_TYPE_F32) return pbx_gemm_launch(c, w, X, n, nullptr, Y, accumulate ? 1 : 0, c->stream);
+  if (w->type == PBX_TYPE_Q4_0 || w->type == PBX_TYPE_Q8_0)
+    return pbx_gemm_launch(c, w, X, n, nullptr, Y, accumulate ? 1 : 0, c->stream);
   if (!accumulate) return pbx_linear_enqueue(c, w, X, n, nullptr, Y, c->stream);
   int rc = pbx_linear_enqueue(c, w, X, n, nullptr, m->btmp, c->stream);
   if (rc) return rc;
@@ -753,11 +762,11 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
     return pbx_fail(c, PBX_EHIP, "model: token upload failed");
   int rc;
   {
-    const void *qs = m->embd->qs, *dsc = m->embd->d;
+    const void *qs = m->embd->qs, *dsc = m->embd->d, *msc = m->embd->m;
     int *tok = m->btok;
     float *x = m->bx;
     int type = kernel_type(m->embd->type), dim = g.dim, vocab = g.vocab_size;
-    void *args[] = {(void *)&qs, (void *)&dsc, &tok, &x, &type, &dim, &vocab};
+    void *args[] = {(void *)&qs, (void *)&dsc, (void *)&msc, &tok, &x, &type, &dim, &vocab};
     if ((rc = launch_k(m, "pbx_embed_rows", dim3((g.dim + 255) / 256, n), dim3(256), args))) return rc;
   }
   const size_t layer_kv = (size_t)g.max_seq * m->kvdim;

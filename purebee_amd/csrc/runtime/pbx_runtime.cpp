@@ -293,8 +293,10 @@ static int stage_repack(pbx_ctx *c, pbx_weight *w, int64_t first_row, int64_t n_
     int64_t row0 = first_row + r0, nrows = rows;
     void *raw = c->d_stage[slot];
     void *args[] = {&raw, &w->qs, &w->d, &row0, &nrows, &B};
+    void *args_q41[] = {&raw, &w->qs, &w->d, &w->m, &row0, &nrows, &B};
     const int64_t blocks = rows * w->B;
-    int rc = pbx_launch(c, kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), args);
+    int rc = pbx_launch(c, kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256),
+                        kernel == PBX_K_REPACK_Q4_1 ? args_q41 : args);
     if (rc) return rc;
     HIPCHK(c, hipEventRecord(c->ev_stage[slot], c->stream));
     slot ^= 1;
@@ -306,6 +308,7 @@ static int stage_repack(pbx_ctx *c, pbx_weight *w, int64_t first_row, int64_t n_
 size_t pbx_type_block_bytes(int type) {
   switch (type) {
     case PBX_TYPE_Q4_0: return 18;
+    case PBX_TYPE_Q4_1: return 20;
     case PBX_TYPE_Q8_0: return 34;
     case PBX_TYPE_F32: return 128;
     default: return 0;
@@ -314,9 +317,14 @@ size_t pbx_type_block_bytes(int type) {
 
 static bool weight_ok(const pbx_weight *w) { return w && w->magic == PBX_WEIGHT_MAGIC; }
 
+static bool upload_type(int type) {
+  return type == PBX_TYPE_Q4_0 || type == PBX_TYPE_Q4_1 || type == PBX_TYPE_Q8_0 ||
+         type == PBX_TYPE_F32;
+}
+
 int pbx_weight_alloc(pbx_ctx *c, int type, int64_t N, int64_t K, pbx_weight **out) {
   *out = nullptr;
-  if (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0 && type != PBX_TYPE_F32)
+  if (!upload_type(type))
     return pbx_fail(c, PBX_EINVAL, "unsupported weight type %d", type);
   if (N <= 0 || K <= 0 || K % 32 != 0)
     return pbx_fail(c, PBX_EINVAL, "bad shape N=%lld K=%lld (need N>0, K>0, K%%32==0)",
@@ -335,8 +343,9 @@ int pbx_weight_alloc(pbx_ctx *c, int type, int64_t N, int64_t K, pbx_weight **ou
   if (type == PBX_TYPE_F32) {
     qs_bytes = (size_t)w->Npad * K * 4;
   } else {
-    qs_bytes = (size_t)w->Npad * w->B * (type == PBX_TYPE_Q4_0 ? 16 : 32);
+    qs_bytes = (size_t)w->Npad * w->B * (type == PBX_TYPE_Q8_0 ? 32 : 16);
     d_bytes = (size_t)w->Npad * w->B * 2;
+    if (type == PBX_TYPE_Q4_1) d_bytes *= 2;  // d plane, then the m plane
   }
   if (hipMalloc(&w->qs, qs_bytes) != hipSuccess) {
     delete w;
@@ -347,6 +356,7 @@ int pbx_weight_alloc(pbx_ctx *c, int type, int64_t N, int64_t K, pbx_weight **ou
     delete w;
     return pbx_fail(c, PBX_ENOMEM, "hipMalloc(%zu) failed", d_bytes);
   }
+  if (type == PBX_TYPE_Q4_1) w->m = (char *)w->d + d_bytes / 2;
   w->bytes = qs_bytes + d_bytes;
   // Pad rows read as zero weights with zero scales.
   if (hipMemsetAsync(w->qs, 0, qs_bytes, c->stream) != hipSuccess ||
@@ -376,8 +386,10 @@ int pbx_weight_write_rows(pbx_ctx *c, pbx_weight *w, int64_t row0, int64_t rows,
   const size_t row_bytes = (size_t)w->B * pbx_type_block_bytes(w->type);
   if (w->type == PBX_TYPE_F32)
     return stage_copy(c, (char *)w->qs + (size_t)row0 * row_bytes, host, (size_t)rows * row_bytes);
-  return stage_repack(c, w, row0, rows, (const uint8_t *)host,
-                      w->type == PBX_TYPE_Q4_0 ? PBX_K_REPACK_Q4_0 : PBX_K_REPACK_Q8_0, row_bytes);
+  const int k = w->type == PBX_TYPE_Q4_0   ? PBX_K_REPACK_Q4_0
+                : w->type == PBX_TYPE_Q4_1 ? PBX_K_REPACK_Q4_1
+                                           : PBX_K_REPACK_Q8_0;
+  return stage_repack(c, w, row0, rows, (const uint8_t *)host, k, row_bytes);
 }
 
 extern "C" int pbx_weight_upload(pbx_ctx *c, int type, int64_t N, int64_t K,
@@ -385,7 +397,7 @@ extern "C" int pbx_weight_upload(pbx_ctx *c, int type, int64_t N, int64_t K,
   if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_weight_upload: ctx is NULL");
   if (!out) return pbx_fail(c, PBX_EINVAL, "pbx_weight_upload: out is NULL");
   *out = nullptr;
-  if (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0 && type != PBX_TYPE_F32)
+  if (!upload_type(type))
     return pbx_fail(c, PBX_EINVAL, "pbx_weight_upload: unsupported weight type %d", type);
   if (N <= 0 || K <= 0 || K % 32 != 0)
     return pbx_fail(c, PBX_EINVAL,
@@ -488,15 +500,19 @@ int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t
     return pbx_launch(c, PBX_K_GEMV_Q8REF, dim3((unsigned)((N + 63) / 64), gy), dim3(512),
                       args, stream);
   }
-  if (M >= PBX_GEMM_MIN_M && w->type != PBX_TYPE_F32)
+  // Q4_1 and F32 rows stay on the GEMV kernels for every M (one grid row
+  // per activation row); the MFMA GEMM covers Q4_0 / Q8_0.
+  if (M >= PBX_GEMM_MIN_M && (w->type == PBX_TYPE_Q4_0 || w->type == PBX_TYPE_Q8_0))
     return pbx_gemm_enqueue(c, w, dX, M, dBias, dY, stream);
   int B = (int)w->B;
-  void *args[] = {(void *)&w->qs, (void *)&w->d, &dX, &dBias, &dY, &N, &B};
+  void *args[] = {(void *)&w->qs, (void *)&w->d, (void *)&w->m, &dX, &dBias, &dY, &N, &B};
+  const bool q4 = w->type == PBX_TYPE_Q4_0 || w->type == PBX_TYPE_Q4_1;
   if (B <= 32) {
     // Small-K path: 4 waves per workgroup, each wave a tile of P*(64/B) rows.
-    const int P = w->type == PBX_TYPE_Q4_0 ? 8 : w->type == PBX_TYPE_Q8_0 ? 4 : 2;
+    const int P = q4 ? 8 : w->type == PBX_TYPE_Q8_0 ? 4 : 2;
     const int T = P * (64 / B);
     const int k = w->type == PBX_TYPE_Q4_0   ? PBX_K_GEMV_Q4_0_SMALL
+                  : w->type == PBX_TYPE_Q4_1 ? PBX_K_GEMV_Q4_1_SMALL
                   : w->type == PBX_TYPE_Q8_0 ? PBX_K_GEMV_Q8_0_SMALL
                                              : PBX_K_GEMV_F32_SMALL;
     return pbx_launch(c, k, dim3((unsigned)((N + 4 * T - 1) / (4 * T)), gy), dim3(256), args,
@@ -509,10 +525,11 @@ int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t
   // Rows per tile: the largest tile that still gives >= 4 workgroups per CU.
   const int target = std::max(4 * c->cu_count, 256);
   int R, k;
-  if (w->type == PBX_TYPE_Q4_0) {
-    if (N / 16 >= target) { R = 16; k = PBX_K_GEMV_Q4_0_WIDE_R16; }
-    else if (N / 8 >= target) { R = 8; k = PBX_K_GEMV_Q4_0_WIDE_R8; }
-    else { R = 4; k = PBX_K_GEMV_Q4_0_WIDE_R4; }
+  if (q4) {
+    const bool q41 = w->type == PBX_TYPE_Q4_1;
+    if (N / 16 >= target) { R = 16; k = q41 ? PBX_K_GEMV_Q4_1_WIDE_R16 : PBX_K_GEMV_Q4_0_WIDE_R16; }
+    else if (N / 8 >= target) { R = 8; k = q41 ? PBX_K_GEMV_Q4_1_WIDE_R8 : PBX_K_GEMV_Q4_0_WIDE_R8; }
+    else { R = 4; k = q41 ? PBX_K_GEMV_Q4_1_WIDE_R4 : PBX_K_GEMV_Q4_0_WIDE_R4; }
   } else if (w->type == PBX_TYPE_Q8_0) {
     if (N / 8 >= target) { R = 8; k = PBX_K_GEMV_Q8_0_WIDE_R8; }
     else { R = 4; k = PBX_K_GEMV_Q8_0_WIDE_R4; }
@@ -582,8 +599,13 @@ extern "C" int pbx_dequant_dev(pbx_ctx *c, const pbx_weight *w, float *dY) {
     return pbx_launch(c, PBX_K_DEQUANT_Q8REF, dim3((unsigned)((n + 255) / 256)), dim3(256), args);
   }
   int N = (int)w->N, B = (int)w->B;
-  void *args[] = {(void *)&w->qs, (void *)&w->d, &dY, &N, &B};
   const int64_t blocks = (int64_t)N * B;
+  if (w->type == PBX_TYPE_Q4_1) {
+    void *args[] = {(void *)&w->qs, (void *)&w->d, (void *)&w->m, &dY, &N, &B};
+    return pbx_launch(c, PBX_K_DEQUANT_Q4_1, dim3((unsigned)((blocks + 255) / 256)), dim3(256),
+                      args);
+  }
+  void *args[] = {(void *)&w->qs, (void *)&w->d, &dY, &N, &B};
   return pbx_launch(c, w->type == PBX_TYPE_Q4_0 ? PBX_K_DEQUANT_Q4_0 : PBX_K_DEQUANT_Q8_0,
                     dim3((unsigned)((blocks + 255) / 256)), dim3(256), args);
 }

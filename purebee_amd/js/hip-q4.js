@@ -22,7 +22,7 @@
 const path = require('path');
 
 const GGML_TYPE = { F32: 0, Q4_0: 2, Q4_1: 3, Q8_0: 8 };
-const BLOCK_BYTES = { 2: 18, 8: 34 };
+const BLOCK_BYTES = { 2: 18, 3: 20, 8: 34 };
 
 let addon = null;
 let _supported = false;
@@ -120,9 +120,13 @@ function q8_0_matvec(x, rawBuf, N, K) {
   return addon.linear(quantHandle(rawBuf, GGML_TYPE.Q8_0, N, K), x, 1, null);
 }
 
-/** Q4_1 is a listed next step; the GPU path does not cover it yet. */
-function q4_1_matvec() {
-  throw new Error('HIP Q4_1 matvec not implemented');
+/**
+ * Q4_1 matvec: y[N] = W_q4_1[N,K] @ x[K].  Signature of wasm-q4.js:758;
+ * 20-byte blocks (fp16 d, fp16 m, 16 nibble bytes), value = nibble*d + m.
+ */
+function q4_1_matvec(x, rawBuf, N, K) {
+  ensure();
+  return addon.linear(quantHandle(rawBuf, GGML_TYPE.Q4_1, N, K), x, 1, null);
 }
 
 /**
@@ -130,6 +134,7 @@ function q4_1_matvec() {
  */
 function matvec(x, rawBuf, type, N, K) {
   if (type === GGML_TYPE.Q4_0) return q4_0_matvec(x, rawBuf, N, K);
+  if (type === GGML_TYPE.Q4_1) return q4_1_matvec(x, rawBuf, N, K);
   if (type === GGML_TYPE.Q8_0) return q8_0_matvec(x, rawBuf, N, K);
   throw new Error(`Unsupported quant type for matvec: ${type}`);
 }

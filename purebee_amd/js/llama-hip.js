@@ -22,7 +22,7 @@
 
 const path = require('path');
 
-const TYPES = { f32: 0, q4_0: 2, q8_0: 8 };
+const TYPES = { f32: 0, q4_0: 2, q4_1: 3, q8_0: 8 };
 const TENSOR = {
   'token_embd.weight': 0, 'output.weight': 1, 'output_norm.weight': 2,
   'attn_norm.weight': 3, 'ffn_norm.weight': 4, 'attn_q.weight': 5, 'attn_k.weight': 6,
@@ -68,7 +68,7 @@ class HipLlamaRuntime {
     });
   }
 
-  /** One GGUF tensor: raw blocks (Q4_0/Q8_0) or a Float32Array (F32, norms). */
+  /** One GGUF tensor: raw blocks (Q4_0/Q4_1/Q8_0) or a Float32Array (F32, norms). */
   loadTensor(name, data) {
     const [tid, layer] = tensorId(name);
     addon.modelSetTensor(this._model, tid, layer, data);

@@ -13,6 +13,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 
 TYPE_F32 = 0
 TYPE_Q4_0 = 2
+TYPE_Q4_1 = 3
 TYPE_Q8_0 = 8
 TYPE_Q8_REF = 100
 
@@ -24,7 +25,8 @@ EXPORTS = (
     "pbx_init", "pbx_shutdown", "pbx_last_error", "pbx_device_info",
     "pbx_weight_upload", "pbx_weight_upload_q8ref", "pbx_weight_free", "pbx_weight_info",
     "pbx_linear", "pbx_linear_dev", "pbx_dequant", "pbx_dequant_dev",
-    "pbx_quantize_q8_0", "pbx_quantize_q4_0", "pbx_quantize_q8_ref", "pbx_synth_normal",
+    "pbx_quantize_q8_0", "pbx_quantize_q4_0", "pbx_quantize_q4_1", "pbx_quantize_q8_ref",
+    "pbx_synth_normal",
     "pbx_dev_alloc", "pbx_dev_free", "pbx_memcpy_h2d", "pbx_memcpy_d2h", "pbx_memset_dev",
     "pbx_dev_copy", "pbx_sync", "pbx_timer_start", "pbx_timer_stop", "pbx_bench_linear",
     "pbx_model_create", "pbx_model_free", "pbx_model_set_tensor", "pbx_model_forward",
@@ -99,6 +101,7 @@ def load_library():
         "pbx_dequant_dev": (ctypes.c_int, [_vp, _vp, _vp]),
         "pbx_quantize_q8_0": (ctypes.c_int, [_f32p, _i64, _i64, _u8p]),
         "pbx_quantize_q4_0": (ctypes.c_int, [_f32p, _i64, _i64, _u8p]),
+        "pbx_quantize_q4_1": (ctypes.c_int, [_f32p, _i64, _i64, _u8p]),
         "pbx_quantize_q8_ref": (ctypes.c_int, [_f32p, _i64, _i8p, _f32p]),
         "pbx_synth_normal": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_double,
                                             ctypes.c_double, _f32p]),
@@ -151,7 +154,7 @@ def _check(rc, ctx_ptr=None):
 
 
 def block_bytes(t):
-    return {TYPE_Q4_0: 18, TYPE_Q8_0: 34, TYPE_F32: 128}[t]
+    return {TYPE_Q4_0: 18, TYPE_Q4_1: 20, TYPE_Q8_0: 34, TYPE_F32: 128}[t]
 
 
 def quantize_q8_0(w):
@@ -167,6 +170,14 @@ def quantize_q4_0(w):
     N, K = w.shape
     out = np.empty(N * (K // 32) * 18, np.uint8)
     _check(load_library().pbx_quantize_q4_0(w, N, K, out))
+    return out
+
+
+def quantize_q4_1(w):
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    out = np.empty(N * (K // 32) * 20, np.uint8)
+    _check(load_library().pbx_quantize_q4_1(w, N, K, out))
     return out
 
 

@@ -2,14 +2,14 @@
 
 Every weight matrix is drawn from N(0, 0.02) with its own seed
 (base + tensor index), quantised with the host quantisers of the C ABI
-(pbx_quantize_q4_0 / pbx_quantize_q8_0) into GGUF blocks; norm weights are
+(pbx_quantize_q4_0 / pbx_quantize_q4_1 / pbx_quantize_q8_0) into GGUF blocks; norm weights are
 1.0 (f32, as GGUF stores them).  Shapes follow the GGUF tensors the reference
 loads (gguf.js:378-410): matrices are [out_features, in_features].
 """
 import numpy as np
 
 from . import native
-from .native import (Model, TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, T_TOKEN_EMBD, T_OUTPUT,
+from .native import (Model, TYPE_F32, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q8_0, T_TOKEN_EMBD, T_OUTPUT,
                      T_OUTPUT_NORM, T_ATTN_NORM, T_FFN_NORM, T_ATTN_Q, T_ATTN_K, T_ATTN_V,
                      T_ATTN_OUTPUT, T_FFN_GATE, T_FFN_UP, T_FFN_DOWN)
 
@@ -58,7 +58,8 @@ def make_tensor(spec, base_seed, index):
     w = native.synth_normal(base_seed + index, N * K, 0.0, WEIGHT_STD).reshape(N, K)
     if t == TYPE_F32:
         return w
-    return native.quantize_q4_0(w) if t == TYPE_Q4_0 else native.quantize_q8_0(w)
+    return {TYPE_Q4_0: native.quantize_q4_0, TYPE_Q4_1: native.quantize_q4_1,
+            TYPE_Q8_0: native.quantize_q8_0}[t](w)
 
 
 def build(ctx, cfg, seed=1000, keep=None):

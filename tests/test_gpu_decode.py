@@ -10,7 +10,7 @@ import pytest
 
 import oracle
 from purebee_amd import PbxError, synth
-from purebee_amd.native import TYPE_F32, TYPE_Q4_0, TYPE_Q8_0
+from purebee_amd.native import TYPE_F32, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q8_0
 from tests.e2e_util import LOGIT_TOL, check_greedy, make_pair
 
 pytestmark = pytest.mark.gpu
@@ -49,7 +49,8 @@ def run_prompt_then_greedy(ctx, cfg, n_prompt, n_gen, seed):
 
 
 @pytest.mark.parametrize("wt,et", [(TYPE_Q4_0, TYPE_Q4_0), (TYPE_Q8_0, TYPE_Q8_0),
-                                   (TYPE_Q8_0, TYPE_F32), (TYPE_F32, TYPE_F32)])
+                                   (TYPE_Q8_0, TYPE_F32), (TYPE_F32, TYPE_F32),
+                                   (TYPE_Q4_1, TYPE_Q4_1)])
 def test_tiny_model_prefill_and_greedy(ctx, wt, et):
     print(f"[case] tiny model weights={wt} embed={et}", flush=True)
     exact, ties, e1, e2 = run_prompt_then_greedy(ctx, tiny(wt, et), 8, 24, seed=50 + wt)
@@ -87,6 +88,16 @@ def test_llama1b_shape(ctx):
     exact, ties, e1, e2 = run_prompt_then_greedy(ctx, "llama32_1b", 8, 16, seed=3000)
     print(f"  exact={exact} ties={ties} prefill_err={e1:.1e} final_err={e2:.1e}")
     assert exact >= 15
+
+
+def test_llama1b_shape_q4_1(ctx):
+    """Llama-3.2-1B shapes with Q4_1 layer matrices and a tied Q4_1 head
+    (the wide GEMV kernels and the row-batched prefill on Q4_1)."""
+    print("[case] llama32_1b q4_1 6-token prompt + 8 greedy", flush=True)
+    cfg = dict(synth.CONFIGS["llama32_1b"], weight_type=TYPE_Q4_1, embed_type=TYPE_Q4_1)
+    exact, ties, e1, e2 = run_prompt_then_greedy(ctx, cfg, 6, 8, seed=3100)
+    print(f"  exact={exact} ties={ties} prefill_err={e1:.1e} final_err={e2:.1e}")
+    assert exact >= 7
 
 
 def test_teacher_forced_logits_every_step(ctx):

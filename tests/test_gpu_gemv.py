@@ -23,15 +23,20 @@ STORIES = [(288, 288), (768, 288), (288, 768)]
 EDGE = [(1, 32), (7, 64), (65, 96), (1000, 1056), (129, 2080), (3, 16384), (63, 4064)]
 
 
+QUANT = [pb.TYPE_Q4_0, pb.TYPE_Q4_1, pb.TYPE_Q8_0]
+
+
 def quantize(t, w):
-    return oracle.quantize_q4_0(w) if t == pb.TYPE_Q4_0 else oracle.quantize_q8_0(w)
+    return {pb.TYPE_Q4_0: oracle.quantize_q4_0, pb.TYPE_Q4_1: oracle.quantize_q4_1,
+            pb.TYPE_Q8_0: oracle.quantize_q8_0}[t](w)
 
 
 def dequant(t, raw, n):
-    return oracle.dequant_q4_0(raw, n) if t == pb.TYPE_Q4_0 else oracle.dequant_q8_0(raw, n)
+    return {pb.TYPE_Q4_0: oracle.dequant_q4_0, pb.TYPE_Q4_1: oracle.dequant_q4_1,
+            pb.TYPE_Q8_0: oracle.dequant_q8_0}[t](raw, n)
 
 
-@pytest.mark.parametrize("t", [pb.TYPE_Q4_0, pb.TYPE_Q8_0])
+@pytest.mark.parametrize("t", QUANT)
 @pytest.mark.parametrize("N,K", LLAMA1B[:2] + SMOLLM2[:2] + STORIES[:2] + EDGE[:4])
 def test_dequant_bit_exact(ctx, t, N, K):
     print(f"[case] dequant type={t} N={N} K={K}", flush=True)
@@ -58,7 +63,7 @@ def test_reference_q4_kat(ctx):
     w.free()
 
 
-@pytest.mark.parametrize("t", [pb.TYPE_Q4_0, pb.TYPE_Q8_0])
+@pytest.mark.parametrize("t", QUANT)
 @pytest.mark.parametrize("N,K", LLAMA1B + SMOLLM2 + STORIES + EDGE)
 def test_matvec_parity(ctx, t, N, K):
     print(f"[case] matvec type={t} N={N} K={K}", flush=True)
@@ -102,7 +107,67 @@ def test_f32_matvec_lm_head(ctx, N, K):
     w.free()
 
 
-@pytest.mark.parametrize("t", [pb.TYPE_Q4_0, pb.TYPE_Q8_0, pb.TYPE_F32])
+def q4_1_special_blocks():
+    """Q4_1 rows of 64 columns covering the scale corner cases: d = 0
+    (constant block: every element is m), negative and positive minima, a
+    subnormal d, and the largest finite fp16 m.  Row r, block b."""
+    cases = [(0x0000, 0x3C00), (0x3C00, 0xC800), (0x2E66, 0x2E66), (0x0001, 0x8000),
+             (0x0200, 0x7BFF), (0x4000, 0x0000), (0x3555, 0xB555), (0x1400, 0x9400)]
+    rng = np.random.default_rng(3)
+    raw = np.zeros((len(cases) // 2, 2, 20), np.uint8)
+    for i, (d, m) in enumerate(cases):
+        blk = raw[i // 2, i % 2]
+        blk[0:2] = [d & 0xFF, d >> 8]
+        blk[2:4] = [m & 0xFF, m >> 8]
+        blk[4:] = rng.integers(0, 256, 16)
+    return raw.ravel(), len(cases) // 2, 64
+
+
+def test_q4_1_special_scales(ctx):
+    """Dequant bit-exact and matvec against gguf.js:288-314 /
+    llama-streaming.js:115-151 on hand-made scale corner cases."""
+    print("[case] q4_1 special scales", flush=True)
+    raw, N, K = q4_1_special_blocks()
+    w = ctx.upload(pb.TYPE_Q4_1, N, K, raw)
+    got = ctx.dequant(w)
+    ref = oracle.dequant_q4_1(raw, N * K).reshape(N, K)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    x = pb.synth_normal(5, K)
+    y = ctx.linear(w, x)
+    assert rel_l2(y, oracle.q4_1_matvec_js(x, raw, N, K)) < 1e-5
+    w.free()
+
+
+def test_q4_1_from_q4_0_kat(ctx):
+    """The reference KAT (wasm-q4.js:673-704) rewritten as Q4_1 blocks with
+    m = -8d, which encode the same values: [32, 128] exactly."""
+    print("[case] q4_1 KAT identity", flush=True)
+    raw = np.zeros(40, np.uint8)
+    raw[0:4] = [0x00, 0x3C, 0x00, 0xC8]   # d = 1, m = -8
+    raw[4:20] = 0x99
+    raw[20:24] = [0x00, 0x40, 0x00, 0xCC]  # d = 2, m = -16
+    raw[24:40] = 0xAA
+    w = ctx.upload(pb.TYPE_Q4_1, 2, 32, raw)
+    y = ctx.linear(w, np.ones(32, np.float32))
+    assert y[0] == 32.0 and y[1] == 128.0
+    w.free()
+
+
+@pytest.mark.parametrize("M", [2, 7, 64])
+def test_q4_1_multi_row(ctx, M):
+    """M > 1 on Q4_1 (one GEMV grid row per activation row)."""
+    N, K = 1536, 576
+    print(f"[case] q4_1 multi-row M={M}", flush=True)
+    raw = oracle.quantize_q4_1(synth_matrix(M + 40, N, K))
+    X = pb.synth_normal(M, M * K).reshape(M, K)
+    w = ctx.upload(pb.TYPE_Q4_1, N, K, raw)
+    Y = ctx.linear(w, X)
+    for m in range(M):
+        assert rel_l2(Y[m], oracle.q4_1_matvec_js(X[m], raw, N, K)) < 1e-5
+    w.free()
+
+
+@pytest.mark.parametrize("t", QUANT + [pb.TYPE_F32])
 def test_bias_and_multi_row(ctx, t):
     N, K, M = 576, 576, 5
     print(f"[case] bias/multi-row type={t}", flush=True)

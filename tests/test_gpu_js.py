@@ -1,8 +1,8 @@
 """The JavaScript drop-ins on the GPU, driven through Node.js exactly as the
 reference's callers would use them:
 
-* js/hip-q4.js      -- wasm-q4.js surface (q4_0_matvec, matvec dispatch,
-                       lmHead) on raw GGUF Q4_0 / Q8_0 blocks;
+* js/hip-q4.js      -- wasm-q4.js surface (q4_0_matvec, q4_1_matvec, matvec
+                       dispatch, lmHead) on raw GGUF Q4_0 / Q4_1 / Q8_0 blocks;
 * js/engine-hip.js  -- ExecutionEngine.tensorMulAdd / tensorMulAddQ8 /
                        tensorMul (f32 [K,N] Tensors and quantize.js's
                        QuantizedTensor);
@@ -59,10 +59,12 @@ def test_hip_q4_module_matvec_and_dispatch(tmp_path):
     w = pb.synth_normal(501, N * K, 0, 0.02).reshape(N, K)
     raw4 = pb.quantize_q4_0(w)
     raw8 = pb.quantize_q8_0(w)
+    raw41 = pb.quantize_q4_1(w)
     x = pb.synth_normal(502, K)
     emb = pb.synth_normal(503, 1000 * K, 0, 0.02)
     raw4.tofile(tmp_path / "w4.bin")
     raw8.tofile(tmp_path / "w8.bin")
+    raw41.tofile(tmp_path / "w41.bin")
     x.tofile(tmp_path / "x.bin")
     emb.tofile(tmp_path / "emb.bin")
     out = run_node(tmp_path, f"""
@@ -73,24 +75,32 @@ const xcopy = Float32Array.from(x);
 const y4 = q.q4_0_matvec(x, w4, meta.N, meta.K);
 const y4b = q.q4_0_matvec(x, w4, meta.N, meta.K);   // resident second call
 const y8 = q.matvec(x, w8, 8, meta.N, meta.K);
+const w41 = rd('w41.bin', Uint8Array);
+const y41 = q.q4_1_matvec(x, w41, meta.N, meta.K);
+const y41d = q.matvec(x, w41, 3, meta.N, meta.K);   // quantizedMatvec type 3
+let rep41 = true; for (let i = 0; i < y41.length; i++) if (y41[i] !== y41d[i]) rep41 = false;
+wr('y41.bin', y41);
 const lm = q.lmHead(x, rd('emb.bin', Float32Array), 1000, meta.K);
 wr('y4.bin', y4); wr('y8.bin', y8); wr('lm.bin', lm);
 let errs = [];
-try {{ q.matvec(x, w4, 3, meta.N, meta.K); }} catch (e) {{ errs.push(e.message); }}
+try {{ q.matvec(x, w4, 1, meta.N, meta.K); }} catch (e) {{ errs.push(e.message); }}
 try {{ q.matvec(x, w4, 6, meta.N, meta.K); }} catch (e) {{ errs.push(e.message); }}
 let same = true; for (let i = 0; i < x.length; i++) if (x[i] !== xcopy[i]) same = false;
 let rep = true; for (let i = 0; i < y4.length; i++) if (y4[i] !== y4b[i]) rep = false;
-console.log(JSON.stringify({{errs, same, rep, supported: q.supported}}));
+console.log(JSON.stringify({{errs, same, rep, rep41, supported: q.supported}}));
 """, {"N": N, "K": K})
     res = json.loads(out.strip().splitlines()[-1])
     assert res["same"], "input mutated"
     assert res["rep"], "second (resident) call differs"
+    assert res["rep41"], "q4_1_matvec and matvec(type 3) differ"
     assert len(res["errs"]) == 2 and all(res["errs"]), res["errs"]
     y4 = np.fromfile(tmp_path / "y4.bin", np.float32)
     y8 = np.fromfile(tmp_path / "y8.bin", np.float32)
     lm = np.fromfile(tmp_path / "lm.bin", np.float32)
     assert rel_l2(y4, oracle.q4_0_matvec_js(x, raw4, N, K)) <= 1e-3
     assert rel_l2(y8, oracle.matvec(TYPE_Q8_0, x, raw8, N, K)) <= 1e-3
+    y41 = np.fromfile(tmp_path / "y41.bin", np.float32)
+    assert rel_l2(y41, oracle.q4_1_matvec_js(x, raw41, N, K)) <= 1e-3
     ref_lm = emb.reshape(1000, K).astype(np.float64) @ x.astype(np.float64)
     assert rel_l2(lm, ref_lm) <= 1e-3
 

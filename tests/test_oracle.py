@@ -2,7 +2,8 @@
 reference's own known-answer tests and against what mathematics fixes.
 
 Reference KATs used:
-  wasm-q4.js:673-704   Q4_0 matvec self-test: rows -> [32, 128]
+  wasm-q4.js:673-704   Q4_0 matvec self-test: rows -> [32, 128] (also, re-encoded
+                       as Q4_1 blocks with m = -8d, the Q4_1 pin)
   wasm-simd.js:367-385 f32 matmul self-test (2x3 . 3x5 identity-like)
   main.js:65-74        TENSOR_MUL [2,3]x[3,2] -> [58, 64, 139, 154]
 """
@@ -160,6 +161,89 @@ def test_matvec_restatements_agree_and_are_linear():
     assert np.array_equal(oracle.q4_0_matvec_cpu_sse(x1, raw, N, K), wasm)
 
 
+def q4_1_from_q4_0(raw0):
+    """Q4_0 blocks -> Q4_1 blocks with the same d and m = -8d (exact in fp16
+    for these scales), which decode to the same values."""
+    b0 = raw0.reshape(-1, 18)
+    d = b0[:, :2].copy().view(np.float16)
+    m = (d.astype(np.float64) * -8).astype(np.float16)
+    assert np.array_equal(m.astype(np.float64), d.astype(np.float64) * -8)
+    b1 = np.zeros((b0.shape[0], 20), np.uint8)
+    b1[:, :2] = d.view(np.uint8)
+    b1[:, 2:4] = m.view(np.uint8)
+    b1[:, 4:] = b0[:, 2:]
+    return b1.ravel()
+
+
+def test_q4_1_reference_kat_through_q4_0_identity():
+    """No KAT for Q4_1 in the reference; the Q4_0 KAT (wasm-q4.js:673-704)
+    re-encoded as Q4_1 with m = -8d must give the same [32, 128]."""
+    raw1 = q4_1_from_q4_0(kat_q4_0_raw())
+    x = np.ones(32, np.float32)
+    for fn in (oracle.q4_1_matvec_js, oracle.q4_1_matvec_wasm):
+        out = fn(x, raw1, 2, 32)
+        assert out[0] == 32.0 and out[1] == 128.0, (fn.__name__, out)
+    assert np.array_equal(oracle.dequant_q4_1(raw1, 64), oracle.dequant_q4_0(kat_q4_0_raw(), 64))
+
+
+def test_q4_1_matches_q4_0_on_equivalent_blocks():
+    rng = np.random.default_rng(21)
+    N, K = 41, 320
+    raw0 = oracle.quantize_q4_0(rng.normal(0, 0.02, (N, K)).astype(np.float32))
+    raw1 = q4_1_from_q4_0(raw0)
+    x = rng.normal(0, 1, K).astype(np.float32)
+    assert np.array_equal(oracle.dequant_q4_1(raw1, N * K), oracle.dequant_q4_0(raw0, N * K))
+    ref = oracle.q4_0_matvec_js(x, raw0, N, K)
+    assert rel_l2(oracle.q4_1_matvec_js(x, raw1, N, K), ref) < 1e-12
+    assert rel_l2(oracle.q4_1_matvec_wasm(x, raw1, N, K), ref) < 1e-5
+
+
+def test_q4_1_dequant_every_byte_value():
+    # gguf.js:288-314: lo(byte j) * d + m at j, hi(byte j) * d + m at j + 16
+    raw = np.zeros(16 * 20, np.uint8).reshape(16, 20)
+    raw[:, 0:2] = np.frombuffer(np.float16(0.375).tobytes(), np.uint8)
+    raw[:, 2:4] = np.frombuffer(np.float16(-1.25).tobytes(), np.uint8)
+    raw[:, 4:] = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    W = oracle.dequant_q4_1(raw.ravel(), 16 * 32).reshape(16, 32)
+    for blk in range(16):
+        for j in range(16):
+            byte = 16 * blk + j
+            assert W[blk, j] == (byte & 15) * 0.375 - 1.25
+            assert W[blk, j + 16] == (byte >> 4) * 0.375 - 1.25
+    # a short last block is truncated like Q4_0's
+    assert np.array_equal(oracle.dequant_q4_1(raw.ravel(), 40), W.ravel()[:40])
+
+
+def test_q4_1_constant_blocks_closed_form():
+    """d = 0: every element is m, so the matvec is m * sum(x) per block."""
+    rng = np.random.default_rng(8)
+    K = 96
+    raw = np.zeros((1, 3, 20), np.uint8)
+    mins = [0.5, -3.0, 0.0078125]
+    for b, mv in enumerate(mins):
+        raw[0, b, 2:4] = np.frombuffer(np.float16(mv).tobytes(), np.uint8)
+        raw[0, b, 4:] = rng.integers(0, 256, 16)  # ignored: d = 0
+    x = rng.normal(0, 1, K).astype(np.float32)
+    exact = sum(mv * x[32 * b:32 * b + 32].astype(np.float64).sum() for b, mv in enumerate(mins))
+    assert abs(oracle.q4_1_matvec_js(x, raw.ravel(), 1, K)[0] - exact) <= 1e-6 * abs(exact)
+    assert abs(oracle.q4_1_matvec_wasm(x, raw.ravel(), 1, K)[0] - exact) <= 1e-5 * abs(exact)
+
+
+def test_q4_1_matvec_restatements_agree_and_are_linear():
+    rng = np.random.default_rng(6)
+    N, K = 37, 288
+    raw = oracle.quantize_q4_1(rng.normal(0.01, 0.02, (N, K)).astype(np.float32))
+    x1 = rng.normal(0, 1, K).astype(np.float32)
+    x2 = rng.normal(0, 1, K).astype(np.float32)
+    js = oracle.q4_1_matvec_js(x1, raw, N, K)
+    W = oracle.dequant_q4_1(raw, N * K).reshape(N, K).astype(np.float64)
+    exact = W @ x1.astype(np.float64)
+    assert rel_l2(js, exact) < 1e-6   # the dequantised f32 weights round once
+    assert rel_l2(oracle.q4_1_matvec_wasm(x1, raw, N, K), js) < 1e-5
+    lin = oracle.q4_1_matvec_js(x1 + 2 * x2, raw, N, K)
+    assert rel_l2(lin, js + 2 * oracle.q4_1_matvec_js(x2, raw, N, K)) < 1e-6
+
+
 def test_cpu_pool_partition_matches_single_thread():
     rng = np.random.default_rng(11)
     N, K = 1003, 256
@@ -239,6 +323,26 @@ def test_q4_quantizer_invariants():
     assert np.all(err[clamped] <= 2 * bound[clamped] + 1e-9)
 
 
+def test_q4_1_quantizer_invariants():
+    rng = np.random.default_rng(13)
+    w = rng.normal(0.01, 0.02, (8, 128)).astype(np.float32)
+    w[0, :32] = 0.25  # a constant block
+    raw = oracle.quantize_q4_1(w).reshape(-1, 20)
+    d = raw[:, :2].copy().view(np.float16).astype(np.float64).ravel()
+    m = raw[:, 2:4].copy().view(np.float16).astype(np.float64).ravel()
+    blocks = w.reshape(-1, 32).astype(np.float64)
+    lo, hi = blocks.min(1), blocks.max(1)
+    assert d[0] == 0 and m[0] == 0.25
+    assert np.array_equal(d, ((hi - lo) / 15).astype(np.float16).astype(np.float64))
+    assert np.array_equal(m, lo.astype(np.float16).astype(np.float64))
+    W = oracle.dequant_q4_1(raw.ravel(), w.size).reshape(-1, 32)
+    assert np.all(W[0] == 0.25)
+    # |x - w| <= d/2 plus the fp16 rounding of d (x15) and of m
+    err = np.abs(W - blocks)
+    bound = d / 2 + 15 * np.abs(d - (hi - lo) / 15) + np.abs(m - lo) + 1e-9
+    assert np.all(err <= bound[:, None] * (1 + 1e-6))
+
+
 def test_matmul_q8_ref_matches_dequantised_product():
     rng = np.random.default_rng(4)
     K, N, M = 64, 96, 3
@@ -262,6 +366,7 @@ def test_product_and_oracle_quantisers_agree():
     w[0, :32] = 0
     assert np.array_equal(pb.quantize_q8_0(w), oracle.quantize_q8_0(w))
     assert np.array_equal(pb.quantize_q4_0(w), oracle.quantize_q4_0(w))
+    assert np.array_equal(pb.quantize_q4_1(w), oracle.quantize_q4_1(w))
     q1, s1 = pb.quantize_q8_ref(w)
     q2, s2 = oracle.quantize_q8_ref(w)
     assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
