@@ -45,9 +45,11 @@ extern "C" {
  * 32 consecutive flat elements, consumed by matmul_q8 (quantize.js:224-266).
  */
 #define PBX_TYPE_F32     0
+#define PBX_TYPE_F16     1
 #define PBX_TYPE_Q4_0    2
 #define PBX_TYPE_Q4_1    3
 #define PBX_TYPE_Q8_0    8
+#define PBX_TYPE_Q6_K    14
 #define PBX_TYPE_Q8_REF  100
 
 typedef struct pbx_ctx pbx_ctx;
@@ -75,9 +77,10 @@ int         pbx_device_info(pbx_ctx *ctx, char *name, size_t cap, int *cu_count)
  *
  * host/nbytes hold GGUF row-major blocks: N rows of K/32 blocks of
  * 18 B (Q4_0: fp16 d + 16 nibble bytes), 20 B (Q4_1: fp16 d, fp16 m +
- * 16 nibble bytes) or 34 B (Q8_0: fp16 d + 32 int8), gguf.js:36-49 and
- * 239-314; for PBX_TYPE_F32, N*K little-endian floats.
- * K must be a multiple of 32 for every type.
+ * 16 nibble bytes) or 34 B (Q8_0: fp16 d + 32 int8), or of K/256 blocks of
+ * 210 B (Q6_K: ql[128], qh[64], int8 scales[16], fp16 d), gguf.js:36-49 and
+ * 239-364; for PBX_TYPE_F32 / PBX_TYPE_F16, N*K little-endian floats /
+ * halves.  K must be a multiple of 32 for every type (256 for Q6_K).
  */
 int pbx_weight_upload(pbx_ctx *ctx, int type, int64_t N, int64_t K,
                       const void *host, size_t nbytes, pbx_weight **out);
@@ -130,11 +133,15 @@ int pbx_dequant_dev(pbx_ctx *ctx, const pbx_weight *W, float *dY);
  * Q4_1 with d = (max-min)/15 and m = min stored as fp16 and nibble =
  * clamp(round((x-m)/d), 0, 15) against the stored values (GGUF Q4_1 layout,
  * gguf.js:288-314).  The reference reads Q4_1 but has no quantiser for it.
- * out must hold N*K/32*34 (Q8_0), N*K/32*18 (Q4_0) or N*K/32*20 (Q4_1)
- * bytes. */
+ * Q6_K (gguf.js:317-364 layout) with sub-block scales absmax/31 rounded
+ * to int8 steps of d = max/127 (fp16) and codes clamp(round(x/(d*sc)),
+ * -32, 31) + 32; the reference reads Q6_K but has no quantiser for it.
+ * out must hold N*K/32*34 (Q8_0), N*K/32*18 (Q4_0), N*K/32*20 (Q4_1) or
+ * N*K/256*210 (Q6_K, K % 256 == 0) bytes. */
 int pbx_quantize_q8_0(const float *w, int64_t N, int64_t K, uint8_t *out);
 int pbx_quantize_q4_0(const float *w, int64_t N, int64_t K, uint8_t *out);
 int pbx_quantize_q4_1(const float *w, int64_t N, int64_t K, uint8_t *out);
+int pbx_quantize_q6_k(const float *w, int64_t N, int64_t K, uint8_t *out);
 /* quantize_q8 itself (quantize.js:79-109): flat, f32 scales (Q8_REF). */
 int pbx_quantize_q8_ref(const float *w, int64_t n, int8_t *q, float *scales);
 

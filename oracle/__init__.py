@@ -42,7 +42,8 @@ def lib():
         L.pbo_f16_to_f32_wasm.argtypes = [ctypes.c_uint16]
         L.pbo_f64_to_f16.restype = ctypes.c_uint16
         L.pbo_f64_to_f16.argtypes = [ctypes.c_double]
-        for name in ("pbo_dequant_q4_0", "pbo_dequant_q8_0", "pbo_dequant_q4_1"):
+        for name in ("pbo_dequant_q4_0", "pbo_dequant_q8_0", "pbo_dequant_q4_1", "pbo_dequant_f16",
+                     "pbo_dequant_q6_k"):
             getattr(L, name).argtypes = [_u8p, _i64, _f32p]
         L.pbo_dequant_q8_ref.argtypes = [_i8p, _f32p, _i64, _f32p]
         for name in ("pbo_q4_0_matvec_js", "pbo_q4_0_matvec_wasm", "pbo_q8_0_matvec_f64",
@@ -53,7 +54,8 @@ def lib():
         L.pbo_matmul_f32_axpy.argtypes = [_f32p, _i64, _i64, _f32p, _i64, ctypes.c_void_p, _f32p]
         L.pbo_matmul_q8_ref.argtypes = [_f32p, _i64, _i64, _i8p, _f32p, _i64, ctypes.c_void_p, _f32p]
         L.pbo_quantize_q8_ref.argtypes = [_f32p, _i64, _i8p, _f32p]
-        for name in ("pbo_quantize_q8_0", "pbo_quantize_q4_0", "pbo_quantize_q4_1"):
+        for name in ("pbo_quantize_q8_0", "pbo_quantize_q4_0", "pbo_quantize_q4_1",
+                     "pbo_quantize_q6_k"):
             getattr(L, name).argtypes = [_f32p, _i64, _i64, _u8p]
         L.pbo_synth_normal.argtypes = [ctypes.c_uint64, _i64, ctypes.c_double, ctypes.c_double, _f32p]
         L.pbo_pool_create.restype = ctypes.c_void_p
@@ -94,6 +96,12 @@ def block_bytes(ggml_type):
     return {2: 18, 3: 20, 8: 34}[ggml_type]
 
 
+def row_bytes(ggml_type, K):
+    """Bytes of one GGUF row of K elements (gguf.js:36-49, 206-213)."""
+    return {0: 4 * K, 1: 2 * K, 2: K // 32 * 18, 3: K // 32 * 20, 8: K // 32 * 34,
+            14: K // 256 * 210}[ggml_type]
+
+
 def dequant_q4_0(raw, n):
     out = np.empty(n, np.float32)
     lib().pbo_dequant_q4_0(_c(raw, np.uint8), n, out)
@@ -104,6 +112,26 @@ def dequant_q4_1(raw, n):
     out = np.empty(n, np.float32)
     lib().pbo_dequant_q4_1(_c(raw, np.uint8), n, out)
     return out
+
+
+def dequant_f16(raw, n):
+    out = np.empty(n, np.float32)
+    lib().pbo_dequant_f16(_c(raw, np.uint8).view(np.uint8), n, out)
+    return out
+
+
+def dequant_q6_k(raw, n):
+    out = np.empty(n, np.float32)
+    lib().pbo_dequant_q6_k(_c(raw, np.uint8), n, out)
+    return out
+
+
+def dequant(ggml_type, raw, n):
+    """loadTensorData (gguf.js:219-367) for the types this build handles."""
+    if ggml_type == 0:
+        return np.frombuffer(np.ascontiguousarray(raw).tobytes(), np.float32)[:n].copy()
+    return {1: dequant_f16, 2: dequant_q4_0, 3: dequant_q4_1, 8: dequant_q8_0,
+            14: dequant_q6_k}[ggml_type](raw, n)
 
 
 def dequant_q8_0(raw, n):
@@ -181,6 +209,10 @@ def matvec(ggml_type, x, raw, N, K):
         return q8_0_matvec(x, raw, N, K)
     if ggml_type == 0:
         return f32_matvec(x, np.asarray(raw, np.float32).reshape(N, K))
+    if ggml_type in (1, 14):
+        # the reference dequantises F16 / Q6_K tensors to f32 (gguf.js:231-237,
+        # 317-364) and runs the f32 matvec
+        return f32_matvec(x, dequant(ggml_type, raw, N * K).reshape(N, K))
     raise ValueError(f"no oracle for type {ggml_type}")
 
 
@@ -229,6 +261,14 @@ def quantize_q4_0(w):
     N, K = w.shape
     out = np.empty(N * K // 32 * 18, np.uint8)
     lib().pbo_quantize_q4_0(w, N, K, out)
+    return out
+
+
+def quantize_q6_k(w):
+    w = _c(w, np.float32)
+    N, K = w.shape
+    out = np.empty(N * K // 256 * 210, np.uint8)
+    lib().pbo_quantize_q6_k(w, N, K, out)
     return out
 
 

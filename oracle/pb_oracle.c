@@ -157,6 +157,40 @@ void pbo_dequant_q4_1(const uint8_t *raw, int64_t n, float *out) {
   }
 }
 
+/* loadTensorData F16 branch, gguf.js:231-237. */
+void pbo_dequant_f16(const uint8_t *raw, int64_t n, float *out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = pbo_f16_to_f32(rd16(raw + 2 * i));
+}
+
+/* loadTensorData Q6_K branch, gguf.js:317-364: 210-byte blocks of 256 values
+ * (ql[128], qh[64], int8 scales[16], fp16 d).  For half h and l < 32, with
+ * the scale index is = 8h + l/16:
+ *   out[128h + l]      = d * sc[is]     * ((ql[64h+l]    & 15 | (qh[32h+l]      & 3) << 4) - 32)
+ *   out[128h + l + 32] = d * sc[is + 2] * ((ql[64h+l+32] & 15 | (qh[32h+l] >> 2 & 3) << 4) - 32)
+ *   out[128h + l + 64] = d * sc[is + 4] * ((ql[64h+l]   >> 4 | (qh[32h+l] >> 4 & 3) << 4) - 32)
+ *   out[128h + l + 96] = d * sc[is + 6] * ((ql[64h+l+32] >> 4 | (qh[32h+l] >> 6 & 3) << 4) - 32)
+ * each a double product rounded once; outputs past n are dropped. */
+void pbo_dequant_q6_k(const uint8_t *raw, int64_t n, float *out) {
+  const int64_t nb = (n + 255) / 256;
+  for (int64_t b = 0; b < nb; ++b) {
+    const uint8_t *blk = raw + b * 210;
+    const uint8_t *ql = blk, *qh = blk + 128;
+    const int8_t *sc = (const int8_t *)(blk + 192);
+    const double d = pbo_f16_to_f32(rd16(blk + 208));
+    for (int h = 0; h < 2; ++h)
+      for (int l = 0; l < 32; ++l) {
+        const int is = h * 8 + l / 16;
+        const int a = ql[h * 64 + l], c = ql[h * 64 + l + 32], hb = qh[h * 32 + l];
+        const int q[4] = {((a & 15) | ((hb & 3) << 4)) - 32, ((c & 15) | (((hb >> 2) & 3) << 4)) - 32,
+                          ((a >> 4) | (((hb >> 4) & 3) << 4)) - 32, ((c >> 4) | (((hb >> 6) & 3) << 4)) - 32};
+        for (int k = 0; k < 4; ++k) {
+          const int64_t idx = b * 256 + h * 128 + l + 32 * k;
+          if (idx < n) out[idx] = (float)(d * sc[is + 2 * k] * q[k]);
+        }
+      }
+  }
+}
+
 /* dequantize_q8, quantize.js:170-181: out[i] = q[i] * scales[floor(i/32)]. */
 void pbo_dequant_q8_ref(const int8_t *q, const float *scales, int64_t n, float *out) {
   for (int64_t i = 0; i < n; ++i) out[i] = (float)((double)q[i] * (double)scales[i / 32]);
@@ -477,6 +511,49 @@ void pbo_quantize_q4_1(const float *w, int64_t N, int64_t K, uint8_t *raw) {
       nib[i] = (int)r;
     }
     for (int j = 0; j < 16; ++j) o[4 + j] = (uint8_t)(nib[j] | (nib[j + 16] << 4));
+  }
+}
+
+/* Q6_K of synthetic workloads (no producer in the reference: parity
+ * unpinned, invariants only).  Per 16-element sub-block s of a 256-block,
+ * the ideal scale a_s = absmax_s / 31; d = max_s |a_s| / 127 as fp16;
+ * sc_s = Math.round(a_s / d) (int8); q = clamp(Math.round(x / (d * sc_s)),
+ * -32, 31) + 32 against the stored d, packed in the layout of
+ * pbo_dequant_q6_k. */
+void pbo_quantize_q6_k(const float *w, int64_t N, int64_t K, uint8_t *raw) {
+  const int64_t nb = N * (K / 256);
+  for (int64_t b = 0; b < nb; ++b) {
+    const float *x = w + b * 256;
+    uint8_t *o = raw + b * 210;
+    memset(o, 0, 210);
+    double a[16], amax = 0;
+    for (int s = 0; s < 16; ++s) {
+      double m = 0;
+      for (int i = 0; i < 16; ++i)
+        if (fabs((double)x[16 * s + i]) > m) m = fabs((double)x[16 * s + i]);
+      a[s] = m / 31;
+      if (a[s] > amax) amax = a[s];
+    }
+    const uint16_t hd = pbo_f64_to_f16(amax / 127);
+    o[208] = (uint8_t)hd;
+    o[209] = (uint8_t)(hd >> 8);
+    const double d = pbo_f16_to_f32(hd);
+    for (int s = 0; s < 16; ++s) {
+      double sc = d > 0 ? js_round(a[s] / d) : 0;
+      if (sc > 127) sc = 127;
+      o[192 + s] = (uint8_t)(int8_t)sc;
+      const double step = d * sc;
+      for (int i = 0; i < 16; ++i) {
+        const int e = 16 * s + i;
+        double r = step > 0 ? js_round((double)x[e] / step) : 0;
+        if (r < -32) r = -32;
+        if (r > 31) r = 31;
+        const int q = (int)r + 32;
+        const int h = e / 128, g = (e % 128) / 32, l = e % 32;
+        o[h * 64 + (g & 1) * 32 + l] |= (uint8_t)((q & 15) << (4 * (g >> 1)));
+        o[128 + h * 32 + l] |= (uint8_t)(((q >> 4) & 3) << (2 * g));
+      }
+    }
   }
 }
 

@@ -55,6 +55,12 @@ DK_MODES_WIDE(PBX_Q41, q41, 4)
 DK_MODES_WIDE(PBX_Q41, q41, 8)
 DK_MODES_WIDE(PBX_Q41, q41, 16)
 DK_MODES_SMALL(PBX_Q41, q41, 8)
+DK_MODES_WIDE(PBX_F16, f16, 4)
+DK_MODES_WIDE(PBX_F16, f16, 8)
+DK_MODES_SMALL(PBX_F16, f16, 4)
+DK_MODES_WIDE(PBX_Q6K, q6k, 4)
+DK_MODES_WIDE(PBX_Q6K, q6k, 8)
+DK_MODES_SMALL(PBX_Q6K, q6k, 4)
 // Integer-limb kernels for the gate|up GEMV (RMSNorm + SwiGLU pair), the
 // largest matrix of a layer; for the smaller GEMVs the activation prologue
 // costs more than the dot products save (measured).
@@ -471,7 +477,7 @@ struct EmbedArgs {
   const uint16_t *dsc;
   float *x;
   const int *state;  // state[1] = token
-  int type;          // PBX_Q4 / PBX_Q8 / PBX_F32 / PBX_Q41
+  int type;          // PBX_Q4 / PBX_Q8 / PBX_F32 / PBX_Q41 / PBX_F16 / PBX_Q6K
   int dim, vocab;
   const uint16_t *msc;  // Q4_1 minima
 };

@@ -15,6 +15,9 @@
 //   Q4_1 : qs plane as Q4_0; d plane as Q4_0 and an m plane of the same
 //          layout (fp16 minima), value = nibble * d + m
 //   F32  : plane     [Npad][K] float
+//   F16  : plane     [Npad][K] fp16
+//   Q6_K : qs plane  [Npad][K/256][208] bytes (ql, qh, int8 scales of each
+//          256-element super-block) and a d plane [Npad/4][K/256][4] fp16
 // The GGUF block formats these come from are gguf.js:36-49 (sizes) and
 // gguf.js:239-286 (element order: Q4_0 byte j holds element j in its low
 // nibble and element j+16 in its high nibble; value = (nibble - 8) * d;
@@ -51,6 +54,10 @@ PBX_WIDE(pbx_gemv_q4_1_wide_r8, PBX_Q41, 8)
 PBX_WIDE(pbx_gemv_q4_1_wide_r16, PBX_Q41, 16)
 PBX_WIDE(pbx_gemv_q8_0_wide_r4, PBX_Q8, 4)
 PBX_WIDE(pbx_gemv_q8_0_wide_r8, PBX_Q8, 8)
+PBX_WIDE(pbx_gemv_f16_wide_r4, PBX_F16, 4)
+PBX_WIDE(pbx_gemv_f16_wide_r8, PBX_F16, 8)
+PBX_WIDE(pbx_gemv_q6_k_wide_r4, PBX_Q6K, 4)
+PBX_WIDE(pbx_gemv_q6_k_wide_r8, PBX_Q6K, 8)
 PBX_WIDE(pbx_gemv_f32_wide_r2, PBX_F32, 2)
 PBX_WIDE(pbx_gemv_f32_wide_r4, PBX_F32, 4)
 
@@ -64,6 +71,8 @@ PBX_SMALL(pbx_gemv_q4_0_small, PBX_Q4, 8)
 PBX_SMALL(pbx_gemv_q4_1_small, PBX_Q41, 8)
 PBX_SMALL(pbx_gemv_q8_0_small, PBX_Q8, 4)
 PBX_SMALL(pbx_gemv_f32_small, PBX_F32, 2)
+PBX_SMALL(pbx_gemv_f16_small, PBX_F16, 4)
+PBX_SMALL(pbx_gemv_q6_k_small, PBX_Q6K, 4)
 
 // Reference Q8 tensor (quantize.js:30-50, matmul_q8 quantize.js:224-266):
 // q is the flat int8 [K,N] array, scales one f32 per 32 flat elements.  The
@@ -163,6 +172,27 @@ pbx_repack_q4_1(const uint32_t *raw, uint8_t *qs, uint16_t *dsc, uint16_t *msc, 
   msc[di] = (uint16_t)(dm >> 16);
 }
 
+// Q6_K: 210-byte blocks (ql[128], qh[64], scales[16], fp16 d) are 2-byte
+// aligned in the staged rows; the first 208 bytes move to the qs plane as
+// thirteen 16-byte stores, d to the scale plane.  B is super-blocks per row.
+extern "C" __global__ void __launch_bounds__(256)
+pbx_repack_q6_k(const uint16_t *raw, uint8_t *qs, uint16_t *dsc, int64_t row0, int64_t rows,
+                int B) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * B) return;
+  const int64_t n = row0 + i / B;
+  const int b = (int)(i % B);
+  const uint16_t *src = raw + i * 105;  // 210 B = 105 halfwords
+  uint4 *dst = reinterpret_cast<uint4 *>(qs + ((size_t)n * B + b) * PBX_Q6K_BYTES);
+#pragma unroll
+  for (int v = 0; v < 13; ++v) {
+    const uint16_t *h = src + 8 * v;
+    dst[v] = make_uint4(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16),
+                        h[4] | ((unsigned)h[5] << 16), h[6] | ((unsigned)h[7] << 16));
+  }
+  dsc[dsc_index((int)n, b, B)] = src[104];
+}
+
 // ---------------------------------------------------------------------------
 // Exact dequantisation to fp32 row-major [N,K] (gguf.js:239-286): the
 // product of an fp16 scale and a small integer is exact in fp32.
@@ -225,6 +255,42 @@ pbx_dequant_q4_1(const uint8_t *qs, const uint16_t *dsc, const uint16_t *msc, fl
   float4 *dst = reinterpret_cast<float4 *>(out + i * 32);
 #pragma unroll
   for (int j = 0; j < 8; ++j) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+}
+
+// F16 (gguf.js:231-237): exact conversion.
+extern "C" __global__ void __launch_bounds__(256)
+pbx_dequant_f16(const uint16_t *qs, float *out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = f16_bits_to_f32(qs[i]);
+}
+
+// Q6_K (gguf.js:317-364): one thread per 32 consecutive outputs of a row
+// (element layout in load_lane); (d * sc) * (q - 32) is exact in fp32.
+extern "C" __global__ void __launch_bounds__(256)
+pbx_dequant_q6_k(const uint8_t *qs, const uint16_t *dsc, float *out, int N, int B) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 32-block index
+  if (i >= (int64_t)N * B * 8) return;
+  const int n = (int)(i / (B * 8)), j = (int)(i % (B * 8));
+  uint4 q[4];
+  unsigned ex;
+  load_lane<PBX_Q6K>(qs, n, j, B * 8, true, q, ex);
+  const float d = f16_bits_to_f32(dsc[dsc_index(n, j >> 3, B)]);
+  const int g = j & 3, sl = (g >> 1) * 4, sh = g * 2;
+  const unsigned ql[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
+  const unsigned qh[8] = {q[2].x, q[2].y, q[2].z, q[2].w, q[3].x, q[3].y, q[3].z, q[3].w};
+  const float ds0 = d * (float)(int8_t)(ex & 0xFFu), ds1 = d * (float)(int8_t)((ex >> 8) & 0xFFu);
+  float v[32];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const unsigned c = ((ql[k] >> sl) & 0x0F0F0F0Fu) | (((qh[k] >> sh) & 0x03030303u) << 4);
+    const float ds = k < 4 ? ds0 : ds1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * k + e] = ds * (float)((int)((c >> (8 * e)) & 0xFFu) - 32);
+  }
+  float4 *dst = reinterpret_cast<float4 *>(out + i * 32);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) dst[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
 }
 
 // dequantize_q8 (quantize.js:170-181): out[i] = q[i] * scales[i/32].

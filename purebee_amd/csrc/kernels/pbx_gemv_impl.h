@@ -23,6 +23,8 @@
 #define PBX_Q8 1
 #define PBX_F32 2
 #define PBX_Q41 3
+#define PBX_F16 4
+#define PBX_Q6K 5
 
 #define PRO_NONE 0
 #define PRO_RMSNORM 1
@@ -115,6 +117,44 @@ __device__ __forceinline__ float dot_q8(const uint4 qa, const uint4 qb,
   return s0 + s1;
 }
 
+// sum_j x[j] * w[j] over 32 fp16 weights (exact conversions).
+__device__ __forceinline__ float dot_f16(const uint4 (&q)[4], const float (&xr)[32]) {
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const unsigned w[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float &s = (k & 1) ? s1 : s0;
+      s = fmaf(xr[8 * j + 2 * k], f16_bits_to_f32(w[k]), s);
+      s = fmaf(xr[8 * j + 2 * k + 1], f16_bits_to_f32(w[k] >> 16), s);
+    }
+  }
+  return s0 + s1;
+}
+
+// One lane's Q6_K term: d * (sc0 * sum_{l<16} x_l (q_l - 32) +
+// sc1 * sum_{l>=16} x_l (q_l - 32)); the unsigned 6-bit codes are assembled
+// four at a time, the offset folded into 32 * (sum of x) per half-block.
+__device__ __forceinline__ float dot_q6k(const uint4 (&q)[4], unsigned ex, int g,
+                                         const float (&xr)[32], float xs, float xlo, float d) {
+  const unsigned ql[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
+  const unsigned qh[8] = {q[2].x, q[2].y, q[2].z, q[2].w, q[3].x, q[3].y, q[3].z, q[3].w};
+  const int sl = (g >> 1) * 4, sh = g * 2;
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const unsigned v = ((ql[k] >> sl) & 0x0F0F0F0Fu) | (((qh[k] >> sh) & 0x03030303u) << 4);
+    float &s = k < 4 ? s0 : s1;
+    s = fmaf(xr[4 * k + 0], (float)(v & 0xFFu), s);
+    s = fmaf(xr[4 * k + 1], (float)((v >> 8) & 0xFFu), s);
+    s = fmaf(xr[4 * k + 2], (float)((v >> 16) & 0xFFu), s);
+    s = fmaf(xr[4 * k + 3], (float)(v >> 24), s);
+  }
+  const float sc0 = (float)(int8_t)(ex & 0xFFu), sc1 = (float)(int8_t)((ex >> 8) & 0xFFu);
+  return d * (sc0 * (s0 - 32.f * xlo) + sc1 * (s1 - 32.f * (xs - xlo)));
+}
+
 __device__ __forceinline__ float dot_f32(const uint4 (&q)[8], const float (&xr)[32]) {
   float s0 = 0.f, s1 = 0.f;
 #pragma unroll
@@ -133,6 +173,56 @@ template <> struct BlockTraits<PBX_Q4> { static constexpr int QB = 16; static co
 template <> struct BlockTraits<PBX_Q8> { static constexpr int QB = 32; static constexpr float OFF = 128.f; };
 template <> struct BlockTraits<PBX_F32> { static constexpr int QB = 128; static constexpr float OFF = 0.f; };
 template <> struct BlockTraits<PBX_Q41> { static constexpr int QB = 16; static constexpr float OFF = 0.f; };
+// F16: 32 halves.  Q6_K: the lane's 32 ql bytes then its 32 qh bytes (see
+// load_lane); the 6-bit codes carry an offset of 32.
+template <> struct BlockTraits<PBX_F16> { static constexpr int QB = 64; static constexpr float OFF = 0.f; };
+template <> struct BlockTraits<PBX_Q6K> { static constexpr int QB = 64; static constexpr float OFF = 32.f; };
+
+// Types with an fp16 scale plane (d per 32-block, or per 256-block for Q6_K).
+template <int TYPE> constexpr bool has_scale() {
+  return TYPE == PBX_Q4 || TYPE == PBX_Q8 || TYPE == PBX_Q41 || TYPE == PBX_Q6K;
+}
+// Q6_K keeps one d per 256-element super-block: block index and blocks per
+// row of the scale plane for the lane's 32-block b.
+template <int TYPE> __device__ __forceinline__ int scale_block(int b) {
+  return TYPE == PBX_Q6K ? b >> 3 : b;
+}
+
+// Q6_K super-block as resident (gguf.js:317-364 minus d, which moves to the
+// scale plane): ql[128] low nibbles, qh[64] high 2-bit pairs, 16 int8
+// sub-block scales; 208 bytes, 16-byte aligned.
+#define PBX_Q6K_BYTES 208
+
+// The weight bytes lane-block b (elements 32b .. 32b+31) of row n needs.
+// Q6_K: element e = 256*sb + 128*half + 32*g + l (l < 32) is
+//   ((ql[64*half + 32*(g&1) + l] >> 4*(g>>1)) & 15)
+//   | ((qh[32*half + l] >> 2*g) & 3) << 4,  minus 32,
+// times d * scales[8*half + 2*g + l/16] (gguf.js:317-364); with b = 8*sb +
+// 4*half + g the lane reads 32 contiguous ql bytes, 32 contiguous qh bytes
+// and the two int8 scales of its half-blocks (returned in ex).
+template <int TYPE>
+__device__ __forceinline__ void load_lane(const uint8_t *qs, int n, int b, int B, bool ok,
+                                          uint4 (&q)[BlockTraits<TYPE>::QB / 16],
+                                          unsigned &ex) {
+  constexpr int QB = BlockTraits<TYPE>::QB;
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+  ex = 0u;
+  if constexpr (TYPE == PBX_Q6K) {
+    const uint8_t *blk = qs + ((size_t)n * (B >> 3) + (b >> 3)) * PBX_Q6K_BYTES;
+    const int half = (b >> 2) & 1, g = b & 3;
+    const uint8_t *ql = blk + half * 64 + (g & 1) * 32;
+    const uint8_t *qh = blk + 128 + half * 32;
+    q[0] = ok ? ld_stream(ql) : z;
+    q[1] = ok ? ld_stream(ql + 16) : z;
+    q[2] = ok ? ld_stream(qh) : z;
+    q[3] = ok ? ld_stream(qh + 16) : z;
+    ex = ok ? *reinterpret_cast<const uint16_t *>(blk + 192 + half * 8 + 2 * g) : 0u;
+  } else {
+    const uint8_t *src = qs + ((size_t)n * B + b) * QB;
+#pragma unroll
+    for (int v = 0; v < QB / 16; ++v) q[v] = ok ? ld_stream(src + v * 16) : z;
+  }
+}
 
 __device__ __forceinline__ void load_block(const float *__restrict__ p, bool valid,
                                            float (&v)[32]) {
@@ -151,11 +241,26 @@ __device__ __forceinline__ void load_block(const float *__restrict__ p, bool val
 }
 
 // Element i of row `tok` of a resident [rows][dim] weight, dequantised
-// exactly as gguf.js:239-314 (Q8_0, Q4_0, Q4_1) or read (F32).
+// exactly as gguf.js:231-364 (F16, Q8_0, Q4_0, Q4_1, Q6_K) or read (F32).
 __device__ __forceinline__ float row_value(const uint8_t *qs, const uint16_t *dsc,
                                           const uint16_t *msc, int type, int tok, int i,
                                           int dim) {
   if (type == PBX_F32) return reinterpret_cast<const float *>(qs)[(size_t)tok * dim + i];
+  if (type == PBX_F16)
+    return f16_bits_to_f32(reinterpret_cast<const uint16_t *>(qs)[(size_t)tok * dim + i]);
+  if (type == PBX_Q6K) {
+    // gguf.js:317-364; (d * sc) * (q - 32) is exact in fp32 (11 + 7 + 5
+    // significant bits), so this equals the reference's double product
+    // rounded once.
+    const int SB = dim / 256, sb = i / 256, r = i % 256;
+    const int half = r >> 7, g = (r >> 5) & 3, l = r & 31;
+    const uint8_t *blk = qs + ((size_t)tok * SB + sb) * PBX_Q6K_BYTES;
+    const int lo = (blk[half * 64 + (g & 1) * 32 + l] >> (4 * (g >> 1))) & 15;
+    const int hi = (blk[128 + half * 32 + l] >> (2 * g)) & 3;
+    const float sc = (float)(int8_t)blk[192 + half * 8 + 2 * g + (l >> 4)];
+    const float d = f16_bits_to_f32(dsc[dsc_index(tok, sb, SB)]);
+    return (d * sc) * (float)((lo | (hi << 4)) - 32);
+  }
   const int B = dim / 32, b = i / 32, j = i % 32;
   const size_t di = dsc_index(tok, b, B);
   const float d = f16_bits_to_f32(dsc[di]);
@@ -223,19 +328,24 @@ __device__ __forceinline__ void apply_rmsnorm(const GemvArgs &a, float ss, int K
   }
 }
 
-// One block-row term.  corr = OFF * sum(x) removes the code offset (Q4_0,
-// Q8_0); Q4_1 (gguf.js:288-314: value = nibble * d + m) instead adds
-// m * sum(x) with corr = sum(x), the split of llama-streaming.js:138-145.
+// One block-row term of the lane's 32-block b.  xs = sum of the lane's 32
+// activations, xlo = sum of the first 16.  OFF * xs removes the code offset
+// (Q4_0, Q8_0); Q4_1 (gguf.js:288-314: value = nibble * d + m) adds m * xs,
+// the split of llama-streaming.js:138-145.
 template <int TYPE>
 __device__ __forceinline__ float block_term(const uint4 (&q)[BlockTraits<TYPE>::QB / 16],
-                                            const float (&xr)[32], float corr, float d,
-                                            float mn) {
+                                            unsigned ex, int b, const float (&xr)[32],
+                                            float xs, float xlo, float d, float mn) {
   if constexpr (TYPE == PBX_Q4) {
-    return (dot_q4(q[0], xr) - corr) * d;
+    return (dot_q4(q[0], xr) - 8.f * xs) * d;
   } else if constexpr (TYPE == PBX_Q41) {
-    return fmaf(dot_q4(q[0], xr), d, mn * corr);
+    return fmaf(dot_q4(q[0], xr), d, mn * xs);
   } else if constexpr (TYPE == PBX_Q8) {
-    return (dot_q8(q[0], q[1], xr) - corr) * d;
+    return (dot_q8(q[0], q[1], xr) - 128.f * xs) * d;
+  } else if constexpr (TYPE == PBX_F16) {
+    return dot_f16(q, xr);
+  } else if constexpr (TYPE == PBX_Q6K) {
+    return dot_q6k(q, ex, b & 3, xr, xs, xlo, d);
   } else {
     return dot_f32(q, xr);
   }
@@ -344,18 +454,15 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
 
   // Issue the weight loads first: they do not depend on the activations.
   uint4 q[R][NV];
+  unsigned ex[R];
 #pragma unroll
-  for (int i = 0; i < R; ++i) {
-    const uint8_t *src = a.qs + ((size_t)tile_row(i) * B + b) * QB;
-#pragma unroll
-    for (int v = 0; v < NV; ++v)
-      q[i][v] = valid ? ld_stream(src + v * 16) : make_uint4(0u, 0u, 0u, 0u);
-  }
+  for (int i = 0; i < R; ++i) load_lane<TYPE>(a.qs, tile_row(i), b, B, valid, q[i], ex[i]);
   float dsf[R], msf[R];
-  if constexpr (TYPE != PBX_F32) {
+  if constexpr (has_scale<TYPE>()) {
     constexpr int SEG = PAIR ? R / 2 : R;  // rows contiguous in the scale plane
-    load_scales<R, SEG>(a.dsc, tile_row, b, B, valid, dsf);
-    if constexpr (TYPE == PBX_Q41) load_scales<R, SEG>(a.msc, tile_row, b, B, valid, msf);
+    const int sb = scale_block<TYPE>(b), SB = scale_block<TYPE>(B);
+    load_scales<R, SEG>(a.dsc, tile_row, sb, SB, valid, dsf);
+    if constexpr (TYPE == PBX_Q41) load_scales<R, SEG>(a.msc, tile_row, sb, SB, valid, msf);
   } else {
 #pragma unroll
     for (int i = 0; i < R; ++i) dsf[i] = 1.f;
@@ -376,17 +483,20 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
     }
     apply_rmsnorm(a, ss, K, b, valid, xr);
   }
-  float xs = 0.f;
-  if constexpr (TYPE != PBX_F32) {
+  float xs = 0.f, xlo = 0.f;
+  if constexpr (TYPE != PBX_F32 && TYPE != PBX_F16) {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) xs += xr[i];
+    for (int i = 0; i < 16; ++i) xlo += xr[i];
+    xs = xlo;
+#pragma unroll
+    for (int i = 16; i < 32; ++i) xs += xr[i];
   }
-  const float corr = TYPE == PBX_Q41 ? xs : BlockTraits<TYPE>::OFF * xs;
 
   float acc[R];
 #pragma unroll
   for (int i = 0; i < R; ++i)
-    acc[i] = block_term<TYPE>(q[i], xr, corr, dsf[i], TYPE == PBX_Q41 ? msf[i] : 0.f);
+    acc[i] = block_term<TYPE>(q[i], ex[i], b, xr, xs, xlo, dsf[i],
+                              TYPE == PBX_Q41 ? msf[i] : 0.f);
 
   const float tot = wave_transpose_reduce<R>(acc, lane);
   const int row = lane / lanes_per_row;
@@ -480,21 +590,20 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
     if (lane < T && r0 + lane < N) res = y[r0 + lane];
 
   uint4 q[P][NV];
+  unsigned ex[P];
   float d[P], mn[P];
+  const int sb = scale_block<TYPE>(b), SB = scale_block<TYPE>(B);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int rw = tile_row(p * rpw + rs);
     const bool ok = active && row_ok(p * rpw + rs);
-    const uint8_t *src = a.qs + ((size_t)rw * B + b) * QB;
-#pragma unroll
-    for (int v = 0; v < NV; ++v)
-      q[p][v] = ok ? ld_stream(src + v * 16) : make_uint4(0u, 0u, 0u, 0u);
+    load_lane<TYPE>(a.qs, rw, b, B, ok, q[p], ex[p]);
     d[p] = 1.f;
     mn[p] = 0.f;
-    if constexpr (TYPE != PBX_F32)
-      d[p] = ok ? f16_bits_to_f32(a.dsc[dsc_index(rw, b, B)]) : 0.f;
+    if constexpr (has_scale<TYPE>())
+      d[p] = ok ? f16_bits_to_f32(a.dsc[dsc_index(rw, sb, SB)]) : 0.f;
     if constexpr (TYPE == PBX_Q41)
-      mn[p] = ok ? f16_bits_to_f32(a.msc[dsc_index(rw, b, B)]) : 0.f;
+      mn[p] = ok ? f16_bits_to_f32(a.msc[dsc_index(rw, sb, SB)]) : 0.f;
   }
 
   float xr[32];
@@ -508,17 +617,19 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
     ss = wave_sum(ss);
     apply_rmsnorm(a, ss, K, b, active, xr);
   }
-  float xs = 0.f;
-  if constexpr (TYPE != PBX_F32) {
+  float xs = 0.f, xlo = 0.f;
+  if constexpr (TYPE != PBX_F32 && TYPE != PBX_F16) {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) xs += xr[i];
+    for (int i = 0; i < 16; ++i) xlo += xr[i];
+    xs = xlo;
+#pragma unroll
+    for (int i = 16; i < 32; ++i) xs += xr[i];
   }
-  const float corr = TYPE == PBX_Q41 ? xs : BlockTraits<TYPE>::OFF * xs;
 
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const bool ok = active && row_ok(p * rpw + rs);
-    part[wave][p][lane] = ok ? block_term<TYPE>(q[p], xr, corr, d[p], mn[p]) : 0.f;
+    part[wave][p][lane] = ok ? block_term<TYPE>(q[p], ex[p], b, xr, xs, xlo, d[p], mn[p]) : 0.f;
   }
   __syncthreads();
   if constexpr (PAIR) {

@@ -152,6 +152,46 @@ extern "C" int pbx_quantize_q4_1(const float *w, int64_t N, int64_t K, uint8_t *
   return PBX_OK;
 }
 
+extern "C" int pbx_quantize_q6_k(const float *w, int64_t N, int64_t K, uint8_t *out) {
+  if (!w || !out || N <= 0 || K <= 0 || K % 256 != 0)
+    return pbx_fail(nullptr, PBX_EINVAL, "pbx_quantize_q6_k: bad arguments (N=%lld K=%lld)",
+                    (long long)N, (long long)K);
+  const int64_t blocks = N * (K / 256);
+#pragma omp parallel for schedule(static)
+  for (int64_t blk = 0; blk < blocks; ++blk) {
+    const float *x = w + blk * 256;
+    uint8_t *dst = out + blk * 210;
+    memset(dst, 0, 210);
+    double ideal[16], top = 0.0;
+    for (int s = 0; s < 16; ++s) {
+      double m = 0.0;
+      for (int i = 0; i < 16; ++i) m = std::max(m, fabs((double)x[16 * s + i]));
+      ideal[s] = m / 31.0;
+      top = std::max(top, ideal[s]);
+    }
+    const uint16_t hd = f64_to_f16_bits(top / 127.0);
+    dst[208] = (uint8_t)(hd & 0xFF);
+    dst[209] = (uint8_t)(hd >> 8);
+    const double d = f16_bits_to_f64(hd);
+    for (int s = 0; s < 16; ++s) {
+      const double sc = d > 0 ? std::min(127.0, js_round(ideal[s] / d)) : 0.0;
+      dst[192 + s] = (uint8_t)(int8_t)sc;
+      const double step = d * sc;
+      for (int i = 0; i < 16; ++i) {
+        const int e = 16 * s + i;
+        const double r = step > 0 ? js_round((double)x[e] / step) : 0.0;
+        const int q = (int)std::min(31.0, std::max(-32.0, r)) + 32;
+        // element e = 128*half + 32*g + l: low nibble in ql[64*half + 32*(g&1) + l]
+        // (high nibble for g >= 2), top two bits in qh[32*half + l] at 2*g
+        const int half = e / 128, g = (e % 128) / 32, l = e % 32;
+        dst[half * 64 + (g & 1) * 32 + l] |= (uint8_t)((q & 15) << (4 * (g >> 1)));
+        dst[128 + half * 32 + l] |= (uint8_t)(((q >> 4) & 3) << (2 * g));
+      }
+    }
+  }
+  return PBX_OK;
+}
+
 extern "C" int pbx_quantize_q8_ref(const float *w, int64_t n, int8_t *q, float *scales) {
   if (!w || !q || !scales || n <= 0)
     return pbx_fail(nullptr, PBX_EINVAL, "pbx_quantize_q8_ref: bad arguments");

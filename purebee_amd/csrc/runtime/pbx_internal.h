@@ -20,6 +20,15 @@
   X(PBX_K_GEMV_Q4_1_WIDE_R8, "pbx_gemv_q4_1_wide_r8")        \
   X(PBX_K_GEMV_Q4_1_WIDE_R16, "pbx_gemv_q4_1_wide_r16")      \
   X(PBX_K_GEMV_Q4_1_SMALL, "pbx_gemv_q4_1_small")            \
+  X(PBX_K_REPACK_Q6_K, "pbx_repack_q6_k")                    \
+  X(PBX_K_DEQUANT_F16, "pbx_dequant_f16")                    \
+  X(PBX_K_DEQUANT_Q6_K, "pbx_dequant_q6_k")                  \
+  X(PBX_K_GEMV_F16_WIDE_R4, "pbx_gemv_f16_wide_r4")          \
+  X(PBX_K_GEMV_F16_WIDE_R8, "pbx_gemv_f16_wide_r8")          \
+  X(PBX_K_GEMV_F16_SMALL, "pbx_gemv_f16_small")              \
+  X(PBX_K_GEMV_Q6_K_WIDE_R4, "pbx_gemv_q6_k_wide_r4")        \
+  X(PBX_K_GEMV_Q6_K_WIDE_R8, "pbx_gemv_q6_k_wide_r8")        \
+  X(PBX_K_GEMV_Q6_K_SMALL, "pbx_gemv_q6_k_small")            \
   X(PBX_K_DEQUANT_Q4_0, "pbx_dequant_q4_0")                  \
   X(PBX_K_DEQUANT_Q8_0, "pbx_dequant_q8_0")                  \
   X(PBX_K_DEQUANT_Q8REF, "pbx_dequant_q8ref")                \
@@ -106,7 +115,8 @@ int pbx_gemm_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M
                      const float *dBias, float *dY, hipStream_t stream);
 int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
                     const float *dBias, float *dY, int accumulate, hipStream_t stream);
-size_t pbx_type_block_bytes(int type);
+// Bytes of one GGUF row of K elements (0 for an unknown type).
+size_t pbx_type_row_bytes(int type, int64_t K);
 void pbx_model_release_all(pbx_ctx *c);
 int pbx_model_clear_range(pbx_model *m, int from, int to);
 const pbx_model_config *pbx_model_cfg(const pbx_model *m);

@@ -106,12 +106,26 @@ struct Layer {
 };
 
 const char *type_tag(int t) {
-  return t == PBX_TYPE_Q4_0 ? "q4" : t == PBX_TYPE_Q4_1 ? "q41" : t == PBX_TYPE_Q8_0 ? "q8" : "f32";
+  switch (t) {
+    case PBX_TYPE_Q4_0: return "q4";
+    case PBX_TYPE_Q4_1: return "q41";
+    case PBX_TYPE_Q8_0: return "q8";
+    case PBX_TYPE_F16: return "f16";
+    case PBX_TYPE_Q6_K: return "q6k";
+    default: return "f32";
+  }
 }
 
-// PBX_Q4 / PBX_Q8 / PBX_F32 / PBX_Q41 of pbx_gemv_impl.h
+// PBX_Q4 / PBX_Q8 / PBX_F32 / PBX_Q41 / PBX_F16 / PBX_Q6K of pbx_gemv_impl.h
 int kernel_type(int t) {
-  return t == PBX_TYPE_Q4_0 ? 0 : t == PBX_TYPE_Q8_0 ? 1 : t == PBX_TYPE_Q4_1 ? 3 : 2;
+  switch (t) {
+    case PBX_TYPE_Q4_0: return 0;
+    case PBX_TYPE_Q8_0: return 1;
+    case PBX_TYPE_Q4_1: return 3;
+    case PBX_TYPE_F16: return 4;
+    case PBX_TYPE_Q6_K: return 5;
+    default: return 2;
+  }
 }
 
 }  // namespace
@@ -190,7 +204,7 @@ static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, int type, int N
   }
   const bool q4 = type == PBX_TYPE_Q4_0 || type == PBX_TYPE_Q4_1;
   if (B <= 32) {
-    const int P = q4 ? 8 : type == PBX_TYPE_Q8_0 ? 4 : 2;
+    const int P = q4 ? 8 : type == PBX_TYPE_F32 ? 2 : 4;
     const int T = P * (64 / B);
     const int gx = (N + 4 * T - 1) / (4 * T);
     *shape = "s";
@@ -204,7 +218,7 @@ static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, int type, int N
   int R;
   if (q4)
     R = (N / 16 >= target) ? 16 : (N / 8 >= target) ? 8 : 4;
-  else if (type == PBX_TYPE_Q8_0)
+  else if (type == PBX_TYPE_Q8_0 || type == PBX_TYPE_F16 || type == PBX_TYPE_Q6_K)
     R = (N / 8 >= target) ? 8 : 4;
   else
     R = (N / 4 >= target) ? 4 : 2;
@@ -235,7 +249,7 @@ static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const c
   op.role = role;
   // weights + activation reads (+ up for SwiGLU, + norm weight) + output
   // (read and written for the residual epilogue)
-  op.bytes = (double)w->N * w->B * pbx_type_block_bytes(w->type) + 4.0 * w->K * (X2 ? 2 : 1) +
+  op.bytes = (double)w->N * pbx_type_row_bytes(w->type, w->K) + 4.0 * w->K * (X2 ? 2 : 1) +
              (normw ? 4.0 * w->K : 0.0) +
              (strcmp(mode, "add") == 0 ? 8.0 * w->N : strcmp(mode, "gu") == 0 ? 2.0 * w->N : 4.0 * w->N);
   if (n_tiles_out) *n_tiles_out = n_tiles;
@@ -255,7 +269,7 @@ static int build_ops(pbx_model *m) {
   e.grid = dim3((g.dim + 255) / 256);
   e.block = dim3(256);
   e.role = "embed";
-  e.bytes = (double)g.dim / 32 * pbx_type_block_bytes(m->embd->type) + 4.0 * g.dim;
+  e.bytes = (double)pbx_type_row_bytes(m->embd->type, g.dim) + 4.0 * g.dim;
   e.embed = EmbedArgsHost{m->embd->qs, m->embd->d, m->x, m->state, kernel_type(m->embd->type),
                           g.dim, g.vocab_size, m->embd->m};
   m->ops.push_back(e);
@@ -473,7 +487,8 @@ static bool split_attention_disabled() {
 }
 
 static bool is_weight_type(int t) {
-  return t == PBX_TYPE_Q4_0 || t == PBX_TYPE_Q4_1 || t == PBX_TYPE_Q8_0 || t == PBX_TYPE_F32;
+  return t == PBX_TYPE_Q4_0 || t == PBX_TYPE_Q4_1 || t == PBX_TYPE_Q8_0 || t == PBX_TYPE_F32 ||
+         t == PBX_TYPE_F16 || t == PBX_TYPE_Q6_K;
 }
 
 extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_model **out) {
@@ -593,7 +608,7 @@ extern "C" int pbx_model_free(pbx_model *m) {
 }
 
 static size_t expect_bytes(int type, int64_t N, int64_t K) {
-  return (size_t)N * (size_t)(K / 32) * pbx_type_block_bytes(type);
+  return (size_t)N * pbx_type_row_bytes(type, K);
 }
 
 extern "C" int pbx_model_set_tensor(pbx_model *m, int tensor, int layer, const void *data,

@@ -289,7 +289,7 @@ static int stage_repack(pbx_ctx *c, pbx_weight *w, int64_t first_row, int64_t n_
     memcpy(c->h_stage[slot], src + (size_t)r0 * row_bytes, n);
     HIPCHK(c, hipMemcpyAsync(c->d_stage[slot], c->h_stage[slot], n, hipMemcpyHostToDevice,
                              c->stream));
-    int B = (int)w->B;
+    int B = (int)(kernel == PBX_K_REPACK_Q6_K ? w->K / 256 : w->B);  // blocks per row
     int64_t row0 = first_row + r0, nrows = rows;
     void *raw = c->d_stage[slot];
     void *args[] = {&raw, &w->qs, &w->d, &row0, &nrows, &B};
@@ -305,12 +305,14 @@ static int stage_repack(pbx_ctx *c, pbx_weight *w, int64_t first_row, int64_t n_
   return PBX_OK;
 }
 
-size_t pbx_type_block_bytes(int type) {
+size_t pbx_type_row_bytes(int type, int64_t K) {
   switch (type) {
-    case PBX_TYPE_Q4_0: return 18;
-    case PBX_TYPE_Q4_1: return 20;
-    case PBX_TYPE_Q8_0: return 34;
-    case PBX_TYPE_F32: return 128;
+    case PBX_TYPE_Q4_0: return (size_t)(K / 32) * 18;
+    case PBX_TYPE_Q4_1: return (size_t)(K / 32) * 20;
+    case PBX_TYPE_Q8_0: return (size_t)(K / 32) * 34;
+    case PBX_TYPE_Q6_K: return (size_t)(K / 256) * 210;
+    case PBX_TYPE_F16: return (size_t)K * 2;
+    case PBX_TYPE_F32: return (size_t)K * 4;
     default: return 0;
   }
 }
@@ -319,16 +321,18 @@ static bool weight_ok(const pbx_weight *w) { return w && w->magic == PBX_WEIGHT_
 
 static bool upload_type(int type) {
   return type == PBX_TYPE_Q4_0 || type == PBX_TYPE_Q4_1 || type == PBX_TYPE_Q8_0 ||
-         type == PBX_TYPE_F32;
+         type == PBX_TYPE_Q6_K || type == PBX_TYPE_F16 || type == PBX_TYPE_F32;
 }
+
+static int64_t k_multiple(int type) { return type == PBX_TYPE_Q6_K ? 256 : 32; }
 
 int pbx_weight_alloc(pbx_ctx *c, int type, int64_t N, int64_t K, pbx_weight **out) {
   *out = nullptr;
   if (!upload_type(type))
     return pbx_fail(c, PBX_EINVAL, "unsupported weight type %d", type);
-  if (N <= 0 || K <= 0 || K % 32 != 0)
-    return pbx_fail(c, PBX_EINVAL, "bad shape N=%lld K=%lld (need N>0, K>0, K%%32==0)",
-                    (long long)N, (long long)K);
+  if (N <= 0 || K <= 0 || K % k_multiple(type) != 0)
+    return pbx_fail(c, PBX_EINVAL, "bad shape N=%lld K=%lld (need N>0, K>0, K%%%lld==0)",
+                    (long long)N, (long long)K, (long long)k_multiple(type));
   if (N > INT32_MAX || K / 32 > (1 << 20))
     return pbx_fail(c, PBX_ENOTSUP, "shape N=%lld K=%lld too large", (long long)N, (long long)K);
   HIPCHK(c, hipSetDevice(c->device));
@@ -340,8 +344,11 @@ int pbx_weight_alloc(pbx_ctx *c, int type, int64_t N, int64_t K, pbx_weight **ou
   w->B = K / 32;
   w->Npad = (N + 63) / 64 * 64;
   size_t qs_bytes, d_bytes = 0;
-  if (type == PBX_TYPE_F32) {
-    qs_bytes = (size_t)w->Npad * K * 4;
+  if (type == PBX_TYPE_F32 || type == PBX_TYPE_F16) {
+    qs_bytes = (size_t)w->Npad * K * (type == PBX_TYPE_F32 ? 4 : 2);
+  } else if (type == PBX_TYPE_Q6_K) {
+    qs_bytes = (size_t)w->Npad * (K / 256) * 208;
+    d_bytes = (size_t)w->Npad * (K / 256) * 2;
   } else {
     qs_bytes = (size_t)w->Npad * w->B * (type == PBX_TYPE_Q8_0 ? 32 : 16);
     d_bytes = (size_t)w->Npad * w->B * 2;
@@ -383,11 +390,12 @@ int pbx_weight_write_rows(pbx_ctx *c, pbx_weight *w, int64_t row0, int64_t rows,
   if (row0 < 0 || rows <= 0 || row0 + rows > w->N)
     return pbx_fail(c, PBX_EINVAL, "rows [%lld, %lld) outside a weight of %lld rows",
                     (long long)row0, (long long)(row0 + rows), (long long)w->N);
-  const size_t row_bytes = (size_t)w->B * pbx_type_block_bytes(w->type);
-  if (w->type == PBX_TYPE_F32)
+  const size_t row_bytes = pbx_type_row_bytes(w->type, w->K);
+  if (w->type == PBX_TYPE_F32 || w->type == PBX_TYPE_F16)
     return stage_copy(c, (char *)w->qs + (size_t)row0 * row_bytes, host, (size_t)rows * row_bytes);
   const int k = w->type == PBX_TYPE_Q4_0   ? PBX_K_REPACK_Q4_0
                 : w->type == PBX_TYPE_Q4_1 ? PBX_K_REPACK_Q4_1
+                : w->type == PBX_TYPE_Q6_K ? PBX_K_REPACK_Q6_K
                                            : PBX_K_REPACK_Q8_0;
   return stage_repack(c, w, row0, rows, (const uint8_t *)host, k, row_bytes);
 }
@@ -399,12 +407,12 @@ extern "C" int pbx_weight_upload(pbx_ctx *c, int type, int64_t N, int64_t K,
   *out = nullptr;
   if (!upload_type(type))
     return pbx_fail(c, PBX_EINVAL, "pbx_weight_upload: unsupported weight type %d", type);
-  if (N <= 0 || K <= 0 || K % 32 != 0)
+  if (N <= 0 || K <= 0 || K % k_multiple(type) != 0)
     return pbx_fail(c, PBX_EINVAL,
-                    "pbx_weight_upload: bad shape N=%lld K=%lld (need N>0, K>0, K%%32==0)",
-                    (long long)N, (long long)K);
+                    "pbx_weight_upload: bad shape N=%lld K=%lld (need N>0, K>0, K%%%lld==0)",
+                    (long long)N, (long long)K, (long long)k_multiple(type));
   if (!host) return pbx_fail(c, PBX_EINVAL, "pbx_weight_upload: host buffer is NULL");
-  const size_t need = (size_t)N * (size_t)(K / 32) * pbx_type_block_bytes(type);
+  const size_t need = (size_t)N * pbx_type_row_bytes(type, K);
   if (nbytes < need)
     return pbx_fail(c, PBX_EINVAL,
                     "pbx_weight_upload: buffer holds %zu bytes, N=%lld x K=%lld needs %zu",
@@ -509,11 +517,13 @@ int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t
   const bool q4 = w->type == PBX_TYPE_Q4_0 || w->type == PBX_TYPE_Q4_1;
   if (B <= 32) {
     // Small-K path: 4 waves per workgroup, each wave a tile of P*(64/B) rows.
-    const int P = q4 ? 8 : w->type == PBX_TYPE_Q8_0 ? 4 : 2;
+    const int P = q4 ? 8 : w->type == PBX_TYPE_F32 ? 2 : 4;
     const int T = P * (64 / B);
     const int k = w->type == PBX_TYPE_Q4_0   ? PBX_K_GEMV_Q4_0_SMALL
                   : w->type == PBX_TYPE_Q4_1 ? PBX_K_GEMV_Q4_1_SMALL
                   : w->type == PBX_TYPE_Q8_0 ? PBX_K_GEMV_Q8_0_SMALL
+                  : w->type == PBX_TYPE_F16  ? PBX_K_GEMV_F16_SMALL
+                  : w->type == PBX_TYPE_Q6_K ? PBX_K_GEMV_Q6_K_SMALL
                                              : PBX_K_GEMV_F32_SMALL;
     return pbx_launch(c, k, dim3((unsigned)((N + 4 * T - 1) / (4 * T)), gy), dim3(256), args,
                       stream);
@@ -533,6 +543,12 @@ int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t
   } else if (w->type == PBX_TYPE_Q8_0) {
     if (N / 8 >= target) { R = 8; k = PBX_K_GEMV_Q8_0_WIDE_R8; }
     else { R = 4; k = PBX_K_GEMV_Q8_0_WIDE_R4; }
+  } else if (w->type == PBX_TYPE_F16) {
+    if (N / 8 >= target) { R = 8; k = PBX_K_GEMV_F16_WIDE_R8; }
+    else { R = 4; k = PBX_K_GEMV_F16_WIDE_R4; }
+  } else if (w->type == PBX_TYPE_Q6_K) {
+    if (N / 8 >= target) { R = 8; k = PBX_K_GEMV_Q6_K_WIDE_R8; }
+    else { R = 4; k = PBX_K_GEMV_Q6_K_WIDE_R4; }
   } else {
     if (N / 4 >= target) { R = 4; k = PBX_K_GEMV_F32_WIDE_R4; }
     else { R = 2; k = PBX_K_GEMV_F32_WIDE_R2; }
@@ -603,6 +619,17 @@ extern "C" int pbx_dequant_dev(pbx_ctx *c, const pbx_weight *w, float *dY) {
   if (w->type == PBX_TYPE_Q4_1) {
     void *args[] = {(void *)&w->qs, (void *)&w->d, (void *)&w->m, &dY, &N, &B};
     return pbx_launch(c, PBX_K_DEQUANT_Q4_1, dim3((unsigned)((blocks + 255) / 256)), dim3(256),
+                      args);
+  }
+  if (w->type == PBX_TYPE_F16) {
+    int64_t n = w->N * w->K;
+    void *args[] = {(void *)&w->qs, &dY, &n};
+    return pbx_launch(c, PBX_K_DEQUANT_F16, dim3((unsigned)((n + 255) / 256)), dim3(256), args);
+  }
+  if (w->type == PBX_TYPE_Q6_K) {
+    int SB = (int)(w->K / 256);
+    void *args[] = {(void *)&w->qs, (void *)&w->d, &dY, &N, &SB};
+    return pbx_launch(c, PBX_K_DEQUANT_Q6_K, dim3((unsigned)((blocks + 255) / 256)), dim3(256),
                       args);
   }
   void *args[] = {(void *)&w->qs, (void *)&w->d, &dY, &N, &B};

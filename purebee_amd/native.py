@@ -12,9 +12,11 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(PKG, "lib")
 
 TYPE_F32 = 0
+TYPE_F16 = 1
 TYPE_Q4_0 = 2
 TYPE_Q4_1 = 3
 TYPE_Q8_0 = 8
+TYPE_Q6_K = 14
 TYPE_Q8_REF = 100
 
 STATUS = {0: "PBX_OK", -1: "PBX_EINVAL", -2: "PBX_ENODEV", -3: "PBX_ENOMEM",
@@ -25,7 +27,8 @@ EXPORTS = (
     "pbx_init", "pbx_shutdown", "pbx_last_error", "pbx_device_info",
     "pbx_weight_upload", "pbx_weight_upload_q8ref", "pbx_weight_free", "pbx_weight_info",
     "pbx_linear", "pbx_linear_dev", "pbx_dequant", "pbx_dequant_dev",
-    "pbx_quantize_q8_0", "pbx_quantize_q4_0", "pbx_quantize_q4_1", "pbx_quantize_q8_ref",
+    "pbx_quantize_q8_0", "pbx_quantize_q4_0", "pbx_quantize_q4_1", "pbx_quantize_q6_k",
+    "pbx_quantize_q8_ref",
     "pbx_synth_normal",
     "pbx_dev_alloc", "pbx_dev_free", "pbx_memcpy_h2d", "pbx_memcpy_d2h", "pbx_memset_dev",
     "pbx_dev_copy", "pbx_sync", "pbx_timer_start", "pbx_timer_stop", "pbx_bench_linear",
@@ -102,6 +105,7 @@ def load_library():
         "pbx_quantize_q8_0": (ctypes.c_int, [_f32p, _i64, _i64, _u8p]),
         "pbx_quantize_q4_0": (ctypes.c_int, [_f32p, _i64, _i64, _u8p]),
         "pbx_quantize_q4_1": (ctypes.c_int, [_f32p, _i64, _i64, _u8p]),
+        "pbx_quantize_q6_k": (ctypes.c_int, [_f32p, _i64, _i64, _u8p]),
         "pbx_quantize_q8_ref": (ctypes.c_int, [_f32p, _i64, _i8p, _f32p]),
         "pbx_synth_normal": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_double,
                                             ctypes.c_double, _f32p]),
@@ -154,7 +158,13 @@ def _check(rc, ctx_ptr=None):
 
 
 def block_bytes(t):
-    return {TYPE_Q4_0: 18, TYPE_Q4_1: 20, TYPE_Q8_0: 34, TYPE_F32: 128}[t]
+    """Bytes per 32 elements (Q6_K: per 256, see row_bytes)."""
+    return {TYPE_Q4_0: 18, TYPE_Q4_1: 20, TYPE_Q8_0: 34, TYPE_F32: 128, TYPE_F16: 64}[t]
+
+
+def row_bytes(t, K):
+    """Bytes of one GGUF row of K elements."""
+    return K // 256 * 210 if t == TYPE_Q6_K else K // 32 * block_bytes(t)
 
 
 def quantize_q8_0(w):
@@ -179,6 +189,19 @@ def quantize_q4_1(w):
     out = np.empty(N * (K // 32) * 20, np.uint8)
     _check(load_library().pbx_quantize_q4_1(w, N, K, out))
     return out
+
+
+def quantize_q6_k(w):
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    out = np.empty(N * (K // 256) * 210, np.uint8)
+    _check(load_library().pbx_quantize_q6_k(w, N, K, out))
+    return out
+
+
+def to_f16_bytes(w):
+    """GGUF F16 bytes of w (round to nearest even)."""
+    return np.ascontiguousarray(w, np.float32).astype(np.float16).view(np.uint8).ravel()
 
 
 def quantize_q8_ref(w):

@@ -9,7 +9,8 @@ loads (gguf.js:378-410): matrices are [out_features, in_features].
 import numpy as np
 
 from . import native
-from .native import (Model, TYPE_F32, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q8_0, T_TOKEN_EMBD, T_OUTPUT,
+from .native import (Model, TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q6_K, TYPE_Q8_0,
+                     T_TOKEN_EMBD, T_OUTPUT,
                      T_OUTPUT_NORM, T_ATTN_NORM, T_FFN_NORM, T_ATTN_Q, T_ATTN_K, T_ATTN_V,
                      T_ATTN_OUTPUT, T_FFN_GATE, T_FFN_UP, T_FFN_DOWN)
 
@@ -59,7 +60,8 @@ def make_tensor(spec, base_seed, index):
     if t == TYPE_F32:
         return w
     return {TYPE_Q4_0: native.quantize_q4_0, TYPE_Q4_1: native.quantize_q4_1,
-            TYPE_Q8_0: native.quantize_q8_0}[t](w)
+            TYPE_Q8_0: native.quantize_q8_0, TYPE_Q6_K: native.quantize_q6_k,
+            TYPE_F16: native.to_f16_bytes}[t](w)
 
 
 def build(ctx, cfg, seed=1000, keep=None):

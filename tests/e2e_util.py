@@ -4,7 +4,7 @@ import numpy as np
 
 import oracle
 from purebee_amd import synth
-from purebee_amd.native import TYPE_F32, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q8_0
+from purebee_amd.native import TYPE_F32
 
 LOGIT_TOL = 2e-3  # max-abs on logits
 
@@ -21,12 +21,8 @@ def make_pair(ctx, cfg, seed=1000):
         tid, layer, N, K, t = spec
         if t == TYPE_F32:
             f = np.asarray(data, np.float32)
-        elif t == TYPE_Q4_0:
-            f = oracle.dequant_q4_0(data, N * K)
-        elif t == TYPE_Q4_1:
-            f = oracle.dequant_q4_1(data, N * K)
         else:
-            f = oracle.dequant_q8_0(data, N * K)
+            f = oracle.dequant(t, data, N * K)
         ref.set(tid, layer, f)
 
     model = synth.build(ctx, cfg, seed, keep)

@@ -10,7 +10,7 @@ import pytest
 
 import oracle
 from purebee_amd import PbxError, synth
-from purebee_amd.native import TYPE_F32, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q8_0
+from purebee_amd.native import TYPE_F16, TYPE_F32, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q6_K, TYPE_Q8_0
 from tests.e2e_util import LOGIT_TOL, check_greedy, make_pair
 
 pytestmark = pytest.mark.gpu
@@ -50,7 +50,8 @@ def run_prompt_then_greedy(ctx, cfg, n_prompt, n_gen, seed):
 
 @pytest.mark.parametrize("wt,et", [(TYPE_Q4_0, TYPE_Q4_0), (TYPE_Q8_0, TYPE_Q8_0),
                                    (TYPE_Q8_0, TYPE_F32), (TYPE_F32, TYPE_F32),
-                                   (TYPE_Q4_1, TYPE_Q4_1)])
+                                   (TYPE_Q4_1, TYPE_Q4_1), (TYPE_Q4_0, TYPE_Q6_K),
+                                   (TYPE_F16, TYPE_F16)])
 def test_tiny_model_prefill_and_greedy(ctx, wt, et):
     print(f"[case] tiny model weights={wt} embed={et}", flush=True)
     exact, ties, e1, e2 = run_prompt_then_greedy(ctx, tiny(wt, et), 8, 24, seed=50 + wt)

@@ -167,6 +167,47 @@ def test_q4_1_multi_row(ctx, M):
     w.free()
 
 
+def gguf_bytes(t, W):
+    """W as the GGUF bytes of type t (F16 halves, or oracle-quantised Q6_K)."""
+    if t == pb.TYPE_F16:
+        return W.astype(np.float16).view(np.uint8).ravel()
+    return oracle.quantize_q6_k(W)
+
+
+EMBED_SHAPES = [(1000, 2048), (300, 576 // 32 * 32), (77, 256), (129, 1024), (64, 8192)]
+
+
+@pytest.mark.parametrize("t", [pb.TYPE_F16, pb.TYPE_Q6_K])
+@pytest.mark.parametrize("N,K", EMBED_SHAPES)
+def test_f16_q6_k_dequant_and_matvec(ctx, t, N, K):
+    """F16 / Q6_K weights (gguf.js:231-237, 317-364): dequantisation
+    bit-exact; the matvec against the reference's route for these types
+    (dequantise to f32, then the f32 matvec) at 1e-5 relative L2."""
+    if t == pb.TYPE_Q6_K and K % 256:
+        K = K // 256 * 256 or 256
+    print(f"[case] type={t} N={N} K={K}", flush=True)
+    W = synth_matrix(N * 3 + K + t, N, K)
+    raw = gguf_bytes(t, W)
+    w = ctx.upload(t, N, K, raw)
+    got = ctx.dequant(w)
+    ref = oracle.dequant(t, raw, N * K).reshape(N, K)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    x = pb.synth_normal(N + K, K)
+    y = ctx.linear(w, x)
+    assert rel_l2(y, oracle.matvec(t, x, raw, N, K)) < 1e-5
+    X = pb.synth_normal(N + K + 1, 3 * K).reshape(3, K)
+    Y = ctx.linear(w, X)
+    for m in range(3):
+        assert rel_l2(Y[m], oracle.matvec(t, X[m], raw, N, K)) < 1e-5
+    w.free()
+
+
+def test_q6_k_rejects_k_not_multiple_of_256(ctx):
+    print("[case] q6_k K % 256", flush=True)
+    with pytest.raises(pb.PbxError):
+        ctx.upload(pb.TYPE_Q6_K, 4, 288, np.zeros(4 * 2 * 210, np.uint8))
+
+
 @pytest.mark.parametrize("t", QUANT + [pb.TYPE_F32])
 def test_bias_and_multi_row(ctx, t):
     N, K, M = 576, 576, 5

@@ -244,6 +244,87 @@ def test_q4_1_matvec_restatements_agree_and_are_linear():
     assert rel_l2(lin, js + 2 * oracle.q4_1_matvec_js(x2, raw, N, K)) < 1e-6
 
 
+def q6k_block(d=1.0, scales=None, ql=None, qh=None):
+    blk = np.zeros(210, np.uint8)
+    if ql is not None:
+        blk[:128] = ql
+    if qh is not None:
+        blk[128:192] = qh
+    blk[192:208] = (np.ones(16, np.int8) if scales is None else np.asarray(scales, np.int8)).view(np.uint8)
+    blk[208:210] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    return blk
+
+
+def test_q6_k_dequant_known_positions():
+    """gguf.js:317-364 by single-byte probes: with every code at its zero
+    point (ql = 0, qh = 0 gives q = -32) a probe byte moves exactly the
+    elements the layout names, by the amount it names."""
+    base = oracle.dequant_q6_k(q6k_block(), 256)
+    assert np.all(base == -32.0)
+    cases = [  # (array, index, value) -> {element: code}
+        ("ql", 5, 0x0F, {5: 15}),            # low nibble of ql[l]      -> l
+        ("ql", 37, 0x0F, {37: 15}),          # low nibble of ql[l + 32] -> l + 32
+        ("ql", 5, 0xF0, {69: 15}),           # high nibble of ql[l]     -> l + 64
+        ("ql", 37, 0xA0, {101: 10}),         # high nibble of ql[l+32]  -> l + 96
+        ("ql", 64 + 3, 0x01, {131: 1}),      # second half: + 128
+        ("qh", 7, 0b11100100, {7: 0, 39: 16, 71: 32, 103: 48}),  # 2-bit fields 0..3
+        ("qh", 32 + 31, 0b00000011, {159: 48}),
+    ]
+    for arr, idx, val, want in cases:
+        ql = np.zeros(128, np.uint8)
+        qh = np.zeros(64, np.uint8)
+        (ql if arr == "ql" else qh)[idx] = val
+        out = oracle.dequant_q6_k(q6k_block(ql=ql, qh=qh), 256)
+        exp = np.full(256, -32.0, np.float32)
+        for e, code in want.items():
+            exp[e] = code - 32
+        assert np.array_equal(out, exp), (arr, idx, np.nonzero(out != exp))
+
+
+def test_q6_k_dequant_scales_and_d():
+    # element e uses int8 scale e // 16 (is = 8*half + l/16, + 2 per group)
+    scales = np.arange(-8, 8, dtype=np.int8) * 3
+    out = oracle.dequant_q6_k(q6k_block(d=0.5, scales=scales), 256)
+    exp = np.repeat(scales.astype(np.float64), 16) * 0.5 * -32
+    assert np.array_equal(out, exp.astype(np.float32))
+    # subnormal d, the largest |scale| and the top code: exact in f32
+    ql = np.full(128, 0xFF, np.uint8)
+    qh = np.full(64, 0xFF, np.uint8)
+    out = oracle.dequant_q6_k(q6k_block(d=2.0 ** -20, scales=[-128] * 16, ql=ql, qh=qh), 256)
+    assert np.all(out == np.float32(2.0 ** -20 * -128 * 31))
+    # a short last block is truncated
+    blk = np.concatenate([q6k_block(scales=scales), q6k_block(d=2.0)])
+    assert np.array_equal(oracle.dequant_q6_k(blk, 300), oracle.dequant_q6_k(blk, 512)[:300])
+
+
+def test_f16_dequant_all_patterns():
+    bits = np.arange(65536, dtype=np.uint16)
+    got = oracle.dequant_f16(bits.view(np.uint8), 65536)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_q6_k_quantizer_invariants():
+    rng = np.random.default_rng(17)
+    w = rng.normal(0, 0.02, (4, 512)).astype(np.float32)
+    w[1, :256] = 0
+    raw = oracle.quantize_q6_k(w)
+    W = oracle.dequant_q6_k(raw, w.size).reshape(-1, 256)
+    blocks = w.reshape(-1, 256).astype(np.float64)
+    assert np.all(W[2] == 0)   # row 1, block 0: all zero
+    d = raw.reshape(-1, 210)[:, 208:210].copy().view(np.float16).astype(np.float64).ravel()
+    sc = raw.reshape(-1, 210)[:, 192:208].view(np.int8).astype(np.float64)
+    step = d[:, None] * sc                      # per 16-element sub-block
+    err = np.abs(W.astype(np.float64) - blocks).reshape(-1, 16, 16)
+    # half a step, plus the edge where x / step rounds past 31 (<= one step)
+    assert np.all(err <= step[:, :, None] * 1.0 + 1e-12)
+    assert np.mean(err <= step[:, :, None] * 0.5 + 1e-12) > 0.99
+    # quantise -> dequantise is close in L2
+    assert rel_l2(W.ravel(), blocks.ravel()) < 0.05
+
+
 def test_cpu_pool_partition_matches_single_thread():
     rng = np.random.default_rng(11)
     N, K = 1003, 256
@@ -367,6 +448,9 @@ def test_product_and_oracle_quantisers_agree():
     assert np.array_equal(pb.quantize_q8_0(w), oracle.quantize_q8_0(w))
     assert np.array_equal(pb.quantize_q4_0(w), oracle.quantize_q4_0(w))
     assert np.array_equal(pb.quantize_q4_1(w), oracle.quantize_q4_1(w))
+    w6 = rng.normal(0, 0.02, (5, 512)).astype(np.float32)
+    w6[2, :256] = 0
+    assert np.array_equal(pb.quantize_q6_k(w6), oracle.quantize_q6_k(w6))
     q1, s1 = pb.quantize_q8_ref(w)
     q2, s2 = oracle.quantize_q8_ref(w)
     assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
