@@ -37,6 +37,7 @@ extern "C" {
 #define PBX_EHIP     -4   /* a HIP runtime call failed                       */
 #define PBX_ENOTSUP  -5   /* shape or type not supported by any kernel       */
 #define PBX_ELOAD    -6   /* code object missing or not loadable (hipModuleLoad) */
+#define PBX_EIO      -7   /* a file could not be opened or mapped            */
 
 /* ---- weight types ----------------------------------------------------
  * GGML numbering, as gguf.js:30-33 (GGML_TYPE).  PBX_TYPE_Q8_REF is the
@@ -185,7 +186,7 @@ typedef struct pbx_model pbx_model;
 typedef struct pbx_model_config {
   int32_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim;
   int32_t vocab_size, max_seq;
-  int32_t weight_type;  /* every layer matrix: PBX_TYPE_Q4_0 / Q8_0 / F32  */
+  int32_t weight_type;  /* every layer matrix: any PBX_TYPE_* but Q8_REF    */
   int32_t embed_type;   /* token_embd (row lookup and, when tied, LM head) */
   int32_t output_type;  /* untied LM head type, or -1: tied to token_embd  */
   float rms_eps;        /* 1e-5 in the reference (purebee.js:164)         */
@@ -255,6 +256,57 @@ int pbx_model_op_name(const pbx_model *m, int i, char *buf, size_t cap);
 int pbx_model_bench_role(pbx_model *m, const char *role, int reps,
                          double *us_per_launch, double *bytes_per_launch,
                          int *launches_per_rep);
+
+/* ---- GGUF files ----------------------------------------------------------
+ * The build's own GGUF v2/v3 reader, replacing GGUFParser and parseHeader
+ * (gguf.js:76-194, streaming-loader.js:35-87): the file is mapped read-only,
+ * header, metadata and tensor table are parsed with bounds checks, and
+ * tensor data is served from the mapping (no copy).  Errors follow the
+ * reference's: bad magic, a version outside 2..3, a tensor type the
+ * reference cannot size (gguf.js:36-49, 206-213) fail the open.  pbx_gguf_*
+ * calls take no context; pbx_last_error(NULL) names the failure.
+ */
+typedef struct pbx_gguf pbx_gguf;
+
+typedef struct pbx_gguf_tensor {
+  const char *name;      /* NUL-terminated, valid until pbx_gguf_close      */
+  int32_t type;          /* GGML type id (gguf.js:30-33)                   */
+  int32_t n_dims;        /* 1..4                                            */
+  int64_t dims[4];       /* GGUF order: dims[0] = row length (K), dims[1] =
+                            rows (N); unused dims are 1                     */
+  uint64_t offset;       /* absolute file offset of the data                */
+  uint64_t nbytes;       /* tensorByteSize (gguf.js:206-213)                */
+  const void *data;      /* the bytes, inside the read-only mapping         */
+} pbx_gguf_tensor;
+
+int     pbx_gguf_open(const char *path, pbx_gguf **out);
+void    pbx_gguf_close(pbx_gguf *g);
+int     pbx_gguf_info(const pbx_gguf *g, uint32_t *version, int64_t *n_tensors,
+                      int64_t *n_kv, uint64_t *data_start);
+int     pbx_gguf_tensor_info(const pbx_gguf *g, int64_t i, pbx_gguf_tensor *out);
+int64_t pbx_gguf_find_tensor(const pbx_gguf *g, const char *name);  /* -1: absent */
+/* Metadata by key: integers (any integer type or bool), floats (f32/f64 or
+ * an integer), strings (pointer into the mapping, not NUL-terminated),
+ * arrays (element type and count). */
+int pbx_gguf_get_int(const pbx_gguf *g, const char *key, int64_t *out);
+int pbx_gguf_get_float(const pbx_gguf *g, const char *key, double *out);
+int pbx_gguf_get_string(const pbx_gguf *g, const char *key, const char **str, uint64_t *len);
+int pbx_gguf_get_array(const pbx_gguf *g, const char *key, uint32_t *elem_type,
+                       uint64_t *count);
+/* extractConfig (gguf.js:429-450) under general.architecture with the
+ * reference's defaults (head_count_kv = head_count, rms eps 1e-5, rope
+ * freq_base 10000); vocab_size = the tokenizer's token count
+ * (streaming-loader.js:57) or token_embd's rows; weight/embed/output types
+ * from blk.0.attn_q / token_embd / output (-1: tied).  max_seq <= 0 takes
+ * min(context_length, 8192). */
+int pbx_gguf_model_config(const pbx_gguf *g, int max_seq, pbx_model_config *cfg);
+/* loadGGUFModel (gguf.js:778-839) / StreamingLlamaRuntime's loader
+ * (streaming-loader.js:245-335) as one step: open, configure, create the
+ * model and upload every tensor once, names mapped as gguf.js:378-410.
+ * Token embedding and output rows past the vocabulary are not uploaded.
+ * Tensors outside the Llama layout, layer matrices of mixed types and
+ * shapes that disagree with the metadata are errors. */
+int pbx_model_load_gguf(pbx_ctx *ctx, const char *path, int max_seq, pbx_model **out);
 
 /* ---- speculative decoding ----------------------------------------------
  * SelfSpeculativeDecoder.generate (speculative.js:58-204) in its greedy

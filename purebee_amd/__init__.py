@@ -7,7 +7,7 @@ the gfx950 code objects ``lib/*.hsaco`` with hipModuleLoad), the N-API addon
 Python callers (tests, bench).
 """
 from .native import (  # noqa: F401
-    PbxError, Context, Weight, Model, ModelConfig, load_library, library_path,
+    PbxError, Context, Weight, Model, ModelConfig, GGUF, load_library, library_path,
     TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q8_0, TYPE_Q6_K, TYPE_Q8_REF, row_bytes,
     quantize_q4_0, quantize_q4_1, quantize_q6_k, quantize_q8_0, to_f16_bytes, quantize_q8_ref, synth_normal, block_bytes,
     speculative_generate,

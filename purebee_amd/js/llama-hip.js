@@ -14,6 +14,7 @@
  *   rt.loadTensor('token_embd.weight', rawBlocks);   // per GGUF tensor
  *   const logits = rt.forward(promptTokens, 0);       // llama.js:204
  *   const out = rt.generate(promptTokens, 64, { greedy: true });
+ *   const rt2 = HipLlamaRuntime.fromGGUF('model.gguf', { maxSeq: 2048 });
  *
  * HipSpeculativeDecoder follows SelfSpeculativeDecoder.generate
  * (speculative.js:58-204) in greedy mode with a separate draft model.
@@ -53,11 +54,25 @@ function tensorId(name) {
 }
 
 class HipLlamaRuntime {
-  constructor(config) {
+  /**
+   * A resident model straight from a GGUF file (the build's reader; weights
+   * uploaded once), configured from its metadata like loadGGUFModel /
+   * parseHeader (gguf.js:778-839, streaming-loader.js:35-87).
+   */
+  static fromGGUF(filePath, opts = {}) {
+    const r = load().modelLoadGGUF(String(filePath), opts.maxSeq || 0);
+    return new HipLlamaRuntime(r.config, r.model);
+  }
+
+  constructor(config, handle) {
     const a = load();
     const c = config;
     this.config = Object.assign({}, c);
     this.config.headDim = c.headDim || Math.floor(c.dim / c.nHeads);
+    if (handle) {
+      this._model = handle;
+      return;
+    }
     this._model = a.modelCreate({
       dim: c.dim, hiddenDim: c.hiddenDim, nLayers: c.nLayers, nHeads: c.nHeads,
       nKvHeads: c.nKvHeads || c.nHeads, headDim: this.config.headDim, vocabSize: c.vocabSize,

@@ -384,6 +384,62 @@ napi_value ModelCreate(napi_env env, napi_callback_info info) {
   return h;
 }
 
+// modelLoadGGUF(path: string, maxSeq = 0) -> {model, config}: the GGUF file
+// through pbx_model_load_gguf; config in extractConfig's field names
+// (gguf.js:429-450) plus the tensor types.
+napi_value ModelLoadGGUF(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[2];
+  size_t argc = 0;
+  get_args(env, info, 2, argv, &argc);
+  char path[4096];
+  size_t len = 0;
+  if (argc < 1 ||
+      napi_get_value_string_utf8(env, argv[0], path, sizeof path, &len) != napi_ok ||
+      len + 1 >= sizeof path)
+    return throw_msg(env, "modelLoadGGUF(path, maxSeq): path must be a string");
+  int64_t max_seq = 0;
+  if (argc >= 2 && !get_i64(env, argv[1], &max_seq))
+    return throw_msg(env, "modelLoadGGUF(path, maxSeq): maxSeq must be a number");
+  pbx_gguf *g = nullptr;
+  pbx_model_config c;
+  int rc = pbx_gguf_open(path, &g);
+  if (!rc) rc = pbx_gguf_model_config(g, (int)max_seq, &c);
+  if (g) pbx_gguf_close(g);
+  if (rc) {  // the reader reports without a context
+    char msg[1200];
+    snprintf(msg, sizeof msg, "modelLoadGGUF: %s (status %d)", pbx_last_error(nullptr), rc);
+    return throw_msg(env, msg);
+  }
+  pbx_model *m = nullptr;
+  rc = pbx_model_load_gguf(g_ctx, path, (int)max_seq, &m);
+  if (rc) return throw_pbx(env, rc, "modelLoadGGUF");
+  ModelRef *r = new ModelRef{m, c.vocab_size, c.max_seq};
+  napi_value h, out, cfg;
+  if (napi_create_external(env, r, finalize_model, nullptr, &h) != napi_ok) {
+    pbx_model_free(m);
+    delete r;
+    return throw_msg(env, "modelLoadGGUF: could not create handle");
+  }
+  napi_create_object(env, &out);
+  napi_create_object(env, &cfg);
+  const struct { const char *k; double v; } fields[] = {
+      {"dim", (double)c.dim}, {"hiddenDim", (double)c.hidden_dim}, {"nLayers", (double)c.n_layers},
+      {"nHeads", (double)c.n_heads}, {"nKvHeads", (double)c.n_kv_heads},
+      {"headDim", (double)c.head_dim}, {"vocabSize", (double)c.vocab_size},
+      {"seqLen", (double)c.max_seq}, {"rmsNormEps", (double)c.rms_eps},
+      {"ropeTheta", c.rope_theta}, {"weightType", (double)c.weight_type},
+      {"embedType", (double)c.embed_type}, {"outputType", (double)c.output_type}};
+  for (const auto &f : fields) {
+    napi_value v;
+    napi_create_double(env, f.v, &v);
+    napi_set_named_property(env, cfg, f.k, v);
+  }
+  napi_set_named_property(env, out, "model", h);
+  napi_set_named_property(env, out, "config", cfg);
+  return out;
+}
+
 // modelSetTensor(model, tensorId, layer, data: TypedArray)
 napi_value ModelSetTensor(napi_env env, napi_callback_info info) {
   if (!need_ctx(env)) return nullptr;
@@ -563,6 +619,7 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
              {"dequant", Dequant},
              {"info", Info},
              {"modelCreate", ModelCreate},
+             {"modelLoadGGUF", ModelLoadGGUF},
              {"modelSetTensor", ModelSetTensor},
              {"modelForward", ModelForward},
              {"modelForwardBatch", ModelForwardBatch},

@@ -36,6 +36,9 @@ EXPORTS = (
     "pbx_model_forward_batch", "pbx_model_generate", "pbx_model_reset_cache", "pbx_model_rollback", "pbx_model_info",
     "pbx_model_profile", "pbx_model_op_name", "pbx_model_bench_role",
     "pbx_speculative_generate",
+    "pbx_gguf_open", "pbx_gguf_close", "pbx_gguf_info", "pbx_gguf_tensor_info",
+    "pbx_gguf_find_tensor", "pbx_gguf_get_int", "pbx_gguf_get_float", "pbx_gguf_get_string",
+    "pbx_gguf_get_array", "pbx_gguf_model_config", "pbx_model_load_gguf",
 )
 
 # Tensor ids of pbx_model_set_tensor (GGUF tensor names, gguf.js:378-410).
@@ -49,6 +52,12 @@ class ModelConfig(ctypes.Structure):
         "dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab_size",
         "max_seq", "weight_type", "embed_type", "output_type")] + \
         [("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_double)]
+
+
+class GgufTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_int32), ("n_dims", ctypes.c_int32),
+                ("dims", ctypes.c_int64 * 4), ("offset", ctypes.c_uint64),
+                ("nbytes", ctypes.c_uint64), ("data", ctypes.c_void_p)]
 
 
 class SpecStats(ctypes.Structure):
@@ -122,6 +131,20 @@ def load_library():
                                             ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i64,
                                             ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
         "pbx_model_create": (ctypes.c_int, [_vp, ctypes.POINTER(ModelConfig), ctypes.POINTER(_vp)]),
+        "pbx_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+        "pbx_gguf_close": (None, [_vp]),
+        "pbx_gguf_info": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_i64),
+                                         ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_uint64)]),
+        "pbx_gguf_tensor_info": (ctypes.c_int, [_vp, _i64, ctypes.POINTER(GgufTensor)]),
+        "pbx_gguf_find_tensor": (_i64, [_vp, ctypes.c_char_p]),
+        "pbx_gguf_get_int": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_i64)]),
+        "pbx_gguf_get_float": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+        "pbx_gguf_get_string": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p),
+                                               ctypes.POINTER(ctypes.c_uint64)]),
+        "pbx_gguf_get_array": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32),
+                                              ctypes.POINTER(ctypes.c_uint64)]),
+        "pbx_gguf_model_config": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.POINTER(ModelConfig)]),
+        "pbx_model_load_gguf": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(_vp)]),
         "pbx_model_free": (ctypes.c_int, [_vp]),
         "pbx_model_set_tensor": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t]),
         "pbx_model_forward": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
@@ -355,8 +378,96 @@ class Context:
         return ms.value
 
 
+class GGUF:
+    """A GGUF file opened with the build's reader (pbx_gguf_*; no GPU use)."""
+
+    def __init__(self, path):
+        self.L = load_library()
+        self._g = None
+        p = _vp()
+        _check(self.L.pbx_gguf_open(os.fsencode(path), ctypes.byref(p)))
+        self._g = p.value
+        v, nt, nk, ds = ctypes.c_uint32(), _i64(), _i64(), ctypes.c_uint64()
+        _check(self.L.pbx_gguf_info(self._g, ctypes.byref(v), ctypes.byref(nt), ctypes.byref(nk),
+                                    ctypes.byref(ds)))
+        self.version, self.n_tensors, self.n_kv, self.data_start = v.value, nt.value, nk.value, ds.value
+
+    def tensor(self, i):
+        t = GgufTensor()
+        _check(self.L.pbx_gguf_tensor_info(self._g, i, ctypes.byref(t)))
+        return {"name": t.name.decode(), "type": t.type, "dims": list(t.dims[:t.n_dims]),
+                "offset": t.offset, "nbytes": t.nbytes, "data": t.data}
+
+    def tensors(self):
+        return [self.tensor(i) for i in range(self.n_tensors)]
+
+    def tensor_bytes(self, i):
+        t = self.tensor(i)
+        return np.ctypeslib.as_array((ctypes.c_uint8 * t["nbytes"]).from_address(t["data"])).copy()
+
+    def find(self, name):
+        return self.L.pbx_gguf_find_tensor(self._g, name.encode())
+
+    def get_int(self, key):
+        v = _i64()
+        _check(self.L.pbx_gguf_get_int(self._g, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def get_float(self, key):
+        v = ctypes.c_double()
+        _check(self.L.pbx_gguf_get_float(self._g, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def get_string(self, key):
+        s, n = ctypes.c_void_p(), ctypes.c_uint64()
+        _check(self.L.pbx_gguf_get_string(self._g, key.encode(), ctypes.byref(s), ctypes.byref(n)))
+        return ctypes.string_at(s.value, n.value).decode() if n.value else ""
+
+    def get_array(self, key):
+        t, n = ctypes.c_uint32(), ctypes.c_uint64()
+        _check(self.L.pbx_gguf_get_array(self._g, key.encode(), ctypes.byref(t), ctypes.byref(n)))
+        return t.value, n.value
+
+    def model_config(self, max_seq=0):
+        cfg = ModelConfig()
+        _check(self.L.pbx_gguf_model_config(self._g, max_seq, ctypes.byref(cfg)))
+        return {f: getattr(cfg, f) for f, _ in ModelConfig._fields_}
+
+    def close(self):
+        if getattr(self, "_g", None):
+            self.L.pbx_gguf_close(self._g)
+            self._g = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        self.close()
+
+
 class Model:
     """A resident Llama-family model with the on-GPU decode step (pbx_model_*)."""
+
+    @classmethod
+    def from_gguf(cls, ctx, path, max_seq=0):
+        """pbx_model_load_gguf: configure from the file's metadata and upload
+        every tensor once."""
+        p = _vp()
+        ctx._call("pbx_model_load_gguf", ctx._p, os.fsencode(path), max_seq, ctypes.byref(p))
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        self._m = p.value
+        cfg = ModelConfig()
+        self.cfg = cfg
+        with GGUF(path) as g:
+            c = g.model_config(max_seq)
+        for f, _ in ModelConfig._fields_:
+            setattr(cfg, f, c[f])
+        self.vocab = cfg.vocab_size
+        return self
 
     def __init__(self, ctx, dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, max_seq,
                  weight_type, embed_type, output_type=-1, head_dim=None, rms_eps=1e-5,

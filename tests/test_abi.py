@@ -86,7 +86,7 @@ def test_napi_addon_loads_and_exports():
     keys = set(__import__("json").loads(r.stdout))
     for k in ("init", "upload", "linear", "dequant", "free", "deviceInfo", "modelCreate",
               "modelSetTensor", "modelForward", "modelForwardBatch", "modelGenerate",
-              "modelRollback", "modelReset", "modelFree", "speculative"):
+              "modelRollback", "modelReset", "modelFree", "speculative", "modelLoadGGUF"):
         assert k in keys, keys
 
 

@@ -216,3 +216,35 @@ rt.free(); dr.free();
     allj = np.fromfile(tmp_path / "all.bin", np.float32).reshape(-1, cfg["vocab_size"])
     assert allj.shape[0] == len(prompt) - 5
     assert float(np.abs(allj[-1] - logits).max()) <= 2e-3
+
+
+def test_llama_runtime_from_gguf(ctx, tmp_path):
+    """HipLlamaRuntime.fromGGUF: the build's GGUF reader from Node; the model
+    equals the one the C ABI loads from the same file."""
+    print("[case] js llama-hip fromGGUF", flush=True)
+    from purebee_amd.native import Model, TYPE_Q6_K
+    from tests.test_gpu_gguf import tiny, write_model
+    cfg = tiny(TYPE_Q4_0, TYPE_Q6_K)
+    path = tmp_path / "m.gguf"
+    write_model(path, cfg, seed=21, n_tokens=1000)
+    m = Model.from_gguf(ctx, path, max_seq=64)
+    prompt = [int(t) for t in synth.random_tokens(22, 6, 1000)]
+    logits, nxt = m.forward(prompt, 0)
+    m.free()
+    out = run_node(tmp_path, f"""
+const {{ HipLlamaRuntime }} = require({os.path.join(JS, 'llama-hip.js')!r});
+const rt = HipLlamaRuntime.fromGGUF(meta.path, {{ maxSeq: 64 }});
+const logits = rt.forward(meta.prompt, 0);
+wr('logits.bin', logits);
+let threw = false;
+try {{ HipLlamaRuntime.fromGGUF(meta.path + '.missing'); }} catch (e) {{ threw = /cannot open/.test(e.message); }}
+console.log(JSON.stringify({{ cfg: rt.config, threw }}));
+rt.free();
+""", {"path": str(path), "prompt": prompt})
+    res = json.loads(out.strip().splitlines()[-1])
+    lj = np.fromfile(tmp_path / "logits.bin", np.float32)
+    assert np.array_equal(lj, logits)
+    c = res["cfg"]
+    assert (c["dim"], c["hiddenDim"], c["nLayers"], c["nHeads"], c["nKvHeads"], c["vocabSize"]) == \
+        (256, 512, 2, 4, 2, 1000)
+    assert c["seqLen"] == 64 and c["embedType"] == TYPE_Q6_K and res["threw"]
