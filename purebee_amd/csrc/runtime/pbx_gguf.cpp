@@ -202,9 +202,10 @@ extern "C" int pbx_gguf_open(const char *path, pbx_gguf **out) {
   }
   g->size = (uint64_t)st.st_size;
   if (g->size < 24) {
+    const unsigned long long n = g->size;
     gguf_release(g);
     return pbx_fail(nullptr, PBX_EINVAL, "pbx_gguf_open: %s: %llu bytes is too short for GGUF",
-                    path, (unsigned long long)g->size);
+                    path, n);
   }
   void *m = mmap(nullptr, g->size, PROT_READ, MAP_PRIVATE, g->fd, 0);
   if (m == MAP_FAILED) {
@@ -292,7 +293,14 @@ extern "C" int pbx_gguf_open(const char *path, pbx_gguf **out) {
       if ((uint64_t)t.dims[d] > (1ull << 62) / n) return bad("tensor too large");
       n *= (uint64_t)t.dims[d];
     }
-    t.nbytes = (n + block - 1) / block * bytes;
+    const uint64_t blocks = (n + block - 1) / block;
+    if (blocks > g->size / (uint64_t)bytes) {  // cannot fit, and the product could wrap
+      char msg[200];
+      snprintf(msg, sizeof msg, "tensor %s: %llu elements do not fit in the file", t.name.c_str(),
+               (unsigned long long)n);
+      return bad(msg);
+    }
+    t.nbytes = blocks * bytes;
     t.offset = g->data_start + t.rel_offset;
     if (t.rel_offset > g->size || t.offset > g->size || t.nbytes > g->size - t.offset) {
       char msg[200];
