@@ -1,6 +1,7 @@
 // pbx_gemm.cpp -- launch path of the M >= 4 instruction: row scaling of the
 // activations to fp16, the MFMA GEMM (pbx_gemm.hip) and, when the K blocks
-// are split across workgroups, the reduction of the partial sums.
+// are split across workgroups, the reduction of the partial sums.  F32
+// weights take the fp32 MFMA kernels, which read the activations as they are.
 
 #include <algorithm>
 #include <string>
@@ -19,15 +20,84 @@ struct GemmArgsHost {  // GemmArgs in pbx_gemm.hip
   float *Y;
   int M, N, Npad, B, KS;
   int accumulate;
+  const void *msc;
 };
+
+struct GemmF32ArgsHost {  // GemmF32Args in pbx_gemm.hip
+  const void *W;
+  const float *X;
+  const float *bias;
+  float *Y;
+  int M, N, Npad, B, KS;
+  int accumulate;
+};
+
+const char *gemm_tag(int type) {
+  switch (type) {
+    case PBX_TYPE_Q4_0: return "q4";
+    case PBX_TYPE_Q8_0: return "q8";
+    case PBX_TYPE_Q4_1: return "q41";
+    case PBX_TYPE_F16: return "f16";
+    case PBX_TYPE_F32: return "f32";
+    default: return nullptr;
+  }
+}
+
+// Sum of the split-K partials into dY (+ bias, or accumulated).
+int launch_reduce(pbx_ctx *c, float *part, const float *dBias, float *dY, int M, int N, int KS,
+                  int accumulate, hipStream_t stream) {
+  hipFunction_t fred = pbx_kernel_by_name(c, "pbx_gemm_reduce");
+  if (!fred) return pbx_fail(c, PBX_ELOAD, "pbx_gemm: kernel pbx_gemm_reduce missing");
+  int m = M, n = N, ks = KS, acc = accumulate;
+  void *args[] = {&part, (void *)&dBias, &dY, &m, &n, &ks, &acc};
+  const int64_t MN = (int64_t)M * N;
+  return pbx_launch_fn(c, fred, "pbx_gemm_reduce", dim3((unsigned)((MN + 255) / 256)), dim3(256),
+                       args, stream);
+}
+
+// F32 weights: fp32 MFMA, wave tile 16*MT x 16*NT (MT 1 / 2 / 4 for
+// M <= 16 / <= 32 / larger), K split for about eight waves per CU.
+int launch_f32(pbx_ctx *c, const pbx_weight *w, const float *dX, int M, const float *dBias,
+               float *dY, int accumulate, hipStream_t stream) {
+  const int N = (int)w->N, B = (int)w->B;
+  const int MT = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  const int mtiles = (M + 16 * MT - 1) / (16 * MT);
+  int NT;
+  if (MT == 1)
+    NT = ((N + 255) / 256) * mtiles >= 2 * c->cu_count ? 4
+         : ((N + 127) / 128) * mtiles >= 2 * c->cu_count ? 2 : 1;
+  else
+    NT = MT == 2 ? 2 : 4;
+  const int nwg = (N + 64 * NT - 1) / (64 * NT);
+  int KS = 1;
+  const int waves = nwg * mtiles * 4;
+  if (waves < 8 * c->cu_count) KS = std::min({B, 8, (8 * c->cu_count + waves - 1) / waves});
+  float *part = nullptr;
+  if (KS > 1) {
+    int rc = pbx_ensure_dev(c, &c->d_gemm, &c->d_gemm_cap, (size_t)KS * M * N * 4);
+    if (rc) return rc;
+    part = (float *)c->d_gemm;
+  }
+  const std::string name = "pbx_gemm_f32_m" + std::to_string(MT) + "_n" + std::to_string(NT);
+  hipFunction_t fg = pbx_kernel_by_name(c, name);
+  if (!fg) return pbx_fail(c, PBX_ELOAD, "pbx_gemm: kernel %s missing", name.c_str());
+  GemmF32ArgsHost g{w->qs, dX, KS == 1 ? dBias : nullptr, KS == 1 ? dY : part,
+                    M, N, (int)w->Npad, B, KS, KS == 1 ? accumulate : 0};
+  void *args[] = {&g};
+  int rc = pbx_launch_fn(c, fg, name.c_str(), dim3(nwg, mtiles, KS), dim3(256), args, stream);
+  if (rc || KS == 1) return rc;
+  return launch_reduce(c, part, dBias, dY, M, N, KS, accumulate, stream);
+}
 
 }  // namespace
 
 int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M64,
                     const float *dBias, float *dY, int accumulate, hipStream_t stream) {
-  if (w->type != PBX_TYPE_Q4_0 && w->type != PBX_TYPE_Q8_0)
+  if (!gemm_tag(w->type))
     return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: weight type %d has no MFMA path", w->type);
   if (M64 > 65535) return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: M=%lld too large", (long long)M64);
+  if (w->type == PBX_TYPE_F32)
+    return launch_f32(c, w, dX, (int)M64, dBias, dY, accumulate, stream);
   const int M = (int)M64, N = (int)w->N, B = (int)w->B, K = B * 32;
   // M > 32: the LDS-tiled 128 x 128 kernel; otherwise one wave per 16*MT
   // rows x 16*NT weight rows.
@@ -73,12 +143,11 @@ int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M6
   float *part = (float *)(ws + x16_bytes + lo_bytes + inv_bytes);
 
   hipFunction_t fprep = pbx_kernel_by_name(c, "pbx_gemm_prep_x");
-  const std::string name = std::string("pbx_gemm_") + (w->type == PBX_TYPE_Q4_0 ? "q4" : "q8") +
+  const std::string name = std::string("pbx_gemm_") + gemm_tag(w->type) +
                            (big ? std::string("_big")
                                 : "_m" + std::to_string(MT) + "_n" + std::to_string(NT));
   hipFunction_t fg = pbx_kernel_by_name(c, name);
-  hipFunction_t fred = pbx_kernel_by_name(c, "pbx_gemm_reduce");
-  if (!fprep || !fg || !fred) return pbx_fail(c, PBX_ELOAD, "pbx_gemm: kernel %s missing", name.c_str());
+  if (!fprep || !fg) return pbx_fail(c, PBX_ELOAD, "pbx_gemm: kernel %s missing", name.c_str());
   {
     int m = M, k = K;
     void *args[] = {(void *)&dX, &x16, &x16lo, &inv, &m, &k};
@@ -86,20 +155,13 @@ int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M6
       return rc;
   }
   GemmArgsHost g{w->qs, w->d, x16, x16lo, inv, KS == 1 ? dBias : nullptr, KS == 1 ? dY : part,
-                 M, N, (int)w->Npad, B, KS, KS == 1 ? accumulate : 0};
+                 M, N, (int)w->Npad, B, KS, KS == 1 ? accumulate : 0, w->m};
   {
     void *args[] = {&g};
     if ((rc = pbx_launch_fn(c, fg, name.c_str(), dim3(nwg, mtiles, KS), dim3(256), args, stream)))
       return rc;
   }
-  if (KS > 1) {
-    int m = M, n = N, ks = KS, acc = accumulate;
-    void *args[] = {&part, (void *)&dBias, &dY, &m, &n, &ks, &acc};
-    const int64_t MN = (int64_t)M * N;
-    if ((rc = pbx_launch_fn(c, fred, "pbx_gemm_reduce", dim3((unsigned)((MN + 255) / 256)),
-                            dim3(256), args, stream)))
-      return rc;
-  }
+  if (KS > 1) return launch_reduce(c, part, dBias, dY, M, N, KS, accumulate, stream);
   return PBX_OK;
 }
 

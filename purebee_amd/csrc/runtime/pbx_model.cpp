@@ -720,8 +720,7 @@ static int ensure_batch(pbx_model *m, int rows, bool all_logits) {
     if (!rc) rc = grow(m, (void **)&m->bgu, R * 2 * g.hidden_dim * 4);
     if (!rc) rc = grow(m, (void **)&m->bh, R * g.hidden_dim * 4);
     // accumulating linears without an MFMA path go through a temporary
-    if (!rc && g.weight_type != PBX_TYPE_Q4_0 && g.weight_type != PBX_TYPE_Q8_0)
-      rc = grow(m, (void **)&m->btmp, R * tmp_cols * 4);
+    if (!rc) rc = grow(m, (void **)&m->btmp, R * tmp_cols * 4);
     if (!rc) rc = grow(m, (void **)&m->btok, R * 4);
     if (!rc) rc = grow(m, (void **)&m->bnext, R * 4);
     if (rc) {
@@ -751,7 +750,7 @@ static int launch_k(pbx_model *m, const char *name, dim3 grid, dim3 block, void 
 static int linear_rows(pbx_model *m, const pbx_weight *w, const float *X, int n, float *Y,
                        bool accumulate) {
   pbx_ctx *c = m->c;
-  if (w->type == PBX_TYPE_Q4_0 || w->type == PBX_TYPE_Q8_0)
+  if (w->type != PBX_TYPE_Q6_K && n >= PBX_GEMM_MIN_M)
     return pbx_gemm_launch(c, w, X, n, nullptr, Y, accumulate ? 1 : 0, c->stream);
   if (!accumulate) return pbx_linear_enqueue(c, w, X, n, nullptr, Y, c->stream);
   int rc = pbx_linear_enqueue(c, w, X, n, nullptr, m->btmp, c->stream);

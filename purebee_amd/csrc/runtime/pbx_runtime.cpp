@@ -508,9 +508,9 @@ int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t
     return pbx_launch(c, PBX_K_GEMV_Q8REF, dim3((unsigned)((N + 63) / 64), gy), dim3(512),
                       args, stream);
   }
-  // Q4_1 and F32 rows stay on the GEMV kernels for every M (one grid row
-  // per activation row); the MFMA GEMM covers Q4_0 / Q8_0.
-  if (M >= PBX_GEMM_MIN_M && (w->type == PBX_TYPE_Q4_0 || w->type == PBX_TYPE_Q8_0))
+  // Q6_K rows stay on the GEMV kernels for every M (one grid row per
+  // activation row); the MFMA GEMM covers the other types.
+  if (M >= PBX_GEMM_MIN_M && w->type != PBX_TYPE_Q6_K)
     return pbx_gemm_enqueue(c, w, dX, M, dBias, dY, stream);
   int B = (int)w->B;
   void *args[] = {(void *)&w->qs, (void *)&w->d, (void *)&w->m, &dX, &dBias, &dY, &N, &B};

@@ -292,17 +292,26 @@ GEMM_SHAPES = [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192), (576, 576)
                (576, 1536), (288, 288), (768, 288), (288, 768), (100, 64)]
 
 
-@pytest.mark.parametrize("t", [pb.TYPE_Q4_0, pb.TYPE_Q8_0])
+def weight_bytes(t, W):
+    if t == pb.TYPE_F32:
+        return W
+    if t == pb.TYPE_F16:
+        return pb.to_f16_bytes(W)
+    return quantize(t, W)
+
+
+@pytest.mark.parametrize("t", QUANT + [pb.TYPE_F16, pb.TYPE_F32])
 @pytest.mark.parametrize("M", [4, 5, 17, 64, 130])
 @pytest.mark.parametrize("N,K", GEMM_SHAPES)
 def test_mfma_gemm_parity(ctx, t, M, N, K):
-    """M >= 4 takes the MFMA path (exact integer weight codes, activations as
-    an fp16 pair hi + lo, fp32 accumulation): every row within 1e-5 relative
-    L2 of the oracle's double-accumulated matvec and of the M=1 GEMV (the
-    matvec bar is 1e-3; single-fp16 activations would sit near 2e-4)."""
+    """M >= 4 takes the MFMA path (exact integer weight codes or fp16
+    weights, activations as an fp16 pair hi + lo; F32 weights on the fp32
+    MFMA; fp32 accumulation): every row within 1e-5 relative L2 of the
+    oracle's double-accumulated matvec and of the M=1 GEMV (the matvec bar is
+    1e-3; single-fp16 activations would sit near 2e-4)."""
     print(f"[case] gemm type={t} M={M} N={N} K={K}", flush=True)
     tol = 1e-5
-    raw = quantize(t, synth_matrix(11 * N + K + M, N, K))
+    raw = weight_bytes(t, synth_matrix(11 * N + K + M, N, K))
     X = pb.synth_normal(M * 7 + K, M * K).reshape(M, K)
     X[1] *= 1e-3   # rows of very different magnitude: per-row scaling
     X[2] *= 300.0
