@@ -230,7 +230,10 @@ def run_decode(args, pb, synth):
                 "us_per_launch_in_step": round(dom["us_per_launch"], 3)}
     step_bytes = sum(r["bytes_per_step"] for r in roles.values())
     m_gt_1 = None if args.no_m_gt_1 else run_m_gt_1(ctx, model, cfg, pb, synth)
-    q4_1 = None if args.no_m_gt_1 else run_q4_1(ctx, pb)
+    next_rows = None
+    if not args.no_m_gt_1:
+        next_rows = {"q4_1_matvec": run_q4_1(ctx, pb), "gemm_types": run_gemm_types(ctx, pb),
+                     "gguf": run_gguf(ctx, pb, synth)}
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the restated reference CPU path ...")
@@ -263,7 +266,7 @@ def run_decode(args, pb, synth):
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in roles.items()},
         "m_gt_1": m_gt_1,
-        "q4_1_matvec": q4_1,
+        "next_rows": next_rows,
         "cpu_baseline": cpu,
     }
     model.free()
@@ -382,6 +385,78 @@ def run_q4_1(ctx, pb):
                 w.free()
         dx.free(), dy.free()
     return res
+
+
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA, vendor figure
+
+
+def run_gemm_types(ctx, pb):
+    """The MFMA GEMM per weight type at M = 512 on a 2048 x 2048 matrix,
+    timed back to back with HIP events: F32 on the fp32 MFMA, F16 / Q4_1 /
+    Q4_0 on the fp16 MFMA (two issues per useful product, activations hi +
+    lo).  Useful FLOPs 2*M*N*K."""
+    res = {}
+    M, N, K = 512, 2048, 2048
+    W = pb.synth_normal(4300, N * K, 0, 0.02).reshape(N, K)
+    dx = ctx.alloc(M * K * 4).upload(np.random.default_rng(6).normal(0, 1, M * K).astype(np.float32))
+    dy = ctx.alloc(M * N * 4)
+    for name, t, data, peak in (("f32", pb.TYPE_F32, W, FP32_MFMA_PEAK_TFLOPS),
+                                ("f16", pb.TYPE_F16, pb.to_f16_bytes(W), MFMA_F16_PEAK_TFLOPS),
+                                ("q4_1", pb.TYPE_Q4_1, pb.quantize_q4_1(W), MFMA_F16_PEAK_TFLOPS),
+                                ("q4_0", pb.TYPE_Q4_0, pb.quantize_q4_0(W), MFMA_F16_PEAK_TFLOPS)):
+        w = ctx.upload(t, N, K, data)
+        ctx.bench_linear([w], [dx.ptr], [dy.ptr], M, 3)
+        reps = 20
+        us = ctx.bench_linear([w], [dx.ptr], [dy.ptr], M, reps) / reps * 1e3
+        tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        res[name] = {"M": M, "N": N, "K": K, "us_per_call": round(us, 2), "TFLOPs": round(tf, 2),
+                     "peak": peak, "frac": round(tf / peak, 4)}
+        log(f"gemm {name} M={M} N={N} K={K}: {us:.1f} us, {tf:.1f} TFLOP/s "
+            f"({100 * tf / peak:.1f}% of {peak:.0f})")
+        w.free()
+    dx.free(), dy.free()
+    return res
+
+
+def run_gguf(ctx, pb, synth):
+    """The file -> device path: a Llama-3.2-1B-shaped GGUF file as llama.cpp
+    lays out a Q4_0 model (Q4_0 layer matrices, tied Q6_K token embedding,
+    F32 norms) is written to a temporary directory, loaded with
+    pbx_model_load_gguf (mmap, one pinned upload per tensor) and decoded
+    greedily with the Q6_K LM head."""
+    import tempfile
+    cfg = dict(synth.CONFIGS["llama32_1b"], embed_type=pb.TYPE_Q6_K, max_seq=512)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "llama32_1b_q4_0.gguf")
+        t0 = time.perf_counter()
+        size = synth.write_gguf(path, cfg, seed=1000)
+        log(f"gguf: wrote {size / 1e9:.2f} GB in {time.perf_counter() - t0:.1f}s")
+        t0 = time.perf_counter()
+        model = pb.Model.from_gguf(ctx, path, max_seq=512)
+        ctx.sync()
+        load_s = time.perf_counter() - t0
+    log(f"gguf: loaded in {load_s * 1e3:.0f} ms ({size / load_s / 1e9:.2f} GB/s file to HBM)")
+    prompt = synth.random_tokens(7, PROMPT, cfg["vocab_size"])
+    _, nxt = model.forward(prompt, 0, want_logits=False)
+    steps = 64
+    model.generate(nxt, PROMPT, 8)
+    model.rollback(PROMPT)
+    ctx.sync()
+    ctx.timer_start()
+    model.generate(nxt, PROMPT, steps)
+    ms = ctx.timer_stop() / steps
+    model.rollback(PROMPT)
+    us, by, _ = model.bench_role("lm_head", 8)
+    log(f"gguf decode: {ms * 1e3:.1f} us/token, {1e3 / ms:.1f} tok/s; Q6_K lm head "
+        f"{us:.1f} us, {by / us / 1e3:.0f} GB/s")
+    model.free()
+    return {"file_bytes": size, "load_ms": round(load_s * 1e3, 1),
+            "load_GBps": round(size / load_s / 1e9, 2),
+            "decode_tok_per_s": round(1e3 / ms, 1), "decode_us_per_token": round(ms * 1e3, 1),
+            "lm_head_q6_k": {"us_per_launch": round(us, 2), "bytes_per_launch": round(by),
+                             "GBps": round(by / us / 1e3, 1),
+                             "frac_hbm": round(by / us / 1e3 / HBM_PEAK_GBS, 4)},
+            "layout": "q4_0 layer matrices, tied q6_k token_embd, f32 norms (llama.cpp Q4_0)"}
 
 
 def run_pmc_probe(args, pb, synth):

@@ -87,3 +87,59 @@ def random_tokens(seed, n, vocab):
     # map the normal draws through their CDF-free rank: a fixed hash of the bits
     bits = u.view(np.uint32).astype(np.uint64)
     return ((bits * np.uint64(2654435761)) % np.uint64(vocab)).astype(np.int32)
+
+
+# GGUF tensor names of the tensor ids (gguf.js:378-410).
+GGUF_NAMES = {T_TOKEN_EMBD: "token_embd.weight", T_OUTPUT: "output.weight",
+              T_OUTPUT_NORM: "output_norm.weight", T_ATTN_NORM: "attn_norm.weight",
+              T_FFN_NORM: "ffn_norm.weight", T_ATTN_Q: "attn_q.weight",
+              T_ATTN_K: "attn_k.weight", T_ATTN_V: "attn_v.weight",
+              T_ATTN_OUTPUT: "attn_output.weight", T_FFN_GATE: "ffn_gate.weight",
+              T_FFN_UP: "ffn_up.weight", T_FFN_DOWN: "ffn_down.weight"}
+
+
+def write_gguf(path, cfg, seed=1000, alignment=32):
+    """Write the seeded model of `cfg` as a GGUF v3 file (llama metadata,
+    the tensors of tensor_specs in their types) for the file -> device
+    path; returns the file size.  Tensor data is streamed, one tensor in
+    memory at a time."""
+    import struct
+    if isinstance(cfg, str):
+        cfg = CONFIGS[cfg]
+    specs = tensor_specs(cfg)
+
+    def s(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+
+    kv = [("general.architecture", 8, s("llama")),
+          ("llama.embedding_length", 4, struct.pack("<I", cfg["dim"])),
+          ("llama.feed_forward_length", 4, struct.pack("<I", cfg["hidden_dim"])),
+          ("llama.block_count", 4, struct.pack("<I", cfg["n_layers"])),
+          ("llama.attention.head_count", 4, struct.pack("<I", cfg["n_heads"])),
+          ("llama.attention.head_count_kv", 4, struct.pack("<I", cfg["n_kv_heads"])),
+          ("llama.context_length", 4, struct.pack("<I", cfg["max_seq"])),
+          ("llama.attention.layer_norm_rms_epsilon", 6, struct.pack("<f", cfg.get("rms_eps", 1e-5))),
+          ("llama.rope.freq_base", 6, struct.pack("<f", cfg.get("rope_theta", 10000.0))),
+          ("general.alignment", 4, struct.pack("<I", alignment))]
+    head = struct.pack("<4sIQQ", b"GGUF", 3, len(specs), len(kv))
+    for key, vt, val in kv:
+        head += s(key) + struct.pack("<I", vt) + val
+    sizes = [native.row_bytes(t, K) * N if t != TYPE_F32 else 4 * N * K
+             for (_, _, N, K, t) in specs]
+    rel, off = [], 0
+    for n in sizes:
+        rel.append(off)
+        off = (off + n + alignment - 1) // alignment * alignment
+    for (tid, layer, N, K, t), r in zip(specs, rel):
+        name = GGUF_NAMES[tid] if layer < 0 else f"blk.{layer}.{GGUF_NAMES[tid]}"
+        dims = [K] if tid in (T_OUTPUT_NORM, T_ATTN_NORM, T_FFN_NORM) else [K, N]
+        head += s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        head += struct.pack("<IQ", t, r)
+    start = (len(head) + alignment - 1) // alignment * alignment
+    with open(path, "wb") as f:
+        f.write(head + bytes(start - len(head)))
+        for i, (spec, r) in enumerate(zip(specs, rel)):
+            f.write(bytes(start + r - f.tell()))
+            f.write(np.ascontiguousarray(make_tensor(spec, seed, i)).view(np.uint8).tobytes())
+        return f.tell()

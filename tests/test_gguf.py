@@ -161,3 +161,29 @@ def test_model_config_extraction(tmp_path):
     gw.write(p3, kv[:2], [emb, q])
     with GGUF(p3) as g, pytest.raises(PbxError, match="block_count"):
         g.model_config()
+
+
+def test_synth_writer_roundtrip(tmp_path):
+    """purebee_amd.synth.write_gguf (the workloads' file writer) produces a
+    file the reader parses into the same config and tensor bytes."""
+    from purebee_amd import synth
+    cfg = dict(dim=256, hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=300,
+               max_seq=64, weight_type=pb.TYPE_Q4_1, embed_type=pb.TYPE_Q6_K, output_type=pb.TYPE_F16,
+               rope_theta=500000.0)
+    p = tmp_path / "s.gguf"
+    size = synth.write_gguf(p, cfg, seed=9)
+    assert size == p.stat().st_size
+    with GGUF(p) as g:
+        c = g.model_config()
+        assert (c["dim"], c["hidden_dim"], c["n_layers"], c["vocab_size"], c["max_seq"]) == \
+            (256, 512, 2, 300, 64)
+        assert (c["weight_type"], c["embed_type"], c["output_type"]) == \
+            (pb.TYPE_Q4_1, pb.TYPE_Q6_K, pb.TYPE_F16)
+        assert c["rope_theta"] == 500000.0
+        for i, spec in enumerate(synth.tensor_specs(cfg)):
+            name = synth.GGUF_NAMES[spec[0]] if spec[1] < 0 else \
+                f"blk.{spec[1]}.{synth.GGUF_NAMES[spec[0]]}"
+            j = g.find(name)
+            assert j >= 0, name
+            want = np.ascontiguousarray(synth.make_tensor(spec, 9, i)).view(np.uint8).ravel()
+            assert np.array_equal(g.tensor_bytes(j), want), name
