@@ -70,14 +70,13 @@ DK_MODES_SMALL(PBX_Q6K, q6k, 4)
       pbx_dk_##TN##_i##WV##x##RT##b##IB##_gu(GemvArgs a) {                                \
     gemv_int<T, WV, RT, IB, PRO_RMSNORM, EPI_SWIGLU>(a);                                  \
   }
+// 16-wave workgroups (at most 128 VGPRs a lane) only where the prologue
+// wave's activation registers still fit: Q4_0 with one block per lane.
 DK_INT_GU(PBX_Q4, q4, 8, 4, 1)
 DK_INT_GU(PBX_Q4, q4, 16, 4, 1)
 DK_INT_GU(PBX_Q4, q4, 8, 4, 2)
-DK_INT_GU(PBX_Q4, q4, 16, 4, 2)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 1)
-DK_INT_GU(PBX_Q8, q8, 16, 4, 1)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 2)
-DK_INT_GU(PBX_Q8, q8, 16, 4, 2)
 
 DK_MODES_WIDE(PBX_F32, f32, 2)
 DK_MODES_WIDE(PBX_F32, f32, 4)

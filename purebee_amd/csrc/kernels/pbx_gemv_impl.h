@@ -200,45 +200,43 @@ template <int TYPE> __device__ __forceinline__ int scale_block(int b) {
 // times d * scales[8*half + 2*g + l/16] (gguf.js:317-364); with b = 8*sb +
 // 4*half + g the lane reads 32 contiguous ql bytes, 32 contiguous qh bytes
 // and the two int8 scales of its half-blocks (returned in ex).
+//
+// The loads are unconditional: a lane that is not `ok` reads block 0 of row
+// n (always in the plane), and its value is cancelled later (zero scales,
+// zero activations; F32 / F16 bytes are masked here).  A load under a
+// branch would make the compiler wait for it at the branch's join, which
+// serialises the row loads of a tile into separate memory round trips.
 template <int TYPE>
 __device__ __forceinline__ void load_lane(const uint8_t *qs, int n, int b, int B, bool ok,
                                           uint4 (&q)[BlockTraits<TYPE>::QB / 16],
                                           unsigned &ex) {
   constexpr int QB = BlockTraits<TYPE>::QB;
-  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+  const int bb = ok ? b : 0;
   ex = 0u;
   if constexpr (TYPE == PBX_Q6K) {
-    const uint8_t *blk = qs + ((size_t)n * (B >> 3) + (b >> 3)) * PBX_Q6K_BYTES;
-    const int half = (b >> 2) & 1, g = b & 3;
+    const uint8_t *blk = qs + ((size_t)n * (B >> 3) + (bb >> 3)) * PBX_Q6K_BYTES;
+    const int half = (bb >> 2) & 1, g = bb & 3;
     const uint8_t *ql = blk + half * 64 + (g & 1) * 32;
     const uint8_t *qh = blk + 128 + half * 32;
-    q[0] = ok ? ld_stream(ql) : z;
-    q[1] = ok ? ld_stream(ql + 16) : z;
-    q[2] = ok ? ld_stream(qh) : z;
-    q[3] = ok ? ld_stream(qh + 16) : z;
-    ex = ok ? *reinterpret_cast<const uint16_t *>(blk + 192 + half * 8 + 2 * g) : 0u;
+    q[0] = ld_stream(ql);
+    q[1] = ld_stream(ql + 16);
+    q[2] = ld_stream(qh);
+    q[3] = ld_stream(qh + 16);
+    ex = *reinterpret_cast<const uint16_t *>(blk + 192 + half * 8 + 2 * g) & (ok ? 0xFFFFu : 0u);
   } else {
-    const uint8_t *src = qs + ((size_t)n * B + b) * QB;
+    const uint8_t *src = qs + ((size_t)n * B + bb) * QB;
 #pragma unroll
-    for (int v = 0; v < QB / 16; ++v) q[v] = ok ? ld_stream(src + v * 16) : z;
+    for (int v = 0; v < QB / 16; ++v) q[v] = ld_stream(src + v * 16);
+    if constexpr (TYPE == PBX_F32 || TYPE == PBX_F16) {
+      const unsigned m = ok ? ~0u : 0u;
+#pragma unroll
+      for (int v = 0; v < QB / 16; ++v) {
+        q[v].x &= m; q[v].y &= m; q[v].z &= m; q[v].w &= m;
+      }
+    }
   }
 }
 
-__device__ __forceinline__ void load_block(const float *__restrict__ p, bool valid,
-                                           float (&v)[32]) {
-  if (valid) {
-    const float4 *xp = reinterpret_cast<const float4 *>(p);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 t = xp[i];
-      v[4 * i + 0] = t.x; v[4 * i + 1] = t.y;
-      v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) v[i] = 0.f;
-  }
-}
 
 // Element i of row `tok` of a resident [rows][dim] weight, dequantised
 // exactly as gguf.js:231-364 (F16, Q8_0, Q4_0, Q4_1, Q6_K) or read (F32).
@@ -271,7 +269,28 @@ __device__ __forceinline__ float row_value(const uint8_t *qs, const uint16_t *ds
   return (float)(nib - 8) * d;
 }
 
+// Block b (32 floats) of base, read unconditionally (block 0 when !valid;
+// the caller zeroes such lanes' values), so the loads issue back to back.
+__device__ __forceinline__ void load_block_nb(const float *__restrict__ base, int b, bool valid,
+                                              float (&v)[32]) {
+  const float4 *xp = reinterpret_cast<const float4 *>(base + (size_t)(valid ? b : 0) * 32);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 t = xp[i];
+    v[4 * i + 0] = t.x; v[4 * i + 1] = t.y;
+    v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+  }
+}
+
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+// Workgroup barrier for LDS hand-offs: waits for this wave's LDS operations
+// only.  __syncthreads also drains the wave's outstanding global loads
+// (its workgroup-scope fence), which would stall a kernel that has weight
+// bytes in flight across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -296,36 +315,6 @@ __device__ __forceinline__ uint64_t argmax_key(float v, unsigned idx) {
   unsigned b = __float_as_uint(v);
   b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   return ((uint64_t)b << 32) | (uint64_t)(0xFFFFFFFFu - idx);
-}
-
-// Activation block b (32 values) after the prologue.  `own` marks the lanes
-// whose block counts once toward the RMSNorm sum of squares.
-template <int PRO>
-__device__ __forceinline__ void prologue_block(const GemvArgs &a, const float *x,
-                                               const float *x2, int b, bool valid,
-                                               float (&xr)[32]) {
-  if constexpr (PRO == PRO_SWIGLU) {
-    float g[32], u[32];
-    load_block(x + (size_t)b * 32, valid, g);
-    load_block(x2 + (size_t)b * 32, valid, u);
-#pragma unroll
-    for (int j = 0; j < 32; ++j) xr[j] = silu(g[j]) * u[j];
-  } else {
-    load_block(x + (size_t)b * 32, valid, xr);
-  }
-}
-
-// RMSNorm (engine.js:429-449): rms = sqrt(sum(x^2)/K + eps); x/rms * w,
-// here as x * (1/rms) * w (one reciprocal instead of 32 divisions).
-__device__ __forceinline__ void apply_rmsnorm(const GemvArgs &a, float ss, int K, int b,
-                                              bool valid, float (&xr)[32]) {
-  const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
-  if (valid) {
-    float w[32];
-    load_block(a.normw + (size_t)b * 32, true, w);
-#pragma unroll
-    for (int j = 0; j < 32; ++j) xr[j] = xr[j] * inv * w[j];
-  }
 }
 
 // One block-row term of the lane's 32-block b.  xs = sum of the lane's 32
@@ -354,25 +343,25 @@ __device__ __forceinline__ float block_term(const uint4 (&q)[BlockTraits<TYPE>::
 // fp16 scales (or Q4_1 minima) of tile rows 0..R) at block b.  SEG is the
 // number of rows of the tile that are consecutive in the plane (R, or R/2
 // for paired gate/up tiles); 4-row groups are one 8-byte load.
+// Loaded unconditionally (block 0 when !valid) and masked to +0.
 template <int R, int SEG, typename RowFn>
-__device__ __forceinline__ void load_scales(const uint16_t *plane, RowFn tile_row, int b, int B,
-                                            bool valid, float (&out)[R]) {
+__device__ __forceinline__ void load_scale_bits(const uint16_t *plane, RowFn tile_row, int b,
+                                                int B, bool valid, unsigned (&out)[R]) {
+  const int bb = valid ? b : 0;
+  const unsigned m = valid ? ~0u : 0u;
   if constexpr (SEG >= 4) {
 #pragma unroll
     for (int g = 0; g < R / 4; ++g) {
-      const int rg = tile_row(g * 4);
-      const uint2 dv = valid ? *reinterpret_cast<const uint2 *>(plane + dsc_index(rg, b, B))
-                             : make_uint2(0u, 0u);
-      out[g * 4 + 0] = f16_bits_to_f32(dv.x);
-      out[g * 4 + 1] = f16_bits_to_f32(dv.x >> 16);
-      out[g * 4 + 2] = f16_bits_to_f32(dv.y);
-      out[g * 4 + 3] = f16_bits_to_f32(dv.y >> 16);
+      const uint2 dv = *reinterpret_cast<const uint2 *>(plane + dsc_index(tile_row(g * 4), bb, B));
+      out[g * 4 + 0] = dv.x & m;
+      out[g * 4 + 1] = (dv.x >> 16) & m;
+      out[g * 4 + 2] = dv.y & m;
+      out[g * 4 + 3] = (dv.y >> 16) & m;
     }
   } else {
     // segments of 1 or 2 rows inside one 4-row group
 #pragma unroll
-    for (int i = 0; i < R; ++i)
-      out[i] = valid ? f16_bits_to_f32(plane[dsc_index(tile_row(i), b, B)]) : 0.f;
+    for (int i = 0; i < R; ++i) out[i] = plane[dsc_index(tile_row(i), bb, B)] & m;
   }
 }
 
@@ -443,33 +432,47 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
     return PAIR ? (i < R / 2 ? r0 + i : N / 2 + r0 + i - R / 2) : r0 + i;
   };
 
-  // The residual rows this thread will store (EPI_ADD), read up front.
+  // Rows past N (the last tile of a paired matrix) are read as row N - 1;
+  // their sums are never stored.
+  auto load_row = [&](int i) -> int { return min(tile_row(i), N - 1); };
+
+  // 1. Activation inputs first (x; x2 for SwiGLU; the RMSNorm weights): a CU
+  //    returns loads in issue order, so inputs requested behind the weight
+  //    stream would arrive only with it.  Then the residual (EPI_ADD).
   const int lanes_per_row = 64 / R;
+  float xa[32], xb[32];
+  load_block_nb(x, b, valid, xa);
+  if constexpr (PRO == PRO_SWIGLU) load_block_nb(x2, b, valid, xb);
+  if constexpr (PRO == PRO_RMSNORM) load_block_nb(a.normw, b, valid, xb);
   float res = 0.f;
   if constexpr (EPI == EPI_ADD) {
     const int rr = nwaves == 1 ? ((lane % lanes_per_row) == 0 ? lane / lanes_per_row : R)
                                : (int)threadIdx.x;
     if (rr < R && r0 + rr < N) res = y[r0 + rr];
   }
-
-  // Issue the weight loads first: they do not depend on the activations.
-  uint4 q[R][NV];
-  unsigned ex[R];
-#pragma unroll
-  for (int i = 0; i < R; ++i) load_lane<TYPE>(a.qs, tile_row(i), b, B, valid, q[i], ex[i]);
-  float dsf[R], msf[R];
+  // 2. Scale bits, then the weight bytes, all issued before any use.
+  unsigned dbits[R], mbits[R];
   if constexpr (has_scale<TYPE>()) {
     constexpr int SEG = PAIR ? R / 2 : R;  // rows contiguous in the scale plane
     const int sb = scale_block<TYPE>(b), SB = scale_block<TYPE>(B);
-    load_scales<R, SEG>(a.dsc, tile_row, sb, SB, valid, dsf);
-    if constexpr (TYPE == PBX_Q41) load_scales<R, SEG>(a.msc, tile_row, sb, SB, valid, msf);
-  } else {
-#pragma unroll
-    for (int i = 0; i < R; ++i) dsf[i] = 1.f;
+    load_scale_bits<R, SEG>(a.dsc, load_row, sb, SB, valid, dbits);
+    if constexpr (TYPE == PBX_Q41) load_scale_bits<R, SEG>(a.msc, load_row, sb, SB, valid, mbits);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 q[R][NV];
+  unsigned ex[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) load_lane<TYPE>(a.qs, load_row(i), b, B, valid, q[i], ex[i]);
+  __builtin_amdgcn_sched_barrier(0);
 
+  // 3. The activation block after the prologue (zero for lanes past B).
   float xr[32];
-  prologue_block<PRO>(a, x, x2, b, valid, xr);
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    float v = xa[j];
+    if constexpr (PRO == PRO_SWIGLU) v = silu(v) * xb[j];
+    xr[j] = valid ? v : 0.f;
+  }
   if constexpr (PRO == PRO_RMSNORM) {
     float ss = 0.f;
 #pragma unroll
@@ -477,11 +480,20 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
     ss = wave_sum(ss);
     if (nwaves > 1) {
       if (lane == 0) ssw[wave] = ss;
-      __syncthreads();
+      lds_barrier();
       ss = 0.f;
       for (int w = 0; w < nwaves; ++w) ss += ssw[w];
     }
-    apply_rmsnorm(a, ss, K, b, valid, xr);
+    // RMSNorm (engine.js:429-449): x * (1/rms) * w
+    const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) xr[j] = xr[j] * inv * xb[j];
+  }
+  float dsf[R], msf[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    dsf[i] = has_scale<TYPE>() ? f16_bits_to_f32(dbits[i]) : 1.f;
+    msf[i] = TYPE == PBX_Q41 ? f16_bits_to_f32(mbits[i]) : 0.f;
   }
   float xs = 0.f, xlo = 0.f;
   if constexpr (TYPE != PBX_F32 && TYPE != PBX_F16) {
@@ -494,9 +506,7 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
 
   float acc[R];
 #pragma unroll
-  for (int i = 0; i < R; ++i)
-    acc[i] = block_term<TYPE>(q[i], ex[i], b, xr, xs, xlo, dsf[i],
-                              TYPE == PBX_Q41 ? msf[i] : 0.f);
+  for (int i = 0; i < R; ++i) acc[i] = block_term<TYPE>(q[i], ex[i], b, xr, xs, xlo, dsf[i], msf[i]);
 
   const float tot = wave_transpose_reduce<R>(acc, lane);
   const int row = lane / lanes_per_row;
@@ -584,38 +594,59 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
     return PAIR ? (r0 + (t < T / 2 ? t : t - T / 2)) < NO : (r0 + t) < N;
   };
 
-  // residual of the first row this lane stores (EPI_ADD), read up front
+  // Activation inputs first, then the residual, the scales and the weight
+  // bytes (the order and branch-free loads of gemv_wide).
+  float xa[32], xb[32];
+  load_block_nb(x, b, active, xa);
+  if constexpr (PRO == PRO_SWIGLU) load_block_nb(x2, b, active, xb);
+  if constexpr (PRO == PRO_RMSNORM) load_block_nb(a.normw, b, active, xb);
+  // residual of the first row this lane stores (EPI_ADD)
   float res = 0.f;
   if constexpr (EPI == EPI_ADD)
     if (lane < T && r0 + lane < N) res = y[r0 + lane];
 
   uint4 q[P][NV];
-  unsigned ex[P];
-  float d[P], mn[P];
+  unsigned ex[P], dbits[P], mbits[P];
   const int sb = scale_block<TYPE>(b), SB = scale_block<TYPE>(B);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
-    const int rw = tile_row(p * rpw + rs);
     const bool ok = active && row_ok(p * rpw + rs);
-    load_lane<TYPE>(a.qs, rw, b, B, ok, q[p], ex[p]);
-    d[p] = 1.f;
-    mn[p] = 0.f;
-    if constexpr (has_scale<TYPE>())
-      d[p] = ok ? f16_bits_to_f32(a.dsc[dsc_index(rw, sb, SB)]) : 0.f;
-    if constexpr (TYPE == PBX_Q41)
-      mn[p] = ok ? f16_bits_to_f32(a.msc[dsc_index(rw, sb, SB)]) : 0.f;
+    const int rw = ok ? tile_row(p * rpw + rs) : 0;
+    const unsigned m = ok ? 0xFFFFu : 0u;
+    dbits[p] = has_scale<TYPE>() ? a.dsc[dsc_index(rw, sb, SB)] & m : 0u;
+    mbits[p] = TYPE == PBX_Q41 ? a.msc[dsc_index(rw, sb, SB)] & m : 0u;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const bool ok = active && row_ok(p * rpw + rs);
+    load_lane<TYPE>(a.qs, ok ? tile_row(p * rpw + rs) : 0, b, B, ok, q[p], ex[p]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float d[P], mn[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    d[p] = has_scale<TYPE>() ? f16_bits_to_f32(dbits[p]) : 1.f;
+    mn[p] = TYPE == PBX_Q41 ? f16_bits_to_f32(mbits[p]) : 0.f;
   }
 
   float xr[32];
-  prologue_block<PRO>(a, x, x2, b, active, xr);
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    float v = xa[j];
+    if constexpr (PRO == PRO_SWIGLU) v = silu(v) * xb[j];
+    xr[j] = active ? v : 0.f;
+  }
   if constexpr (PRO == PRO_RMSNORM) {
     float ss = 0.f;
-    if (active && rs == 0) {
+    if (rs == 0) {  // each block counted once
 #pragma unroll
       for (int j = 0; j < 32; ++j) ss = fmaf(xr[j], xr[j], ss);
     }
     ss = wave_sum(ss);
-    apply_rmsnorm(a, ss, K, b, active, xr);
+    const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) xr[j] = xr[j] * inv * xb[j];
   }
   float xs = 0.f, xlo = 0.f;
   if constexpr (TYPE != PBX_F32 && TYPE != PBX_F16) {
@@ -690,13 +721,14 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) {
 template <int TYPE, int WV, int RT, int IB, int PRO, int EPI>
 __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   static_assert(TYPE == PBX_Q4 || TYPE == PBX_Q8, "quantised weights only");
+  static_assert(IB <= WV, "one prologue wave per 64 blocks");
   constexpr int QB = BlockTraits<TYPE>::QB;
   constexpr int NV = QB / 16;
-  constexpr int T = WV * 64;
   constexpr bool PAIR = EPI == EPI_SWIGLU;
   __shared__ __attribute__((aligned(16))) int limb[3][PBX_INT_MAXK / 4];
   __shared__ int bsum[PBX_INT_MAXK / 32];
-  __shared__ float red[2][WV];
+  __shared__ float red[2][IB];
+  __shared__ float xscale;
   __shared__ uint64_t kred[WV];
 
   const int N = a.N, B = a.B, K = B * 32;
@@ -711,110 +743,150 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   };
   constexpr int LPR = 64 / RT;  // lanes per row after the transposed reduction
   float *y = a.Y;
+
+  // 1. Prologue waves (wave w < IB owns blocks 64w + lane) request their
+  //    activation block and RMSNorm weights before any wave requests weight
+  //    bytes: a CU returns loads in issue order, so activations requested
+  //    behind the weight stream would arrive only with it.
+  const int pb = wave * 64 + lane;  // the prologue lane's block
+  const bool pro = wave < IB;
+  const bool pvalid = pro && pb < B;
+  float4 xv[8], nv[8];
+  if (pro) {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const float *src = a.X + (size_t)(pvalid ? pb : 0) * 32 + 4 * v;
+      xv[v] = *reinterpret_cast<const float4 *>(src);
+      nv[v] = make_float4(1.f, 1.f, 1.f, 1.f);
+      if constexpr (PRO == PRO_RMSNORM)
+        nv[v] = *reinterpret_cast<const float4 *>(a.normw + (size_t)(pvalid ? pb : 0) * 32 + 4 * v);
+    }
+  }
+  lds_barrier();
+
+  // 2. Every wave: the residual it will add (EPI_ADD), the block scales, then
+  //    the weight bytes.  Loads are unconditional from clamped addresses
+  //    (rows past N read row 0, blocks past B read block 0) so the compiler
+  //    issues them back to back; a zero scale cancels what such lanes read.
   float res = 0.f;
   if constexpr (EPI == EPI_ADD) {
     const int rr = (lane % LPR) == 0 ? lane / LPR : RT;
     if (rr < RT && r0 + rr < N) res = y[r0 + rr];
   }
-
-  // weights first: they do not depend on the activations
-  uint4 q[RT][IB][NV];
-  float dsf[RT][IB];
+  unsigned dbits[RT][IB];
 #pragma unroll
   for (int i = 0; i < RT; ++i) {
-    const int rw = tile_row(i);
     const bool rok = row_ok(i);
+    const int rw = rok ? tile_row(i) : 0;
 #pragma unroll
     for (int j = 0; j < IB; ++j) {
       const int b = lane + 64 * j;
       const bool ok = rok && b < B;
-      const uint8_t *src = a.qs + ((size_t)rw * B + b) * QB;
-#pragma unroll
-      for (int v = 0; v < NV; ++v)
-        q[i][j][v] = ok ? ld_stream(src + v * 16) : make_uint4(0u, 0u, 0u, 0u);
-      dsf[i][j] = ok ? f16_bits_to_f32(a.dsc[dsc_index(rw, b, B)]) : 0.f;
+      dbits[i][j] = a.dsc[dsc_index(rw, ok ? b : 0, B)] & (ok ? 0xFFFFu : 0u);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 q[RT][IB][NV];
+#pragma unroll
+  for (int i = 0; i < RT; ++i) {
+    const int rw = row_ok(i) ? tile_row(i) : 0;
+#pragma unroll
+    for (int j = 0; j < IB; ++j) {
+      const int b = lane + 64 * j;
+      const uint8_t *src = a.qs + ((size_t)rw * B + (b < B ? b : 0)) * QB;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) q[i][j][v] = ld_stream(src + v * 16);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
 
-  // pass 1: sum of squares (RMSNorm) and max |x * w|
+  // 3. Prologue waves: sum of squares (RMSNorm) and max |x * w| of their
+  //    blocks, combined across the IB prologue waves through LDS.
   float ss = 0.f, mw = 0.f;
-  for (int i = tid * 4; i < K; i += T * 4) {
-    const float4 v = *reinterpret_cast<const float4 *>(a.X + i);
-    float4 w = make_float4(1.f, 1.f, 1.f, 1.f);
-    if constexpr (PRO == PRO_RMSNORM) {
-      w = *reinterpret_cast<const float4 *>(a.normw + i);
-      ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+  if (pro) {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const float4 t = pvalid ? xv[v] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[v];
+      if constexpr (PRO == PRO_RMSNORM)
+        ss = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, ss))));
+      mw = fmaxf(mw, fmaxf(fmaxf(fabsf(t.x * w.x), fabsf(t.y * w.y)),
+                           fmaxf(fabsf(t.z * w.z), fabsf(t.w * w.w))));
     }
-    mw = fmaxf(mw, fmaxf(fmaxf(fabsf(v.x * w.x), fabsf(v.y * w.y)),
-                         fmaxf(fabsf(v.z * w.z), fabsf(v.w * w.w))));
-  }
-  if constexpr (PRO == PRO_RMSNORM) ss = wave_sum(ss);
+    if constexpr (PRO == PRO_RMSNORM) ss = wave_sum(ss);
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mw = fmaxf(mw, __shfl_xor(mw, off, 64));
-  if (lane == 0) {
-    red[0][wave] = ss;
-    red[1][wave] = mw;
+    for (int off = 32; off >= 1; off >>= 1) mw = fmaxf(mw, __shfl_xor(mw, off, 64));
   }
-  __syncthreads();
-  ss = 0.f;
-  mw = 0.f;
-#pragma unroll
-  for (int w = 0; w < WV; ++w) {
-    ss += red[0][w];
-    mw = fmaxf(mw, red[1][w]);
-  }
-  const float inv = PRO == PRO_RMSNORM ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.f;
-  int e = 0;
-  const float mx = mw * inv;
-  if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
-  const float c = inv * ldexpf(1.f, 22 - e);  // x_q = rint(x * w * c)
-  const float unscale = ldexpf(1.f, e - 22);
-
-  // pass 2: limbs and per-block sums (8 consecutive threads cover a block)
-  for (int i = tid * 4; i < K; i += T * 4) {
-    const float4 v = *reinterpret_cast<const float4 *>(a.X + i);
-    float4 w = make_float4(1.f, 1.f, 1.f, 1.f);
-    if constexpr (PRO == PRO_RMSNORM) w = *reinterpret_cast<const float4 *>(a.normw + i);
-    const int xq[4] = {(int)rintf(v.x * w.x * c), (int)rintf(v.y * w.y * c),
-                       (int)rintf(v.z * w.z * c), (int)rintf(v.w * w.w * c)};
-    unsigned l0 = 0, l1 = 0, l2 = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int x0 = (int)(int8_t)(xq[k] & 0xFF);
-      const int r1 = (xq[k] - x0) >> 8;
-      const int x1 = (int)(int8_t)(r1 & 0xFF);
-      const int x2 = (r1 - x1) >> 8;
-      l0 |= (unsigned)(x0 & 0xFF) << (8 * k);
-      l1 |= (unsigned)(x1 & 0xFF) << (8 * k);
-      l2 |= (unsigned)(x2 & 0xFF) << (8 * k);
+  if constexpr (IB > 1) {
+    if (pro && lane == 0) {
+      red[0][wave] = ss;
+      red[1][wave] = mw;
     }
-    limb[0][i >> 2] = (int)l0;
-    limb[1][i >> 2] = (int)l1;
-    limb[2][i >> 2] = (int)l2;
-    int s4 = xq[0] + xq[1] + xq[2] + xq[3];
-    s4 += __shfl_xor(s4, 1, 64);
-    s4 += __shfl_xor(s4, 2, 64);
-    s4 += __shfl_xor(s4, 4, 64);
-    if ((tid & 7) == 0) bsum[i >> 5] = s4;
+    lds_barrier();
+    if (pro) {
+      ss = 0.f;
+      mw = 0.f;
+#pragma unroll
+      for (int w = 0; w < IB; ++w) {
+        ss += red[0][w];
+        mw = fmaxf(mw, red[1][w]);
+      }
+    }
   }
-  __syncthreads();
+  // 4. Prologue waves: fixed point x_q = rint(x * w * inv * 2^(22 - e)) of
+  //    their block as three byte limbs plus the block sum, into LDS.
+  if (pro) {
+    const float inv = PRO == PRO_RMSNORM ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.f;
+    int e = 0;
+    const float mx = mw * inv;
+    if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
+    const float c = inv * ldexpf(1.f, 22 - e);
+    if (pvalid) {
+      int bs = 0;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const float4 t = xv[v], w = nv[v];
+        const int xq[4] = {(int)rintf(t.x * w.x * c), (int)rintf(t.y * w.y * c),
+                           (int)rintf(t.z * w.z * c), (int)rintf(t.w * w.w * c)};
+        unsigned l0 = 0, l1 = 0, l2 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int x0 = (int)(int8_t)(xq[k] & 0xFF);
+          const int r1 = (xq[k] - x0) >> 8;
+          const int x1 = (int)(int8_t)(r1 & 0xFF);
+          const int x2 = (r1 - x1) >> 8;
+          l0 |= (unsigned)(x0 & 0xFF) << (8 * k);
+          l1 |= (unsigned)(x1 & 0xFF) << (8 * k);
+          l2 |= (unsigned)(x2 & 0xFF) << (8 * k);
+          bs += xq[k];
+        }
+        limb[0][pb * 8 + v] = (int)l0;
+        limb[1][pb * 8 + v] = (int)l1;
+        limb[2][pb * 8 + v] = (int)l2;
+      }
+      bsum[pb] = bs;
+    }
+    if (tid == 0) xscale = ldexpf(1.f, e - 22);
+  }
+  lds_barrier();
+  const float unscale = xscale;
 
+  // 5. Dot products as the weight rows arrive.
   float acc[RT];
 #pragma unroll
   for (int i = 0; i < RT; ++i) acc[i] = 0.f;
 #pragma unroll
   for (int j = 0; j < IB; ++j) {
     const int b = lane + 64 * j;
-    if (b >= B) continue;
+    const int bl = b < B ? b : 0;  // lanes past B: zero scales cancel them
     int xl[3][8];
 #pragma unroll
     for (int L = 0; L < 3; ++L) {
-      const int4 t0 = *reinterpret_cast<const int4 *>(&limb[L][b * 8]);
-      const int4 t1 = *reinterpret_cast<const int4 *>(&limb[L][b * 8 + 4]);
+      const int4 t0 = *reinterpret_cast<const int4 *>(&limb[L][bl * 8]);
+      const int4 t1 = *reinterpret_cast<const int4 *>(&limb[L][bl * 8 + 4]);
       xl[L][0] = t0.x; xl[L][1] = t0.y; xl[L][2] = t0.z; xl[L][3] = t0.w;
       xl[L][4] = t1.x; xl[L][5] = t1.y; xl[L][6] = t1.z; xl[L][7] = t1.w;
     }
-    const float corr = TYPE == PBX_Q4 ? 8.f * (float)bsum[b] : 0.f;
+    const float corr = TYPE == PBX_Q4 ? 8.f * (float)bsum[bl] : 0.f;
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
       int s0 = 0, s1 = 0, s2 = 0;
@@ -840,7 +912,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
         }
       }
       const float f = fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0)) - corr;
-      acc[i] = fmaf(f, dsf[i][j], acc[i]);
+      acc[i] = fmaf(f, f16_bits_to_f32(dbits[i][j]), acc[i]);
     }
   }
 

@@ -168,8 +168,8 @@ struct pbx_model {
 static bool model_ok(const pbx_model *m) { return m && m->magic == PBX_MODEL_MAGIC; }
 
 // Integer-limb kernel for the gate|up GEMV (K = 2048..4096, Q4_0 / Q8_0):
-// 16 waves x 4 rows per workgroup when that still gives >= 256 workgroups,
-// else 8 x 4.  PBX_GEMV_INT=0 at model creation selects the float-unpack
+// 16 waves x 4 rows per workgroup (Q4_0, K <= 2048) when that still gives
+// >= 256 workgroups, else 8 x 4.  PBX_GEMV_INT=0 at model creation selects the float-unpack
 // kernel instead.
 static bool int_gemv_disabled() {
   const char *e = getenv("PBX_GEMV_INT");
@@ -184,7 +184,8 @@ static bool int_shape(bool enabled, const char *mode, int type, int N, int B, in
     return false;
   *ib = B <= 64 ? 1 : 2;
   *rt = 4;
-  *wv = N / 64 >= 256 ? 16 : 8;
+  // 16 waves only for Q4_0 with one block per lane (register budget)
+  *wv = (type == PBX_TYPE_Q4_0 && *ib == 1 && N / 64 >= 256) ? 16 : 8;
   return true;
 }
 
