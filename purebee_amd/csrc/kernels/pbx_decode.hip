@@ -316,15 +316,17 @@ extern "C" __global__ void __launch_bounds__(1024) pbx_attention_split(AttnSplit
   constexpr int TL = 4;
   const int T = min(PBX_SPLIT_TILE, TL * (int)blockDim.x / hd4);
   float4 kreg[TL], vreg[TL];
+  // Unconditional loads (slots past the tile read position t0; the row at
+  // pos is replaced by the new k, v in store_tile): a load under a branch
+  // would wait at the branch's join.
   auto load_tile = [&](int t0, int n) {
 #pragma unroll
     for (int r = 0; r < TL; ++r) {
       const int i = threadIdx.x + r * blockDim.x;
-      const int j = i / hd4, c4 = 4 * (i % hd4), p = t0 + j;
-      if (i < n * hd4 && p != pos) {
-        kreg[r] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvdim + c4);
-        vreg[r] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvdim + c4);
-      }
+      const bool in = i < n * hd4;
+      const int j = in ? i / hd4 : 0, c4 = in ? 4 * (i % hd4) : 0, p = min(t0 + j, pos);
+      kreg[r] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvdim + c4);
+      vreg[r] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvdim + c4);
     }
   };
   auto store_tile = [&](int t0, int n) {
@@ -343,21 +345,24 @@ extern "C" __global__ void __launch_bounds__(1024) pbx_attention_split(AttnSplit
       }
     }
   };
-  // The first tile's K/V loads do not depend on q: issue them first.
-  if (p0 < p1) load_tile(p0, min(T, p1 - p0));
-
   // q pairs of the group's heads: Gq * hd/2 <= 64 * Gq = threads, so one
-  // pair per thread; the new k, v pair (hd/2 <= 64) likewise.
+  // pair per thread; the new k, v pair (hd/2 <= 64) likewise.  They are
+  // needed first, so they are requested before the first K/V tile (a wave's
+  // loads complete in issue order).  Unconditional loads from clamped
+  // addresses, used only where valid.
   {
     const int i = threadIdx.x;
     const bool qok = i < Gq * half, kok = has_pos && i < half;
-    const int hh = i / half, k = i % half;
-    const float2 cs = (qok || kok) ? *reinterpret_cast<const float2 *>(rp + 2 * k) : make_float2(0.f, 0.f);
-    const float2 qv = qok ? *reinterpret_cast<const float2 *>(a.qkv + (size_t)(g * Gq + hh) * hd + 2 * k)
-                          : make_float2(0.f, 0.f);
+    const int hh = qok ? i / half : 0, k = i % half;
+    const int ik = i < half ? i : 0;
+    const float2 cs = *reinterpret_cast<const float2 *>(rp + 2 * k);
+    const float2 qv = *reinterpret_cast<const float2 *>(a.qkv + (size_t)(g * Gq + hh) * hd + 2 * k);
     const float *kp = a.qkv + dim + (size_t)g * hd;
-    const float2 kv = kok ? *reinterpret_cast<const float2 *>(kp + 2 * i) : make_float2(0.f, 0.f);
-    const float2 vv = kok ? *reinterpret_cast<const float2 *>(kp + kvdim + 2 * i) : make_float2(0.f, 0.f);
+    const float2 kv = *reinterpret_cast<const float2 *>(kp + 2 * ik);
+    const float2 vv = *reinterpret_cast<const float2 *>(kp + kvdim + 2 * ik);
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile(p0, min(T, p1 - p0));  // an empty split reads row pos, unused
+    __builtin_amdgcn_sched_barrier(0);
     if (qok) {
       qs[hh][2 * k] = qv.x * cs.x - qv.y * cs.y;
       qs[hh][2 * k + 1] = qv.x * cs.y + qv.y * cs.x;
@@ -369,7 +374,7 @@ extern "C" __global__ void __launch_bounds__(1024) pbx_attention_split(AttnSplit
       vnew[2 * i + 1] = vv.y;
     }
   }
-  __syncthreads();
+  lds_barrier();  // LDS hand-off only; K/V loads stay in flight
   if (has_pos)
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
       kbase[(size_t)pos * kvdim + d] = knew[d];
@@ -381,7 +386,7 @@ extern "C" __global__ void __launch_bounds__(1024) pbx_attention_split(AttnSplit
     const int n = min(T, p1 - t0);
     if (t0 != p0) load_tile(t0, n);
     store_tile(t0, n);
-    __syncthreads();
+    lds_barrier();  // LDS hand-off only; K/V loads stay in flight
     if (w < Gq) {
       float sc = -INFINITY;
       if (lane < n) {
@@ -408,7 +413,7 @@ extern "C" __global__ void __launch_bounds__(1024) pbx_attention_split(AttnSplit
       }
       m = mn;
     }
-    __syncthreads();
+    lds_barrier();  // LDS hand-off only; K/V loads stay in flight
   }
   if (w < Gq) {
     float *pp = a.part + ((size_t)(g * Gq + w) * a.S + s) * (hd + 2);
@@ -430,16 +435,27 @@ extern "C" __global__ void __launch_bounds__(64)
 pbx_attention_combine(const float *part, float *out, int head_dim, int S) {
   const int h = blockIdx.x, lane = threadIdx.x, hd = head_dim, st = hd + 2;
   const float *pb = part + (size_t)h * S * st;
-  // every load of the first 32 splits is issued before any reduction
+  // Every load of the first 32 splits is issued before any reduction, from
+  // clamped addresses (split 0, column 0) and masked afterwards: loads under
+  // a branch would each wait at the branch's join.
+  const int c0 = lane < hd ? lane : 0, c1 = lane + 64 < hd ? lane + 64 : 0;
   float v0[32], v1[32];
 #pragma unroll
   for (int i = 0; i < 32; ++i) {
-    const bool ok = i < S;
-    v0[i] = (ok && lane < hd) ? pb[(size_t)i * st + 2 + lane] : 0.f;
-    v1[i] = (ok && lane + 64 < hd) ? pb[(size_t)i * st + 2 + 64 + lane] : 0.f;
+    const int si = i < S ? i : 0;
+    v0[i] = pb[(size_t)si * st + 2 + c0];
+    v1[i] = pb[(size_t)si * st + 2 + c1];
   }
-  const float mt = lane < S ? pb[(size_t)lane * st] : -INFINITY;
-  const float lt = lane < S ? pb[(size_t)lane * st + 1] : 0.f;
+  const int sl = lane < S ? lane : 0;
+  const float mraw = pb[(size_t)sl * st], lraw = pb[(size_t)sl * st + 1];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    v0[i] = (i < S && lane < hd) ? v0[i] : 0.f;
+    v1[i] = (i < S && lane + 64 < hd) ? v1[i] : 0.f;
+  }
+  const float mt = lane < S ? mraw : -INFINITY;
+  const float lt = lane < S ? lraw : 0.f;
   float mx = mt;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
@@ -450,9 +466,14 @@ pbx_attention_combine(const float *part, float *out, int head_dim, int S) {
     if (t0 > 0) {
 #pragma unroll
       for (int i = 0; i < 32; ++i) {
-        const bool ok = t0 + i < S;
-        v0[i] = (ok && lane < hd) ? pb[(size_t)(t0 + i) * st + 2 + lane] : 0.f;
-        v1[i] = (ok && lane + 64 < hd) ? pb[(size_t)(t0 + i) * st + 2 + 64 + lane] : 0.f;
+        const int si = t0 + i < S ? t0 + i : 0;
+        v0[i] = pb[(size_t)si * st + 2 + c0];
+        v1[i] = pb[(size_t)si * st + 2 + c1];
+      }
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        v0[i] = (t0 + i < S && lane < hd) ? v0[i] : 0.f;
+        v1[i] = (t0 + i < S && lane + 64 < hd) ? v1[i] : 0.f;
       }
     }
 #pragma unroll
