@@ -279,6 +279,172 @@ extern "C" __global__ void __launch_bounds__(256) pbx_attention_decode(AttnArgs 
 // holding `pos` rotates the new k, appends k and v to the cache and uses them
 // from LDS; no other split reads position pos.
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// Flash decoding in one workgroup per query head (head_dim <= 64): the
+// attention of llama.js:258-301 / llama-streaming.js:543-573 at batch 1.
+// Lane t of the workgroup takes position c0 + t of a 512-position chunk:
+// each wave keeps its own running max, sum and weighted V sum over its 64
+// positions (online softmax), and the eight waves merge once through LDS at
+// the end, so no second kernel and no barrier inside the position loop.
+// Loads (all unconditional, from clamped addresses; q and the new k, v
+// first): lane t reads the K row of its position as 16-byte pieces, and
+// the wave's V rows as 16-byte pieces too, lane l taking dims
+// 4(l%16)..4(l%16)+3 of positions 4k + l/16 (k < 16), so its weighted V sum
+// covers 4 dims over 16 positions and two shuffles finish the sum over the
+// wave's 64.  The row at pos is replaced by the rotated new k / new v (the
+// cache row may hold an older value); the group's first head writes them to
+// the cache.
+// ---------------------------------------------------------------------------
+#define PBX_HA_MAX_HD 64
+#define PBX_HA_WAVES 8
+
+struct HeadChunk {
+  float4 k[PBX_HA_MAX_HD / 4];  // the lane's K row
+  float4 v[16];                 // V dims 4(l%16).. of positions 4j + l/16
+};
+
+extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_head(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float qsh[PBX_HA_MAX_HD];
+  __shared__ __attribute__((aligned(16))) float knew[PBX_HA_MAX_HD];
+  __shared__ __attribute__((aligned(16))) float vnew[PBX_HA_MAX_HD];
+  __shared__ float wm[PBX_HA_WAVES], wl[PBX_HA_WAVES];
+  __shared__ __attribute__((aligned(16))) float wacc[PBX_HA_WAVES][PBX_HA_MAX_HD];
+  __shared__ float dnew;  // q . (new k)
+  constexpr int CH = PBX_HA_WAVES * 64;  // positions per chunk
+  const int h = blockIdx.x, hd = a.head_dim, half = hd / 2, hd4 = hd / 4;
+  const int Gq = a.n_heads / a.n_kv_heads, g = h / Gq;
+  const int dim = a.n_heads * hd, kvdim = a.n_kv_heads * hd;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int pos = a.state[0], L = pos + 1;
+  float *kb = a.kcache + (size_t)g * hd, *vb = a.vcache + (size_t)g * hd;
+  const int dg = lane & 15, ps = lane >> 4;      // V: dim group, position slot
+  const int dcol = 4 * min(dg, hd4 - 1);         // clamped for head_dim < 64
+
+  // 1. this token's q, k, v pair (thread t < hd/2 owns pair t)
+  const int k2 = tid < half ? tid : 0;
+  const float2 cs = *reinterpret_cast<const float2 *>(a.rope + (size_t)pos * hd + 2 * k2);
+  const float2 qv = *reinterpret_cast<const float2 *>(a.qkv + (size_t)h * hd + 2 * k2);
+  const float2 kv = *reinterpret_cast<const float2 *>(a.qkv + dim + (size_t)g * hd + 2 * k2);
+  const float2 vv = *reinterpret_cast<const float2 *>(a.qkv + dim + kvdim + (size_t)g * hd + 2 * k2);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. K rows and V pieces of the first chunk
+  auto load_chunk = [&](int c0, HeadChunk &ch) {
+    const int pk = min(c0 + tid, pos);
+#pragma unroll
+    for (int i = 0; i < PBX_HA_MAX_HD / 4; ++i)
+      ch.k[i] = *reinterpret_cast<const float4 *>(kb + (size_t)pk * kvdim + 4 * min(i, hd4 - 1));
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      ch.v[j] = *reinterpret_cast<const float4 *>(
+          vb + (size_t)min(c0 + w * 64 + 4 * j + ps, pos) * kvdim + dcol);
+  };
+  HeadChunk first;
+  load_chunk(0, first);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. RoPE (adjacent pairs, llama.js:163-190) of q and the new k
+  if (w == 0) {  // hd/2 <= 32: the pairs live in wave 0
+    const float q0 = qv.x * cs.x - qv.y * cs.y, q1 = qv.x * cs.y + qv.y * cs.x;
+    const float k0 = kv.x * cs.x - kv.y * cs.y, k1 = kv.x * cs.y + kv.y * cs.x;
+    if (tid < half) {
+      qsh[2 * tid] = q0;
+      qsh[2 * tid + 1] = q1;
+      knew[2 * tid] = k0;
+      knew[2 * tid + 1] = k1;
+      vnew[2 * tid] = vv.x;
+      vnew[2 * tid + 1] = vv.y;
+    }
+    const float dq = wave_sum(tid < half ? fmaf(q0, k0, q1 * k1) : 0.f);
+    if (tid == 0) dnew = dq;
+  }
+  lds_barrier();
+  if (h % Gq == 0 && tid < hd) {  // KV-cache append, once per group
+    kb[(size_t)pos * kvdim + tid] = knew[tid];
+    vb[(size_t)pos * kvdim + tid] = vnew[tid];
+  }
+  const float4 vnw = *reinterpret_cast<const float4 *>(&vnew[dcol]);
+
+  // 4. scores and the wave's softmax-weighted V sum, chunk by chunk (the
+  //    first chunk from the registers loaded above; later ones, for
+  //    contexts past 512 positions, load their own)
+  float m = -INFINITY, l = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto chunk = [&](int c0, const HeadChunk &ch) {
+    const int p = c0 + tid;
+    const bool valid = p < L, cur = p == pos;
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < PBX_HA_MAX_HD / 4; ++i) {
+      const float4 qq = *reinterpret_cast<const float4 *>(&qsh[4 * i]);
+      const float4 kk = ch.k[i];
+      // dims past head_dim hold repeats of the last column: masked out
+      const float mq = i < hd4 ? 1.f : 0.f;
+      d0 = fmaf(qq.x * mq, kk.x, d0);
+      d1 = fmaf(qq.y * mq, kk.y, d1);
+      d0 = fmaf(qq.z * mq, kk.z, d0);
+      d1 = fmaf(qq.w * mq, kk.w, d1);
+    }
+    const float dot = cur ? dnew : d0 + d1;  // position pos: the new k
+    const float sc = valid ? dot * a.scale : -INFINITY;
+    float mt = sc;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
+    const float mn = fmaxf(m, mt);
+    const float f = m == -INFINITY ? 0.f : expf(m - mn);  // nothing accumulated yet
+    const float pr = valid ? expf(sc - mn) : 0.f;
+    l = fmaf(l, f, wave_sum(pr));
+    acc.x *= f; acc.y *= f; acc.z *= f; acc.w *= f;
+    const int pw = c0 + w * 64;  // the wave's first position
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int slot = 4 * j + ps;
+      const float pj = __shfl(pr, slot, 64);
+      const float4 vj = pw + slot == pos ? vnw : ch.v[j];
+      acc.x = fmaf(pj, vj.x, acc.x);
+      acc.y = fmaf(pj, vj.y, acc.y);
+      acc.z = fmaf(pj, vj.z, acc.z);
+      acc.w = fmaf(pj, vj.w, acc.w);
+    }
+    m = mn;
+  };
+  chunk(0, first);
+  for (int c0 = CH; c0 < L; c0 += CH) {
+    HeadChunk next;
+    load_chunk(c0, next);
+    chunk(c0, next);
+  }
+  // the four position slots of each dim group
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+    acc.x += __shfl_xor(acc.x, off, 64);
+    acc.y += __shfl_xor(acc.y, off, 64);
+    acc.z += __shfl_xor(acc.z, off, 64);
+    acc.w += __shfl_xor(acc.w, off, 64);
+  }
+
+  // 5. merge the waves
+  if (lane == 0) {
+    wm[w] = m;
+    wl[w] = l;
+  }
+  if (lane < hd4) *reinterpret_cast<float4 *>(&wacc[w][4 * lane]) = acc;
+  lds_barrier();
+  if (tid < hd) {
+    float M = wm[0];
+#pragma unroll
+    for (int i = 1; i < PBX_HA_WAVES; ++i) M = fmaxf(M, wm[i]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int i = 0; i < PBX_HA_WAVES; ++i) {
+      const float e = wm[i] == -INFINITY ? 0.f : expf(wm[i] - M);
+      num = fmaf(e, wacc[i][tid], num);
+      den = fmaf(e, wl[i], den);
+    }
+    a.out[(size_t)h * hd + tid] = num / den;
+  }
+}
+
 #define PBX_SPLIT_TILE 32
 #define PBX_SPLIT_MAX_HD 128
 #define PBX_SPLIT_MAX_GQ 16

@@ -83,6 +83,7 @@ struct ArgmaxArgsHost {  // ArgmaxArgs in pbx_decode.hip
 };
 
 enum ArgKind { ARG_GEMV, ARG_ATTN, ARG_ATTN_SPLIT, ARG_COMBINE, ARG_EMBED, ARG_ARGMAX };
+enum AttnMode { ATTN_HEAD, ATTN_SPLIT, ATTN_DECODE };
 
 struct Op {
   hipFunction_t f = nullptr;
@@ -147,6 +148,7 @@ struct pbx_model {
   // split-position attention: S splits per KV head and their partials
   int attn_splits = 0;
   float *attn_part = nullptr;
+  int attn_mode = 0;  // AttnMode
   int *state = nullptr;
   int *hist = nullptr;
   int hist_cap = 0;
@@ -275,7 +277,8 @@ static int build_ops(pbx_model *m) {
                           g.dim, g.vocab_size, m->embd->m};
   m->ops.push_back(e);
   hipFunction_t fattn = pbx_kernel_by_name(c, "pbx_attention_decode");
-  if (!fattn) return pbx_fail(c, PBX_ELOAD, "model: kernel pbx_attention_decode not found");
+  hipFunction_t fhead = pbx_kernel_by_name(c, "pbx_attention_head");
+  if (!fattn || !fhead) return pbx_fail(c, PBX_ELOAD, "model: attention kernels not found");
   hipFunction_t fsplit = pbx_kernel_by_name(c, "pbx_attention_split");
   hipFunction_t fcomb = pbx_kernel_by_name(c, "pbx_attention_combine");
   if (!fsplit || !fcomb)
@@ -289,7 +292,17 @@ static int build_ops(pbx_model *m) {
     a.role = "attn";
     a.bytes = 2.0 * 4.0 * m->kvdim;  // K and V of one cached position, all KV heads
     a.block = dim3(256);
-    if (m->attn_splits > 0) {
+    if (m->attn_mode == ATTN_HEAD) {
+      a.kind = ARG_ATTN;
+      a.name = "pbx_attention_head";
+      a.f = fhead;
+      a.grid = dim3(g.n_heads);
+      a.block = dim3(512);
+      a.attn = AttnArgsHost{m->qkv, m->kcache + l * layer_kv, m->vcache + l * layer_kv, m->rope,
+                            m->attn, m->state, g.n_heads, g.n_kv_heads, g.head_dim,
+                            (float)(1.0 / sqrt((double)g.head_dim))};
+      m->ops.push_back(a);
+    } else if (m->attn_splits > 0) {
       a.kind = ARG_ATTN_SPLIT;
       a.name = "pbx_attention_split";
       a.f = fsplit;
@@ -481,10 +494,21 @@ void pbx_model_release_all(pbx_ctx *c) {
   c->models = nullptr;
 }
 
-// PBX_SPLIT_ATTENTION=0 selects the one-workgroup-per-head attention kernel.
-static bool split_attention_disabled() {
-  const char *e = getenv("PBX_SPLIT_ATTENTION");
-  return e && e[0] == '0';
+// Decode attention kernel: "head" (pbx_attention_head, one workgroup per
+// query head with in-workgroup position splits; head_dim <= 64), "split"
+// (pbx_attention_split + pbx_attention_combine; head_dim <= 128) or
+// "decode" (pbx_attention_decode).  The default is the first that applies;
+// PBX_ATTENTION=split|decode at model creation forces one (and the older
+// PBX_SPLIT_ATTENTION=0 selects "decode").
+static AttnMode attention_mode(const pbx_model_config &g) {
+  const bool split_ok = g.head_dim <= 128 && g.n_heads / g.n_kv_heads <= 16;
+  const char *e = getenv("PBX_ATTENTION");
+  const char *legacy = getenv("PBX_SPLIT_ATTENTION");
+  if (legacy && legacy[0] == '0') return ATTN_DECODE;
+  if (e && strcmp(e, "decode") == 0) return ATTN_DECODE;
+  if (e && strcmp(e, "split") == 0) return split_ok ? ATTN_SPLIT : ATTN_DECODE;
+  if (g.head_dim <= 64) return ATTN_HEAD;
+  return split_ok ? ATTN_SPLIT : ATTN_DECODE;
 }
 
 static bool is_weight_type(int t) {
@@ -562,7 +586,8 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
   // Split-position attention when its tiles fit (head_dim <= 128, <= 16
   // query heads per KV head): about 256 workgroups per layer, at most 64
   // splits, never more splits than positions.
-  if (!rc && g.head_dim <= 128 && g.n_heads / g.n_kv_heads <= 16 && !split_attention_disabled()) {
+  m->attn_mode = attention_mode(g);
+  if (!rc && m->attn_mode == ATTN_SPLIT) {
     m->attn_splits = std::min({64, g.max_seq, std::max(4, (256 + g.n_kv_heads - 1) / g.n_kv_heads)});
     rc = dalloc(m, (void **)&m->attn_part,
                 (size_t)g.n_heads * m->attn_splits * (g.head_dim + 2) * 4);

@@ -143,30 +143,37 @@ def test_cache_rollback_and_reset(ctx):
     ref.close()
 
 
-def test_split_attention_matches_one_workgroup_per_head(ctx, monkeypatch):
-    """The split-position attention (KV group x position split, online
-    softmax over 32-position tiles, last-workgroup combine) against the
-    one-workgroup-per-head kernel and the oracle.  64 KV heads give 4 splits,
-    so 160 positions take two tiles per split."""
-    print("[case] split attention vs per-head attention, 64 heads, 160 positions", flush=True)
-    cfg = tiny(TYPE_Q8_0, TYPE_Q8_0, dim=2048, hidden_dim=256, n_layers=1, n_heads=64,
-               n_kv_heads=64, vocab_size=512, max_seq=256)
-    split, ref, cfg = make_pair(ctx, cfg, 97)
-    monkeypatch.setenv("PBX_SPLIT_ATTENTION", "0")
+@pytest.mark.parametrize("mode,heads,kv,steps", [
+    ("split", 64, 64, 160),   # 4 splits: 160 positions take two tiles per split
+    ("head", 64, 64, 160),    # head_dim 32
+    ("head", 32, 8, 560),     # head_dim 64, GQA 4:1, past one 512-position chunk
+])
+def test_attention_kernels_match_one_workgroup_per_head(ctx, monkeypatch, mode, heads, kv, steps):
+    """The decode attention kernels against the one-workgroup-per-head kernel
+    and the oracle: split-position attention (KV group x position split,
+    online softmax over 32-position tiles, combine kernel) and the per-head
+    flash-decoding kernel (eight waves of 64 positions merged in LDS, chunks
+    of 512 positions)."""
+    print(f"[case] attention {mode} vs per-head, {heads}/{kv} heads, {steps} positions", flush=True)
+    cfg = tiny(TYPE_Q8_0, TYPE_Q8_0, dim=2048, hidden_dim=256, n_layers=1, n_heads=heads,
+               n_kv_heads=kv, vocab_size=512, max_seq=max(256, steps + 8))
+    monkeypatch.setenv("PBX_ATTENTION", mode)
+    under, ref, cfg = make_pair(ctx, cfg, 97)
+    monkeypatch.setenv("PBX_ATTENTION", "decode")
     one = synth.build(ctx, cfg, 97)
-    monkeypatch.delenv("PBX_SPLIT_ATTENTION")
-    toks = [int(t) for t in synth.random_tokens(98, 160, cfg["vocab_size"])]
+    monkeypatch.delenv("PBX_ATTENTION")
+    toks = [int(t) for t in synth.random_tokens(98, steps, cfg["vocab_size"])]
     worst = 0.0
     for p, t in enumerate(toks):
-        a, _ = split.forward([t], p)
+        a, _ = under.forward([t], p)
         b, _ = one.forward([t], p)
         worst = max(worst, float(np.abs(a - b).max()))
     r = ref.forward(toks, 0)
     err = float(np.abs(a - r).max())
-    print(f"  split vs per-head max-abs {worst:.2e}, vs oracle {err:.2e}")
+    print(f"  {mode} vs per-head max-abs {worst:.2e}, vs oracle {err:.2e}")
     assert worst <= 1e-4
     assert err <= LOGIT_TOL
-    split.free()
+    under.free()
     one.free()
     ref.close()
 
