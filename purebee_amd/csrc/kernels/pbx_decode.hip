@@ -298,9 +298,12 @@ extern "C" __global__ void __launch_bounds__(256) pbx_attention_decode(AttnArgs 
 #define PBX_HA_MAX_HD 64
 #define PBX_HA_WAVES 8
 
+// Lane l of wave w holds dims 4(l%16)..4(l%16)+3 of the wave's positions
+// 4j + l/16, j = 0..15, of K and of V: each load instruction reads four
+// whole 256-byte rows.
 struct HeadChunk {
-  float4 k[PBX_HA_MAX_HD / 4];  // the lane's K row
-  float4 v[16];                 // V dims 4(l%16).. of positions 4j + l/16
+  float4 k[16];
+  float4 v[16];
 };
 
 extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_head(AttnArgs a) {
@@ -329,11 +332,12 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
   __builtin_amdgcn_sched_barrier(0);
 
   // 2. K rows and V pieces of the first chunk
-  auto load_chunk = [&](int c0, HeadChunk &ch) {
-    const int pk = min(c0 + tid, pos);
+  auto load_chunk = [&](int c0, HeadChunk &ch) {  // all of K before V: the
+    // scores need all of K while V is still arriving
 #pragma unroll
-    for (int i = 0; i < PBX_HA_MAX_HD / 4; ++i)
-      ch.k[i] = *reinterpret_cast<const float4 *>(kb + (size_t)pk * kvdim + 4 * min(i, hd4 - 1));
+    for (int j = 0; j < 16; ++j)
+      ch.k[j] = *reinterpret_cast<const float4 *>(
+          kb + (size_t)min(c0 + w * 64 + 4 * j + ps, pos) * kvdim + dcol);
 #pragma unroll
     for (int j = 0; j < 16; ++j)
       ch.v[j] = *reinterpret_cast<const float4 *>(
@@ -370,22 +374,31 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
   //    contexts past 512 positions, load their own)
   float m = -INFINITY, l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  // the lane's q piece; dims past head_dim (repeats of the last column)
+  // are masked out
+  float4 qq = *reinterpret_cast<const float4 *>(&qsh[dcol]);
+  if (dg >= hd4) qq = make_float4(0.f, 0.f, 0.f, 0.f);
   auto chunk = [&](int c0, const HeadChunk &ch) {
-    const int p = c0 + tid;
-    const bool valid = p < L, cur = p == pos;
-    float d0 = 0.f, d1 = 0.f;
+    // partial dots of the 16 positions, then a reduce-scatter over the 16
+    // lanes of a position slot: after halving across lane bits 3, 2, 1, 0
+    // lane l holds the whole dot of position 4(l%16) + l/16
+    float s[16];
 #pragma unroll
-    for (int i = 0; i < PBX_HA_MAX_HD / 4; ++i) {
-      const float4 qq = *reinterpret_cast<const float4 *>(&qsh[4 * i]);
-      const float4 kk = ch.k[i];
-      // dims past head_dim hold repeats of the last column: masked out
-      const float mq = i < hd4 ? 1.f : 0.f;
-      d0 = fmaf(qq.x * mq, kk.x, d0);
-      d1 = fmaf(qq.y * mq, kk.y, d1);
-      d0 = fmaf(qq.z * mq, kk.z, d0);
-      d1 = fmaf(qq.w * mq, kk.w, d1);
+    for (int j = 0; j < 16; ++j)
+      s[j] = fmaf(qq.x, ch.k[j].x, fmaf(qq.y, ch.k[j].y, fmaf(qq.z, ch.k[j].z, qq.w * ch.k[j].w)));
+#pragma unroll
+    for (int half_n = 8; half_n >= 1; half_n >>= 1) {
+      const bool upper = dg & half_n;
+#pragma unroll
+      for (int k = 0; k < half_n; ++k) {
+        const float send = upper ? s[k] : s[k + half_n];
+        const float keep = upper ? s[k + half_n] : s[k];
+        s[k] = keep + __shfl_xor(send, half_n, 64);
+      }
     }
-    const float dot = cur ? dnew : d0 + d1;  // position pos: the new k
+    const int p = c0 + w * 64 + 4 * dg + ps;
+    const bool valid = p < L, cur = p == pos;
+    const float dot = cur ? dnew : s[0];  // position pos: the new k
     const float sc = valid ? dot * a.scale : -INFINITY;
     float mt = sc;
 #pragma unroll
@@ -399,7 +412,7 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int slot = 4 * j + ps;
-      const float pj = __shfl(pr, slot, 64);
+      const float pj = __shfl(pr, (lane & 48) | j, 64);  // slot 4j + ps
       const float4 vj = pw + slot == pos ? vnw : ch.v[j];
       acc.x = fmaf(pj, vj.x, acc.x);
       acc.y = fmaf(pj, vj.y, acc.y);
