@@ -61,15 +61,17 @@ DK_MODES_SMALL(PBX_F16, f16, 4)
 DK_MODES_WIDE(PBX_Q6K, q6k, 4)
 DK_MODES_WIDE(PBX_Q6K, q6k, 8)
 DK_MODES_SMALL(PBX_Q6K, q6k, 4)
-// Integer-limb kernels for the gate|up GEMV (RMSNorm + SwiGLU pair), the
-// largest matrix of a layer; for the smaller GEMVs the activation prologue
-// costs more than the dot products save (measured).
-// Name: pbx_dk_<type>_i<WV>x<RT>b<IB>_gu.
-#define DK_INT_GU(T, TN, WV, RT, IB)                                                      \
+// Integer-limb kernels (Q4_0 / Q8_0, 2048 <= K <= 8192).
+// Name: pbx_dk_<type>_i<WV>x<RT>b<IB>_<mode>.
+#define DK_INT(T, TN, WV, RT, IB, PRO, EPI, MN)                                            \
   extern "C" __global__ void __launch_bounds__(WV * 64)                                   \
-      pbx_dk_##TN##_i##WV##x##RT##b##IB##_gu(GemvArgs a) {                                \
-    gemv_int<T, WV, RT, IB, PRO_RMSNORM, EPI_SWIGLU>(a);                                  \
+      pbx_dk_##TN##_i##WV##x##RT##b##IB##_##MN(GemvArgs a) {                              \
+    gemv_int<T, WV, RT, IB, PRO, EPI>(a);                                                 \
   }
+#define DK_INT_GU(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_RMSNORM, EPI_SWIGLU, gu)
+#define DK_INT_QKV(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_RMSNORM, EPI_STORE, qkv)
+#define DK_INT_ADD(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_NONE, EPI_ADD, add)
+#define DK_INT_LMH(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_RMSNORM, EPI_ARGMAX, lmh)
 // 16-wave workgroups (at most 128 VGPRs a lane) only where the prologue
 // wave's activation registers still fit: Q4_0 with one block per lane.
 DK_INT_GU(PBX_Q4, q4, 8, 4, 1)
@@ -77,6 +79,24 @@ DK_INT_GU(PBX_Q4, q4, 16, 4, 1)
 DK_INT_GU(PBX_Q4, q4, 8, 4, 2)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 1)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 2)
+DK_INT_QKV(PBX_Q4, q4, 4, 2, 1)
+DK_INT_QKV(PBX_Q4, q4, 4, 4, 1)
+DK_INT_QKV(PBX_Q4, q4, 8, 2, 1)
+DK_INT_QKV(PBX_Q4, q4, 8, 4, 1)
+DK_INT_QKV(PBX_Q4, q4, 16, 2, 1)
+DK_INT_ADD(PBX_Q4, q4, 4, 2, 1)
+DK_INT_ADD(PBX_Q4, q4, 4, 4, 1)
+DK_INT_ADD(PBX_Q4, q4, 8, 2, 1)
+DK_INT_ADD(PBX_Q4, q4, 8, 4, 1)
+DK_INT_ADD(PBX_Q4, q4, 16, 2, 1)
+DK_INT_ADD(PBX_Q4, q4, 4, 2, 4)
+DK_INT_ADD(PBX_Q4, q4, 4, 4, 4)
+DK_INT_ADD(PBX_Q4, q4, 8, 2, 4)
+DK_INT_ADD(PBX_Q4, q4, 8, 4, 4)
+DK_INT_LMH(PBX_Q4, q4, 4, 8, 1)
+DK_INT_LMH(PBX_Q4, q4, 8, 4, 1)
+DK_INT_LMH(PBX_Q4, q4, 8, 8, 1)
+DK_INT_LMH(PBX_Q4, q4, 16, 4, 1)
 
 DK_MODES_WIDE(PBX_F32, f32, 2)
 DK_MODES_WIDE(PBX_F32, f32, 4)
@@ -386,24 +406,12 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
 #pragma unroll
     for (int j = 0; j < 16; ++j)
       s[j] = fmaf(qq.x, ch.k[j].x, fmaf(qq.y, ch.k[j].y, fmaf(qq.z, ch.k[j].z, qq.w * ch.k[j].w)));
-#pragma unroll
-    for (int half_n = 8; half_n >= 1; half_n >>= 1) {
-      const bool upper = dg & half_n;
-#pragma unroll
-      for (int k = 0; k < half_n; ++k) {
-        const float send = upper ? s[k] : s[k + half_n];
-        const float keep = upper ? s[k + half_n] : s[k];
-        s[k] = keep + __shfl_xor(send, half_n, 64);
-      }
-    }
+    transpose_stage<16, 8, 16>(s, lane);
     const int p = c0 + w * 64 + 4 * dg + ps;
     const bool valid = p < L, cur = p == pos;
     const float dot = cur ? dnew : s[0];  // position pos: the new k
     const float sc = valid ? dot * a.scale : -INFINITY;
-    float mt = sc;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
-    const float mn = fmaxf(m, mt);
+    const float mn = fmaxf(m, wave_max(sc));
     const float f = m == -INFINITY ? 0.f : expf(m - mn);  // nothing accumulated yet
     const float pr = valid ? expf(sc - mn) : 0.f;
     l = fmaf(l, f, wave_sum(pr));

@@ -292,10 +292,43 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// The value the butterfly partner at distance OFF holds.  Distances inside
+// a 16-lane row use DPP (a VALU operand modifier: no LDS round trip), with a
+// partner that differs in bit OFF and agrees in the bits above it:
+//   8 -> row_ror:8 (lane ^ 8), 4 -> row_half_mirror (lane ^ 7),
+//   2 -> quad_perm 3,2,1,0 (lane ^ 3), 1 -> quad_perm 1,0,3,2 (lane ^ 1).
+// 16 and 32 go through ds_bpermute.  The masks 32, 16, 8, 7, 3, 1 are
+// independent, so a butterfly over them sums all 64 lanes, and each stage's
+// partner agrees on the bits earlier stages split on, which the transposed
+// reductions rely on.  All 64 lanes must be active.
+template <int OFF>
+__device__ __forceinline__ float lane_partner(float v) {
+  if constexpr (OFF >= 16) {
+    return __shfl_xor(v, OFF, 64);
+  } else {
+    constexpr int ctrl = OFF == 8 ? 0x128 : OFF == 4 ? 0x141 : OFF == 2 ? 0x1B : 0xB1;
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false));
+  }
+}
+
+template <int OFF = 32>
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  if constexpr (OFF >= 1) {
+    v += lane_partner<OFF>(v);
+    return wave_sum<OFF / 2>(v);
+  } else {
+    return v;
+  }
+}
+
+template <int OFF = 32>
+__device__ __forceinline__ float wave_max(float v) {
+  if constexpr (OFF >= 1) {
+    v = fmaxf(v, lane_partner<OFF>(v));
+    return wave_max<OFF / 2>(v);
+  } else {
+    return v;
+  }
 }
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
@@ -378,7 +411,7 @@ __device__ __forceinline__ void transpose_stage(float (&v)[R], int lane) {
     for (int i = 0; i < CNT / 2; ++i) {
       const float keep = up ? v[i + CNT / 2] : v[i];
       const float send = up ? v[i] : v[i + CNT / 2];
-      v[i] = keep + __shfl_xor(send, OFF, 64);
+      v[i] = keep + lane_partner<OFF>(send);
     }
     transpose_stage<CNT / 2, OFF / 2, R>(v, lane);
   }
@@ -387,10 +420,7 @@ __device__ __forceinline__ void transpose_stage(float (&v)[R], int lane) {
 template <int R>
 __device__ __forceinline__ float wave_transpose_reduce(float (&v)[R], int lane) {
   transpose_stage<R, 32, R>(v, lane);
-  float r = v[0];
-#pragma unroll
-  for (int off = (64 / R) / 2; off >= 1; off >>= 1) r += __shfl_xor(r, off, 64);
-  return r;
+  return wave_sum<(64 / R) / 2>(v[0]);
 }
 
 // Store of output row n; `res` is the residual y[n] read at kernel start
@@ -712,7 +742,7 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
 // Workgroup: WV waves x RT rows each (PAIR: RT/2 gate + RT/2 up rows); lane
 // l owns blocks l, l+64, ... (IB of them).
 // ---------------------------------------------------------------------------
-#define PBX_INT_MAXK 4096
+#define PBX_INT_MAXK 8192
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
@@ -725,8 +755,9 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   constexpr int QB = BlockTraits<TYPE>::QB;
   constexpr int NV = QB / 16;
   constexpr bool PAIR = EPI == EPI_SWIGLU;
-  __shared__ __attribute__((aligned(16))) int limb[3][PBX_INT_MAXK / 4];
-  __shared__ int bsum[PBX_INT_MAXK / 32];
+  static_assert(IB * 64 * 32 <= PBX_INT_MAXK, "K limit");
+  __shared__ __attribute__((aligned(16))) int limb[3][IB * 64 * 8];
+  __shared__ int bsum[IB * 64];
   __shared__ float red[2][IB];
   __shared__ float xscale;
   __shared__ uint64_t kred[WV];
@@ -813,8 +844,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
                            fmaxf(fabsf(t.z * w.z), fabsf(t.w * w.w))));
     }
     if constexpr (PRO == PRO_RMSNORM) ss = wave_sum(ss);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mw = fmaxf(mw, __shfl_xor(mw, off, 64));
+    mw = wave_max(mw);
   }
   if constexpr (IB > 1) {
     if (pro && lane == 0) {

@@ -178,13 +178,34 @@ static bool int_gemv_disabled() {
   return e && e[0] == '0';
 }
 
-static bool int_shape(bool enabled, const char *mode, int type, int N, int B, int *wv, int *rt,
-                      int *ib) {
-  if (!enabled) return false;
-  if (strcmp(mode, "gu") != 0 || (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0) || B < 64 ||
-      B > 128)
+// PBX_GEMV_INT_SHAPES="role=WVxRT,..." (roles qkv, o, gate_up, down,
+// lm_head), read when the step is planned: the integer-limb kernel with WV
+// waves x RT rows for the listed roles (Q4_0 / Q8_0, K = 2048..8192), for
+// tuning.  A shape that was not compiled fails the plan.
+static bool int_override(const char *role, int *wv, int *rt) {
+  const char *e = getenv("PBX_GEMV_INT_SHAPES");
+  if (!e || !role) return false;
+  const std::string s(e), key = std::string(role) + "=";
+  size_t p = 0;
+  while (p < s.size()) {
+    size_t q = s.find(',', p);
+    if (q == std::string::npos) q = s.size();
+    const std::string item = s.substr(p, q - p);
+    if (item.compare(0, key.size(), key) == 0 &&
+        sscanf(item.c_str() + key.size(), "%dx%d", wv, rt) == 2)
+      return true;
+    p = q + 1;
+  }
+  return false;
+}
+
+static bool int_shape(bool enabled, const char *mode, const char *role, int type, int N, int B,
+                      int *wv, int *rt, int *ib) {
+  if (!enabled || (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0) || B < 64 || B > 256)
     return false;
-  *ib = B <= 64 ? 1 : 2;
+  *ib = (B + 63) / 64;
+  if (int_override(role, wv, rt)) return *ib <= *wv;
+  if (strcmp(mode, "gu") != 0 || B > 128) return false;
   *rt = 4;
   // 16 waves only for Q4_0 with one block per lane (register budget)
   *wv = (type == PBX_TYPE_Q4_0 && *ib == 1 && N / 64 >= 256) ? 16 : 8;
@@ -195,10 +216,10 @@ static bool int_shape(bool enabled, const char *mode, int type, int N, int B, in
 // instruction): the integer-limb kernel for the gate|up GEMV where it
 // applies; else the small-K kernel for B <= 32, otherwise ceil(B/64) waves
 // per workgroup and the largest row tile that keeps >= 4 workgroups per CU.
-static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, int type, int N, int B,
-                      std::string *shape, dim3 *grid, dim3 *block, int *n_tiles) {
+static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, const char *role, int type,
+                      int N, int B, std::string *shape, dim3 *grid, dim3 *block, int *n_tiles) {
   int wv, rt, ib;
-  if (int_shape(int_ok, mode, type, N, B, &wv, &rt, &ib)) {
+  if (int_shape(int_ok, mode, role, type, N, B, &wv, &rt, &ib)) {
     *shape = "i" + std::to_string(wv) + "x" + std::to_string(rt) + "b" + std::to_string(ib);
     *grid = dim3((N + wv * rt - 1) / (wv * rt));
     *block = dim3(64 * wv);
@@ -239,7 +260,7 @@ static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const c
   op.kind = ARG_GEMV;
   std::string shape;
   int n_tiles = 0;
-  plan_gemv(c, m->gemv_int, mode, w->type, (int)w->N, (int)w->B, &shape, &op.grid, &op.block,
+  plan_gemv(c, m->gemv_int, mode, role, w->type, (int)w->N, (int)w->B, &shape, &op.grid, &op.block,
             &n_tiles);
   if (w->B > 32 && (w->B + 63) / 64 > 8)
     return pbx_fail(c, PBX_ENOTSUP, "model: K=%lld exceeds the GEMV limit of 16384",
