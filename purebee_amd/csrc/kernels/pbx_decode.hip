@@ -61,7 +61,8 @@ DK_MODES_SMALL(PBX_F16, f16, 4)
 DK_MODES_WIDE(PBX_Q6K, q6k, 4)
 DK_MODES_WIDE(PBX_Q6K, q6k, 8)
 DK_MODES_SMALL(PBX_Q6K, q6k, 4)
-// Integer-limb kernels (Q4_0 / Q8_0, 2048 <= K <= 8192).
+// Integer-limb kernels (Q4_0 / Q8_0, 2048 <= K <= 8192): gate|up for both
+// types, every decode GEMV for Q4_0.
 // Name: pbx_dk_<type>_i<WV>x<RT>b<IB>_<mode>.
 #define DK_INT(T, TN, WV, RT, IB, PRO, EPI, MN)                                            \
   extern "C" __global__ void __launch_bounds__(WV * 64)                                   \
@@ -79,24 +80,19 @@ DK_INT_GU(PBX_Q4, q4, 16, 4, 1)
 DK_INT_GU(PBX_Q4, q4, 8, 4, 2)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 1)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 2)
-DK_INT_QKV(PBX_Q4, q4, 4, 2, 1)
+// Q4_0 decode roles (measured on Llama-3.2-1B shapes): qkv 4 x 4, o and
+// down 4 x 2, lm head 4 x 16; the others are tuning alternatives.
 DK_INT_QKV(PBX_Q4, q4, 4, 4, 1)
+DK_INT_QKV(PBX_Q4, q4, 4, 4, 2)
 DK_INT_QKV(PBX_Q4, q4, 8, 2, 1)
-DK_INT_QKV(PBX_Q4, q4, 8, 4, 1)
-DK_INT_QKV(PBX_Q4, q4, 16, 2, 1)
 DK_INT_ADD(PBX_Q4, q4, 4, 2, 1)
-DK_INT_ADD(PBX_Q4, q4, 4, 4, 1)
-DK_INT_ADD(PBX_Q4, q4, 8, 2, 1)
-DK_INT_ADD(PBX_Q4, q4, 8, 4, 1)
-DK_INT_ADD(PBX_Q4, q4, 16, 2, 1)
+DK_INT_ADD(PBX_Q4, q4, 4, 2, 2)
 DK_INT_ADD(PBX_Q4, q4, 4, 2, 4)
-DK_INT_ADD(PBX_Q4, q4, 4, 4, 4)
-DK_INT_ADD(PBX_Q4, q4, 8, 2, 4)
-DK_INT_ADD(PBX_Q4, q4, 8, 4, 4)
+DK_INT_ADD(PBX_Q4, q4, 4, 1, 1)
+DK_INT_ADD(PBX_Q4, q4, 4, 1, 4)
+DK_INT_LMH(PBX_Q4, q4, 4, 16, 1)
+DK_INT_LMH(PBX_Q4, q4, 4, 16, 2)
 DK_INT_LMH(PBX_Q4, q4, 4, 8, 1)
-DK_INT_LMH(PBX_Q4, q4, 8, 4, 1)
-DK_INT_LMH(PBX_Q4, q4, 8, 8, 1)
-DK_INT_LMH(PBX_Q4, q4, 16, 4, 1)
 
 DK_MODES_WIDE(PBX_F32, f32, 2)
 DK_MODES_WIDE(PBX_F32, f32, 4)

@@ -144,7 +144,7 @@ struct pbx_model {
   float *x = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
   uint64_t *partials = nullptr;
   int n_partials_cap = 0;
-  bool gemv_int = true;  // integer-limb gate|up GEMV where it applies
+  bool gemv_int = true;  // integer-limb GEMV kernels where they apply
   // split-position attention: S splits per KV head and their partials
   int attn_splits = 0;
   float *attn_part = nullptr;
@@ -169,10 +169,11 @@ struct pbx_model {
 
 static bool model_ok(const pbx_model *m) { return m && m->magic == PBX_MODEL_MAGIC; }
 
-// Integer-limb kernel for the gate|up GEMV (K = 2048..4096, Q4_0 / Q8_0):
-// 16 waves x 4 rows per workgroup (Q4_0, K <= 2048) when that still gives
-// >= 256 workgroups, else 8 x 4.  PBX_GEMV_INT=0 at model creation selects the float-unpack
-// kernel instead.
+// Integer-limb GEMV kernels (K = 2048..8192): the gate|up GEMV for Q4_0 and
+// Q8_0, 16 waves x 4 rows per workgroup (Q4_0, K <= 2048) when that still
+// gives >= 256 workgroups, else 8 x 4; the other Q4_0 decode GEMVs with 4
+// waves (qkv 4 rows, o / down 2, lm head 16 rows a wave).  PBX_GEMV_INT=0
+// at model creation selects the float-unpack kernels instead.
 static bool int_gemv_disabled() {
   const char *e = getenv("PBX_GEMV_INT");
   return e && e[0] == '0';
@@ -205,11 +206,28 @@ static bool int_shape(bool enabled, const char *mode, const char *role, int type
     return false;
   *ib = (B + 63) / 64;
   if (int_override(role, wv, rt)) return *ib <= *wv;
-  if (strcmp(mode, "gu") != 0 || B > 128) return false;
-  *rt = 4;
-  // 16 waves only for Q4_0 with one block per lane (register budget)
-  *wv = (type == PBX_TYPE_Q4_0 && *ib == 1 && N / 64 >= 256) ? 16 : 8;
-  return true;
+  if (strcmp(mode, "gu") == 0) {
+    if (B > 128) return false;
+    *rt = 4;
+    // 16 waves only for Q4_0 with one block per lane (register budget)
+    *wv = (type == PBX_TYPE_Q4_0 && *ib == 1 && N / 64 >= 256) ? 16 : 8;
+    return true;
+  }
+  if (type != PBX_TYPE_Q4_0) return false;
+  *wv = 4;
+  if (strcmp(mode, "qkv") == 0) {
+    *rt = 4;
+    return *ib <= 2;
+  }
+  if (strcmp(mode, "add") == 0) {
+    *rt = 2;
+    return *ib != 3;
+  }
+  if (strcmp(mode, "lmh") == 0) {
+    *rt = 16;
+    return *ib <= 2;
+  }
+  return false;
 }
 
 // Kernel shape for a GEMV of N rows x B blocks (the same rules as the plain

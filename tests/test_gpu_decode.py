@@ -178,13 +178,18 @@ def test_attention_kernels_match_one_workgroup_per_head(ctx, monkeypatch, mode, 
     ref.close()
 
 
-@pytest.mark.parametrize("wt", [TYPE_Q4_0, TYPE_Q8_0])
-def test_integer_limb_gate_up_matches_float_kernel(ctx, monkeypatch, wt):
-    """The gate|up GEMV on integer limbs (v_dot4 over a fixed-point activation)
-    against the float-unpack kernel and the oracle, K = 2048."""
-    print(f"[case] integer-limb gate|up vs float kernel, type {wt}", flush=True)
-    cfg = tiny(wt, wt, dim=2048, hidden_dim=1024, n_layers=1, n_heads=16, n_kv_heads=4,
-               vocab_size=512, max_seq=64)
+@pytest.mark.parametrize("wt,dim,hidden", [(TYPE_Q4_0, 2048, 1024), (TYPE_Q8_0, 2048, 1024),
+                                           (TYPE_Q4_0, 4096, 8192), (TYPE_Q8_0, 4096, 4096)])
+def test_integer_limb_kernels_match_float_kernels(ctx, monkeypatch, wt, dim, hidden):
+    """The GEMVs on integer limbs (v_dot4 over a fixed-point activation)
+    against the float-unpack kernels and the oracle: gate|up for Q4_0 and
+    Q8_0, and for Q4_0 also qkv, o, down and the lm head, with one, two and
+    four 64-block groups per lane (K = 2048, 4096, 8192)."""
+    print(f"[case] integer-limb vs float kernels, type {wt}, dim {dim}, hidden {hidden}",
+          flush=True)
+    heads = dim // 128
+    cfg = tiny(wt, wt, dim=dim, hidden_dim=hidden, n_layers=1, n_heads=heads,
+               n_kv_heads=heads // 4, vocab_size=512, max_seq=64)
     fast, ref, cfg = make_pair(ctx, cfg, 99)
     monkeypatch.setenv("PBX_GEMV_INT", "0")
     slow = synth.build(ctx, cfg, 99)
