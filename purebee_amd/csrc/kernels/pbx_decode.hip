@@ -73,6 +73,12 @@ DK_MODES_SMALL(PBX_Q6K, q6k, 4)
 #define DK_INT_QKV(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_RMSNORM, EPI_STORE, qkv)
 #define DK_INT_ADD(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_NONE, EPI_ADD, add)
 #define DK_INT_LMH(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_RMSNORM, EPI_ARGMAX, lmh)
+// lm head with a tile loop per workgroup: pbx_dk_<type>_i<WV>x<RT>b<IB>l_lmh
+#define DK_INT_LMHL(T, TN, WV, RT, IB)                                                    \
+  extern "C" __global__ void __launch_bounds__(WV * 64)                                   \
+      pbx_dk_##TN##_i##WV##x##RT##b##IB##l_lmh(GemvArgs a) {                              \
+    gemv_int<T, WV, RT, IB, PRO_RMSNORM, EPI_ARGMAX, true>(a);                            \
+  }
 // 16-wave workgroups (at most 128 VGPRs a lane) only where the prologue
 // wave's activation registers still fit: Q4_0 with one block per lane.
 DK_INT_GU(PBX_Q4, q4, 8, 4, 1)
@@ -81,7 +87,8 @@ DK_INT_GU(PBX_Q4, q4, 8, 4, 2)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 1)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 2)
 // Q4_0 decode roles (measured on Llama-3.2-1B shapes): qkv 4 x 4, o and
-// down 4 x 2, lm head 4 x 16; the others are tuning alternatives.
+// down 4 x 2, lm head 4 x 8 with the tile loop (4 x 16 at K = 4096); the
+// others are tuning alternatives.
 DK_INT_QKV(PBX_Q4, q4, 4, 4, 1)
 DK_INT_QKV(PBX_Q4, q4, 4, 4, 2)
 DK_INT_QKV(PBX_Q4, q4, 8, 2, 1)
@@ -93,6 +100,8 @@ DK_INT_ADD(PBX_Q4, q4, 4, 1, 4)
 DK_INT_LMH(PBX_Q4, q4, 4, 16, 1)
 DK_INT_LMH(PBX_Q4, q4, 4, 16, 2)
 DK_INT_LMH(PBX_Q4, q4, 4, 8, 1)
+DK_INT_LMHL(PBX_Q4, q4, 4, 8, 1)
+DK_INT_LMHL(PBX_Q4, q4, 4, 4, 1)
 
 DK_MODES_WIDE(PBX_F32, f32, 2)
 DK_MODES_WIDE(PBX_F32, f32, 4)

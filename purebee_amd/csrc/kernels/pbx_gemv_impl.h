@@ -748,10 +748,14 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
-template <int TYPE, int WV, int RT, int IB, int PRO, int EPI>
+// LOOP (lm head): a workgroup takes tiles blockIdx.x, blockIdx.x + G, ...
+// (G = gridDim.x) with the next tile's bytes in flight while a tile is
+// reduced, builds the activation limbs once, and writes one argmax key.
+template <int TYPE, int WV, int RT, int IB, int PRO, int EPI, bool LOOP = false>
 __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   static_assert(TYPE == PBX_Q4 || TYPE == PBX_Q8, "quantised weights only");
   static_assert(IB <= WV, "one prologue wave per 64 blocks");
+  static_assert(!LOOP || EPI == EPI_ARGMAX, "the tile loop serves the lm head");
   constexpr int QB = BlockTraits<TYPE>::QB;
   constexpr int NV = QB / 16;
   constexpr bool PAIR = EPI == EPI_SWIGLU;
@@ -765,11 +769,14 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   const int N = a.N, B = a.B, K = B * 32;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
   const int NO = PAIR ? N / 2 : N;
-  const int r0 = (blockIdx.x * WV + wave) * (PAIR ? RT / 2 : RT);
-  auto tile_row = [&](int i) -> int {
+  constexpr int RTO = PAIR ? RT / 2 : RT;  // output rows a wave
+  const int n_tiles = (NO + WV * RTO - 1) / (WV * RTO);
+  // first output row of the wave in tile t
+  auto rbase = [&](int t) -> int { return (t * WV + wave) * RTO; };
+  auto tile_row = [&](int r0, int i) -> int {
     return PAIR ? (i < RT / 2 ? r0 + i : N / 2 + r0 + i - RT / 2) : r0 + i;
   };
-  auto row_ok = [&](int i) -> bool {
+  auto row_ok = [&](int r0, int i) -> bool {
     return PAIR ? (r0 + (i < RT / 2 ? i : i - RT / 2)) < NO : (r0 + i) < N;
   };
   constexpr int LPR = 64 / RT;  // lanes per row after the transposed reduction
@@ -797,37 +804,46 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
 
   // 2. Every wave: the residual it will add (EPI_ADD), the block scales, then
   //    the weight bytes.  Loads are unconditional from clamped addresses
-  //    (rows past N read row 0, blocks past B read block 0) so the compiler
-  //    issues them back to back; a zero scale cancels what such lanes read.
+  //    (rows past N read row 0 and are never stored, blocks past B read
+  //    block 0 and get a zero scale where the dots use it) so the compiler
+  //    issues them back to back; nothing is computed from a loaded value
+  //    before the weight bytes are requested.
   float res = 0.f;
   if constexpr (EPI == EPI_ADD) {
+    const int r0 = rbase(blockIdx.x);
     const int rr = (lane % LPR) == 0 ? lane / LPR : RT;
     if (rr < RT && r0 + rr < N) res = y[r0 + rr];
   }
-  unsigned dbits[RT][IB];
+  auto load_tile = [&](int t, unsigned (&db)[RT][IB], uint4 (&qq)[RT][IB][NV]) {
+    const int r0 = rbase(t);
 #pragma unroll
-  for (int i = 0; i < RT; ++i) {
-    const bool rok = row_ok(i);
-    const int rw = rok ? tile_row(i) : 0;
+    for (int i = 0; i < RT; ++i) {
+      const int rw = row_ok(r0, i) ? tile_row(r0, i) : 0;
 #pragma unroll
-    for (int j = 0; j < IB; ++j) {
-      const int b = lane + 64 * j;
-      const bool ok = rok && b < B;
-      dbits[i][j] = a.dsc[dsc_index(rw, ok ? b : 0, B)] & (ok ? 0xFFFFu : 0u);
+      for (int j = 0; j < IB; ++j) {
+        const int b = lane + 64 * j;
+        db[i][j] = a.dsc[dsc_index(rw, b < B ? b : 0, B)];
+      }
     }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  uint4 q[RT][IB][NV];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int i = 0; i < RT; ++i) {
-    const int rw = row_ok(i) ? tile_row(i) : 0;
+    for (int i = 0; i < RT; ++i) {
+      const int rw = row_ok(r0, i) ? tile_row(r0, i) : 0;
 #pragma unroll
-    for (int j = 0; j < IB; ++j) {
-      const int b = lane + 64 * j;
-      const uint8_t *src = a.qs + ((size_t)rw * B + (b < B ? b : 0)) * QB;
+      for (int j = 0; j < IB; ++j) {
+        const int b = lane + 64 * j;
+        const uint8_t *src = a.qs + ((size_t)rw * B + (b < B ? b : 0)) * QB;
 #pragma unroll
-      for (int v = 0; v < NV; ++v) q[i][j][v] = ld_stream(src + v * 16);
+        for (int v = 0; v < NV; ++v) qq[i][j][v] = ld_stream(src + v * 16);
+      }
     }
+  };
+  unsigned dbA[RT][IB], dbB[RT][IB];
+  uint4 qA[RT][IB][NV], qB[RT][IB][NV];
+  const int G = gridDim.x;
+  load_tile(blockIdx.x, dbA, qA);
+  if constexpr (LOOP) {
+    if (blockIdx.x + G < n_tiles) load_tile(blockIdx.x + G, dbB, qB);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -900,54 +916,93 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   lds_barrier();
   const float unscale = xscale;
 
-  // 5. Dot products as the weight rows arrive.
-  float acc[RT];
+  // 5. Dot products as the weight rows arrive; the lane's row sum after the
+  //    transposed reduction.
+  auto dots = [&](const unsigned (&db)[RT][IB], const uint4 (&qq)[RT][IB][NV]) -> float {
+    float acc[RT];
 #pragma unroll
-  for (int i = 0; i < RT; ++i) acc[i] = 0.f;
+    for (int i = 0; i < RT; ++i) acc[i] = 0.f;
 #pragma unroll
-  for (int j = 0; j < IB; ++j) {
-    const int b = lane + 64 * j;
-    const int bl = b < B ? b : 0;  // lanes past B: zero scales cancel them
-    int xl[3][8];
+    for (int j = 0; j < IB; ++j) {
+      const int b = lane + 64 * j;
+      const int bl = b < B ? b : 0;  // lanes past B: zero scales cancel them
+      int xl[3][8];
 #pragma unroll
-    for (int L = 0; L < 3; ++L) {
-      const int4 t0 = *reinterpret_cast<const int4 *>(&limb[L][bl * 8]);
-      const int4 t1 = *reinterpret_cast<const int4 *>(&limb[L][bl * 8 + 4]);
-      xl[L][0] = t0.x; xl[L][1] = t0.y; xl[L][2] = t0.z; xl[L][3] = t0.w;
-      xl[L][4] = t1.x; xl[L][5] = t1.y; xl[L][6] = t1.z; xl[L][7] = t1.w;
-    }
-    const float corr = TYPE == PBX_Q4 ? 8.f * (float)bsum[bl] : 0.f;
-#pragma unroll
-    for (int i = 0; i < RT; ++i) {
-      int s0 = 0, s1 = 0, s2 = 0;
-      if constexpr (TYPE == PBX_Q4) {
-        // byte t holds element t (low nibble) and t+16 (high): word k covers
-        // elements 4k..4k+3 (limb word k) and 16+4k.. (limb word 4+k)
-        const unsigned w[4] = {q[i][j][0].x, q[i][j][0].y, q[i][j][0].z, q[i][j][0].w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int lo = (int)(w[k] & 0x0F0F0F0Fu), hi = (int)((w[k] >> 4) & 0x0F0F0F0Fu);
-          s0 = sdot4(lo, xl[0][k], s0); s0 = sdot4(hi, xl[0][4 + k], s0);
-          s1 = sdot4(lo, xl[1][k], s1); s1 = sdot4(hi, xl[1][4 + k], s1);
-          s2 = sdot4(lo, xl[2][k], s2); s2 = sdot4(hi, xl[2][4 + k], s2);
-        }
-      } else {
-        const unsigned w[8] = {q[i][j][0].x, q[i][j][0].y, q[i][j][0].z, q[i][j][0].w,
-                               q[i][j][1].x, q[i][j][1].y, q[i][j][1].z, q[i][j][1].w};
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          s0 = sdot4((int)w[k], xl[0][k], s0);
-          s1 = sdot4((int)w[k], xl[1][k], s1);
-          s2 = sdot4((int)w[k], xl[2][k], s2);
-        }
+      for (int L = 0; L < 3; ++L) {
+        const int4 t0 = *reinterpret_cast<const int4 *>(&limb[L][bl * 8]);
+        const int4 t1 = *reinterpret_cast<const int4 *>(&limb[L][bl * 8 + 4]);
+        xl[L][0] = t0.x; xl[L][1] = t0.y; xl[L][2] = t0.z; xl[L][3] = t0.w;
+        xl[L][4] = t1.x; xl[L][5] = t1.y; xl[L][6] = t1.z; xl[L][7] = t1.w;
       }
-      const float f = fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0)) - corr;
-      acc[i] = fmaf(f, f16_bits_to_f32(dbits[i][j]), acc[i]);
+      const float corr = TYPE == PBX_Q4 ? 8.f * (float)bsum[bl] : 0.f;
+      const unsigned bmask = b < B ? 0xFFFFu : 0u;
+#pragma unroll
+      for (int i = 0; i < RT; ++i) {
+        int s0 = 0, s1 = 0, s2 = 0;
+        if constexpr (TYPE == PBX_Q4) {
+          // byte t holds element t (low nibble) and t+16 (high): word k covers
+          // elements 4k..4k+3 (limb word k) and 16+4k.. (limb word 4+k)
+          const unsigned w[4] = {qq[i][j][0].x, qq[i][j][0].y, qq[i][j][0].z, qq[i][j][0].w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int lo = (int)(w[k] & 0x0F0F0F0Fu), hi = (int)((w[k] >> 4) & 0x0F0F0F0Fu);
+            s0 = sdot4(lo, xl[0][k], s0); s0 = sdot4(hi, xl[0][4 + k], s0);
+            s1 = sdot4(lo, xl[1][k], s1); s1 = sdot4(hi, xl[1][4 + k], s1);
+            s2 = sdot4(lo, xl[2][k], s2); s2 = sdot4(hi, xl[2][4 + k], s2);
+          }
+        } else {
+          const unsigned w[8] = {qq[i][j][0].x, qq[i][j][0].y, qq[i][j][0].z, qq[i][j][0].w,
+                                 qq[i][j][1].x, qq[i][j][1].y, qq[i][j][1].z, qq[i][j][1].w};
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            s0 = sdot4((int)w[k], xl[0][k], s0);
+            s1 = sdot4((int)w[k], xl[1][k], s1);
+            s2 = sdot4((int)w[k], xl[2][k], s2);
+          }
+        }
+        const float f = fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0)) - corr;
+        acc[i] = fmaf(f, f16_bits_to_f32(db[i][j] & bmask), acc[i]);
+      }
     }
+    return wave_transpose_reduce<RT>(acc, lane) * unscale;
+  };
+  const int row = lane / LPR;
+
+  if constexpr (LOOP) {
+    // tiles t (registers A) and t + G (B); each buffer is refilled with the
+    // tile two strides on as soon as it has been reduced
+    uint64_t best = 0;
+    auto consume = [&](int t, float tot) {
+      const int n = rbase(t) + row;
+      if ((lane % LPR) == 0 && n < N) {
+        epilogue_row<EPI>(a, y, n, tot, 0.f);
+        const uint64_t key = argmax_key(tot, (unsigned)n);
+        best = key > best ? key : best;
+      }
+    };
+    for (int t = blockIdx.x; t < n_tiles; t += 2 * G) {
+      const float ta = dots(dbA, qA);
+      if (t + 2 * G < n_tiles) load_tile(t + 2 * G, dbA, qA);
+      consume(t, ta);
+      if (t + G >= n_tiles) break;
+      const float tb = dots(dbB, qB);
+      if (t + 3 * G < n_tiles) load_tile(t + 3 * G, dbB, qB);
+      consume(t + G, tb);
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) kred[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t k = kred[0];
+#pragma unroll
+      for (int w = 1; w < WV; ++w) k = kred[w] > k ? kred[w] : k;
+      a.partials[blockIdx.x] = k;
+    }
+    return;
   }
 
-  const float tot = wave_transpose_reduce<RT>(acc, lane) * unscale;
-  const int row = lane / LPR;
+  const float tot = dots(dbA, qA);
+  const int r0 = rbase(blockIdx.x);
   if constexpr (PAIR) {
     const float up = __shfl_xor(tot, 32, 64);
     if (lane < 32 && (lane % LPR) == 0) {

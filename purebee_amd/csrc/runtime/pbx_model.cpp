@@ -172,18 +172,20 @@ static bool model_ok(const pbx_model *m) { return m && m->magic == PBX_MODEL_MAG
 // Integer-limb GEMV kernels (K = 2048..8192): the gate|up GEMV for Q4_0 and
 // Q8_0, 16 waves x 4 rows per workgroup (Q4_0, K <= 2048) when that still
 // gives >= 256 workgroups, else 8 x 4; the other Q4_0 decode GEMVs with 4
-// waves (qkv 4 rows, o / down 2, lm head 16 rows a wave).  PBX_GEMV_INT=0
-// at model creation selects the float-unpack kernels instead.
+// waves (qkv 4 rows, o / down 2, lm head 8 rows a wave in a tile loop at
+// K = 2048, else 16).  PBX_GEMV_INT=0 at model creation selects the
+// float-unpack kernels instead.
 static bool int_gemv_disabled() {
   const char *e = getenv("PBX_GEMV_INT");
   return e && e[0] == '0';
 }
 
-// PBX_GEMV_INT_SHAPES="role=WVxRT,..." (roles qkv, o, gate_up, down,
+// PBX_GEMV_INT_SHAPES="role=WVxRT[l],..." (roles qkv, o, gate_up, down,
 // lm_head), read when the step is planned: the integer-limb kernel with WV
-// waves x RT rows for the listed roles (Q4_0 / Q8_0, K = 2048..8192), for
-// tuning.  A shape that was not compiled fails the plan.
-static bool int_override(const char *role, int *wv, int *rt) {
+// waves x RT rows for the listed roles (Q4_0 / Q8_0, K = 2048..8192; a
+// trailing l selects the lm head's tile loop), for tuning.  A shape that
+// was not compiled fails the plan.
+static bool int_override(const char *role, int *wv, int *rt, bool *loop) {
   const char *e = getenv("PBX_GEMV_INT_SHAPES");
   if (!e || !role) return false;
   const std::string s(e), key = std::string(role) + "=";
@@ -193,19 +195,22 @@ static bool int_override(const char *role, int *wv, int *rt) {
     if (q == std::string::npos) q = s.size();
     const std::string item = s.substr(p, q - p);
     if (item.compare(0, key.size(), key) == 0 &&
-        sscanf(item.c_str() + key.size(), "%dx%d", wv, rt) == 2)
+        sscanf(item.c_str() + key.size(), "%dx%d", wv, rt) == 2) {
+      *loop = item.back() == 'l';
       return true;
+    }
     p = q + 1;
   }
   return false;
 }
 
 static bool int_shape(bool enabled, const char *mode, const char *role, int type, int N, int B,
-                      int *wv, int *rt, int *ib) {
+                      int *wv, int *rt, int *ib, bool *loop) {
   if (!enabled || (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0) || B < 64 || B > 256)
     return false;
   *ib = (B + 63) / 64;
-  if (int_override(role, wv, rt)) return *ib <= *wv;
+  *loop = false;
+  if (int_override(role, wv, rt, loop)) return *ib <= *wv;
   if (strcmp(mode, "gu") == 0) {
     if (B > 128) return false;
     *rt = 4;
@@ -223,8 +228,9 @@ static bool int_shape(bool enabled, const char *mode, const char *role, int type
     *rt = 2;
     return *ib != 3;
   }
-  if (strcmp(mode, "lmh") == 0) {
-    *rt = 16;
+  if (strcmp(mode, "lmh") == 0) {  // K = 2048: 8-row waves with the tile loop
+    *rt = *ib == 1 ? 8 : 16;
+    *loop = *ib == 1;
     return *ib <= 2;
   }
   return false;
@@ -237,9 +243,14 @@ static bool int_shape(bool enabled, const char *mode, const char *role, int type
 static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, const char *role, int type,
                       int N, int B, std::string *shape, dim3 *grid, dim3 *block, int *n_tiles) {
   int wv, rt, ib;
-  if (int_shape(int_ok, mode, role, type, N, B, &wv, &rt, &ib)) {
-    *shape = "i" + std::to_string(wv) + "x" + std::to_string(rt) + "b" + std::to_string(ib);
-    *grid = dim3((N + wv * rt - 1) / (wv * rt));
+  bool loop;
+  if (int_shape(int_ok, mode, role, type, N, B, &wv, &rt, &ib, &loop)) {
+    *shape = "i" + std::to_string(wv) + "x" + std::to_string(rt) + "b" + std::to_string(ib) +
+             (loop ? "l" : "");
+    const int tiles = (N + wv * rt - 1) / (wv * rt);
+    // tile loop: two workgroups per CU (four for 4-row waves), each taking
+    // every G-th tile
+    *grid = dim3(loop ? std::min(tiles, (rt <= 4 ? 4 : 2) * c->cu_count) : tiles);
     *block = dim3(64 * wv);
     *n_tiles = (int)grid->x;
     return;
