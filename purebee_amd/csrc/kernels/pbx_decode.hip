@@ -307,18 +307,19 @@ extern "C" __global__ void __launch_bounds__(256) pbx_attention_decode(AttnArgs 
 // ---------------------------------------------------------------------------
 // Flash decoding in one workgroup per query head (head_dim <= 64): the
 // attention of llama.js:258-301 / llama-streaming.js:543-573 at batch 1.
-// Lane t of the workgroup takes position c0 + t of a 512-position chunk:
-// each wave keeps its own running max, sum and weighted V sum over its 64
-// positions (online softmax), and the eight waves merge once through LDS at
-// the end, so no second kernel and no barrier inside the position loop.
-// Loads (all unconditional, from clamped addresses; q and the new k, v
-// first): lane t reads the K row of its position as 16-byte pieces, and
-// the wave's V rows as 16-byte pieces too, lane l taking dims
-// 4(l%16)..4(l%16)+3 of positions 4k + l/16 (k < 16), so its weighted V sum
-// covers 4 dims over 16 positions and two shuffles finish the sum over the
-// wave's 64.  The row at pos is replaced by the rotated new k / new v (the
-// cache row may hold an older value); the group's first head writes them to
-// the cache.
+// A chunk is 512 positions; wave w takes positions 64w..64w+63 of it.  Each
+// wave keeps its own running max, sum and weighted V sum over its
+// positions (online softmax), and the eight waves merge once through LDS
+// at the end, so no second kernel and no barrier inside the position loop.
+// Lane l holds dims 4(l%16)..4(l%16)+3 of everything: of q, the new k and
+// v (which it rotates itself, llama.js:163-190, from the RoPE pairs of
+// those dims), and of the wave's positions 4j + l/16 (j < 16) of K and V,
+// so every 16-byte load reads four whole 256-byte cache rows.  The partial
+// dots over 4 dims are finished by a 16-lane reduce-scatter, after which
+// lane l holds the score of position 4(l%16) + l/16.  The row at pos is
+// replaced by the new k / v from registers (the cache row may still hold
+// an older value); the group's first head writes them to the cache.
+// All loads are unconditional, from clamped addresses: q, k, v first.
 // ---------------------------------------------------------------------------
 #define PBX_HA_MAX_HD 64
 #define PBX_HA_WAVES 8
@@ -332,33 +333,29 @@ struct HeadChunk {
 };
 
 extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_head(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) float qsh[PBX_HA_MAX_HD];
-  __shared__ __attribute__((aligned(16))) float knew[PBX_HA_MAX_HD];
-  __shared__ __attribute__((aligned(16))) float vnew[PBX_HA_MAX_HD];
   __shared__ float wm[PBX_HA_WAVES], wl[PBX_HA_WAVES];
   __shared__ __attribute__((aligned(16))) float wacc[PBX_HA_WAVES][PBX_HA_MAX_HD];
-  __shared__ float dnew;  // q . (new k)
   constexpr int CH = PBX_HA_WAVES * 64;  // positions per chunk
-  const int h = blockIdx.x, hd = a.head_dim, half = hd / 2, hd4 = hd / 4;
+  const int h = blockIdx.x, hd = a.head_dim, hd4 = hd / 4;
   const int Gq = a.n_heads / a.n_kv_heads, g = h / Gq;
   const int dim = a.n_heads * hd, kvdim = a.n_kv_heads * hd;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int pos = a.state[0], L = pos + 1;
   float *kb = a.kcache + (size_t)g * hd, *vb = a.vcache + (size_t)g * hd;
-  const int dg = lane & 15, ps = lane >> 4;      // V: dim group, position slot
-  const int dcol = 4 * min(dg, hd4 - 1);         // clamped for head_dim < 64
+  const int dg = lane & 15, ps = lane >> 4;  // dim group, position slot
+  const int dcol = 4 * min(dg, hd4 - 1);     // clamped for head_dim < 64
 
-  // 1. this token's q, k, v pair (thread t < hd/2 owns pair t)
-  const int k2 = tid < half ? tid : 0;
-  const float2 cs = *reinterpret_cast<const float2 *>(a.rope + (size_t)pos * hd + 2 * k2);
-  const float2 qv = *reinterpret_cast<const float2 *>(a.qkv + (size_t)h * hd + 2 * k2);
-  const float2 kv = *reinterpret_cast<const float2 *>(a.qkv + dim + (size_t)g * hd + 2 * k2);
-  const float2 vv = *reinterpret_cast<const float2 *>(a.qkv + dim + kvdim + (size_t)g * hd + 2 * k2);
+  // 1. the lane's dims of q, the new k and v, and their RoPE pairs
+  const float4 cs = *reinterpret_cast<const float4 *>(a.rope + (size_t)pos * hd + dcol);
+  const float4 qv = *reinterpret_cast<const float4 *>(a.qkv + (size_t)h * hd + dcol);
+  const float4 kv = *reinterpret_cast<const float4 *>(a.qkv + dim + (size_t)g * hd + dcol);
+  const float4 vnw =
+      *reinterpret_cast<const float4 *>(a.qkv + dim + kvdim + (size_t)g * hd + dcol);
   __builtin_amdgcn_sched_barrier(0);
 
-  // 2. K rows and V pieces of the first chunk
-  auto load_chunk = [&](int c0, HeadChunk &ch) {  // all of K before V: the
-    // scores need all of K while V is still arriving
+  // 2. K and V of the first chunk (all of K before V: the scores need all
+  //    of K while V is still arriving)
+  auto load_chunk = [&](int c0, HeadChunk &ch) {
 #pragma unroll
     for (int j = 0; j < 16; ++j)
       ch.k[j] = *reinterpret_cast<const float4 *>(
@@ -372,37 +369,25 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
   load_chunk(0, first);
   __builtin_amdgcn_sched_barrier(0);
 
-  // 3. RoPE (adjacent pairs, llama.js:163-190) of q and the new k
-  if (w == 0) {  // hd/2 <= 32: the pairs live in wave 0
-    const float q0 = qv.x * cs.x - qv.y * cs.y, q1 = qv.x * cs.y + qv.y * cs.x;
-    const float k0 = kv.x * cs.x - kv.y * cs.y, k1 = kv.x * cs.y + kv.y * cs.x;
-    if (tid < half) {
-      qsh[2 * tid] = q0;
-      qsh[2 * tid + 1] = q1;
-      knew[2 * tid] = k0;
-      knew[2 * tid + 1] = k1;
-      vnew[2 * tid] = vv.x;
-      vnew[2 * tid + 1] = vv.y;
-    }
-    const float dq = wave_sum(tid < half ? fmaf(q0, k0, q1 * k1) : 0.f);
-    if (tid == 0) dnew = dq;
+  // 3. RoPE (adjacent pairs, llama.js:163-190) of the lane's q and new-k
+  //    dims; q . (new k) summed over the 16 lanes of a row; the KV-cache
+  //    append (the group's first head, lanes 0..hd/4-1)
+  float4 qq = make_float4(qv.x * cs.x - qv.y * cs.y, qv.x * cs.y + qv.y * cs.x,
+                          qv.z * cs.z - qv.w * cs.w, qv.z * cs.w + qv.w * cs.z);
+  const float4 knw = make_float4(kv.x * cs.x - kv.y * cs.y, kv.x * cs.y + kv.y * cs.x,
+                                 kv.z * cs.z - kv.w * cs.w, kv.z * cs.w + kv.w * cs.z);
+  if (dg >= hd4) qq = make_float4(0.f, 0.f, 0.f, 0.f);  // repeats of the last dims
+  const float dnew = wave_sum<8>(fmaf(qq.x, knw.x, fmaf(qq.y, knw.y, fmaf(qq.z, knw.z, qq.w * knw.w))));
+  if (h % Gq == 0 && tid < hd4) {
+    *reinterpret_cast<float4 *>(kb + (size_t)pos * kvdim + dcol) = knw;
+    *reinterpret_cast<float4 *>(vb + (size_t)pos * kvdim + dcol) = vnw;
   }
-  lds_barrier();
-  if (h % Gq == 0 && tid < hd) {  // KV-cache append, once per group
-    kb[(size_t)pos * kvdim + tid] = knew[tid];
-    vb[(size_t)pos * kvdim + tid] = vnew[tid];
-  }
-  const float4 vnw = *reinterpret_cast<const float4 *>(&vnew[dcol]);
 
   // 4. scores and the wave's softmax-weighted V sum, chunk by chunk (the
   //    first chunk from the registers loaded above; later ones, for
   //    contexts past 512 positions, load their own)
   float m = -INFINITY, l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  // the lane's q piece; dims past head_dim (repeats of the last column)
-  // are masked out
-  float4 qq = *reinterpret_cast<const float4 *>(&qsh[dcol]);
-  if (dg >= hd4) qq = make_float4(0.f, 0.f, 0.f, 0.f);
   auto chunk = [&](int c0, const HeadChunk &ch) {
     // partial dots of the 16 positions, then a reduce-scatter over the 16
     // lanes of a position slot: after halving across lane bits 3, 2, 1, 0
@@ -704,7 +689,9 @@ extern "C" __global__ void __launch_bounds__(256) pbx_embed(EmbedArgs a) {
 
 // ---------------------------------------------------------------------------
 // Final argmax over the LM head's per-tile partial keys; records the token,
-// appends it to the history and advances the position.
+// appends it to the history and advances the position, then writes the
+// token's embedding row into x for the next step (the step's first op), so
+// a step ends where the next one begins.
 // ---------------------------------------------------------------------------
 struct ArgmaxArgs {
   const uint64_t *partials;
@@ -712,10 +699,12 @@ struct ArgmaxArgs {
   int *hist;
   int n_partials;
   int hist_cap;
+  EmbedArgs emb;  // the embedding table and x
 };
 
 extern "C" __global__ void __launch_bounds__(1024) pbx_argmax_final(ArgmaxArgs a) {
   __shared__ uint64_t red[16];
+  __shared__ int tok_sh;
   uint64_t best = 0;
   for (int i = threadIdx.x; i < a.n_partials; i += blockDim.x) {
     const uint64_t k = a.partials[i];
@@ -734,7 +723,12 @@ extern "C" __global__ void __launch_bounds__(1024) pbx_argmax_final(ArgmaxArgs a
     if (a.hist && step >= 0 && step < a.hist_cap) a.hist[step] = tok;
     a.state[2] = step + 1;
     a.state[0] = a.state[0] + 1;
+    tok_sh = tok < 0 || tok >= a.emb.vocab ? 0 : tok;
   }
+  __syncthreads();
+  const int tok = tok_sh;
+  for (int i = threadIdx.x; i < a.emb.dim; i += blockDim.x)
+    a.emb.x[i] = row_value(a.emb.qs, a.emb.dsc, a.emb.msc, a.emb.type, tok, i, a.emb.dim);
 }
 
 // Zero cache positions [from, max_seq) of every layer (resetCache /

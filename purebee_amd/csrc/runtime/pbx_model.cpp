@@ -80,6 +80,7 @@ struct ArgmaxArgsHost {  // ArgmaxArgs in pbx_decode.hip
   int *hist;
   int n_partials;
   int hist_cap;
+  EmbedArgsHost emb;
 };
 
 enum ArgKind { ARG_GEMV, ARG_ATTN, ARG_ATTN_SPLIT, ARG_COMBINE, ARG_EMBED, ARG_ARGMAX };
@@ -153,6 +154,7 @@ struct pbx_model {
   int *hist = nullptr;
   int hist_cap = 0;
   std::vector<Op> ops;
+  Op embed_op;  // the embedding of a token set by the host (steps embed their own)
   bool ops_ready = false;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -325,7 +327,7 @@ static int build_ops(pbx_model *m) {
   e.bytes = (double)pbx_type_row_bytes(m->embd->type, g.dim) + 4.0 * g.dim;
   e.embed = EmbedArgsHost{m->embd->qs, m->embd->d, m->x, m->state, kernel_type(m->embd->type),
                           g.dim, g.vocab_size, m->embd->m};
-  m->ops.push_back(e);
+  m->embed_op = e;
   hipFunction_t fattn = pbx_kernel_by_name(c, "pbx_attention_decode");
   hipFunction_t fhead = pbx_kernel_by_name(c, "pbx_attention_head");
   if (!fattn || !fhead) return pbx_fail(c, PBX_ELOAD, "model: attention kernels not found");
@@ -401,9 +403,10 @@ static int build_ops(pbx_model *m) {
   if (!am.f) return pbx_fail(c, PBX_ELOAD, "model: kernel pbx_argmax_final not found");
   am.grid = dim3(1);
   am.block = dim3(1024);
-  am.role = "argmax";
+  am.role = "argmax";  // + the next step's embedding
   am.bytes = 8.0 * n_tiles;
-  am.amax = ArgmaxArgsHost{m->partials, m->state, m->hist, n_tiles, m->hist_cap};
+  am.amax = ArgmaxArgsHost{m->partials, m->state, m->hist, n_tiles, m->hist_cap, e.embed};
+  am.bytes += (double)pbx_type_row_bytes(m->embd->type, g.dim) + 4.0 * g.dim;
   m->ops.push_back(am);
   m->ops_ready = true;
   return PBX_OK;
@@ -478,12 +481,17 @@ static int run_step(pbx_model *m) {
   return enqueue_ops(m);
 }
 
-static int set_state(pbx_model *m, int pos, int token, int step) {
+// Device state for a host-driven step; with `embed`, also the token's
+// embedding row into x (a step's argmax embeds the token it picks).
+static int set_state(pbx_model *m, int pos, int token, int step, bool embed) {
   hipFunction_t f = pbx_kernel_by_name(m->c, "pbx_set_state");
   if (!f) return pbx_fail(m->c, PBX_ELOAD, "model: kernel pbx_set_state not found");
   int *st = m->state;
   void *args[] = {&st, &pos, &token, &step};
-  return pbx_launch_fn(m->c, f, "pbx_set_state", dim3(1), dim3(64), args, m->c->stream);
+  int rc = pbx_launch_fn(m->c, f, "pbx_set_state", dim3(1), dim3(64), args, m->c->stream);
+  if (rc || !embed) return rc;
+  if (!m->ops_ready && (rc = build_ops(m))) return rc;
+  return enqueue_op(m, m->embed_op);
 }
 
 static int kv_fill(pbx_model *m, int from) {
@@ -909,7 +917,7 @@ static int prefill_batched(pbx_model *m, const int32_t *tokens, int n, int start
   if (rc) return rc;
   if (!m->ops_ready && (rc = build_ops(m))) return rc;
   if ((rc = batch_layers(m, tokens, n, start))) return rc;
-  if ((rc = set_state(m, start + n - 1, tokens[n - 1], 0))) return rc;
+  if ((rc = set_state(m, start + n - 1, tokens[n - 1], 0, false))) return rc;
   if (hipMemcpyAsync(m->x, m->bx + (size_t)(n - 1) * m->cfg.dim, (size_t)m->cfg.dim * 4,
                      hipMemcpyDeviceToDevice, m->c->stream) != hipSuccess)
     return pbx_fail(m->c, PBX_EHIP, "model: residual copy failed");
@@ -945,7 +953,7 @@ extern "C" int pbx_model_forward(pbx_model *m, const int32_t *tokens, int n_toke
     if ((rc = prefill_batched(m, tokens, n_tokens, start_pos))) return rc;
   } else {
     for (int t = 0; t < n_tokens; ++t) {
-      if ((rc = set_state(m, start_pos + t, tokens[t], 0))) return rc;
+      if ((rc = set_state(m, start_pos + t, tokens[t], 0, true))) return rc;
       if ((rc = run_step(m))) return rc;
     }
   }
@@ -1028,7 +1036,7 @@ extern "C" int pbx_model_generate(pbx_model *m, int32_t token, int start_pos, in
   if (rc) return rc;
   if (hipSetDevice(c->device) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_generate: hipSetDevice failed");
-  if ((rc = set_state(m, start_pos, token, 0))) return rc;
+  if ((rc = set_state(m, start_pos, token, 0, true))) return rc;
   for (int i = 0; i < n_steps; ++i)
     if ((rc = run_step(m))) return rc;
   if (hipMemcpyAsync(out_tokens, m->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost,
@@ -1110,7 +1118,7 @@ extern "C" int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int
       return pbx_fail(c, PBX_EHIP, "pbx_model_profile: hipEventCreate failed");
     }
   std::vector<double> acc(n, 0.0), bytes(n, 0.0);
-  if ((rc = set_state(m, start_pos, token, 0))) goto out;
+  if ((rc = set_state(m, start_pos, token, 0, true))) goto out;
   for (int s = 0; s < n_steps && !rc; ++s) {
     if (hipEventRecord(ev[0], c->stream) != hipSuccess) { rc = pbx_fail(c, PBX_EHIP, "event"); break; }
     for (int i = 0; i < n && !rc; ++i) {
