@@ -345,16 +345,12 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
   const int dg = lane & 15, ps = lane >> 4;  // dim group, position slot
   const int dcol = 4 * min(dg, hd4 - 1);     // clamped for head_dim < 64
 
-  // 1. the lane's dims of q, the new k and v, and their RoPE pairs
-  const float4 cs = *reinterpret_cast<const float4 *>(a.rope + (size_t)pos * hd + dcol);
-  const float4 qv = *reinterpret_cast<const float4 *>(a.qkv + (size_t)h * hd + dcol);
-  const float4 kv = *reinterpret_cast<const float4 *>(a.qkv + dim + (size_t)g * hd + dcol);
-  const float4 vnw =
-      *reinterpret_cast<const float4 *>(a.qkv + dim + kvdim + (size_t)g * hd + dcol);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 2. K and V of the first chunk (all of K before V: the scores need all
-  //    of K while V is still arriving)
+  // 1. K and V of the first chunk (all of K before V: the scores need all
+  //    of K while V is still arriving).  A wave whose positions all lie
+  //    past pos loads and scores nothing (a wave-uniform branch); its
+  //    clamped loads would cost the CU's load return path as much as real
+  //    ones.  These go before the q loads: behind a branch, a later use of
+  //    an earlier load waits for everything the branch may have issued.
   auto load_chunk = [&](int c0, HeadChunk &ch) {
 #pragma unroll
     for (int j = 0; j < 16; ++j)
@@ -365,23 +361,26 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
       ch.v[j] = *reinterpret_cast<const float4 *>(
           vb + (size_t)min(c0 + w * 64 + 4 * j + ps, pos) * kvdim + dcol);
   };
+  const bool wact = w * 64 < L;
   HeadChunk first;
-  load_chunk(0, first);
+  if (wact) load_chunk(0, first);
+
+  // 2. the lane's dims of q, the new k and v, and their RoPE pairs
+  const float4 cs = *reinterpret_cast<const float4 *>(a.rope + (size_t)pos * hd + dcol);
+  const float4 qv = *reinterpret_cast<const float4 *>(a.qkv + (size_t)h * hd + dcol);
+  const float4 kv = *reinterpret_cast<const float4 *>(a.qkv + dim + (size_t)g * hd + dcol);
+  const float4 vnw =
+      *reinterpret_cast<const float4 *>(a.qkv + dim + kvdim + (size_t)g * hd + dcol);
   __builtin_amdgcn_sched_barrier(0);
 
   // 3. RoPE (adjacent pairs, llama.js:163-190) of the lane's q and new-k
-  //    dims; q . (new k) summed over the 16 lanes of a row; the KV-cache
-  //    append (the group's first head, lanes 0..hd/4-1)
+  //    dims; q . (new k) summed over the 16 lanes of a row
   float4 qq = make_float4(qv.x * cs.x - qv.y * cs.y, qv.x * cs.y + qv.y * cs.x,
                           qv.z * cs.z - qv.w * cs.w, qv.z * cs.w + qv.w * cs.z);
   const float4 knw = make_float4(kv.x * cs.x - kv.y * cs.y, kv.x * cs.y + kv.y * cs.x,
                                  kv.z * cs.z - kv.w * cs.w, kv.z * cs.w + kv.w * cs.z);
   if (dg >= hd4) qq = make_float4(0.f, 0.f, 0.f, 0.f);  // repeats of the last dims
   const float dnew = wave_sum<8>(fmaf(qq.x, knw.x, fmaf(qq.y, knw.y, fmaf(qq.z, knw.z, qq.w * knw.w))));
-  if (h % Gq == 0 && tid < hd4) {
-    *reinterpret_cast<float4 *>(kb + (size_t)pos * kvdim + dcol) = knw;
-    *reinterpret_cast<float4 *>(vb + (size_t)pos * kvdim + dcol) = vnw;
-  }
 
   // 4. scores and the wave's softmax-weighted V sum, chunk by chunk (the
   //    first chunk from the registers loaded above; later ones, for
@@ -419,8 +418,9 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
     }
     m = mn;
   };
-  chunk(0, first);
+  if (wact) chunk(0, first);
   for (int c0 = CH; c0 < L; c0 += CH) {
+    if (c0 + w * 64 >= L) break;  // wave-uniform
     HeadChunk next;
     load_chunk(c0, next);
     chunk(c0, next);
@@ -453,6 +453,12 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
       den = fmaf(e, wl[i], den);
     }
     a.out[(size_t)h * hd + tid] = num / den;
+  }
+  // 6. the KV-cache append (the group's first head, lanes 0..hd/4-1), last:
+  //    every head of the group takes row pos from registers
+  if (h % Gq == 0 && tid < hd4) {
+    *reinterpret_cast<float4 *>(kb + (size_t)pos * kvdim + dcol) = knw;
+    *reinterpret_cast<float4 *>(vb + (size_t)pos * kvdim + dcol) = vnw;
   }
 }
 
