@@ -840,11 +840,14 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   };
   unsigned dbA[RT][IB], dbB[RT][IB];
   uint4 qA[RT][IB][NV], qB[RT][IB][NV];
+  // LOOP: the workgroup's tiles are blockIdx.x + k*G, k < TW.  Loads are
+  // issued without branches (the second from a clamped index when TW = 1):
+  // behind a branch, the wait for an earlier load would also wait for
+  // everything the branch may have issued.
   const int G = gridDim.x;
+  const int TW = LOOP ? (n_tiles - (int)blockIdx.x + G - 1) / G : 1;
   load_tile(blockIdx.x, dbA, qA);
-  if constexpr (LOOP) {
-    if (blockIdx.x + G < n_tiles) load_tile(blockIdx.x + G, dbB, qB);
-  }
+  if constexpr (LOOP) load_tile(blockIdx.x + (TW > 1 ? G : 0), dbB, qB);
   __builtin_amdgcn_sched_barrier(0);
 
   // 3. Prologue waves: sum of squares (RMSNorm) and max |x * w| of their
@@ -969,26 +972,34 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   const int row = lane / LPR;
 
   if constexpr (LOOP) {
-    // tiles t (registers A) and t + G (B); each buffer is refilled with the
-    // tile two strides on as soon as it has been reduced
+    // tiles k (registers A) and k + 1 (B); each buffer is refilled with the
+    // tile two on as soon as it has been reduced.  The steady-state loop
+    // issues its loads unconditionally; the last two or three tiles follow.
     uint64_t best = 0;
-    auto consume = [&](int t, float tot) {
-      const int n = rbase(t) + row;
+    auto consume = [&](int k, float tot) {
+      const int n = rbase(blockIdx.x + k * G) + row;
       if ((lane % LPR) == 0 && n < N) {
-        epilogue_row<EPI>(a, y, n, tot, 0.f);
+        y[n] = tot;  // no bias on the lm head (a load here would wait for the stream)
         const uint64_t key = argmax_key(tot, (unsigned)n);
         best = key > best ? key : best;
       }
     };
-    for (int t = blockIdx.x; t < n_tiles; t += 2 * G) {
+    int k = 0;
+    for (; k + 3 < TW; k += 2) {
       const float ta = dots(dbA, qA);
-      if (t + 2 * G < n_tiles) load_tile(t + 2 * G, dbA, qA);
-      consume(t, ta);
-      if (t + G >= n_tiles) break;
+      load_tile(blockIdx.x + (k + 2) * G, dbA, qA);
+      consume(k, ta);
       const float tb = dots(dbB, qB);
-      if (t + 3 * G < n_tiles) load_tile(t + 3 * G, dbB, qB);
-      consume(t + G, tb);
+      load_tile(blockIdx.x + (k + 3) * G, dbB, qB);
+      consume(k + 1, tb);
     }
+    {
+      const float ta = dots(dbA, qA);
+      if (k + 2 < TW) load_tile(blockIdx.x + (k + 2) * G, dbA, qA);
+      consume(k, ta);
+    }
+    if (k + 1 < TW) consume(k + 1, dots(dbB, qB));
+    if (k + 2 < TW) consume(k + 2, dots(dbA, qA));
     best = wave_max_u64(best);
     if (lane == 0) kred[wave] = best;
     __syncthreads();
