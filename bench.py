@@ -229,6 +229,7 @@ def run_decode(args, pb, synth):
                 "bytes_per_launch": round(by), "us_per_launch": round(us, 3),
                 "us_per_launch_in_step": round(dom["us_per_launch"], 3)}
     step_bytes = sum(r["bytes_per_step"] for r in roles.values())
+    matvec_shapes = run_matvec_shapes(ctx, pb)
     m_gt_1 = None if args.no_m_gt_1 else run_m_gt_1(ctx, model, cfg, pb, synth)
     next_rows = None
     if not args.no_m_gt_1:
@@ -265,6 +266,7 @@ def run_decode(args, pb, synth):
         "roofline": roofline,
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in roles.items()},
+        "matvec_shapes": matvec_shapes,
         "m_gt_1": m_gt_1,
         "next_rows": next_rows,
         "cpu_baseline": cpu,
@@ -383,6 +385,47 @@ def run_q4_1(ctx, pb):
             log(f"{qname} matvec {name} {N}x{K}: {us:.2f} us, {b / us / 1e3:.0f} GB/s")
             for w in ws:
                 w.free()
+        dx.free(), dy.free()
+    return res
+
+
+def run_matvec_shapes(ctx, pb):
+    """The plain instruction (q4_0_matvec / quantizedMatvec, M = 1) on each
+    Llama-3.2-1B matvec shape with Q4_0 weights: N(0, 0.02) quantised, x from
+    N(0, 1).  Each shape's launches rotate through distinct device copies of
+    the weight totalling >= 600 MB (beyond the 256 MB last-level cache).
+    `us_per_launch`: the rotation captured as one HIP graph and replayed
+    (>= 100 launches streaming, no host launch gaps); `launched_us`: the same
+    launches issued one by one from the host; `single_us`: one launch between
+    two events, the latency a lone call sees.  Algorithmic bytes:
+    N*K/32*18 + 4K + 4N."""
+    res = {}
+    rng = np.random.default_rng(7)
+    for name, N, K in (("q_o", 2048, 2048), ("k_v", 512, 2048), ("gate_up", 8192, 2048),
+                       ("down", 2048, 8192), ("lm_head", 128256, 2048)):
+        raw = pb.quantize_q4_0(pb.synth_normal(5000 + N + K, N * K, 0, 0.02).reshape(N, K))
+        b = q4_bytes(N, K) + 4 * (N + K)
+        copies = min(256, -(-600_000_000 // b))
+        ws = [ctx.upload(pb.TYPE_Q4_0, N, K, raw) for _ in range(copies)]
+        dx = ctx.alloc(K * 4).upload(rng.normal(0, 1, K).astype(np.float32))
+        dy = ctx.alloc(N * 4)
+        reps = max(2, -(-100 // copies))
+        xs, ys = [dx.ptr] * copies, [dy.ptr] * copies
+        ctx.bench_linear(ws, xs, ys, 1, 1)
+        us = ctx.bench_linear(ws, xs, ys, 1, reps, graph=True) / reps / copies * 1e3
+        launched = ctx.bench_linear(ws, xs, ys, 1, reps) / reps / copies * 1e3
+        single = min(ctx.bench_linear([ws[i]], [dx.ptr], [dy.ptr], 1, 1) * 1e3
+                     for i in range(min(8, copies)))
+        res[name] = {"N": N, "K": K, "us_per_launch": round(us, 2),
+                     "launched_us": round(launched, 2), "single_us": round(single, 2),
+                     "achieved_GBps": round(b / us / 1e3, 1),
+                     "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "algorithmic_bytes": b,
+                     "rotated_copies": copies}
+        log(f"q4_0 matvec {name} {N}x{K}: {us:.2f} us in a graph ({b / us / 1e3:.0f} GB/s, "
+            f"{b / us / 1e3 / HBM_PEAK_GBS:.3f} of peak), {launched:.2f} us launched one by one, "
+            f"{single:.2f} us alone")
+        for w in ws:
+            w.free()
         dx.free(), dy.free()
     return res
 

@@ -171,6 +171,12 @@ int pbx_timer_stop(pbx_ctx *ctx, double *elapsed_ms);
 int pbx_bench_linear(pbx_ctx *ctx, int n_ops, const pbx_weight *const *W,
                      const float *const *dX, float *const *dY, int64_t M,
                      int reps, double *elapsed_ms);
+/* The same pass captured once into a HIP graph and replayed `reps` times
+ * (the launches stream without host launch gaps).  Timing helpers; no
+ * reference counterpart. */
+int pbx_bench_linear_graph(pbx_ctx *ctx, int n_ops, const pbx_weight *const *W,
+                           const float *const *dX, float *const *dY, int64_t M,
+                           int reps, double *elapsed_ms);
 
 /* ---- resident model and on-GPU decode step ----------------------------
  * A Llama-family model held in device memory, replacing the reference's

@@ -74,6 +74,33 @@ PBX_SMALL(pbx_gemv_f32_small, PBX_F32, 2)
 PBX_SMALL(pbx_gemv_f16_small, PBX_F16, 4)
 PBX_SMALL(pbx_gemv_q6_k_small, PBX_Q6K, 4)
 
+// Integer-limb GEMVs (Q4_0 / Q8_0, K = 2048..8192; pbx_gemv_impl.h) for the
+// instruction, launched with a GemvArgs block (X, bias, Y, N, B, the weight
+// planes; grid y = activation rows).  Name: pbx_gemv_<type>_i<WV>x<RT>b<IB>,
+// with a trailing l for the tile-loop variant (tall matrices, no bias).
+#define PBX_INT(NAME, TYPE, WV, RT, IB, LOOP)                                 \
+  extern "C" __global__ void __launch_bounds__(WV * 64) NAME(GemvArgs a) {   \
+    gemv_int<TYPE, WV, RT, IB, PRO_NONE, EPI_STORE, LOOP>(a);                 \
+  }
+PBX_INT(pbx_gemv_q4_0_i16x4b1, PBX_Q4, 16, 4, 1, false)
+PBX_INT(pbx_gemv_q4_0_i4x2b1, PBX_Q4, 4, 2, 1, false)
+PBX_INT(pbx_gemv_q4_0_i4x1b1, PBX_Q4, 4, 1, 1, false)
+PBX_INT(pbx_gemv_q4_0_i4x8b1l, PBX_Q4, 4, 8, 1, true)
+PBX_INT(pbx_gemv_q4_0_i8x4b2, PBX_Q4, 8, 4, 2, false)
+PBX_INT(pbx_gemv_q4_0_i4x2b2, PBX_Q4, 4, 2, 2, false)
+PBX_INT(pbx_gemv_q4_0_i4x1b2, PBX_Q4, 4, 1, 2, false)
+PBX_INT(pbx_gemv_q4_0_i4x2b4, PBX_Q4, 4, 2, 4, false)
+PBX_INT(pbx_gemv_q4_0_i4x1b4, PBX_Q4, 4, 1, 4, false)
+PBX_INT(pbx_gemv_q8_0_i8x4b1, PBX_Q8, 8, 4, 1, false)
+PBX_INT(pbx_gemv_q8_0_i4x2b1, PBX_Q8, 4, 2, 1, false)
+PBX_INT(pbx_gemv_q8_0_i4x1b1, PBX_Q8, 4, 1, 1, false)
+PBX_INT(pbx_gemv_q8_0_i4x8b1l, PBX_Q8, 4, 8, 1, true)
+PBX_INT(pbx_gemv_q8_0_i8x4b2, PBX_Q8, 8, 4, 2, false)
+PBX_INT(pbx_gemv_q8_0_i4x2b2, PBX_Q8, 4, 2, 2, false)
+PBX_INT(pbx_gemv_q8_0_i4x1b2, PBX_Q8, 4, 1, 2, false)
+PBX_INT(pbx_gemv_q8_0_i4x2b4, PBX_Q8, 4, 2, 4, false)
+PBX_INT(pbx_gemv_q8_0_i4x1b4, PBX_Q8, 4, 1, 4, false)
+
 // Reference Q8 tensor (quantize.js:30-50, matmul_q8 quantize.js:224-266):
 // q is the flat int8 [K,N] array, scales one f32 per 32 flat elements.  The
 // scale used for (k, n) is the one matmul_q8 picks: the block holding the

@@ -748,14 +748,16 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
-// LOOP (lm head): a workgroup takes tiles blockIdx.x, blockIdx.x + G, ...
-// (G = gridDim.x) with the next tile's bytes in flight while a tile is
-// reduced, builds the activation limbs once, and writes one argmax key.
+// LOOP (lm heads, tall matrices): a workgroup takes tiles blockIdx.x,
+// blockIdx.x + G, ... (G = gridDim.x) with the next tile's bytes in flight
+// while a tile is reduced and builds the activation limbs once; EPI_ARGMAX
+// writes one key per workgroup, EPI_STORE stores without a bias.
+// Activation row blockIdx.y (the plain instruction's M < 4 rows).
 template <int TYPE, int WV, int RT, int IB, int PRO, int EPI, bool LOOP = false>
 __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   static_assert(TYPE == PBX_Q4 || TYPE == PBX_Q8, "quantised weights only");
   static_assert(IB <= WV, "one prologue wave per 64 blocks");
-  static_assert(!LOOP || EPI == EPI_ARGMAX, "the tile loop serves the lm head");
+  static_assert(!LOOP || EPI == EPI_ARGMAX || EPI == EPI_STORE, "tile loop epilogues");
   constexpr int QB = BlockTraits<TYPE>::QB;
   constexpr int NV = QB / 16;
   constexpr bool PAIR = EPI == EPI_SWIGLU;
@@ -780,7 +782,8 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     return PAIR ? (r0 + (i < RT / 2 ? i : i - RT / 2)) < NO : (r0 + i) < N;
   };
   constexpr int LPR = 64 / RT;  // lanes per row after the transposed reduction
-  float *y = a.Y;
+  const float *X = a.X + (size_t)blockIdx.y * K;
+  float *y = a.Y + (size_t)blockIdx.y * NO;
 
   // 1. Prologue waves (wave w < IB owns blocks 64w + lane) request their
   //    activation block and RMSNorm weights before any wave requests weight
@@ -793,7 +796,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   if (pro) {
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      const float *src = a.X + (size_t)(pvalid ? pb : 0) * 32 + 4 * v;
+      const float *src = X + (size_t)(pvalid ? pb : 0) * 32 + 4 * v;
       xv[v] = *reinterpret_cast<const float4 *>(src);
       nv[v] = make_float4(1.f, 1.f, 1.f, 1.f);
       if constexpr (PRO == PRO_RMSNORM)
@@ -979,9 +982,11 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     auto consume = [&](int k, float tot) {
       const int n = rbase(blockIdx.x + k * G) + row;
       if ((lane % LPR) == 0 && n < N) {
-        y[n] = tot;  // no bias on the lm head (a load here would wait for the stream)
-        const uint64_t key = argmax_key(tot, (unsigned)n);
-        best = key > best ? key : best;
+        y[n] = tot;  // no bias in the loop (a load here would wait for the stream)
+        if constexpr (EPI == EPI_ARGMAX) {
+          const uint64_t key = argmax_key(tot, (unsigned)n);
+          best = key > best ? key : best;
+        }
       }
     };
     int k = 0;
@@ -1000,6 +1005,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     }
     if (k + 1 < TW) consume(k + 1, dots(dbB, qB));
     if (k + 2 < TW) consume(k + 2, dots(dbA, qA));
+    if constexpr (EPI != EPI_ARGMAX) return;
     best = wave_max_u64(best);
     if (lane == 0) kred[wave] = best;
     __syncthreads();

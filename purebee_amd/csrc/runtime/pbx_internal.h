@@ -59,9 +59,26 @@ enum {
 
 #define PBX_WEIGHT_MAGIC 0x50425857u  // "PBXW"
 
+// Host-side layout of GemvArgs (pbx_gemv_impl.h), passed by value to the
+// GEMV kernels that take the argument block.
+struct pbx_gemv_args {
+  const void *qs;
+  const void *dsc;
+  const float *X;
+  const float *X2;
+  const float *normw;
+  const float *bias;
+  float *Y;
+  uint64_t *partials;
+  int N, B;
+  float eps;
+  const void *msc;
+};
+
 struct pbx_ctx {
   int device = 0;
   int cu_count = 256;
+  bool gemv_int = true;  // integer-limb GEMVs for the instruction (PBX_GEMV_INT=0: off)
   char name[256] = {0};
   std::string code_object;
   std::string err;

@@ -23,19 +23,7 @@
 
 namespace {
 
-struct GemvArgsHost {  // layout of GemvArgs in pbx_gemv_impl.h
-  const void *qs;
-  const void *dsc;
-  const float *X;
-  const float *X2;
-  const float *normw;
-  const float *bias;
-  float *Y;
-  uint64_t *partials;
-  int N, B;
-  float eps;
-  const void *msc;
-};
+using GemvArgsHost = pbx_gemv_args;
 
 struct AttnArgsHost {  // AttnArgs in pbx_decode.hip
   const float *qkv;

@@ -106,6 +106,10 @@ extern "C" int pbx_init(int device, pbx_ctx **out) {
     snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
     c->cu_count = prop.multiProcessorCount;
   }
+  {
+    const char *gi = getenv("PBX_GEMV_INT");
+    c->gemv_int = !(gi && gi[0] == '0');
+  }
   for (int m = 0; m < kModuleCount; ++m) {
     std::string path = dir + "/" + kModuleFiles[m];
     e = hipModuleLoad(&c->modules[m], path.c_str());
@@ -513,6 +517,37 @@ int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t
   if (M >= PBX_GEMM_MIN_M && w->type != PBX_TYPE_Q6_K)
     return pbx_gemm_enqueue(c, w, dX, M, dBias, dY, stream);
   int B = (int)w->B;
+  // Integer-limb kernels (gemv_int) for Q4_0 / Q8_0 with K = 2048..8192 (not
+  // 4097..6144): rows per workgroup by N so the grid keeps >= 256 workgroups
+  // where it can, and the tile loop (two workgroups a CU) for tall matrices
+  // without a bias.
+  if (c->gemv_int && (w->type == PBX_TYPE_Q4_0 || w->type == PBX_TYPE_Q8_0) && B >= 64 &&
+      B <= 256 && (B + 63) / 64 != 3) {
+    const bool is_q4 = w->type == PBX_TYPE_Q4_0;
+    const int ib = (B + 63) / 64;
+    int wv = 4, rt = 1;
+    bool loop = false;
+    if (ib == 1 && N >= 65536 && !dBias) {
+      rt = 8;
+      loop = true;
+    } else if (ib <= 2 && N >= 8192) {
+      wv = ib == 1 && is_q4 ? 16 : 8;
+      rt = 4;
+    } else if (N >= 2048) {
+      rt = 2;
+    }
+    const std::string name = std::string("pbx_gemv_") + (is_q4 ? "q4_0" : "q8_0") + "_i" +
+                             std::to_string(wv) + "x" + std::to_string(rt) + "b" +
+                             std::to_string(ib) + (loop ? "l" : "");
+    hipFunction_t f = pbx_kernel_by_name(c, name);
+    if (!f) return pbx_fail(c, PBX_ELOAD, "pbx_linear: kernel %s missing", name.c_str());
+    const int tiles = (N + wv * rt - 1) / (wv * rt);
+    pbx_gemv_args g{w->qs, w->d, dX, nullptr, nullptr, dBias, dY, nullptr, N, B, 0.f, w->m};
+    void *gargs[] = {&g};
+    return pbx_launch_fn(c, f, name.c_str(),
+                         dim3((unsigned)(loop ? std::min(tiles, 2 * c->cu_count) : tiles), gy),
+                         dim3(64 * wv), gargs, stream);
+  }
   void *args[] = {(void *)&w->qs, (void *)&w->d, (void *)&w->m, &dX, &dBias, &dY, &N, &B};
   const bool q4 = w->type == PBX_TYPE_Q4_0 || w->type == PBX_TYPE_Q4_1;
   if (B <= 32) {
@@ -749,4 +784,40 @@ extern "C" int pbx_bench_linear(pbx_ctx *c, int n_ops, const pbx_weight *const *
       if (rc) return rc;
     }
   return pbx_timer_stop(c, ms);
+}
+
+extern "C" int pbx_bench_linear_graph(pbx_ctx *c, int n_ops, const pbx_weight *const *W,
+                                      const float *const *dX, float *const *dY, int64_t M,
+                                      int reps, double *ms) {
+  if (!c || !W || !dX || !dY || !ms || n_ops <= 0 || reps <= 0 || M <= 0 || M >= PBX_GEMM_MIN_M)
+    return pbx_fail(c, PBX_EINVAL, "pbx_bench_linear_graph: bad arguments (M < %d)",
+                    PBX_GEMM_MIN_M);
+  for (int i = 0; i < n_ops; ++i)
+    if (!weight_ok(W[i]) || !dX[i] || !dY[i])
+      return pbx_fail(c, PBX_EINVAL, "pbx_bench_linear_graph: bad operand %d", i);
+  HIPCHK(c, hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  HIPCHK(c, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  int rc = PBX_OK;
+  for (int i = 0; i < n_ops && !rc; ++i) rc = pbx_linear_enqueue(c, W[i], dX[i], M, nullptr, dY[i], s);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(s, &g);
+  if (rc || e != hipSuccess || !g) {
+    if (g) hipGraphDestroy(g);
+    return rc ? rc : pbx_fail(c, PBX_EHIP, "pbx_bench_linear_graph: capture failed");
+  }
+  hipGraphExec_t x = nullptr;
+  if (hipGraphInstantiate(&x, g, nullptr, nullptr, 0) != hipSuccess) {
+    hipGraphDestroy(g);
+    return pbx_fail(c, PBX_EHIP, "pbx_bench_linear_graph: instantiate failed");
+  }
+  if (hipGraphLaunch(x, s) != hipSuccess) rc = pbx_fail(c, PBX_EHIP, "graph launch failed");
+  if (!rc && hipEventRecord(c->ev0, s) != hipSuccess) rc = pbx_fail(c, PBX_EHIP, "event failed");
+  for (int r = 0; r < reps && !rc; ++r)
+    if (hipGraphLaunch(x, s) != hipSuccess) rc = pbx_fail(c, PBX_EHIP, "graph launch failed");
+  if (!rc) rc = pbx_timer_stop(c, ms);
+  hipStreamSynchronize(s);
+  hipGraphExecDestroy(x);
+  hipGraphDestroy(g);
+  return rc;
 }

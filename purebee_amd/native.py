@@ -32,6 +32,7 @@ EXPORTS = (
     "pbx_synth_normal",
     "pbx_dev_alloc", "pbx_dev_free", "pbx_memcpy_h2d", "pbx_memcpy_d2h", "pbx_memset_dev",
     "pbx_dev_copy", "pbx_sync", "pbx_timer_start", "pbx_timer_stop", "pbx_bench_linear",
+    "pbx_bench_linear_graph",
     "pbx_model_create", "pbx_model_free", "pbx_model_set_tensor", "pbx_model_forward",
     "pbx_model_forward_batch", "pbx_model_generate", "pbx_model_reset_cache", "pbx_model_rollback", "pbx_model_info",
     "pbx_model_profile", "pbx_model_op_name", "pbx_model_bench_role",
@@ -128,6 +129,9 @@ def load_library():
         "pbx_timer_start": (ctypes.c_int, [_vp]),
         "pbx_timer_stop": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_double)]),
         "pbx_bench_linear": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.POINTER(_vp),
+                                            ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i64,
+                                            ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
+        "pbx_bench_linear_graph": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.POINTER(_vp),
                                             ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i64,
                                             ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
         "pbx_model_create": (ctypes.c_int, [_vp, ctypes.POINTER(ModelConfig), ctypes.POINTER(_vp)]),
@@ -368,13 +372,16 @@ class Context:
         self._call("pbx_timer_stop", self._p, ctypes.byref(ms))
         return ms.value
 
-    def bench_linear(self, weights, dXs, dYs, M, reps):
+    def bench_linear(self, weights, dXs, dYs, M, reps, graph=False):
+        """ms for `reps` passes over the linears, launched one by one or (graph)
+        as one captured HIP graph replayed `reps` times."""
         n = len(weights)
         W = (_vp * n)(*[w.ptr for w in weights])
         X = (_vp * n)(*dXs)
         Y = (_vp * n)(*dYs)
         ms = ctypes.c_double()
-        self._call("pbx_bench_linear", self._p, n, W, X, Y, M, reps, ctypes.byref(ms))
+        self._call("pbx_bench_linear_graph" if graph else "pbx_bench_linear", self._p, n, W, X, Y,
+                   M, reps, ctypes.byref(ms))
         return ms.value
 
 

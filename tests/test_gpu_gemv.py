@@ -225,6 +225,41 @@ def test_bias_and_multi_row(ctx, t):
     w.free()
 
 
+@pytest.mark.parametrize("t", [pb.TYPE_Q4_0, pb.TYPE_Q8_0])
+@pytest.mark.parametrize("N,K,M,bias", [
+    (512, 2048, 3, True),      # 4 waves x 1 row, one 64-block group a lane
+    (2048, 2048, 2, False),    # 4 x 2
+    (8192, 2048, 1, True),     # 16 x 4 (Q4_0) / 8 x 4 (Q8_0)
+    (8192, 4096, 2, True),     # 8 x 4, two groups
+    (1000, 3104, 3, False),    # B = 97: the second group's lanes past B masked
+    (2048, 8192, 1, True),     # 4 x 2, four groups
+    (70000, 2048, 1, False),   # tall, no bias: the tile loop (512 workgroups)
+    (70000, 2048, 2, True),    # tall with bias: one tile a workgroup
+])
+def test_integer_limb_instruction(ctx, monkeypatch, t, N, K, M, bias):
+    """The instruction's integer-limb kernels (Q4_0 / Q8_0, K = 2048..8192)
+    against the oracle and against the float-unpack kernels
+    (PBX_GEMV_INT=0), for 1-3 activation rows with and without bias."""
+    print(f"[case] integer-limb linear type={t} N={N} K={K} M={M} bias={bias}", flush=True)
+    raw = quantize(t, synth_matrix(3 * N + K, N, K))
+    X = pb.synth_normal(N + 5 * K, M * K).reshape(M, K)
+    b = pb.synth_normal(N + 1, N) if bias else None
+    w = ctx.upload(t, N, K, raw)
+    Y = ctx.linear(w, X, b)
+    monkeypatch.setenv("PBX_GEMV_INT", "0")
+    fctx = pb.Context(0)
+    monkeypatch.delenv("PBX_GEMV_INT")
+    wf = fctx.upload(t, N, K, raw)
+    F = fctx.linear(wf, X, b)
+    for m in range(M):
+        ref = oracle.matvec(t, X[m], raw, N, K) + (b if bias else 0)
+        assert rel_l2(Y[m], ref) < 1e-5, (m, rel_l2(Y[m], ref))
+        assert rel_l2(Y[m], F[m]) < 1e-5
+    wf.free()
+    fctx.close()
+    w.free()
+
+
 @pytest.mark.parametrize("K,N,M", [(288, 288, 1), (288, 768, 1), (768, 288, 3), (64, 100, 2)])
 def test_q8_ref_tensor_matches_matmul_q8(ctx, K, N, M):
     """The reference's own QuantizedTensor (quantize.js) through
