@@ -103,6 +103,21 @@ DK_INT_LMH(PBX_Q4, q4, 4, 8, 1)
 DK_INT_LMHL(PBX_Q4, q4, 4, 8, 1)
 DK_INT_LMHL(PBX_Q4, q4, 4, 4, 1)
 
+// Row-batched integer-limb GEMVs: up to MR activation rows against one pass
+// over the weights (speculative verify, prompts of 4..MR tokens), args.rows
+// valid.  Name: pbx_dk_<type>_i<WV>x<RT>b<IB>r<MR>[l]_<mode>; mode lmh here
+// stores logit rows (no argmax).
+#define DK_INT_ROWS(T, TN, WV, RT, IB, MR, LOOP, L, PRO, EPI, MN)                          \
+  extern "C" __global__ void __launch_bounds__(WV * 64)                                   \
+      pbx_dk_##TN##_i##WV##x##RT##b##IB##r##MR##L##_##MN(GemvArgs a) {                    \
+    gemv_int<T, WV, RT, IB, PRO, EPI, LOOP, MR>(a);                                       \
+  }
+DK_INT_ROWS(PBX_Q4, q4, 8, 2, 1, 8, false, , PRO_RMSNORM, EPI_STORE, qkv)
+DK_INT_ROWS(PBX_Q4, q4, 8, 1, 1, 8, false, , PRO_NONE, EPI_ADD, add)
+DK_INT_ROWS(PBX_Q4, q4, 8, 1, 4, 5, false, , PRO_NONE, EPI_ADD, add)  // LDS: 5 rows x 24 KB
+DK_INT_ROWS(PBX_Q4, q4, 8, 4, 1, 8, false, , PRO_RMSNORM, EPI_SWIGLU, gu)
+DK_INT_ROWS(PBX_Q4, q4, 8, 2, 1, 8, true, l, PRO_RMSNORM, EPI_STORE, lmh)
+
 DK_MODES_WIDE(PBX_F32, f32, 2)
 DK_MODES_WIDE(PBX_F32, f32, 4)
 DK_MODES_SMALL(PBX_F32, f32, 2)

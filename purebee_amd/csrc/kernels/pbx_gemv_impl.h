@@ -50,6 +50,7 @@ struct GemvArgs {
   int N, B;
   float eps;
   const uint16_t *msc;  // fp16 min plane (Q4_1), same layout as dsc
+  int rows;             // gemv_int with MR > 1: valid activation rows
 };
 
 namespace pbx {
@@ -752,25 +753,33 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) {
 // blockIdx.x + G, ... (G = gridDim.x) with the next tile's bytes in flight
 // while a tile is reduced and builds the activation limbs once; EPI_ARGMAX
 // writes one key per workgroup, EPI_STORE stores without a bias.
-// Activation row blockIdx.y (the plain instruction's M < 4 rows).
-template <int TYPE, int WV, int RT, int IB, int PRO, int EPI, bool LOOP = false>
+// MR > 1: MR activation rows (the first a.rows of them valid; row stride K
+// in, N out) against one pass over the weight bytes -- the speculative
+// verify and short prompts.  The prologue's (row, 64-block group) slots are
+// spread over the waves.  MR = 1: activation row blockIdx.y (the plain
+// instruction's M < 4 rows).
+template <int TYPE, int WV, int RT, int IB, int PRO, int EPI, bool LOOP = false, int MR = 1>
 __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   static_assert(TYPE == PBX_Q4 || TYPE == PBX_Q8, "quantised weights only");
-  static_assert(IB <= WV, "one prologue wave per 64 blocks");
+  static_assert(MR > 1 || IB <= WV, "one prologue wave per 64 blocks");
   static_assert(!LOOP || EPI == EPI_ARGMAX || EPI == EPI_STORE, "tile loop epilogues");
+  static_assert(MR == 1 || EPI != EPI_ARGMAX, "argmax keys for one row");
   constexpr int QB = BlockTraits<TYPE>::QB;
   constexpr int NV = QB / 16;
   constexpr bool PAIR = EPI == EPI_SWIGLU;
   static_assert(IB * 64 * 32 <= PBX_INT_MAXK, "K limit");
-  __shared__ __attribute__((aligned(16))) int limb[3][IB * 64 * 8];
-  __shared__ int bsum[IB * 64];
-  __shared__ float red[2][IB];
-  __shared__ float xscale;
+  constexpr int PP = MR * IB;             // prologue slots: (row, 64-block group)
+  constexpr int PS = (PP + WV - 1) / WV;  // slots a wave
+  __shared__ __attribute__((aligned(16))) int limb[MR][3][IB * 64 * 8];
+  __shared__ int bsum[MR][IB * 64];
+  __shared__ float red[2][MR][IB];
+  __shared__ float xscale[MR];
   __shared__ uint64_t kred[WV];
 
   const int N = a.N, B = a.B, K = B * 32;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
   const int NO = PAIR ? N / 2 : N;
+  const int rows = MR == 1 ? 1 : a.rows;  // valid activation rows
   constexpr int RTO = PAIR ? RT / 2 : RT;  // output rows a wave
   const int n_tiles = (NO + WV * RTO - 1) / (WV * RTO);
   // first output row of the wave in tile t
@@ -782,40 +791,48 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     return PAIR ? (r0 + (i < RT / 2 ? i : i - RT / 2)) < NO : (r0 + i) < N;
   };
   constexpr int LPR = 64 / RT;  // lanes per row after the transposed reduction
-  const float *X = a.X + (size_t)blockIdx.y * K;
-  float *y = a.Y + (size_t)blockIdx.y * NO;
+  const float *X = a.X + (size_t)blockIdx.y * MR * K;
+  float *y = a.Y + (size_t)blockIdx.y * MR * NO;
 
-  // 1. Prologue waves (wave w < IB owns blocks 64w + lane) request their
-  //    activation block and RMSNorm weights before any wave requests weight
-  //    bytes: a CU returns loads in issue order, so activations requested
-  //    behind the weight stream would arrive only with it.
-  const int pb = wave * 64 + lane;  // the prologue lane's block
-  const bool pro = wave < IB;
-  const bool pvalid = pro && pb < B;
-  float4 xv[8], nv[8];
-  if (pro) {
+  // 1. Prologue slots (slot p = wave + WV*s: activation row p / IB, blocks
+  //    64*(p % IB) + lane) request their activation blocks and RMSNorm
+  //    weights before any wave requests weight bytes: a CU returns loads in
+  //    issue order, so activations requested behind the weight stream would
+  //    arrive only with it.  Rows past `rows` read row 0 and are not stored.
+  float4 xv[PS][8], nv[PS][8];
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const float *src = X + (size_t)(pvalid ? pb : 0) * 32 + 4 * v;
-      xv[v] = *reinterpret_cast<const float4 *>(src);
-      nv[v] = make_float4(1.f, 1.f, 1.f, 1.f);
-      if constexpr (PRO == PRO_RMSNORM)
-        nv[v] = *reinterpret_cast<const float4 *>(a.normw + (size_t)(pvalid ? pb : 0) * 32 + 4 * v);
+  for (int sl = 0; sl < PS; ++sl) {
+    const int p = wave + WV * sl;
+    if (p < PP) {
+      const int pm = p / IB, pb = (p % IB) * 64 + lane;
+      const int bl = pb < B ? pb : 0;
+      const float *xr = X + (size_t)(pm < rows ? pm : 0) * K;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        xv[sl][v] = *reinterpret_cast<const float4 *>(xr + (size_t)bl * 32 + 4 * v);
+        nv[sl][v] = make_float4(1.f, 1.f, 1.f, 1.f);
+        if constexpr (PRO == PRO_RMSNORM)
+          nv[sl][v] = *reinterpret_cast<const float4 *>(a.normw + (size_t)bl * 32 + 4 * v);
+      }
     }
   }
   lds_barrier();
 
-  // 2. Every wave: the residual it will add (EPI_ADD), the block scales, then
-  //    the weight bytes.  Loads are unconditional from clamped addresses
-  //    (rows past N read row 0 and are never stored, blocks past B read
-  //    block 0 and get a zero scale where the dots use it) so the compiler
-  //    issues them back to back; nothing is computed from a loaded value
-  //    before the weight bytes are requested.
-  float res = 0.f;
+  // 2. Every wave: the residuals it will add (EPI_ADD), the block scales,
+  //    then the weight bytes.  Loads are unconditional from clamped
+  //    addresses (rows past N read row 0 and are never stored, blocks past B
+  //    read block 0 and get a zero scale where the dots use it) so the
+  //    compiler issues them back to back; nothing is computed from a loaded
+  //    value before the weight bytes are requested.
+  float res[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) res[m] = 0.f;
   if constexpr (EPI == EPI_ADD) {
     const int r0 = rbase(blockIdx.x);
     const int rr = (lane % LPR) == 0 ? lane / LPR : RT;
-    if (rr < RT && r0 + rr < N) res = y[r0 + rr];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      if (rr < RT && r0 + rr < N) res[m] = y[(size_t)(m < rows ? m : 0) * NO + r0 + rr];
   }
   auto load_tile = [&](int t, unsigned (&db)[RT][IB], uint4 (&qq)[RT][IB][NV]) {
     const int r0 = rbase(t);
@@ -853,124 +870,151 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   if constexpr (LOOP) load_tile(blockIdx.x + (TW > 1 ? G : 0), dbB, qB);
   __builtin_amdgcn_sched_barrier(0);
 
-  // 3. Prologue waves: sum of squares (RMSNorm) and max |x * w| of their
-  //    blocks, combined across the IB prologue waves through LDS.
-  float ss = 0.f, mw = 0.f;
-  if (pro) {
+  // 3. Prologue slots: sum of squares (RMSNorm) and max |x * w| of their
+  //    blocks, combined across a row's IB slots through LDS.
+  float ss[PS], mw[PS];
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const float4 t = pvalid ? xv[v] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[v];
-      if constexpr (PRO == PRO_RMSNORM)
-        ss = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, ss))));
-      mw = fmaxf(mw, fmaxf(fmaxf(fabsf(t.x * w.x), fabsf(t.y * w.y)),
-                           fmaxf(fabsf(t.z * w.z), fabsf(t.w * w.w))));
-    }
-    if constexpr (PRO == PRO_RMSNORM) ss = wave_sum(ss);
-    mw = wave_max(mw);
-  }
-  if constexpr (IB > 1) {
-    if (pro && lane == 0) {
-      red[0][wave] = ss;
-      red[1][wave] = mw;
-    }
-    lds_barrier();
-    if (pro) {
-      ss = 0.f;
-      mw = 0.f;
-#pragma unroll
-      for (int w = 0; w < IB; ++w) {
-        ss += red[0][w];
-        mw = fmaxf(mw, red[1][w]);
-      }
-    }
-  }
-  // 4. Prologue waves: fixed point x_q = rint(x * w * inv * 2^(22 - e)) of
-  //    their block as three byte limbs plus the block sum, into LDS.
-  if (pro) {
-    const float inv = PRO == PRO_RMSNORM ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.f;
-    int e = 0;
-    const float mx = mw * inv;
-    if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
-    const float c = inv * ldexpf(1.f, 22 - e);
-    if (pvalid) {
-      int bs = 0;
+  for (int sl = 0; sl < PS; ++sl) {
+    ss[sl] = 0.f;
+    mw[sl] = 0.f;
+    const int p = wave + WV * sl;
+    if (p < PP) {
+      const bool pvalid = (p % IB) * 64 + lane < B;
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
-        const float4 t = xv[v], w = nv[v];
-        const int xq[4] = {(int)rintf(t.x * w.x * c), (int)rintf(t.y * w.y * c),
-                           (int)rintf(t.z * w.z * c), (int)rintf(t.w * w.w * c)};
-        unsigned l0 = 0, l1 = 0, l2 = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int x0 = (int)(int8_t)(xq[k] & 0xFF);
-          const int r1 = (xq[k] - x0) >> 8;
-          const int x1 = (int)(int8_t)(r1 & 0xFF);
-          const int x2 = (r1 - x1) >> 8;
-          l0 |= (unsigned)(x0 & 0xFF) << (8 * k);
-          l1 |= (unsigned)(x1 & 0xFF) << (8 * k);
-          l2 |= (unsigned)(x2 & 0xFF) << (8 * k);
-          bs += xq[k];
-        }
-        limb[0][pb * 8 + v] = (int)l0;
-        limb[1][pb * 8 + v] = (int)l1;
-        limb[2][pb * 8 + v] = (int)l2;
+        const float4 t = pvalid ? xv[sl][v] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[sl][v];
+        if constexpr (PRO == PRO_RMSNORM)
+          ss[sl] = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, ss[sl]))));
+        mw[sl] = fmaxf(mw[sl], fmaxf(fmaxf(fabsf(t.x * w.x), fabsf(t.y * w.y)),
+                                     fmaxf(fabsf(t.z * w.z), fabsf(t.w * w.w))));
       }
-      bsum[pb] = bs;
+      if constexpr (PRO == PRO_RMSNORM) ss[sl] = wave_sum(ss[sl]);
+      mw[sl] = wave_max(mw[sl]);
     }
-    if (tid == 0) xscale = ldexpf(1.f, e - 22);
+  }
+  if constexpr (IB > 1) {
+#pragma unroll
+    for (int sl = 0; sl < PS; ++sl) {
+      const int p = wave + WV * sl;
+      if (p < PP && lane == 0) {
+        red[0][p / IB][p % IB] = ss[sl];
+        red[1][p / IB][p % IB] = mw[sl];
+      }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int sl = 0; sl < PS; ++sl) {
+      const int p = wave + WV * sl;
+      if (p < PP) {
+        ss[sl] = 0.f;
+        mw[sl] = 0.f;
+#pragma unroll
+        for (int w = 0; w < IB; ++w) {
+          ss[sl] += red[0][p / IB][w];
+          mw[sl] = fmaxf(mw[sl], red[1][p / IB][w]);
+        }
+      }
+    }
+  }
+  // 4. Prologue slots: fixed point x_q = rint(x * w * inv * 2^(22 - e)) of
+  //    their blocks as three byte limbs plus the block sums, into LDS.
+#pragma unroll
+  for (int sl = 0; sl < PS; ++sl) {
+    const int p = wave + WV * sl;
+    if (p < PP) {
+      const int pm = p / IB, pb = (p % IB) * 64 + lane;
+      const float inv = PRO == PRO_RMSNORM ? 1.0f / sqrtf(ss[sl] / (float)K + a.eps) : 1.f;
+      int e = 0;
+      const float mx = mw[sl] * inv;
+      if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
+      const float c = inv * ldexpf(1.f, 22 - e);
+      if (pb < B) {
+        int bs = 0;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const float4 t = xv[sl][v], w = nv[sl][v];
+          const int xq[4] = {(int)rintf(t.x * w.x * c), (int)rintf(t.y * w.y * c),
+                             (int)rintf(t.z * w.z * c), (int)rintf(t.w * w.w * c)};
+          unsigned l0 = 0, l1 = 0, l2 = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int x0 = (int)(int8_t)(xq[k] & 0xFF);
+            const int r1 = (xq[k] - x0) >> 8;
+            const int x1 = (int)(int8_t)(r1 & 0xFF);
+            const int x2 = (r1 - x1) >> 8;
+            l0 |= (unsigned)(x0 & 0xFF) << (8 * k);
+            l1 |= (unsigned)(x1 & 0xFF) << (8 * k);
+            l2 |= (unsigned)(x2 & 0xFF) << (8 * k);
+            bs += xq[k];
+          }
+          limb[pm][0][pb * 8 + v] = (int)l0;
+          limb[pm][1][pb * 8 + v] = (int)l1;
+          limb[pm][2][pb * 8 + v] = (int)l2;
+        }
+        bsum[pm][pb] = bs;
+      }
+      if (p % IB == 0 && lane == 0) xscale[pm] = ldexpf(1.f, e - 22);
+    }
   }
   lds_barrier();
-  const float unscale = xscale;
 
-  // 5. Dot products as the weight rows arrive; the lane's row sum after the
-  //    transposed reduction.
-  auto dots = [&](const unsigned (&db)[RT][IB], const uint4 (&qq)[RT][IB][NV]) -> float {
-    float acc[RT];
+  // 5. Dot products as the weight rows arrive; each row's sum after the
+  //    transposed reduction, per activation row.
+  auto dots = [&](const unsigned (&db)[RT][IB], const uint4 (&qq)[RT][IB][NV],
+                  float (&tot)[MR]) {
+    float acc[MR][RT];
 #pragma unroll
-    for (int i = 0; i < RT; ++i) acc[i] = 0.f;
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int i = 0; i < RT; ++i) acc[m][i] = 0.f;
 #pragma unroll
     for (int j = 0; j < IB; ++j) {
       const int b = lane + 64 * j;
       const int bl = b < B ? b : 0;  // lanes past B: zero scales cancel them
-      int xl[3][8];
-#pragma unroll
-      for (int L = 0; L < 3; ++L) {
-        const int4 t0 = *reinterpret_cast<const int4 *>(&limb[L][bl * 8]);
-        const int4 t1 = *reinterpret_cast<const int4 *>(&limb[L][bl * 8 + 4]);
-        xl[L][0] = t0.x; xl[L][1] = t0.y; xl[L][2] = t0.z; xl[L][3] = t0.w;
-        xl[L][4] = t1.x; xl[L][5] = t1.y; xl[L][6] = t1.z; xl[L][7] = t1.w;
-      }
-      const float corr = TYPE == PBX_Q4 ? 8.f * (float)bsum[bl] : 0.f;
       const unsigned bmask = b < B ? 0xFFFFu : 0u;
 #pragma unroll
-      for (int i = 0; i < RT; ++i) {
-        int s0 = 0, s1 = 0, s2 = 0;
-        if constexpr (TYPE == PBX_Q4) {
-          // byte t holds element t (low nibble) and t+16 (high): word k covers
-          // elements 4k..4k+3 (limb word k) and 16+4k.. (limb word 4+k)
-          const unsigned w[4] = {qq[i][j][0].x, qq[i][j][0].y, qq[i][j][0].z, qq[i][j][0].w};
+      for (int m = 0; m < MR; ++m) {
+        if (MR > 1 && m >= rows) break;  // uniform: rows past the batch
+        int xl[3][8];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int lo = (int)(w[k] & 0x0F0F0F0Fu), hi = (int)((w[k] >> 4) & 0x0F0F0F0Fu);
-            s0 = sdot4(lo, xl[0][k], s0); s0 = sdot4(hi, xl[0][4 + k], s0);
-            s1 = sdot4(lo, xl[1][k], s1); s1 = sdot4(hi, xl[1][4 + k], s1);
-            s2 = sdot4(lo, xl[2][k], s2); s2 = sdot4(hi, xl[2][4 + k], s2);
-          }
-        } else {
-          const unsigned w[8] = {qq[i][j][0].x, qq[i][j][0].y, qq[i][j][0].z, qq[i][j][0].w,
-                                 qq[i][j][1].x, qq[i][j][1].y, qq[i][j][1].z, qq[i][j][1].w};
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            s0 = sdot4((int)w[k], xl[0][k], s0);
-            s1 = sdot4((int)w[k], xl[1][k], s1);
-            s2 = sdot4((int)w[k], xl[2][k], s2);
-          }
+        for (int L = 0; L < 3; ++L) {
+          const int4 t0 = *reinterpret_cast<const int4 *>(&limb[m][L][bl * 8]);
+          const int4 t1 = *reinterpret_cast<const int4 *>(&limb[m][L][bl * 8 + 4]);
+          xl[L][0] = t0.x; xl[L][1] = t0.y; xl[L][2] = t0.z; xl[L][3] = t0.w;
+          xl[L][4] = t1.x; xl[L][5] = t1.y; xl[L][6] = t1.z; xl[L][7] = t1.w;
         }
-        const float f = fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0)) - corr;
-        acc[i] = fmaf(f, f16_bits_to_f32(db[i][j] & bmask), acc[i]);
+        const float corr = TYPE == PBX_Q4 ? 8.f * (float)bsum[m][bl] : 0.f;
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          int s0 = 0, s1 = 0, s2 = 0;
+          if constexpr (TYPE == PBX_Q4) {
+            // byte t holds element t (low nibble) and t+16 (high): word k
+            // covers elements 4k..4k+3 (limb word k) and 16+4k.. (word 4+k)
+            const unsigned w[4] = {qq[i][j][0].x, qq[i][j][0].y, qq[i][j][0].z, qq[i][j][0].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const int lo = (int)(w[k] & 0x0F0F0F0Fu), hi = (int)((w[k] >> 4) & 0x0F0F0F0Fu);
+              s0 = sdot4(lo, xl[0][k], s0); s0 = sdot4(hi, xl[0][4 + k], s0);
+              s1 = sdot4(lo, xl[1][k], s1); s1 = sdot4(hi, xl[1][4 + k], s1);
+              s2 = sdot4(lo, xl[2][k], s2); s2 = sdot4(hi, xl[2][4 + k], s2);
+            }
+          } else {
+            const unsigned w[8] = {qq[i][j][0].x, qq[i][j][0].y, qq[i][j][0].z, qq[i][j][0].w,
+                                   qq[i][j][1].x, qq[i][j][1].y, qq[i][j][1].z, qq[i][j][1].w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              s0 = sdot4((int)w[k], xl[0][k], s0);
+              s1 = sdot4((int)w[k], xl[1][k], s1);
+              s2 = sdot4((int)w[k], xl[2][k], s2);
+            }
+          }
+          const float f = fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0)) - corr;
+          acc[m][i] = fmaf(f, f16_bits_to_f32(db[i][j] & bmask), acc[m][i]);
+        }
       }
     }
-    return wave_transpose_reduce<RT>(acc, lane) * unscale;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) tot[m] = wave_transpose_reduce<RT>(acc[m], lane) * xscale[m];
   };
   const int row = lane / LPR;
 
@@ -979,52 +1023,63 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     // tile two on as soon as it has been reduced.  The steady-state loop
     // issues its loads unconditionally; the last two or three tiles follow.
     uint64_t best = 0;
-    auto consume = [&](int k, float tot) {
+    auto consume = [&](int k, const float (&tot)[MR]) {
       const int n = rbase(blockIdx.x + k * G) + row;
       if ((lane % LPR) == 0 && n < N) {
-        y[n] = tot;  // no bias in the loop (a load here would wait for the stream)
+#pragma unroll
+        for (int m = 0; m < MR; ++m)  // no bias in the loop (a load here would wait)
+          if (m < rows) y[(size_t)m * NO + n] = tot[m];
         if constexpr (EPI == EPI_ARGMAX) {
-          const uint64_t key = argmax_key(tot, (unsigned)n);
+          const uint64_t key = argmax_key(tot[0], (unsigned)n);
           best = key > best ? key : best;
         }
       }
     };
+    float tt[MR];
     int k = 0;
     for (; k + 3 < TW; k += 2) {
-      const float ta = dots(dbA, qA);
+      dots(dbA, qA, tt);
       load_tile(blockIdx.x + (k + 2) * G, dbA, qA);
-      consume(k, ta);
-      const float tb = dots(dbB, qB);
+      consume(k, tt);
+      dots(dbB, qB, tt);
       load_tile(blockIdx.x + (k + 3) * G, dbB, qB);
-      consume(k + 1, tb);
+      consume(k + 1, tt);
     }
-    {
-      const float ta = dots(dbA, qA);
-      if (k + 2 < TW) load_tile(blockIdx.x + (k + 2) * G, dbA, qA);
-      consume(k, ta);
+    dots(dbA, qA, tt);
+    if (k + 2 < TW) load_tile(blockIdx.x + (k + 2) * G, dbA, qA);
+    consume(k, tt);
+    if (k + 1 < TW) {
+      dots(dbB, qB, tt);
+      consume(k + 1, tt);
     }
-    if (k + 1 < TW) consume(k + 1, dots(dbB, qB));
-    if (k + 2 < TW) consume(k + 2, dots(dbA, qA));
+    if (k + 2 < TW) {
+      dots(dbA, qA, tt);
+      consume(k + 2, tt);
+    }
     if constexpr (EPI != EPI_ARGMAX) return;
     best = wave_max_u64(best);
     if (lane == 0) kred[wave] = best;
     __syncthreads();
     if (tid == 0) {
-      uint64_t k = kred[0];
+      uint64_t kk = kred[0];
 #pragma unroll
-      for (int w = 1; w < WV; ++w) k = kred[w] > k ? kred[w] : k;
-      a.partials[blockIdx.x] = k;
+      for (int w = 1; w < WV; ++w) kk = kred[w] > kk ? kred[w] : kk;
+      a.partials[blockIdx.x] = kk;
     }
     return;
   }
 
-  const float tot = dots(dbA, qA);
+  float tot[MR];
+  dots(dbA, qA, tot);
   const int r0 = rbase(blockIdx.x);
   if constexpr (PAIR) {
-    const float up = __shfl_xor(tot, 32, 64);
-    if (lane < 32 && (lane % LPR) == 0) {
-      const int n = r0 + row;
-      if (n < NO) y[n] = silu(tot) * up;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float up = __shfl_xor(tot[m], 32, 64);
+      if (m < rows && lane < 32 && (lane % LPR) == 0) {
+        const int n = r0 + row;
+        if (n < NO) y[(size_t)m * NO + n] = silu(tot[m]) * up;
+      }
     }
     return;
   }
@@ -1032,8 +1087,10 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   if ((lane % LPR) == 0) {
     const int n = r0 + row;
     if (n < N) {
-      epilogue_row<EPI>(a, y, n, tot, res);
-      if constexpr (EPI == EPI_ARGMAX) key = argmax_key(tot, (unsigned)n);
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < rows) epilogue_row<EPI>(a, y + (size_t)m * NO, n, tot[m], res[m]);
+      if constexpr (EPI == EPI_ARGMAX) key = argmax_key(tot[0], (unsigned)n);
     }
   }
   if constexpr (EPI == EPI_ARGMAX) {

@@ -73,6 +73,7 @@ struct pbx_gemv_args {
   int N, B;
   float eps;
   const void *msc;
+  int rows;
 };
 
 struct pbx_ctx {

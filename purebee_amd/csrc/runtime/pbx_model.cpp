@@ -833,6 +833,41 @@ static int linear_rows(pbx_model *m, const pbx_weight *w, const float *X, int n,
   return launch_k(m, "pbx_add_inplace", dim3((unsigned)((count + 255) / 256)), dim3(256), args);
 }
 
+// Row-batched integer-limb GEMVs (pbx_dk_q4_*r<MR>_*): one pass over the
+// weights for up to MR activation rows, with the RMSNorm prologue and the
+// residual / SwiGLU epilogues fused, for 1..8 rows (speculative verify,
+// short prompts) of a Q4_0 model with dim <= 2048 and hidden_dim 6145..8192.
+#define ROWS_MAX 8
+static bool rows_int_ok(const pbx_model *m) {
+  const pbx_model_config &g = m->cfg;
+  if (!m->gemv_int || g.weight_type != PBX_TYPE_Q4_0 || g.dim > 2048 || g.hidden_dim > 8192 ||
+      g.hidden_dim <= 6144)
+    return false;
+  const pbx_weight *head = m->output ? m->output : m->embd;
+  return head->type == PBX_TYPE_Q4_0;
+}
+
+// Launches kernel `name` (MR rows a launch) over n rows in groups of MR.
+static int launch_rows(pbx_model *m, const char *name, const pbx_weight *w, const float *X,
+                       const float *normw, float *Y, int n, int MR, int rows_per_wg,
+                       int wg_cap) {
+  hipFunction_t f = pbx_kernel_by_name(m->c, name);
+  if (!f) return pbx_fail(m->c, PBX_ELOAD, "model: kernel %s not found", name);
+  const bool pair = strstr(name, "_gu") != nullptr;
+  const int NO = pair ? (int)w->N / 2 : (int)w->N;
+  int tiles = (NO + rows_per_wg - 1) / rows_per_wg;
+  if (wg_cap > 0) tiles = std::min(tiles, wg_cap);
+  for (int r0 = 0; r0 < n; r0 += MR) {
+    pbx_gemv_args g{w->qs, w->d, X + (size_t)r0 * w->K, nullptr, normw, nullptr,
+                    Y + (size_t)r0 * NO, nullptr, (int)w->N, (int)w->B, m->cfg.rms_eps, w->m,
+                    std::min(MR, n - r0)};
+    void *args[] = {&g};
+    int rc = pbx_launch_fn(m->c, f, name, dim3((unsigned)tiles), dim3(512), args, m->c->stream);
+    if (rc) return rc;
+  }
+  return PBX_OK;
+}
+
 static int rmsnorm_rows(pbx_model *m, const float *x, const float *w, float *out, int n) {
   int dim = m->cfg.dim;
   float eps = m->cfg.rms_eps;
@@ -856,11 +891,18 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
     if ((rc = launch_k(m, "pbx_embed_rows", dim3((g.dim + 255) / 256, n), dim3(256), args))) return rc;
   }
   const size_t layer_kv = (size_t)g.max_seq * m->kvdim;
+  const bool rows_int = n <= ROWS_MAX && rows_int_ok(m);
   for (int l = 0; l < g.n_layers; ++l) {
     Layer &L = m->layers[l];
     float *kc = m->kcache + l * layer_kv, *vc = m->vcache + l * layer_kv;
-    if ((rc = rmsnorm_rows(m, m->bx, L.attn_norm, m->bxn, n))) return rc;
-    if ((rc = linear_rows(m, L.wqkv, m->bxn, n, m->bqkv, false))) return rc;
+    if (rows_int) {
+      if ((rc = launch_rows(m, "pbx_dk_q4_i8x2b1r8_qkv", L.wqkv, m->bx, L.attn_norm, m->bqkv, n,
+                            8, 16, 0)))
+        return rc;
+    } else {
+      if ((rc = rmsnorm_rows(m, m->bx, L.attn_norm, m->bxn, n))) return rc;
+      if ((rc = linear_rows(m, L.wqkv, m->bxn, n, m->bqkv, false))) return rc;
+    }
     {
       float *qkv = m->bqkv, *rope = m->rope;
       int st = start, nh = g.n_heads, nkv = g.n_kv_heads, hd = g.head_dim;
@@ -881,6 +923,15 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
         rc = launch_k(m, "pbx_attention_rows", dim3(g.n_heads, n), dim3(256), args);
       }
       if (rc) return rc;
+    }
+    if (rows_int) {
+      if ((rc = launch_rows(m, "pbx_dk_q4_i8x1b1r8_add", L.wo, m->battn, nullptr, m->bx, n, 8, 8,
+                            0)) ||
+          (rc = launch_rows(m, "pbx_dk_q4_i8x4b1r8_gu", L.wgu, m->bx, L.ffn_norm, m->bh, n, 8, 16,
+                            0)) ||
+          (rc = launch_rows(m, "pbx_dk_q4_i8x1b4r5_add", L.wd, m->bh, nullptr, m->bx, n, 5, 8, 0)))
+        return rc;
+      continue;
     }
     if ((rc = linear_rows(m, L.wo, m->battn, n, m->bx, true))) return rc;
     if ((rc = rmsnorm_rows(m, m->bx, L.ffn_norm, m->bxn, n))) return rc;
@@ -981,9 +1032,16 @@ extern "C" int pbx_model_forward_batch(pbx_model *m, const int32_t *tokens, int 
   const int n = n_tokens;
   if ((rc = ensure_batch(m, n, true))) return rc;
   if ((rc = batch_layers(m, tokens, n, start_pos))) return rc;
-  if ((rc = rmsnorm_rows(m, m->bx, m->out_norm, m->bxn, n))) return rc;
   const pbx_weight *head = m->output ? m->output : m->embd;
-  if ((rc = linear_rows(m, head, m->bxn, n, m->blogits, false))) return rc;
+  if (n <= ROWS_MAX && rows_int_ok(m)) {
+    // RMSNorm + LM head over the rows: a tile loop, one workgroup a CU
+    if ((rc = launch_rows(m, "pbx_dk_q4_i8x2b1r8l_lmh", head, m->bx, m->out_norm, m->blogits, n,
+                          8, 16, c->cu_count)))
+      return rc;
+  } else {
+    if ((rc = rmsnorm_rows(m, m->bx, m->out_norm, m->bxn, n))) return rc;
+    if ((rc = linear_rows(m, head, m->bxn, n, m->blogits, false))) return rc;
+  }
   {
     // P partial keys per row (<= 64, the bkeys row stride), ~2048 columns each
     const float *lg = m->blogits;

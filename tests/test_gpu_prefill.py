@@ -133,6 +133,36 @@ def test_llama1b_verify_rows_equal_sequential(ctx):
     model.free()
 
 
+@pytest.mark.parametrize("n", [1, 3, 6, 8])
+def test_llama1b_row_batched_gemvs(ctx, monkeypatch, n):
+    """Up to 8 rows through the row-batched integer-limb GEMVs (one pass over
+    the weights for all rows; 6..8 rows split 5 + rest for down) against the
+    same rows through the MFMA GEMM path (PBX_GEMV_INT=0) and against n
+    single-token forwards."""
+    print(f"[case] llama32_1b row-batched GEMVs, {n} rows", flush=True)
+    model = synth.build(ctx, "llama32_1b", 3300)
+    monkeypatch.setenv("PBX_GEMV_INT", "0")
+    ref = synth.build(ctx, "llama32_1b", 3300)
+    monkeypatch.delenv("PBX_GEMV_INT")
+    vocab = synth.CONFIGS["llama32_1b"]["vocab_size"]
+    prompt = [int(t) for t in synth.random_tokens(3301, 40, vocab)]
+    rows = [int(t) for t in synth.random_tokens(3302, n, vocab)]
+    model.forward(prompt, 0)
+    ref.forward(prompt, 0)
+    lb, nb = model.forward_batch(rows, 40)
+    lr, _ = ref.forward_batch(rows, 40)
+    ls = _sequential_logits(model, rows, 40)
+    e_gemm = float(np.abs(lb - lr).max())
+    e_seq = float(np.abs(lb - ls).max())
+    print(f"  vs GEMM path {e_gemm:.2e}, vs sequential {e_seq:.2e}")
+    assert e_gemm <= LOGIT_TOL and e_seq <= LOGIT_TOL
+    for t in range(n):
+        s = int(np.argmax(ls[t]))
+        assert nb[t] == s or top_gap(ls[t], s, nb[t]) < LOGIT_TOL
+    model.free()
+    ref.free()
+
+
 def test_llama1b_prefill_512_equals_sequential(ctx):
     """Batched prefill of a 512-token prompt (M = 512 through the MFMA GEMM)
     against the same prompt fed one decode step at a time."""
