@@ -760,7 +760,7 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) {
 // instruction's M < 4 rows).
 template <int TYPE, int WV, int RT, int IB, int PRO, int EPI, bool LOOP = false, int MR = 1>
 __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
-  static_assert(TYPE == PBX_Q4 || TYPE == PBX_Q8, "quantised weights only");
+  static_assert(TYPE == PBX_Q4 || TYPE == PBX_Q8 || TYPE == PBX_Q6K, "quantised weights only");
   static_assert(MR > 1 || IB <= WV, "one prologue wave per 64 blocks");
   static_assert(!LOOP || EPI == EPI_ARGMAX || EPI == EPI_STORE, "tile loop epilogues");
   static_assert(MR == 1 || EPI != EPI_ARGMAX, "argmax keys for one row");
@@ -770,8 +770,11 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   static_assert(IB * 64 * 32 <= PBX_INT_MAXK, "K limit");
   constexpr int PP = MR * IB;             // prologue slots: (row, 64-block group)
   constexpr int PS = (PP + WV - 1) / WV;  // slots a wave
-  __shared__ __attribute__((aligned(16))) int limb[MR][3][IB * 64 * 8];
-  __shared__ int bsum[MR][IB * 64];
+  // limb words 4q..4q+3 of block b at limb[m][L][q][b]: lane l's 16-byte
+  // reads of block l are contiguous across the wave (no bank conflicts)
+  __shared__ int4 limb[MR][3][2][IB * 64];
+  // exact sums of a block's x_q ([0]; Q6_K: its two 16-element halves)
+  __shared__ int bsum[MR][2][IB * 64];
   __shared__ float red[2][MR][IB];
   __shared__ float xscale[MR];
   __shared__ uint64_t kred[WV];
@@ -834,15 +837,18 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     for (int m = 0; m < MR; ++m)
       if (rr < RT && r0 + rr < N) res[m] = y[(size_t)(m < rows ? m : 0) * NO + r0 + rr];
   }
-  auto load_tile = [&](int t, unsigned (&db)[RT][IB], uint4 (&qq)[RT][IB][NV]) {
+  // Q6_K: db holds the super-block's d, ex the lane's two int8 sub-block
+  // scales (load_lane); both are used only in the dots.
+  auto load_tile = [&](int t, unsigned (&db)[RT][IB], uint4 (&qq)[RT][IB][NV],
+                       unsigned (&ex)[RT][IB]) {
     const int r0 = rbase(t);
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
       const int rw = row_ok(r0, i) ? tile_row(r0, i) : 0;
 #pragma unroll
       for (int j = 0; j < IB; ++j) {
-        const int b = lane + 64 * j;
-        db[i][j] = a.dsc[dsc_index(rw, b < B ? b : 0, B)];
+        const int b = lane + 64 * j, bb = b < B ? b : 0;
+        db[i][j] = a.dsc[TYPE == PBX_Q6K ? dsc_index(rw, bb >> 3, B >> 3) : dsc_index(rw, bb, B)];
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -852,13 +858,18 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
 #pragma unroll
       for (int j = 0; j < IB; ++j) {
         const int b = lane + 64 * j;
-        const uint8_t *src = a.qs + ((size_t)rw * B + (b < B ? b : 0)) * QB;
+        ex[i][j] = 0u;
+        if constexpr (TYPE == PBX_Q6K) {
+          load_lane<PBX_Q6K>(a.qs, rw, b, B, b < B, qq[i][j], ex[i][j]);
+        } else {
+          const uint8_t *src = a.qs + ((size_t)rw * B + (b < B ? b : 0)) * QB;
 #pragma unroll
-        for (int v = 0; v < NV; ++v) qq[i][j][v] = ld_stream(src + v * 16);
+          for (int v = 0; v < NV; ++v) qq[i][j][v] = ld_stream(src + v * 16);
+        }
       }
     }
   };
-  unsigned dbA[RT][IB], dbB[RT][IB];
+  unsigned dbA[RT][IB], dbB[RT][IB], exA[RT][IB], exB[RT][IB];
   uint4 qA[RT][IB][NV], qB[RT][IB][NV];
   // LOOP: the workgroup's tiles are blockIdx.x + k*G, k < TW.  Loads are
   // issued without branches (the second from a clamped index when TW = 1):
@@ -866,8 +877,8 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   // everything the branch may have issued.
   const int G = gridDim.x;
   const int TW = LOOP ? (n_tiles - (int)blockIdx.x + G - 1) / G : 1;
-  load_tile(blockIdx.x, dbA, qA);
-  if constexpr (LOOP) load_tile(blockIdx.x + (TW > 1 ? G : 0), dbB, qB);
+  load_tile(blockIdx.x, dbA, qA, exA);
+  if constexpr (LOOP) load_tile(blockIdx.x + (TW > 1 ? G : 0), dbB, qB, exB);
   __builtin_amdgcn_sched_barrier(0);
 
   // 3. Prologue slots: sum of squares (RMSNorm) and max |x * w| of their
@@ -929,7 +940,8 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
       if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
       const float c = inv * ldexpf(1.f, 22 - e);
       if (pb < B) {
-        int bs = 0;
+        int bs = 0, bs_lo = 0;  // block sum; sum of elements 0..15
+        int lw[3][8];
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
           const float4 t = xv[sl][v], w = nv[sl][v];
@@ -947,11 +959,18 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
             l2 |= (unsigned)(x2 & 0xFF) << (8 * k);
             bs += xq[k];
           }
-          limb[pm][0][pb * 8 + v] = (int)l0;
-          limb[pm][1][pb * 8 + v] = (int)l1;
-          limb[pm][2][pb * 8 + v] = (int)l2;
+          lw[0][v] = (int)l0;
+          lw[1][v] = (int)l1;
+          lw[2][v] = (int)l2;
+          if (v == 3) bs_lo = bs;
         }
-        bsum[pm][pb] = bs;
+#pragma unroll
+        for (int L = 0; L < 3; ++L) {
+          limb[pm][L][0][pb] = make_int4(lw[L][0], lw[L][1], lw[L][2], lw[L][3]);
+          limb[pm][L][1][pb] = make_int4(lw[L][4], lw[L][5], lw[L][6], lw[L][7]);
+        }
+        bsum[pm][0][pb] = TYPE == PBX_Q6K ? bs_lo : bs;
+        bsum[pm][1][pb] = bs - bs_lo;
       }
       if (p % IB == 0 && lane == 0) xscale[pm] = ldexpf(1.f, e - 22);
     }
@@ -961,7 +980,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   // 5. Dot products as the weight rows arrive; each row's sum after the
   //    transposed reduction, per activation row.
   auto dots = [&](const unsigned (&db)[RT][IB], const uint4 (&qq)[RT][IB][NV],
-                  float (&tot)[MR]) {
+                  const unsigned (&ex)[RT][IB], float (&tot)[MR]) {
     float acc[MR][RT];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
@@ -978,12 +997,12 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
         int xl[3][8];
 #pragma unroll
         for (int L = 0; L < 3; ++L) {
-          const int4 t0 = *reinterpret_cast<const int4 *>(&limb[m][L][bl * 8]);
-          const int4 t1 = *reinterpret_cast<const int4 *>(&limb[m][L][bl * 8 + 4]);
+          const int4 t0 = limb[m][L][0][bl];
+          const int4 t1 = limb[m][L][1][bl];
           xl[L][0] = t0.x; xl[L][1] = t0.y; xl[L][2] = t0.z; xl[L][3] = t0.w;
           xl[L][4] = t1.x; xl[L][5] = t1.y; xl[L][6] = t1.z; xl[L][7] = t1.w;
         }
-        const float corr = TYPE == PBX_Q4 ? 8.f * (float)bsum[m][bl] : 0.f;
+        const float corr = TYPE == PBX_Q4 ? 8.f * (float)bsum[m][0][bl] : 0.f;
 #pragma unroll
         for (int i = 0; i < RT; ++i) {
           int s0 = 0, s1 = 0, s2 = 0;
@@ -998,6 +1017,34 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
               s1 = sdot4(lo, xl[1][k], s1); s1 = sdot4(hi, xl[1][4 + k], s1);
               s2 = sdot4(lo, xl[2][k], s2); s2 = sdot4(hi, xl[2][4 + k], s2);
             }
+          } else if constexpr (TYPE == PBX_Q6K) {
+            // 6-bit codes of elements 4k..4k+3: low nibbles of the lane's ql
+            // bytes (high nibbles for groups 2, 3) | 2-bit qh fields << 4;
+            // the two 16-element halves carry their own int8 scales
+            const unsigned shl = 4 * ((b & 3) >> 1), shh = 2 * (b & 3);
+            const unsigned wl[8] = {qq[i][j][0].x, qq[i][j][0].y, qq[i][j][0].z, qq[i][j][0].w,
+                                    qq[i][j][1].x, qq[i][j][1].y, qq[i][j][1].z, qq[i][j][1].w};
+            const unsigned wh[8] = {qq[i][j][2].x, qq[i][j][2].y, qq[i][j][2].z, qq[i][j][2].w,
+                                    qq[i][j][3].x, qq[i][j][3].y, qq[i][j][3].z, qq[i][j][3].w};
+            int h0 = 0, h1 = 0, h2 = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const int c = (int)(((wl[k] >> shl) & 0x0F0F0F0Fu) | (((wh[k] >> shh) & 0x03030303u) << 4));
+              if (k < 4) {
+                s0 = sdot4(c, xl[0][k], s0); s1 = sdot4(c, xl[1][k], s1); s2 = sdot4(c, xl[2][k], s2);
+              } else {
+                h0 = sdot4(c, xl[0][k], h0); h1 = sdot4(c, xl[1][k], h1); h2 = sdot4(c, xl[2][k], h2);
+              }
+            }
+            const float flo = fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0)) -
+                              32.f * (float)bsum[m][0][bl];
+            const float fhi = fmaf((float)h2, 65536.f, fmaf((float)h1, 256.f, (float)h0)) -
+                              32.f * (float)bsum[m][1][bl];
+            const float sc0 = (float)(int8_t)(ex[i][j] & 0xFFu);
+            const float sc1 = (float)(int8_t)((ex[i][j] >> 8) & 0xFFu);
+            acc[m][i] = fmaf(fmaf(sc0, flo, sc1 * fhi), f16_bits_to_f32(db[i][j] & bmask),
+                             acc[m][i]);
+            continue;
           } else {
             const unsigned w[8] = {qq[i][j][0].x, qq[i][j][0].y, qq[i][j][0].z, qq[i][j][0].w,
                                    qq[i][j][1].x, qq[i][j][1].y, qq[i][j][1].z, qq[i][j][1].w};
@@ -1038,22 +1085,22 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     float tt[MR];
     int k = 0;
     for (; k + 3 < TW; k += 2) {
-      dots(dbA, qA, tt);
-      load_tile(blockIdx.x + (k + 2) * G, dbA, qA);
+      dots(dbA, qA, exA, tt);
+      load_tile(blockIdx.x + (k + 2) * G, dbA, qA, exA);
       consume(k, tt);
-      dots(dbB, qB, tt);
-      load_tile(blockIdx.x + (k + 3) * G, dbB, qB);
+      dots(dbB, qB, exB, tt);
+      load_tile(blockIdx.x + (k + 3) * G, dbB, qB, exB);
       consume(k + 1, tt);
     }
-    dots(dbA, qA, tt);
-    if (k + 2 < TW) load_tile(blockIdx.x + (k + 2) * G, dbA, qA);
+    dots(dbA, qA, exA, tt);
+    if (k + 2 < TW) load_tile(blockIdx.x + (k + 2) * G, dbA, qA, exA);
     consume(k, tt);
     if (k + 1 < TW) {
-      dots(dbB, qB, tt);
+      dots(dbB, qB, exB, tt);
       consume(k + 1, tt);
     }
     if (k + 2 < TW) {
-      dots(dbA, qA, tt);
+      dots(dbA, qA, exA, tt);
       consume(k + 2, tt);
     }
     if constexpr (EPI != EPI_ARGMAX) return;
@@ -1070,7 +1117,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   }
 
   float tot[MR];
-  dots(dbA, qA, tot);
+  dots(dbA, qA, exA, tot);
   const int r0 = rbase(blockIdx.x);
   if constexpr (PAIR) {
 #pragma unroll

@@ -196,10 +196,17 @@ static bool int_override(const char *role, int *wv, int *rt, bool *loop) {
 
 static bool int_shape(bool enabled, const char *mode, const char *role, int type, int N, int B,
                       int *wv, int *rt, int *ib, bool *loop) {
-  if (!enabled || (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0) || B < 64 || B > 256)
-    return false;
+  if (!enabled || B < 64 || B > 256) return false;
   *ib = (B + 63) / 64;
   *loop = false;
+  if (type == PBX_TYPE_Q6_K) {  // the lm head at K = 2048: 4 waves x 4 rows, tile loop
+    if (strcmp(mode, "lmh") != 0 || B != 64) return false;
+    *wv = 4;
+    *rt = 4;
+    *loop = true;
+    return true;
+  }
+  if (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0) return false;
   if (int_override(role, wv, rt, loop)) return *ib <= *wv;
   if (strcmp(mode, "gu") == 0) {
     if (B > 128) return false;
@@ -240,7 +247,9 @@ static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, const char *rol
     const int tiles = (N + wv * rt - 1) / (wv * rt);
     // tile loop: two workgroups per CU (four for 4-row waves), each taking
     // every G-th tile
-    *grid = dim3(loop ? std::min(tiles, (rt <= 4 ? 4 : 2) * c->cu_count) : tiles);
+    // (Q6_K: one, its two tile buffers fill the registers)
+    const int per_cu = type == PBX_TYPE_Q6_K ? 1 : rt <= 4 ? 4 : 2;
+    *grid = dim3(loop ? std::min(tiles, per_cu * c->cu_count) : tiles);
     *block = dim3(64 * wv);
     *n_tiles = (int)grid->x;
     return;

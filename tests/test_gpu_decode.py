@@ -178,20 +178,22 @@ def test_attention_kernels_match_one_workgroup_per_head(ctx, monkeypatch, mode, 
     ref.close()
 
 
-@pytest.mark.parametrize("wt,dim,hidden,vocab", [(TYPE_Q4_0, 2048, 1024, 40000),
-                                                 (TYPE_Q8_0, 2048, 1024, 512),
-                                                 (TYPE_Q4_0, 4096, 8192, 512),
-                                                 (TYPE_Q8_0, 4096, 4096, 512)])
-def test_integer_limb_kernels_match_float_kernels(ctx, monkeypatch, wt, dim, hidden, vocab):
+@pytest.mark.parametrize("wt,et,dim,hidden,vocab", [(TYPE_Q4_0, TYPE_Q4_0, 2048, 1024, 40000),
+                                                    (TYPE_Q4_0, TYPE_Q6_K, 2048, 1024, 40000),
+                                                    (TYPE_Q8_0, TYPE_Q8_0, 2048, 1024, 512),
+                                                    (TYPE_Q4_0, TYPE_Q4_0, 4096, 8192, 512),
+                                                    (TYPE_Q8_0, TYPE_Q8_0, 4096, 4096, 512)])
+def test_integer_limb_kernels_match_float_kernels(ctx, monkeypatch, wt, et, dim, hidden, vocab):
     """The GEMVs on integer limbs (v_dot4 over a fixed-point activation)
     against the float-unpack kernels and the oracle: gate|up for Q4_0 and
     Q8_0, and for Q4_0 also qkv, o, down and the lm head (K = 2048: a loop
-    over 1250 row tiles in 512 workgroups), with one, two and four 64-block
-    groups per lane (K = 2048, 4096, 8192)."""
-    print(f"[case] integer-limb vs float kernels, type {wt}, dim {dim}, hidden {hidden}, "
-          f"vocab {vocab}", flush=True)
+    over 1250 row tiles in 512 workgroups; a Q6_K tied head on its own
+    loop), with one, two and four 64-block groups per lane (K = 2048, 4096,
+    8192)."""
+    print(f"[case] integer-limb vs float kernels, type {wt}, embed {et}, dim {dim}, "
+          f"hidden {hidden}, vocab {vocab}", flush=True)
     heads = dim // 128
-    cfg = tiny(wt, wt, dim=dim, hidden_dim=hidden, n_layers=1, n_heads=heads,
+    cfg = tiny(wt, et, dim=dim, hidden_dim=hidden, n_layers=1, n_heads=heads,
                n_kv_heads=heads // 4, vocab_size=vocab, max_seq=64)
     fast, ref, cfg = make_pair(ctx, cfg, 99)
     monkeypatch.setenv("PBX_GEMV_INT", "0")
