@@ -103,7 +103,7 @@ DK_INT_LMH(PBX_Q4, q4, 4, 8, 1)
 DK_INT_LMHL(PBX_Q4, q4, 4, 8, 1)
 DK_INT_LMHL(PBX_Q4, q4, 4, 4, 1)
 // Q6_K lm head (the output matrix of llama.cpp Q4_0 files), K = 2048
-DK_INT_LMHL(PBX_Q6K, q6k, 4, 4, 1)
+DK_INT_LMHL(PBX_Q6K, q6k, 4, 2, 1)
 
 // Row-batched integer-limb GEMVs: up to MR activation rows against one pass
 // over the weights (speculative verify, prompts of 4..MR tokens), args.rows

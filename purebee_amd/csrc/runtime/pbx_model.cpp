@@ -199,10 +199,10 @@ static bool int_shape(bool enabled, const char *mode, const char *role, int type
   if (!enabled || B < 64 || B > 256) return false;
   *ib = (B + 63) / 64;
   *loop = false;
-  if (type == PBX_TYPE_Q6_K) {  // the lm head at K = 2048: 4 waves x 4 rows, tile loop
+  if (type == PBX_TYPE_Q6_K) {  // the lm head at K = 2048: 4 waves x 2 rows, tile loop
     if (strcmp(mode, "lmh") != 0 || B != 64) return false;
     *wv = 4;
-    *rt = 4;
+    *rt = 2;
     *loop = true;
     return true;
   }
@@ -247,8 +247,8 @@ static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, const char *rol
     const int tiles = (N + wv * rt - 1) / (wv * rt);
     // tile loop: two workgroups per CU (four for 4-row waves), each taking
     // every G-th tile
-    // (Q6_K: one, its two tile buffers fill the registers)
-    const int per_cu = type == PBX_TYPE_Q6_K ? 1 : rt <= 4 ? 4 : 2;
+    // (Q6_K: two, its tile buffers are 64-byte lane blocks)
+    const int per_cu = type == PBX_TYPE_Q6_K ? 2 : rt <= 4 ? 4 : 2;
     *grid = dim3(loop ? std::min(tiles, per_cu * c->cu_count) : tiles);
     *block = dim3(64 * wv);
     *n_tiles = (int)grid->x;
