@@ -270,7 +270,8 @@ GEMM_KERNEL(pbx_gemm_f16_m1_n4, PBX_F16, 1, 4)
 GEMM_KERNEL(pbx_gemm_f16_m2_n2, PBX_F16, 2, 2)
 
 // ---------------------------------------------------------------------------
-// Large-M kernel (M > 32): workgroup tile 128 (M) x 128 (N), four waves in
+// Large-M kernel for Q8_0, Q4_1 and F16 (M > 32; Q4_0 has its own below):
+// workgroup tile 128 (M) x 128 (N), four waves in
 // a 2 x 2 arrangement, each wave 64 x 64 (4 x 4 MFMA tiles).  The activation
 // tile of a block (128 rows x 32 k, hi and lo, 16 KB) is loaded once per
 // workgroup into LDS (double buffered: block b+1 is read from global while
@@ -404,47 +405,272 @@ __device__ __forceinline__ void gemm_big(const GemmArgs &a) {
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_big(GemmArgs a) { gemm_big<PBX_Q4, 2>(a); }
 extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q8_big(GemmArgs a) { gemm_big<PBX_Q8, 2>(a); }
 extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q41_big(GemmArgs a) { gemm_big<PBX_Q41, 2>(a); }
 extern "C" __global__ void __launch_bounds__(256) pbx_gemm_f16_big(GemmArgs a) { gemm_big<PBX_F16, 2>(a); }
 
+// ---------------------------------------------------------------------------
+// Q4_0 large-M kernel (M > 32): 32x32x16 MFMAs with every operand moved to
+// LDS by DMA.  Operand lane layout of v_mfma_f32_32x32x16_f16 (checked on
+// the device): A: lane l holds A[l%32][8*(l/32) + e]; B: lane l holds
+// B[8*(l/32) + e][l%32]; D: lane l, register r holds
+// D[8*(r/4) + 4*(l/32) + r%4][l%32].  A 32-wide block is two MFMAs per
+// operand: j = 0 takes k = 8h + e and j = 1 takes k = 16 + 8h + e
+// (h = l/32), which are the low and high nibbles of the Q4_0 bytes 8h..8h+7:
+// a lane reads its 8 code bytes once.  Each lane's 16 outputs share one
+// column (weight row), so the block scale is one value per lane.
+// Workgroup tile 128 (M) x 128 (N), four waves in 2 x 2, wave tile 64 x 64
+// (2 x 2 MFMA tiles).  A ring of NS LDS stages, each [hi/lo][128 rows][4
+// chunks of 8 halves] of activations, the 128 weight rows' 16 code bytes and
+// their 128 scales.  Per block every wave issues exactly five DMA
+// instructions (global_load_lds: lane i's bytes land at the instruction's LDS
+// base + size * i): four activation chunks, and the codes of 64 rows (waves
+// 0, 1) or the scales (waves 2, 3, the same bytes), so one wait count fits
+// every wave; the loads are issued from inline assembly with SGPR bases, so
+// the compiler adds no waits of its own, and no register load is in flight
+// across the block loop.  The chunks of activation row r are stored in the
+// order q ^ swz(r), swz(r) = ((r >> 1) ^ (r >> 3)) & 3: the 16-byte reads of
+// 16 consecutive rows at one chunk fall in 16 distinct bank groups.  The
+// loop is unrolled by NS so every LDS offset is an immediate.
+// Needs X16 / X16lo padded to a multiple of 128 rows.
+// ---------------------------------------------------------------------------
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ int a_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// LDS DMA with a uniform 64-bit base in SGPRs and a per-lane 32-bit offset
+// (the saddr form): lane i's SIZE bytes from base + voff land at LDS byte
+// address m0 + SIZE * i.  m0 must be wave-uniform.
+template <int SIZE>
+__device__ __forceinline__ void dma_to_lds_s(const void *base, unsigned voff, unsigned m0) {
+  if constexpr (SIZE == 16)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 ::"v"(voff), "s"(base), "s"(m0));
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+                 ::"v"(voff), "s"(base), "s"(m0));
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int NS>
+__device__ __forceinline__ void gemm_q4_dma(const GemmArgs &a) {
+  constexpr int ASTAGE = 2 * 128 * 32 * 2;            // bytes
+  constexpr int STAGE = ASTAGE + 128 * 16 + 128 * 2;  // bytes
+  __shared__ __attribute__((aligned(1024))) uint8_t S[NS * STAGE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR bases
+  const int lr = lane & 31, h = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n0 = blockIdx.x * 128 + wn * 64;
+  const int mblk = blockIdx.y * 128;
+  const int m0 = wm * 64;
+  const int K = a.B * 32;
+  const int per = (a.B + a.KS - 1) / a.KS;
+  const int b0 = blockIdx.z * per;
+  const int b1 = min(a.B, b0 + per);
+  const floatx16 zero16 = {};
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) acc[t][u] = zero16;
+
+  if (b0 < b1) {
+    // activation DMA i (i = 0..3) of this wave: plane i >> 1, LDS chunks
+    // (4 i + wave) * 64 + lane; per-lane byte offset from the plane's tile base
+    unsigned avoff[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = (4 * i + wave) * 64 + lane;  // plane 0 chunk (same offsets in plane 1)
+      const int r = (c & 511) >> 2, q = (c & 3) ^ a_swz(r);
+      avoff[i] = (unsigned)((r * K + q * 8) * 2);
+    }
+    const uint8_t *xhi = reinterpret_cast<const uint8_t *>(a.X16 + (size_t)mblk * K);
+    const uint8_t *xlo = reinterpret_cast<const uint8_t *>(a.X16lo + (size_t)mblk * K);
+    // weight DMA: waves 0, 1 the codes of 64 rows each; waves 2, 3 the scales
+    const bool codes = wave < 2;
+    const uint8_t *wbase;
+    unsigned wvoff;
+    // (bases at the workgroup's first row, so the per-lane offsets stay small)
+    if (codes) {
+      const int n = min(blockIdx.x * 128 + wave * 64 + lane, a.Npad - 1) - blockIdx.x * 128;
+      wbase = a.qs + (size_t)blockIdx.x * 128 * a.B * 16;
+      wvoff = (unsigned)(n * a.B * 16);
+    } else {
+      const int g = min(blockIdx.x * 32 + (lane >> 1), a.Npad / 4 - 1) - blockIdx.x * 32;
+      wbase = reinterpret_cast<const uint8_t *>(a.dsc) + (size_t)blockIdx.x * 32 * a.B * 8;
+      wvoff = (unsigned)(g * a.B * 8 + (lane & 1) * 4);
+    }
+    const unsigned lds0 = __builtin_amdgcn_readfirstlane(lds_addr(&S[0]) + wave * 1024);
+    const unsigned ldsw = __builtin_amdgcn_readfirstlane(
+        lds_addr(&S[0]) + ASTAGE + (codes ? wave * 1024 : 2048));
+    auto dma = [&](int b, int stage) {
+      const unsigned so = stage * STAGE;
+      dma_to_lds_s<16>(xhi + b * 64, avoff[0], lds0 + so);
+      dma_to_lds_s<16>(xhi + b * 64, avoff[1], lds0 + so + 4096);
+      dma_to_lds_s<16>(xlo + b * 64, avoff[0], lds0 + so + 8192);
+      dma_to_lds_s<16>(xlo + b * 64, avoff[1], lds0 + so + 12288);
+      if (codes)
+        dma_to_lds_s<16>(wbase + (size_t)b * 16, wvoff, ldsw + so);
+      else
+        dma_to_lds_s<4>(wbase + (size_t)b * 8, wvoff, ldsw + so);
+    };
+    // this lane's read offsets in a stage
+    const uint8_t *rbase = &S[0];
+    int aoff[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = m0 + 32 * t + lr;
+        aoff[t][j] = (r * 32 + (((2 * j + h) ^ a_swz(r)) * 8)) * 2;
+      }
+    int wofs[2], sofs[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int nl = wn * 64 + 32 * u + lr;
+      wofs[u] = ASTAGE + nl * 16 + 8 * h;
+      sofs[u] = ASTAGE + 128 * 16 + nl * 2;
+    }
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) dma(min(b0 + s, b1 - 1), s);
+
+    for (int kb = b0; kb < b1; kb += NS) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int b = kb + s;
+        if (b >= b1) break;
+        wait_vm<(NS - 2) * 5>();
+        lds_barrier();
+        dma(min(b + NS - 1, b1 - 1), s == 0 ? NS - 1 : s - 1);
+        const uint8_t *sb = rbase + s * STAGE;
+        half8 B0[2], B1[2];
+        float d[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const uint2 raw = *reinterpret_cast<const uint2 *>(sb + wofs[u]);
+          B0[u] = codes_operand<PBX_Q4>(raw, 0);
+          B1[u] = codes_operand<PBX_Q4>(raw, 2);
+          d[u] = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(sb + sofs[u]));
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const half8 Ah0 = *reinterpret_cast<const half8 *>(sb + aoff[t][0]);
+          const half8 Ah1 = *reinterpret_cast<const half8 *>(sb + aoff[t][1]);
+          const half8 Al0 = *reinterpret_cast<const half8 *>(sb + 128 * 64 + aoff[t][0]);
+          const half8 Al1 = *reinterpret_cast<const half8 *>(sb + 128 * 64 + aoff[t][1]);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            floatx16 blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah0, B0[u], zero16, 0, 0, 0);
+            blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al0, B0[u], blk, 0, 0, 0);
+            blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah1, B1[u], blk, 0, 0, 0);
+            blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al1, B1[u], blk, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[t][u][r] = fmaf(blk[r], d[u], acc[t][u][r]);
+          }
+        }
+      }
+    }
+    wait_vm<0>();
+  }
+
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int n = n0 + 32 * u + lr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = mblk + m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (m < a.M && n < a.N) {
+          const float v = acc[t][u][r] * a.inv[m];
+          if (a.KS == 1) {
+            float *y = a.Y + (size_t)m * a.N + n;
+            if (a.accumulate)
+              *y += v;
+            else
+              *y = v + (a.bias ? a.bias[n] : 0.f);
+          } else {
+            a.Y[((size_t)blockIdx.z * a.M + m) * a.N + n] = v;
+          }
+        }
+      }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_big(GemmArgs a) { gemm_q4_dma<3>(a); }
+
 // Row scaling to fp16: one workgroup per (padded) row.  The scale is
 // 2^(15 - e) with 2^(e-1) <= max|x| < 2^e, so every scaled value is below
 // 2^15 in magnitude (fp16 max 65504); padding rows are zero.  X16lo gets
-// the residual x*scale - X16 rounded to fp16.
+// the residual x*scale - X16 rounded to fp16.  K <= PREP_KREG: each thread
+// keeps its float4s in registers, so the row is read once; longer rows read
+// it twice.
+#define PREP_KREG 8192
 extern "C" __global__ void __launch_bounds__(256)
 pbx_gemm_prep_x(const float *X, _Float16 *X16, _Float16 *X16lo, float *inv, int M, int K) {
   __shared__ float red[4];
-  const int m = blockIdx.x;
+  const int m = blockIdx.x, tid = threadIdx.x;
   _Float16 *dst = X16 + (size_t)m * K;
   _Float16 *lo = X16lo + (size_t)m * K;
+  const int K4 = K / 4;  // K is a multiple of 32
+  typedef _Float16 half4v __attribute__((ext_vector_type(4)));
   if (m >= M) {
-    for (int k = threadIdx.x; k < K; k += blockDim.x) {
-      dst[k] = (_Float16)0.f;
-      lo[k] = (_Float16)0.f;
+    const half4v z = {};
+    for (int k = tid; k < K4; k += 256) {
+      reinterpret_cast<half4v *>(dst)[k] = z;
+      reinterpret_cast<half4v *>(lo)[k] = z;
     }
-    if (threadIdx.x == 0) inv[m] = 0.f;
+    if (tid == 0) inv[m] = 0.f;
     return;
   }
-  const float *src = X + (size_t)m * K;
+  const float4 *src = reinterpret_cast<const float4 *>(X + (size_t)m * K);
+  constexpr int R = PREP_KREG / 1024;  // float4s per thread held in registers
+  float4 v[R];
   float mx = 0.f;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) mx = fmaxf(mx, fabsf(src[k]));
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  for (int i = 0; i < R; ++i) {
+    const int k = tid + 256 * i;
+    v[i] = k < K4 ? src[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+  }
+  for (int k = tid + 256 * R; k < K4; k += 256) {
+    const float4 t = src[k];
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
+  }
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   int e = 0;
   if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
   const float scale = mx > 0.f ? ldexpf(1.f, 15 - e) : 1.f;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) {
-    const float v = src[k] * scale;  // exact: scale is a power of two
-    const _Float16 h = (_Float16)v;
-    dst[k] = h;
-    lo[k] = (_Float16)(v - (float)h);
+  auto put = [&](int k, float4 t) {
+    // exact: scale is a power of two
+    const float a0 = t.x * scale, a1 = t.y * scale, a2 = t.z * scale, a3 = t.w * scale;
+    const half4v hv = {(_Float16)a0, (_Float16)a1, (_Float16)a2, (_Float16)a3};
+    const half4v lv = {(_Float16)(a0 - (float)hv[0]), (_Float16)(a1 - (float)hv[1]),
+                       (_Float16)(a2 - (float)hv[2]), (_Float16)(a3 - (float)hv[3])};
+    reinterpret_cast<half4v *>(dst)[k] = hv;
+    reinterpret_cast<half4v *>(lo)[k] = lv;
+  };
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int k = tid + 256 * i;
+    if (k < K4) put(k, v[i]);
   }
-  if (threadIdx.x == 0) inv[m] = mx > 0.f ? ldexpf(1.f, e - 15) : 1.f;
+  for (int k = tid + 256 * R; k < K4; k += 256) put(k, src[k]);
+  if (tid == 0) inv[m] = mx > 0.f ? ldexpf(1.f, e - 15) : 1.f;
 }
 
 // Sum of the split-K partials (+ bias, or accumulated into Y).
