@@ -286,6 +286,217 @@ pbx_attention_tiled(const float *qkv, const float *kcache, const float *vcache, 
   }
 }
 
+// Causal attention on 32x32x16 MFMAs for head_dim 16..64 (a multiple of 16),
+// the computation of pbx_attention_tiled.  Operand layout of
+// v_mfma_f32_32x32x16_f16: A: lane l holds A[l%32][8*(l/32) + e]; B: lane l
+// holds B[8*(l/32) + e][l%32]; D: lane l, register r holds
+// D[8*(r/4) + 4*(l/32) + r%4][l%32].  fp32 values enter as fp16 pairs
+// hi = fp16(x), lo = fp16(x - hi), and a product of two such values is taken
+// as hi*hi + hi*lo + lo*hi (three MFMAs; ~22 significant bits, the lo*lo term
+// is below fp32 rounding of the sum).
+// Workgroup: 64 query rows of one head, four waves; wave (qg, kh) holds the
+// 32 queries qg and, of every 64-key stage in LDS, the 32 keys kh.  Scores
+// are computed transposed, S^T = K . Q^T (A = keys x dims from LDS, B = the
+// wave's queries' dims, kept in registers), so each lane owns one query:
+// the softmax max and sum run over the lane's 16 registers and one exchange
+// with lane l ^ 32.  The lane's probabilities are then exactly the B operand
+// of O^T = V^T . P^T for 16 keys when the keys of a 16-key chunk are taken
+// in the order {0-3, 8-11} (h = 0) and {4-7, 12-15} (h = 1), which V^T
+// (stored [dim][key] in LDS) follows.  The two key halves of a query group
+// merge their running max, sum and output through LDS at the end.
+#define FA_KT 64           // keys per LDS stage
+#define FA_KP (64 + 8)     // halves per K row (dims) and per V^T row (keys)
+
+// hi = fp16(x), lo = fp16(x - hi), assigned to H and L (vector elements allowed)
+#define SPLIT_F16(x, H, L)                       \
+  do {                                           \
+    const float x_ = (x);                        \
+    const _Float16 h_ = (_Float16)x_;            \
+    (H) = h_;                                    \
+    (L) = (_Float16)(x_ - (float)h_);            \
+  } while (0)
+
+extern "C" __global__ void __launch_bounds__(256)
+pbx_attention_mfma(const float *qkv, const float *kcache, const float *vcache, float *out,
+                   int start, int n_rows, int n_heads, int n_kv_heads, int head_dim,
+                   float scale) {
+  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 half2t __attribute__((ext_vector_type(2)));
+  typedef _Float16 half4t __attribute__((ext_vector_type(4)));
+  typedef float floatx16 __attribute__((ext_vector_type(16)));
+  __shared__ __attribute__((aligned(16))) _Float16 Kh[FA_KT * FA_KP], Kl[FA_KT * FA_KP];
+  __shared__ __attribute__((aligned(16))) _Float16 Vh[64 * FA_KP], Vl[64 * FA_KP];  // [dim][key]
+  const int h = blockIdx.x, t0 = blockIdx.y * 64, hd = head_dim, hd4 = hd / 4, nc = hd / 16;
+  const int group = n_heads / n_kv_heads, kvh = h / group;
+  const int dim = n_heads * hd, kvdim = n_kv_heads * hd, rs = dim + 2 * kvdim;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qg = wave & 1, kh = wave >> 1, lq = lane & 31, hh = lane >> 5;
+  const int nq = min(64, n_rows - t0);
+  const int qrow = 32 * qg + lq;  // this lane's query within the tile
+  const int qpos = start + t0 + qrow;
+  const floatx16 zero16 = {};
+
+  // the lane's query dims 16c + 8hh .. +7 (scaled), as hi / lo B operands
+  half8 Qh[4], Ql[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    if (c < nc) {
+      float qv[8];
+      if (qrow < nq) {
+        const float *q = qkv + (size_t)(t0 + qrow) * rs + (size_t)h * hd + 16 * c + 8 * hh;
+        const float4 a = *reinterpret_cast<const float4 *>(q);
+        const float4 b = *reinterpret_cast<const float4 *>(q + 4);
+        qv[0] = a.x; qv[1] = a.y; qv[2] = a.z; qv[3] = a.w;
+        qv[4] = b.x; qv[5] = b.y; qv[6] = b.z; qv[7] = b.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) SPLIT_F16(qv[e] * scale, Qh[c][e], Ql[c][e]);
+    }
+  }
+
+  float m_run = -INFINITY, l_run = 0.f;
+  floatx16 acc[2] = {zero16, zero16};  // O^T, dims 32 dt + 8 (r/4) + 4 hh + r%4
+  const int last_key = start + t0 + nq - 1;
+  const float *kb = kcache + (size_t)kvh * hd, *vb = vcache + (size_t)kvh * hd;
+  for (int k0 = 0; k0 <= last_key; k0 += FA_KT) {
+    const int nk = min(FA_KT, last_key + 1 - k0);
+    __syncthreads();  // the previous stage's reads are done
+    for (int i = tid; i < FA_KT * hd4; i += 256) {
+      const int key = i / hd4, c4 = 4 * (i % hd4);
+      const float4 v = key < nk ? *reinterpret_cast<const float4 *>(kb + (size_t)(k0 + key) * kvdim + c4)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+      half4t hv, lv;
+      SPLIT_F16(v.x, hv[0], lv[0]);
+      SPLIT_F16(v.y, hv[1], lv[1]);
+      SPLIT_F16(v.z, hv[2], lv[2]);
+      SPLIT_F16(v.w, hv[3], lv[3]);
+      *reinterpret_cast<half4t *>(&Kh[key * FA_KP + c4]) = hv;
+      *reinterpret_cast<half4t *>(&Kl[key * FA_KP + c4]) = lv;
+    }
+    for (int i = tid; i < (FA_KT / 2) * hd4; i += 256) {
+      const int kp = 2 * (i / hd4), c4 = 4 * (i % hd4);
+      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 v0 = kp < nk ? *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + kp) * kvdim + c4) : z;
+      const float4 v1 = kp + 1 < nk ? *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + kp + 1) * kvdim + c4) : z;
+#define FA_PUTV(e, x0, x1)                                                  \
+  do {                                                                      \
+    half2t hv_, lv_;                                                        \
+    SPLIT_F16(x0, hv_[0], lv_[0]);                                          \
+    SPLIT_F16(x1, hv_[1], lv_[1]);                                          \
+    *reinterpret_cast<half2t *>(&Vh[(c4 + (e)) * FA_KP + kp]) = hv_;        \
+    *reinterpret_cast<half2t *>(&Vl[(c4 + (e)) * FA_KP + kp]) = lv_;        \
+  } while (0)
+      FA_PUTV(0, v0.x, v1.x);
+      FA_PUTV(1, v0.y, v1.y);
+      FA_PUTV(2, v0.z, v1.z);
+      FA_PUTV(3, v0.w, v1.w);
+#undef FA_PUTV
+    }
+    __syncthreads();
+
+    // S^T for this wave's 32 keys (rows) x 32 queries (columns)
+    const int kr = 32 * kh + lq;  // A row: key kr of the stage
+    floatx16 s = zero16;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c < nc) {
+        const half8 ah = *reinterpret_cast<const half8 *>(&Kh[kr * FA_KP + 16 * c + 8 * hh]);
+        const half8 al = *reinterpret_cast<const half8 *>(&Kl[kr * FA_KP + 16 * c + 8 * hh]);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, Qh[c], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, Ql[c], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, Qh[c], s, 0, 0, 0);
+      }
+    }
+    // mask, online softmax for the lane's query over its 16 keys and lane ^ 32's
+    float mt = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kpos = k0 + 32 * kh + 8 * (r >> 2) + 4 * hh + (r & 3);
+      if (kpos > qpos || kpos > last_key) s[r] = -INFINITY;
+      mt = fmaxf(mt, s[r]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m_run, mt);
+    const float f = mn == -INFINITY ? 1.f : expf(m_run - mn);
+    float ps = 0.f;
+    half8 Ph[2], Pl[2];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float pr = mn == -INFINITY ? 0.f : expf(s[r] - mn);
+      ps += pr;
+      SPLIT_F16(pr, Ph[r >> 3][r & 7], Pl[r >> 3][r & 7]);
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    l_run = fmaf(l_run, f, ps);
+    m_run = mn;
+    // O^T += V^T . P^T over the 32 keys (two chunks of 16)
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      if (32 * dt < hd) {
+        acc[dt] *= f;
+        const int vr = (32 * dt + lq) * FA_KP + 32 * kh + 4 * hh;  // V^T row (dim), key base
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          half8 ah, al;
+          const half4t h0 = *reinterpret_cast<const half4t *>(&Vh[vr + 16 * cc]);
+          const half4t h1 = *reinterpret_cast<const half4t *>(&Vh[vr + 16 * cc + 8]);
+          const half4t l0 = *reinterpret_cast<const half4t *>(&Vl[vr + 16 * cc]);
+          const half4t l1 = *reinterpret_cast<const half4t *>(&Vl[vr + 16 * cc + 8]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            ah[e] = h0[e]; ah[4 + e] = h1[e];
+            al[e] = l0[e]; al[4 + e] = l1[e];
+          }
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, Ph[cc], acc[dt], 0, 0, 0);
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, Pl[cc], acc[dt], 0, 0, 0);
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, Ph[cc], acc[dt], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // merge the two key halves of each query group: kh = 1 hands over through LDS
+  __syncthreads();
+  float *mg = reinterpret_cast<float *>(Kh);  // [qg][lane][34]: acc (32), m, l
+  float *mine = mg + (qg * 64 + lane) * 34;
+  if (kh == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      mine[r] = acc[0][r];
+      mine[16 + r] = acc[1][r];
+    }
+    mine[32] = m_run;
+    mine[33] = l_run;
+  }
+  __syncthreads();
+  if (kh == 0 && qrow < nq) {
+    const float m1 = mine[32], l1 = mine[33];
+    const float M = fmaxf(m_run, m1);
+    const float f0 = m_run == -INFINITY ? 0.f : expf(m_run - M);
+    const float f1 = m1 == -INFINITY ? 0.f : expf(m1 - M);
+    const float inv = 1.0f / (l_run * f0 + l1 * f1);
+    float *o = out + (size_t)(t0 + qrow) * dim + (size_t)h * hd;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = 32 * dt + 8 * g4 + 4 * hh;
+        if (d0 < hd) {
+          float4 v;
+          v.x = (acc[dt][4 * g4 + 0] * f0 + mine[16 * dt + 4 * g4 + 0] * f1) * inv;
+          v.y = (acc[dt][4 * g4 + 1] * f0 + mine[16 * dt + 4 * g4 + 1] * f1) * inv;
+          v.z = (acc[dt][4 * g4 + 2] * f0 + mine[16 * dt + 4 * g4 + 2] * f1) * inv;
+          v.w = (acc[dt][4 * g4 + 3] * f0 + mine[16 * dt + 4 * g4 + 3] * f1) * inv;
+          *reinterpret_cast<float4 *>(o + d0) = v;
+        }
+      }
+    }
+  }
+}
+
 // SwiGLU rows (llama.js:329-333): h[t][i] = silu(gate[t][i]) * up[t][i],
 // gate and up side by side in gu[t] = [gate | up].
 extern "C" __global__ void __launch_bounds__(256)

@@ -925,8 +925,10 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
       // 64-row query tiles sharing K/V tiles in LDS pay off from 16 rows; a
       // few rows (speculative verify) spread better one workgroup per row.
       if (g.head_dim <= 64 && n >= 16) {
+        // MFMA kernel for head dims that are a multiple of 16, else fp32 FMAs
         void *args[] = {&qkv, &kc, &vc, &out, &st, &rows, &nh, &nkv, &hd, &scale};
-        rc = launch_k(m, "pbx_attention_tiled", dim3(g.n_heads, (n + 63) / 64), dim3(256), args);
+        rc = launch_k(m, g.head_dim % 16 == 0 ? "pbx_attention_mfma" : "pbx_attention_tiled",
+                      dim3(g.n_heads, (n + 63) / 64), dim3(256), args);
       } else {
         void *args[] = {&qkv, &kc, &vc, &out, &st, &nh, &nkv, &hd, &scale};
         rc = launch_k(m, "pbx_attention_rows", dim3(g.n_heads, n), dim3(256), args);

@@ -78,6 +78,31 @@ def test_batched_prefill_vs_oracle(ctx, n):
     ref.close()
 
 
+@pytest.mark.parametrize("n_heads,n_kv", [(4, 2), (8, 2), (4, 4)])
+def test_batched_chunks_every_row_vs_oracle(ctx, n_heads, n_kv):
+    """A 50-token batched prefill, then a 30-token batch at position 50
+    (forward_batch keeps every row's logits): the batched attention with a
+    non-zero start, keys over two 64-key stages and a partial query tile, for
+    head_dim 64 (4 heads) and 32 (8 heads), GQA and MHA; every row against the
+    oracle at its position."""
+    print(f"[case] batched chunks 50 + 30, heads {n_heads}/{n_kv}", flush=True)
+    model, ref, cfg = make_pair(ctx, tiny(TYPE_Q4_0, TYPE_Q4_0, n_heads=n_heads, n_kv_heads=n_kv),
+                                330 + n_heads + n_kv)
+    first = [int(t) for t in synth.random_tokens(331, 50, cfg["vocab_size"])]
+    model.forward(first, 0)
+    ref.forward(first, 0)
+    rows = [int(t) for t in synth.random_tokens(332, 30, cfg["vocab_size"])]
+    logits, _ = model.forward_batch(rows, 50)
+    worst = 0.0
+    for t, tok in enumerate(rows):
+        r = ref.forward([tok], 50 + t)
+        worst = max(worst, float(np.abs(logits[t] - r).max()))
+    print(f"  worst max-abs {worst:.2e}")
+    assert worst <= LOGIT_TOL
+    model.free()
+    ref.close()
+
+
 def test_prefill_gqa_untied_head(ctx):
     print("[case] batched prefill, GQA 6/2, untied Q8_0 head, head_dim 48", flush=True)
     cfg = tiny(TYPE_Q8_0, TYPE_F32, dim=288, hidden_dim=768, n_heads=6, n_kv_heads=2,
