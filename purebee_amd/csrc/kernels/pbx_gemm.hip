@@ -613,64 +613,214 @@ extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_big(GemmArgs a) { 
 // Row scaling to fp16: one workgroup per (padded) row.  The scale is
 // 2^(15 - e) with 2^(e-1) <= max|x| < 2^e, so every scaled value is below
 // 2^15 in magnitude (fp16 max 65504); padding rows are zero.  X16lo gets
-// the residual x*scale - X16 rounded to fp16.  K <= PREP_KREG: each thread
-// keeps its float4s in registers, so the row is read once; longer rows read
-// it twice.
-#define PREP_KREG 8192
-extern "C" __global__ void __launch_bounds__(256)
-pbx_gemm_prep_x(const float *X, _Float16 *X16, _Float16 *X16lo, float *inv, int M, int K) {
-  __shared__ float red[4];
-  const int m = blockIdx.x, tid = threadIdx.x;
-  _Float16 *dst = X16 + (size_t)m * K;
-  _Float16 *lo = X16lo + (size_t)m * K;
-  const int K4 = K / 4;  // K is a multiple of 32
-  typedef _Float16 half4v __attribute__((ext_vector_type(4)));
-  if (m >= M) {
-    const half4v z = {};
-    for (int k = tid; k < K4; k += 256) {
-      reinterpret_cast<half4v *>(dst)[k] = z;
-      reinterpret_cast<half4v *>(lo)[k] = z;
-    }
-    if (tid == 0) inv[m] = 0.f;
-    return;
+// the residual x*scale - X16 rounded to fp16.  The row is held in registers
+// (PREP_R float4s a thread, K <= 1024 * PREP_R), so it is read once;
+// pbx_gemm_prep_x reads longer rows twice.  The
+// variants compute the row first: RMSNorm of a residual row (optionally
+// after adding split-K partials into it), or SwiGLU of a gate|up row.
+#define PREP_R 8
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void prep_zero_row(_Float16 *dst, _Float16 *lo, float *inv, int K4) {
+  const half4v z = {};
+  for (int k = threadIdx.x; k < K4; k += 256) {
+    reinterpret_cast<half4v *>(dst)[k] = z;
+    reinterpret_cast<half4v *>(lo)[k] = z;
   }
-  const float4 *src = reinterpret_cast<const float4 *>(X + (size_t)m * K);
-  constexpr int R = PREP_KREG / 1024;  // float4s per thread held in registers
-  float4 v[R];
+  if (threadIdx.x == 0) *inv = 0.f;
+}
+
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+  v = wave_sum(v);
+  __syncthreads();  // red may still be read from an earlier reduction
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __forceinline__ float max4(float4 t) {
+  return fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w)));
+}
+
+// Scale and split the row v (element 4 (tid + 256 i) + c of float4 i) into
+// dst / lo, and write the power of two that undoes the scale.
+__device__ __forceinline__ void prep_split_row(const float4 (&v)[PREP_R], int K4, _Float16 *dst,
+                                               _Float16 *lo, float *inv, float *red) {
+  const int tid = threadIdx.x;
   float mx = 0.f;
 #pragma unroll
-  for (int i = 0; i < R; ++i) {
-    const int k = tid + 256 * i;
-    v[i] = k < K4 ? src[k] : make_float4(0.f, 0.f, 0.f, 0.f);
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
-  }
-  for (int k = tid + 256 * R; k < K4; k += 256) {
-    const float4 t = src[k];
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
-  }
+  for (int i = 0; i < PREP_R; ++i) mx = fmaxf(mx, max4(v[i]));  // unused slots hold zeros
   mx = wave_max(mx);
+  __syncthreads();
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   int e = 0;
   if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
   const float scale = mx > 0.f ? ldexpf(1.f, 15 - e) : 1.f;
-  auto put = [&](int k, float4 t) {
-    // exact: scale is a power of two
-    const float a0 = t.x * scale, a1 = t.y * scale, a2 = t.z * scale, a3 = t.w * scale;
-    const half4v hv = {(_Float16)a0, (_Float16)a1, (_Float16)a2, (_Float16)a3};
-    const half4v lv = {(_Float16)(a0 - (float)hv[0]), (_Float16)(a1 - (float)hv[1]),
-                       (_Float16)(a2 - (float)hv[2]), (_Float16)(a3 - (float)hv[3])};
-    reinterpret_cast<half4v *>(dst)[k] = hv;
-    reinterpret_cast<half4v *>(lo)[k] = lv;
-  };
 #pragma unroll
-  for (int i = 0; i < R; ++i) {
+  for (int i = 0; i < PREP_R; ++i) {
     const int k = tid + 256 * i;
-    if (k < K4) put(k, v[i]);
+    if (k < K4) {
+      // exact: scale is a power of two
+      const float a0 = v[i].x * scale, a1 = v[i].y * scale, a2 = v[i].z * scale, a3 = v[i].w * scale;
+      const half4v hv = {(_Float16)a0, (_Float16)a1, (_Float16)a2, (_Float16)a3};
+      const half4v lv = {(_Float16)(a0 - (float)hv[0]), (_Float16)(a1 - (float)hv[1]),
+                         (_Float16)(a2 - (float)hv[2]), (_Float16)(a3 - (float)hv[3])};
+      reinterpret_cast<half4v *>(dst)[k] = hv;
+      reinterpret_cast<half4v *>(lo)[k] = lv;
+    }
   }
-  for (int k = tid + 256 * R; k < K4; k += 256) put(k, src[k]);
-  if (tid == 0) inv[m] = mx > 0.f ? ldexpf(1.f, e - 15) : 1.f;
+  if (tid == 0) *inv = mx > 0.f ? ldexpf(1.f, e - 15) : 1.f;
+}
+
+__device__ __forceinline__ void load_row(const float *x, int K4, float4 (&v)[PREP_R]) {
+#pragma unroll
+  for (int i = 0; i < PREP_R; ++i) {
+    const int k = threadIdx.x + 256 * i;
+    v[i] = k < K4 ? reinterpret_cast<const float4 *>(x)[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+// RMSNorm of v in place (llama.js rmsnorm: x * (1 / sqrt(mean(x^2) + eps)) * w).
+__device__ __forceinline__ void rms_row(float4 (&v)[PREP_R], const float *w, int K4, float eps,
+                                        float *red) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PREP_R; ++i) {
+    ss = fmaf(v[i].x, v[i].x, ss);
+    ss = fmaf(v[i].y, v[i].y, ss);
+    ss = fmaf(v[i].z, v[i].z, ss);
+    ss = fmaf(v[i].w, v[i].w, ss);
+  }
+  ss = block_sum256(ss, red);
+  const float r = 1.0f / sqrtf(ss / (float)(4 * K4) + eps);
+#pragma unroll
+  for (int i = 0; i < PREP_R; ++i) {
+    const int k = threadIdx.x + 256 * i;
+    if (k < K4) {
+      const float4 g = reinterpret_cast<const float4 *>(w)[k];
+      v[i] = make_float4(v[i].x * r * g.x, v[i].y * r * g.y, v[i].z * r * g.z, v[i].w * r * g.w);
+    }
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+pbx_gemm_prep_x(const float *X, _Float16 *X16, _Float16 *X16lo, float *inv, int M, int K) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, K4 = K / 4;  // K is a multiple of 32, at most 1024 * PREP_R
+  _Float16 *dst = X16 + (size_t)m * K, *lo = X16lo + (size_t)m * K;
+  if (m >= M) return prep_zero_row(dst, lo, inv + m, K4);
+  if (K4 > 256 * PREP_R) {
+    // longer rows: read twice
+    const float4 *src = reinterpret_cast<const float4 *>(X + (size_t)m * K);
+    float mx = 0.f;
+    for (int k = threadIdx.x; k < K4; k += 256) mx = fmaxf(mx, max4(src[k]));
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
+    const float scale = mx > 0.f ? ldexpf(1.f, 15 - e) : 1.f;
+    for (int k = threadIdx.x; k < K4; k += 256) {
+      const float4 t = src[k];
+      const float a0 = t.x * scale, a1 = t.y * scale, a2 = t.z * scale, a3 = t.w * scale;
+      const half4v hv = {(_Float16)a0, (_Float16)a1, (_Float16)a2, (_Float16)a3};
+      const half4v lv = {(_Float16)(a0 - (float)hv[0]), (_Float16)(a1 - (float)hv[1]),
+                         (_Float16)(a2 - (float)hv[2]), (_Float16)(a3 - (float)hv[3])};
+      reinterpret_cast<half4v *>(dst)[k] = hv;
+      reinterpret_cast<half4v *>(lo)[k] = lv;
+    }
+    if (threadIdx.x == 0) inv[m] = mx > 0.f ? ldexpf(1.f, e - 15) : 1.f;
+    return;
+  }
+  float4 v[PREP_R];
+  load_row(X + (size_t)m * K, K4, v);
+  prep_split_row(v, K4, dst, lo, inv + m, red);
+}
+
+// X16 rows of RMSNorm(x) * w (K <= 1024 * PREP_R).
+extern "C" __global__ void __launch_bounds__(256)
+pbx_gemm_prep_rms(const float *X, const float *normw, float eps, _Float16 *X16, _Float16 *X16lo,
+                  float *inv, int M, int K) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, K4 = K / 4;
+  _Float16 *dst = X16 + (size_t)m * K, *lo = X16lo + (size_t)m * K;
+  if (m >= M) return prep_zero_row(dst, lo, inv + m, K4);
+  float4 v[PREP_R];
+  load_row(X + (size_t)m * K, K4, v);
+  rms_row(v, normw, K4, eps, red);
+  prep_split_row(v, K4, dst, lo, inv + m, red);
+}
+
+// x[m] += the sum of the KS split-K partials of row m (the residual add of a
+// split GEMM, summed in split order like pbx_gemm_reduce); then, if normw,
+// the X16 row of RMSNorm(x[m]) * normw for the next GEMM.
+extern "C" __global__ void __launch_bounds__(256)
+pbx_gemm_reduce_rms(const float *part, int KS, float *X, const float *normw, float eps,
+                    _Float16 *X16, _Float16 *X16lo, float *inv, int M, int K) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, K4 = K / 4;
+  _Float16 *dst = X16 + (size_t)m * K, *lo = X16lo + (size_t)m * K;
+  if (m >= M) {
+    if (normw) prep_zero_row(dst, lo, inv + m, K4);
+    return;
+  }
+  float4 v[PREP_R];
+  float *x = X + (size_t)m * K;
+  const size_t MK = (size_t)M * K;
+#pragma unroll
+  for (int i = 0; i < PREP_R; ++i) {
+    const int k = threadIdx.x + 256 * i;
+    if (k < K4) {
+      // every partial load issued before the sum (KS <= 8)
+      float4 pp[8];
+#pragma unroll
+      for (int p = 0; p < 8; ++p)
+        pp[p] = p < KS ? reinterpret_cast<const float4 *>(part + p * MK + (size_t)m * K)[k]
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 s = pp[0];
+#pragma unroll
+      for (int p = 1; p < 8; ++p)
+        if (p < KS) {
+          s.x += pp[p].x; s.y += pp[p].y; s.z += pp[p].z; s.w += pp[p].w;
+        }
+      float4 r = reinterpret_cast<float4 *>(x)[k];
+      r.x += s.x; r.y += s.y; r.z += s.z; r.w += s.w;
+      reinterpret_cast<float4 *>(x)[k] = r;
+      v[i] = r;
+    } else {
+      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  if (!normw) return;
+  rms_row(v, normw, K4, eps, red);
+  prep_split_row(v, K4, dst, lo, inv + m, red);
+}
+
+// X16 rows of silu(gate) * up from gate|up rows [M][2 * hidden] (llama.js:329-333).
+extern "C" __global__ void __launch_bounds__(256)
+pbx_gemm_prep_swiglu(const float *GU, _Float16 *X16, _Float16 *X16lo, float *inv, int M,
+                     int hidden) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, K4 = hidden / 4;
+  _Float16 *dst = X16 + (size_t)m * hidden, *lo = X16lo + (size_t)m * hidden;
+  if (m >= M) return prep_zero_row(dst, lo, inv + m, K4);
+  const float4 *g4 = reinterpret_cast<const float4 *>(GU + (size_t)m * 2 * hidden);
+  const float4 *u4 = g4 + K4;
+  float4 v[PREP_R];
+#pragma unroll
+  for (int i = 0; i < PREP_R; ++i) {
+    const int k = threadIdx.x + 256 * i;
+    if (k < K4) {
+      const float4 g = g4[k], u = u4[k];
+      v[i] = make_float4(silu(g.x) * u.x, silu(g.y) * u.y, silu(g.z) * u.z, silu(g.w) * u.w);
+    } else {
+      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  prep_split_row(v, K4, dst, lo, inv + m, red);
 }
 
 // Sum of the split-K partials (+ bias, or accumulated into Y).

@@ -56,12 +56,34 @@ pbx_rmsnorm_rows(const float *x, const float *w, float *out, int dim, float eps)
 
 // RoPE of q and k in place for each row t (position start + t) and append of
 // k, v to the cache (llama.js:159-191, 243-255).  qkv rows: [dim | kv | kv].
+// With part, the rows are first the sum of the KS split-K partials
+// [KS][rows][dim + 2 kv] of the q|k|v GEMM (summed in split order).
 extern "C" __global__ void __launch_bounds__(256)
 pbx_rope_append_rows(float *qkv, float *kcache, float *vcache, const float *rope, int start,
-                     int n_heads, int n_kv_heads, int head_dim) {
+                     int n_heads, int n_kv_heads, int head_dim, const float *part, int KS) {
   const int t = blockIdx.x, pos = start + t;
   const int dim = n_heads * head_dim, kvdim = n_kv_heads * head_dim;
-  float *row = qkv + (size_t)t * (dim + 2 * kvdim);
+  const int rl = dim + 2 * kvdim;
+  float *row = qkv + (size_t)t * rl;
+  if (part) {
+    // float4 columns (rl is a multiple of 4); all partial loads of a column
+    // are issued before the sum (KS <= 8)
+    const size_t stride4 = (size_t)gridDim.x * rl / 4;
+    const float4 *pr = reinterpret_cast<const float4 *>(part + (size_t)t * rl);
+    for (int i = threadIdx.x; i < rl / 4; i += blockDim.x) {
+      float4 p[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) p[k] = k < KS ? pr[k * stride4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 v = p[0];
+#pragma unroll
+      for (int k = 1; k < 8; ++k)
+        if (k < KS) {
+          v.x += p[k].x; v.y += p[k].y; v.z += p[k].z; v.w += p[k].w;
+        }
+      reinterpret_cast<float4 *>(row)[i] = v;
+    }
+    __syncthreads();
+  }
   const float *rp = rope + (size_t)pos * head_dim;
   const int half = head_dim / 2;
   for (int p = threadIdx.x; p < (n_heads + n_kv_heads) * half; p += blockDim.x) {

@@ -91,14 +91,11 @@ int launch_f32(pbx_ctx *c, const pbx_weight *w, const float *dX, int M, const fl
 
 }  // namespace
 
-int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M64,
-                    const float *dBias, float *dY, int accumulate, hipStream_t stream) {
-  if (!gemm_tag(w->type))
-    return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: weight type %d has no MFMA path", w->type);
-  if (M64 > 65535) return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: M=%lld too large", (long long)M64);
-  if (w->type == PBX_TYPE_F32)
-    return launch_f32(c, w, dX, (int)M64, dBias, dY, accumulate, stream);
-  const int M = (int)M64, N = (int)w->N, B = (int)w->B, K = B * 32;
+int pbx_gemm_make_plan(pbx_ctx *c, const pbx_weight *w, int M, pbx_gemm_plan *p) {
+  if (!gemm_tag(w->type) || w->type == PBX_TYPE_F32)
+    return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: weight type %d has no fp16 MFMA path", w->type);
+  if (M <= 0 || M > 65535) return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: M=%d out of range", M);
+  const int N = (int)w->N, B = (int)w->B;
   // M > 32: the LDS-tiled 128 x 128 kernel; otherwise one wave per 16*MT
   // rows x 16*NT weight rows.
   const bool big = M > 32;
@@ -128,40 +125,63 @@ int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M6
     const int waves = nwg * mtiles * 4;
     if (waves < 8 * c->cu_count) KS = std::min({B, 8, (8 * c->cu_count + waves - 1) / waves});
   }
-  // fp16 activations and their fp16 rounding residuals
-  const size_t x16_bytes = ((size_t)Mpad * K * 2 + 255) / 256 * 256;
-  const size_t lo_bytes = x16_bytes;
-  const size_t inv_bytes = ((size_t)Mpad * 4 + 255) / 256 * 256;
-  const size_t part_bytes = KS > 1 ? (size_t)KS * M * N * 4 : 0;
-  int rc = pbx_ensure_dev(c, &c->d_gemm, &c->d_gemm_cap,
-                          x16_bytes + lo_bytes + inv_bytes + part_bytes);
+  p->M = M;
+  p->Mpad = Mpad;
+  p->mtiles = mtiles;
+  p->nwg = nwg;
+  p->KS = KS;
+  p->name = std::string("pbx_gemm_") + gemm_tag(w->type) +
+            (big ? std::string("_big") : "_m" + std::to_string(MT) + "_n" + std::to_string(NT));
+  return PBX_OK;
+}
+
+int pbx_gemm_run(pbx_ctx *c, const pbx_weight *w, const pbx_gemm_plan &p, const void *x16,
+                 const void *x16lo, const float *inv, const float *dBias, float *out,
+                 int accumulate, hipStream_t stream) {
+  hipFunction_t fg = pbx_kernel_by_name(c, p.name);
+  if (!fg) return pbx_fail(c, PBX_ELOAD, "pbx_gemm: kernel %s missing", p.name.c_str());
+  GemmArgsHost g{w->qs, w->d, x16, x16lo, inv, p.KS == 1 ? dBias : nullptr, out,
+                 p.M, (int)w->N, (int)w->Npad, (int)w->B, p.KS, p.KS == 1 ? accumulate : 0, w->m};
+  void *args[] = {&g};
+  return pbx_launch_fn(c, fg, p.name.c_str(), dim3(p.nwg, p.mtiles, p.KS), dim3(256), args, stream);
+}
+
+int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M64,
+                    const float *dBias, float *dY, int accumulate, hipStream_t stream) {
+  if (!gemm_tag(w->type))
+    return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: weight type %d has no MFMA path", w->type);
+  if (M64 > 65535) return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: M=%lld too large", (long long)M64);
+  if (w->type == PBX_TYPE_F32)
+    return launch_f32(c, w, dX, (int)M64, dBias, dY, accumulate, stream);
+  const int M = (int)M64, N = (int)w->N, K = (int)w->B * 32;
+  pbx_gemm_plan p;
+  int rc = pbx_gemm_make_plan(c, w, M, &p);
   if (rc) return rc;
+  // fp16 activations and their fp16 rounding residuals
+  const size_t x16_bytes = ((size_t)p.Mpad * K * 2 + 255) / 256 * 256;
+  const size_t lo_bytes = x16_bytes;
+  const size_t inv_bytes = ((size_t)p.Mpad * 4 + 255) / 256 * 256;
+  const size_t part_bytes = p.KS > 1 ? (size_t)p.KS * M * N * 4 : 0;
+  if ((rc = pbx_ensure_dev(c, &c->d_gemm, &c->d_gemm_cap,
+                           x16_bytes + lo_bytes + inv_bytes + part_bytes)))
+    return rc;
   char *ws = (char *)c->d_gemm;
   void *x16 = ws;
   void *x16lo = ws + x16_bytes;
   float *inv = (float *)(ws + x16_bytes + lo_bytes);
   float *part = (float *)(ws + x16_bytes + lo_bytes + inv_bytes);
-
   hipFunction_t fprep = pbx_kernel_by_name(c, "pbx_gemm_prep_x");
-  const std::string name = std::string("pbx_gemm_") + gemm_tag(w->type) +
-                           (big ? std::string("_big")
-                                : "_m" + std::to_string(MT) + "_n" + std::to_string(NT));
-  hipFunction_t fg = pbx_kernel_by_name(c, name);
-  if (!fprep || !fg) return pbx_fail(c, PBX_ELOAD, "pbx_gemm: kernel %s missing", name.c_str());
+  if (!fprep) return pbx_fail(c, PBX_ELOAD, "pbx_gemm: kernel pbx_gemm_prep_x missing");
   {
     int m = M, k = K;
     void *args[] = {(void *)&dX, &x16, &x16lo, &inv, &m, &k};
-    if ((rc = pbx_launch_fn(c, fprep, "pbx_gemm_prep_x", dim3(Mpad), dim3(256), args, stream)))
+    if ((rc = pbx_launch_fn(c, fprep, "pbx_gemm_prep_x", dim3(p.Mpad), dim3(256), args, stream)))
       return rc;
   }
-  GemmArgsHost g{w->qs, w->d, x16, x16lo, inv, KS == 1 ? dBias : nullptr, KS == 1 ? dY : part,
-                 M, N, (int)w->Npad, B, KS, KS == 1 ? accumulate : 0, w->m};
-  {
-    void *args[] = {&g};
-    if ((rc = pbx_launch_fn(c, fg, name.c_str(), dim3(nwg, mtiles, KS), dim3(256), args, stream)))
-      return rc;
-  }
-  if (KS > 1) return launch_reduce(c, part, dBias, dY, M, N, KS, accumulate, stream);
+  if ((rc = pbx_gemm_run(c, w, p, x16, x16lo, inv, dBias, p.KS == 1 ? dY : part, accumulate,
+                         stream)))
+    return rc;
+  if (p.KS > 1) return launch_reduce(c, part, dBias, dY, M, N, p.KS, accumulate, stream);
   return PBX_OK;
 }
 

@@ -129,6 +129,18 @@ int pbx_ensure_dev(pbx_ctx *c, void **p, size_t *cap, size_t need);
 int pbx_ensure_pinned(pbx_ctx *c, void **p, size_t *cap, size_t need);
 int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
                        const float *dBias, float *dY, hipStream_t stream);
+// The fp16 MFMA GEMM in two parts, for callers that prepare the fp16
+// activation pair (X16, X16lo, inv: [Mpad][K]) themselves: the kernel, grid
+// and K split for M rows of weight w, and the launch, which writes Y (KS == 1,
+// += if accumulate) or the KS partials [KS][M][N].
+struct pbx_gemm_plan {
+  int M = 0, Mpad = 0, mtiles = 0, nwg = 0, KS = 1;
+  std::string name;
+};
+int pbx_gemm_make_plan(pbx_ctx *c, const pbx_weight *w, int M, pbx_gemm_plan *p);
+int pbx_gemm_run(pbx_ctx *c, const pbx_weight *w, const pbx_gemm_plan &p, const void *x16,
+                 const void *x16lo, const float *inv, const float *dBias, float *out,
+                 int accumulate, hipStream_t stream);
 int pbx_gemm_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
                      const float *dBias, float *dY, hipStream_t stream);
 int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,

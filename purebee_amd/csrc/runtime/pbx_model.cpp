@@ -155,6 +155,11 @@ struct pbx_model {
         *bh = nullptr, *btmp = nullptr, *blogits = nullptr;
   int *btok = nullptr, *bnext = nullptr;
   uint64_t *bkeys = nullptr;  // [logits_cap][64] partial argmax keys
+  // fused batched layers: the fp16 activation pair of the next GEMM and the
+  // split-K partials of the last one
+  void *g16 = nullptr, *g16lo = nullptr;
+  float *ginv = nullptr, *gpart = nullptr;
+  size_t g16_cap = 0, gpart_cap = 0;
 };
 
 static bool model_ok(const pbx_model *m) { return m && m->magic == PBX_MODEL_MAGIC; }
@@ -535,7 +540,8 @@ static void model_release(pbx_model *m) {
     if (p) hipFree(p);
   for (void *p : {(void *)m->bx, (void *)m->bxn, (void *)m->bqkv, (void *)m->battn,
                   (void *)m->bgu, (void *)m->bh, (void *)m->btmp, (void *)m->blogits,
-                  (void *)m->btok, (void *)m->bnext, (void *)m->bkeys})
+                  (void *)m->btok, (void *)m->bnext, (void *)m->bkeys, m->g16, m->g16lo,
+                  (void *)m->ginv, (void *)m->gpart})
     if (p) hipFree(p);
   m->magic = 0;
   delete m;
@@ -884,6 +890,94 @@ static int rmsnorm_rows(pbx_model *m, const float *x, const float *w, float *out
   return launch_k(m, "pbx_rmsnorm_rows", dim3(n), dim3(256), args);
 }
 
+// Fused batched layers (fp16 MFMA GEMMs): the activation preparation of
+// each GEMM is folded into the kernel that produces its input, and split-K
+// partials are summed by the kernel that consumes them.  Per layer:
+//   qkv GEMM -> RoPE + KV append (+ partial sum) -> attention -> prep -> o GEMM
+//   -> residual add (+ partial sum) + RMSNorm + prep -> gate|up GEMM
+//   -> SwiGLU + prep -> down GEMM -> residual add + next layer's RMSNorm + prep.
+static bool fused_ok(const pbx_model *m, int n) {
+  const pbx_model_config &g = m->cfg;
+  const int t = g.weight_type;
+  return n >= PBX_GEMM_MIN_M &&
+         (t == PBX_TYPE_Q4_0 || t == PBX_TYPE_Q8_0 || t == PBX_TYPE_Q4_1 || t == PBX_TYPE_F16) &&
+         g.dim <= 8192 && g.hidden_dim <= 8192;
+}
+
+struct FusedPlans {
+  pbx_gemm_plan qkv, o, gu, d;
+};
+
+static int fused_plans(pbx_model *m, int n, FusedPlans *P) {
+  pbx_ctx *c = m->c;
+  const Layer &L = m->layers[0];
+  int rc;
+  if ((rc = pbx_gemm_make_plan(c, L.wqkv, n, &P->qkv)) || (rc = pbx_gemm_make_plan(c, L.wo, n, &P->o)) ||
+      (rc = pbx_gemm_make_plan(c, L.wgu, n, &P->gu)) || (rc = pbx_gemm_make_plan(c, L.wd, n, &P->d)))
+    return rc;
+  const pbx_model_config &g = m->cfg;
+  const size_t kmax = std::max(g.dim, g.hidden_dim);
+  const size_t act = ((size_t)P->qkv.Mpad * kmax * 2 + 255) / 256 * 256;
+  size_t part = 0;
+  for (const pbx_gemm_plan *p : {&P->qkv, &P->o, &P->gu, &P->d}) {
+    const pbx_weight *w = p == &P->qkv ? L.wqkv : p == &P->o ? L.wo : p == &P->gu ? L.wgu : L.wd;
+    if (p->KS > 1) part = std::max(part, (size_t)p->KS * n * w->N * 4);
+  }
+  if (act > m->g16_cap) {
+    m->g16_cap = 0;
+    if ((rc = grow(m, &m->g16, act)) || (rc = grow(m, &m->g16lo, act)) ||
+        (rc = grow(m, (void **)&m->ginv, (size_t)P->qkv.Mpad * 4)))
+      return rc;
+    m->g16_cap = act;
+  }
+  if (part > m->gpart_cap) {
+    m->gpart_cap = 0;
+    if ((rc = grow(m, (void **)&m->gpart, part))) return rc;
+    m->gpart_cap = part;
+  }
+  return PBX_OK;
+}
+
+// The GEMM of plan p on the prepared activations into Y (KS == 1; += if
+// accumulate) or into the partials.
+static int fused_gemm(pbx_model *m, const pbx_weight *w, const pbx_gemm_plan &p, float *Y,
+                      bool accumulate) {
+  return pbx_gemm_run(m->c, w, p, m->g16, m->g16lo, m->ginv, nullptr, p.KS == 1 ? Y : m->gpart,
+                      accumulate ? 1 : 0, m->c->stream);
+}
+
+static int launch_k(pbx_model *m, const char *name, dim3 grid, dim3 block, void **args);
+
+// Y (+)= the sum of the partials of a split GEMM (plain reduce).
+static int fused_reduce(pbx_model *m, const pbx_gemm_plan &p, int N, float *Y, bool accumulate) {
+  const float *part = m->gpart, *bias = nullptr;
+  int M = p.M, n = N, ks = p.KS, acc = accumulate ? 1 : 0;
+  const int64_t total = (int64_t)M * N;
+  void *args[] = {(void *)&part, (void *)&bias, &Y, &M, &n, &ks, &acc};
+  return launch_k(m, "pbx_gemm_reduce", dim3((unsigned)((total + 255) / 256)), dim3(256), args);
+}
+
+// x += the partials of the GEMM of plan p if it was split (p null: nothing to
+// add), then the prepared RMSNorm(x) * normw for the next GEMM (none if
+// normw is null).  M rows, Mpad prepared rows.
+static int fused_residual_norm(pbx_model *m, const pbx_gemm_plan *p, int M, int Mpad, float *x,
+                               const float *normw) {
+  const pbx_model_config &g = m->cfg;
+  int rows = M, K = g.dim;
+  float eps = g.rms_eps;
+  void *x16 = m->g16, *x16lo = m->g16lo;
+  float *inv = m->ginv;
+  if (p && p->KS > 1) {
+    const float *part = m->gpart;
+    int ks = p->KS;
+    void *args[] = {(void *)&part, &ks, &x, (void *)&normw, &eps, &x16, &x16lo, &inv, &rows, &K};
+    return launch_k(m, "pbx_gemm_reduce_rms", dim3(normw ? Mpad : M), dim3(256), args);
+  }
+  if (!normw) return PBX_OK;
+  void *args[] = {(void *)&x, (void *)&normw, &eps, &x16, &x16lo, &inv, &rows, &K};
+  return launch_k(m, "pbx_gemm_prep_rms", dim3(Mpad), dim3(256), args);
+}
+
 // Runs the layer stack over n rows; leaves the residual stream in m->bx.
 static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
   pbx_ctx *c = m->c;
@@ -901,6 +995,63 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
   }
   const size_t layer_kv = (size_t)g.max_seq * m->kvdim;
   const bool rows_int = n <= ROWS_MAX && rows_int_ok(m);
+  if (!rows_int && fused_ok(m, n)) {
+    FusedPlans P;
+    if ((rc = fused_plans(m, n, &P))) return rc;
+    if ((rc = fused_residual_norm(m, nullptr, n, P.qkv.Mpad, m->bx, m->layers[0].attn_norm))) return rc;
+    for (int l = 0; l < g.n_layers; ++l) {
+      Layer &L = m->layers[l];
+      float *kc = m->kcache + l * layer_kv, *vc = m->vcache + l * layer_kv;
+      if ((rc = fused_gemm(m, L.wqkv, P.qkv, m->bqkv, false))) return rc;
+      {
+        float *qkv = m->bqkv, *rope = m->rope;
+        const float *part = P.qkv.KS > 1 ? m->gpart : nullptr;
+        int st = start, nh = g.n_heads, nkv = g.n_kv_heads, hd = g.head_dim, ks = P.qkv.KS;
+        void *args[] = {&qkv, &kc, &vc, &rope, &st, &nh, &nkv, &hd, (void *)&part, &ks};
+        if ((rc = launch_k(m, "pbx_rope_append_rows", dim3(n), dim3(256), args))) return rc;
+      }
+      {
+        float *qkv = m->bqkv, *out = m->battn;
+        int st = start, nh = g.n_heads, nkv = g.n_kv_heads, hd = g.head_dim, rows = n;
+        float scale = (float)(1.0 / sqrt((double)g.head_dim));
+        if (g.head_dim <= 64 && n >= 16) {
+          void *args[] = {&qkv, &kc, &vc, &out, &st, &rows, &nh, &nkv, &hd, &scale};
+          rc = launch_k(m, g.head_dim % 16 == 0 ? "pbx_attention_mfma" : "pbx_attention_tiled",
+                        dim3(g.n_heads, (n + 63) / 64), dim3(256), args);
+        } else {
+          void *args[] = {&qkv, &kc, &vc, &out, &st, &nh, &nkv, &hd, &scale};
+          rc = launch_k(m, "pbx_attention_rows", dim3(g.n_heads, n), dim3(256), args);
+        }
+        if (rc) return rc;
+      }
+      {
+        float *x = m->battn;
+        void *x16 = m->g16, *x16lo = m->g16lo;
+        float *inv = m->ginv;
+        int M = n, K = g.dim;
+        void *args[] = {&x, &x16, &x16lo, &inv, &M, &K};
+        if ((rc = launch_k(m, "pbx_gemm_prep_x", dim3(P.o.Mpad), dim3(256), args))) return rc;
+      }
+      if ((rc = fused_gemm(m, L.wo, P.o, m->bx, true)) ||
+          (rc = fused_residual_norm(m, &P.o, n, P.o.Mpad, m->bx, L.ffn_norm)) ||
+          (rc = fused_gemm(m, L.wgu, P.gu, m->bgu, false)))
+        return rc;
+      if (P.gu.KS > 1 && (rc = fused_reduce(m, P.gu, (int)L.wgu->N, m->bgu, false))) return rc;
+      {
+        float *gu = m->bgu;
+        void *x16 = m->g16, *x16lo = m->g16lo;
+        float *inv = m->ginv;
+        int M = n, hidden = g.hidden_dim;
+        void *args[] = {&gu, &x16, &x16lo, &inv, &M, &hidden};
+        if ((rc = launch_k(m, "pbx_gemm_prep_swiglu", dim3(P.gu.Mpad), dim3(256), args))) return rc;
+      }
+      if ((rc = fused_gemm(m, L.wd, P.d, m->bx, true)) ||
+          (rc = fused_residual_norm(m, &P.d, n, P.d.Mpad, m->bx,
+                                    l + 1 < g.n_layers ? m->layers[l + 1].attn_norm : nullptr)))
+        return rc;
+    }
+    return PBX_OK;
+  }
   for (int l = 0; l < g.n_layers; ++l) {
     Layer &L = m->layers[l];
     float *kc = m->kcache + l * layer_kv, *vc = m->vcache + l * layer_kv;
@@ -915,7 +1066,9 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
     {
       float *qkv = m->bqkv, *rope = m->rope;
       int st = start, nh = g.n_heads, nkv = g.n_kv_heads, hd = g.head_dim;
-      void *args[] = {&qkv, &kc, &vc, &rope, &st, &nh, &nkv, &hd};
+      const float *part = nullptr;
+      int ks = 1;
+      void *args[] = {&qkv, &kc, &vc, &rope, &st, &nh, &nkv, &hd, (void *)&part, &ks};
       if ((rc = launch_k(m, "pbx_rope_append_rows", dim3(n), dim3(256), args))) return rc;
     }
     {
