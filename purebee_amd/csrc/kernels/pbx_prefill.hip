@@ -383,26 +383,50 @@ pbx_attention_mfma(const float *qkv, const float *kcache, const float *vcache, f
   floatx16 acc[2] = {zero16, zero16};  // O^T, dims 32 dt + 8 (r/4) + 4 hh + r%4
   const int last_key = start + t0 + nq - 1;
   const float *kb = kcache + (size_t)kvh * hd, *vb = vcache + (size_t)kvh * hd;
-  for (int k0 = 0; k0 <= last_key; k0 += FA_KT) {
+  // the next stage's K and V rows are loaded into registers while the current
+  // stage is multiplied: K item i (< 4) = key (tid + 256 i) / hd4, float4
+  // column (tid + 256 i) % hd4; V item i = keys 2 p, 2 p + 1 of item
+  // p = (tid + 256 i) / hd4 (< 32 key pairs), same column
+  float4 kreg[4], vreg0[2], vreg1[2];
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto load_stage = [&](int k0) {
     const int nk = min(FA_KT, last_key + 1 - k0);
-    __syncthreads();  // the previous stage's reads are done
-    for (int i = tid; i < FA_KT * hd4; i += 256) {
-      const int key = i / hd4, c4 = 4 * (i % hd4);
-      const float4 v = key < nk ? *reinterpret_cast<const float4 *>(kb + (size_t)(k0 + key) * kvdim + c4)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
-      half4t hv, lv;
-      SPLIT_F16(v.x, hv[0], lv[0]);
-      SPLIT_F16(v.y, hv[1], lv[1]);
-      SPLIT_F16(v.z, hv[2], lv[2]);
-      SPLIT_F16(v.w, hv[3], lv[3]);
-      *reinterpret_cast<half4t *>(&Kh[key * FA_KP + c4]) = hv;
-      *reinterpret_cast<half4t *>(&Kl[key * FA_KP + c4]) = lv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int it = tid + 256 * i, key = it / hd4, c4 = 4 * (it % hd4);
+      kreg[i] = (it < FA_KT * hd4 && key < nk)
+                    ? *reinterpret_cast<const float4 *>(kb + (size_t)(k0 + key) * kvdim + c4) : z4;
     }
-    for (int i = tid; i < (FA_KT / 2) * hd4; i += 256) {
-      const int kp = 2 * (i / hd4), c4 = 4 * (i % hd4);
-      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 v0 = kp < nk ? *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + kp) * kvdim + c4) : z;
-      const float4 v1 = kp + 1 < nk ? *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + kp + 1) * kvdim + c4) : z;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int it = tid + 256 * i, kp = 2 * (it / hd4), c4 = 4 * (it % hd4);
+      const bool ok = it < (FA_KT / 2) * hd4;
+      vreg0[i] = ok && kp < nk ? *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + kp) * kvdim + c4) : z4;
+      vreg1[i] = ok && kp + 1 < nk ? *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + kp + 1) * kvdim + c4) : z4;
+    }
+  };
+  load_stage(0);
+  for (int k0 = 0; k0 <= last_key; k0 += FA_KT) {
+    __syncthreads();  // the previous stage's reads are done
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int it = tid + 256 * i, key = it / hd4, c4 = 4 * (it % hd4);
+      if (it < FA_KT * hd4) {
+        const float4 v = kreg[i];
+        half4t hv, lv;
+        SPLIT_F16(v.x, hv[0], lv[0]);
+        SPLIT_F16(v.y, hv[1], lv[1]);
+        SPLIT_F16(v.z, hv[2], lv[2]);
+        SPLIT_F16(v.w, hv[3], lv[3]);
+        *reinterpret_cast<half4t *>(&Kh[key * FA_KP + c4]) = hv;
+        *reinterpret_cast<half4t *>(&Kl[key * FA_KP + c4]) = lv;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int it = tid + 256 * i, kp = 2 * (it / hd4), c4 = 4 * (it % hd4);
+      if (it < (FA_KT / 2) * hd4) {
+        const float4 v0 = vreg0[i], v1 = vreg1[i];
 #define FA_PUTV(e, x0, x1)                                                  \
   do {                                                                      \
     half2t hv_, lv_;                                                        \
@@ -411,13 +435,15 @@ pbx_attention_mfma(const float *qkv, const float *kcache, const float *vcache, f
     *reinterpret_cast<half2t *>(&Vh[(c4 + (e)) * FA_KP + kp]) = hv_;        \
     *reinterpret_cast<half2t *>(&Vl[(c4 + (e)) * FA_KP + kp]) = lv_;        \
   } while (0)
-      FA_PUTV(0, v0.x, v1.x);
-      FA_PUTV(1, v0.y, v1.y);
-      FA_PUTV(2, v0.z, v1.z);
-      FA_PUTV(3, v0.w, v1.w);
+        FA_PUTV(0, v0.x, v1.x);
+        FA_PUTV(1, v0.y, v1.y);
+        FA_PUTV(2, v0.z, v1.z);
+        FA_PUTV(3, v0.w, v1.w);
 #undef FA_PUTV
+      }
     }
     __syncthreads();
+    if (k0 + FA_KT <= last_key) load_stage(k0 + FA_KT);
 
     // S^T for this wave's 32 keys (rows) x 32 queries (columns)
     const int kr = 32 * kh + lq;  // A row: key kr of the stage
