@@ -269,164 +269,26 @@ GEMM_KERNEL(pbx_gemm_f16_m1_n2, PBX_F16, 1, 2)
 GEMM_KERNEL(pbx_gemm_f16_m1_n4, PBX_F16, 1, 4)
 GEMM_KERNEL(pbx_gemm_f16_m2_n2, PBX_F16, 2, 2)
 
-// ---------------------------------------------------------------------------
-// Large-M kernel for Q8_0, Q4_1 and F16 (M > 32; Q4_0 has its own below):
-// workgroup tile 128 (M) x 128 (N), four waves in
-// a 2 x 2 arrangement, each wave 64 x 64 (4 x 4 MFMA tiles).  The activation
-// tile of a block (128 rows x 32 k, hi and lo, 16 KB) is loaded once per
-// workgroup into LDS (double buffered: block b+1 is read from global while
-// block b is multiplied) and read by the two waves that share it; each wave
-// reads its 64 weight rows' codes one block ahead.  LDS rows are padded to
-// 48 halves (measured against 32, 36 and 40).
-// Needs X16 / X16lo padded to a multiple of 128 rows.
-// ---------------------------------------------------------------------------
-#define BIG_TM 128
-#define BIG_LDSR 48  // halves per LDS row (32 + 16 padding: fewest bank conflicts measured)
-
-// WN waves along N: 2 (128 x 128 tile, 256 threads).  A 128 x 256 tile
-// (WN = 4, 512 threads) measured 35% slower at M = 512 and is not built.
-template <int TYPE, int WN>
-__device__ __forceinline__ void gemm_big(const GemmArgs &a) {
-  constexpr int NTH = 128 * WN;  // threads
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][2][BIG_TM * BIG_LDSR];  // [buf][hi/lo]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int li = lane & 15, g = lane >> 4;
-  const int wm = wave / WN, wn = wave % WN;
-  const int n0 = blockIdx.x * (64 * WN) + wn * 64;
-  const int mblk = blockIdx.y * BIG_TM;
-  const int m0 = wm * 64;  // within the workgroup tile
-  const int K = a.B * 32;
-  const int per = (a.B + a.KS - 1) / a.KS;
-  const int b0 = blockIdx.z * per;
-  const int b1 = min(a.B, b0 + per);
-  const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
-
-  // global -> LDS staging: 1024 16-byte chunks per block (2 planes x 128
-  // rows x 4 chunks), CH = 1024 / NTH per thread: chunk c = tid + NTH i is
-  // plane c / 512, row (c & 511) / 4, 8-half quarter c & 3
-  // Thread tid stages chunks c = tid + NTH * i (i < 1024 / NTH): plane c / 512,
-  // row (c & 511) / 4, quarter c & 3.  With NTH = 256 the four chunks are
-  // (hi, row r), (hi, r + 64), (lo, r), (lo, r + 64); with 512 they are
-  // (hi, r) and (lo, r), r = tid / 4.
-  const int sq = tid & 3, sr = (tid & 511) >> 2;
-  const _Float16 *ghi = a.X16 + (size_t)(mblk + sr) * K + sq * 8;
-  const _Float16 *glo = a.X16lo + (size_t)(mblk + sr) * K + sq * 8;
-  const size_t g64 = (size_t)64 * K;  // 64 rows further down
-  const int lofs = sr * BIG_LDSR + sq * 8, l64 = 64 * BIG_LDSR;
-  uint4 st0, st1, st2, st3;
-#define BIG_LOAD_A(b)                                                              \
-  do {                                                                             \
-    st0 = *reinterpret_cast<const uint4 *>(ghi + (b) * 32);                        \
-    st2 = *reinterpret_cast<const uint4 *>(glo + (b) * 32);                        \
-    if constexpr (NTH == 256) {                                                    \
-      st1 = *reinterpret_cast<const uint4 *>(ghi + g64 + (b) * 32);                \
-      st3 = *reinterpret_cast<const uint4 *>(glo + g64 + (b) * 32);                \
-    }                                                                              \
-  } while (0)
-#define BIG_STORE_A(buf)                                                           \
-  do {                                                                             \
-    *reinterpret_cast<uint4 *>(&As[buf][0][lofs]) = st0;                           \
-    *reinterpret_cast<uint4 *>(&As[buf][1][lofs]) = st2;                           \
-    if constexpr (NTH == 256) {                                                    \
-      *reinterpret_cast<uint4 *>(&As[buf][0][lofs + l64]) = st1;                   \
-      *reinterpret_cast<uint4 *>(&As[buf][1][lofs + l64]) = st3;                   \
-    }                                                                              \
-  } while (0)
-
-  floatx4 acc[4][4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) acc[t][u] = zero;
-
-  typename RawT<TYPE>::type raw[4];
-  unsigned dbits[4], mbits[4];
-  if (b0 < b1) {
-    BIG_LOAD_A(b0);
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      load_codes<TYPE>(a, n0 + 16 * u + li, b0, g, &raw[u], &dbits[u], &mbits[u]);
-    BIG_STORE_A(0);
-  }
-  __syncthreads();
-  for (int b = b0; b < b1; ++b) {
-    const int buf = (b - b0) & 1;
-    const bool more = b + 1 < b1;
-    if (more) BIG_LOAD_A(b + 1);
-    half8 W[4];
-    float d[4], mn[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      W[u] = codes_operand<TYPE>(raw[u], g);
-      d[u] = f16_bits_to_f32(dbits[u]);
-      mn[u] = f16_bits_to_f32(mbits[u]);
-    }
-    if (more) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        load_codes<TYPE>(a, n0 + 16 * u + li, b + 1, g, &raw[u], &dbits[u], &mbits[u]);
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int r = m0 + 16 * t + li;
-      const half8 Ah = *reinterpret_cast<const half8 *>(&As[buf][0][r * BIG_LDSR + 8 * g]);
-      const half8 Al = *reinterpret_cast<const half8 *>(&As[buf][1][r * BIG_LDSR + 8 * g]);
-      const floatx4 xs = TYPE == PBX_Q41 ? block_sums(Ah, Al) : zero;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) block_mma<TYPE>(acc[t][u], Ah, Al, W[u], d[u], mn[u], xs);
-    }
-    if (more) BIG_STORE_A(buf ^ 1);
-    __syncthreads();
-  }
-#undef BIG_LOAD_A
-#undef BIG_STORE_A
-
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int n = n0 + 16 * u + li;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int m = mblk + m0 + 16 * t + 4 * g + rr;
-        if (m < a.M && n < a.N) {
-          const float v = acc[t][u][rr] * a.inv[m];
-          if (a.KS == 1) {
-            float *y = a.Y + (size_t)m * a.N + n;
-            if (a.accumulate)
-              *y += v;
-            else
-              *y = v + (a.bias ? a.bias[n] : 0.f);
-          } else {
-            a.Y[((size_t)blockIdx.z * a.M + m) * a.N + n] = v;
-          }
-        }
-      }
-    }
-}
-
-extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q8_big(GemmArgs a) { gemm_big<PBX_Q8, 2>(a); }
-extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q41_big(GemmArgs a) { gemm_big<PBX_Q41, 2>(a); }
-extern "C" __global__ void __launch_bounds__(256) pbx_gemm_f16_big(GemmArgs a) { gemm_big<PBX_F16, 2>(a); }
 
 // ---------------------------------------------------------------------------
-// Q4_0 large-M kernel (M > 32): 32x32x16 MFMAs with every operand moved to
-// LDS by DMA.  Operand lane layout of v_mfma_f32_32x32x16_f16 (checked on
+// Large-M kernel (M > 32): 32x32x16 MFMAs with every operand moved to LDS
+// by DMA.  Operand lane layout of v_mfma_f32_32x32x16_f16 (checked on
 // the device): A: lane l holds A[l%32][8*(l/32) + e]; B: lane l holds
 // B[8*(l/32) + e][l%32]; D: lane l, register r holds
 // D[8*(r/4) + 4*(l/32) + r%4][l%32].  A 32-wide block is two MFMAs per
 // operand: j = 0 takes k = 8h + e and j = 1 takes k = 16 + 8h + e
-// (h = l/32), which are the low and high nibbles of the Q4_0 bytes 8h..8h+7:
-// a lane reads its 8 code bytes once.  Each lane's 16 outputs share one
-// column (weight row), so the block scale is one value per lane.
+// (h = l/32), which are the low and high nibbles of the Q4_0 / Q4_1 bytes
+// 8h..8h+7 (a lane reads its 8 code bytes once), the Q8_0 bytes 8h.. and
+// 16+8h.., the F16 halves likewise.  Each lane's 16 outputs share one column
+// (weight row), so the block scale is one value per lane.
 // Workgroup tile 128 (M) x 128 (N), four waves in 2 x 2, wave tile 64 x 64
 // (2 x 2 MFMA tiles).  A ring of NS LDS stages, each [hi/lo][128 rows][4
-// chunks of 8 halves] of activations, the 128 weight rows' 16 code bytes and
-// their 128 scales.  Per block every wave issues exactly five DMA
-// instructions (global_load_lds: lane i's bytes land at the instruction's LDS
-// base + size * i): four activation chunks, and the codes of 64 rows (waves
-// 0, 1) or the scales (waves 2, 3, the same bytes), so one wait count fits
-// every wave; the loads are issued from inline assembly with SGPR bases, so
+// chunks of 8 halves] of activations, the 128 weight rows' code bytes (or
+// F16 weights) and their scales (and Q4_1 mins).  Per block every wave
+// issues the same number of DMA instructions (global_load_lds: lane i's bytes
+// land at the instruction's LDS base + size * i): four activation chunks and
+// its share of the weight data (DmaW), so one wait count fits every wave;
+// the loads are issued from inline assembly with SGPR bases, so
 // the compiler adds no waits of its own, and no register load is in flight
 // across the block loop.  The chunks of activation row r are stored in the
 // order q ^ swz(r), swz(r) = ((r >> 1) ^ (r >> 3)) & 3: the 16-byte reads of
@@ -460,10 +322,21 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int NS>
-__device__ __forceinline__ void gemm_q4_dma(const GemmArgs &a) {
-  constexpr int ASTAGE = 2 * 128 * 32 * 2;            // bytes
-  constexpr int STAGE = ASTAGE + 128 * 16 + 128 * 2;  // bytes
+// Weight bytes of one row and block in the stage: Q4_0 / Q4_1 16 code bytes,
+// Q8_0 32, F16 64 (the fp16 weights); per-block scales (and Q4_1 mins) follow.
+template <int TYPE> struct DmaW {
+  static constexpr int CB = TYPE == PBX_F16 ? 64 : TYPE == PBX_Q8 ? 32 : 16;
+  static constexpr int CODES = 128 * CB;                  // bytes of a stage
+  static constexpr int NSC = TYPE == PBX_F16 ? 0 : TYPE == PBX_Q41 ? 2 : 1;  // 256-byte planes
+  static constexpr int WD = TYPE == PBX_Q8 || TYPE == PBX_F16 ? 2 : 1;      // weight DMAs a wave
+};
+
+template <int TYPE, int NS>
+__device__ __forceinline__ void gemm_dma(const GemmArgs &a) {
+  typedef DmaW<TYPE> W;
+  constexpr int ASTAGE = 2 * 128 * 32 * 2;                        // bytes
+  constexpr int STAGE = ASTAGE + W::CODES + 256 * W::NSC;         // bytes
+  constexpr int PER = 4 + W::WD;                                  // DMA instructions a wave and block
   __shared__ __attribute__((aligned(1024))) uint8_t S[NS * STAGE];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR bases
@@ -496,33 +369,67 @@ __device__ __forceinline__ void gemm_q4_dma(const GemmArgs &a) {
     }
     const uint8_t *xhi = reinterpret_cast<const uint8_t *>(a.X16 + (size_t)mblk * K);
     const uint8_t *xlo = reinterpret_cast<const uint8_t *>(a.X16lo + (size_t)mblk * K);
-    // weight DMA: waves 0, 1 the codes of 64 rows each; waves 2, 3 the scales
-    const bool codes = wave < 2;
-    const uint8_t *wbase;
-    unsigned wvoff;
-    // (bases at the workgroup's first row, so the per-lane offsets stay small)
-    if (codes) {
-      const int n = min(blockIdx.x * 128 + wave * 64 + lane, a.Npad - 1) - blockIdx.x * 128;
-      wbase = a.qs + (size_t)blockIdx.x * 128 * a.B * 16;
-      wvoff = (unsigned)(n * a.B * 16);
-    } else {
+    // Weight DMAs of this wave (bases at the workgroup's first row, so the
+    // per-lane offsets stay small).  Code DMA d moves 1 KB: rows
+    // (1024 / CB) d + lane / (CB / 16), 16-byte chunk lane % (CB / 16), into
+    // the row-major [128][CB] code area.  A plane DMA moves the 128 rows'
+    // fp16 scales (or Q4_1 mins): lane i takes dword i & 1 of four-row group
+    // i >> 1.  Q4_0: waves 0, 1 codes, waves 2, 3 scales (the same bytes);
+    // Q4_1: waves 0, 1 codes, wave 2 scales, wave 3 mins; Q8_0: codes d = wave
+    // and the scales; F16: codes d = 2 wave, 2 wave + 1.
+    const uint8_t *wb[2];
+    unsigned wv[2], wl[2];
+    int wstep[2], wsz[2];
+    const size_t rowbytes = (size_t)a.B * W::CB;
+    auto code_dma = [&](int k, int d) {
+      const int per_row = W::CB / 16;
+      const int n = min(blockIdx.x * 128 + (1024 / W::CB) * d + lane / per_row, a.Npad - 1) - blockIdx.x * 128;
+      wb[k] = a.qs + (size_t)blockIdx.x * 128 * rowbytes;
+      wv[k] = (unsigned)(n * rowbytes + (lane % per_row) * 16);
+      wl[k] = ASTAGE + d * 1024;
+      wstep[k] = W::CB;
+      wsz[k] = 16;
+    };
+    auto plane_dma = [&](int k, const uint16_t *plane, int which) {
       const int g = min(blockIdx.x * 32 + (lane >> 1), a.Npad / 4 - 1) - blockIdx.x * 32;
-      wbase = reinterpret_cast<const uint8_t *>(a.dsc) + (size_t)blockIdx.x * 32 * a.B * 8;
-      wvoff = (unsigned)(g * a.B * 8 + (lane & 1) * 4);
+      wb[k] = reinterpret_cast<const uint8_t *>(plane) + (size_t)blockIdx.x * 32 * a.B * 8;
+      wv[k] = (unsigned)(g * a.B * 8 + (lane & 1) * 4);
+      wl[k] = ASTAGE + W::CODES + 256 * which;
+      wstep[k] = 8;
+      wsz[k] = 4;
+    };
+    if constexpr (TYPE == PBX_Q4) {
+      if (wave < 2) code_dma(0, wave);
+      else plane_dma(0, a.dsc, 0);
+    } else if constexpr (TYPE == PBX_Q41) {
+      if (wave < 2) code_dma(0, wave);
+      else if (wave == 2) plane_dma(0, a.dsc, 0);
+      else plane_dma(0, a.msc, 1);
+    } else if constexpr (TYPE == PBX_Q8) {
+      code_dma(0, wave);
+      plane_dma(1, a.dsc, 0);
+    } else {
+      code_dma(0, 2 * wave);
+      code_dma(1, 2 * wave + 1);
     }
-    const unsigned lds0 = __builtin_amdgcn_readfirstlane(lds_addr(&S[0]) + wave * 1024);
-    const unsigned ldsw = __builtin_amdgcn_readfirstlane(
-        lds_addr(&S[0]) + ASTAGE + (codes ? wave * 1024 : 2048));
+    const unsigned lbase = lds_addr(&S[0]);
+    const unsigned lds0 = __builtin_amdgcn_readfirstlane(lbase + wave * 1024);
+    unsigned ldw[2];
+#pragma unroll
+    for (int k = 0; k < W::WD; ++k) ldw[k] = __builtin_amdgcn_readfirstlane(lbase + wl[k]);
     auto dma = [&](int b, int stage) {
       const unsigned so = stage * STAGE;
       dma_to_lds_s<16>(xhi + b * 64, avoff[0], lds0 + so);
       dma_to_lds_s<16>(xhi + b * 64, avoff[1], lds0 + so + 4096);
       dma_to_lds_s<16>(xlo + b * 64, avoff[0], lds0 + so + 8192);
       dma_to_lds_s<16>(xlo + b * 64, avoff[1], lds0 + so + 12288);
-      if (codes)
-        dma_to_lds_s<16>(wbase + (size_t)b * 16, wvoff, ldsw + so);
-      else
-        dma_to_lds_s<4>(wbase + (size_t)b * 8, wvoff, ldsw + so);
+#pragma unroll
+      for (int k = 0; k < W::WD; ++k) {
+        if (wsz[k] == 16)
+          dma_to_lds_s<16>(wb[k] + (size_t)b * wstep[k], wv[k], ldw[k] + so);
+        else
+          dma_to_lds_s<4>(wb[k] + (size_t)b * wstep[k], wv[k], ldw[k] + so);
+      }
     };
     // this lane's read offsets in a stage
     const uint8_t *rbase = &S[0];
@@ -534,13 +441,9 @@ __device__ __forceinline__ void gemm_q4_dma(const GemmArgs &a) {
         const int r = m0 + 32 * t + lr;
         aoff[t][j] = (r * 32 + (((2 * j + h) ^ a_swz(r)) * 8)) * 2;
       }
-    int wofs[2], sofs[2];
+    int sofs[2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int nl = wn * 64 + 32 * u + lr;
-      wofs[u] = ASTAGE + nl * 16 + 8 * h;
-      sofs[u] = ASTAGE + 128 * 16 + nl * 2;
-    }
+    for (int u = 0; u < 2; ++u) sofs[u] = ASTAGE + W::CODES + (wn * 64 + 32 * u + lr) * 2;
 
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) dma(min(b0 + s, b1 - 1), s);
@@ -550,18 +453,32 @@ __device__ __forceinline__ void gemm_q4_dma(const GemmArgs &a) {
       for (int s = 0; s < NS; ++s) {
         const int b = kb + s;
         if (b >= b1) break;
-        wait_vm<(NS - 2) * 5>();
+        wait_vm<(NS - 2) * PER>();
         lds_barrier();
         dma(min(b + NS - 1, b1 - 1), s == 0 ? NS - 1 : s - 1);
         const uint8_t *sb = rbase + s * STAGE;
         half8 B0[2], B1[2];
-        float d[2];
+        float d[2], mn[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          const uint2 raw = *reinterpret_cast<const uint2 *>(sb + wofs[u]);
-          B0[u] = codes_operand<PBX_Q4>(raw, 0);
-          B1[u] = codes_operand<PBX_Q4>(raw, 2);
-          d[u] = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(sb + sofs[u]));
+          const uint8_t *wr = sb + ASTAGE + (wn * 64 + 32 * u + lr) * W::CB;
+          if constexpr (TYPE == PBX_F16) {
+            B0[u] = *reinterpret_cast<const half8 *>(wr + 16 * h);
+            B1[u] = *reinterpret_cast<const half8 *>(wr + 32 + 16 * h);
+            d[u] = 1.f;
+          } else {
+            if constexpr (TYPE == PBX_Q8) {
+              B0[u] = codes_operand<PBX_Q8>(*reinterpret_cast<const uint2 *>(wr + 8 * h), 0);
+              B1[u] = codes_operand<PBX_Q8>(*reinterpret_cast<const uint2 *>(wr + 16 + 8 * h), 0);
+            } else {
+              const uint2 raw = *reinterpret_cast<const uint2 *>(wr + 8 * h);
+              B0[u] = codes_operand<TYPE>(raw, 0);  // low nibbles
+              B1[u] = codes_operand<TYPE>(raw, 2);  // high nibbles
+            }
+            d[u] = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(sb + sofs[u]));
+          }
+          mn[u] = TYPE == PBX_Q41 ? f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(sb + sofs[u] + 256))
+                                  : 0.f;
         }
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -569,14 +486,35 @@ __device__ __forceinline__ void gemm_q4_dma(const GemmArgs &a) {
           const half8 Ah1 = *reinterpret_cast<const half8 *>(sb + aoff[t][1]);
           const half8 Al0 = *reinterpret_cast<const half8 *>(sb + 128 * 64 + aoff[t][0]);
           const half8 Al1 = *reinterpret_cast<const half8 *>(sb + 128 * 64 + aoff[t][1]);
+          floatx16 xs = zero16;
+          if constexpr (TYPE == PBX_Q41) {
+            // the block sums of the activation rows: the product with all-ones weights
+            half8 ones;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.f;
+            xs = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah0, ones, xs, 0, 0, 0);
+            xs = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al0, ones, xs, 0, 0, 0);
+            xs = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah1, ones, xs, 0, 0, 0);
+            xs = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al1, ones, xs, 0, 0, 0);
+          }
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            floatx16 blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah0, B0[u], zero16, 0, 0, 0);
-            blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al0, B0[u], blk, 0, 0, 0);
-            blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah1, B1[u], blk, 0, 0, 0);
-            blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al1, B1[u], blk, 0, 0, 0);
+            if constexpr (TYPE == PBX_F16) {
+              acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah0, B0[u], acc[t][u], 0, 0, 0);
+              acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al0, B0[u], acc[t][u], 0, 0, 0);
+              acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah1, B1[u], acc[t][u], 0, 0, 0);
+              acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al1, B1[u], acc[t][u], 0, 0, 0);
+            } else {
+              floatx16 blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah0, B0[u], zero16, 0, 0, 0);
+              blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al0, B0[u], blk, 0, 0, 0);
+              blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah1, B1[u], blk, 0, 0, 0);
+              blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al1, B1[u], blk, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[t][u][r] = fmaf(blk[r], d[u], acc[t][u][r]);
+              for (int r = 0; r < 16; ++r) {
+                acc[t][u][r] = fmaf(blk[r], d[u], acc[t][u][r]);
+                if constexpr (TYPE == PBX_Q41) acc[t][u][r] = fmaf(xs[r], mn[u], acc[t][u][r]);
+              }
+            }
           }
         }
       }
@@ -608,7 +546,10 @@ __device__ __forceinline__ void gemm_q4_dma(const GemmArgs &a) {
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_big(GemmArgs a) { gemm_q4_dma<3>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_big(GemmArgs a) { gemm_dma<PBX_Q4, 3>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q8_big(GemmArgs a) { gemm_dma<PBX_Q8, 3>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q41_big(GemmArgs a) { gemm_dma<PBX_Q41, 3>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_f16_big(GemmArgs a) { gemm_dma<PBX_F16, 3>(a); }
 
 // Row scaling to fp16: one workgroup per (padded) row.  The scale is
 // 2^(15 - e) with 2^(e-1) <= max|x| < 2^e, so every scaled value is below
