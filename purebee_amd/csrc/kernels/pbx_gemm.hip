@@ -893,3 +893,134 @@ GEMM_F32_KERNEL(pbx_gemm_f32_m1_n2, 1, 2, 2)
 GEMM_F32_KERNEL(pbx_gemm_f32_m1_n4, 1, 4, 2)
 GEMM_F32_KERNEL(pbx_gemm_f32_m2_n2, 2, 2, 2)
 GEMM_F32_KERNEL(pbx_gemm_f32_m4_n4, 4, 4, 1)
+
+// F32 weights, M > 32: v_mfma_f32_32x32x2f32 (A: lane l holds A[l%32][l/32];
+// B: lane l holds B[l/32][l%32]; D as the f16 32x32 form; checked on the
+// device) with every operand moved to LDS by DMA, the tiling of gemm_dma.
+// A stage covers 16 k: the activation tile [128 rows][4 chunks of 4 floats]
+// and the weight tile [128 rows][4 chunks], chunks stored in the order
+// q ^ swz(row).  Within a group of 8 k (chunks 2g, 2g + 1) lane (r, h)
+// reads chunk 2g + h of its row as one float4 and MFMA i (i < 4) takes its
+// element i, i.e. k = 8g + 4h + i: every k of the group is used once per
+// output.  Each wave issues four DMA instructions a stage (two activation
+// and two weight kilobytes).  Rows past M (activations) or Npad (weights)
+// are clamped.
+template <int NS>
+__device__ __forceinline__ void gemm_f32_dma(const GemmF32Args &a) {
+  constexpr int TILE = 128 * 64;      // bytes of one operand tile
+  constexpr int STAGE = 2 * TILE;     // activations, weights
+  __shared__ __attribute__((aligned(1024))) uint8_t S[NS * STAGE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, h = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n0 = blockIdx.x * 128 + wn * 64;
+  const int mblk = blockIdx.y * 128;
+  const int m0 = wm * 64;
+  const int K = a.B * 32, steps = 2 * a.B;  // 16 k a step
+  const int per = (steps + a.KS - 1) / a.KS;
+  const int s0 = blockIdx.z * per;
+  const int s1 = min(steps, s0 + per);
+  const floatx16 zero16 = {};
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) acc[t][u] = zero16;
+
+  if (s0 < s1) {
+    // DMA k (k = 0, 1) of this wave for each tile: rows 16 (2 wave + k) + lane / 4
+    const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.X) + (size_t)mblk * K * 4;
+    const uint8_t *wb = reinterpret_cast<const uint8_t *>(a.W) + (size_t)blockIdx.x * 128 * K * 4;
+    unsigned xv[2], wv[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int row = 16 * (2 * wave + k) + (lane >> 2), q = (lane & 3) ^ a_swz(row);
+      const int xr = min(mblk + row, a.M - 1) - mblk;
+      const int wr = min(blockIdx.x * 128 + row, a.Npad - 1) - blockIdx.x * 128;
+      xv[k] = (unsigned)((xr * K + 4 * q) * 4);
+      wv[k] = (unsigned)((wr * K + 4 * q) * 4);
+    }
+    const unsigned lbase = lds_addr(&S[0]);
+    const unsigned ldx = __builtin_amdgcn_readfirstlane(lbase + wave * 2048);
+    auto dma = [&](int st, int stage) {
+      const unsigned so = stage * STAGE;
+      const size_t ko = (size_t)st * 64;  // 16 floats
+      dma_to_lds_s<16>(xb + ko, xv[0], ldx + so);
+      dma_to_lds_s<16>(xb + ko, xv[1], ldx + so + 1024);
+      dma_to_lds_s<16>(wb + ko, wv[0], ldx + so + TILE);
+      dma_to_lds_s<16>(wb + ko, wv[1], ldx + so + TILE + 1024);
+    };
+    int aoff[2][2], boff[2][2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int r = m0 + 32 * t + lr;
+        aoff[g][t] = r * 64 + (((2 * g + h) ^ a_swz(r)) * 16);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int r = wn * 64 + 32 * u + lr;
+        boff[g][u] = TILE + r * 64 + (((2 * g + h) ^ a_swz(r)) * 16);
+      }
+    }
+    const uint8_t *rbase = &S[0];
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st) dma(min(s0 + st, s1 - 1), st);
+    for (int kb = s0; kb < s1; kb += NS) {
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        const int b = kb + st;
+        if (b >= s1) break;
+        wait_vm<(NS - 2) * 4>();
+        lds_barrier();
+        dma(min(b + NS - 1, s1 - 1), st == 0 ? NS - 1 : st - 1);
+        const uint8_t *sb = rbase + st * STAGE;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          float4 av[2], bv[2];
+#pragma unroll
+          for (int t = 0; t < 2; ++t) av[t] = *reinterpret_cast<const float4 *>(sb + aoff[g][t]);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) bv[u] = *reinterpret_cast<const float4 *>(sb + boff[g][u]);
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[t].x, bv[u].x, acc[t][u], 0, 0, 0);
+              acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[t].y, bv[u].y, acc[t][u], 0, 0, 0);
+              acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[t].z, bv[u].z, acc[t][u], 0, 0, 0);
+              acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[t].w, bv[u].w, acc[t][u], 0, 0, 0);
+            }
+        }
+      }
+    }
+    wait_vm<0>();
+  }
+
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int n = n0 + 32 * u + lr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = mblk + m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (m < a.M && n < a.N) {
+          const float v = acc[t][u][r];
+          if (a.KS == 1) {
+            float *y = a.Y + (size_t)m * a.N + n;
+            if (a.accumulate)
+              *y += v;
+            else
+              *y = v + (a.bias ? a.bias[n] : 0.f);
+          } else {
+            a.Y[((size_t)blockIdx.z * a.M + m) * a.N + n] = v;
+          }
+        }
+      }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_f32_big(GemmF32Args a) { gemm_f32_dma<3>(a); }

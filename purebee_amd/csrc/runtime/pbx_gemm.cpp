@@ -55,11 +55,33 @@ int launch_reduce(pbx_ctx *c, float *part, const float *dBias, float *dY, int M,
                        args, stream);
 }
 
-// F32 weights: fp32 MFMA, wave tile 16*MT x 16*NT (MT 1 / 2 / 4 for
-// M <= 16 / <= 32 / larger), K split for about eight waves per CU.
+// F32 weights: fp32 MFMA.  M > 32: the LDS-DMA 128 x 128 kernel; otherwise
+// wave tile 16*MT x 16*NT (MT 1 / 2 for M <= 16 / <= 32), K split for about
+// eight waves per CU.
 int launch_f32(pbx_ctx *c, const pbx_weight *w, const float *dX, int M, const float *dBias,
                float *dY, int accumulate, hipStream_t stream) {
   const int N = (int)w->N, B = (int)w->B;
+  if (M > 32) {
+    // 128 x 128 tiles on the LDS-DMA kernel, K split (16-k steps) for about
+    // one workgroup per CU
+    const int nwg = (N + 127) / 128, mtiles = (M + 127) / 128, wgs = nwg * mtiles;
+    int KS = 1;
+    if (wgs < c->cu_count) KS = std::min({2 * B, 8, (c->cu_count + wgs - 1) / wgs});
+    float *part = nullptr;
+    if (KS > 1) {
+      int rc = pbx_ensure_dev(c, &c->d_gemm, &c->d_gemm_cap, (size_t)KS * M * N * 4);
+      if (rc) return rc;
+      part = (float *)c->d_gemm;
+    }
+    hipFunction_t fg = pbx_kernel_by_name(c, "pbx_gemm_f32_big");
+    if (!fg) return pbx_fail(c, PBX_ELOAD, "pbx_gemm: kernel pbx_gemm_f32_big missing");
+    GemmF32ArgsHost g{w->qs, dX, KS == 1 ? dBias : nullptr, KS == 1 ? dY : part,
+                      M, N, (int)w->Npad, B, KS, KS == 1 ? accumulate : 0};
+    void *args[] = {&g};
+    int rc = pbx_launch_fn(c, fg, "pbx_gemm_f32_big", dim3(nwg, mtiles, KS), dim3(256), args, stream);
+    if (rc || KS == 1) return rc;
+    return launch_reduce(c, part, dBias, dY, M, N, KS, accumulate, stream);
+  }
   const int MT = M <= 16 ? 1 : M <= 32 ? 2 : 4;
   const int mtiles = (M + 16 * MT - 1) / (16 * MT);
   int NT;
