@@ -780,7 +780,9 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   __shared__ uint64_t kred[WV];
 
   const int N = a.N, B = a.B, K = B * 32;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
+  const int lane = threadIdx.x & 63, tid = threadIdx.x;
+  // wave-uniform (SGPR): row bases and weight addresses are scalar arithmetic
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int NO = PAIR ? N / 2 : N;
   const int rows = MR == 1 ? 1 : a.rows;  // valid activation rows
   constexpr int RTO = PAIR ? RT / 2 : RT;  // output rows a wave
