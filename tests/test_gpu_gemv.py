@@ -324,7 +324,7 @@ def test_error_paths_on_device(ctx):
 
 
 GEMM_SHAPES = [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192), (576, 576), (1536, 576),
-               (576, 1536), (288, 288), (768, 288), (288, 768), (100, 64)]
+               (576, 1536), (288, 288), (768, 288), (288, 768), (100, 64), (64, 32)]
 
 
 def weight_bytes(t, W):
@@ -336,7 +336,7 @@ def weight_bytes(t, W):
 
 
 @pytest.mark.parametrize("t", QUANT + [pb.TYPE_F16, pb.TYPE_F32])
-@pytest.mark.parametrize("M", [4, 5, 17, 64, 130])
+@pytest.mark.parametrize("M", [4, 5, 17, 33, 64, 130])
 @pytest.mark.parametrize("N,K", GEMM_SHAPES)
 def test_mfma_gemm_parity(ctx, t, M, N, K):
     """M >= 4 takes the MFMA path (exact integer weight codes or fp16
