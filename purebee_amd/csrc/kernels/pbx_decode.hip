@@ -117,8 +117,6 @@ DK_INT_LMHL(PBX_Q6K, q6k, 4, 2, 1)
 DK_INT_ROWS(PBX_Q4, q4, 8, 2, 1, 8, false, , PRO_RMSNORM, EPI_STORE, qkv)
 DK_INT_ROWS(PBX_Q4, q4, 8, 1, 1, 8, false, , PRO_NONE, EPI_ADD, add)
 DK_INT_ROWS(PBX_Q4, q4, 8, 1, 4, 5, false, , PRO_NONE, EPI_ADD, add)  // LDS: 5 rows x 24 KB
-DK_INT_ROWS(PBX_Q4, q4, 8, 4, 1, 8, false, , PRO_RMSNORM, EPI_SWIGLU, gu)
-DK_INT_ROWS(PBX_Q4, q4, 8, 2, 1, 8, true, l, PRO_RMSNORM, EPI_STORE, lmh)
 
 DK_MODES_WIDE(PBX_F32, f32, 2)
 DK_MODES_WIDE(PBX_F32, f32, 4)

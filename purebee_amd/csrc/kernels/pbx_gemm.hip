@@ -1024,3 +1024,279 @@ __device__ __forceinline__ void gemm_f32_dma(const GemmF32Args &a) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) pbx_gemm_f32_big(GemmF32Args a) { gemm_f32_dma<3>(a); }
+
+// ---------------------------------------------------------------------------
+// Skinny Q4_0 GEMM for 1..8 activation rows (speculative verify, short
+// batches): the rows of a layer input are normalised once per workgroup
+// (RMSNorm when normw is given), scaled per row by a power of two and held in
+// LDS as fp16 pairs (hi, lo) in chunks of SK_KC columns; the weights stream
+// through v_mfma_f32_32x32x16_f16 (operand layout of gemm_dma) 32 weight rows
+// a tile, the four waves of a workgroup splitting the tile's blocks.  A rows
+// 8..31 of the MFMA read an all-zero LDS row, so of a lane's 16 outputs only
+// registers 0..3 (activation rows 4h + r) carry results and take the block
+// scale.  Epilogues: store, add (residual) or SwiGLU of the gate|up pair
+// (a tile holds 16 gate and the matching 16 up rows).  K above SK_KC runs one
+// tile per workgroup, the chunks converted in turn.
+// ---------------------------------------------------------------------------
+#define SK_MR 8
+#define SK_KC 2048
+#define SK_LD (SK_KC + 8)  // halves per LDS row
+
+struct SkinnyArgs {
+  const uint8_t *qs;     // Q4_0 code plane [Npad][B][16]
+  const uint16_t *dsc;   // fp16 scales (4-row groups)
+  const float *X;        // [M][K]
+  const float *normw;    // [K] or null
+  float *Y;              // [M][ldy]
+  int N, B, M, ldy;
+  float eps;
+};
+
+enum { SK_STORE = 0, SK_ADD = 1, SK_SWIGLU = 2 };
+
+template <int EPI>
+__device__ __forceinline__ void skinny_q4(const SkinnyArgs &a) {
+  __shared__ __attribute__((aligned(16))) _Float16 Ah[SK_MR + 1][SK_LD], Al[SK_MR + 1][SK_LD];
+  __shared__ float rs_scale[SK_MR], rs_inv[SK_MR], rs_norm[SK_MR];
+  __shared__ float wred[4][SK_MR][2];
+  __shared__ float tred[3][64][4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, h = lane >> 5;
+  const int M = a.M, B = a.B, K = B * 32, K4 = K / 4;
+  const bool norm = a.normw != nullptr;
+
+  // 1. per-row statistics: sum of squares (RMSNorm) and the largest |x w|.
+  // Rows of at most SK_KC columns are loaded once into registers (item j of
+  // a thread: row j / 2, float4 column tid + 256 (j % 2)) and converted from
+  // there; longer rows are read twice (statistics, then chunk by chunk).
+  constexpr int IT = SK_MR * SK_KC / 4 / 256;  // 16 float4 items a thread
+  const bool one = K <= SK_KC;
+  float4 xr[IT], gr[2];
+  float ss[SK_MR], mx[SK_MR];
+#pragma unroll
+  for (int m = 0; m < SK_MR; ++m) {
+    ss[m] = 0.f;
+    mx[m] = 0.f;
+  }
+  if (one) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int k4 = tid + 256 * q;
+      gr[q] = norm && k4 < K4 ? reinterpret_cast<const float4 *>(a.normw)[k4] : make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+#pragma unroll
+    for (int j = 0; j < IT; ++j) {
+      const int m = j >> 1, k4 = tid + 256 * (j & 1);
+      xr[j] = m < M && k4 < K4 ? reinterpret_cast<const float4 *>(a.X + (size_t)m * K)[k4]
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < IT; ++j) {
+      const int m = j >> 1;
+      const float4 x = xr[j], g = gr[j & 1];
+      ss[m] = fmaf(x.x, x.x, fmaf(x.y, x.y, fmaf(x.z, x.z, fmaf(x.w, x.w, ss[m]))));
+      mx[m] = fmaxf(mx[m], fmaxf(fmaxf(fabsf(x.x * g.x), fabsf(x.y * g.y)),
+                                 fmaxf(fabsf(x.z * g.z), fabsf(x.w * g.w))));
+    }
+  } else {
+#pragma unroll 4
+    for (int k = tid; k < K4; k += 256) {
+      const float4 g = norm ? reinterpret_cast<const float4 *>(a.normw)[k] : make_float4(1.f, 1.f, 1.f, 1.f);
+#pragma unroll
+      for (int m = 0; m < SK_MR; ++m) {
+        if (m < M) {
+          const float4 x = reinterpret_cast<const float4 *>(a.X + (size_t)m * K)[k];
+          ss[m] = fmaf(x.x, x.x, fmaf(x.y, x.y, fmaf(x.z, x.z, fmaf(x.w, x.w, ss[m]))));
+          mx[m] = fmaxf(mx[m], fmaxf(fmaxf(fabsf(x.x * g.x), fabsf(x.y * g.y)),
+                                     fmaxf(fabsf(x.z * g.z), fabsf(x.w * g.w))));
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < SK_MR; ++m) {
+    const float s = wave_sum(ss[m]), x = wave_max(mx[m]);
+    if (lane == 0) {
+      wred[wave][m][0] = s;
+      wred[wave][m][1] = x;
+    }
+  }
+  __syncthreads();
+  if (tid < SK_MR) {
+    const int m = tid;
+    const float s = (wred[0][m][0] + wred[1][m][0]) + (wred[2][m][0] + wred[3][m][0]);
+    const float x = fmaxf(fmaxf(wred[0][m][1], wred[1][m][1]), fmaxf(wred[2][m][1], wred[3][m][1]));
+    const float r = norm ? 1.0f / sqrtf(s / (float)K + a.eps) : 1.f;
+    const float vmax = x * r;  // the row's largest magnitude after normalisation
+    int e = 0;
+    if (vmax > 0.f && vmax < INFINITY) frexpf(vmax, &e);
+    rs_norm[m] = r;
+    rs_scale[m] = vmax > 0.f ? ldexpf(1.f, 15 - e) : 1.f;
+    rs_inv[m] = vmax > 0.f ? ldexpf(1.f, e - 15) : 1.f;
+  }
+  // the zero row that MFMA rows 8..31 (and rows past M) read
+  for (int k = tid; k < SK_LD; k += 256) {
+    Ah[SK_MR][k] = (_Float16)0.f;
+    Al[SK_MR][k] = (_Float16)0.f;
+  }
+
+  const int NO = EPI == SK_SWIGLU ? a.N / 2 : a.N;
+  const int per_tile = EPI == SK_SWIGLU ? 16 : 32;
+  const int ntiles = (NO + per_tile - 1) / per_tile;
+  const int nchunks = (K + SK_KC - 1) / SK_KC;
+  const int arow = lr < M ? lr : SK_MR;  // LDS row of this lane's A operand
+  constexpr int BPW = SK_KC / 32 / 4;     // blocks of a chunk per wave
+
+  // weight row of this lane's column in tile t
+  auto tile_row = [&](int t) -> int {
+    int n;
+    if constexpr (EPI == SK_SWIGLU)
+      n = lr < 16 ? per_tile * t + lr : a.N / 2 + per_tile * t + lr - 16;
+    else
+      n = per_tile * t + lr;
+    return min(n, a.N - 1);
+  };
+  // the wave's blocks cb0 + wave + 4 i of chunk [cb0, cb1) of row n, all
+  // requested at once (blocks past cb1 re-read the last one; not used)
+  auto load_blocks = [&](int n, int cb0, int cb1, uint2 (&raw)[BPW], unsigned (&db)[BPW]) {
+    const uint8_t *wrow = a.qs + (size_t)n * B * 16 + 8 * h;
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+      const int b = min(cb0 + wave + 4 * i, cb1 - 1);
+      raw[i] = *reinterpret_cast<const uint2 *>(wrow + (size_t)b * 16);
+      db[i] = a.dsc[dsc_index(n, b, B)];
+    }
+  };
+  auto mma_blocks = [&](int cb0, int cb1, const uint2 (&raw)[BPW], const unsigned (&db)[BPW],
+                        float (&acc)[4]) {
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+      const int b = cb0 + wave + 4 * i;
+      if (b < cb1) {
+        const half8 B0 = codes_operand<PBX_Q4>(raw[i], 0), B1 = codes_operand<PBX_Q4>(raw[i], 2);
+        const int kk = (b - cb0) * 32 + 8 * h;
+        const half8 Ah0 = *reinterpret_cast<const half8 *>(&Ah[arow][kk]);
+        const half8 Ah1 = *reinterpret_cast<const half8 *>(&Ah[arow][kk + 16]);
+        const half8 Al0 = *reinterpret_cast<const half8 *>(&Al[arow][kk]);
+        const half8 Al1 = *reinterpret_cast<const half8 *>(&Al[arow][kk + 16]);
+        const floatx16 zero16 = {};
+        floatx16 blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah0, B0, zero16, 0, 0, 0);
+        blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al0, B0, blk, 0, 0, 0);
+        blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah1, B1, blk, 0, 0, 0);
+        blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al1, B1, blk, 0, 0, 0);
+        const float d = f16_bits_to_f32(db[i]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(blk[r], d, acc[r]);
+      }
+      // one block at a time: unpacking every block's operands up front
+      // would need more registers than two waves a SIMD have
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // one float4 item (row m, columns k .. k+3 of the chunk) into LDS:
+  // the RMSNorm product of pbx_rmsnorm_rows, then the exact power-of-two scale
+  auto put = [&](int m, int k, float4 x, float4 g) {
+    half4v hv = {}, lv = {};
+    if (m < M) {
+      const float r = rs_norm[m], sc = rs_scale[m];
+      const float v0 = (x.x * r) * g.x * sc, v1 = (x.y * r) * g.y * sc;
+      const float v2 = (x.z * r) * g.z * sc, v3 = (x.w * r) * g.w * sc;
+      hv[0] = (_Float16)v0; hv[1] = (_Float16)v1; hv[2] = (_Float16)v2; hv[3] = (_Float16)v3;
+      lv[0] = (_Float16)(v0 - (float)hv[0]); lv[1] = (_Float16)(v1 - (float)hv[1]);
+      lv[2] = (_Float16)(v2 - (float)hv[2]); lv[3] = (_Float16)(v3 - (float)hv[3]);
+    }
+    *reinterpret_cast<half4v *>(&Ah[m][k]) = hv;
+    *reinterpret_cast<half4v *>(&Al[m][k]) = lv;
+  };
+  // chunk c of the activation rows into LDS (a full chunk: the items of
+  // xr, from registers for K <= SK_KC, else loaded here in one batch)
+  auto convert = [&](int c) {
+    const int k0 = c * SK_KC;
+    __syncthreads();  // rs_* are written; earlier reads of the chunk buffer are done
+    if (!one) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        gr[q] = norm ? reinterpret_cast<const float4 *>(a.normw + k0)[tid + 256 * q]
+                     : make_float4(1.f, 1.f, 1.f, 1.f);
+#pragma unroll
+      for (int j = 0; j < IT; ++j) {
+        const int m = j >> 1, k4 = tid + 256 * (j & 1);
+        xr[j] = m < M ? reinterpret_cast<const float4 *>(a.X + (size_t)m * K + k0)[k4]
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    const int kc4 = min(SK_KC, K - k0) / 4;
+#pragma unroll
+    for (int j = 0; j < IT; ++j) {
+      const int m = j >> 1, k4 = tid + 256 * (j & 1);
+      if (k4 < kc4) put(m, 4 * k4, xr[j], gr[j & 1]);
+    }
+    __syncthreads();
+  };
+  // the four waves' partial sums of tile t; wave 0 applies the epilogue
+  auto finish = [&](int t, float (&acc)[4]) {
+    if (wave > 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tred[wave - 1][lane][r] = acc[r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] += (tred[0][lane][r] + tred[1][lane][r]) + tred[2][lane][r];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * h + r;
+        const float v = acc[r] * rs_inv[m];
+        const int col = per_tile * t + lr;
+        if constexpr (EPI == SK_SWIGLU) {
+          const float u = __shfl(v, (lane & 32) | ((lr + 16) & 31), 64);  // the up row of this gate column
+          if (lr < 16 && m < M && col < NO) a.Y[(size_t)m * a.ldy + col] = silu(v) * u;
+        } else {
+          if (m < M && col < NO) {
+            float *y = a.Y + (size_t)m * a.ldy + col;
+            if constexpr (EPI == SK_ADD)
+              *y += v;
+            else
+              *y = v;
+          }
+        }
+      }
+    }
+    __syncthreads();  // tred is reused by the next tile
+  };
+
+  uint2 rawA[BPW];
+  unsigned dA[BPW];
+  if (nchunks == 1) {
+    // whole rows in LDS once, then tiles t, t + G, ...: all of a tile's
+    // blocks requested at once (two workgroups a CU overlap the tiles)
+    const int G = gridDim.x, cb1 = B;
+    int t = blockIdx.x;
+    if (t >= ntiles) return;
+    convert(0);
+    for (; t < ntiles; t += G) {
+      load_blocks(tile_row(t), 0, cb1, rawA, dA);
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      mma_blocks(0, cb1, rawA, dA, acc);
+      finish(t, acc);
+    }
+  } else {
+    // one tile a workgroup (grid = tiles), chunk by chunk
+    const int t = blockIdx.x;
+    if (t >= ntiles) return;
+    const int n = tile_row(t);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < nchunks; ++c) {
+      const int cb0 = c * (SK_KC / 32), cb1 = min(B, cb0 + SK_KC / 32);
+      load_blocks(n, cb0, cb1, rawA, dA);
+      convert(c);
+      mma_blocks(cb0, cb1, rawA, dA, acc);
+    }
+    finish(t, acc);
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256, 2) pbx_sk_q4_store(SkinnyArgs a) { skinny_q4<SK_STORE>(a); }
+extern "C" __global__ void __launch_bounds__(256, 2) pbx_sk_q4_add(SkinnyArgs a) { skinny_q4<SK_ADD>(a); }
+extern "C" __global__ void __launch_bounds__(256, 2) pbx_sk_q4_swiglu(SkinnyArgs a) { skinny_q4<SK_SWIGLU>(a); }
