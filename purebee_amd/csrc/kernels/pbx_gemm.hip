@@ -1214,19 +1214,22 @@ __device__ __forceinline__ void skinny_q4(const SkinnyArgs &a) {
   auto convert = [&](int c) {
     const int k0 = c * SK_KC;
     __syncthreads();  // rs_* are written; earlier reads of the chunk buffer are done
+    const int kc4 = min(SK_KC, K - k0) / 4;
     if (!one) {
+      // a last chunk may be shorter than SK_KC: columns past it are not read
 #pragma unroll
-      for (int q = 0; q < 2; ++q)
-        gr[q] = norm ? reinterpret_cast<const float4 *>(a.normw + k0)[tid + 256 * q]
-                     : make_float4(1.f, 1.f, 1.f, 1.f);
+      for (int q = 0; q < 2; ++q) {
+        const int k4 = tid + 256 * q;
+        gr[q] = norm && k4 < kc4 ? reinterpret_cast<const float4 *>(a.normw + k0)[k4]
+                                 : make_float4(1.f, 1.f, 1.f, 1.f);
+      }
 #pragma unroll
       for (int j = 0; j < IT; ++j) {
         const int m = j >> 1, k4 = tid + 256 * (j & 1);
-        xr[j] = m < M ? reinterpret_cast<const float4 *>(a.X + (size_t)m * K + k0)[k4]
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        xr[j] = m < M && k4 < kc4 ? reinterpret_cast<const float4 *>(a.X + (size_t)m * K + k0)[k4]
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
-    const int kc4 = min(SK_KC, K - k0) / 4;
 #pragma unroll
     for (int j = 0; j < IT; ++j) {
       const int m = j >> 1, k4 = tid + 256 * (j & 1);
@@ -1298,5 +1301,4 @@ __device__ __forceinline__ void skinny_q4(const SkinnyArgs &a) {
 }
 
 extern "C" __global__ void __launch_bounds__(256, 2) pbx_sk_q4_store(SkinnyArgs a) { skinny_q4<SK_STORE>(a); }
-extern "C" __global__ void __launch_bounds__(256, 2) pbx_sk_q4_add(SkinnyArgs a) { skinny_q4<SK_ADD>(a); }
 extern "C" __global__ void __launch_bounds__(256, 2) pbx_sk_q4_swiglu(SkinnyArgs a) { skinny_q4<SK_SWIGLU>(a); }
