@@ -347,7 +347,12 @@ struct HeadChunk {
   float4 v[16];
 };
 
-extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_head(AttnArgs a) {
+// ROWS: one row of a batch whose q is already rotated and whose k, v are
+// already in the cache at every position up to pos (pbx_rope_append_rows):
+// no RoPE, no new-row substitution and no append; a.qkv and a.out point at
+// the row, the position comes from the caller.
+template <bool ROWS>
+__device__ __forceinline__ void attention_head_body(const AttnArgs &a, const int pos) {
   __shared__ float wm[PBX_HA_WAVES], wl[PBX_HA_WAVES];
   __shared__ __attribute__((aligned(16))) float wacc[PBX_HA_WAVES][PBX_HA_MAX_HD];
   constexpr int CH = PBX_HA_WAVES * 64;  // positions per chunk
@@ -355,7 +360,7 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
   const int Gq = a.n_heads / a.n_kv_heads, g = h / Gq;
   const int dim = a.n_heads * hd, kvdim = a.n_kv_heads * hd;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int pos = a.state[0], L = pos + 1;
+  const int L = pos + 1;
   float *kb = a.kcache + (size_t)g * hd, *vb = a.vcache + (size_t)g * hd;
   const int dg = lane & 15, ps = lane >> 4;  // dim group, position slot
   const int dcol = 4 * min(dg, hd4 - 1);     // clamped for head_dim < 64
@@ -381,17 +386,20 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
   if (wact) load_chunk(0, first);
 
   // 2. the lane's dims of q, the new k and v, and their RoPE pairs
-  const float4 cs = *reinterpret_cast<const float4 *>(a.rope + (size_t)pos * hd + dcol);
+  const float4 cs = ROWS ? make_float4(1.f, 0.f, 1.f, 0.f)
+                        : *reinterpret_cast<const float4 *>(a.rope + (size_t)pos * hd + dcol);
   const float4 qv = *reinterpret_cast<const float4 *>(a.qkv + (size_t)h * hd + dcol);
-  const float4 kv = *reinterpret_cast<const float4 *>(a.qkv + dim + (size_t)g * hd + dcol);
-  const float4 vnw =
-      *reinterpret_cast<const float4 *>(a.qkv + dim + kvdim + (size_t)g * hd + dcol);
+  const float4 kv = ROWS ? make_float4(0.f, 0.f, 0.f, 0.f)
+                         : *reinterpret_cast<const float4 *>(a.qkv + dim + (size_t)g * hd + dcol);
+  const float4 vnw = ROWS ? make_float4(0.f, 0.f, 0.f, 0.f)
+                          : *reinterpret_cast<const float4 *>(a.qkv + dim + kvdim + (size_t)g * hd + dcol);
   __builtin_amdgcn_sched_barrier(0);
 
   // 3. RoPE (adjacent pairs, llama.js:163-190) of the lane's q and new-k
   //    dims; q . (new k) summed over the 16 lanes of a row
-  float4 qq = make_float4(qv.x * cs.x - qv.y * cs.y, qv.x * cs.y + qv.y * cs.x,
-                          qv.z * cs.z - qv.w * cs.w, qv.z * cs.w + qv.w * cs.z);
+  float4 qq = ROWS ? qv
+                   : make_float4(qv.x * cs.x - qv.y * cs.y, qv.x * cs.y + qv.y * cs.x,
+                                 qv.z * cs.z - qv.w * cs.w, qv.z * cs.w + qv.w * cs.z);
   const float4 knw = make_float4(kv.x * cs.x - kv.y * cs.y, kv.x * cs.y + kv.y * cs.x,
                                  kv.z * cs.z - kv.w * cs.w, kv.z * cs.w + kv.w * cs.z);
   if (dg >= hd4) qq = make_float4(0.f, 0.f, 0.f, 0.f);  // repeats of the last dims
@@ -412,7 +420,7 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
       s[j] = fmaf(qq.x, ch.k[j].x, fmaf(qq.y, ch.k[j].y, fmaf(qq.z, ch.k[j].z, qq.w * ch.k[j].w)));
     transpose_stage<16, 8, 16>(s, lane);
     const int p = c0 + w * 64 + 4 * dg + ps;
-    const bool valid = p < L, cur = p == pos;
+    const bool valid = p < L, cur = !ROWS && p == pos;
     const float dot = cur ? dnew : s[0];  // position pos: the new k
     const float sc = valid ? dot * a.scale : -INFINITY;
     const float mn = fmaxf(m, wave_max(sc));
@@ -425,7 +433,7 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
     for (int j = 0; j < 16; ++j) {
       const int slot = 4 * j + ps;
       const float pj = __shfl(pr, (lane & 48) | j, 64);  // slot 4j + ps
-      const float4 vj = pw + slot == pos ? vnw : ch.v[j];
+      const float4 vj = !ROWS && pw + slot == pos ? vnw : ch.v[j];
       acc.x = fmaf(pj, vj.x, acc.x);
       acc.y = fmaf(pj, vj.y, acc.y);
       acc.z = fmaf(pj, vj.z, acc.z);
@@ -471,10 +479,28 @@ extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_he
   }
   // 6. the KV-cache append (the group's first head, lanes 0..hd/4-1), last:
   //    every head of the group takes row pos from registers
-  if (h % Gq == 0 && tid < hd4) {
+  if (!ROWS && h % Gq == 0 && tid < hd4) {
     *reinterpret_cast<float4 *>(kb + (size_t)pos * kvdim + dcol) = knw;
     *reinterpret_cast<float4 *>(vb + (size_t)pos * kvdim + dcol) = vnw;
   }
+}
+
+
+extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_head(AttnArgs a) {
+  attention_head_body<false>(a, a.state[0]);
+}
+
+// Batched rows (speculative verify, short batches; head_dim <= 64): workgroup
+// (head, row t) at position start + t, after pbx_rope_append_rows has rotated
+// q and k of every row and appended k and v; the arguments of
+// pbx_attention_rows.
+extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64)
+pbx_attention_head_rows(const float *qkv, float *kcache, float *vcache, float *out, int start,
+                        int n_heads, int n_kv_heads, int head_dim, float scale) {
+  const int t = blockIdx.y, dim = n_heads * head_dim;
+  AttnArgs a{qkv + (size_t)t * (dim + 2 * n_kv_heads * head_dim), kcache, vcache, nullptr,
+             out + (size_t)t * dim, nullptr, n_heads, n_kv_heads, head_dim, scale};
+  attention_head_body<true>(a, start + t);
 }
 
 #define PBX_SPLIT_TILE 32

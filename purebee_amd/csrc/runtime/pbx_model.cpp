@@ -1045,7 +1045,10 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
                         dim3(g.n_heads, (n + 63) / 64), dim3(256), args);
         } else {
           void *args[] = {&qkv, &kc, &vc, &out, &st, &nh, &nkv, &hd, &scale};
-          rc = launch_k(m, "pbx_attention_rows", dim3(g.n_heads, n), dim3(256), args);
+          if (g.head_dim <= 64)
+            rc = launch_k(m, "pbx_attention_head_rows", dim3(g.n_heads, n), dim3(512), args);
+          else
+            rc = launch_k(m, "pbx_attention_rows", dim3(g.n_heads, n), dim3(256), args);
         }
         if (rc) return rc;
       }
@@ -1109,7 +1112,12 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
                       dim3(g.n_heads, (n + 63) / 64), dim3(256), args);
       } else {
         void *args[] = {&qkv, &kc, &vc, &out, &st, &nh, &nkv, &hd, &scale};
-        rc = launch_k(m, "pbx_attention_rows", dim3(g.n_heads, n), dim3(256), args);
+        // head_dim <= 64: the decode kernel's flash layout per (head, row);
+        // the generic one-workgroup-per-(head, row) kernel otherwise
+        if (g.head_dim <= 64)
+          rc = launch_k(m, "pbx_attention_head_rows", dim3(g.n_heads, n), dim3(512), args);
+        else
+          rc = launch_k(m, "pbx_attention_rows", dim3(g.n_heads, n), dim3(256), args);
       }
       if (rc) return rc;
     }
