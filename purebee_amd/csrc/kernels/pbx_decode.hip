@@ -102,8 +102,45 @@ DK_INT_LMH(PBX_Q4, q4, 4, 16, 2)
 DK_INT_LMH(PBX_Q4, q4, 4, 8, 1)
 DK_INT_LMHL(PBX_Q4, q4, 4, 8, 1)
 DK_INT_LMHL(PBX_Q4, q4, 4, 4, 1)
-// Q6_K lm head (the output matrix of llama.cpp Q4_0 files), K = 2048
+// Q6_K lm head (the output matrix of llama.cpp Q4_0 files), K = 2048, on
+// the resident Q6_K layout and on the lane-packed copy
 DK_INT_LMHL(PBX_Q6K, q6k, 4, 2, 1)
+DK_INT_LMHL(PBX_Q6KP, q6kp, 4, 2, 1)
+
+// Lane-packed copy (PBX_Q6KP layout, PBX_Q6KP_ROW bytes per 32-block) of a
+// resident Q6_K matrix of N rows x B 32-blocks: one thread per (row, block)
+// decodes the block's 32 codes from its super-block and writes them back
+// in the lane-major byte order.  d stays in the matrix's scale plane.
+extern "C" __global__ void __launch_bounds__(256)
+pbx_pack_q6_k_lanes(const uint8_t *qs, uint8_t *dst, int N, int B) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)N * B) return;
+  const int n = (int)(i / B), b = (int)(i % B);
+  const uint8_t *blk = qs + ((size_t)n * (B >> 3) + (b >> 3)) * PBX_Q6K_BYTES;
+  const int half = (b >> 2) & 1, g = b & 3;
+  const uint8_t *ql = blk + half * 64 + (g & 1) * 32, *qh = blk + 128 + half * 32;
+  uint8_t code[32];
+#pragma unroll
+  for (int l = 0; l < 32; ++l)
+    code[l] = (uint8_t)(((ql[l] >> (4 * (g >> 1))) & 15) | (((qh[l] >> (2 * g)) & 3) << 4));
+  uint8_t *row = dst + (size_t)n * B * PBX_Q6KP_ROW;
+  uint8_t *lo = row + (size_t)b * 16, *hi = row + (size_t)B * 16 + (size_t)b * 8;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) lo[j] = (uint8_t)((code[j] & 15) | ((code[j + 16] & 15) << 4));
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      unsigned v = 0;
+#pragma unroll
+      for (int sf = 0; sf < 4; ++sf) v |= (unsigned)((code[16 * u + 4 * sf + t] >> 4) & 3) << (2 * sf);
+      hi[4 * u + t] = (uint8_t)v;
+    }
+  const uint8_t *sc = blk + 192 + half * 8 + 2 * g;
+  uint8_t *so = row + (size_t)B * 24 + (size_t)b * 2;
+  so[0] = sc[0];
+  so[1] = sc[1];
+}
 
 // Row-batched integer-limb GEMVs: up to MR activation rows against one pass
 // over the weights (speculative verify, prompts of 4..MR tokens), args.rows

@@ -25,6 +25,7 @@
 #define PBX_Q41 3
 #define PBX_F16 4
 #define PBX_Q6K 5
+#define PBX_Q6KP 6  // Q6_K codes repacked lane-major (integer-limb kernel only)
 
 #define PRO_NONE 0
 #define PRO_RMSNORM 1
@@ -178,21 +179,34 @@ template <> struct BlockTraits<PBX_Q41> { static constexpr int QB = 16; static c
 // load_lane); the 6-bit codes carry an offset of 32.
 template <> struct BlockTraits<PBX_F16> { static constexpr int QB = 64; static constexpr float OFF = 0.f; };
 template <> struct BlockTraits<PBX_Q6K> { static constexpr int QB = 64; static constexpr float OFF = 32.f; };
+// Q6_K lane-packed: the 16 low-nibble bytes then the 8 high-field bytes of
+// the lane's 32 codes (see load_lane), in two 16-byte registers.
+template <> struct BlockTraits<PBX_Q6KP> { static constexpr int QB = 32; static constexpr float OFF = 32.f; };
+template <int TYPE> constexpr bool is_q6k() { return TYPE == PBX_Q6K || TYPE == PBX_Q6KP; }
 
 // Types with an fp16 scale plane (d per 32-block, or per 256-block for Q6_K).
 template <int TYPE> constexpr bool has_scale() {
-  return TYPE == PBX_Q4 || TYPE == PBX_Q8 || TYPE == PBX_Q41 || TYPE == PBX_Q6K;
+  return TYPE == PBX_Q4 || TYPE == PBX_Q8 || TYPE == PBX_Q41 || is_q6k<TYPE>();
 }
 // Q6_K keeps one d per 256-element super-block: block index and blocks per
 // row of the scale plane for the lane's 32-block b.
 template <int TYPE> __device__ __forceinline__ int scale_block(int b) {
-  return TYPE == PBX_Q6K ? b >> 3 : b;
+  return is_q6k<TYPE>() ? b >> 3 : b;
 }
 
 // Q6_K super-block as resident (gguf.js:317-364 minus d, which moves to the
 // scale plane): ql[128] low nibbles, qh[64] high 2-bit pairs, 16 int8
 // sub-block scales; 208 bytes, 16-byte aligned.
 #define PBX_Q6K_BYTES 208
+
+// Q6_K lane-packed copy (PBX_Q6KP), 26 bytes per 32-block, row by row:
+// [B][16] bytes whose byte j holds code j's low nibble (bits 0-3) and code
+// j+16's (bits 4-7); [B][8] bytes whose byte 4u+t holds the 2-bit high
+// fields of codes 16u+4s+t at bits 2s, s < 4; [B][2] the int8 scales of the
+// two 16-code halves.  Codes are those of the Q6_K layout above, so the
+// integer dots of both layouts are the same sums.  A lane's block is one
+// 16-byte, one 8-byte and one 2-byte load (the Q6_K layout needs 64 bytes).
+#define PBX_Q6KP_ROW 26
 
 // The weight bytes lane-block b (elements 32b .. 32b+31) of row n needs.
 // Q6_K: element e = 256*sb + 128*half + 32*g + l (l < 32) is
@@ -224,6 +238,14 @@ __device__ __forceinline__ void load_lane(const uint8_t *qs, int n, int b, int B
     q[2] = ld_stream(qh);
     q[3] = ld_stream(qh + 16);
     ex = *reinterpret_cast<const uint16_t *>(blk + 192 + half * 8 + 2 * g) & (ok ? 0xFFFFu : 0u);
+  } else if constexpr (TYPE == PBX_Q6KP) {
+    // row n: [B][16] low nibbles, [B][8] high fields, [B][2] int8 scales
+    const uint8_t *row = qs + (size_t)n * (B * PBX_Q6KP_ROW);
+    q[0] = ld_stream(row + (size_t)bb * 16);
+    const uint2 h = *reinterpret_cast<const uint2 *>(row + (size_t)B * 16 + (size_t)bb * 8);
+    q[1] = make_uint4(h.x, h.y, 0u, 0u);
+    ex = *reinterpret_cast<const uint16_t *>(row + (size_t)B * 24 + (size_t)bb * 2) &
+         (ok ? 0xFFFFu : 0u);
   } else {
     const uint8_t *src = qs + ((size_t)n * B + bb) * QB;
 #pragma unroll
@@ -760,7 +782,7 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) {
 // instruction's M < 4 rows).
 template <int TYPE, int WV, int RT, int IB, int PRO, int EPI, bool LOOP = false, int MR = 1>
 __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
-  static_assert(TYPE == PBX_Q4 || TYPE == PBX_Q8 || TYPE == PBX_Q6K, "quantised weights only");
+  static_assert(TYPE == PBX_Q4 || TYPE == PBX_Q8 || is_q6k<TYPE>(), "quantised weights only");
   static_assert(MR > 1 || IB <= WV, "one prologue wave per 64 blocks");
   static_assert(!LOOP || EPI == EPI_ARGMAX || EPI == EPI_STORE, "tile loop epilogues");
   static_assert(MR == 1 || EPI != EPI_ARGMAX, "argmax keys for one row");
@@ -850,7 +872,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
 #pragma unroll
       for (int j = 0; j < IB; ++j) {
         const int b = lane + 64 * j, bb = b < B ? b : 0;
-        db[i][j] = a.dsc[TYPE == PBX_Q6K ? dsc_index(rw, bb >> 3, B >> 3) : dsc_index(rw, bb, B)];
+        db[i][j] = a.dsc[is_q6k<TYPE>() ? dsc_index(rw, bb >> 3, B >> 3) : dsc_index(rw, bb, B)];
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -861,8 +883,8 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
       for (int j = 0; j < IB; ++j) {
         const int b = lane + 64 * j;
         ex[i][j] = 0u;
-        if constexpr (TYPE == PBX_Q6K) {
-          load_lane<PBX_Q6K>(a.qs, rw, b, B, b < B, qq[i][j], ex[i][j]);
+        if constexpr (is_q6k<TYPE>()) {
+          load_lane<TYPE>(a.qs, rw, b, B, b < B, qq[i][j], ex[i][j]);
         } else {
           const uint8_t *src = a.qs + ((size_t)rw * B + (b < B ? b : 0)) * QB;
 #pragma unroll
@@ -971,7 +993,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
           limb[pm][L][0][pb] = make_int4(lw[L][0], lw[L][1], lw[L][2], lw[L][3]);
           limb[pm][L][1][pb] = make_int4(lw[L][4], lw[L][5], lw[L][6], lw[L][7]);
         }
-        bsum[pm][0][pb] = TYPE == PBX_Q6K ? bs_lo : bs;
+        bsum[pm][0][pb] = is_q6k<TYPE>() ? bs_lo : bs;
         bsum[pm][1][pb] = bs - bs_lo;
       }
       if (p % IB == 0 && lane == 0) xscale[pm] = ldexpf(1.f, e - 22);
@@ -1019,19 +1041,34 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
               s1 = sdot4(lo, xl[1][k], s1); s1 = sdot4(hi, xl[1][4 + k], s1);
               s2 = sdot4(lo, xl[2][k], s2); s2 = sdot4(hi, xl[2][4 + k], s2);
             }
-          } else if constexpr (TYPE == PBX_Q6K) {
-            // 6-bit codes of elements 4k..4k+3: low nibbles of the lane's ql
-            // bytes (high nibbles for groups 2, 3) | 2-bit qh fields << 4;
-            // the two 16-element halves carry their own int8 scales
-            const unsigned shl = 4 * ((b & 3) >> 1), shh = 2 * (b & 3);
-            const unsigned wl[8] = {qq[i][j][0].x, qq[i][j][0].y, qq[i][j][0].z, qq[i][j][0].w,
-                                    qq[i][j][1].x, qq[i][j][1].y, qq[i][j][1].z, qq[i][j][1].w};
-            const unsigned wh[8] = {qq[i][j][2].x, qq[i][j][2].y, qq[i][j][2].z, qq[i][j][2].w,
-                                    qq[i][j][3].x, qq[i][j][3].y, qq[i][j][3].z, qq[i][j][3].w};
+          } else if constexpr (is_q6k<TYPE>()) {
+            // 6-bit codes of elements 4k..4k+3: low nibbles | 2-bit high
+            // fields << 4; the two 16-element halves carry their own int8
+            // scales.  Q6_K: the lane's ql bytes (high nibbles for groups 2,
+            // 3) and qh bytes; lane-packed: nibble bytes (high nibbles for
+            // codes 16..31) and one 2-bit field a byte per group of four.
+            unsigned cw[8];
+            if constexpr (TYPE == PBX_Q6K) {
+              const unsigned shl = 4 * ((b & 3) >> 1), shh = 2 * (b & 3);
+              const unsigned wl[8] = {qq[i][j][0].x, qq[i][j][0].y, qq[i][j][0].z, qq[i][j][0].w,
+                                      qq[i][j][1].x, qq[i][j][1].y, qq[i][j][1].z, qq[i][j][1].w};
+              const unsigned wh[8] = {qq[i][j][2].x, qq[i][j][2].y, qq[i][j][2].z, qq[i][j][2].w,
+                                      qq[i][j][3].x, qq[i][j][3].y, qq[i][j][3].z, qq[i][j][3].w};
+#pragma unroll
+              for (int k = 0; k < 8; ++k)
+                cw[k] = ((wl[k] >> shl) & 0x0F0F0F0Fu) | (((wh[k] >> shh) & 0x03030303u) << 4);
+            } else {
+              const unsigned wl[4] = {qq[i][j][0].x, qq[i][j][0].y, qq[i][j][0].z, qq[i][j][0].w};
+              const unsigned wh[2] = {qq[i][j][1].x, qq[i][j][1].y};
+#pragma unroll
+              for (int k = 0; k < 8; ++k)
+                cw[k] = ((wl[k & 3] >> (k < 4 ? 0 : 4)) & 0x0F0F0F0Fu) |
+                        (((wh[k >> 2] >> (2 * (k & 3))) & 0x03030303u) << 4);
+            }
             int h0 = 0, h1 = 0, h2 = 0;
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-              const int c = (int)(((wl[k] >> shl) & 0x0F0F0F0Fu) | (((wh[k] >> shh) & 0x03030303u) << 4));
+              const int c = (int)cw[k];
               if (k < 4) {
                 s0 = sdot4(c, xl[0][k], s0); s1 = sdot4(c, xl[1][k], s1); s2 = sdot4(c, xl[2][k], s2);
               } else {

@@ -127,6 +127,9 @@ struct pbx_model {
   int kvdim = 0, qkv_rows = 0;
   std::vector<Layer> layers;
   pbx_weight *embd = nullptr, *output = nullptr;
+  // lane-packed copy of a Q6_K LM head for the integer-limb kernel (26 bytes
+  // per 32-block; its d stays in the head's scale plane)
+  void *head_lanes = nullptr;
   float *out_norm = nullptr;
   unsigned global_mask = 0;
   float *kcache = nullptr, *vcache = nullptr, *rope = nullptr;
@@ -314,6 +317,22 @@ static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const c
   return PBX_OK;
 }
 
+static int dalloc(pbx_model *m, void **p, size_t bytes);
+
+// Fills m->head_lanes from the resident Q6_K LM head (pbx_pack_q6_k_lanes).
+static int pack_head_lanes(pbx_model *m) {
+  const pbx_weight *head = m->output ? m->output : m->embd;
+  hipFunction_t f = pbx_kernel_by_name(m->c, "pbx_pack_q6_k_lanes");
+  if (!f) return pbx_fail(m->c, PBX_ELOAD, "model: kernel pbx_pack_q6_k_lanes not found");
+  const void *qs = head->qs;
+  void *dst = m->head_lanes;
+  int N = (int)head->N, B = (int)head->B;
+  void *args[] = {&qs, &dst, &N, &B};
+  const int64_t total = (int64_t)N * B;
+  return pbx_launch_fn(m->c, f, "pbx_pack_q6_k_lanes", dim3((unsigned)((total + 255) / 256)),
+                       dim3(256), args, m->c->stream);
+}
+
 static int build_ops(pbx_model *m) {
   pbx_ctx *c = m->c;
   const pbx_model_config &g = m->cfg;
@@ -395,6 +414,19 @@ static int build_ops(pbx_model *m) {
   const pbx_weight *head = m->output ? m->output : m->embd;
   int rc = add_gemv(m, head, "lmh", "lm_head", m->x, nullptr, m->out_norm, m->logits, &n_tiles);
   if (rc) return rc;
+  if (m->ops.back().name.rfind("pbx_dk_q6k_i", 0) == 0) {
+    // Q6_K head on the integer-limb kernel: the same kernel on the
+    // lane-packed copy (one 16-, 8- and 2-byte load per lane block)
+    Op &op = m->ops.back();
+    if (!m->head_lanes &&
+        ((rc = dalloc(m, &m->head_lanes, (size_t)head->N * head->B * 26)) ||
+         (rc = pack_head_lanes(m))))
+      return rc;
+    op.name.replace(0, strlen("pbx_dk_q6k_"), "pbx_dk_q6kp_");
+    op.f = pbx_kernel_by_name(c, op.name);
+    if (!op.f) return pbx_fail(c, PBX_ELOAD, "model: kernel %s not found", op.name.c_str());
+    op.gemv.qs = m->head_lanes;
+  }
   if (n_tiles > m->n_partials_cap)
     return pbx_fail(c, PBX_EINVAL, "model: %d argmax partials exceed capacity %d", n_tiles,
                     m->n_partials_cap);
@@ -536,7 +568,7 @@ static void model_release(pbx_model *m) {
   for (void *p : {(void *)m->out_norm, (void *)m->kcache, (void *)m->vcache, (void *)m->rope,
                   (void *)m->x, (void *)m->qkv, (void *)m->attn, (void *)m->gu, (void *)m->logits,
                   (void *)m->partials, (void *)m->state, (void *)m->hist,
-                  (void *)m->attn_part})
+                  (void *)m->attn_part, m->head_lanes})
     if (p) hipFree(p);
   for (void *p : {(void *)m->bx, (void *)m->bxn, (void *)m->bqkv, (void *)m->battn,
                   (void *)m->bgu, (void *)m->bh, (void *)m->btmp, (void *)m->blogits,
@@ -748,6 +780,10 @@ extern "C" int pbx_model_set_tensor(pbx_model *m, int tensor, int layer, const v
       return pbx_fail(c, PBX_EINVAL, "pbx_model_set_tensor: unknown tensor id %d", tensor);
   }
   if (rc) return rc;
+  // a rewritten LM head: refresh its lane-packed copy
+  if (m->head_lanes && tensor == (m->output ? PBX_T_OUTPUT : PBX_T_TOKEN_EMBD) &&
+      (rc = pack_head_lanes(m)))
+    return rc;
   if (per_layer)
     m->layers[layer].set_mask |= bit;
   else

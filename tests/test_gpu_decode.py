@@ -215,6 +215,29 @@ def test_integer_limb_kernels_match_float_kernels(ctx, monkeypatch, wt, et, dim,
     ref.close()
 
 
+def test_q6k_head_copy_follows_rewrites(ctx):
+    """A Q6_K head at K = 2048 runs on a lane-packed copy of its codes: a
+    head rewritten after the step was built (copy made) gives the same
+    logits as a model that held the new head from the start."""
+    print("[case] q6_k head copy after a rewrite", flush=True)
+    from purebee_amd.native import T_TOKEN_EMBD
+    cfg = tiny(TYPE_Q4_0, TYPE_Q6_K, dim=2048, hidden_dim=1024, n_layers=1, n_heads=16,
+               n_kv_heads=4, vocab_size=4096, max_seq=16)
+    specs = synth.tensor_specs(cfg)
+    i = next(k for k, s in enumerate(specs) if s[0] == T_TOKEN_EMBD)
+    new = synth.make_tensor(specs[i], 77, i)
+    a = synth.build(ctx, cfg, 41)
+    a.forward([3], 0)  # builds the step and the copy of the old head
+    a.set_tensor(T_TOKEN_EMBD, -1, new)
+    b = synth.build(ctx, cfg, 41)
+    b.set_tensor(T_TOKEN_EMBD, -1, new)
+    la, na = a.forward([5], 0)
+    lb, nb = b.forward([5], 0)
+    assert np.array_equal(la, lb) and na == nb
+    a.free()
+    b.free()
+
+
 def test_model_argument_errors(ctx):
     print("[case] model errors", flush=True)
     cfg = tiny(TYPE_Q4_0, TYPE_Q4_0)
