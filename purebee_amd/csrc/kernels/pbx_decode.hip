@@ -104,8 +104,8 @@ DK_INT_LMHL(PBX_Q4, q4, 4, 8, 1)
 DK_INT_LMHL(PBX_Q4, q4, 4, 4, 1)
 // Q6_K lm head (the output matrix of llama.cpp Q4_0 files), K = 2048, on
 // the resident Q6_K layout and on the lane-packed copy
-DK_INT_LMHL(PBX_Q6K, q6k, 4, 2, 1)
-DK_INT_LMHL(PBX_Q6KP, q6kp, 4, 2, 1)
+DK_INT_LMHL(PBX_Q6K, q6k, 4, 4, 1)
+DK_INT_LMHL(PBX_Q6KP, q6kp, 4, 4, 1)
 
 // Lane-packed copy (PBX_Q6KP layout, PBX_Q6KP_ROW bytes per 32-block) of a
 // resident Q6_K matrix of N rows x B 32-blocks: one thread per (row, block)

@@ -179,8 +179,9 @@ static bool int_gemv_disabled() {
 }
 
 // PBX_GEMV_INT_SHAPES="role=WVxRT[l],..." (roles qkv, o, gate_up, down,
-// lm_head), read when the step is planned: the integer-limb kernel with WV
-// waves x RT rows for the listed roles (Q4_0 / Q8_0, K = 2048..8192; a
+// lm_head; lm_head_q6k for a Q6_K head), read when the step is planned: the
+// integer-limb kernel with WV waves x RT rows for the listed roles (Q4_0 /
+// Q8_0, K = 2048..8192; a Q6_K head at K = 2048; a
 // trailing l selects the lm head's tile loop), for tuning.  A shape that
 // was not compiled fails the plan.
 static bool int_override(const char *role, int *wv, int *rt, bool *loop) {
@@ -207,10 +208,11 @@ static bool int_shape(bool enabled, const char *mode, const char *role, int type
   if (!enabled || B < 64 || B > 256) return false;
   *ib = (B + 63) / 64;
   *loop = false;
-  if (type == PBX_TYPE_Q6_K) {  // the lm head at K = 2048: 4 waves x 2 rows, tile loop
+  if (type == PBX_TYPE_Q6_K) {  // the lm head at K = 2048: 4 waves x 4 rows, tile loop
     if (strcmp(mode, "lmh") != 0 || B != 64) return false;
+    if (int_override("lm_head_q6k", wv, rt, loop)) return true;
     *wv = 4;
-    *rt = 2;
+    *rt = 4;
     *loop = true;
     return true;
   }
