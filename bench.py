@@ -16,9 +16,11 @@ Workload "m-gt-1": only the M>1 measurements of the default line (batched
 512-token prefill, the MFMA GEMM at M=512, M=5 verify, speculative decoding).
 
 Prints one JSON line: the bench contract plus `roofline` (the kernel with the
-largest share of a step; HIP events on the model's stream), `kernels` (per
-role) and `cpu_baseline` (the restated reference CPU path on a bounded sample
-of the same work, timed on this host's cores).
+largest share of a step: its algorithmic bytes over its mean execution time
+inside decode steps, from HIP events that the kernel's own dispatch stamps),
+`kernels` (per role), `seam` (the synchronous host-buffer instruction as
+llama-streaming.js calls it) and `cpu_baseline` (the restated reference CPU
+path on a bounded sample of the same work, timed on this host's cores).
 """
 import argparse
 import json
@@ -44,16 +46,26 @@ def q4_bytes(N, K):
     return N * K // 32 * 18
 
 
+def host_threads():
+    """Threads for the CPU baseline: the CPUs this process may run on, at most
+    16 (a one-GPU box's share of its host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
 def cpu_baseline(host, cfg, seconds):
     """Restated reference CPU path on the same weights: wasm-q4.js Q4_0 kernel
     in SSE under the thread-pool.js row split for the 7 matvecs of each layer,
     and the single-threaded f32 LM head (wasmQ4.lmHead) over the exactly
     dequantised tied embedding.  Attention and norms (<1% of the reference's
-    per-token time) are left out of the sample."""
+    per-token time) are left out of the sample.  Timed with the host's
+    threads (value) and with one thread (t1_value)."""
     import oracle
     from purebee_amd import native as N_
-    threads = min(16, os.cpu_count() or 1)
-    pool = oracle.CpuPool(threads)
+    threads = host_threads()
     d, h, L, V = cfg["dim"], cfg["hidden_dim"], cfg["n_layers"], cfg["vocab_size"]
     emb = oracle.dequant_q4_0(host[(N_.T_TOKEN_EMBD, -1)], V * d)
     x = {d: np.random.default_rng(1).normal(0, 1, d).astype(np.float32),
@@ -63,26 +75,35 @@ def cpu_baseline(host, cfg, seconds):
             (N_.T_FFN_DOWN, d, h)]
     kv = cfg["n_kv_heads"] * (d // cfg["n_heads"])
 
-    def one_token():
-        for l in range(L):
-            for tid, n, k in mats:
-                n = kv if n < 0 else n
-                pool.q4_0_matvec(x[k], host[(tid, l)], n, k)
-        oracle.cpu_lm_head(x[d], emb, V, d)
+    def timed(pool, budget, cap):
+        def one_token():
+            for l in range(L):
+                for tid, n, k in mats:
+                    n = kv if n < 0 else n
+                    pool.q4_0_matvec(x[k], host[(tid, l)], n, k)
+            oracle.cpu_lm_head(x[d], emb, V, d)
 
-    one_token()
-    t0 = time.perf_counter()
-    one_token()
-    per = time.perf_counter() - t0
-    n = max(2, min(60, int(seconds / max(per, 1e-3))))
-    t0 = time.perf_counter()
-    for _ in range(n):
         one_token()
-    dt = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        one_token()
+        per = time.perf_counter() - t0
+        n = max(2, min(cap, int(budget / max(per, 1e-3))))
+        t0 = time.perf_counter()
+        for _ in range(n):
+            one_token()
+        return n, time.perf_counter() - t0
+
+    pool = oracle.CpuPool(threads)
+    n, dt = timed(pool, seconds, 60)
     pool.close()
+    pool1 = oracle.CpuPool(1)
+    n1, dt1 = timed(pool1, seconds * 0.75, 20)
+    pool1.close()
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "host_cpus": os.cpu_count(), "t1_value": round(n1 / dt1, 3),
             "sample": f"{n} decode tokens of Q4_0 matvec work (16 layers x 7 matvecs, "
-                      f"{threads} threads) + single-threaded f32 LM head, {dt:.1f}s"}
+                      f"{threads} threads) + single-threaded f32 LM head, {dt:.1f}s; "
+                      f"t1_value: {n1} tokens on 1 thread, {dt1:.1f}s"}
 
 
 COPY_BYTES = 256 << 20
@@ -171,7 +192,7 @@ def run_decode(args, pb, synth):
         if t == pb.TYPE_Q4_0:
             host[(tid, layer)] = data
 
-    model = synth.build(ctx, cfg, seed=1000, keep=keep if not args.no_cpu_baseline else None)
+    model = synth.build(ctx, cfg, seed=1000, keep=keep)
     info = model.info()
     log(f"model built + uploaded in {time.time() - t0:.1f}s, {info['device_bytes'] / 1e9:.2f} GB resident")
 
@@ -189,51 +210,71 @@ def run_decode(args, pb, synth):
     prefill_s = time.perf_counter() - t0
     log(f"prefill {PROMPT} tokens (one batched forward, warm): {prefill_s * 1e3:.1f} ms")
 
+    def time_decode(steps):
+        model.rollback(PROMPT)
+        ctx.sync()
+        ctx.timer_start()
+        t = model.generate(nxt, PROMPT, steps)
+        return ctx.timer_stop() / steps, t
+
     model.generate(nxt, PROMPT, args.warmup)
-    model.rollback(PROMPT)
-    ctx.sync()
-    ctx.timer_start()
-    toks = model.generate(nxt, PROMPT, args.steps)
-    ms = ctx.timer_stop()
-    ms_per_step = ms / args.steps
+    ms_per_step, toks = time_decode(args.steps)
     log(f"decode {args.steps} steps: {ms_per_step * 1e3:.1f} us/token, {1e3 / ms_per_step:.1f} tok/s "
         f"(graph={model.info()['graph']})")
+    # the workload's full length (KV 128 -> 384), reported beside the timed steps
+    ms256 = ms_per_step if args.steps == 256 else time_decode(256)[0]
+    log(f"decode 256 steps (KV {PROMPT}->{PROMPT + 256}): {ms256 * 1e3:.1f} us/token, "
+        f"{1e3 / ms256:.1f} tok/s")
     model.rollback(PROMPT)
 
-    # per-kernel attribution: the same steps launched kernel by kernel with
-    # an event after each kernel
-    prof = model.profile(nxt, PROMPT, 8)
+    # per-kernel execution times inside decode steps: the same steps launched
+    # kernel by kernel, each kernel's start / stop events stamped by its own
+    # dispatch (the durations a kernel trace of these launches reports)
+    n_prof = 16
+    prof = model.profile(nxt, PROMPT, n_prof)
     model.rollback(PROMPT)
     roles = {}
     for role, kern, us, by in prof:
-        r = roles.setdefault(role, {"kernel": kern, "launches_per_step": 0, "us_per_step": 0.0,
-                                    "bytes_per_step": 0.0})
+        r = roles.setdefault(role, {"kernel": kern, "launches_per_step": 0,
+                                    "kernel_us_per_step": 0.0, "bytes_per_step": 0.0})
         r["launches_per_step"] += 1
-        r["us_per_step"] += us
+        r["kernel_us_per_step"] += us
         r["bytes_per_step"] += by
+    kernel_sum = sum(r["kernel_us_per_step"] for r in roles.values())
     for role, r in roles.items():
         n = r["launches_per_step"]
-        r["us_per_launch"] = r["us_per_step"] / n
+        r["us_per_launch_in_step"] = r["kernel_us_per_step"] / n
         r["bytes_per_launch"] = r["bytes_per_step"] / n
-        r["GBps"] = r["bytes_per_step"] / r["us_per_step"] / 1e3 if r["us_per_step"] else 0.0
-        log(f"{role:8s} {r['kernel']:24s} x{n:3d}: {r['us_per_launch']:7.2f} us/launch, "
-            f"{r['GBps']:7.0f} GB/s, {r['us_per_step']:7.1f} us/step")
+        r["GBps"] = r["bytes_per_step"] / r["kernel_us_per_step"] / 1e3 if r["kernel_us_per_step"] else 0.0
+        # the graph-replayed step's time split over the roles in proportion
+        # to their execution times (the shares add up to ms_per_step)
+        r["share_of_step_us"] = ms_per_step * 1e3 * r["kernel_us_per_step"] / kernel_sum
+        log(f"{role:8s} {r['kernel']:24s} x{n:3d}: {r['us_per_launch_in_step']:7.2f} us/launch in step, "
+            f"{r['GBps']:7.0f} GB/s, {r['kernel_us_per_step']:7.1f} us/step")
+    log(f"kernel execution sum {kernel_sum:.1f} us per step (kernel by kernel); "
+        f"graph step {ms_per_step * 1e3:.1f} us")
     gemv_roles = {k: v for k, v in roles.items() if k in ("qkv", "o", "gate_up", "down", "lm_head")}
-    dom_name, dom = max(gemv_roles.items(), key=lambda kv: kv[1]["us_per_step"])
-    # the dominant kernel timed on its own: its launches back to back over all
-    # layers' weights (the gate/up set, 302 MB, exceeds the 256 MB MALL)
-    us, by, nl = model.bench_role(dom_name, max(2, 640 // dom["launches_per_step"]))
+    dom_name, dom = max(gemv_roles.items(), key=lambda kv: kv[1]["kernel_us_per_step"])
+    # the dominant kernel also timed back to back over all layers' weights
+    # (the gate/up set, 302 MB, exceeds the 256 MB MALL)
+    us_b2b, by, nl = model.bench_role(dom_name, max(2, 640 // dom["launches_per_step"]))
     model.rollback(PROMPT)
-    gbps = by / us / 1e3
-    log(f"dominant {dom_name} ({dom['kernel']}) back to back: {us:.2f} us/launch, "
-        f"{by / 1e6:.2f} MB/launch, {gbps:.0f} GB/s")
+    us_in = dom["us_per_launch_in_step"]
+    gbps = dom["bytes_per_launch"] / us_in / 1e3
+    log(f"dominant {dom_name} ({dom['kernel']}): {us_in:.2f} us in step, {gbps:.0f} GB/s; "
+        f"back to back {us_b2b:.2f} us, {by / us_b2b / 1e3:.0f} GB/s")
     roofline = {"bound": "hbm", "kernel": f"{dom['kernel']} ({dom_name})",
                 "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbps / HBM_PEAK_GBS, 4),
                 "traffic": load_traffic(dom["kernel"]),
-                "bytes_per_launch": round(by), "us_per_launch": round(us, 3),
-                "us_per_launch_in_step": round(dom["us_per_launch"], 3)}
+                "bytes_per_launch": round(dom["bytes_per_launch"]),
+                "us_per_launch": round(us_in, 3),
+                "timing": f"mean execution of the {dom['launches_per_step']} launches in each of "
+                          f"{n_prof} decode steps (kernel by kernel; dispatch-stamped HIP events)",
+                "us_back_to_back": round(us_b2b, 3),
+                "frac_back_to_back": round(by / us_b2b / 1e3 / HBM_PEAK_GBS, 4)}
     step_bytes = sum(r["bytes_per_step"] for r in roles.values())
+    seam = run_seam(ctx, pb, cfg, host) if host else None
     matvec_shapes = run_matvec_shapes(ctx, pb)
     m_gt_1 = None if args.no_m_gt_1 else run_m_gt_1(ctx, model, cfg, pb, synth)
     next_rows = None
@@ -267,10 +308,15 @@ def run_decode(args, pb, synth):
                    "effective_GBps": round(step_bytes / ms_per_step / 1e6, 1),
                    "prefill_ms": round(prefill_s * 1e3, 2), "device": dev,
                    "copy_kernel_GBps": round(copy["GBps"], 1),
+                   "decode_256": {"kv": f"{PROMPT}->{PROMPT + 256}",
+                                  "us_per_token": round(ms256 * 1e3, 2),
+                                  "tok_per_s": round(1e3 / ms256, 2)},
+                   "kernel_us_per_step": round(kernel_sum, 2),
                    "first_tokens": [int(t) for t in toks[:8]]},
         "roofline": roofline,
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in roles.items()},
+        "seam": seam,
         "matvec_shapes": matvec_shapes,
         "m_gt_1": m_gt_1,
         "next_rows": next_rows,
@@ -282,6 +328,43 @@ def run_decode(args, pb, synth):
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA, vendor figure
+
+
+def run_seam(ctx, pb, cfg, host, tokens=8):
+    """The synchronous instruction seam StreamingLlamaRuntime goes through
+    (quantizedMatvec, llama-streaming.js:168-177, called 7 times a layer by
+    _runLayerQ4, llama-streaming.js:505-606) plus the LM head: one pbx_linear
+    call per matvec with host activations in and host outputs back, 113 calls
+    a token for Llama-3.2-1B, on the same Q4_0 weights uploaded as separate
+    matrices.  Reports the matvec time a token spends in that seam."""
+    from purebee_amd import native as N_
+    d, h, L, V = cfg["dim"], cfg["hidden_dim"], cfg["n_layers"], cfg["vocab_size"]
+    kv = cfg["n_kv_heads"] * (d // cfg["n_heads"])
+    shapes = [(N_.T_ATTN_Q, d, d), (N_.T_ATTN_K, kv, d), (N_.T_ATTN_V, kv, d),
+              (N_.T_ATTN_OUTPUT, d, d), (N_.T_FFN_GATE, h, d), (N_.T_FFN_UP, h, d),
+              (N_.T_FFN_DOWN, d, h)]
+    ws = [(ctx.upload(pb.TYPE_Q4_0, n, k, host[(tid, l)]), k) for l in range(L) for tid, n, k in shapes]
+    ws.append((ctx.upload(pb.TYPE_Q4_0, V, d, host[(N_.T_TOKEN_EMBD, -1)]), d))
+    xs = {k: np.random.default_rng(k).normal(0, 1, k).astype(np.float32) for k in (d, h)}
+
+    def one_token():
+        for w, k in ws:
+            ctx.linear(w, xs[k])
+
+    one_token()
+    t0 = time.perf_counter()
+    for _ in range(tokens):
+        one_token()
+    dt = (time.perf_counter() - t0) / tokens
+    for w, _ in ws:
+        w.free()
+    calls = len(ws)
+    log(f"seam: {calls} host-buffer pbx_linear calls a token, {dt * 1e3:.2f} ms/token "
+        f"({dt / calls * 1e6:.1f} us a call), {1 / dt:.1f} tok/s of matvec work")
+    return {"calls_per_token": calls, "ms_per_token": round(dt * 1e3, 3),
+            "us_per_call": round(dt / calls * 1e6, 2), "tok_per_s": round(1 / dt, 2),
+            "note": "matvecs only (q, k, v, o, gate, up, down per layer + LM head), host buffers, "
+                    "synchronous; attention and norms are not in this leg"}
 
 
 def run_m_gt_1(ctx, model, cfg, pb, synth):

@@ -226,6 +226,16 @@ int pbx_model_set_tensor(pbx_model *m, int tensor, int layer, const void *data,
  * the last position's logits (if logits != NULL, [vocab]) and its argmax. */
 int pbx_model_forward(pbx_model *m, const int32_t *tokens, int n_tokens,
                       int start_pos, float *logits, int32_t *next_token);
+/* StreamingLlamaRuntime.forward(tokenIds, startPos, {maxLayers})
+ * (llama-streaming.js:738-815): as pbx_model_forward, but only the first
+ * max_layers layers run (0: all of them, `maxLayers || nLayers`; the limit
+ * is min(max_layers, n_layers)), then the final RMSNorm and the LM head on
+ * their output; the KV cache of the later layers is not written at these
+ * positions.  *layers_used (if not NULL) receives the layers run, the
+ * `layersUsed` of the reference's result. */
+int pbx_model_forward_layers(pbx_model *m, const int32_t *tokens, int n_tokens,
+                             int start_pos, int max_layers, float *logits,
+                             int32_t *next_token, int *layers_used);
 /* forward() over n tokens in ONE batched pass that keeps every position's
  * output (the reference computes them inside forward, llama.js:204-371, and
  * keeps only the last): logits [n][vocab] (or NULL) and next_tokens[n], the
@@ -245,10 +255,12 @@ int pbx_model_reset_cache(pbx_model *m);
 int pbx_model_rollback(pbx_model *m, int pos);
 int pbx_model_info(const pbx_model *m, size_t *device_bytes, int *uses_graph);
 /* Measurement: n_steps greedy decode steps launched kernel by kernel (no
- * graph) with a HIP event on the model's stream after every kernel.
- * op_us[i] is the mean time from the end of kernel i-1 to the end of
- * kernel i, op_bytes[i] its mean algorithmic bytes (may be NULL); *n_ops is
- * the kernel count per step (arrays hold min(cap, *n_ops) entries).
+ * graph), each kernel carrying a start and a stop HIP event that its own
+ * dispatch stamps (hipExtModuleLaunchKernel).  op_us[i] is the mean
+ * execution time of kernel i (the duration a kernel trace reports, without
+ * the gaps between kernels), op_bytes[i] its mean algorithmic bytes (may be
+ * NULL); *n_ops is the kernel count per step (arrays hold min(cap, *n_ops)
+ * entries).
  * pbx_model_op_name gives "role:kernel" of kernel i (no reference
  * counterpart: the reference has no GPU kernels to profile). */
 int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int n_steps,
@@ -337,6 +349,17 @@ int pbx_speculative_generate(pbx_model *target, pbx_model *draft, const int32_t 
                              int n_prompt, int max_tokens, int draft_count,
                              const int32_t *eos_ids, int n_eos, int batched_verify,
                              int32_t *out_tokens, int *n_out, pbx_spec_stats *stats);
+
+/* SelfSpeculativeDecoder.generate (speculative.js:58-204) as the reference
+ * runs it, greedy: the draft is the model's own first draft_layers layers
+ * (forward([t], pos, {maxLayers: draftLayers}) and argmax, draft_count
+ * times, speculative.js:96-111), on its own KV cache; the rest as
+ * pbx_speculative_generate with target = draft = m.  Prompt tokens must lie
+ * in the vocabulary. */
+int pbx_self_speculative_generate(pbx_model *m, const int32_t *prompt, int n_prompt,
+                                  int max_tokens, int draft_layers, int draft_count,
+                                  const int32_t *eos_ids, int n_eos, int batched_verify,
+                                  int32_t *out_tokens, int *n_out, pbx_spec_stats *stats);
 
 #ifdef __cplusplus
 }

@@ -68,6 +68,9 @@ def lib():
         L.pbo_llama_set.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _f32p]
         L.pbo_llama_forward.argtypes = [ctypes.c_void_p, np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS"),
                                         ctypes.c_int, ctypes.c_int, _f32p]
+        L.pbo_llama_forward_layers.argtypes = [
+            ctypes.c_void_p, np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS"),
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p]
         L.pbo_llama_rollback.argtypes = [ctypes.c_void_p, ctypes.c_int]
         L.pbo_llama_free.argtypes = [ctypes.c_void_p]
         L.pbo_argmax.restype = ctypes.c_int
@@ -334,10 +337,12 @@ class LlamaRef:
     def set(self, tensor, layer, data):
         lib().pbo_llama_set(self._p, tensor, layer, _c(data, np.float32).ravel())
 
-    def forward(self, tokens, start_pos):
+    def forward(self, tokens, start_pos, max_layers=0):
+        """Logits of the last position; max_layers as StreamingLlamaRuntime's
+        {maxLayers} (0: every layer)."""
         toks = np.ascontiguousarray(tokens, np.int32)
         out = np.empty(self.vocab, np.float32)
-        lib().pbo_llama_forward(self._p, toks, len(toks), start_pos, out)
+        lib().pbo_llama_forward_layers(self._p, toks, len(toks), start_pos, max_layers, out)
         return out
 
     def rollback(self, pos):

@@ -125,9 +125,17 @@ static void linear(const float *x, int S, int K, const float *W, int N, float *o
   }
 }
 
-/* llama.js:204-371 for tokens[0..S) at start_pos; logits of the last position. */
-void pbo_llama_forward(pbo_llama *m, const int *tokens, int S, int start_pos, float *logits) {
+/* llama.js:204-371 for tokens[0..S) at start_pos; logits of the last position.
+ * max_layers: StreamingLlamaRuntime.forward's {maxLayers}
+ * (llama-streaming.js:745, 764-792): `maxLayers || nLayers` layers, at most
+ * n_layers, then the final norm and head on their output; later layers'
+ * caches are not written. */
+void pbo_llama_forward_layers(pbo_llama *m, const int *tokens, int S, int start_pos,
+                              int max_layers, float *logits) {
   const pbo_cfg *c = &m->c;
+  int nl = max_layers == 0 ? c->n_layers : max_layers;
+  if (nl > c->n_layers) nl = c->n_layers;
+  if (nl < 0) nl = 0;
   const int D = c->dim, H = c->hidden, HD = c->head_dim, NH = c->n_heads, KV = m->kv_dim;
   const int cacheLen = start_pos + S;
   float *x = (float *)malloc((size_t)S * D * 4), *xn = (float *)malloc((size_t)S * D * 4);
@@ -141,7 +149,7 @@ void pbo_llama_forward(pbo_llama *m, const int *tokens, int S, int start_pos, fl
 
   const int per_kv = NH / c->n_kv;
   const double scale = 1.0 / sqrt((double)HD);
-  for (int l = 0; l < c->n_layers; ++l) {
+  for (int l = 0; l < nl; ++l) {
     pbo_layer *L = &m->L[l];
     rmsnorm(x, L->att_norm, S, D, c->eps, xn);
     linear(xn, S, D, L->wq, D, q);
@@ -214,6 +222,10 @@ void pbo_llama_forward(pbo_llama *m, const int *tokens, int S, int start_pos, fl
   const float *last = xn + (size_t)(S - 1) * D;
   linear(last, 1, D, m->out_w ? m->out_w : m->emb, c->vocab, logits);
   free(x); free(xn); free(q); free(k); free(v); free(att); free(proj); free(g); free(u); free(sc);
+}
+
+void pbo_llama_forward(pbo_llama *m, const int *tokens, int S, int start_pos, float *logits) {
+  pbo_llama_forward_layers(m, tokens, S, start_pos, 0, logits);
 }
 
 /* llama.js:432-442: first index of the maximum (strict >). */

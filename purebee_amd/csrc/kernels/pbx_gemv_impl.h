@@ -797,7 +797,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   __shared__ int4 limb[MR][3][2][IB * 64];
   // exact sums of a block's x_q ([0]; Q6_K: its two 16-element halves)
   __shared__ int bsum[MR][2][IB * 64];
-  __shared__ float red[2][MR][IB];
+  __shared__ float red[3][MR][IB];
   __shared__ float xscale[MR];
   __shared__ uint64_t kred[WV];
 
@@ -906,12 +906,15 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   __builtin_amdgcn_sched_barrier(0);
 
   // 3. Prologue slots: sum of squares (RMSNorm) and max |x * w| of their
-  //    blocks, combined across a row's IB slots through LDS.
-  float ss[PS], mw[PS];
+  //    blocks, combined across a row's IB slots through LDS.  nf is the sum
+  //    of (x * w) * 0 over the blocks: NaN exactly when an element of x * w
+  //    is infinite or NaN (which fmaxf would drop), else 0.
+  float ss[PS], mw[PS], nf[PS];
 #pragma unroll
   for (int sl = 0; sl < PS; ++sl) {
     ss[sl] = 0.f;
     mw[sl] = 0.f;
+    nf[sl] = 0.f;
     const int p = wave + WV * sl;
     if (p < PP) {
       const bool pvalid = (p % IB) * 64 + lane < B;
@@ -920,11 +923,13 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
         const float4 t = pvalid ? xv[sl][v] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[sl][v];
         if constexpr (PRO == PRO_RMSNORM)
           ss[sl] = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, ss[sl]))));
-        mw[sl] = fmaxf(mw[sl], fmaxf(fmaxf(fabsf(t.x * w.x), fabsf(t.y * w.y)),
-                                     fmaxf(fabsf(t.z * w.z), fabsf(t.w * w.w))));
+        const float px = t.x * w.x, py = t.y * w.y, pz = t.z * w.z, pw = t.w * w.w;
+        mw[sl] = fmaxf(mw[sl], fmaxf(fmaxf(fabsf(px), fabsf(py)), fmaxf(fabsf(pz), fabsf(pw))));
+        nf[sl] = fmaf(px, 0.f, fmaf(py, 0.f, fmaf(pz, 0.f, fmaf(pw, 0.f, nf[sl]))));
       }
       if constexpr (PRO == PRO_RMSNORM) ss[sl] = wave_sum(ss[sl]);
       mw[sl] = wave_max(mw[sl]);
+      nf[sl] = wave_sum(nf[sl]);
     }
   }
   if constexpr (IB > 1) {
@@ -934,6 +939,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
       if (p < PP && lane == 0) {
         red[0][p / IB][p % IB] = ss[sl];
         red[1][p / IB][p % IB] = mw[sl];
+        red[2][p / IB][p % IB] = nf[sl];
       }
     }
     lds_barrier();
@@ -943,10 +949,12 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
       if (p < PP) {
         ss[sl] = 0.f;
         mw[sl] = 0.f;
+        nf[sl] = 0.f;
 #pragma unroll
         for (int w = 0; w < IB; ++w) {
           ss[sl] += red[0][p / IB][w];
           mw[sl] = fmaxf(mw[sl], red[1][p / IB][w]);
+          nf[sl] += red[2][p / IB][w];
         }
       }
     }
@@ -996,7 +1004,9 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
         bsum[pm][0][pb] = is_q6k<TYPE>() ? bs_lo : bs;
         bsum[pm][1][pb] = bs - bs_lo;
       }
-      if (p % IB == 0 && lane == 0) xscale[pm] = ldexpf(1.f, e - 22);
+      // a non-finite activation makes every output of the row NaN (the
+      // reference's sums are then NaN or +-inf; fixed point cannot hold them)
+      if (p % IB == 0 && lane == 0) xscale[pm] = ldexpf(1.f, e - 22) + nf[sl];
     }
   }
   lds_barrier();

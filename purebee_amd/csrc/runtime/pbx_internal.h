@@ -121,6 +121,8 @@ int pbx_launch(pbx_ctx *c, int kernel, dim3 grid, dim3 block, void **args,
 hipFunction_t pbx_kernel_by_name(pbx_ctx *c, const std::string &name);
 int pbx_launch_fn(pbx_ctx *c, hipFunction_t f, const char *name, dim3 grid, dim3 block,
                   void **args, hipStream_t stream);
+int pbx_launch_fn_timed(pbx_ctx *c, hipFunction_t f, const char *name, dim3 grid, dim3 block,
+                        void **args, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 int pbx_weight_alloc(pbx_ctx *c, int type, int64_t N, int64_t K, pbx_weight **out);
 int pbx_weight_write_rows(pbx_ctx *c, pbx_weight *w, int64_t row0, int64_t rows,
                           const void *host);
@@ -149,6 +151,10 @@ int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
 size_t pbx_type_row_bytes(int type, int64_t K);
 void pbx_model_release_all(pbx_ctx *c);
 int pbx_model_clear_range(pbx_model *m, int from, int to);
+// pbx_model_generate with every step stopping after the first max_layers
+// layers (0: all); the self-speculative draft.
+int pbx_model_generate_layers(pbx_model *m, int32_t token, int start_pos, int n_steps,
+                              int max_layers, int32_t *out_tokens);
 const pbx_model_config *pbx_model_cfg(const pbx_model *m);
 pbx_ctx *pbx_model_ctx(const pbx_model *m);
 

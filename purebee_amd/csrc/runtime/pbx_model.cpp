@@ -145,11 +145,22 @@ struct pbx_model {
   int *hist = nullptr;
   int hist_cap = 0;
   std::vector<Op> ops;
+  // ops[layer_op[l]] is the first kernel of layer l; layer_op[n_layers] is
+  // the LM head's (then the argmax)
+  std::vector<size_t> layer_op;
   Op embed_op;  // the embedding of a token set by the host (steps embed their own)
   bool ops_ready = false;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   bool graph_tried = false, graph_ok = false;
+  // steps that stop after the first L < n_layers layers (forward with
+  // maxLayers), one captured graph per L, made on first use
+  struct PartGraph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    bool tried = false, ok = false;
+  };
+  std::vector<PartGraph> part;
   size_t bytes = 0;
   // Row-batched forward (prefill / verify): activations of up to batch_cap
   // rows, grown on demand; logits of every row up to logits_cap rows.
@@ -339,6 +350,7 @@ static int build_ops(pbx_model *m) {
   pbx_ctx *c = m->c;
   const pbx_model_config &g = m->cfg;
   m->ops.clear();
+  m->layer_op.assign(g.n_layers + 1, 0);
   Op e;
   e.kind = ARG_EMBED;
   e.name = "pbx_embed";
@@ -362,6 +374,7 @@ static int build_ops(pbx_model *m) {
   for (int l = 0; l < g.n_layers; ++l) {
     Layer &L = m->layers[l];
     int rc;
+    m->layer_op[l] = m->ops.size();
     if ((rc = add_gemv(m, L.wqkv, "qkv", "qkv", m->x, nullptr, L.attn_norm, m->qkv, nullptr))) return rc;
     Op a;
     a.role = "attn";
@@ -414,6 +427,7 @@ static int build_ops(pbx_model *m) {
   }
   int n_tiles = 0;
   const pbx_weight *head = m->output ? m->output : m->embd;
+  m->layer_op[g.n_layers] = m->ops.size();
   int rc = add_gemv(m, head, "lmh", "lm_head", m->x, nullptr, m->out_norm, m->logits, &n_tiles);
   if (rc) return rc;
   if (m->ops.back().name.rfind("pbx_dk_q6k_i", 0) == 0) {
@@ -448,29 +462,24 @@ static int build_ops(pbx_model *m) {
   return PBX_OK;
 }
 
-static int enqueue_op(pbx_model *m, Op &op) {
+// Launches op on the model's stream; with t0 / t1, the kernel's own
+// dispatch stamps them (its execution time, for measurement).
+static int enqueue_op(pbx_model *m, Op &op, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr) {
   void *arg;
+  void *comb[] = {&op.comb.part, &op.comb.out, &op.comb.head_dim, &op.comb.S};
   switch (op.kind) {
     case ARG_GEMV: arg = &op.gemv; break;
     case ARG_ATTN: arg = &op.attn; break;
     case ARG_ATTN_SPLIT: arg = &op.split; break;
-    case ARG_COMBINE: {
-      void *args[] = {&op.comb.part, &op.comb.out, &op.comb.head_dim, &op.comb.S};
-      return pbx_launch_fn(m->c, op.f, op.name.c_str(), op.grid, op.block, args, m->c->stream);
-    }
     case ARG_EMBED: arg = &op.embed; break;
     default: arg = &op.amax; break;
   }
-  void *args[] = {arg};
+  void *one[] = {arg};
+  void **args = op.kind == ARG_COMBINE ? comb : one;
+  if (t0)
+    return pbx_launch_fn_timed(m->c, op.f, op.name.c_str(), op.grid, op.block, args, m->c->stream,
+                               t0, t1);
   return pbx_launch_fn(m->c, op.f, op.name.c_str(), op.grid, op.block, args, m->c->stream);
-}
-
-static int enqueue_ops(pbx_model *m) {
-  for (Op &op : m->ops) {
-    int rc = enqueue_op(m, op);
-    if (rc) return rc;
-  }
-  return PBX_OK;
 }
 
 static void drop_graph(pbx_model *m) {
@@ -479,6 +488,11 @@ static void drop_graph(pbx_model *m) {
   m->exec = nullptr;
   m->graph = nullptr;
   m->graph_tried = m->graph_ok = false;
+  for (auto &p : m->part) {
+    if (p.exec) hipGraphExecDestroy(p.exec);
+    if (p.graph) hipGraphDestroy(p.graph);
+  }
+  m->part.clear();
 }
 
 static bool use_graphs() {
@@ -486,36 +500,70 @@ static bool use_graphs() {
   return !(e && e[0] == '0');
 }
 
-// One decode step on the context's stream: graph replay when capture worked.
-static int run_step(pbx_model *m) {
+// The kernels of a step that runs the first L layers: ops [0, layer_op[L])
+// then the LM head and the argmax.
+static int enqueue_ops_layers(pbx_model *m, int L) {
+  const size_t stop = m->layer_op[L], head = m->layer_op[m->cfg.n_layers];
+  for (size_t i = 0; i < m->ops.size(); ++i) {
+    if (i >= stop && i < head) continue;
+    int rc = enqueue_op(m, m->ops[i]);
+    if (rc) return rc;
+  }
+  return PBX_OK;
+}
+
+// Captures the step of the first L layers into a graph (false: capture
+// failed, the caller launches kernel by kernel).
+static bool capture_step(pbx_model *m, int L, hipGraph_t *graph, hipGraphExec_t *exec) {
+  bool ok = false;
+  hipStream_t s = m->c->stream;
+  if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+    int rc = enqueue_ops_layers(m, L);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (!rc && e == hipSuccess && g && hipGraphInstantiate(exec, g, nullptr, nullptr, 0) == hipSuccess) {
+      *graph = g;
+      ok = true;
+    } else if (g) {
+      hipGraphDestroy(g);
+    }
+  }
+  (void)hipGetLastError();
+  return ok;
+}
+
+// One decode step through the first L layers (L = n_layers: the whole
+// step) on the context's stream: graph replay when capture worked.
+static int run_step_layers(pbx_model *m, int L) {
   if (!m->ops_ready) {
     int rc = build_ops(m);
     if (rc) return rc;
   }
-  if (use_graphs() && !m->graph_tried) {
-    m->graph_tried = true;
-    hipStream_t s = m->c->stream;
-    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-      int rc = enqueue_ops(m);
-      hipGraph_t g = nullptr;
-      hipError_t e = hipStreamEndCapture(s, &g);
-      if (!rc && e == hipSuccess && g &&
-          hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0) == hipSuccess) {
-        m->graph = g;
-        m->graph_ok = true;
-      } else if (g) {
-        hipGraphDestroy(g);
-      }
-    }
-    (void)hipGetLastError();
+  const int nl = m->cfg.n_layers;
+  bool *tried = &m->graph_tried, *ok = &m->graph_ok;
+  hipGraph_t *graph = &m->graph;
+  hipGraphExec_t *exec = &m->exec;
+  if (L < nl) {
+    if ((int)m->part.size() < nl) m->part.resize(nl);
+    auto &p = m->part[L];
+    tried = &p.tried;
+    ok = &p.ok;
+    graph = &p.graph;
+    exec = &p.exec;
   }
-  if (m->graph_ok) {
-    if (hipGraphLaunch(m->exec, m->c->stream) != hipSuccess)
+  if (use_graphs() && !*tried) {
+    *tried = true;
+    *ok = capture_step(m, L, graph, exec);
+  }
+  if (*ok) {
+    if (hipGraphLaunch(*exec, m->c->stream) != hipSuccess)
       return pbx_fail(m->c, PBX_EHIP, "model: hipGraphLaunch failed");
     return PBX_OK;
   }
-  return enqueue_ops(m);
+  return enqueue_ops_layers(m, L);
 }
+
+static int run_step(pbx_model *m) { return run_step_layers(m, m->cfg.n_layers); }
 
 // Device state for a host-driven step; with `embed`, also the token's
 // embedding row into x (a step's argmax embeds the token it picks).
@@ -1041,8 +1089,10 @@ static int fused_residual_norm(pbx_model *m, const pbx_gemm_plan *p, int M, int 
   return launch_k(m, "pbx_gemm_prep_rms", dim3(Mpad), dim3(256), args);
 }
 
-// Runs the layer stack over n rows; leaves the residual stream in m->bx.
-static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
+// Runs the first nl layers of the stack over n rows (the KV cache of later
+// layers is not written, as llama-streaming.js:765-792 with maxLayers);
+// leaves the residual stream in m->bx.
+static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, int nl) {
   pbx_ctx *c = m->c;
   const pbx_model_config &g = m->cfg;
   if (hipMemcpyAsync(m->btok, tokens, (size_t)n * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess)
@@ -1061,8 +1111,10 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
   if (!rows_int && fused_ok(m, n)) {
     FusedPlans P;
     if ((rc = fused_plans(m, n, &P))) return rc;
-    if ((rc = fused_residual_norm(m, nullptr, n, P.qkv.Mpad, m->bx, m->layers[0].attn_norm))) return rc;
-    for (int l = 0; l < g.n_layers; ++l) {
+    if (nl > 0 &&
+        (rc = fused_residual_norm(m, nullptr, n, P.qkv.Mpad, m->bx, m->layers[0].attn_norm)))
+      return rc;
+    for (int l = 0; l < nl; ++l) {
       Layer &L = m->layers[l];
       float *kc = m->kcache + l * layer_kv, *vc = m->vcache + l * layer_kv;
       if ((rc = fused_gemm(m, L.wqkv, P.qkv, m->bqkv, false))) return rc;
@@ -1113,12 +1165,12 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
       }
       if ((rc = fused_gemm(m, L.wd, P.d, m->bx, true)) ||
           (rc = fused_residual_norm(m, &P.d, n, P.d.Mpad, m->bx,
-                                    l + 1 < g.n_layers ? m->layers[l + 1].attn_norm : nullptr)))
+                                    l + 1 < nl ? m->layers[l + 1].attn_norm : nullptr)))
         return rc;
     }
     return PBX_OK;
   }
-  for (int l = 0; l < g.n_layers; ++l) {
+  for (int l = 0; l < nl; ++l) {
     Layer &L = m->layers[l];
     float *kc = m->kcache + l * layer_kv, *vc = m->vcache + l * layer_kv;
     if (rows_int) {
@@ -1188,11 +1240,11 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start) {
 // Prefill: the layer stack over n rows, then the decode step's own LM head
 // and argmax on the last row, which leave the device state at
 // (start + n, next token) as n sequential steps would.
-static int prefill_batched(pbx_model *m, const int32_t *tokens, int n, int start) {
+static int prefill_batched(pbx_model *m, const int32_t *tokens, int n, int start, int nl) {
   int rc = ensure_batch(m, n, false);
   if (rc) return rc;
   if (!m->ops_ready && (rc = build_ops(m))) return rc;
-  if ((rc = batch_layers(m, tokens, n, start))) return rc;
+  if ((rc = batch_layers(m, tokens, n, start, nl))) return rc;
   if ((rc = set_state(m, start + n - 1, tokens[n - 1], 0, false))) return rc;
   if (hipMemcpyAsync(m->x, m->bx + (size_t)(n - 1) * m->cfg.dim, (size_t)m->cfg.dim * 4,
                      hipMemcpyDeviceToDevice, m->c->stream) != hipSuccess)
@@ -1209,6 +1261,12 @@ static bool batched_prefill_enabled() {
 
 extern "C" int pbx_model_forward(pbx_model *m, const int32_t *tokens, int n_tokens,
                                  int start_pos, float *logits, int32_t *next_token) {
+  return pbx_model_forward_layers(m, tokens, n_tokens, start_pos, 0, logits, next_token, nullptr);
+}
+
+extern "C" int pbx_model_forward_layers(pbx_model *m, const int32_t *tokens, int n_tokens,
+                                        int start_pos, int max_layers, float *logits,
+                                        int32_t *next_token, int *layers_used) {
   if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_forward: not a live model");
   pbx_ctx *c = m->c;
   const pbx_model_config &g = m->cfg;
@@ -1225,14 +1283,18 @@ extern "C" int pbx_model_forward(pbx_model *m, const int32_t *tokens, int n_toke
   if (rc) return rc;
   if (hipSetDevice(c->device) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward: hipSetDevice failed");
+  // llama-streaming.js:745, 764: `options.maxLayers || nLayers`, then
+  // min(maxLayers, nLayers) (a negative limit runs no layer)
+  const int nl = max_layers == 0 ? g.n_layers : std::max(0, std::min(max_layers, g.n_layers));
   if (n_tokens >= PBX_GEMM_MIN_M && batched_prefill_enabled()) {
-    if ((rc = prefill_batched(m, tokens, n_tokens, start_pos))) return rc;
+    if ((rc = prefill_batched(m, tokens, n_tokens, start_pos, nl))) return rc;
   } else {
     for (int t = 0; t < n_tokens; ++t) {
       if ((rc = set_state(m, start_pos + t, tokens[t], 0, true))) return rc;
-      if ((rc = run_step(m))) return rc;
+      if ((rc = run_step_layers(m, nl))) return rc;
     }
   }
+  if (layers_used) *layers_used = nl;
   if (logits && hipMemcpyAsync(logits, m->logits, (size_t)g.vocab_size * 4,
                                hipMemcpyDeviceToHost, c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward: logits copy failed");
@@ -1268,7 +1330,7 @@ extern "C" int pbx_model_forward_batch(pbx_model *m, const int32_t *tokens, int 
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward_batch: hipSetDevice failed");
   const int n = n_tokens;
   if ((rc = ensure_batch(m, n, true))) return rc;
-  if ((rc = batch_layers(m, tokens, n, start_pos))) return rc;
+  if ((rc = batch_layers(m, tokens, n, start_pos, g.n_layers))) return rc;
   const pbx_weight *head = m->output ? m->output : m->embd;
   if (n <= ROWS_MAX && rows_int_ok(m)) {
     // RMSNorm + LM head over the rows: a tile loop, one workgroup a CU
@@ -1334,6 +1396,35 @@ extern "C" int pbx_model_generate(pbx_model *m, int32_t token, int start_pos, in
   return PBX_OK;
 }
 
+// The greedy chain of pbx_model_generate with every step stopping after the
+// first max_layers layers: the self-speculative draft (speculative.js:96-111,
+// forward([t], pos, {maxLayers}) then argmax, repeated), replayed on the
+// device.  out_tokens receives the n_steps drafted tokens.
+int pbx_model_generate_layers(pbx_model *m, int32_t token, int start_pos, int n_steps,
+                              int max_layers, int32_t *out_tokens) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_generate: not a live model");
+  pbx_ctx *c = m->c;
+  const pbx_model_config &g = m->cfg;
+  if (n_steps <= 0 || !out_tokens || max_layers < 0)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_generate: bad arguments");
+  if (token < 0 || token >= g.vocab_size)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_generate: token %d out of range", token);
+  if (start_pos < 0 || (int64_t)start_pos + n_steps > g.max_seq)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_generate: positions [%d, %lld) exceed max_seq %d",
+                    start_pos, (long long)start_pos + n_steps, g.max_seq);
+  int rc = check_complete(m);
+  if (rc) return rc;
+  const int nl = max_layers == 0 ? g.n_layers : std::min(max_layers, g.n_layers);
+  if ((rc = set_state(m, start_pos, token, 0, true))) return rc;
+  for (int i = 0; i < n_steps; ++i)
+    if ((rc = run_step_layers(m, nl))) return rc;
+  if (hipMemcpyAsync(out_tokens, m->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost,
+                     c->stream) != hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_generate: step failed on the device");
+  return PBX_OK;
+}
+
 extern "C" int pbx_model_reset_cache(pbx_model *m) {
   if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_reset_cache: not a live model");
   return kv_fill(m, 0);
@@ -1394,7 +1485,8 @@ extern "C" int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int
   if (rc) return rc;
   if (!m->ops_ready && (rc = build_ops(m))) return rc;
   const int n = (int)m->ops.size();
-  std::vector<hipEvent_t> ev(n + 1, nullptr);
+  // a start and a stop event per kernel, stamped by the kernel's dispatch
+  std::vector<hipEvent_t> ev(2 * n, nullptr);
   for (auto &e : ev)
     if (hipEventCreate(&e) != hipSuccess) {
       for (auto &f : ev)
@@ -1404,19 +1496,14 @@ extern "C" int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int
   std::vector<double> acc(n, 0.0), bytes(n, 0.0);
   if ((rc = set_state(m, start_pos, token, 0, true))) goto out;
   for (int s = 0; s < n_steps && !rc; ++s) {
-    if (hipEventRecord(ev[0], c->stream) != hipSuccess) { rc = pbx_fail(c, PBX_EHIP, "event"); break; }
-    for (int i = 0; i < n && !rc; ++i) {
-      rc = enqueue_op(m, m->ops[i]);
-      if (!rc && hipEventRecord(ev[i + 1], c->stream) != hipSuccess)
-        rc = pbx_fail(c, PBX_EHIP, "pbx_model_profile: hipEventRecord failed");
-    }
-    if (rc || hipEventSynchronize(ev[n]) != hipSuccess) {
+    for (int i = 0; i < n && !rc; ++i) rc = enqueue_op(m, m->ops[i], ev[2 * i], ev[2 * i + 1]);
+    if (rc || hipEventSynchronize(ev[2 * n - 1]) != hipSuccess) {
       if (!rc) rc = pbx_fail(c, PBX_EHIP, "pbx_model_profile: step failed on the device");
       break;
     }
     for (int i = 0; i < n; ++i) {
       float ms = 0.f;
-      hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+      hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]);
       acc[i] += ms * 1e3;
       const Op &op = m->ops[i];
       bytes[i] += (op.kind == ARG_ATTN || op.kind == ARG_ATTN_SPLIT) ? op.bytes * (start_pos + s + 1)

@@ -198,6 +198,31 @@ int pbx_launch_fn(pbx_ctx *c, hipFunction_t f, const char *name, dim3 grid, dim3
   return PBX_OK;
 }
 
+// hip/hip_ext.h (its templates need the device-side headers a host-only
+// build does not include)
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX,
+                                               uint32_t globalWorkSizeY, uint32_t globalWorkSizeZ,
+                                               uint32_t localWorkSizeX, uint32_t localWorkSizeY,
+                                               uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void **kernelParams,
+                                               void **extra, hipEvent_t startEvent,
+                                               hipEvent_t stopEvent, uint32_t flags);
+
+// As pbx_launch_fn, with `start` / `stop` stamped by the kernel's own
+// dispatch (hipExtModuleLaunchKernel): their elapsed time is the kernel's
+// execution, without the queue's gaps before or after it.
+int pbx_launch_fn_timed(pbx_ctx *c, hipFunction_t f, const char *name, dim3 grid, dim3 block,
+                        void **args, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return PBX_OK;
+  hipError_t e = hipExtModuleLaunchKernel(f, grid.x * block.x, grid.y * block.y, grid.z * block.z,
+                                          block.x, block.y, block.z, 0,
+                                          stream ? stream : c->stream, args, nullptr, start, stop,
+                                          0);
+  if (e != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "launch of %s failed: %s", name, hipGetErrorString(e));
+  return PBX_OK;
+}
+
 int pbx_launch(pbx_ctx *c, int kernel, dim3 grid, dim3 block, void **args,
                hipStream_t stream) {
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return PBX_OK;

@@ -457,27 +457,33 @@ napi_value ModelSetTensor(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
-// modelForward(model, tokens, startPos) -> {logits: Float32Array [vocab], next}
+// modelForward(model, tokens, startPos, maxLayers = 0)
+//   -> {logits: Float32Array [vocab], next, layersUsed}
 napi_value ModelForward(napi_env env, napi_callback_info info) {
   if (!need_ctx(env)) return nullptr;
-  napi_value argv[3];
-  get_args(env, info, 3, argv);
+  napi_value argv[4];
+  get_args(env, info, 4, argv);
   ModelRef *r = get_model(env, argv[0]);
   std::vector<int32_t> toks;
-  int64_t start;
-  if (!r || !get_tokens(env, argv[1], &toks) || !get_i64(env, argv[2], &start))
-    return throw_msg(env, "modelForward(model, tokens, startPos): bad arguments");
+  int64_t start, max_layers = 0;
+  if (!r || !get_tokens(env, argv[1], &toks) || !get_i64(env, argv[2], &start) ||
+      (!is_nullish(env, argv[3]) && !get_i64(env, argv[3], &max_layers)))
+    return throw_msg(env, "modelForward(model, tokens, startPos, maxLayers): bad arguments");
   float *lg;
   napi_value logits = new_f32(env, (size_t)r->vocab, &lg);
   if (!logits) return throw_msg(env, "modelForward: out of memory");
   int32_t next = 0;
-  int rc = pbx_model_forward(r->m, toks.data(), (int)toks.size(), (int)start, lg, &next);
+  int used = 0;
+  int rc = pbx_model_forward_layers(r->m, toks.data(), (int)toks.size(), (int)start,
+                                    (int)max_layers, lg, &next, &used);
   if (rc) return throw_pbx(env, rc, "modelForward");
   napi_value o, nv;
   napi_create_object(env, &o);
   napi_set_named_property(env, o, "logits", logits);
   napi_create_int32(env, next, &nv);
   napi_set_named_property(env, o, "next", nv);
+  napi_create_int32(env, used, &nv);
+  napi_set_named_property(env, o, "layersUsed", nv);
   return o;
 }
 
@@ -606,6 +612,51 @@ napi_value Speculative(napi_env env, napi_callback_info info) {
   return o;
 }
 
+// selfSpeculative(model, prompt, maxTokens, draftLayers = 4, draftCount = 4, eosIds = [2],
+//                 batched = true)
+//   -> {tokens: Int32Array, rounds, drafted, accepted, prefillMs, decodeMs}
+napi_value SelfSpeculative(napi_env env, napi_callback_info info) {
+  if (!need_ctx(env)) return nullptr;
+  napi_value argv[7];
+  get_args(env, info, 7, argv);
+  ModelRef *r = get_model(env, argv[0]);
+  std::vector<int32_t> prompt, eos = {2};
+  int64_t maxTok, dl = 4, dc = 4;
+  if (!r || !get_tokens(env, argv[1], &prompt) || !get_i64(env, argv[2], &maxTok) ||
+      maxTok <= 0 || (!is_nullish(env, argv[3]) && !get_i64(env, argv[3], &dl)) ||
+      (!is_nullish(env, argv[4]) && !get_i64(env, argv[4], &dc)) ||
+      (!is_nullish(env, argv[5]) && !get_tokens(env, argv[5], &eos)))
+    return throw_msg(env, "selfSpeculative(model, prompt, maxTokens, draftLayers, draftCount, "
+                          "eosIds, batched): bad arguments");
+  bool batched = true;
+  if (!is_nullish(env, argv[6])) napi_get_value_bool(env, argv[6], &batched);
+  std::vector<int32_t> out((size_t)maxTok + 1);
+  int n = 0;
+  pbx_spec_stats st;
+  int rc = pbx_self_speculative_generate(r->m, prompt.data(), (int)prompt.size(), (int)maxTok,
+                                         (int)dl, (int)dc, eos.empty() ? nullptr : eos.data(),
+                                         (int)eos.size(), batched ? 1 : 0, out.data(), &n, &st);
+  if (rc) return throw_pbx(env, rc, "selfSpeculative");
+  int32_t *tk;
+  napi_value toks = new_i32(env, (size_t)n, &tk);
+  if (!toks) return throw_msg(env, "selfSpeculative: out of memory");
+  memcpy(tk, out.data(), (size_t)n * 4);
+  napi_value o, v;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "tokens", toks);
+  napi_create_int32(env, st.rounds, &v);
+  napi_set_named_property(env, o, "rounds", v);
+  napi_create_int32(env, st.drafted, &v);
+  napi_set_named_property(env, o, "drafted", v);
+  napi_create_int32(env, st.accepted, &v);
+  napi_set_named_property(env, o, "accepted", v);
+  napi_create_double(env, st.prefill_ms, &v);
+  napi_set_named_property(env, o, "prefillMs", v);
+  napi_create_double(env, st.decode_ms, &v);
+  napi_set_named_property(env, o, "decodeMs", v);
+  return o;
+}
+
 napi_value ModuleInit(napi_env env, napi_value exports) {
   struct {
     const char *name;
@@ -627,7 +678,8 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
              {"modelRollback", ModelRollback},
              {"modelReset", ModelReset},
              {"modelFree", ModelFree},
-             {"speculative", Speculative}};
+             {"speculative", Speculative},
+             {"selfSpeculative", SelfSpeculative}};
   for (auto &f : fns) {
     napi_value fn;
     napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn);

@@ -36,7 +36,7 @@ EXPORTS = (
     "pbx_model_create", "pbx_model_free", "pbx_model_set_tensor", "pbx_model_forward",
     "pbx_model_forward_batch", "pbx_model_generate", "pbx_model_reset_cache", "pbx_model_rollback", "pbx_model_info",
     "pbx_model_profile", "pbx_model_op_name", "pbx_model_bench_role",
-    "pbx_speculative_generate",
+    "pbx_speculative_generate", "pbx_model_forward_layers", "pbx_self_speculative_generate",
     "pbx_gguf_open", "pbx_gguf_close", "pbx_gguf_info", "pbx_gguf_tensor_info",
     "pbx_gguf_find_tensor", "pbx_gguf_get_int", "pbx_gguf_get_float", "pbx_gguf_get_string",
     "pbx_gguf_get_array", "pbx_gguf_model_config", "pbx_model_load_gguf",
@@ -153,6 +153,14 @@ def load_library():
         "pbx_model_set_tensor": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t]),
         "pbx_model_forward": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
         "pbx_model_forward_batch": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+        "pbx_model_forward_layers": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int,
+                                                    ctypes.c_int, _vp, _vp,
+                                                    ctypes.POINTER(ctypes.c_int)]),
+        "pbx_self_speculative_generate": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int,
+                                                         ctypes.c_int, ctypes.c_int, _vp,
+                                                         ctypes.c_int, ctypes.c_int, _vp,
+                                                         ctypes.POINTER(ctypes.c_int),
+                                                         ctypes.POINTER(SpecStats)]),
         "pbx_model_generate": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int, ctypes.c_int, _vp, _vp]),
         "pbx_model_reset_cache": (ctypes.c_int, [_vp]),
         "pbx_model_rollback": (ctypes.c_int, [_vp, ctypes.c_int]),
@@ -498,12 +506,17 @@ class Model:
         data = np.ascontiguousarray(data)
         self._mcall("pbx_model_set_tensor", tensor, layer, data.ctypes.data, data.nbytes)
 
-    def forward(self, tokens, start_pos, want_logits=True):
+    def forward(self, tokens, start_pos, want_logits=True, max_layers=0):
+        """(logits of the last position or None, their argmax); max_layers as
+        StreamingLlamaRuntime.forward's {maxLayers} (0: every layer)."""
         toks = np.ascontiguousarray(tokens, np.int32)
         logits = np.empty(self.vocab, np.float32) if want_logits else None
         nxt = ctypes.c_int32()
-        self._mcall("pbx_model_forward", toks.ctypes.data, len(toks), start_pos,
-                    None if logits is None else logits.ctypes.data, ctypes.byref(nxt))
+        used = ctypes.c_int()
+        self._mcall("pbx_model_forward_layers", toks.ctypes.data, len(toks), start_pos,
+                    int(max_layers), None if logits is None else logits.ctypes.data,
+                    ctypes.byref(nxt), ctypes.byref(used))
+        self.layers_used = used.value
         return logits, nxt.value
 
     def forward_batch(self, tokens, start_pos, want_logits=True):
@@ -576,6 +589,29 @@ def speculative_generate(target, draft, prompt, max_tokens, draft_count=4, eos_i
                                         draft_count, eos.ctypes.data if len(eos) else None,
                                         len(eos), 1 if batched_verify else 0, out.ctypes.data,
                                         ctypes.byref(n), ctypes.byref(st))
+    if rc != 0:
+        msg = ctx.L.pbx_last_error(ctx._p)
+        raise PbxError(rc, msg.decode() if msg else "")
+    stats = {k: getattr(st, k) for k, _ in SpecStats._fields_}
+    return out[:n.value].copy(), stats
+
+
+def self_speculative_generate(model, prompt, max_tokens, draft_layers=4, draft_count=4,
+                              eos_ids=(2,), batched_verify=True):
+    """SelfSpeculativeDecoder.generate (speculative.js:58-204), greedy, drafting
+    with the model's own first draft_layers layers.  Returns (generated
+    tokens, stats dict)."""
+    ctx = model.ctx
+    p = np.ascontiguousarray(prompt, np.int32)
+    eos = np.ascontiguousarray(list(eos_ids), np.int32)
+    out = np.empty(max_tokens + 1, np.int32)
+    n = ctypes.c_int()
+    st = SpecStats()
+    rc = ctx.L.pbx_self_speculative_generate(model._m, p.ctypes.data, len(p), max_tokens,
+                                             draft_layers, draft_count,
+                                             eos.ctypes.data if len(eos) else None, len(eos),
+                                             1 if batched_verify else 0, out.ctypes.data,
+                                             ctypes.byref(n), ctypes.byref(st))
     if rc != 0:
         msg = ctx.L.pbx_last_error(ctx._p)
         raise PbxError(rc, msg.decode() if msg else "")

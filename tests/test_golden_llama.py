@@ -64,3 +64,36 @@ def test_position_zero_attention_is_v(fixture):
     assert not np.array_equal(base.forward([8], 1), alt.forward([8], 1))
     base.close()
     alt.close()
+
+
+def test_max_layers_equals_truncated_model(fixture):
+    """StreamingLlamaRuntime.forward(tokens, pos, {maxLayers: L})
+    (llama-streaming.js:745, 764-792) runs the first L layers, then the final
+    norm and head: bit for bit the forward of a model holding only those L
+    layers, including over several calls that read the cache those layers
+    wrote.  maxLayers 0 (or >= nLayers) is the full forward."""
+    c = dict(fixture["config"])
+    full = oracle_model(fixture)
+    L = c["nLayers"] - 1
+    trunc = oracle.LlamaRef(c["dim"], c["hiddenDim"], L, c["nHeads"], c["nKvHeads"],
+                            c["dim"] // c["nHeads"], c["vocabSize"], c["seqLen"], c["ropeTheta"])
+    for tid, layer, w in lf.weights(fixture):
+        if layer < L:
+            trunc.set(tid, layer, w)
+    prompt = fixture["steps"][0]["tokens"]
+    assert np.array_equal(full.forward(prompt, 0, max_layers=L), trunc.forward(prompt, 0))
+    n = len(prompt)
+    for p, t in enumerate([3, 9, 27]):
+        assert np.array_equal(full.forward([t], n + p, max_layers=L), trunc.forward([t], n + p))
+    ref = oracle_model(fixture)
+    full.rollback(0)
+    a = full.forward(prompt, 0, max_layers=0)
+    full.rollback(0)
+    b = full.forward(prompt, 0, max_layers=c["nLayers"] + 3)
+    assert np.array_equal(a, ref.forward(prompt, 0)) and np.array_equal(a, b)
+    # the truncated forward differs from the full one (the last layer matters)
+    ref.rollback(0)
+    assert not np.array_equal(ref.forward(prompt, 0, max_layers=L), a)
+    full.close()
+    trunc.close()
+    ref.close()

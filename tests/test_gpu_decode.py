@@ -91,6 +91,50 @@ def test_llama1b_shape(ctx):
     assert exact >= 15
 
 
+def test_llama1b_prompt128_greedy64_every_step(ctx):
+    """Llama-3.2-1B-shaped Q4_0 decode at its workload's length: a 128-token
+    random prompt through the batched prefill, then 64 greedy steps replayed
+    from the captured step (llama.js:452-505).  The GPU's tokens are then fed
+    again one at a time from position 128 and every step's logits are
+    compared with the oracle's teacher-forced forward (llama.js:204-371) at
+    the logit tolerance; every greedy choice must be the oracle's argmax or
+    a tie below that tolerance."""
+    print("[case] llama32_1b 128-token prompt + 64 greedy, logits every step", flush=True)
+    model, ref, cfg = make_pair(ctx, "llama32_1b", 3300)
+    n_prompt, n_gen = 128, 64
+    prompt = synth.random_tokens(3301, n_prompt, cfg["vocab_size"])
+    ref_logits = ref.forward(prompt, 0)
+    logits, nxt = model.forward(prompt, 0)
+    worst = float(np.abs(logits - ref_logits).max())
+    assert worst <= LOGIT_TOL, f"prefill logits max-abs {worst:.2e}"
+    first = oracle.argmax(ref_logits)
+    if nxt != first:
+        assert ref_logits[first] - ref_logits[nxt] < LOGIT_TOL
+    toks = model.generate(nxt, n_prompt, n_gen)
+    # teacher-forced replay of the same tokens: positions 128 .. 191
+    model.rollback(n_prompt)
+    feed = [nxt] + [int(t) for t in toks[:-1]]
+    exact, ties = 0, 0
+    for i, tok in enumerate(feed):
+        g, gnext = model.forward([tok], n_prompt + i)
+        r = ref.forward([tok], n_prompt + i)
+        err = float(np.abs(g - r).max())
+        worst = max(worst, err)
+        assert err <= LOGIT_TOL, f"step {i}: logits max-abs {err:.2e}"
+        assert gnext == int(toks[i]), f"step {i}: replay chose {gnext}, generate chose {toks[i]}"
+        best = oracle.argmax(r)
+        if gnext == best:
+            exact += 1
+        else:
+            gap = float(r[best] - r[gnext])
+            assert gap < LOGIT_TOL, f"step {i}: GPU {gnext} vs oracle {best}, gap {gap:.3e}"
+            ties += 1
+    print(f"  exact={exact} ties={ties} worst logits max-abs={worst:.1e}")
+    assert exact >= n_gen - 2
+    model.free()
+    ref.close()
+
+
 def test_llama1b_shape_q4_1(ctx):
     """Llama-3.2-1B shapes with Q4_1 layer matrices and a tied Q4_1 head
     (the wide GEMV kernels and the row-batched prefill on Q4_1)."""

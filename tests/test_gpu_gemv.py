@@ -202,6 +202,40 @@ def test_f16_q6_k_dequant_and_matvec(ctx, t, N, K):
     w.free()
 
 
+def test_f16_all_patterns_on_gpu(ctx):
+    """float16ToFloat32 (gguf.js:55-70) on the GPU over all 65,536 patterns:
+    once as one F16 weight (gguf.js:231-237) and once as the fp16 scales of
+    65,536 Q8_0 blocks whose codes are +1 / -1 (gguf.js:239-257), so the
+    dequantised values are +-f16(pattern).  Bit-exact against the oracle,
+    NaN compared by isnan (subnormals, +-0, +-inf included)."""
+    print("[case] f16 all patterns (F16 weight, Q8_0 scales)", flush=True)
+    bits = np.arange(65536, dtype=np.uint16)
+    raw = bits.view(np.uint8).copy()
+    w = ctx.upload(pb.TYPE_F16, 64, 1024, raw)
+    got = ctx.dequant(w).ravel()
+    w.free()
+    ref = oracle.dequant_f16(raw, 65536)
+    ieee = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(nan, np.isnan(ieee)) and np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    assert np.array_equal(ref[~nan].view(np.uint32), ieee[~nan].view(np.uint32))
+    blk = np.zeros((65536, 34), np.uint8)
+    blk[:, :2] = bits.view(np.uint8).reshape(-1, 2)
+    blk[:, 2:18] = 1
+    blk[:, 18:] = 0xFF  # int8 -1
+    raw8 = blk.ravel()
+    w = ctx.upload(pb.TYPE_Q8_0, 2048, 1024, raw8)
+    got8 = ctx.dequant(w).reshape(65536, 32)
+    w.free()
+    ref8 = oracle.dequant_q8_0(raw8, 65536 * 32).reshape(65536, 32)
+    nan8 = np.isnan(ref8)
+    assert np.array_equal(np.isnan(got8), nan8)
+    assert np.array_equal(got8[~nan8].view(np.uint32), ref8[~nan8].view(np.uint32))
+    assert np.array_equal(got8[:, 0][~nan].view(np.uint32), ieee[~nan].view(np.uint32))
+    assert np.array_equal(got8[:, 31][~nan].view(np.uint32), (-ieee)[~nan].view(np.uint32))
+
+
 def test_q6_k_rejects_k_not_multiple_of_256(ctx):
     print("[case] q6_k K % 256", flush=True)
     with pytest.raises(pb.PbxError):
@@ -255,6 +289,43 @@ def test_integer_limb_instruction(ctx, monkeypatch, t, N, K, M, bias):
         ref = oracle.matvec(t, X[m], raw, N, K) + (b if bias else 0)
         assert rel_l2(Y[m], ref) < 1e-5, (m, rel_l2(Y[m], ref))
         assert rel_l2(Y[m], F[m]) < 1e-5
+    wf.free()
+    fctx.close()
+    w.free()
+
+
+@pytest.mark.parametrize("t", [pb.TYPE_Q4_0, pb.TYPE_Q8_0])
+@pytest.mark.parametrize("N,K", [(512, 2048), (2048, 8192), (70000, 2048)])
+def test_integer_limb_non_finite_activations(ctx, monkeypatch, t, N, K):
+    """A row of x holding +inf, -inf or NaN: the reference's sums
+    (llama-streaming.js:72-104) are then NaN or +-inf in every output; the
+    integer-limb kernels (one and several prologue slots, the tile loop)
+    must give non-finite outputs exactly where the oracle and the float
+    kernels (PBX_GEMV_INT=0) do, and the finite rows of the same call must
+    be unaffected."""
+    print(f"[case] integer-limb non-finite x type={t} N={N} K={K}", flush=True)
+    raw = quantize(t, synth_matrix(7 * N + K, N, K))
+    X = pb.synth_normal(N + 3 * K, 4 * K).reshape(4, K)
+    X[0, 5] = np.inf
+    X[1, K - 1] = -np.inf
+    X[2, K // 2] = np.nan
+    w = ctx.upload(t, N, K, raw)
+    Y = np.stack([ctx.linear(w, X[m]) for m in range(4)])
+    Y3 = ctx.linear(w, X[[3, 0, 3]])  # rows of one launch: finite, inf, finite
+    monkeypatch.setenv("PBX_GEMV_INT", "0")
+    fctx = pb.Context(0)
+    monkeypatch.delenv("PBX_GEMV_INT")
+    wf = fctx.upload(t, N, K, raw)
+    F = np.stack([fctx.linear(wf, X[m]) for m in range(4)])
+    for m in range(3):
+        ref = oracle.matvec(t, X[m], raw, N, K)
+        assert not np.isfinite(ref).any()
+        assert not np.isfinite(F[m]).any()
+        assert not np.isfinite(Y[m]).any(), (m, np.isfinite(Y[m]).sum())
+    ref3 = oracle.matvec(t, X[3], raw, N, K)
+    assert rel_l2(Y[3], ref3) < 1e-5
+    assert rel_l2(Y3[0], ref3) < 1e-5 and rel_l2(Y3[2], ref3) < 1e-5
+    assert not np.isfinite(Y3[1]).any()
     wf.free()
     fctx.close()
     w.free()

@@ -200,10 +200,9 @@ wr('all.bin', all.logits);
 const dr = mk();
 const sd = new HipSpeculativeDecoder(rt, dr, {{ draftCount: 4 }});
 const sp = sd.generate(meta.prompt, 20, {{ eosIds: [] }});
-let threw = false;
-try {{ rt.generate(meta.prompt, 4, {{}}); }} catch (e) {{ threw = true; }}
+const sampled = rt.generate(meta.prompt, 4, {{ eosId: -1 }}).tokens.slice(meta.prompt.length);
 console.log(JSON.stringify({{ gen: gen.tokens.slice(meta.prompt.length), spec: sp.tokens.slice(meta.prompt.length),
-  acc: sp.acceptanceRate, threw, argmax: rt.argmax(logits) }}));
+  acc: sp.acceptanceRate, sampled, argmax: rt.argmax(logits) }}));
 rt.free(); dr.free();
 """, {"cfg": cfg, "files": files, "prompt": prompt})
     res = json.loads(out.strip().splitlines()[-1])
@@ -212,7 +211,7 @@ rt.free(); dr.free();
     assert res["argmax"] == int(np.argmax(lj))
     assert res["gen"] == greedy
     assert res["spec"][:20] == greedy
-    assert res["threw"], "non-greedy generate must throw"
+    assert len(res["sampled"]) == 4 and all(0 <= t < cfg["vocab_size"] for t in res["sampled"])
     allj = np.fromfile(tmp_path / "all.bin", np.float32).reshape(-1, cfg["vocab_size"])
     assert allj.shape[0] == len(prompt) - 5
     assert float(np.abs(allj[-1] - logits).max()) <= 2e-3
@@ -248,3 +247,92 @@ rt.free();
     assert (c["dim"], c["hiddenDim"], c["nLayers"], c["nHeads"], c["nKvHeads"], c["vocabSize"]) == \
         (256, 512, 2, 4, 2, 1000)
     assert c["seqLen"] == 64 and c["embedType"] == TYPE_Q6_K and res["threw"]
+
+
+def test_streaming_runtime_max_layers_sampling_self_spec(ctx, tmp_path):
+    """HipStreamingLlamaRuntime through Node, as StreamingLlamaRuntime's callers
+    use it (llama-streaming.js:738-970, speculative.js:58-204):
+    * forward(tokens, pos, {maxLayers: 4}) -> {logits, layersUsed: 4}, logits
+      within 2e-3 of the oracle's forward truncated to 4 layers (prefill and
+      decode steps), and the full forward afterwards;
+    * generate() with sampling: a seeded draw source gives the same tokens as
+      forward + sample() step by step;
+    * HipSelfSpeculativeDecoder (draft = the first 2 layers) in greedy mode
+      emits the greedy tokens; with sampling it emits maxTokens tokens."""
+    print("[case] js streaming runtime maxLayers / sampling / self-speculative", flush=True)
+    from tests.e2e_util import make_pair
+    cfg = dict(dim=256, hidden_dim=512, n_layers=6, n_heads=4, n_kv_heads=2, vocab_size=1000,
+               max_seq=96, weight_type=TYPE_Q4_0, embed_type=TYPE_Q4_0, rope_theta=10000.0)
+    names = {0: "token_embd.weight", 2: "output_norm.weight", 3: "attn_norm.weight",
+             4: "ffn_norm.weight", 5: "attn_q.weight", 6: "attn_k.weight", 7: "attn_v.weight",
+             8: "attn_output.weight", 9: "ffn_gate.weight", 10: "ffn_up.weight",
+             11: "ffn_down.weight"}
+    files = []
+
+    def keep(spec, data):
+        tid, layer, N, K, t = spec
+        nm = names[tid] if layer < 0 else f"blk.{layer}.{names[tid]}"
+        fn = f"t{len(files)}.bin"
+        np.ascontiguousarray(data).tofile(tmp_path / fn)
+        files.append([nm, fn, "f32" if data.dtype == np.float32 else "u8"])
+
+    model = synth.build(ctx, cfg, 650, keep)
+    model.free()
+    _, ref, _ = make_pair(ctx, cfg, 650)
+    prompt = [int(t) for t in synth.random_tokens(651, 12, cfg["vocab_size"])]
+    steps = [(int(t), L) for t, L in zip(synth.random_tokens(652, 4, 1000), (4, 4, 0, 2))]
+    want = [ref.forward(prompt, 0, max_layers=4)]
+    for i, (t, L) in enumerate(steps):
+        want.append(ref.forward([t], 12 + i, max_layers=L))
+    ref.close()
+    out = run_node(tmp_path, f"""
+const {{ HipStreamingLlamaRuntime, HipSelfSpeculativeDecoder, sampleTopK }} =
+  require({os.path.join(JS, 'llama-hip.js')!r});
+const c = meta.cfg;
+const seeded = (s) => () => {{ s = (s * 16807) % 2147483647; return (s - 1) / 2147483646; }};
+const rt = new HipStreamingLlamaRuntime({{ dim: c.dim, hiddenDim: c.hidden_dim, nLayers: c.n_layers,
+  nHeads: c.n_heads, nKvHeads: c.n_kv_heads, vocabSize: c.vocab_size, seqLen: c.max_seq,
+  ropeTheta: c.rope_theta, weightType: 'q4_0', embedType: 'q4_0' }});
+for (const [nm, fn, ty] of meta.files) rt.loadTensor(nm, rd(fn, ty === 'f32' ? Float32Array : Uint8Array));
+const used = [];
+let r = rt.forward(meta.prompt, 0, {{ maxLayers: 4 }});
+used.push(r.layersUsed); wr('l0.bin', r.logits);
+meta.steps.forEach(([t, L], i) => {{
+  r = rt.forward([t], 12 + i, L ? {{ maxLayers: L }} : {{}});
+  used.push(r.layersUsed); wr('l' + (i + 1) + '.bin', r.logits);
+}});
+// sampled generate vs forward + sample with the same draws
+rt.random = seeded(7);
+const gen = rt.generate(meta.prompt, 10, {{ temperature: 0.7, topK: 20, eosId: -1 }});
+const rnd = seeded(7);
+rt.resetCache();
+let lg = rt.forward(meta.prompt, 0).logits, pos = meta.prompt.length;
+const manual = [];
+for (let i = 0; i < 10; i++) {{
+  const t = sampleTopK(lg, 20, 0.7, rnd, false);
+  manual.push(t);
+  if (i < 9) lg = rt.forward([t], pos++).logits;
+}}
+const greedy = rt.generate(meta.prompt, 24, {{ greedy: true, eosId: -1 }});
+const sd = new HipSelfSpeculativeDecoder(rt, {{ draftLayers: 2, draftCount: 4 }});
+const sg = sd.generate(meta.prompt, 24, {{ greedy: true, eosIds: [] }});
+const ss = sd.generate(meta.prompt, 16, {{ eosIds: [], temperature: 0.7 }});
+console.log(JSON.stringify({{ used, gen: gen.tokens.slice(meta.prompt.length), manual,
+  avgLayers: gen.avgLayers, greedy: greedy.tokens.slice(meta.prompt.length),
+  sg: sg.tokens.slice(meta.prompt.length), ss: ss.tokens.slice(meta.prompt.length),
+  stats: sd.stats }}));
+rt.free();
+""", {"cfg": cfg, "files": files, "prompt": prompt, "steps": steps})
+    res = json.loads(out.strip().splitlines()[-1])
+    print(f"  {res['stats']}")
+    assert res["used"] == [4, 4, 4, 6, 2]
+    worst = 0.0
+    for i, w in enumerate(want):
+        got = np.fromfile(tmp_path / f"l{i}.bin", np.float32)
+        worst = max(worst, float(np.abs(got - w).max()))
+    print(f"  maxLayers logits worst max-abs {worst:.2e}")
+    assert worst <= 2e-3
+    assert res["gen"] == res["manual"] and len(res["gen"]) == 10
+    assert res["avgLayers"] == "6.0"
+    assert res["sg"][:24] == res["greedy"]
+    assert len(res["ss"]) in (16, 17) and all(0 <= t < 1000 for t in res["ss"])

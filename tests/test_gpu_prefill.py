@@ -15,7 +15,8 @@ import pytest
 
 import oracle
 from purebee_amd import PbxError, synth
-from purebee_amd.native import TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, speculative_generate
+from purebee_amd.native import (TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, self_speculative_generate,
+                                speculative_generate)
 from tests.e2e_util import LOGIT_TOL, make_pair
 
 pytestmark = pytest.mark.gpu
@@ -158,6 +159,39 @@ def test_llama1b_verify_rows_equal_sequential(ctx):
     model.free()
 
 
+def test_row_batched_kernels_vs_oracle(ctx):
+    """The up-to-8-row verify kernels (skinny MFMA gate|up + SwiGLU and LM
+    head, integer-limb rows GEMVs for q|k|v, o and down, batched-row
+    attention) run for Q4_0 models with dim <= 2048, 6144 < hidden <= 8192
+    and a Q4_0 head.  A one-layer model of that shape with a small
+    vocabulary, after a 40-token prompt: forward_batch of n = 1, 5 and 8
+    rows, every row's logits against the oracle's forward at the same
+    position (llama.js:204-371, teacher-forced on the same tokens)."""
+    print("[case] 1-layer dim 2048 / hidden 8192 Q4_0 rows kernels vs oracle", flush=True)
+    cfg = dict(dim=2048, hidden_dim=8192, n_layers=1, n_heads=32, n_kv_heads=8, vocab_size=4096,
+               max_seq=128, weight_type=TYPE_Q4_0, embed_type=TYPE_Q4_0, rope_theta=500000.0)
+    model, ref, cfg = make_pair(ctx, cfg, 3400)
+    prompt = [int(t) for t in synth.random_tokens(3401, 40, cfg["vocab_size"])]
+    model.forward(prompt, 0)
+    ref.forward(prompt, 0)
+    worst = 0.0
+    for n in (1, 5, 8):
+        rows = [int(t) for t in synth.random_tokens(3402 + n, n, cfg["vocab_size"])]
+        model.rollback(40)
+        ref.rollback(40)
+        logits, nxt = model.forward_batch(rows, 40)
+        for t, tok in enumerate(rows):
+            r = ref.forward([tok], 40 + t)
+            err = float(np.abs(logits[t] - r).max())
+            worst = max(worst, err)
+            assert err <= LOGIT_TOL, f"n={n} row {t}: max-abs {err:.2e}"
+            best = oracle.argmax(r)
+            assert nxt[t] == best or top_gap(r, best, nxt[t]) < LOGIT_TOL
+    print(f"  worst max-abs {worst:.2e}")
+    model.free()
+    ref.close()
+
+
 @pytest.mark.parametrize("n", [1, 3, 6, 8])
 def test_llama1b_row_batched_gemvs(ctx, monkeypatch, n):
     """Up to 8 rows through the row-batched integer-limb GEMVs (one pass over
@@ -294,6 +328,79 @@ def test_speculative_config_shapes(ctx):
     assert list(out_b) == list(out_s)
     target.free()
     draft.free()
+
+
+@pytest.mark.parametrize("wt", [TYPE_Q4_0, TYPE_Q8_0])
+def test_forward_max_layers_vs_truncated_oracle(ctx, wt):
+    """StreamingLlamaRuntime.forward(tokens, pos, {maxLayers}) (llama-streaming.js:
+    738-815): the first L layers, then the final norm and head, against the
+    oracle's forward with the same limit -- through the batched prefill (a
+    prompt of >= 4 tokens) and the captured decode step of L layers (one
+    token); then the full forward resumes with the cache the partial calls
+    left (later layers unwritten at those positions, as in the reference)."""
+    print(f"[case] forward maxLayers vs oracle weights={wt}", flush=True)
+    model, ref, cfg = make_pair(ctx, tiny(wt, wt, n_layers=6), 430 + wt)
+    prompt = [int(t) for t in synth.random_tokens(431, 12, cfg["vocab_size"])]
+    worst = 0.0
+    g, _ = model.forward(prompt, 0, max_layers=4)
+    assert model.layers_used == 4
+    r = ref.forward(prompt, 0, max_layers=4)
+    worst = max(worst, float(np.abs(g - r).max()))
+    for i, t in enumerate(synth.random_tokens(432, 6, cfg["vocab_size"])):
+        L = (4, 2, 4, 0, 9, -1)[i]
+        g, nxt = model.forward([int(t)], 12 + i, max_layers=L)
+        assert model.layers_used == (6 if L in (0, 9) else max(L, 0))
+        r = ref.forward([int(t)], 12 + i, max_layers=L)
+        worst = max(worst, float(np.abs(g - r).max()))
+        assert nxt == int(np.argmax(g))
+    g, _ = model.forward([7, 8, 9, 10, 11], 18)  # full layers over the mixed cache
+    r = ref.forward([7, 8, 9, 10, 11], 18)
+    worst = max(worst, float(np.abs(g - r).max()))
+    print(f"  worst max-abs {worst:.2e}")
+    assert worst <= LOGIT_TOL
+    model.free()
+    ref.close()
+
+
+@pytest.mark.parametrize("batched", [True, False])
+def test_self_speculative_equals_greedy(ctx, batched):
+    """SelfSpeculativeDecoder's own scheme (speculative.js:58-204, draft =
+    the first draftLayers layers of the target, speculative.js:96-111) in
+    greedy mode emits the model's greedy tokens; with draftLayers = nLayers
+    the draft is the full model and every draft is accepted."""
+    print(f"[case] self-speculative batched={batched}", flush=True)
+    tcfg = tiny(TYPE_Q4_0, TYPE_Q4_0, n_layers=4, max_seq=200)
+    model = synth.build(ctx, tcfg, 440)
+    prompt = [int(t) for t in synth.random_tokens(441, 16, tcfg["vocab_size"])]
+    n_gen = 40
+    ref = _greedy(model, prompt, n_gen)
+    out, st = self_speculative_generate(model, prompt, n_gen, draft_layers=2, draft_count=4,
+                                        eos_ids=(), batched_verify=batched)
+    print(f"  draft 2 layers: {st}")
+    assert list(out[:n_gen]) == ref and len(out) in (n_gen, n_gen + 1)
+    assert st["rounds"] > 0 and st["drafted"] >= st["rounds"]
+    out, st = self_speculative_generate(model, prompt, n_gen, draft_layers=4, draft_count=4,
+                                        eos_ids=(), batched_verify=batched)
+    print(f"  draft 4 layers: {st}")
+    assert list(out[:n_gen]) == ref
+    assert st["accepted"] >= st["drafted"] - 2  # near-ties between batched and single rows
+    # the cache after the run equals a plain greedy run's over the same tokens
+    n = len(out)
+    a, _ = model.forward([int(out[-1])], len(prompt) + n - 1)
+    model.reset_cache()
+    model.forward(prompt, 0)
+    model.forward([int(t) for t in out[:-1]], len(prompt))
+    b, _ = model.forward([int(out[-1])], len(prompt) + n - 1)
+    assert float(np.abs(a - b).max()) <= LOGIT_TOL
+    eos = ref[7]
+    out, _ = self_speculative_generate(model, prompt, n_gen, draft_layers=2, eos_ids=(eos,),
+                                       batched_verify=batched)
+    assert list(out) == ref[:ref.index(eos) + 1]
+    with pytest.raises(PbxError):
+        self_speculative_generate(model, prompt, n_gen, draft_layers=0)
+    with pytest.raises(PbxError):
+        self_speculative_generate(model, prompt, 190, draft_layers=2)  # beyond max_seq
+    model.free()
 
 
 def test_speculative_errors(ctx):

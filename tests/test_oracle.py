@@ -133,6 +133,68 @@ def test_dequant_every_byte_value():
     assert np.array_equal(W8, np.arange(256).astype(np.uint8).view(np.int8).astype(np.float32) * -1.5)
 
 
+def q8_0_from_q4_0(raw0):
+    """Q4_0 blocks -> Q8_0 blocks with the same d and int8 codes nibble - 8
+    (gguf.js:239-286: both decode to code * d)."""
+    b0 = raw0.reshape(-1, 18)
+    b8 = np.zeros((b0.shape[0], 34), np.uint8)
+    b8[:, :2] = b0[:, :2]
+    lo = (b0[:, 2:] & 15).astype(np.int16) - 8
+    hi = (b0[:, 2:] >> 4).astype(np.int16) - 8
+    b8[:, 2:18] = lo.astype(np.int8).view(np.uint8)
+    b8[:, 18:34] = hi.astype(np.int8).view(np.uint8)
+    return b8.ravel()
+
+
+def numpy_dequant_q8_0(raw, N, K):
+    """gguf.js:239-257 written independently of the oracle: int8 * fp16 d."""
+    blk = raw.reshape(N * K // 32, 34)
+    d = blk[:, :2].copy().view(np.float16).astype(np.float32)
+    q = blk[:, 2:].copy().view(np.int8).astype(np.float32)
+    return (q * d).reshape(N, K)
+
+
+def test_q8_0_matvec_reference_kat_reencoded():
+    """The Q4_0 KAT of wasm-q4.js:673-704 re-encoded as Q8_0 blocks (d = 1
+    with int8 1s, d = 2 with int8 2s) must give exactly [32, 128] through the
+    Q8_0 checker of every Q8_0 GPU matvec and GEMM test."""
+    raw8 = q8_0_from_q4_0(kat_q4_0_raw())
+    assert np.array_equal(raw8.reshape(2, 34)[0, 2:].view(np.int8), np.ones(32, np.int8))
+    assert np.array_equal(raw8.reshape(2, 34)[1, 2:].view(np.int8), np.full(32, 2, np.int8))
+    out = oracle.q8_0_matvec(np.ones(32, np.float32), raw8, 2, 32)
+    assert out[0] == 32.0 and out[1] == 128.0
+
+
+def test_q8_0_matvec_columns_and_exact_product():
+    """x = e_k must return column k of the dequantised matrix (bit-exact),
+    every int8 value and sign included; a general x must equal the exactly
+    rounded dequantised product to within the final fp32 rounding.  A wrong
+    block stride, an unsigned code or a per-row scale fails the first."""
+    rng = np.random.default_rng(21)
+    N, K = 5, 96
+    raw = rng.integers(0, 256, N * (K // 32) * 34, dtype=np.uint8)
+    for b in range(N * K // 32):
+        raw[b * 34:b * 34 + 2] = np.frombuffer(
+            np.float16(rng.uniform(-2, 2)).tobytes(), np.uint8)
+    raw.reshape(-1, 34)[0, 2:34] = np.arange(-128, 128, 8).astype(np.int8).view(np.uint8)
+    W = numpy_dequant_q8_0(raw, N, K)
+    for k in range(K):
+        e = np.zeros(K, np.float32)
+        e[k] = 1
+        assert np.array_equal(oracle.q8_0_matvec(e, raw, N, K), W[:, k]), k
+    import math
+    x = rng.normal(0, 1, K).astype(np.float32)
+    out = oracle.q8_0_matvec(x, raw, N, K)
+    for n in range(N):
+        exact = math.fsum(float(W[n, k]) * float(x[k]) for k in range(K))
+        assert abs(float(out[n]) - exact) <= abs(exact) * 2.0 ** -23 + 1e-30, (n, out[n], exact)
+    # agrees with the Q4_0 checker on blocks both formats can hold
+    raw4 = oracle.quantize_q4_0(rng.normal(0, 0.02, (N, K)).astype(np.float32))
+    x = rng.normal(0, 1, K).astype(np.float32)
+    assert rel_l2(oracle.q8_0_matvec(x, q8_0_from_q4_0(raw4), N, K),
+                  oracle.q4_0_matvec_js(x, raw4, N, K)) < 1e-12
+
+
 def test_dequant_partial_last_block():
     rng = np.random.default_rng(3)
     raw = rng.integers(0, 256, 2 * 18, dtype=np.uint8)
