@@ -117,6 +117,18 @@ int pbx_linear(pbx_ctx *ctx, const pbx_weight *W, const float *X, int64_t M,
                const float *bias, float *Y);
 int pbx_linear_dev(pbx_ctx *ctx, const pbx_weight *W, const float *dX,
                    int64_t M, const float *dBias, float *dY);
+/* pbx_linear_dev that allocates nothing: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The same
+ * kernels and results as pbx_linear_dev; the M >= 4 GEMM's activation pair,
+ * row scales and split-K partials live in one static device array of
+ * PBX_NOALLOC_WORKSPACE_BYTES per GPU (held until the process ends) instead
+ * of the context's grow-only buffers.  A shape that needs more workspace
+ * fails with PBX_EINVAL.  Calls on one GPU share that array: calls that
+ * overlap on one GPU (other contexts or streams) race. */
+#define PBX_NOALLOC_WORKSPACE_BYTES (64u << 20)
+int pbx_linear_dev_noalloc(pbx_ctx *ctx, const pbx_weight *W, const float *dX, int64_t M,
+                           const float *dBias, float *dY);
 
 /* Exact dequantisation of a resident weight to fp32, row-major [N,K]
  * (for PBX_TYPE_Q8_REF: [K,N], the reference's own orientation).

@@ -63,11 +63,21 @@ def build_runtime(verbose=False):
     os.makedirs(LIB, exist_ok=True)
     rdir = os.path.join(PKG, "csrc", "runtime")
     srcs = sorted(os.path.join(rdir, f) for f in os.listdir(rdir) if f.endswith(".cpp"))
+    incs = ["-I", os.path.join(ROOT, "include"), "-I", rdir]
+    # runtime files with device code (the static workspace array): compiled by
+    # hipcc for gfx950 into objects linked into the library
+    objs = []
+    for f in sorted(os.listdir(rdir)):
+        if f.endswith(".hip"):
+            obj = os.path.join(LIB, f[:-4] + ".o")
+            _run([HIPCC, "-c", "-fPIC", *HIP_FLAGS, *incs, os.path.join(rdir, f), "-o", obj],
+                 verbose)
+            objs.append(obj)
     out = os.path.join(LIB, "libpbhip.so")
     tmp = out + ".tmp"
     _run(["g++", *HOST_FLAGS, "-shared", "-fopenmp",
-          "-I", os.path.join(ROOT, "include"), "-I", rdir, "-I", os.path.join(ROCM, "include"),
-          *srcs, "-o", tmp,
+          *incs, "-I", os.path.join(ROCM, "include"),
+          *srcs, *objs, "-o", tmp,
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
           "-Wl,--no-undefined"], verbose)
     os.replace(tmp, out)

@@ -43,6 +43,26 @@ const char *gemm_tag(int type) {
   }
 }
 
+// `need` bytes of workspace: from ws when the caller brings one (an error if
+// it is too small), else the context's grow-only GEMM buffer.
+int workspace(pbx_ctx *c, const pbx_workspace *ws, size_t need, char **out) {
+  if (ws) {
+    if (!ws->ptr)
+      return pbx_fail(c, PBX_ENOTSUP, "pbx_linear: no device workspace available");
+    if (need > ws->bytes)
+      return pbx_fail(c, PBX_EINVAL,
+                      "pbx_linear: this shape needs %zu bytes of workspace, above the %zu-byte "
+                      "limit of the no-allocation entry point",
+                      need, ws->bytes);
+    *out = (char *)ws->ptr;
+    return PBX_OK;
+  }
+  int rc = pbx_ensure_dev(c, &c->d_gemm, &c->d_gemm_cap, need);
+  if (rc) return rc;
+  *out = (char *)c->d_gemm;
+  return PBX_OK;
+}
+
 // Sum of the split-K partials into dY (+ bias, or accumulated).
 int launch_reduce(pbx_ctx *c, float *part, const float *dBias, float *dY, int M, int N, int KS,
                   int accumulate, hipStream_t stream) {
@@ -59,7 +79,7 @@ int launch_reduce(pbx_ctx *c, float *part, const float *dBias, float *dY, int M,
 // wave tile 16*MT x 16*NT (MT 1 / 2 for M <= 16 / <= 32), K split for about
 // eight waves per CU.
 int launch_f32(pbx_ctx *c, const pbx_weight *w, const float *dX, int M, const float *dBias,
-               float *dY, int accumulate, hipStream_t stream) {
+               float *dY, int accumulate, hipStream_t stream, const pbx_workspace *ws) {
   const int N = (int)w->N, B = (int)w->B;
   if (M > 32) {
     // 128 x 128 tiles on the LDS-DMA kernel, K split (16-k steps) for about
@@ -69,9 +89,10 @@ int launch_f32(pbx_ctx *c, const pbx_weight *w, const float *dX, int M, const fl
     if (wgs < c->cu_count) KS = std::min({2 * B, 8, (c->cu_count + wgs - 1) / wgs});
     float *part = nullptr;
     if (KS > 1) {
-      int rc = pbx_ensure_dev(c, &c->d_gemm, &c->d_gemm_cap, (size_t)KS * M * N * 4);
+      char *p = nullptr;
+      int rc = workspace(c, ws, (size_t)KS * M * N * 4, &p);
       if (rc) return rc;
-      part = (float *)c->d_gemm;
+      part = (float *)p;
     }
     hipFunction_t fg = pbx_kernel_by_name(c, "pbx_gemm_f32_big");
     if (!fg) return pbx_fail(c, PBX_ELOAD, "pbx_gemm: kernel pbx_gemm_f32_big missing");
@@ -96,9 +117,10 @@ int launch_f32(pbx_ctx *c, const pbx_weight *w, const float *dX, int M, const fl
   if (waves < 8 * c->cu_count) KS = std::min({B, 8, (8 * c->cu_count + waves - 1) / waves});
   float *part = nullptr;
   if (KS > 1) {
-    int rc = pbx_ensure_dev(c, &c->d_gemm, &c->d_gemm_cap, (size_t)KS * M * N * 4);
+    char *p = nullptr;
+    int rc = workspace(c, ws, (size_t)KS * M * N * 4, &p);
     if (rc) return rc;
-    part = (float *)c->d_gemm;
+    part = (float *)p;
   }
   const std::string name = "pbx_gemm_f32_m" + std::to_string(MT) + "_n" + std::to_string(NT);
   hipFunction_t fg = pbx_kernel_by_name(c, name);
@@ -172,12 +194,13 @@ int pbx_gemm_run(pbx_ctx *c, const pbx_weight *w, const pbx_gemm_plan &p, const 
 }
 
 int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M64,
-                    const float *dBias, float *dY, int accumulate, hipStream_t stream) {
+                    const float *dBias, float *dY, int accumulate, hipStream_t stream,
+                    const pbx_workspace *wsp) {
   if (!gemm_tag(w->type))
     return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: weight type %d has no MFMA path", w->type);
   if (M64 > 65535) return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: M=%lld too large", (long long)M64);
   if (w->type == PBX_TYPE_F32)
-    return launch_f32(c, w, dX, (int)M64, dBias, dY, accumulate, stream);
+    return launch_f32(c, w, dX, (int)M64, dBias, dY, accumulate, stream, wsp);
   const int M = (int)M64, N = (int)w->N, K = (int)w->B * 32;
   pbx_gemm_plan p;
   int rc = pbx_gemm_make_plan(c, w, M, &p);
@@ -187,10 +210,8 @@ int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M6
   const size_t lo_bytes = x16_bytes;
   const size_t inv_bytes = ((size_t)p.Mpad * 4 + 255) / 256 * 256;
   const size_t part_bytes = p.KS > 1 ? (size_t)p.KS * M * N * 4 : 0;
-  if ((rc = pbx_ensure_dev(c, &c->d_gemm, &c->d_gemm_cap,
-                           x16_bytes + lo_bytes + inv_bytes + part_bytes)))
-    return rc;
-  char *ws = (char *)c->d_gemm;
+  char *ws = nullptr;
+  if ((rc = workspace(c, wsp, x16_bytes + lo_bytes + inv_bytes + part_bytes, &ws))) return rc;
   void *x16 = ws;
   void *x16lo = ws + x16_bytes;
   float *inv = (float *)(ws + x16_bytes + lo_bytes);
@@ -211,6 +232,6 @@ int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M6
 }
 
 int pbx_gemm_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
-                     const float *dBias, float *dY, hipStream_t stream) {
-  return pbx_gemm_launch(c, w, dX, M, dBias, dY, 0, stream);
+                     const float *dBias, float *dY, hipStream_t stream, const pbx_workspace *ws) {
+  return pbx_gemm_launch(c, w, dX, M, dBias, dY, 0, stream, ws);
 }

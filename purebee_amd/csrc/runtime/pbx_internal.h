@@ -100,6 +100,11 @@ struct pbx_ctx {
   void *h_stage[2] = {nullptr, nullptr};
   size_t h_stage_cap[2] = {0, 0};
   void *models = nullptr;  // decode-step models owned by this context
+  // this device's copy of the library's static device array (pbx_scratch.hip),
+  // the workspace of pbx_linear_dev_noalloc; null when the lookup failed
+  void *scratch = nullptr;
+  size_t scratch_bytes = 0;
+  std::string scratch_err;
   std::unordered_map<std::string, hipFunction_t> named;  // kernels looked up by name
 };
 
@@ -129,8 +134,19 @@ int pbx_weight_write_rows(pbx_ctx *c, pbx_weight *w, int64_t row0, int64_t rows,
 void pbx_weight_release(pbx_weight *w);
 int pbx_ensure_dev(pbx_ctx *c, void **p, size_t *cap, size_t need);
 int pbx_ensure_pinned(pbx_ctx *c, void **p, size_t *cap, size_t need);
+// Device memory a launch path may use instead of growing the context's own
+// buffers (pbx_linear_dev_noalloc); a path that would need more fails.
+struct pbx_workspace {
+  void *ptr;
+  size_t bytes;
+};
 int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
-                       const float *dBias, float *dY, hipStream_t stream);
+                       const float *dBias, float *dY, hipStream_t stream,
+                       const pbx_workspace *ws = nullptr);
+// Bytes of the static device workspace (pbx_scratch.hip) and the lookup of
+// its address on the context's device (call with that device current).
+#define PBX_SCRATCH_BYTES ((size_t)PBX_NOALLOC_WORKSPACE_BYTES)
+int pbx_scratch_lookup(pbx_ctx *c);
 // The fp16 MFMA GEMM in two parts, for callers that prepare the fp16
 // activation pair (X16, X16lo, inv: [Mpad][K]) themselves: the kernel, grid
 // and K split for M rows of weight w, and the launch, which writes Y (KS == 1,
@@ -144,9 +160,11 @@ int pbx_gemm_run(pbx_ctx *c, const pbx_weight *w, const pbx_gemm_plan &p, const 
                  const void *x16lo, const float *inv, const float *dBias, float *out,
                  int accumulate, hipStream_t stream);
 int pbx_gemm_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
-                     const float *dBias, float *dY, hipStream_t stream);
+                     const float *dBias, float *dY, hipStream_t stream,
+                     const pbx_workspace *ws = nullptr);
 int pbx_gemm_launch(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
-                    const float *dBias, float *dY, int accumulate, hipStream_t stream);
+                    const float *dBias, float *dY, int accumulate, hipStream_t stream,
+                    const pbx_workspace *ws = nullptr);
 // Bytes of one GGUF row of K elements (0 for an unknown type).
 size_t pbx_type_row_bytes(int type, int64_t K);
 void pbx_model_release_all(pbx_ctx *c);

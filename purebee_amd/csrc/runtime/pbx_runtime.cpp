@@ -110,6 +110,9 @@ extern "C" int pbx_init(int device, pbx_ctx **out) {
     const char *gi = getenv("PBX_GEMV_INT");
     c->gemv_int = !(gi && gi[0] == '0');
   }
+  // the no-allocation entry point's workspace on this device (a failed
+  // lookup only disables that entry point)
+  (void)pbx_scratch_lookup(c);
   for (int m = 0; m < kModuleCount; ++m) {
     std::string path = dir + "/" + kModuleFiles[m];
     e = hipModuleLoad(&c->modules[m], path.c_str());
@@ -527,7 +530,8 @@ extern "C" int pbx_weight_info(const pbx_weight *w, int *type, int64_t *N, int64
 // The instruction.
 // ---------------------------------------------------------------------------
 int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t M,
-                       const float *dBias, float *dY, hipStream_t stream) {
+                       const float *dBias, float *dY, hipStream_t stream,
+                       const pbx_workspace *ws) {
   if (M > 65535) return pbx_fail(c, PBX_ENOTSUP, "pbx_linear: M=%lld > 65535", (long long)M);
   int N = (int)w->N;
   const unsigned gy = (unsigned)M;
@@ -540,7 +544,7 @@ int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t
   // Q6_K rows stay on the GEMV kernels for every M (one grid row per
   // activation row); the MFMA GEMM covers the other types.
   if (M >= PBX_GEMM_MIN_M && w->type != PBX_TYPE_Q6_K)
-    return pbx_gemm_enqueue(c, w, dX, M, dBias, dY, stream);
+    return pbx_gemm_enqueue(c, w, dX, M, dBias, dY, stream, ws);
   int B = (int)w->B;
   // Integer-limb kernels (gemv_int) for Q4_0 / Q8_0 with K = 2048..8192 (not
   // 4097..6144): rows per workgroup by N so the grid keeps >= 256 workgroups
@@ -631,6 +635,18 @@ extern "C" int pbx_linear_dev(pbx_ctx *c, const pbx_weight *w, const float *dX, 
   if (rc) return rc;
   HIPCHK(c, hipSetDevice(c->device));
   return pbx_linear_enqueue(c, w, dX, M, dBias, dY, c->stream);
+}
+
+extern "C" int pbx_linear_dev_noalloc(pbx_ctx *c, const pbx_weight *w, const float *dX,
+                                      int64_t M, const float *dBias, float *dY) {
+  int rc = check_linear_args(c, w, dX, M, dY, "pbx_linear_dev_noalloc");
+  if (rc) return rc;
+  if (!c->scratch)
+    return pbx_fail(c, PBX_ENOTSUP, "pbx_linear_dev_noalloc: no device workspace (%s)",
+                    c->scratch_err.c_str());
+  HIPCHK(c, hipSetDevice(c->device));
+  const pbx_workspace ws{c->scratch, c->scratch_bytes};
+  return pbx_linear_enqueue(c, w, dX, M, dBias, dY, c->stream, &ws);
 }
 
 extern "C" int pbx_linear(pbx_ctx *c, const pbx_weight *w, const float *X, int64_t M,

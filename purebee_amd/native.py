@@ -26,7 +26,7 @@ STATUS = {0: "PBX_OK", -1: "PBX_EINVAL", -2: "PBX_ENODEV", -3: "PBX_ENOMEM",
 EXPORTS = (
     "pbx_init", "pbx_shutdown", "pbx_last_error", "pbx_device_info",
     "pbx_weight_upload", "pbx_weight_upload_q8ref", "pbx_weight_free", "pbx_weight_info",
-    "pbx_linear", "pbx_linear_dev", "pbx_dequant", "pbx_dequant_dev",
+    "pbx_linear", "pbx_linear_dev", "pbx_linear_dev_noalloc", "pbx_dequant", "pbx_dequant_dev",
     "pbx_quantize_q8_0", "pbx_quantize_q4_0", "pbx_quantize_q4_1", "pbx_quantize_q6_k",
     "pbx_quantize_q8_ref",
     "pbx_synth_normal",
@@ -110,6 +110,7 @@ def load_library():
                                            ctypes.POINTER(ctypes.c_size_t)]),
         "pbx_linear": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
         "pbx_linear_dev": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
+        "pbx_linear_dev_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
         "pbx_dequant": (ctypes.c_int, [_vp, _vp, _vp]),
         "pbx_dequant_dev": (ctypes.c_int, [_vp, _vp, _vp]),
         "pbx_quantize_q8_0": (ctypes.c_int, [_f32p, _i64, _i64, _u8p]),
@@ -356,6 +357,10 @@ class Context:
 
     def linear_dev(self, w, dX, M, dY, dBias=None):
         self._call("pbx_linear_dev", self._p, w.ptr, dX, M, dBias, dY)
+
+    def linear_dev_noalloc(self, w, dX, M, dY, dBias=None):
+        """pbx_linear_dev_noalloc: the same result, no device allocation."""
+        self._call("pbx_linear_dev_noalloc", self._p, w.ptr, dX, M, dBias, dY)
 
     def dequant(self, w):
         shape = (w.K, w.N) if w.type == TYPE_Q8_REF else (w.N, w.K)

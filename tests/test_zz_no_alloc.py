@@ -1,0 +1,64 @@
+"""pbx_linear_dev_noalloc (the entry point that allocates nothing; its GEMM
+workspace is a static device array) against pbx_linear_dev on the same
+inputs: identical outputs, for two calls in a row, the second with a
+smaller input, over the GEMV (M < 4) and MFMA GEMM (split K) paths and the
+f32 path; a shape beyond the workspace limit is refused."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+import purebee_amd as pb
+from tests.conftest import rel_l2, synth_matrix
+
+pytestmark = pytest.mark.gpu
+
+
+def run_both(ctx, w, K, N, M, bias):
+    X = pb.synth_normal(17 * M + K, M * K).reshape(M, K)
+    dx = ctx.alloc(M * K * 4).upload(X)
+    db = ctx.alloc(N * 4).upload(bias) if bias is not None else None
+    dy1, dy2 = ctx.alloc(M * N * 4), ctx.alloc(M * N * 4)
+    ctx.linear_dev(w, dx.ptr, M, dy1.ptr, db.ptr if db else None)
+    ctx.linear_dev_noalloc(w, dx.ptr, M, dy2.ptr, db.ptr if db else None)
+    ctx.sync()
+    y1 = dy1.download(np.float32, M * N).reshape(M, N)
+    y2 = dy2.download(np.float32, M * N).reshape(M, N)
+    for b in (dx, db, dy1, dy2):
+        if b is not None:
+            b.free()
+    return X, y1, y2
+
+
+@pytest.mark.parametrize("t,N,K,Ms", [
+    (pb.TYPE_Q4_0, 2048, 2048, (512, 64)),   # MFMA GEMM, then a smaller split-K GEMM
+    (pb.TYPE_Q4_0, 16384, 2048, (5, 2)),     # skinny GEMM, then the GEMV
+    (pb.TYPE_Q8_0, 576, 1536, (33, 4)),
+    (pb.TYPE_F32, 1024, 512, (100, 8)),      # f32 MFMA with split-K partials
+])
+def test_noalloc_equals_linear_dev(ctx, t, N, K, Ms):
+    print(f"[case] noalloc type={t} N={N} K={K} M={Ms}", flush=True)
+    W = synth_matrix(N + 3 * K + t, N, K)
+    data = W if t == pb.TYPE_F32 else {pb.TYPE_Q4_0: oracle.quantize_q4_0,
+                                       pb.TYPE_Q8_0: oracle.quantize_q8_0}[t](W)
+    w = ctx.upload(t, N, K, data)
+    bias = pb.synth_normal(N + 7, N)
+    for i, M in enumerate(Ms):
+        X, y1, y2 = run_both(ctx, w, K, N, M, bias if i == 0 else None)
+        assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32)), (M, np.abs(y1 - y2).max())
+        m = M - 1
+        ref = (oracle.f32_matvec(X[m], W) if t == pb.TYPE_F32
+               else oracle.matvec(t, X[m], data, N, K)) + (bias if i == 0 else 0)
+        assert rel_l2(y2[m], ref) < 1e-3
+    w.free()
+
+
+def test_noalloc_rejects_shapes_beyond_the_workspace(ctx):
+    print("[case] noalloc workspace limit", flush=True)
+    N, K, M = 256, 8192, 4096   # fp16 activation pair alone: 2 * 4096 * 8192 * 2 B = 128 MiB
+    w = ctx.upload(pb.TYPE_Q4_0, N, K, oracle.quantize_q4_0(synth_matrix(5, N, K)))
+    dx, dy = ctx.alloc(M * K * 4), ctx.alloc(M * N * 4)
+    with pytest.raises(pb.PbxError, match="workspace"):
+        ctx.linear_dev_noalloc(w, dx.ptr, M, dy.ptr)
+    dx.free(), dy.free(), w.free()
