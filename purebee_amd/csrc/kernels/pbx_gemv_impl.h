@@ -750,25 +750,77 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
 }
 
 // ---------------------------------------------------------------------------
-// Integer-limb GEMV for Q4_0 / Q8_0 with K >= 2048 (decode).  The workgroup
-// first turns the (normalised) activation vector into fixed point with one
-// power-of-two scale for the whole vector,
-//   x_q = rint(x * 2^(22 - e)),  2^(e-1) <= max|x| < 2^e,  |x_q| < 2^22,
-// held in LDS as three signed-byte limbs x_q = x2*65536 + x1*256 + x0 (with
-// x0, x1 the sign-extended low bytes) plus the exact per-block sums of x_q.
-// A block-row dot is then 8 (Q4_0: nibble words) or 8 (Q8_0: int8 words)
-// v_dot4_i32_i8 per limb, exact in int32, combined once in fp32 and scaled
-// by the block's d; 2^(e-22) is applied after the reduction.  Rounding x to
-// x_q costs at most 2^-23 of max|x| per element (~1e-6 relative to the
-// output for these vectors), against the ~75 VALU operations per block-row
-// of the float unpack the other kernels use.
+// Integer-limb GEMV for Q4_0 / Q8_0 (and Q6_K heads) with K >= 2048 (decode).
+// The workgroup first turns the activation row(s) into fixed point, one
+// power-of-two scale per 32-element block:
+//   x_q = rint(x * w * 2^(21 - e_b)),  2^(e_b-1) <= max_b |x * w| < 2^e_b,
+// (w: the RMSNorm weights, or 1) held in LDS as three signed-byte limbs
+// x_q = x2*65536 + x1*256 + x0 plus the exact block sums of x_q and the
+// block's 2^(e_b-21).  A block-row dot is then 8 v_dot4_i32_i8 per limb,
+// exact in int32, combined once in fp32 with the block's scale and d.
+// RMSNorm's 1/rms multiplies the finished sums (the dot is linear in x), so
+// only the blocks' own maxima are needed before the limbs can be built.
+// Rounding costs at most 2^-22 of the block's max |x * w| per element, against
+// the ~75 VALU operations per block-row of the float unpack.
+// Q = 1..4 consecutive lanes share a block (8/Q float4s each), so the block
+// reductions are 0..2 DPP steps and no builder waits for another before the
+// one barrier that publishes the limbs.
 // Workgroup: WV waves x RT rows each (PAIR: RT/2 gate + RT/2 up rows); lane
-// l owns blocks l, l+64, ... (IB of them).
+// l owns blocks l, l+64, ... (IB of them) in the dots.
 // ---------------------------------------------------------------------------
 #define PBX_INT_MAXK 8192
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// Sum / max over aligned groups of Q consecutive lanes (Q = 1, 2, 4, 8:
+// partners lane^1, lane^3, lane^7 stay inside the group).
+template <int Q>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (Q >= 2) v += lane_partner<1>(v);
+  if constexpr (Q >= 4) v += lane_partner<2>(v);
+  if constexpr (Q >= 8) v += lane_partner<4>(v);
+  return v;
+}
+template <int Q>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (Q >= 2) v = fmaxf(v, lane_partner<1>(v));
+  if constexpr (Q >= 4) v = fmaxf(v, lane_partner<2>(v));
+  if constexpr (Q >= 8) v = fmaxf(v, lane_partner<4>(v));
+  return v;
+}
+template <int Q>
+__device__ __forceinline__ int group_isum(int v) {
+  if constexpr (Q >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  if constexpr (Q >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x1B, 0xF, 0xF, false);
+  if constexpr (Q >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+  return v;
+}
+
+// Fixed point of four products p (|p * scale| < 2^21): the float
+// p * scale + 1.5 * 2^23 + 0x8080 holds rint(p * scale) + 0x8080 in its low
+// 22 bits, so its bytes 0 and 1 are x0 + 128 and x1 + 128 and byte 2 is
+// x2 + 64 (x_q = x0 + 256 x1 + 65536 x2, t = x_q + 0x8080 split by bytes).
+// Out: the three limb words of the four elements (element i in byte i) and
+// the sum of their x_q.
+__device__ __forceinline__ void limb_words(float4 p, float scale, int &w0, int &w1, int &w2,
+                                           int &sum) {
+  constexpr float MAGIC = 12615808.0f;  // 1.5 * 2^23 + 0x8080
+  const unsigned a = __float_as_uint(fmaf(p.x, scale, MAGIC));
+  const unsigned b = __float_as_uint(fmaf(p.y, scale, MAGIC));
+  const unsigned c = __float_as_uint(fmaf(p.z, scale, MAGIC));
+  const unsigned d = __float_as_uint(fmaf(p.w, scale, MAGIC));
+  // bits = 0x4B408080 + x_q
+  sum = (int)(a + b + c + d - 4u * 0x4B408080u);
+  const unsigned ab01 = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+  const unsigned cd01 = __builtin_amdgcn_perm(d, c, 0x05010400u);  // c0 d0 c1 d1
+  const unsigned ab2 = __builtin_amdgcn_perm(b, a, 0x07030602u);   // a2 b2 . .
+  const unsigned cd2 = __builtin_amdgcn_perm(d, c, 0x07030602u);   // c2 d2 . .
+  w0 = (int)(__builtin_amdgcn_perm(cd01, ab01, 0x05040100u) ^ 0x80808080u);
+  w1 = (int)(__builtin_amdgcn_perm(cd01, ab01, 0x07060302u) ^ 0x80808080u);
+  // bytes x2 + 64 in [0x20, 0x60]: + 0x40 (no carries) then ^ 0x80 is x2 mod 256
+  w2 = (int)((__builtin_amdgcn_perm(cd2, ab2, 0x05040100u) + 0x40404040u) ^ 0x80808080u);
 }
 
 // LOOP (lm heads, tall matrices): a workgroup takes tiles blockIdx.x,
@@ -777,28 +829,38 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) {
 // writes one key per workgroup, EPI_STORE stores without a bias.
 // MR > 1: MR activation rows (the first a.rows of them valid; row stride K
 // in, N out) against one pass over the weight bytes -- the speculative
-// verify and short prompts.  The prologue's (row, 64-block group) slots are
-// spread over the waves.  MR = 1: activation row blockIdx.y (the plain
+// verify and short prompts.  MR = 1: activation row blockIdx.y (the plain
 // instruction's M < 4 rows).
 template <int TYPE, int WV, int RT, int IB, int PRO, int EPI, bool LOOP = false, int MR = 1>
 __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   static_assert(TYPE == PBX_Q4 || TYPE == PBX_Q8 || is_q6k<TYPE>(), "quantised weights only");
-  static_assert(MR > 1 || IB <= WV, "one prologue wave per 64 blocks");
   static_assert(!LOOP || EPI == EPI_ARGMAX || EPI == EPI_STORE, "tile loop epilogues");
   static_assert(MR == 1 || EPI != EPI_ARGMAX, "argmax keys for one row");
   constexpr int QB = BlockTraits<TYPE>::QB;
   constexpr int NV = QB / 16;
   constexpr bool PAIR = EPI == EPI_SWIGLU;
   static_assert(IB * 64 * 32 <= PBX_INT_MAXK, "K limit");
-  constexpr int PP = MR * IB;             // prologue slots: (row, 64-block group)
-  constexpr int PS = (PP + WV - 1) / WV;  // slots a wave
+  constexpr int T = WV * 64;
+  constexpr int NB = MR * IB * 64;  // activation blocks (past B: unused)
+  // lanes per block in the build, float4s a builder lane covers, and the
+  // blocks a lane builds one after another (Q = 1 only).  With more than
+  // four waves the blocks are not split: only wave 0 builds (MR = 1), its
+  // activations requested first, while the others stream weight bytes.
+  constexpr int TB = T <= 256 ? T : 64;
+  constexpr int Q = TB >= 8 * NB ? 8 : TB >= 4 * NB ? 4 : TB >= 2 * NB ? 2 : 1;
+  constexpr int FPL = 8 / Q;
+  constexpr int IT = (NB * Q + T - 1) / T;
   // limb words 4q..4q+3 of block b at limb[m][L][q][b]: lane l's 16-byte
   // reads of block l are contiguous across the wave (no bank conflicts)
   __shared__ int4 limb[MR][3][2][IB * 64];
   // exact sums of a block's x_q ([0]; Q6_K: its two 16-element halves)
   __shared__ int bsum[MR][2][IB * 64];
-  __shared__ float red[3][MR][IB];
-  __shared__ float xscale[MR];
+  // the block's 2^(e_b - 21) (NaN: the block holds a non-finite x * w)
+  __shared__ float bscale[MR][IB * 64];
+  // RMSNorm: sums of x^2 of each 16-lane row of the builder waves, SSP per
+  // activation row (a builder wave covers 64 / Q blocks of one row)
+  constexpr int SSP = IB * Q * 4;
+  __shared__ float4 ssq[PRO == PRO_RMSNORM ? MR : 1][SSP / 4];
   __shared__ uint64_t kred[WV];
 
   const int N = a.N, B = a.B, K = B * 32;
@@ -821,29 +883,31 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   const float *X = a.X + (size_t)blockIdx.y * MR * K;
   float *y = a.Y + (size_t)blockIdx.y * MR * NO;
 
-  // 1. Prologue slots (slot p = wave + WV*s: activation row p / IB, blocks
-  //    64*(p % IB) + lane) request their activation blocks and RMSNorm
+  // 1. Builder segments (segment s = L + T * it: block s / Q of the rows,
+  //    its float4s FPL*(s % Q) ..) request their activations and RMSNorm
   //    weights before any wave requests weight bytes: a CU returns loads in
   //    issue order, so activations requested behind the weight stream would
-  //    arrive only with it.  Rows past `rows` read row 0 and are not stored.
-  float4 xv[PS][8], nv[PS][8];
+  //    arrive only with it.  Loads are unconditional from clamped addresses.
+  float4 xv[IT][FPL], nv[IT][FPL];
+  // whole waves hold segments or none (NB * Q is a multiple of 64); the
+  // others skip the build: waiting for loads they do not need would hold
+  // the barrier behind their weight bytes
+  auto builds = [&](int it) -> bool { return wave * 64 + T * it < NB * Q; };
 #pragma unroll
-  for (int sl = 0; sl < PS; ++sl) {
-    const int p = wave + WV * sl;
-    if (p < PP) {
-      const int pm = p / IB, pb = (p % IB) * 64 + lane;
-      const int bl = pb < B ? pb : 0;
-      const float *xr = X + (size_t)(pm < rows ? pm : 0) * K;
+  for (int it = 0; it < IT; ++it) {
+    if (!builds(it)) continue;
+    const int sg = tid + T * it;
+    const int gb = sg / Q, m = gb / (IB * 64), b = gb % (IB * 64), qd = sg % Q;
+    const bool ok = b < B && m < rows;
+    const float *xr = X + (ok ? (size_t)m * K + (size_t)b * 32 + qd * FPL * 4 : 0);
+    const float *wr = a.normw + (ok ? (size_t)b * 32 + qd * FPL * 4 : 0);
 #pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        xv[sl][v] = *reinterpret_cast<const float4 *>(xr + (size_t)bl * 32 + 4 * v);
-        nv[sl][v] = make_float4(1.f, 1.f, 1.f, 1.f);
-        if constexpr (PRO == PRO_RMSNORM)
-          nv[sl][v] = *reinterpret_cast<const float4 *>(a.normw + (size_t)bl * 32 + 4 * v);
-      }
+    for (int v = 0; v < FPL; ++v) {
+      xv[it][v] = *reinterpret_cast<const float4 *>(xr + 4 * v);
+      nv[it][v] = make_float4(1.f, 1.f, 1.f, 1.f);
+      if constexpr (PRO == PRO_RMSNORM) nv[it][v] = *reinterpret_cast<const float4 *>(wr + 4 * v);
     }
   }
-  lds_barrier();
 
   // 2. Every wave: the residuals it will add (EPI_ADD), the block scales,
   //    then the weight bytes.  Loads are unconditional from clamped
@@ -905,113 +969,101 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   if constexpr (LOOP) load_tile(blockIdx.x + (TW > 1 ? G : 0), dbB, qB, exB);
   __builtin_amdgcn_sched_barrier(0);
 
-  // 3. Prologue slots: sum of squares (RMSNorm) and max |x * w| of their
-  //    blocks, combined across a row's IB slots through LDS.  nf is the sum
-  //    of (x * w) * 0 over the blocks: NaN exactly when an element of x * w
-  //    is infinite or NaN (which fmaxf would drop), else 0.
-  float ss[PS], mw[PS], nf[PS];
+  // 3. Build: each segment's products x * w, their block's max |x * w| and
+  //    exponent (over the Q lanes of the block), the fixed point as limb
+  //    words, the block sums; then one barrier publishes them.  nf = sum of
+  //    (x * w) * 0 is NaN exactly when a product is infinite or NaN (which
+  //    fmaxf would drop); it makes the block's scale NaN, so every output
+  //    of the row becomes NaN (the reference's sums are then NaN or +-inf).
 #pragma unroll
-  for (int sl = 0; sl < PS; ++sl) {
-    ss[sl] = 0.f;
-    mw[sl] = 0.f;
-    nf[sl] = 0.f;
-    const int p = wave + WV * sl;
-    if (p < PP) {
-      const bool pvalid = (p % IB) * 64 + lane < B;
+  for (int it = 0; it < IT; ++it) {
+    if (!builds(it)) continue;
+    const int sg = tid + T * it;
+    const int gb = sg / Q, m = gb / (IB * 64), b = gb % (IB * 64), qd = sg % Q;
+    const bool ok = b < B && m < rows;
+    float4 p[FPL];
+    float mx = 0.f, nf = 0.f, sq = 0.f;
 #pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        const float4 t = pvalid ? xv[sl][v] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[sl][v];
-        if constexpr (PRO == PRO_RMSNORM)
-          ss[sl] = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, ss[sl]))));
-        const float px = t.x * w.x, py = t.y * w.y, pz = t.z * w.z, pw = t.w * w.w;
-        mw[sl] = fmaxf(mw[sl], fmaxf(fmaxf(fabsf(px), fabsf(py)), fmaxf(fabsf(pz), fabsf(pw))));
-        nf[sl] = fmaf(px, 0.f, fmaf(py, 0.f, fmaf(pz, 0.f, fmaf(pw, 0.f, nf[sl]))));
-      }
-      if constexpr (PRO == PRO_RMSNORM) ss[sl] = wave_sum(ss[sl]);
-      mw[sl] = wave_max(mw[sl]);
-      nf[sl] = wave_sum(nf[sl]);
+    for (int v = 0; v < FPL; ++v) {
+      const float4 t = ok ? xv[it][v] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[it][v];
+      if constexpr (PRO == PRO_RMSNORM)
+        sq = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, sq))));
+      p[v] = make_float4(t.x * w.x, t.y * w.y, t.z * w.z, t.w * w.w);
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(p[v].x), fabsf(p[v].y)), fmaxf(fabsf(p[v].z), fabsf(p[v].w))));
+      nf = fmaf(p[v].x, 0.f, fmaf(p[v].y, 0.f, fmaf(p[v].z, 0.f, fmaf(p[v].w, 0.f, nf))));
     }
-  }
-  if constexpr (IB > 1) {
-#pragma unroll
-    for (int sl = 0; sl < PS; ++sl) {
-      const int p = wave + WV * sl;
-      if (p < PP && lane == 0) {
-        red[0][p / IB][p % IB] = ss[sl];
-        red[1][p / IB][p % IB] = mw[sl];
-        red[2][p / IB][p % IB] = nf[sl];
+    if constexpr (Q > 1) {
+      mx = group_max<Q>(mx);
+      nf = group_sum<Q>(nf);
+    }
+    if constexpr (PRO == PRO_RMSNORM) {
+      // sum over the 16-lane row (DPP only); lane 16r of the wave writes it
+      sq = wave_sum<8>(ok ? sq : 0.f);
+      if ((lane & 15) == 0) {
+        const int chunk = (wave * 64 + T * it) / Q - m * IB * 64;  // first block of the wave
+        reinterpret_cast<float *>(&ssq[m][0])[chunk * Q / 64 * 4 + (lane >> 4)] = sq;
       }
     }
-    lds_barrier();
+    int e = 0;
+    if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
+    e = max(e, -100);  // the scale stays finite; such blocks round to 0
+    const float scale = ldexpf(1.f, 21 - e);
+    int wl[3][FPL], slo = 0, shi = 0;
 #pragma unroll
-    for (int sl = 0; sl < PS; ++sl) {
-      const int p = wave + WV * sl;
-      if (p < PP) {
-        ss[sl] = 0.f;
-        mw[sl] = 0.f;
-        nf[sl] = 0.f;
-#pragma unroll
-        for (int w = 0; w < IB; ++w) {
-          ss[sl] += red[0][p / IB][w];
-          mw[sl] = fmaxf(mw[sl], red[1][p / IB][w]);
-          nf[sl] += red[2][p / IB][w];
-        }
-      }
+    for (int v = 0; v < FPL; ++v) {
+      int sv;
+      limb_words(p[v], scale, wl[0][v], wl[1][v], wl[2][v], sv);
+      // float4 qd*FPL + v of the block: elements 0..15 are float4s 0..3
+      if (qd * FPL + v < 4) slo += sv; else shi += sv;
     }
-  }
-  // 4. Prologue slots: fixed point x_q = rint(x * w * inv * 2^(22 - e)) of
-  //    their blocks as three byte limbs plus the block sums, into LDS.
+    if constexpr (Q > 1) {
+      slo = group_isum<Q>(slo);
+      shi = group_isum<Q>(shi);
+    }
+    if (ok) {
 #pragma unroll
-  for (int sl = 0; sl < PS; ++sl) {
-    const int p = wave + WV * sl;
-    if (p < PP) {
-      const int pm = p / IB, pb = (p % IB) * 64 + lane;
-      const float inv = PRO == PRO_RMSNORM ? 1.0f / sqrtf(ss[sl] / (float)K + a.eps) : 1.f;
-      int e = 0;
-      const float mx = mw[sl] * inv;
-      if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
-      const float c = inv * ldexpf(1.f, 22 - e);
-      if (pb < B) {
-        int bs = 0, bs_lo = 0;  // block sum; sum of elements 0..15
-        int lw[3][8];
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          const float4 t = xv[sl][v], w = nv[sl][v];
-          const int xq[4] = {(int)rintf(t.x * w.x * c), (int)rintf(t.y * w.y * c),
-                             (int)rintf(t.z * w.z * c), (int)rintf(t.w * w.w * c)};
-          unsigned l0 = 0, l1 = 0, l2 = 0;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int x0 = (int)(int8_t)(xq[k] & 0xFF);
-            const int r1 = (xq[k] - x0) >> 8;
-            const int x1 = (int)(int8_t)(r1 & 0xFF);
-            const int x2 = (r1 - x1) >> 8;
-            l0 |= (unsigned)(x0 & 0xFF) << (8 * k);
-            l1 |= (unsigned)(x1 & 0xFF) << (8 * k);
-            l2 |= (unsigned)(x2 & 0xFF) << (8 * k);
-            bs += xq[k];
-          }
-          lw[0][v] = (int)l0;
-          lw[1][v] = (int)l1;
-          lw[2][v] = (int)l2;
-          if (v == 3) bs_lo = bs;
+      for (int L = 0; L < 3; ++L) {
+        const int f0 = qd * FPL;  // first word; words 4.. sit in the q = 1 plane
+        if constexpr (FPL == 1) {
+          reinterpret_cast<int *>(&limb[m][L][f0 >> 2][b])[f0 & 3] = wl[L][0];
+        } else if constexpr (FPL == 2) {
+          reinterpret_cast<int2 *>(&limb[m][L][f0 >> 2][b])[(f0 & 3) >> 1] =
+              make_int2(wl[L][0], wl[L][1]);
+        } else if constexpr (FPL == 4) {
+          limb[m][L][f0 >> 2][b] = make_int4(wl[L][0], wl[L][1], wl[L][2], wl[L][3]);
+        } else {
+          limb[m][L][0][b] = make_int4(wl[L][0], wl[L][1], wl[L][2], wl[L][3]);
+          limb[m][L][1][b] = make_int4(wl[L][4], wl[L][5], wl[L][6], wl[L][7]);
         }
-#pragma unroll
-        for (int L = 0; L < 3; ++L) {
-          limb[pm][L][0][pb] = make_int4(lw[L][0], lw[L][1], lw[L][2], lw[L][3]);
-          limb[pm][L][1][pb] = make_int4(lw[L][4], lw[L][5], lw[L][6], lw[L][7]);
-        }
-        bsum[pm][0][pb] = is_q6k<TYPE>() ? bs_lo : bs;
-        bsum[pm][1][pb] = bs - bs_lo;
       }
-      // a non-finite activation makes every output of the row NaN (the
-      // reference's sums are then NaN or +-inf; fixed point cannot hold them)
-      if (p % IB == 0 && lane == 0) xscale[pm] = ldexpf(1.f, e - 22) + nf[sl];
+      if (qd == 0) {
+        bsum[m][0][b] = is_q6k<TYPE>() ? slo : slo + shi;
+        bsum[m][1][b] = shi;
+        bscale[m][b] = ldexpf(1.f, e - 21) + nf;
+      }
     }
   }
   lds_barrier();
+  // RMSNorm's 1/rms of each activation row from the builders' row sums
+  // (broadcast LDS reads, while the weight bytes are still arriving); it
+  // multiplies the blocks' scales, so the dots need it and no wave
+  // computes it at its tail
+  float inv[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    inv[m] = 1.f;
+    if constexpr (PRO == PRO_RMSNORM) {
+      float sm = 0.f;
+#pragma unroll
+      for (int c = 0; c < SSP / 4; ++c) {
+        const float4 v = ssq[m][c];
+        sm += (v.x + v.y) + (v.z + v.w);
+      }
+      inv[m] = 1.0f / sqrtf(sm / (float)K + a.eps);
+    }
+  }
 
-  // 5. Dot products as the weight rows arrive; each row's sum after the
+  // 4. Dot products as the weight rows arrive; each row's sum after the
   //    transposed reduction, per activation row.
   auto dots = [&](const unsigned (&db)[RT][IB], const uint4 (&qq)[RT][IB][NV],
                   const unsigned (&ex)[RT][IB], float (&tot)[MR]) {
@@ -1023,8 +1075,9 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
 #pragma unroll
     for (int j = 0; j < IB; ++j) {
       const int b = lane + 64 * j;
-      const int bl = b < B ? b : 0;  // lanes past B: zero scales cancel them
-      const unsigned bmask = b < B ? 0xFFFFu : 0u;
+      const bool bok = b < B;
+      const int bl = bok ? b : 0;  // lanes past B: zero scales cancel them
+      const unsigned bmask = bok ? 0xFFFFu : 0u;
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
         if (MR > 1 && m >= rows) break;  // uniform: rows past the batch
@@ -1036,7 +1089,10 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
           xl[L][0] = t0.x; xl[L][1] = t0.y; xl[L][2] = t0.z; xl[L][3] = t0.w;
           xl[L][4] = t1.x; xl[L][5] = t1.y; xl[L][6] = t1.z; xl[L][7] = t1.w;
         }
-        const float corr = TYPE == PBX_Q4 ? 8.f * (float)bsum[m][0][bl] : 0.f;
+        // the block's scale (times 1/rms) folded into the limb weights
+        const float c0 = bok ? bscale[m][bl] * inv[m] : 0.f;
+        const float C1 = 256.f * c0, C2 = 65536.f * c0;
+        const float corr = TYPE == PBX_Q4 ? 8.f * (float)bsum[m][0][bl] * c0 : 0.f;
 #pragma unroll
         for (int i = 0; i < RT; ++i) {
           int s0 = 0, s1 = 0, s2 = 0;
@@ -1085,10 +1141,10 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
                 h0 = sdot4(c, xl[0][k], h0); h1 = sdot4(c, xl[1][k], h1); h2 = sdot4(c, xl[2][k], h2);
               }
             }
-            const float flo = fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0)) -
-                              32.f * (float)bsum[m][0][bl];
-            const float fhi = fmaf((float)h2, 65536.f, fmaf((float)h1, 256.f, (float)h0)) -
-                              32.f * (float)bsum[m][1][bl];
+            const float flo = fmaf((float)s2, C2, fmaf((float)s1, C1, fmaf((float)s0, c0,
+                              -32.f * (float)bsum[m][0][bl] * c0)));
+            const float fhi = fmaf((float)h2, C2, fmaf((float)h1, C1, fmaf((float)h0, c0,
+                              -32.f * (float)bsum[m][1][bl] * c0)));
             const float sc0 = (float)(int8_t)(ex[i][j] & 0xFFu);
             const float sc1 = (float)(int8_t)((ex[i][j] >> 8) & 0xFFu);
             acc[m][i] = fmaf(fmaf(sc0, flo, sc1 * fhi), f16_bits_to_f32(db[i][j] & bmask),
@@ -1104,13 +1160,13 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
               s2 = sdot4((int)w[k], xl[2][k], s2);
             }
           }
-          const float f = fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0)) - corr;
+          const float f = fmaf((float)s2, C2, fmaf((float)s1, C1, fmaf((float)s0, c0, -corr)));
           acc[m][i] = fmaf(f, f16_bits_to_f32(db[i][j] & bmask), acc[m][i]);
         }
       }
     }
 #pragma unroll
-    for (int m = 0; m < MR; ++m) tot[m] = wave_transpose_reduce<RT>(acc[m], lane) * xscale[m];
+    for (int m = 0; m < MR; ++m) tot[m] = wave_transpose_reduce<RT>(acc[m], lane);
   };
   const int row = lane / LPR;
 
@@ -1119,14 +1175,14 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     // tile two on as soon as it has been reduced.  The steady-state loop
     // issues its loads unconditionally; the last two or three tiles follow.
     uint64_t best = 0;
-    auto consume = [&](int k, const float (&tot)[MR]) {
+    auto consume = [&](int k, const float (&tt)[MR]) {
       const int n = rbase(blockIdx.x + k * G) + row;
       if ((lane % LPR) == 0 && n < N) {
 #pragma unroll
         for (int m = 0; m < MR; ++m)  // no bias in the loop (a load here would wait)
-          if (m < rows) y[(size_t)m * NO + n] = tot[m];
+          if (m < rows) y[(size_t)m * NO + n] = tt[m];
         if constexpr (EPI == EPI_ARGMAX) {
-          const uint64_t key = argmax_key(tot[0], (unsigned)n);
+          const uint64_t key = argmax_key(tt[0], (unsigned)n);
           best = key > best ? key : best;
         }
       }
