@@ -359,169 +359,166 @@ extern "C" __global__ void __launch_bounds__(256) pbx_attention_decode(AttnArgs 
 // ---------------------------------------------------------------------------
 // Flash decoding in one workgroup per query head (head_dim <= 64): the
 // attention of llama.js:258-301 / llama-streaming.js:543-573 at batch 1.
-// A chunk is 512 positions; wave w takes positions 64w..64w+63 of it.  Each
-// wave keeps its own running max, sum and weighted V sum over its
-// positions (online softmax), and the eight waves merge once through LDS
-// at the end, so no second kernel and no barrier inside the position loop.
-// Lane l holds dims 4(l%16)..4(l%16)+3 of everything: of q, the new k and
-// v (which it rotates itself, llama.js:163-190, from the RoPE pairs of
-// those dims), and of the wave's positions 4j + l/16 (j < 16) of K and V,
-// so every 16-byte load reads four whole 256-byte cache rows.  The partial
-// dots over 4 dims are finished by a 16-lane reduce-scatter, after which
-// lane l holds the score of position 4(l%16) + l/16.  The row at pos is
-// replaced by the new k / v from registers (the cache row may still hold
-// an older value); the group's first head writes them to the cache.
-// All loads are unconditional, from clamped addresses: q, k, v first.
+// The positions read from the cache go in chunks of up to 512; a chunk of
+// 32J positions (J = 1..16, as many as the context needs) gives every one
+// of the eight waves 4J consecutive positions, so all waves carry the same
+// short dependency chain whatever the context length.  Lane l holds dims
+// 4(l%16)..4(l%16)+3 of q (which it rotates itself, llama.js:163-190) and
+// of its row's positions base + 4j + l/16 of K and V, so each 16-byte load
+// reads four whole 256-byte cache rows.  A position's dot is summed over
+// the 16 lanes of its row by DPP, which leaves it in all 16 lanes: the row
+// then runs its own online softmax (running max m, sum l and weighted V
+// sum) with no cross-lane traffic at all.  Scores are kept in base-2 units
+// (q is pre-scaled by scale * log2 e, so every exponential is one v_exp).
+// The 32 row states and the new position (q . rotated new k, weight 1,
+// value v) merge once through LDS, in one wave: lane i rescales state i by
+// 2^(m_i - M) and every lane then sums its output dim over the states.
+// The new position never comes from the cache: the group's first head
+// appends k and v at pos after everything has been read, so no workgroup
+// depends on another's write.
 // ---------------------------------------------------------------------------
 #define PBX_HA_MAX_HD 64
 #define PBX_HA_WAVES 8
+#define PBX_HA_STATES (PBX_HA_WAVES * 4 + 1)  // row states + the new position
 
-// Lane l of wave w holds dims 4(l%16)..4(l%16)+3 of the wave's positions
-// 4j + l/16, j = 0..15, of K and of V: each load instruction reads four
-// whole 256-byte rows.
-struct HeadChunk {
-  float4 k[16];
-  float4 v[16];
-};
+// One chunk for the calling wave: positions base + 4j + ps (j < J) of the
+// nc cached positions (loads clamped to the last one, scores past it masked
+// to -inf), folded into the row's running (m, l, acc).
+template <int J>
+__device__ __forceinline__ void head_chunk(const float *kb, const float *vb, int kvdim, int dcol,
+                                           int base, int nc, int ps, const float4 qq, float &m,
+                                           float &l, float4 &acc) {
+  float4 k[J], v[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    k[j] = *reinterpret_cast<const float4 *>(kb + (size_t)min(base + 4 * j + ps, nc - 1) * kvdim + dcol);
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    v[j] = *reinterpret_cast<const float4 *>(vb + (size_t)min(base + 4 * j + ps, nc - 1) * kvdim + dcol);
+  float s[J];
+  float mc = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const float d = wave_sum<8>(fmaf(qq.x, k[j].x, fmaf(qq.y, k[j].y, fmaf(qq.z, k[j].z, qq.w * k[j].w))));
+    s[j] = base + 4 * j + ps < nc ? d : -INFINITY;
+    mc = fmaxf(mc, s[j]);
+  }
+  const float mn = fmaxf(m, mc);
+  const float ms = mn == -INFINITY ? 0.f : mn;  // a row with no position yet
+  const float f = __builtin_amdgcn_exp2f(m - ms);
+  float ls = 0.f;
+  float4 a = make_float4(acc.x * f, acc.y * f, acc.z * f, acc.w * f);
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const float p = __builtin_amdgcn_exp2f(s[j] - ms);
+    ls += p;
+    a.x = fmaf(p, v[j].x, a.x);
+    a.y = fmaf(p, v[j].y, a.y);
+    a.z = fmaf(p, v[j].z, a.z);
+    a.w = fmaf(p, v[j].w, a.w);
+  }
+  l = fmaf(l, f, ls);
+  acc = a;
+  m = mn;
+}
 
 // ROWS: one row of a batch whose q is already rotated and whose k, v are
 // already in the cache at every position up to pos (pbx_rope_append_rows):
-// no RoPE, no new-row substitution and no append; a.qkv and a.out point at
-// the row, the position comes from the caller.
+// every position comes from the cache, no RoPE, no new-position state and
+// no append; a.qkv and a.out point at the row, the position comes from the
+// caller.
 template <bool ROWS>
 __device__ __forceinline__ void attention_head_body(const AttnArgs &a, const int pos) {
-  __shared__ float wm[PBX_HA_WAVES], wl[PBX_HA_WAVES];
-  __shared__ __attribute__((aligned(16))) float wacc[PBX_HA_WAVES][PBX_HA_MAX_HD];
-  constexpr int CH = PBX_HA_WAVES * 64;  // positions per chunk
+  __shared__ float st_m[PBX_HA_STATES], st_l[PBX_HA_STATES], st_e[PBX_HA_STATES];
+  __shared__ __attribute__((aligned(16))) float st_acc[PBX_HA_STATES][PBX_HA_MAX_HD];
   const int h = blockIdx.x, hd = a.head_dim, hd4 = hd / 4;
   const int Gq = a.n_heads / a.n_kv_heads, g = h / Gq;
   const int dim = a.n_heads * hd, kvdim = a.n_kv_heads * hd;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int L = pos + 1;
-  float *kb = a.kcache + (size_t)g * hd, *vb = a.vcache + (size_t)g * hd;
-  const int dg = lane & 15, ps = lane >> 4;  // dim group, position slot
+  const int dg = lane & 15, ps = lane >> 4;  // dim group, row (position slot)
   const int dcol = 4 * min(dg, hd4 - 1);     // clamped for head_dim < 64
+  float *kb = a.kcache + (size_t)g * hd, *vb = a.vcache + (size_t)g * hd;
+  const int nc = ROWS ? pos + 1 : pos;  // positions read from the cache
 
-  // 1. K and V of the first chunk (all of K before V: the scores need all
-  //    of K while V is still arriving).  A wave whose positions all lie
-  //    past pos loads and scores nothing (a wave-uniform branch); its
-  //    clamped loads would cost the CU's load return path as much as real
-  //    ones.  These go before the q loads: behind a branch, a later use of
-  //    an earlier load waits for everything the branch may have issued.
-  auto load_chunk = [&](int c0, HeadChunk &ch) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      ch.k[j] = *reinterpret_cast<const float4 *>(
-          kb + (size_t)min(c0 + w * 64 + 4 * j + ps, pos) * kvdim + dcol);
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      ch.v[j] = *reinterpret_cast<const float4 *>(
-          vb + (size_t)min(c0 + w * 64 + 4 * j + ps, pos) * kvdim + dcol);
-  };
-  const bool wact = w * 64 < L;
-  HeadChunk first;
-  if (wact) load_chunk(0, first);
-
-  // 2. the lane's dims of q, the new k and v, and their RoPE pairs
+  // the lane's dims of q, the new k and v, and their RoPE pairs
   const float4 cs = ROWS ? make_float4(1.f, 0.f, 1.f, 0.f)
-                        : *reinterpret_cast<const float4 *>(a.rope + (size_t)pos * hd + dcol);
+                         : *reinterpret_cast<const float4 *>(a.rope + (size_t)pos * hd + dcol);
   const float4 qv = *reinterpret_cast<const float4 *>(a.qkv + (size_t)h * hd + dcol);
   const float4 kv = ROWS ? make_float4(0.f, 0.f, 0.f, 0.f)
                          : *reinterpret_cast<const float4 *>(a.qkv + dim + (size_t)g * hd + dcol);
   const float4 vnw = ROWS ? make_float4(0.f, 0.f, 0.f, 0.f)
                           : *reinterpret_cast<const float4 *>(a.qkv + dim + kvdim + (size_t)g * hd + dcol);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 3. RoPE (adjacent pairs, llama.js:163-190) of the lane's q and new-k
-  //    dims; q . (new k) summed over the 16 lanes of a row
+  const float c = a.scale * 1.44269504088896340736f;  // scale * log2 e
   float4 qq = ROWS ? qv
                    : make_float4(qv.x * cs.x - qv.y * cs.y, qv.x * cs.y + qv.y * cs.x,
                                  qv.z * cs.z - qv.w * cs.w, qv.z * cs.w + qv.w * cs.z);
-  const float4 knw = make_float4(kv.x * cs.x - kv.y * cs.y, kv.x * cs.y + kv.y * cs.x,
-                                 kv.z * cs.z - kv.w * cs.w, kv.z * cs.w + kv.w * cs.z);
   if (dg >= hd4) qq = make_float4(0.f, 0.f, 0.f, 0.f);  // repeats of the last dims
-  const float dnew = wave_sum<8>(fmaf(qq.x, knw.x, fmaf(qq.y, knw.y, fmaf(qq.z, knw.z, qq.w * knw.w))));
+  qq = make_float4(qq.x * c, qq.y * c, qq.z * c, qq.w * c);
 
-  // 4. scores and the wave's softmax-weighted V sum, chunk by chunk (the
-  //    first chunk from the registers loaded above; later ones, for
-  //    contexts past 512 positions, load their own)
   float m = -INFINITY, l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  auto chunk = [&](int c0, const HeadChunk &ch) {
-    // partial dots of the 16 positions, then a reduce-scatter over the 16
-    // lanes of a position slot: after halving across lane bits 3, 2, 1, 0
-    // lane l holds the whole dot of position 4(l%16) + l/16
-    float s[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      s[j] = fmaf(qq.x, ch.k[j].x, fmaf(qq.y, ch.k[j].y, fmaf(qq.z, ch.k[j].z, qq.w * ch.k[j].w)));
-    transpose_stage<16, 8, 16>(s, lane);
-    const int p = c0 + w * 64 + 4 * dg + ps;
-    const bool valid = p < L, cur = !ROWS && p == pos;
-    const float dot = cur ? dnew : s[0];  // position pos: the new k
-    const float sc = valid ? dot * a.scale : -INFINITY;
-    const float mn = fmaxf(m, wave_max(sc));
-    const float f = m == -INFINITY ? 0.f : expf(m - mn);  // nothing accumulated yet
-    const float pr = valid ? expf(sc - mn) : 0.f;
-    l = fmaf(l, f, wave_sum(pr));
-    acc.x *= f; acc.y *= f; acc.z *= f; acc.w *= f;
-    const int pw = c0 + w * 64;  // the wave's first position
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int slot = 4 * j + ps;
-      const float pj = __shfl(pr, (lane & 48) | j, 64);  // slot 4j + ps
-      const float4 vj = !ROWS && pw + slot == pos ? vnw : ch.v[j];
-      acc.x = fmaf(pj, vj.x, acc.x);
-      acc.y = fmaf(pj, vj.y, acc.y);
-      acc.z = fmaf(pj, vj.z, acc.z);
-      acc.w = fmaf(pj, vj.w, acc.w);
+  for (int c0 = 0; c0 < nc; c0 += PBX_HA_WAVES * 64) {
+    const int J = min(16, (nc - c0 + 4 * PBX_HA_WAVES - 1) / (4 * PBX_HA_WAVES));
+    const int base = c0 + 4 * w * J;
+    if (base >= nc) continue;  // wave-uniform: nothing of this wave's
+    switch (J) {
+#define PBX_HEAD_CHUNK(n) \
+  case n: head_chunk<n>(kb, vb, kvdim, dcol, base, nc, ps, qq, m, l, acc); break;
+      PBX_HEAD_CHUNK(1) PBX_HEAD_CHUNK(2) PBX_HEAD_CHUNK(3) PBX_HEAD_CHUNK(4)
+      PBX_HEAD_CHUNK(5) PBX_HEAD_CHUNK(6) PBX_HEAD_CHUNK(7) PBX_HEAD_CHUNK(8)
+      PBX_HEAD_CHUNK(9) PBX_HEAD_CHUNK(10) PBX_HEAD_CHUNK(11) PBX_HEAD_CHUNK(12)
+      PBX_HEAD_CHUNK(13) PBX_HEAD_CHUNK(14) PBX_HEAD_CHUNK(15) PBX_HEAD_CHUNK(16)
+#undef PBX_HEAD_CHUNK
+      default: break;
     }
-    m = mn;
-  };
-  if (wact) chunk(0, first);
-  for (int c0 = CH; c0 < L; c0 += CH) {
-    if (c0 + w * 64 >= L) break;  // wave-uniform
-    HeadChunk next;
-    load_chunk(c0, next);
-    chunk(c0, next);
-  }
-  // the four position slots of each dim group
-#pragma unroll
-  for (int off = 16; off <= 32; off <<= 1) {
-    acc.x += __shfl_xor(acc.x, off, 64);
-    acc.y += __shfl_xor(acc.y, off, 64);
-    acc.z += __shfl_xor(acc.z, off, 64);
-    acc.w += __shfl_xor(acc.w, off, 64);
   }
 
-  // 5. merge the waves
-  if (lane == 0) {
-    wm[w] = m;
-    wl[w] = l;
+  // state 4w + ps: the row's; state 32: the new position
+  const int si = 4 * w + ps;
+  if (dg == 0) {
+    st_m[si] = m;
+    st_l[si] = l;
   }
-  if (lane < hd4) *reinterpret_cast<float4 *>(&wacc[w][4 * lane]) = acc;
-  lds_barrier();
-  if (tid < hd) {
-    float M = wm[0];
-#pragma unroll
-    for (int i = 1; i < PBX_HA_WAVES; ++i) M = fmaxf(M, wm[i]);
-    float num = 0.f, den = 0.f;
-#pragma unroll
-    for (int i = 0; i < PBX_HA_WAVES; ++i) {
-      const float e = wm[i] == -INFINITY ? 0.f : expf(wm[i] - M);
-      num = fmaf(e, wacc[i][tid], num);
-      den = fmaf(e, wl[i], den);
+  *reinterpret_cast<float4 *>(&st_acc[si][4 * dg]) = acc;
+  float4 knw = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (!ROWS) {
+    knw = make_float4(kv.x * cs.x - kv.y * cs.y, kv.x * cs.y + kv.y * cs.x,
+                      kv.z * cs.z - kv.w * cs.w, kv.z * cs.w + kv.w * cs.z);
+    if (w == 0 && ps == 0) {
+      const float sn = wave_sum<8>(fmaf(qq.x, knw.x, fmaf(qq.y, knw.y, fmaf(qq.z, knw.z, qq.w * knw.w))));
+      if (dg == 0) {
+        st_m[PBX_HA_STATES - 1] = sn;
+        st_l[PBX_HA_STATES - 1] = 1.f;
+      }
+      *reinterpret_cast<float4 *>(&st_acc[PBX_HA_STATES - 1][4 * dg]) = vnw;
     }
-    a.out[(size_t)h * hd + tid] = num / den;
   }
-  // 6. the KV-cache append (the group's first head, lanes 0..hd/4-1), last:
-  //    every head of the group takes row pos from registers
+  lds_barrier();
+
+  // merge: M is finite (the new position, or position pos of a batch row)
+  if (w == 0) {
+    constexpr int NS = ROWS ? PBX_HA_STATES - 1 : PBX_HA_STATES;
+    const float mi = lane < NS ? st_m[lane] : -INFINITY;
+    const float li = lane < NS ? st_l[lane] : 0.f;
+    const float M = wave_max(mi);
+    const float e = __builtin_amdgcn_exp2f(mi - M);
+    const float den = wave_sum(e * li);
+    if (lane < NS) st_e[lane] = e;
+    // the wave reads what its own lanes wrote: LDS keeps a wave's order
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float num = 0.f;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) num = fmaf(st_e[i], st_acc[i][lane], num);
+    if (lane < hd) a.out[(size_t)h * hd + lane] = num / den;
+  }
+  // the KV-cache append (the group's first head, lanes 0..hd/4-1), last
   if (!ROWS && h % Gq == 0 && tid < hd4) {
     *reinterpret_cast<float4 *>(kb + (size_t)pos * kvdim + dcol) = knw;
     *reinterpret_cast<float4 *>(vb + (size_t)pos * kvdim + dcol) = vnw;
   }
 }
-
 
 extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_head(AttnArgs a) {
   attention_head_body<false>(a, a.state[0]);
