@@ -275,7 +275,7 @@ def run_decode(args, pb, synth):
                 "frac_back_to_back": round(by / us_b2b / 1e3 / HBM_PEAK_GBS, 4)}
     step_bytes = sum(r["bytes_per_step"] for r in roles.values())
     seam = run_seam(ctx, pb, cfg, host) if host else None
-    matvec_shapes = run_matvec_shapes(ctx, pb)
+    matvec_shapes = None if args.no_matvec_shapes else run_matvec_shapes(ctx, pb)
     m_gt_1 = None if args.no_m_gt_1 else run_m_gt_1(ctx, model, cfg, pb, synth)
     next_rows = None
     if not args.no_m_gt_1:
@@ -666,6 +666,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-m-gt-1", action="store_true",
                     help="skip the prefill / verify / speculative measurements")
+    ap.add_argument("--no-matvec-shapes", action="store_true",
+                    help="skip the isolated matvec shapes (their timing captures HIP graphs, "
+                         "which rocprofv3's kernel tracer can fault on)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write profiles/traffic_decode.json from two rocprofv3 --pmc runs")
     args = ap.parse_args()
