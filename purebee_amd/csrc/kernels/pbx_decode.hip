@@ -79,10 +79,19 @@ DK_MODES_SMALL(PBX_Q6K, q6k, 4)
       pbx_dk_##TN##_i##WV##x##RT##b##IB##l_lmh(GemvArgs a) {                              \
     gemv_int<T, WV, RT, IB, PRO_RMSNORM, EPI_ARGMAX, true>(a);                            \
   }
+// Scheduled variants (pbx_gemv_impl.h): w<BW> = BW builder waves beside the
+// WV row waves, p<PRE> = rows requested before the limb barrier.
+// Name: pbx_dk_<type>_i<WV>x<RT>b<IB>[w<BW>][p<PRE>]_<mode>.
+#define DK_INT_S(T, TN, WV, RT, IB, BW, PRE, SUF, PRO, EPI, MN)                               \
+  extern "C" __global__ void __launch_bounds__((WV + BW) * 64)                            \
+      pbx_dk_##TN##_i##WV##x##RT##b##IB##SUF##_##MN(GemvArgs a) {                         \
+    gemv_int<T, WV, RT, IB, PRO, EPI, false, 1, BW, PRE>(a);                              \
+  }
 // 16-wave workgroups (at most 128 VGPRs a lane) only where the prologue
 // wave's activation registers still fit: Q4_0 with one block per lane.
 DK_INT_GU(PBX_Q4, q4, 8, 4, 1)
 DK_INT_GU(PBX_Q4, q4, 16, 4, 1)
+DK_INT_S(PBX_Q4, q4, 16, 4, 1, 0, 2, p2, PRO_RMSNORM, EPI_SWIGLU, gu)
 DK_INT_GU(PBX_Q4, q4, 8, 4, 2)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 1)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 2)
@@ -95,6 +104,8 @@ DK_INT_QKV(PBX_Q4, q4, 8, 2, 1)
 DK_INT_ADD(PBX_Q4, q4, 4, 2, 1)
 DK_INT_ADD(PBX_Q4, q4, 4, 2, 2)
 DK_INT_ADD(PBX_Q4, q4, 4, 2, 4)
+DK_INT_S(PBX_Q4, q4, 4, 2, 4, 8, 2, w8, PRO_NONE, EPI_ADD, add)
+DK_INT_S(PBX_Q4, q4, 4, 2, 4, 4, 2, w4, PRO_NONE, EPI_ADD, add)
 DK_INT_ADD(PBX_Q4, q4, 4, 1, 1)
 DK_INT_ADD(PBX_Q4, q4, 4, 1, 4)
 DK_INT_LMH(PBX_Q4, q4, 4, 16, 1)

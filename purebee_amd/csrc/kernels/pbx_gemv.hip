@@ -82,7 +82,15 @@ PBX_SMALL(pbx_gemv_q6_k_small, PBX_Q6K, 4)
   extern "C" __global__ void __launch_bounds__(WV * 64) NAME(GemvArgs a) {   \
     gemv_int<TYPE, WV, RT, IB, PRO_NONE, EPI_STORE, LOOP>(a);                 \
   }
+// Scheduled variants (pbx_gemv_impl.h): w<BW> = BW builder waves beside the
+// WV row waves, p<PRE> = rows requested before the limb barrier.
+#define PBX_INT_S(NAME, TYPE, WV, RT, IB, BW, PRE)                            \
+  extern "C" __global__ void __launch_bounds__((WV + BW) * 64) NAME(GemvArgs a) { \
+    gemv_int<TYPE, WV, RT, IB, PRO_NONE, EPI_STORE, false, 1, BW, PRE>(a);    \
+  }
 PBX_INT(pbx_gemv_q4_0_i16x4b1, PBX_Q4, 16, 4, 1, false)
+PBX_INT_S(pbx_gemv_q4_0_i16x4b1p2, PBX_Q4, 16, 4, 1, 0, 2)
+PBX_INT_S(pbx_gemv_q4_0_i4x2b4w8, PBX_Q4, 4, 2, 4, 8, 2)
 PBX_INT(pbx_gemv_q4_0_i4x2b1, PBX_Q4, 4, 2, 1, false)
 PBX_INT(pbx_gemv_q4_0_i4x1b1, PBX_Q4, 4, 1, 1, false)
 PBX_INT(pbx_gemv_q4_0_i4x8b1l, PBX_Q4, 4, 8, 1, true)

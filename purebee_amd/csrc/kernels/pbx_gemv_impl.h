@@ -823,6 +823,21 @@ __device__ __forceinline__ void limb_words(float4 p, float scale, int &w0, int &
   w2 = (int)((__builtin_amdgcn_perm(cd2, ab2, 0x05040100u) + 0x40404040u) ^ 0x80808080u);
 }
 
+// Schedules for one activation row without the tile loop:
+//  * BW > 0: the first BW waves of the workgroup only build the limbs and
+//    the WV waves after them only stream rows.  A builder reads the
+//    activations in contiguous 1 KB chunks (lane l: float4 l % 8 of block
+//    8 * chunk + l / 8) and writes the limb words of its blocks to LDS.  A
+//    wave that builds and also streams rows can start its build only once
+//    its weight requests have been accepted, and the CU accepts them about
+//    as fast as earlier requests return, so the barrier would wait for
+//    most of the weight stream (measured on the K = 8192 down GEMV: limbs
+//    ready 2.0 us after the start with every wave building, 1.7 us with 8
+//    builder waves beside the 4 row waves).
+//  * PRE < RT: each wave requests rows 0..PRE-1 before the build and
+//    barrier and the others after it, so the barrier is not held behind
+//    the issue of the whole tile (16 x 4 gate|up: limbs ready 1.4 us after
+//    the start instead of 2.1 us; the dots then overlap the stream).
 // LOOP (lm heads, tall matrices): a workgroup takes tiles blockIdx.x,
 // blockIdx.x + G, ... (G = gridDim.x) with the next tile's bytes in flight
 // while a tile is reduced and builds the activation limbs once; EPI_ARGMAX
@@ -831,16 +846,20 @@ __device__ __forceinline__ void limb_words(float4 p, float scale, int &w0, int &
 // in, N out) against one pass over the weight bytes -- the speculative
 // verify and short prompts.  MR = 1: activation row blockIdx.y (the plain
 // instruction's M < 4 rows).
-template <int TYPE, int WV, int RT, int IB, int PRO, int EPI, bool LOOP = false, int MR = 1>
+template <int TYPE, int WV, int RT, int IB, int PRO, int EPI, bool LOOP = false, int MR = 1,
+          int BW = 0, int PRE = RT>
 __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   static_assert(TYPE == PBX_Q4 || TYPE == PBX_Q8 || is_q6k<TYPE>(), "quantised weights only");
+  static_assert(BW == 0 || (MR == 1 && !LOOP && EPI != EPI_ARGMAX && (IB * 8) % BW == 0),
+                "builder waves: one activation row, no tile loop, whole chunks per builder");
+  static_assert(PRE >= 1 && (PRE >= RT || (MR == 1 && !LOOP)), "split issue: one row, no loop");
   static_assert(!LOOP || EPI == EPI_ARGMAX || EPI == EPI_STORE, "tile loop epilogues");
   static_assert(MR == 1 || EPI != EPI_ARGMAX, "argmax keys for one row");
   constexpr int QB = BlockTraits<TYPE>::QB;
   constexpr int NV = QB / 16;
   constexpr bool PAIR = EPI == EPI_SWIGLU;
   static_assert(IB * 64 * 32 <= PBX_INT_MAXK, "K limit");
-  constexpr int T = WV * 64;
+  constexpr int T = WV * 64;        // threads of the row waves
   constexpr int NB = MR * IB * 64;  // activation blocks (past B: unused)
   // lanes per block in the build, float4s a builder lane covers, and the
   // blocks a lane builds one after another (Q = 1 only).  With more than
@@ -862,11 +881,14 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   constexpr int SSP = IB * Q * 4;
   __shared__ float4 ssq[PRO == PRO_RMSNORM ? MR : 1][SSP / 4];
   __shared__ uint64_t kred[WV];
+  __shared__ float ssqb[BW > 0 ? BW : 1];  // BW > 0: sum of x^2 of each builder wave
 
   const int N = a.N, B = a.B, K = B * 32;
   const int lane = threadIdx.x & 63, tid = threadIdx.x;
-  // wave-uniform (SGPR): row bases and weight addresses are scalar arithmetic
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // wave-uniform (SGPR): row bases and weight addresses are scalar arithmetic;
+  // with builder waves, `wave` numbers the row waves (builders: negative)
+  const int wave_hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = wave_hw - BW;
   const int NO = PAIR ? N / 2 : N;
   const int rows = MR == 1 ? 1 : a.rows;  // valid activation rows
   constexpr int RTO = PAIR ? RT / 2 : RT;  // output rows a wave
@@ -883,6 +905,61 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   const float *X = a.X + (size_t)blockIdx.y * MR * K;
   float *y = a.Y + (size_t)blockIdx.y * MR * NO;
 
+  if constexpr (BW > 0) {
+    if (wave < 0) {
+      // builder wave wave_hw: chunks wave_hw, wave_hw + BW, ... of 256
+      // activations (8 blocks), all requested before any arithmetic
+      constexpr int CPB = IB * 8 / BW;
+      const int qd = lane & 7;
+      float4 xv[CPB], nv[CPB];
+#pragma unroll
+      for (int c = 0; c < CPB; ++c) {
+        const int e0 = (wave_hw + BW * c) * 256 + lane * 4;
+        const int ec = e0 < K ? e0 : 0;
+        xv[c] = *reinterpret_cast<const float4 *>(X + ec);
+        nv[c] = make_float4(1.f, 1.f, 1.f, 1.f);
+        if constexpr (PRO == PRO_RMSNORM) nv[c] = *reinterpret_cast<const float4 *>(a.normw + ec);
+      }
+      float sq = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPB; ++c) {
+        const int b = (wave_hw + BW * c) * 8 + (lane >> 3);
+        const bool ok = b < B;
+        const float4 t = ok ? xv[c] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[c];
+        if constexpr (PRO == PRO_RMSNORM)
+          sq = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, sq))));
+        const float4 p = make_float4(t.x * w.x, t.y * w.y, t.z * w.z, t.w * w.w);
+        float mx = fmaxf(fmaxf(fabsf(p.x), fabsf(p.y)), fmaxf(fabsf(p.z), fabsf(p.w)));
+        float nf = fmaf(p.x, 0.f, fmaf(p.y, 0.f, fmaf(p.z, 0.f, p.w * 0.f)));
+        mx = group_max<8>(mx);
+        nf = group_sum<8>(nf);
+        int e = 0;
+        if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
+        e = max(e, -100);
+        int w0, w1, w2, sv;
+        limb_words(p, ldexpf(1.f, 21 - e), w0, w1, w2, sv);
+        // float4s 0..3 of a block are its elements 0..15
+        const int slo = group_isum<8>(qd < 4 ? sv : 0), shi = group_isum<8>(qd < 4 ? 0 : sv);
+        if (ok) {
+          reinterpret_cast<int *>(&limb[0][0][qd >> 2][b])[qd & 3] = w0;
+          reinterpret_cast<int *>(&limb[0][1][qd >> 2][b])[qd & 3] = w1;
+          reinterpret_cast<int *>(&limb[0][2][qd >> 2][b])[qd & 3] = w2;
+          if (qd == 0) {
+            bsum[0][0][b] = is_q6k<TYPE>() ? slo : slo + shi;
+            bsum[0][1][b] = shi;
+            bscale[0][b] = ldexpf(1.f, e - 21) + nf;
+          }
+        }
+      }
+      if constexpr (PRO == PRO_RMSNORM) {
+        sq = wave_sum(sq);
+        if (lane == 0) ssqb[wave_hw] = sq;
+      }
+      lds_barrier();
+      return;
+    }
+  }
+
   // 1. Builder segments (segment s = L + T * it: block s / Q of the rows,
   //    its float4s FPL*(s % Q) ..) request their activations and RMSNorm
   //    weights before any wave requests weight bytes: a CU returns loads in
@@ -892,7 +969,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   // whole waves hold segments or none (NB * Q is a multiple of 64); the
   // others skip the build: waiting for loads they do not need would hold
   // the barrier behind their weight bytes
-  auto builds = [&](int it) -> bool { return wave * 64 + T * it < NB * Q; };
+  auto builds = [&](int it) -> bool { return BW == 0 && wave * 64 + T * it < NB * Q; };
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     if (!builds(it)) continue;
@@ -927,11 +1004,13 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   }
   // Q6_K: db holds the super-block's d, ex the lane's two int8 sub-block
   // scales (load_lane); both are used only in the dots.
-  auto load_tile = [&](int t, unsigned (&db)[RT][IB], uint4 (&qq)[RT][IB][NV],
+  // rows i0..i1-1 of tile t (constants after inlining)
+  auto load_rows = [&](int t, int i0, int i1, unsigned (&db)[RT][IB], uint4 (&qq)[RT][IB][NV],
                        unsigned (&ex)[RT][IB]) {
     const int r0 = rbase(t);
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
+      if (i < i0 || i >= i1) continue;
       const int rw = row_ok(r0, i) ? tile_row(r0, i) : 0;
 #pragma unroll
       for (int j = 0; j < IB; ++j) {
@@ -942,6 +1021,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
+      if (i < i0 || i >= i1) continue;
       const int rw = row_ok(r0, i) ? tile_row(r0, i) : 0;
 #pragma unroll
       for (int j = 0; j < IB; ++j) {
@@ -957,6 +1037,9 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
       }
     }
   };
+  auto load_tile = [&](int t, unsigned (&db)[RT][IB], uint4 (&qq)[RT][IB][NV],
+                       unsigned (&ex)[RT][IB]) { load_rows(t, 0, RT, db, qq, ex); };
+  constexpr int PRE_R = PRE < RT ? PRE : RT;  // rows requested before the barrier
   unsigned dbA[RT][IB], dbB[RT][IB], exA[RT][IB], exB[RT][IB];
   uint4 qA[RT][IB][NV], qB[RT][IB][NV];
   // LOOP: the workgroup's tiles are blockIdx.x + k*G, k < TW.  Loads are
@@ -965,7 +1048,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   // everything the branch may have issued.
   const int G = gridDim.x;
   const int TW = LOOP ? (n_tiles - (int)blockIdx.x + G - 1) / G : 1;
-  load_tile(blockIdx.x, dbA, qA, exA);
+  load_rows(blockIdx.x, 0, PRE_R, dbA, qA, exA);
   if constexpr (LOOP) load_tile(blockIdx.x + (TW > 1 ? G : 0), dbB, qB, exB);
   __builtin_amdgcn_sched_barrier(0);
 
@@ -1044,6 +1127,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     }
   }
   lds_barrier();
+  if constexpr (PRE_R < RT) load_rows(blockIdx.x, PRE_R, RT, dbA, qA, exA);
   // RMSNorm's 1/rms of each activation row from the builders' row sums
   // (broadcast LDS reads, while the weight bytes are still arriving); it
   // multiplies the blocks' scales, so the dots need it and no wave
@@ -1054,10 +1138,15 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     inv[m] = 1.f;
     if constexpr (PRO == PRO_RMSNORM) {
       float sm = 0.f;
+      if constexpr (BW > 0) {
 #pragma unroll
-      for (int c = 0; c < SSP / 4; ++c) {
-        const float4 v = ssq[m][c];
-        sm += (v.x + v.y) + (v.z + v.w);
+        for (int c = 0; c < BW; ++c) sm += ssqb[c];
+      } else {
+#pragma unroll
+        for (int c = 0; c < SSP / 4; ++c) {
+          const float4 v = ssq[m][c];
+          sm += (v.x + v.y) + (v.z + v.w);
+        }
       }
       inv[m] = 1.0f / sqrtf(sm / (float)K + a.eps);
     }

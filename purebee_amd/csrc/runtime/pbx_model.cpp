@@ -189,13 +189,22 @@ static bool int_gemv_disabled() {
   return e && e[0] == '0';
 }
 
-// PBX_GEMV_INT_SHAPES="role=WVxRT[l],..." (roles qkv, o, gate_up, down,
-// lm_head; lm_head_q6k for a Q6_K head), read when the step is planned: the
-// integer-limb kernel with WV waves x RT rows for the listed roles (Q4_0 /
-// Q8_0, K = 2048..8192; a Q6_K head at K = 2048; a
-// trailing l selects the lm head's tile loop), for tuning.  A shape that
-// was not compiled fails the plan.
-static bool int_override(const char *role, int *wv, int *rt, bool *loop) {
+// Integer-limb kernel shape: WV row waves x RT rows, IB blocks a lane, BW
+// builder waves, PRE rows requested before the limb barrier (0: all), tile
+// loop.  Kernel name part: i<WV>x<RT>b<IB>[w<BW>][p<PRE>][l].
+struct IntShape {
+  int wv = 4, rt = 1, ib = 1, bw = 0, pre = 0;
+  bool loop = false;
+};
+
+// PBX_GEMV_INT_SHAPES="role=WVxRT[wBW][pPRE][l],..." (roles qkv, o, gate_up,
+// down, lm_head; lm_head_q6k for a Q6_K head), read when the step is
+// planned: the integer-limb kernel with WV row waves x RT rows (BW builder
+// waves, PRE rows requested before the barrier) for the listed roles (Q4_0 /
+// Q8_0, K = 2048..8192; a Q6_K head at K = 2048; a trailing l selects the
+// lm head's tile loop), for tuning.  A shape that was not compiled fails
+// the plan.
+static bool int_override(const char *role, IntShape *sh) {
   const char *e = getenv("PBX_GEMV_INT_SHAPES");
   if (!e || !role) return false;
   const std::string s(e), key = std::string(role) + "=";
@@ -204,9 +213,16 @@ static bool int_override(const char *role, int *wv, int *rt, bool *loop) {
     size_t q = s.find(',', p);
     if (q == std::string::npos) q = s.size();
     const std::string item = s.substr(p, q - p);
+    int wv, rt, n = 0;
     if (item.compare(0, key.size(), key) == 0 &&
-        sscanf(item.c_str() + key.size(), "%dx%d", wv, rt) == 2) {
-      *loop = item.back() == 'l';
+        sscanf(item.c_str() + key.size(), "%dx%d%n", &wv, &rt, &n) == 2) {
+      sh->wv = wv;
+      sh->rt = rt;
+      sh->bw = sh->pre = 0;
+      const char *t = item.c_str() + key.size() + n;
+      if (*t == 'w') sh->bw = (int)strtol(t + 1, (char **)&t, 10);
+      if (*t == 'p') sh->pre = (int)strtol(t + 1, (char **)&t, 10);
+      sh->loop = *t == 'l';
       return true;
     }
     p = q + 1;
@@ -215,41 +231,48 @@ static bool int_override(const char *role, int *wv, int *rt, bool *loop) {
 }
 
 static bool int_shape(bool enabled, const char *mode, const char *role, int type, int N, int B,
-                      int *wv, int *rt, int *ib, bool *loop) {
+                      IntShape *sh) {
   if (!enabled || B < 64 || B > 256) return false;
-  *ib = (B + 63) / 64;
-  *loop = false;
+  *sh = IntShape();
+  sh->ib = (B + 63) / 64;
   if (type == PBX_TYPE_Q6_K) {  // the lm head at K = 2048: 4 waves x 4 rows, tile loop
     if (strcmp(mode, "lmh") != 0 || B != 64) return false;
-    if (int_override("lm_head_q6k", wv, rt, loop)) return true;
-    *wv = 4;
-    *rt = 4;
-    *loop = true;
+    if (int_override("lm_head_q6k", sh)) return true;
+    sh->wv = 4;
+    sh->rt = 4;
+    sh->loop = true;
     return true;
   }
   if (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0) return false;
-  if (int_override(role, wv, rt, loop)) return *ib <= *wv;
+  if (int_override(role, sh)) return sh->bw > 0 || sh->ib <= sh->wv;
   if (strcmp(mode, "gu") == 0) {
     if (B > 128) return false;
-    *rt = 4;
-    // 16 waves only for Q4_0 with one block per lane (register budget)
-    *wv = (type == PBX_TYPE_Q4_0 && *ib == 1 && N / 64 >= 256) ? 16 : 8;
+    sh->rt = 4;
+    // 16 waves only for Q4_0 with one block per lane (register budget); their
+    // first two rows requested before the limb barrier
+    if (type == PBX_TYPE_Q4_0 && sh->ib == 1 && N / 64 >= 256) {
+      sh->wv = 16;
+      sh->pre = 2;
+    } else {
+      sh->wv = 8;
+    }
     return true;
   }
   if (type != PBX_TYPE_Q4_0) return false;
-  *wv = 4;
+  sh->wv = 4;
   if (strcmp(mode, "qkv") == 0) {
-    *rt = 4;
-    return *ib <= 2;
+    sh->rt = 4;
+    return sh->ib <= 2;
   }
   if (strcmp(mode, "add") == 0) {
-    *rt = 2;
-    return *ib != 3;
+    sh->rt = 2;
+    if (sh->ib == 4) sh->bw = 8;  // K = 8192 (down): 8 builder waves
+    return sh->ib != 3;
   }
   if (strcmp(mode, "lmh") == 0) {  // K = 2048: 8-row waves with the tile loop
-    *rt = *ib == 1 ? 8 : 16;
-    *loop = *ib == 1;
-    return *ib <= 2;
+    sh->rt = sh->ib == 1 ? 8 : 16;
+    sh->loop = sh->ib == 1;
+    return sh->ib <= 2;
   }
   return false;
 }
@@ -260,18 +283,20 @@ static bool int_shape(bool enabled, const char *mode, const char *role, int type
 // per workgroup and the largest row tile that keeps >= 4 workgroups per CU.
 static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, const char *role, int type,
                       int N, int B, std::string *shape, dim3 *grid, dim3 *block, int *n_tiles) {
-  int wv, rt, ib;
-  bool loop;
-  if (int_shape(int_ok, mode, role, type, N, B, &wv, &rt, &ib, &loop)) {
-    *shape = "i" + std::to_string(wv) + "x" + std::to_string(rt) + "b" + std::to_string(ib) +
-             (loop ? "l" : "");
+  IntShape sh;
+  if (int_shape(int_ok, mode, role, type, N, B, &sh)) {
+    const int wv = sh.wv, rt = sh.rt;
+    const bool loop = sh.loop;
+    *shape = "i" + std::to_string(wv) + "x" + std::to_string(rt) + "b" + std::to_string(sh.ib) +
+             (sh.bw ? "w" + std::to_string(sh.bw) : "") +
+             (sh.pre ? "p" + std::to_string(sh.pre) : "") + (loop ? "l" : "");
     const int tiles = (N + wv * rt - 1) / (wv * rt);
     // tile loop: two workgroups per CU (four for 4-row waves), each taking
     // every G-th tile
     // (Q6_K: two, its tile buffers are 64-byte lane blocks)
     const int per_cu = type == PBX_TYPE_Q6_K ? 2 : rt <= 4 ? 4 : 2;
     *grid = dim3(loop ? std::min(tiles, per_cu * c->cu_count) : tiles);
-    *block = dim3(64 * wv);
+    *block = dim3(64 * (wv + sh.bw));
     *n_tiles = (int)grid->x;
     return;
   }

@@ -554,7 +554,7 @@ int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t
       B <= 256 && (B + 63) / 64 != 3) {
     const bool is_q4 = w->type == PBX_TYPE_Q4_0;
     const int ib = (B + 63) / 64;
-    int wv = 4, rt = 1;
+    int wv = 4, rt = 1, bw = 0, pre = 0;
     bool loop = false;
     if (ib == 1 && N >= 65536 && !dBias) {
       rt = 8;
@@ -562,12 +562,15 @@ int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t
     } else if (ib <= 2 && N >= 8192) {
       wv = ib == 1 && is_q4 ? 16 : 8;
       rt = 4;
+      if (wv == 16) pre = 2;  // two rows requested before the limb barrier
     } else if (N >= 2048) {
       rt = 2;
+      if (ib == 4 && is_q4) bw = 8;  // K = 8192: 8 builder waves
     }
     const std::string name = std::string("pbx_gemv_") + (is_q4 ? "q4_0" : "q8_0") + "_i" +
                              std::to_string(wv) + "x" + std::to_string(rt) + "b" +
-                             std::to_string(ib) + (loop ? "l" : "");
+                             std::to_string(ib) + (bw ? "w" + std::to_string(bw) : "") +
+                             (pre ? "p" + std::to_string(pre) : "") + (loop ? "l" : "");
     hipFunction_t f = pbx_kernel_by_name(c, name);
     if (!f) return pbx_fail(c, PBX_ELOAD, "pbx_linear: kernel %s missing", name.c_str());
     const int tiles = (N + wv * rt - 1) / (wv * rt);
@@ -575,7 +578,7 @@ int pbx_linear_enqueue(pbx_ctx *c, const pbx_weight *w, const float *dX, int64_t
     void *gargs[] = {&g};
     return pbx_launch_fn(c, f, name.c_str(),
                          dim3((unsigned)(loop ? std::min(tiles, 2 * c->cu_count) : tiles), gy),
-                         dim3(64 * wv), gargs, stream);
+                         dim3(64 * (wv + bw)), gargs, stream);
   }
   void *args[] = {(void *)&w->qs, (void *)&w->d, (void *)&w->m, &dX, &dBias, &dY, &N, &B};
   const bool q4 = w->type == PBX_TYPE_Q4_0 || w->type == PBX_TYPE_Q4_1;
