@@ -71,6 +71,8 @@ DK_MODES_SMALL(PBX_Q6K, q6k, 4)
   }
 #define DK_INT_GU(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_RMSNORM, EPI_SWIGLU, gu)
 #define DK_INT_QKV(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_RMSNORM, EPI_STORE, qkv)
+// q|k|v with RoPE and the cache append (EPI_ROPE): pbx_dk_<type>_i<WV>x<RT>b<IB>_qkvr
+#define DK_INT_QKVR(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_RMSNORM, EPI_ROPE, qkvr)
 #define DK_INT_ADD(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_NONE, EPI_ADD, add)
 #define DK_INT_LMH(T, TN, WV, RT, IB) DK_INT(T, TN, WV, RT, IB, PRO_RMSNORM, EPI_ARGMAX, lmh)
 // lm head with a tile loop per workgroup: pbx_dk_<type>_i<WV>x<RT>b<IB>l_lmh
@@ -99,6 +101,7 @@ DK_INT_GU(PBX_Q8, q8, 8, 4, 2)
 // down 4 x 2, lm head 4 x 8 with the tile loop (4 x 16 at K = 4096); the
 // others are tuning alternatives.
 DK_INT_QKV(PBX_Q4, q4, 4, 4, 1)
+DK_INT_QKVR(PBX_Q4, q4, 4, 4, 1)
 DK_INT_QKV(PBX_Q4, q4, 4, 4, 2)
 DK_INT_QKV(PBX_Q4, q4, 8, 2, 1)
 DK_INT_ADD(PBX_Q4, q4, 4, 2, 1)
@@ -204,6 +207,7 @@ struct AttnArgs {
   const int *state;    // state[0] = position
   int n_heads, n_kv_heads, head_dim;
   float scale;         // 1/sqrt(head_dim)
+  int max_seq;         // cache rows (pbx_attention_head_c)
 };
 
 // One workgroup per query head (llama.js:258-301 / llama-streaming.js:543-573):
@@ -433,12 +437,6 @@ __device__ __forceinline__ void head_chunk(const float *kb, const float *vb, int
   m = mn;
 }
 
-// ROWS: one row of a batch whose q is already rotated and whose k, v are
-// already in the cache at every position up to pos (pbx_rope_append_rows):
-// every position comes from the cache, no RoPE, no new-position state and
-// no append; a.qkv and a.out point at the row, the position comes from the
-// caller.
-template <bool ROWS>
 __device__ __forceinline__ void attention_head_body(const AttnArgs &a, const int pos) {
   __shared__ float st_m[PBX_HA_STATES], st_l[PBX_HA_STATES], st_e[PBX_HA_STATES];
   __shared__ __attribute__((aligned(16))) float st_acc[PBX_HA_STATES][PBX_HA_MAX_HD];
@@ -449,20 +447,16 @@ __device__ __forceinline__ void attention_head_body(const AttnArgs &a, const int
   const int dg = lane & 15, ps = lane >> 4;  // dim group, row (position slot)
   const int dcol = 4 * min(dg, hd4 - 1);     // clamped for head_dim < 64
   float *kb = a.kcache + (size_t)g * hd, *vb = a.vcache + (size_t)g * hd;
-  const int nc = ROWS ? pos + 1 : pos;  // positions read from the cache
+  const int nc = pos;  // positions read from the cache
 
   // the lane's dims of q, the new k and v, and their RoPE pairs
-  const float4 cs = ROWS ? make_float4(1.f, 0.f, 1.f, 0.f)
-                         : *reinterpret_cast<const float4 *>(a.rope + (size_t)pos * hd + dcol);
+  const float4 cs = *reinterpret_cast<const float4 *>(a.rope + (size_t)pos * hd + dcol);
   const float4 qv = *reinterpret_cast<const float4 *>(a.qkv + (size_t)h * hd + dcol);
-  const float4 kv = ROWS ? make_float4(0.f, 0.f, 0.f, 0.f)
-                         : *reinterpret_cast<const float4 *>(a.qkv + dim + (size_t)g * hd + dcol);
-  const float4 vnw = ROWS ? make_float4(0.f, 0.f, 0.f, 0.f)
-                          : *reinterpret_cast<const float4 *>(a.qkv + dim + kvdim + (size_t)g * hd + dcol);
+  const float4 kv = *reinterpret_cast<const float4 *>(a.qkv + dim + (size_t)g * hd + dcol);
+  const float4 vnw = *reinterpret_cast<const float4 *>(a.qkv + dim + kvdim + (size_t)g * hd + dcol);
   const float c = a.scale * 1.44269504088896340736f;  // scale * log2 e
-  float4 qq = ROWS ? qv
-                   : make_float4(qv.x * cs.x - qv.y * cs.y, qv.x * cs.y + qv.y * cs.x,
-                                 qv.z * cs.z - qv.w * cs.w, qv.z * cs.w + qv.w * cs.z);
+  float4 qq = make_float4(qv.x * cs.x - qv.y * cs.y, qv.x * cs.y + qv.y * cs.x,
+                          qv.z * cs.z - qv.w * cs.w, qv.z * cs.w + qv.w * cs.z);
   if (dg >= hd4) qq = make_float4(0.f, 0.f, 0.f, 0.f);  // repeats of the last dims
   qq = make_float4(qq.x * c, qq.y * c, qq.z * c, qq.w * c);
 
@@ -491,24 +485,21 @@ __device__ __forceinline__ void attention_head_body(const AttnArgs &a, const int
     st_l[si] = l;
   }
   *reinterpret_cast<float4 *>(&st_acc[si][4 * dg]) = acc;
-  float4 knw = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (!ROWS) {
-    knw = make_float4(kv.x * cs.x - kv.y * cs.y, kv.x * cs.y + kv.y * cs.x,
-                      kv.z * cs.z - kv.w * cs.w, kv.z * cs.w + kv.w * cs.z);
-    if (w == 0 && ps == 0) {
-      const float sn = wave_sum<8>(fmaf(qq.x, knw.x, fmaf(qq.y, knw.y, fmaf(qq.z, knw.z, qq.w * knw.w))));
-      if (dg == 0) {
-        st_m[PBX_HA_STATES - 1] = sn;
-        st_l[PBX_HA_STATES - 1] = 1.f;
-      }
-      *reinterpret_cast<float4 *>(&st_acc[PBX_HA_STATES - 1][4 * dg]) = vnw;
+  const float4 knw = make_float4(kv.x * cs.x - kv.y * cs.y, kv.x * cs.y + kv.y * cs.x,
+                                 kv.z * cs.z - kv.w * cs.w, kv.z * cs.w + kv.w * cs.z);
+  if (w == 0 && ps == 0) {
+    const float sn = wave_sum<8>(fmaf(qq.x, knw.x, fmaf(qq.y, knw.y, fmaf(qq.z, knw.z, qq.w * knw.w))));
+    if (dg == 0) {
+      st_m[PBX_HA_STATES - 1] = sn;
+      st_l[PBX_HA_STATES - 1] = 1.f;
     }
+    *reinterpret_cast<float4 *>(&st_acc[PBX_HA_STATES - 1][4 * dg]) = vnw;
   }
   lds_barrier();
 
-  // merge: M is finite (the new position, or position pos of a batch row)
+  // merge: M is finite (the new position)
   if (w == 0) {
-    constexpr int NS = ROWS ? PBX_HA_STATES - 1 : PBX_HA_STATES;
+    constexpr int NS = PBX_HA_STATES;
     const float mi = lane < NS ? st_m[lane] : -INFINITY;
     const float li = lane < NS ? st_l[lane] : 0.f;
     const float M = wave_max(mi);
@@ -525,14 +516,171 @@ __device__ __forceinline__ void attention_head_body(const AttnArgs &a, const int
     if (lane < hd) a.out[(size_t)h * hd + lane] = num / den;
   }
   // the KV-cache append (the group's first head, lanes 0..hd/4-1), last
-  if (!ROWS && h % Gq == 0 && tid < hd4) {
+  if (h % Gq == 0 && tid < hd4) {
     *reinterpret_cast<float4 *>(kb + (size_t)pos * kvdim + dcol) = knw;
     *reinterpret_cast<float4 *>(vb + (size_t)pos * kvdim + dcol) = vnw;
   }
 }
 
 extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_head(AttnArgs a) {
-  attention_head_body<false>(a, a.state[0]);
+  attention_head_body(a, a.state[0]);
+}
+
+// ---------------------------------------------------------------------------
+// The same attention on a cache that already holds k and v at every position
+// 0..pos and a q that is already rotated (the decode step's q|k|v GEMV with
+// the RoPE epilogue, or pbx_rope_append_rows for a batch): no RoPE, no
+// new-position state and no append here.  Positions are interleaved over
+// the lanes: slot i holds positions 32i..32i+31, and the row ps of wave w
+// takes position 32i + 4w + ps.  SPEC (decode): the first PBX_HC_SPEC slots
+// are requested before the position is known (their rows do not depend on
+// it), so the K/V transfer overlaps the load of the position; positions
+// past it are masked, their V replaced by zeros (rows never written may
+// hold anything).
+// ---------------------------------------------------------------------------
+#ifndef PBX_HC_SPEC
+#define PBX_HC_SPEC 2
+#endif
+
+// Folds slots s0..s0+J-1 (K rows k, V rows v of the calling lane's row)
+// into the row's running (m, l, acc); positions >= nc are masked.
+template <int J, bool MASKV>
+__device__ __forceinline__ void head_fold(const float4 (&k)[J], const float4 (&v)[J], int s0,
+                                          int pl, int nc, const float4 qq, float &m, float &l,
+                                          float4 &acc) {
+  float s[J];
+  float mc = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const float d = wave_sum<8>(fmaf(qq.x, k[j].x, fmaf(qq.y, k[j].y, fmaf(qq.z, k[j].z, qq.w * k[j].w))));
+    s[j] = 32 * (s0 + j) + pl < nc ? d : -INFINITY;
+    mc = fmaxf(mc, s[j]);
+  }
+  const float mn = fmaxf(m, mc);
+  const float ms = mn == -INFINITY ? 0.f : mn;  // a row with no position yet
+  const float f = __builtin_amdgcn_exp2f(m - ms);
+  float ls = 0.f;
+  float4 a = make_float4(acc.x * f, acc.y * f, acc.z * f, acc.w * f);
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const float p = __builtin_amdgcn_exp2f(s[j] - ms);
+    float4 vv = v[j];
+    if (MASKV && !(32 * (s0 + j) + pl < nc)) vv = make_float4(0.f, 0.f, 0.f, 0.f);
+    ls += p;
+    a.x = fmaf(p, vv.x, a.x);
+    a.y = fmaf(p, vv.y, a.y);
+    a.z = fmaf(p, vv.z, a.z);
+    a.w = fmaf(p, vv.w, a.w);
+  }
+  l = fmaf(l, f, ls);
+  acc = a;
+  m = mn;
+}
+
+// Slots s0..s0+J-1 from the cache, rows clamped to nc - 1.
+template <int J>
+__device__ __forceinline__ void head_chunk_c(const float *kb, const float *vb, int kvdim, int dcol,
+                                             int s0, int pl, int nc, const float4 qq, float &m,
+                                             float &l, float4 &acc) {
+  float4 k[J], v[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    k[j] = *reinterpret_cast<const float4 *>(kb + (size_t)min(32 * (s0 + j) + pl, nc - 1) * kvdim + dcol);
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    v[j] = *reinterpret_cast<const float4 *>(vb + (size_t)min(32 * (s0 + j) + pl, nc - 1) * kvdim + dcol);
+  head_fold<J, false>(k, v, s0, pl, nc, qq, m, l, acc);
+}
+
+template <bool SPEC>
+__device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const int pos_arg) {
+  __shared__ float st_m[PBX_HA_WAVES], st_l[PBX_HA_WAVES];
+  __shared__ __attribute__((aligned(16))) float st_acc[PBX_HA_WAVES][PBX_HA_MAX_HD];
+  const int h = blockIdx.x, hd = a.head_dim, hd4 = hd / 4;
+  const int Gq = a.n_heads / a.n_kv_heads, g = h / Gq;
+  const int kvdim = a.n_kv_heads * hd;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int dg = lane & 15, ps = lane >> 4;  // dim group, row
+  const int dcol = 4 * min(dg, hd4 - 1);     // clamped for head_dim < 64
+  const int pl = 4 * w + ps;                 // the row's position in a slot
+  const float *kb = a.kcache + (size_t)g * hd, *vb = a.vcache + (size_t)g * hd;
+
+  float4 k0[SPEC ? PBX_HC_SPEC : 1], v0[SPEC ? PBX_HC_SPEC : 1];
+  if constexpr (SPEC) {
+#pragma unroll
+    for (int j = 0; j < PBX_HC_SPEC; ++j)
+      k0[j] = *reinterpret_cast<const float4 *>(kb + (size_t)min(32 * j + pl, a.max_seq - 1) * kvdim + dcol);
+#pragma unroll
+    for (int j = 0; j < PBX_HC_SPEC; ++j)
+      v0[j] = *reinterpret_cast<const float4 *>(vb + (size_t)min(32 * j + pl, a.max_seq - 1) * kvdim + dcol);
+  }
+  const float4 qv = *reinterpret_cast<const float4 *>(a.qkv + (size_t)h * hd + dcol);
+  const int nc = (SPEC ? a.state[0] : pos_arg) + 1;  // positions 0..pos
+  const float c = a.scale * 1.44269504088896340736f;  // scale * log2 e
+  float4 qq = dg < hd4 ? make_float4(qv.x * c, qv.y * c, qv.z * c, qv.w * c)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);  // repeats of the last dims
+
+  float m = -INFINITY, l = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  int s0 = 0;
+  if constexpr (SPEC) {
+    head_fold<PBX_HC_SPEC, true>(k0, v0, 0, pl, nc, qq, m, l, acc);
+    s0 = PBX_HC_SPEC;
+  }
+  while (32 * s0 < nc) {
+    const int J = min(16, (nc - 32 * s0 + 31) / 32);
+    switch (J) {
+#define PBX_HEAD_CHUNK_C(n) \
+  case n: head_chunk_c<n>(kb, vb, kvdim, dcol, s0, pl, nc, qq, m, l, acc); break;
+      PBX_HEAD_CHUNK_C(1) PBX_HEAD_CHUNK_C(2) PBX_HEAD_CHUNK_C(3) PBX_HEAD_CHUNK_C(4)
+      PBX_HEAD_CHUNK_C(5) PBX_HEAD_CHUNK_C(6) PBX_HEAD_CHUNK_C(7) PBX_HEAD_CHUNK_C(8)
+      PBX_HEAD_CHUNK_C(9) PBX_HEAD_CHUNK_C(10) PBX_HEAD_CHUNK_C(11) PBX_HEAD_CHUNK_C(12)
+      PBX_HEAD_CHUNK_C(13) PBX_HEAD_CHUNK_C(14) PBX_HEAD_CHUNK_C(15) PBX_HEAD_CHUNK_C(16)
+#undef PBX_HEAD_CHUNK_C
+      default: break;
+    }
+    s0 += J;
+  }
+
+  // merge in two levels: the wave's 4 rows (same dims, 16 lanes apart) in
+  // registers, then the 8 wave states through LDS in one wave
+  float mw = fmaxf(m, __shfl_xor(m, 16, 64));
+  mw = fmaxf(mw, __shfl_xor(mw, 32, 64));  // finite for wave 0 (position 0)
+  const float er = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mw);
+  float lw = l * er;
+  float4 aw = make_float4(acc.x * er, acc.y * er, acc.z * er, acc.w * er);
+#pragma unroll
+  for (int off = 16; off <= 32; off *= 2) {
+    lw += __shfl_xor(lw, off, 64);
+    aw.x += __shfl_xor(aw.x, off, 64);
+    aw.y += __shfl_xor(aw.y, off, 64);
+    aw.z += __shfl_xor(aw.z, off, 64);
+    aw.w += __shfl_xor(aw.w, off, 64);
+  }
+  if (lane == 0) {
+    st_m[w] = mw;
+    st_l[w] = lw;
+  }
+  if (lane < 16) *reinterpret_cast<float4 *>(&st_acc[w][4 * dg]) = aw;
+  lds_barrier();
+  if (w == 0) {
+    const float mi = lane < PBX_HA_WAVES ? st_m[lane] : -INFINITY;
+    const float li = lane < PBX_HA_WAVES ? st_l[lane] : 0.f;
+    const float M = wave_max<4>(mi);  // lanes 0..7 hold the states
+    const float e = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - M);
+    const float den = wave_sum<4>(e * li);
+    float num = 0.f;
+#pragma unroll
+    for (int i = 0; i < PBX_HA_WAVES; ++i)
+      num = fmaf(__shfl(e, i, 64), st_acc[i][lane], num);
+    const float dn = __shfl(den, 0, 64);
+    if (lane < hd) a.out[(size_t)h * hd + lane] = num / dn;
+  }
+}
+
+// Decode step on the cache-complete layout (after pbx_dk_*_qkvr).
+extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_head_c(AttnArgs a) {
+  attention_cached_body<true>(a, 0);
 }
 
 // Batched rows (speculative verify, short batches; head_dim <= 64): workgroup
@@ -544,8 +692,8 @@ pbx_attention_head_rows(const float *qkv, float *kcache, float *vcache, float *o
                         int n_heads, int n_kv_heads, int head_dim, float scale) {
   const int t = blockIdx.y, dim = n_heads * head_dim;
   AttnArgs a{qkv + (size_t)t * (dim + 2 * n_kv_heads * head_dim), kcache, vcache, nullptr,
-             out + (size_t)t * dim, nullptr, n_heads, n_kv_heads, head_dim, scale};
-  attention_head_body<true>(a, start + t);
+             out + (size_t)t * dim, nullptr, n_heads, n_kv_heads, head_dim, scale, 0};
+  attention_cached_body<false>(a, start + t);
 }
 
 #define PBX_SPLIT_TILE 32

@@ -37,6 +37,11 @@
 // Paired rows: the weight holds N/2 gate rows then N/2 up rows; a workgroup
 // reads matching gate and up rows and stores silu(gate)*up (N/2 outputs).
 #define EPI_SWIGLU 3
+// The q|k|v rows of a decode step (integer-limb kernel, one activation row):
+// RoPE of the q and k rows at the position state[0] (adjacent row pairs,
+// llama.js:163-190), q stored to Y, k and v stored to the cache row of that
+// position (the attention then reads every position from the cache).
+#define EPI_ROPE 4
 
 // Everything a fused GEMV launch needs; passed by value.
 struct GemvArgs {
@@ -52,6 +57,13 @@ struct GemvArgs {
   float eps;
   const uint16_t *msc;  // fp16 min plane (Q4_1), same layout as dsc
   int rows;             // gemv_int with MR > 1: valid activation rows
+  // EPI_ROPE: position, RoPE table [max_seq][head_dim/2][cos, sin], this
+  // layer's caches [max_seq][kvdim], q rows [0, qdim), k rows [qdim,
+  // qdim + kvdim), v rows after them
+  const int *state;
+  const float *rope;
+  float *kcache, *vcache;
+  int qdim, kvdim, head_dim;
 };
 
 namespace pbx {
@@ -855,6 +867,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   static_assert(PRE >= 1 && (PRE >= RT || (MR == 1 && !LOOP)), "split issue: one row, no loop");
   static_assert(!LOOP || EPI == EPI_ARGMAX || EPI == EPI_STORE, "tile loop epilogues");
   static_assert(MR == 1 || EPI != EPI_ARGMAX, "argmax keys for one row");
+  static_assert(EPI != EPI_ROPE || (MR == 1 && !LOOP && RT % 2 == 0), "RoPE rows in pairs");
   constexpr int QB = BlockTraits<TYPE>::QB;
   constexpr int NV = QB / 16;
   constexpr bool PAIR = EPI == EPI_SWIGLU;
@@ -904,6 +917,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   constexpr int LPR = 64 / RT;  // lanes per row after the transposed reduction
   const float *X = a.X + (size_t)blockIdx.y * MR * K;
   float *y = a.Y + (size_t)blockIdx.y * MR * NO;
+  const int pos = EPI == EPI_ROPE ? a.state[0] : 0;
 
   if constexpr (BW > 0) {
     if (wave < 0) {
@@ -1128,6 +1142,13 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   }
   lds_barrier();
   if constexpr (PRE_R < RT) load_rows(blockIdx.x, PRE_R, RT, dbA, qA, exA);
+  // EPI_ROPE: cos and sin of the lane's row (its pair index inside the head)
+  float2 rp = make_float2(1.f, 0.f);
+  if constexpr (EPI == EPI_ROPE) {
+    const int n = rbase(blockIdx.x) + lane / (64 / RT);
+    const int i = ((n < a.qdim + a.kvdim ? n : 0) % a.head_dim) >> 1;
+    rp = *reinterpret_cast<const float2 *>(a.rope + (size_t)pos * a.head_dim + 2 * i);
+  }
   // RMSNorm's 1/rms of each activation row from the builders' row sums
   // (broadcast LDS reads, while the weight bytes are still arriving); it
   // multiplies the blocks' scales, so the dots need it and no wave
@@ -1313,6 +1334,23 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   float tot[MR];
   dots(dbA, qA, exA, tot);
   const int r0 = rbase(blockIdx.x);
+  if constexpr (EPI == EPI_ROPE) {
+    // rows 2i, 2i+1 sit LPR lanes apart after the transposed reduction
+    const float pt = __shfl_xor(tot[0], LPR, 64);
+    if ((lane % LPR) == 0) {
+      const int n = r0 + row;
+      const float t = tot[0];
+      if (n < a.qdim + a.kvdim) {
+        // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
+        const float o = (n & 1) ? fmaf(pt, rp.y, t * rp.x) : fmaf(t, rp.x, -pt * rp.y);
+        if (n < a.qdim) y[n] = o;
+        else a.kcache[(size_t)pos * a.kvdim + (n - a.qdim)] = o;
+      } else if (n < N) {
+        a.vcache[(size_t)pos * a.kvdim + (n - a.qdim - a.kvdim)] = t;
+      }
+    }
+    return;
+  }
   if constexpr (PAIR) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) {

@@ -74,6 +74,11 @@ struct pbx_gemv_args {
   float eps;
   const void *msc;
   int rows;
+  // the q|k|v rows of a decode step (RoPE + cache append epilogue)
+  const int *state;
+  const float *rope;
+  float *kcache, *vcache;
+  int qdim, kvdim, head_dim;
 };
 
 struct pbx_ctx {

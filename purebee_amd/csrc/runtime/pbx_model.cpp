@@ -33,6 +33,7 @@ struct AttnArgsHost {  // AttnArgs in pbx_decode.hip
   const int *state;
   int n_heads, n_kv_heads, head_dim;
   float scale;
+  int max_seq;
 };
 
 struct AttnSplitArgsHost {  // AttnSplitArgs in pbx_decode.hip
@@ -334,8 +335,10 @@ static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const c
   op.kind = ARG_GEMV;
   std::string shape;
   int n_tiles = 0;
-  plan_gemv(c, m->gemv_int, mode, role, w->type, (int)w->N, (int)w->B, &shape, &op.grid, &op.block,
-            &n_tiles);
+  // qkvr (RoPE + cache append epilogue) is planned as qkv
+  const char *plan_mode = strcmp(mode, "qkvr") == 0 ? "qkv" : mode;
+  plan_gemv(c, m->gemv_int, plan_mode, role, w->type, (int)w->N, (int)w->B, &shape, &op.grid,
+            &op.block, &n_tiles);
   if (w->B > 32 && (w->B + 63) / 64 > 8)
     return pbx_fail(c, PBX_ENOTSUP, "model: K=%lld exceeds the GEMV limit of 16384",
                     (long long)w->K);
@@ -396,16 +399,53 @@ static int build_ops(pbx_model *m) {
   if (!fsplit || !fcomb)
     return pbx_fail(c, PBX_ELOAD, "model: split attention kernels not found");
   const size_t layer_kv = (size_t)g.max_seq * m->kvdim;
+  // The head attention on the cache-complete layout when the q|k|v GEMV is
+  // the integer-limb kernel with even row tiles: that kernel rotates q and
+  // k and appends k and v (EPI_ROPE), the attention reads every position
+  // from the cache.
+  bool cached = false;
+  if (m->attn_mode == ATTN_HEAD && g.head_dim % 2 == 0 && g.dim % 4 == 0 && m->kvdim % 4 == 0) {
+    std::string shape;
+    dim3 gr, bl;
+    int nt;
+    const pbx_weight *w0 = m->layers[0].wqkv;
+    plan_gemv(c, m->gemv_int, "qkv", "qkv", w0->type, (int)w0->N, (int)w0->B, &shape, &gr, &bl, &nt);
+    cached = shape == "i4x4b1";
+  }
+  hipFunction_t fheadc = pbx_kernel_by_name(c, "pbx_attention_head_c");
+  if (cached && !fheadc) return pbx_fail(c, PBX_ELOAD, "model: kernel pbx_attention_head_c not found");
   for (int l = 0; l < g.n_layers; ++l) {
     Layer &L = m->layers[l];
     int rc;
     m->layer_op[l] = m->ops.size();
-    if ((rc = add_gemv(m, L.wqkv, "qkv", "qkv", m->x, nullptr, L.attn_norm, m->qkv, nullptr))) return rc;
+    if ((rc = add_gemv(m, L.wqkv, cached ? "qkvr" : "qkv", "qkv", m->x, nullptr, L.attn_norm,
+                       m->qkv, nullptr)))
+      return rc;
+    if (cached) {
+      pbx_gemv_args &ga = m->ops.back().gemv;
+      ga.state = m->state;
+      ga.rope = m->rope;
+      ga.kcache = m->kcache + l * layer_kv;
+      ga.vcache = m->vcache + l * layer_kv;
+      ga.qdim = g.dim;
+      ga.kvdim = m->kvdim;
+      ga.head_dim = g.head_dim;
+    }
     Op a;
     a.role = "attn";
     a.bytes = 2.0 * 4.0 * m->kvdim;  // K and V of one cached position, all KV heads
     a.block = dim3(256);
-    if (m->attn_mode == ATTN_HEAD) {
+    if (cached) {
+      a.kind = ARG_ATTN;
+      a.name = "pbx_attention_head_c";
+      a.f = fheadc;
+      a.grid = dim3(g.n_heads);
+      a.block = dim3(512);
+      a.attn = AttnArgsHost{m->qkv, m->kcache + l * layer_kv, m->vcache + l * layer_kv, m->rope,
+                            m->attn, m->state, g.n_heads, g.n_kv_heads, g.head_dim,
+                            (float)(1.0 / sqrt((double)g.head_dim)), g.max_seq};
+      m->ops.push_back(a);
+    } else if (m->attn_mode == ATTN_HEAD) {
       a.kind = ARG_ATTN;
       a.name = "pbx_attention_head";
       a.f = fhead;
@@ -413,7 +453,7 @@ static int build_ops(pbx_model *m) {
       a.block = dim3(512);
       a.attn = AttnArgsHost{m->qkv, m->kcache + l * layer_kv, m->vcache + l * layer_kv, m->rope,
                             m->attn, m->state, g.n_heads, g.n_kv_heads, g.head_dim,
-                            (float)(1.0 / sqrt((double)g.head_dim))};
+                            (float)(1.0 / sqrt((double)g.head_dim)), g.max_seq};
       m->ops.push_back(a);
     } else if (m->attn_splits > 0) {
       a.kind = ARG_ATTN_SPLIT;
@@ -443,7 +483,7 @@ static int build_ops(pbx_model *m) {
       a.grid = dim3(g.n_heads);
       a.attn = AttnArgsHost{m->qkv, m->kcache + l * layer_kv, m->vcache + l * layer_kv, m->rope,
                             m->attn, m->state, g.n_heads, g.n_kv_heads, g.head_dim,
-                            (float)(1.0 / sqrt((double)g.head_dim))};
+                            (float)(1.0 / sqrt((double)g.head_dim)), g.max_seq};
       m->ops.push_back(a);
     }
     if ((rc = add_gemv(m, L.wo, "add", "o", m->attn, nullptr, nullptr, m->x, nullptr))) return rc;
