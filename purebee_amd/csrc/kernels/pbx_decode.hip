@@ -169,6 +169,22 @@ DK_INT_ROWS(PBX_Q4, q4, 8, 2, 1, 8, false, , PRO_RMSNORM, EPI_STORE, qkv)
 DK_INT_ROWS(PBX_Q4, q4, 8, 1, 1, 8, false, , PRO_NONE, EPI_ADD, add)
 DK_INT_ROWS(PBX_Q4, q4, 8, 1, 4, 5, false, , PRO_NONE, EPI_ADD, add)  // LDS: 5 rows x 24 KB
 
+// Row-batched GEMVs on int8 MFMAs for 1..5 activation rows (gemv_mr):
+// pbx_mr_q4_<RW>x<KS>b<IB>_<mode>, RW 16-row tiles x KS K slices a workgroup.
+// One workgroup a CU is the plan (LDS), so a lane may hold up to 512
+// registers: the weight requests then never wait for registers that an
+// earlier load still has to fill.
+#define MR_K(RW, KS, IB, PRO, EPI, MN)                                                       \
+  extern "C" __global__ void __launch_bounds__(RW * KS * 64)                                \
+      __attribute__((amdgpu_waves_per_eu(1, 1)))                                             \
+      pbx_mr_q4_##RW##x##KS##b##IB##_##MN(GemvArgs a) {                                      \
+    gemv_mr<RW, KS, IB, PRO, EPI, 5>(a);                                                     \
+  }
+MR_K(1, 4, 1, PRO_RMSNORM, EPI_ROPE, qkvr)
+MR_K(1, 4, 1, PRO_NONE, EPI_ADD, add)
+MR_K(4, 1, 1, PRO_RMSNORM, EPI_SWIGLU, gu)
+MR_K(1, 8, 4, PRO_NONE, EPI_ADD, add)
+
 DK_MODES_WIDE(PBX_F32, f32, 2)
 DK_MODES_WIDE(PBX_F32, f32, 4)
 DK_MODES_SMALL(PBX_F32, f32, 2)

@@ -64,6 +64,7 @@ struct GemvArgs {
   const float *rope;
   float *kcache, *vcache;
   int qdim, kvdim, head_dim;
+  int pos0;             // EPI_ROPE with several activation rows: row m at pos0 + m
 };
 
 namespace pbx {
@@ -1382,6 +1383,382 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
       for (int w = 1; w < WV; ++w) best = kred[w] > best ? kred[w] : best;
       a.partials[blockIdx.x] = best;
     }
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Row-batched GEMV on int8 MFMAs: up to MR = 5 activation rows against one
+// pass over Q4_0 weights (K = 2048..8192), for the speculative verify and
+// short prompts.  The activations are fixed point as in gemv_int (per row
+// and 32-block: x_q = rint(x w 2^(21-e)) in three signed byte limbs), held
+// in LDS as the B operand of v_mfma_i32_16x16x32_i8: column c = 3m + L is
+// limb L of activation row m (column 15 is zero).  The A operand is the
+// codes (0..15) of one block of 16 weight rows.  Operand lanes (checked on
+// the device): A lane l holds A[l%16][8(l/16) + j], B lane l holds
+// B[8(l/16) + j][l%16], D lane l holds D[4(l/16) + r][l%16].  Element order
+// inside a block (the same for A and B): lane group g takes elements
+// 4g..4g+3 (low nibbles of bytes 4g..4g+3, limb word g) then 16+4g..16+4g+3
+// (their high nibbles, limb word 4+g).  One MFMA a block gives the exact
+// integer dots of 16 weight rows with every limb of every row; the lane of
+// column (m, L) adds dot * 256^L * 2^(e_mb - 21) / rms_m * d_nb, less
+// 8 sum(x_q) on limb 0 (the Q4_0 offset), for its 4 weight rows, and the
+// three limb lanes of a row are summed at the end.
+// Weight bytes move in 16-byte loads, lane l taking block b + l/16 of row
+// l%16 (whole cache-line pieces), and through a 1 KB LDS slot of the wave
+// into the A layout (lane l's 16 bytes at 16 l: the A reads of one block hit
+// 64 distinct banks); the tile's fp16 row scales likewise in 16-byte loads
+// (lane l: row group l/16, two blocks) through a per-wave LDS table.  The B operand of block b lives at slots
+// 64 b + ((4c + g) ^ (b & 31)) (int2 each), so the builders' writes of one
+// word over 64 blocks spread over the banks and the A-side reads of one
+// block stay a permutation of its 64 slots.
+// Workgroup: RW x KS waves; wave w computes weight-row tiles (16 rows;
+// EPI_SWIGLU: 8 gate rows then their 8 up rows) over the w / RW -th of KS
+// slices of the blocks; slices are summed through LDS.  LOOP (KS = 1): the
+// workgroup takes tiles blockIdx.x * RW + w % RW + k * gridDim.x * RW, the
+// next tile's weights requested while one is multiplied.
+// EPI_ROPE: rows of q|k|v at positions pos0 + m (RoPE of q and k, k and v
+// written to the cache rows, q to Y).
+// ---------------------------------------------------------------------------
+typedef int pbx_v4i __attribute__((ext_vector_type(4)));
+
+template <int RW, int KS, int IB, int PRO, int EPI, int MR, bool LOOP = false>
+__device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
+  static_assert(MR >= 1 && 3 * MR <= 15, "three limb columns a row, 16 columns");
+  static_assert(EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_SWIGLU || EPI == EPI_ROPE,
+                "epilogues");
+  static_assert(!LOOP || (KS == 1 && EPI == EPI_STORE), "tile loop: one slice, stored rows");
+  static_assert((IB * 64) % (4 * KS) == 0, "whole 4-block steps a slice");
+  constexpr int WV = RW * KS, T = WV * 64;
+  constexpr int NB = IB * 64;  // blocks a row (past B: unused)
+  constexpr bool PAIR = EPI == EPI_SWIGLU;
+  // lanes per (row, block) segment in the build and float4s each covers
+  constexpr int NSEG = MR * NB;
+  // 8 lanes a block: each wave reads 1 KB contiguous per activation load
+  // (one lane a block reads 64 cache lines per instruction, several times
+  // slower for these sizes)
+  constexpr int Q = 8;
+  constexpr int FPL = 8 / Q;
+  constexpr int IT = (NSEG * Q + T - 1) / T;
+  constexpr int CH = NB * Q / 64;       // wave-chunks a row (one row each)
+  constexpr int BSM = (NB + KS - 1) / KS;  // blocks a slice at most
+  constexpr int NQ = (BSM + 3) / 4;        // 4-block loads a slice
+  constexpr int NSC = (BSM + 31) / 32;     // 16-byte scale loads a lane
+  __shared__ int2 xb[NB * 64];          // B operand (see the slot rule above)
+  __shared__ float2 xsc[NB][MR];        // 2^(e - 21) (NaN: non-finite block), 8 sum(x_q) of it
+  __shared__ float ssq[MR][CH];         // RMSNorm: sum of x^2 per wave-chunk
+  // a wave's 4 weight blocks (during the dots), then the K-slice partials
+  constexpr int RED = (KS > 1 ? KS - 1 : 1) * RW * 64;  // float4s
+  constexpr int NSLOT = IB > 2 ? 1 : 2;  // weight slots a wave (LDS budget at K = 8192)
+  __shared__ float4 wst_red[WV * 64 * NSLOT > RED ? WV * 64 * NSLOT : RED];
+  __shared__ __attribute__((aligned(16))) uint2 wsc[WV][4][NSC * 32];  // row group, block
+
+  const int N = a.N, B = a.B, K = B * 32;
+  const int lane = threadIdx.x & 63, tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rw = wave % RW, ks = wave / RW;
+  const int NO = PAIR ? N / 2 : N;
+  const int rows = a.rows;
+  const int col = lane & 15, g = lane >> 4;
+  const int mcol = col / 3, lcol = col - 3 * mcol;  // activation row and limb of the column
+  const int n_tiles = (NO + (PAIR ? 7 : 15)) / (PAIR ? 8 : 16);
+  auto tile_r0 = [&](int t) -> int { return PAIR ? t * 8 : t * 16; };
+  auto wrow = [&](int r0, int i) -> int {  // weight row of tile row i (0..15)
+    return PAIR ? (i < 8 ? r0 + i : N / 2 + r0 + i - 8) : r0 + i;
+  };
+  auto wrow_ok = [&](int r0, int i) -> bool { return (PAIR ? r0 + (i & 7) : r0 + i) < NO; };
+  // the wave's K slice
+  const int BS = (B + KS - 1) / KS, b0 = ks * BS, b1 = min(B, b0 + BS);
+
+  // 1. activation segments (row m, block b; Q lanes each), requested first
+  float4 xv[IT][FPL], nv[IT][FPL];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int sg = tid + T * it;
+    const int gb = sg / Q, m = gb / NB, b = gb % NB, qd = sg % Q;
+    const bool ok = m < rows && b < B;
+    const float *xr = a.X + (ok ? (size_t)m * K + (size_t)b * 32 + qd * FPL * 4 : 0);
+    const float *wr = a.normw + (ok ? (size_t)b * 32 + qd * FPL * 4 : 0);
+#pragma unroll
+    for (int v = 0; v < FPL; ++v) {
+      xv[it][v] = *reinterpret_cast<const float4 *>(xr + 4 * v);
+      nv[it][v] = make_float4(1.f, 1.f, 1.f, 1.f);
+      if constexpr (PRO == PRO_RMSNORM) nv[it][v] = *reinterpret_cast<const float4 *>(wr + 4 * v);
+    }
+  }
+  // 2. the first tile's residuals (EPI_ADD), row scales and weights
+  const int t0 = blockIdx.x * RW + rw;
+  float res[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) res[i] = 0.f;
+  if constexpr (EPI == EPI_ADD) {
+    const int r0 = tile_r0(t0);
+    if (lcol == 0 && mcol < MR) {
+      const int mm = mcol < rows ? mcol : 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ti = 4 * g + i;
+        res[i] = a.Y[(size_t)mm * NO + (wrow_ok(r0, ti) ? wrow(r0, ti) : 0)];
+      }
+    }
+  }
+  // tile t: row scales (lane l: rows 4(l/16)..+3 of the tile, blocks
+  // b0 + 32 s + 2(l%16), +1), 16-byte weight pieces (lane l: row l%16,
+  // blocks b0 + 4q + l/16)
+  auto load_tile = [&](int t, uint4 (&wd)[NSC], uint4 (&wq)[NQ]) {
+    const int r0 = tile_r0(t < n_tiles ? t : 0);
+    const int rd = wrow_ok(r0, 4 * g) ? wrow(r0, 4 * g) : 0;
+#pragma unroll
+    for (int sgi = 0; sgi < NSC; ++sgi) {
+      const int b = b0 + 32 * sgi + 2 * col;  // even: the pair lies inside B
+      // a vector load (a struct copy would go through private memory)
+      const u32x4_t v = *reinterpret_cast<const u32x4_t *>(a.dsc + dsc_index(rd, b + 1 < b1 ? b : b0, B));
+      wd[sgi] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int ra = wrow_ok(r0, col) ? wrow(r0, col) : 0;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int b = b0 + 4 * q + g;
+      wq[q] = ld_stream(a.qs + ((size_t)ra * B + (b < b1 ? b : b0)) * 16);
+    }
+  };
+  uint4 wdA[NSC], wdB[NSC];
+  uint4 wqA[NQ], wqB[NQ];
+  load_tile(t0, wdA, wqA);
+  const int G = gridDim.x * RW;  // LOOP: tiles a step
+  if constexpr (LOOP) load_tile(t0 + G, wdB, wqB);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. build: fixed point of each segment into the B operand slots
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int sg = tid + T * it;
+    const int gb = sg / Q, m = gb / NB, b = gb % NB, qd = sg % Q;
+    if (m >= MR) continue;  // wave-uniform: whole waves hold segments or none
+    const bool ok = m < rows && b < B;
+    float4 p[FPL];
+    float mx = 0.f, nf = 0.f, sq = 0.f;
+#pragma unroll
+    for (int v = 0; v < FPL; ++v) {
+      const float4 x = ok ? xv[it][v] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[it][v];
+      if constexpr (PRO == PRO_RMSNORM)
+        sq = fmaf(x.x, x.x, fmaf(x.y, x.y, fmaf(x.z, x.z, fmaf(x.w, x.w, sq))));
+      p[v] = make_float4(x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w);
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(p[v].x), fabsf(p[v].y)), fmaxf(fabsf(p[v].z), fabsf(p[v].w))));
+      nf = fmaf(p[v].x, 0.f, fmaf(p[v].y, 0.f, fmaf(p[v].z, 0.f, fmaf(p[v].w, 0.f, nf))));
+    }
+    if constexpr (Q > 1) {
+      mx = group_max<Q>(mx);
+      nf = group_sum<Q>(nf);
+    }
+    if constexpr (PRO == PRO_RMSNORM) {
+      sq = wave_sum(sq);  // the wave-chunk lies in one activation row
+      if (lane == 0) ssq[m][((tid + T * it) / 64) % CH] = sq;
+    }
+    int e = 0;
+    if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
+    e = max(e, -100);
+    const float scale = ldexpf(1.f, 21 - e);
+    int sum = 0;
+    int *xbi = reinterpret_cast<int *>(xb);
+    const int sw = b & 31;
+#pragma unroll
+    for (int v = 0; v < FPL; ++v) {
+      int w0, w1, w2, sv;
+      limb_words(p[v], scale, w0, w1, w2, sv);
+      sum += sv;
+      // word k = float4 k of the block: lane group k & 3, half k >> 2
+      const int k = qd * FPL + v, gg = k & 3, hf = k >> 2;
+      const int base = 2 * (64 * b);
+      xbi[base + 2 * ((4 * (3 * m) + gg) ^ sw) + hf] = w0;
+      xbi[base + 2 * ((4 * (3 * m + 1) + gg) ^ sw) + hf] = w1;
+      xbi[base + 2 * ((4 * (3 * m + 2) + gg) ^ sw) + hf] = w2;
+      if (m == 0) xbi[base + 2 * ((4 * 15 + gg) ^ sw) + hf] = 0;
+    }
+    if constexpr (Q > 1) sum = group_isum<Q>(sum);
+    if (qd == 0) {
+      const float c0 = ldexpf(1.f, e - 21) + nf;
+      xsc[b][m] = make_float2(c0, 8.f * (float)sum * c0);
+    }
+  }
+  lds_barrier();
+
+  // 4. dots: one MFMA a block, the lane's column scales, 4 weight rows a lane
+  float inv = 1.f;  // 1/rms of the lane's activation row
+  if constexpr (PRO == PRO_RMSNORM) {
+    if (mcol < MR) {
+      float sm = 0.f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) sm += ssq[mcol][c];
+      inv = 1.0f / sqrtf(sm / (float)K + a.eps);
+    }
+  }
+  const float fl = (lcol == 0 ? 1.f : lcol == 1 ? 256.f : 65536.f) * inv;
+  const float fk = lcol == 0 ? inv : 0.f;  // the code offset on limb 0 only
+  const int mc = mcol < MR ? mcol : 0;
+  const int slot = 4 * col + g;
+  unsigned *wsl = reinterpret_cast<unsigned *>(wst_red) + 256 * NSLOT * wave;
+  auto dots = [&](const uint4 (&wd)[NSC], const uint4 (&wq)[NQ], float (&acc)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = 0.f;
+    // the tile's scales into the wave's table: group g, blocks 32 s + 2 col, +1
+    // (kept after the weight requests: a store moved above them would wait
+    // for the scales before the weights are requested)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int sgi = 0; sgi < NSC; ++sgi) {
+      const u32x4_t v = {wd[sgi].x, wd[sgi].y, wd[sgi].z, wd[sgi].w};
+      *reinterpret_cast<u32x4_t *>(&wsc[wave][g][32 * sgi + 2 * col]) = v;
+    }
+    // 4 blocks a step through the wave's LDS slots (two alternate when the
+    // budget allows: the next step's weights are stored while this step's
+    // operands are read); the step's 4 MFMAs issue back to back and their
+    // results are scaled after them.  A wave's LDS operations complete in
+    // order, so a slot is rewritten only after the reads issued before.
+    auto stage = [&](int q) {
+      const u32x4_t wv = {wq[q].x, wq[q].y, wq[q].z, wq[q].w};
+      *reinterpret_cast<u32x4_t *>(wsl + 256 * (q % NSLOT) + 4 * lane) = wv;
+    };
+    if constexpr (NSLOT == 2) stage(0);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      if constexpr (NSLOT == 2) {
+        if (q + 1 < NQ) stage(q + 1);
+      } else {
+        stage(q);
+      }
+      const unsigned *sl = wsl + 256 * (q % NSLOT);
+      unsigned w[4];
+      int2 bo[4];
+      float2 cs[4];
+      uint2 dw[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = 4 * q + u, b = b0 + j;
+        w[u] = sl[4 * (col + 16 * u) + g];  // row col, block b: dword g
+        bo[u] = xb[64 * b + (slot ^ (b & 31))];
+        cs[u] = xsc[b][mc];
+        dw[u] = wsc[wave][g][j];
+      }
+      pbx_v4i d[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const long ao =
+            (long)(((unsigned long long)((w[u] >> 4) & 0x0F0F0F0Fu) << 32) | (w[u] & 0x0F0F0F0Fu));
+        const long bl = (long)(((unsigned long long)(unsigned)bo[u].y << 32) | (unsigned)bo[u].x);
+        const pbx_v4i z = {0, 0, 0, 0};
+        d[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ao, bl, z, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float c = cs[u].x * fl, kk = cs[u].y * fk;
+        acc[0] = fmaf(fmaf((float)d[u][0], c, -kk), f16_bits_to_f32(dw[u].x), acc[0]);
+        acc[1] = fmaf(fmaf((float)d[u][1], c, -kk), f16_bits_to_f32(dw[u].x >> 16), acc[1]);
+        acc[2] = fmaf(fmaf((float)d[u][2], c, -kk), f16_bits_to_f32(dw[u].y), acc[2]);
+        acc[3] = fmaf(fmaf((float)d[u][3], c, -kk), f16_bits_to_f32(dw[u].y >> 16), acc[3]);
+      }
+    }
+    // limbs 0..2 of a row sit in columns 3m..3m+2 (adjacent lanes)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += __shfl_down(acc[i], 1, 16) + __shfl_down(acc[i], 2, 16);
+  };
+
+  float acc[4];
+  if constexpr (LOOP) {
+    // tiles t0 + k G: registers A, B alternate, each refilled two tiles on
+    for (int k = 0;; k += 2) {
+      const int ta = t0 + k * G;
+      if (ta >= n_tiles) break;
+      dots(wdA, wqA, acc);
+      load_tile(ta + 2 * G, wdA, wqA);
+      if (lcol == 0 && mcol < rows) {
+        const int r0 = tile_r0(ta);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = r0 + 4 * g + i;
+          if (n < N) a.Y[(size_t)mcol * NO + n] = acc[i];
+        }
+      }
+      const int tb = ta + G;
+      if (tb >= n_tiles) break;
+      dots(wdB, wqB, acc);
+      load_tile(tb + 2 * G, wdB, wqB);
+      if (lcol == 0 && mcol < rows) {
+        const int r0 = tile_r0(tb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = r0 + 4 * g + i;
+          if (n < N) a.Y[(size_t)mcol * NO + n] = acc[i];
+        }
+      }
+    }
+    return;
+  }
+
+  dots(wdA, wqA, acc);
+  // K slices: slices 1.. through LDS (over the weight slots, once every
+  // wave is past its dots), slice 0 sums and finishes
+  if constexpr (KS > 1) {
+    lds_barrier();
+    if (ks > 0) wst_red[((ks - 1) * RW + rw) * 64 + lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    lds_barrier();
+    if (ks > 0) return;
+#pragma unroll
+    for (int s = 0; s < KS - 1; ++s) {
+      const float4 v = wst_red[(s * RW + rw) * 64 + lane];
+      acc[0] += v.x; acc[1] += v.y; acc[2] += v.z; acc[3] += v.w;
+    }
+  }
+  const int r0 = tile_r0(t0);
+  if (t0 >= n_tiles) return;
+  if constexpr (PAIR) {
+    // tile rows 0..7 (lane groups 0, 1) are gate rows, 8..15 their up rows
+    float up[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(acc[i], 32, 64);
+    if (lcol == 0 && mcol < rows && g < 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = r0 + 4 * g + i;
+        if (n < NO) a.Y[(size_t)mcol * NO + n] = silu(acc[i]) * up[i];
+      }
+    }
+    return;
+  }
+  if (lcol != 0 || mcol >= rows) return;
+  if constexpr (EPI == EPI_ROPE) {
+    const int pos = a.pos0 + mcol;
+#pragma unroll
+    for (int i = 0; i < 4; i += 2) {
+      const int n = r0 + 4 * g + i;  // even: rows n, n + 1 are a RoPE pair
+      if (n >= N) continue;
+      if (n < a.qdim + a.kvdim) {
+        const float2 cs = *reinterpret_cast<const float2 *>(
+            a.rope + (size_t)pos * a.head_dim + (n % a.head_dim));
+        const float o0 = fmaf(acc[i], cs.x, -acc[i + 1] * cs.y);
+        const float o1 = fmaf(acc[i], cs.y, acc[i + 1] * cs.x);
+        if (n < a.qdim) {
+          a.Y[(size_t)mcol * N + n] = o0;
+          a.Y[(size_t)mcol * N + n + 1] = o1;
+        } else {
+          float *kc = a.kcache + (size_t)pos * a.kvdim + (n - a.qdim);
+          kc[0] = o0;
+          kc[1] = o1;
+        }
+      } else {
+        float *vc = a.vcache + (size_t)pos * a.kvdim + (n - a.qdim - a.kvdim);
+        vc[0] = acc[i];
+        vc[1] = acc[i + 1];
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = r0 + 4 * g + i;
+    if (n < N) a.Y[(size_t)mcol * NO + n] = EPI == EPI_ADD ? res[i] + acc[i] : acc[i];
   }
 }
 

@@ -74,11 +74,13 @@ struct pbx_gemv_args {
   float eps;
   const void *msc;
   int rows;
-  // the q|k|v rows of a decode step (RoPE + cache append epilogue)
-  const int *state;
-  const float *rope;
-  float *kcache, *vcache;
-  int qdim, kvdim, head_dim;
+  // the q|k|v rows of a decode step or a batch (RoPE + cache append
+  // epilogue; a batch's row m sits at position pos0 + m)
+  const int *state = nullptr;
+  const float *rope = nullptr;
+  float *kcache = nullptr, *vcache = nullptr;
+  int qdim = 0, kvdim = 0, head_dim = 0;
+  int pos0 = 0;
 };
 
 struct pbx_ctx {

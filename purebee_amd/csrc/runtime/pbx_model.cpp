@@ -1034,6 +1034,41 @@ static int launch_rows(pbx_model *m, const char *name, const pbx_weight *w, cons
   return PBX_OK;
 }
 
+// Row-batched GEMVs on int8 MFMAs (pbx_mr_q4_<RW>x<KS>b<IB>_<mode>, gemv_mr)
+// for 1..5 rows: RW 16-row weight tiles (8 gate + 8 up rows for gu) a
+// workgroup of RW x KS waves.  rope: q|k|v rows at positions start.. with
+// RoPE and the cache append (the KV caches of layer l).
+#define MR_MAX 5
+static int launch_mr(pbx_model *m, const char *name, const pbx_weight *w, const float *X,
+                     const float *normw, float *Y, int n, int RW, int KS, int rope_layer = -1,
+                     int start = 0, bool loop = false) {
+  hipFunction_t f = pbx_kernel_by_name(m->c, name);
+  if (!f) return pbx_fail(m->c, PBX_ELOAD, "model: kernel %s not found", name);
+  // the kernels take whole 64-block rows and whole 4-block steps a slice
+  if (w->type != PBX_TYPE_Q4_0 || w->B % 64 != 0 || w->B % (4 * KS) != 0 || n > MR_MAX)
+    return pbx_fail(m->c, PBX_EINVAL, "model: %s does not take this shape", name);
+  const bool pair = strstr(name, "_gu") != nullptr;
+  const int NO = pair ? (int)w->N / 2 : (int)w->N;
+  const int tiles = (NO + (pair ? 7 : 15)) / (pair ? 8 : 16);
+  pbx_gemv_args g{w->qs, w->d, X, nullptr, normw, nullptr, Y, nullptr, (int)w->N, (int)w->B,
+                  m->cfg.rms_eps, w->m, n};
+  if (rope_layer >= 0) {
+    const size_t layer_kv = (size_t)m->cfg.max_seq * m->kvdim;
+    g.rope = m->rope;
+    g.kcache = m->kcache + rope_layer * layer_kv;
+    g.vcache = m->vcache + rope_layer * layer_kv;
+    g.qdim = m->cfg.dim;
+    g.kvdim = m->kvdim;
+    g.head_dim = m->cfg.head_dim;
+    g.pos0 = start;
+  }
+  void *args[] = {&g};
+  int grid = (tiles + RW - 1) / RW;
+  if (loop) grid = std::min(grid, 2 * m->c->cu_count);  // tile loop: two workgroups a CU
+  return pbx_launch_fn(m->c, f, name, dim3((unsigned)grid), dim3(64 * RW * KS), args,
+                       m->c->stream);
+}
+
 // Skinny Q4_0 MFMA kernels (pbx_sk_q4_*) for up to 8 rows: Y[r] (+)= W .
 // (RMSNorm(X[r]) if normw) per row r < n, n <= 8.
 struct SkinnyArgsHost {
@@ -1238,7 +1273,15 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, i
   for (int l = 0; l < nl; ++l) {
     Layer &L = m->layers[l];
     float *kc = m->kcache + l * layer_kv, *vc = m->vcache + l * layer_kv;
-    if (rows_int) {
+    // 1..5 rows with head_dim <= 64: q|k|v on the MFMA rows kernel with RoPE
+    // and the cache append (no pbx_rope_append_rows)
+    const bool mr = rows_int && n <= MR_MAX && (int)L.wqkv->B == 64 && g.head_dim <= 64 &&
+                    g.head_dim % 2 == 0 && g.dim % 16 == 0 && m->kvdim % 16 == 0;
+    if (mr) {
+      if ((rc = launch_mr(m, "pbx_mr_q4_1x4b1_qkvr", L.wqkv, m->bx, L.attn_norm, m->bqkv, n, 1, 4,
+                          l, start)))
+        return rc;
+    } else if (rows_int) {
       if ((rc = launch_rows(m, "pbx_dk_q4_i8x2b1r8_qkv", L.wqkv, m->bx, L.attn_norm, m->bqkv, n,
                             8, 16, 0)))
         return rc;
@@ -1246,7 +1289,7 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, i
       if ((rc = rmsnorm_rows(m, m->bx, L.attn_norm, m->bxn, n))) return rc;
       if ((rc = linear_rows(m, L.wqkv, m->bxn, n, m->bqkv, false))) return rc;
     }
-    {
+    if (!mr) {
       float *qkv = m->bqkv, *rope = m->rope;
       int st = start, nh = g.n_heads, nkv = g.n_kv_heads, hd = g.head_dim;
       const float *part = nullptr;
@@ -1275,6 +1318,13 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, i
           rc = launch_k(m, "pbx_attention_rows", dim3(g.n_heads, n), dim3(256), args);
       }
       if (rc) return rc;
+    }
+    if (mr && (int)L.wd->B == 256) {
+      if ((rc = launch_mr(m, "pbx_mr_q4_1x4b1_add", L.wo, m->battn, nullptr, m->bx, n, 1, 4)) ||
+          (rc = launch_mr(m, "pbx_mr_q4_4x1b1_gu", L.wgu, m->bx, L.ffn_norm, m->bh, n, 4, 1)) ||
+          (rc = launch_mr(m, "pbx_mr_q4_1x8b4_add", L.wd, m->bh, nullptr, m->bx, n, 1, 8)))
+        return rc;
+      continue;
     }
     if (rows_int) {
       // RMSNorm + gate|up + SwiGLU on the skinny MFMA kernel (17 us against 19
@@ -1398,7 +1448,6 @@ extern "C" int pbx_model_forward_batch(pbx_model *m, const int32_t *tokens, int 
   if ((rc = batch_layers(m, tokens, n, start_pos, g.n_layers))) return rc;
   const pbx_weight *head = m->output ? m->output : m->embd;
   if (n <= ROWS_MAX && rows_int_ok(m)) {
-    // RMSNorm + LM head over the rows: a tile loop, one workgroup a CU
     // RMSNorm + LM head over the rows on the skinny MFMA kernel (66 us against
     // 91 for the integer-limb tile loop at 5 rows)
     if ((rc = launch_skinny(m, "pbx_sk_q4_store", head, m->bx, m->out_norm, m->blogits, n)))
