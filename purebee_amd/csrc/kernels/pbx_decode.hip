@@ -94,6 +94,8 @@ DK_MODES_SMALL(PBX_Q6K, q6k, 4)
 DK_INT_GU(PBX_Q4, q4, 8, 4, 1)
 DK_INT_GU(PBX_Q4, q4, 16, 4, 1)
 DK_INT_S(PBX_Q4, q4, 16, 4, 1, 0, 2, p2, PRO_RMSNORM, EPI_SWIGLU, gu)
+// after pbx_attention_o_*: the input is x + the pending update
+DK_INT_S(PBX_Q4, q4, 16, 4, 1, 0, 2, p2, PRO_RMSACC, EPI_SWIGLU, gua)
 DK_INT_GU(PBX_Q4, q4, 8, 4, 2)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 1)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 2)
@@ -108,6 +110,7 @@ DK_INT_ADD(PBX_Q4, q4, 4, 2, 1)
 DK_INT_ADD(PBX_Q4, q4, 4, 2, 2)
 DK_INT_ADD(PBX_Q4, q4, 4, 2, 4)
 DK_INT_S(PBX_Q4, q4, 4, 2, 4, 8, 2, w8, PRO_NONE, EPI_ADD, add)
+DK_INT_S(PBX_Q4, q4, 4, 2, 4, 8, 2, w8, PRO_NONE, EPI_ADDACC, adda)  // folds the update in
 DK_INT_S(PBX_Q4, q4, 4, 2, 4, 4, 2, w4, PRO_NONE, EPI_ADD, add)
 DK_INT_ADD(PBX_Q4, q4, 4, 1, 1)
 DK_INT_ADD(PBX_Q4, q4, 4, 1, 4)
@@ -224,6 +227,13 @@ struct AttnArgs {
   int n_heads, n_kv_heads, head_dim;
   float scale;         // 1/sqrt(head_dim)
   int max_seq;         // cache rows (pbx_attention_head_c)
+  // pbx_attention_o_*: the layer's o projection (Q4_0 planes: dim rows of
+  // dim / 32 blocks), the residual's pending update [dim] (2^-32 units) and
+  // the residual row (set to NaN where a head's product is not finite)
+  const uint8_t *oqs;
+  const uint16_t *odsc;
+  long long *oacc;
+  float *ox;
 };
 
 // One workgroup per query head (llama.js:258-301 / llama-streaming.js:543-573):
@@ -608,11 +618,44 @@ __device__ __forceinline__ void head_chunk_c(const float *kb, const float *vb, i
   head_fold<J, false>(k, v, s0, pl, nc, qq, m, l, acc);
 }
 
-template <bool SPEC>
+// Query head h and part s of workgroup column b (n_heads * parts columns).
+// Workgroups go to the 8 XCDs round robin (column b on XCD b % 8 while the
+// grid's x extent is a multiple of 8), each XCD with its own L2; with
+// n_heads a multiple of 8, XCD x takes the consecutive heads x * n_heads / 8
+// .. (all their parts), so the heads of a KV group share an L2 and their K/V
+// rows come from HBM once instead of once per head; so do the 128-byte
+// lines of the o projection that 4 adjacent heads read.
+__device__ __forceinline__ void xcd_head(int b, int n_heads, int &h, int &s) {
+  if (n_heads % 8) {
+    h = b % n_heads;
+    s = b / n_heads;
+  } else {
+    const int hpx = n_heads / 8, k = b / 8;
+    h = (b % 8) * hpx + k % hpx;
+    s = k / hpx;
+  }
+}
+
+// IPT > 0 (pbx_attention_o_*, head_dim 64, Q4_0 o projection): after the
+// head's attention output o_h, the workgroup multiplies it by the 64 columns
+// of W_o it meets (blocks 2h and 2h + 1 of every row) for its 256 * IPT
+// output rows [256 * IPT * s, ..) and adds each row's product into the
+// residual's pending update as a 2^-32 fixed-point integer (64-bit atomics:
+// integer addition is associative, so the sum of the n_heads products does
+// not depend on the order the workgroups reach it).  The gate|up GEMV reads
+// x + update as its input and the down GEMV folds the update into x.  A
+// product that is not finite or not below 2^26 in magnitude (the sum of 32
+// of them would leave the 64-bit range) sets the residual element to NaN.
+// The weight bytes are requested right after the first K/V slots, so they
+// stream in under the attention.
+template <bool SPEC, int IPT = 0>
 __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const int pos_arg) {
   __shared__ float st_m[PBX_HA_WAVES], st_l[PBX_HA_WAVES];
   __shared__ __attribute__((aligned(16))) float st_acc[PBX_HA_WAVES][PBX_HA_MAX_HD];
-  const int h = blockIdx.x, hd = a.head_dim, hd4 = hd / 4;
+  __shared__ float o_h[IPT > 0 ? 64 : 1], o_sum[2];
+  int h, part;
+  xcd_head(blockIdx.x, a.n_heads, h, part);
+  const int hd = a.head_dim, hd4 = hd / 4;
   const int Gq = a.n_heads / a.n_kv_heads, g = h / Gq;
   const int kvdim = a.n_kv_heads * hd;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -631,6 +674,20 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
       v0[j] = *reinterpret_cast<const float4 *>(vb + (size_t)min(32 * j + pl, a.max_seq - 1) * kvdim + dcol);
   }
   const float4 qv = *reinterpret_cast<const float4 *>(a.qkv + (size_t)h * hd + dcol);
+  // IPT > 0: the o projection's bytes of the workgroup's items (item j: row
+  // 256 * IPT * part + j / 2, block 2h + j % 2; thread t holds items t + 512 i)
+  uint4 wq[IPT > 0 ? IPT : 1];
+  unsigned wd[IPT > 0 ? IPT : 1];
+  if constexpr (IPT > 0) {
+    const int B = a.n_heads * 2;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+      const int it = tid + PBX_HA_WAVES * 64 * i;
+      const int row = 256 * IPT * part + (it >> 1), blk = 2 * h + (it & 1);
+      wq[i] = ld_stream(a.oqs + ((size_t)row * B + blk) * 16);
+      wd[i] = a.odsc[dsc_index(row, blk, B)];
+    }
+  }
   const int nc = (SPEC ? a.state[0] : pos_arg) + 1;  // positions 0..pos
   const float c = a.scale * 1.44269504088896340736f;  // scale * log2 e
   float4 qq = dg < hd4 ? make_float4(qv.x * c, qv.y * c, qv.z * c, qv.w * c)
@@ -690,7 +747,45 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
     for (int i = 0; i < PBX_HA_WAVES; ++i)
       num = fmaf(__shfl(e, i, 64), st_acc[i][lane], num);
     const float dn = __shfl(den, 0, 64);
-    if (lane < hd) a.out[(size_t)h * hd + lane] = num / dn;
+    if constexpr (IPT == 0) {
+      if (lane < hd) a.out[(size_t)h * hd + lane] = num / dn;
+    } else {
+      const float o = num / dn;  // head_dim 64: every lane
+      o_h[lane] = o;
+      const float sb = wave_sum<16>(o);  // lanes 0..31 and 32..63: the two blocks
+      if ((lane & 31) == 0) o_sum[lane >> 5] = sb;
+    }
+  }
+  if constexpr (IPT > 0) {
+    lds_barrier();
+    const int B = a.n_heads * 2;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+      const int it = tid + PBX_HA_WAVES * 64 * i;
+      const int row = 256 * IPT * part + (it >> 1), hb = it & 1;
+      const float *ov = o_h + 32 * hb;
+      // sum of q * o over the block (q: codes 0..15), then (sum - 8 sum o) d
+      const unsigned w4[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+      float t = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const unsigned lo = w4[j] & 0x0F0F0F0Fu, hi = (w4[j] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          t = fmaf((float)((lo >> (8 * k)) & 0xFFu), ov[4 * j + k], t);
+          t = fmaf((float)((hi >> (8 * k)) & 0xFFu), ov[16 + 4 * j + k], t);
+        }
+      }
+      float p = fmaf(-8.f, o_sum[hb], t) * f16_bits_to_f32(wd[i]);
+      p += __shfl_xor(p, 1, 64);  // the row's other block: the adjacent lane
+      if (hb == 0) {
+        if (fabsf(p) < 0x1p26f)
+          atomicAdd(reinterpret_cast<unsigned long long *>(a.oacc) + row,
+                    (unsigned long long)(long long)rintf(p * 0x1p32f));
+        else
+          a.ox[row] = __builtin_nanf("");
+      }
+    }
   }
 }
 
@@ -698,6 +793,18 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
 extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64) pbx_attention_head_c(AttnArgs a) {
   attention_cached_body<true>(a, 0);
 }
+
+// The same with the o projection fused (n_heads * dim / (256 * IPT)
+// workgroups; head_dim 64, Q4_0 o projection, dim a multiple of 256 * IPT).
+#define PBX_ATTN_O(IPT)                                                                     \
+  extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64)                           \
+      pbx_attention_o_c##IPT(AttnArgs a) {                                                  \
+    attention_cached_body<true, IPT>(a, 0);                                                 \
+  }
+PBX_ATTN_O(1)
+PBX_ATTN_O(2)
+PBX_ATTN_O(4)
+#undef PBX_ATTN_O
 
 // Batched rows (speculative verify, short batches; head_dim <= 64): workgroup
 // (head, row t) at position start + t, after pbx_rope_append_rows has rotated

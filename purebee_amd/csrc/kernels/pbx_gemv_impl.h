@@ -30,6 +30,10 @@
 #define PRO_NONE 0
 #define PRO_RMSNORM 1
 #define PRO_SWIGLU 2
+// RMSNorm of x + acc * 2^-32 (integer-limb kernel, one activation row): the
+// residual row plus the pending update the fused attention + o projection
+// accumulated as 2^-32 fixed-point integers
+#define PRO_RMSACC 3
 
 #define EPI_STORE 0
 #define EPI_ADD 1
@@ -42,6 +46,9 @@
 // llama.js:163-190), q stored to Y, k and v stored to the cache row of that
 // position (the attention then reads every position from the cache).
 #define EPI_ROPE 4
+// y = (y + acc * 2^-32) + W x, then acc = 0: the residual add that also folds
+// the pending update into the residual row (integer-limb kernel)
+#define EPI_ADDACC 5
 
 // Everything a fused GEMV launch needs; passed by value.
 struct GemvArgs {
@@ -65,11 +72,13 @@ struct GemvArgs {
   float *kcache, *vcache;
   int qdim, kvdim, head_dim;
   int pos0;             // EPI_ROPE with several activation rows: row m at pos0 + m
+  long long *acc;       // PRO_RMSACC / EPI_ADDACC: pending update [N] (2^-32 units)
 };
 
 namespace pbx {
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef long long i64x2_t __attribute__((ext_vector_type(2)));
 
 // 16-byte streaming load of weight bytes that are read once per matvec
 // (nontemporal: they should not displace the activations in the caches).
@@ -459,12 +468,23 @@ __device__ __forceinline__ float wave_transpose_reduce(float (&v)[R], int lane) 
   return wave_sum<(64 / R) / 2>(v[0]);
 }
 
+// x + q * 2^-32 rounded once: the residual row with its pending
+// fixed-point update (PRO_RMSACC and EPI_ADDACC form the same value).
+__device__ __forceinline__ float residual_acc(float x, long long q) {
+  return (float)fma((double)q, 0x1p-32, (double)x);
+}
+
 // Store of output row n; `res` is the residual y[n] read at kernel start
-// (EPI_ADD), so the epilogue does not wait on a second round trip.
+// (EPI_ADD), so the epilogue does not wait on a second round trip;
+// EPI_ADDACC: `racc` its pending update, cleared here.
 template <int EPI>
-__device__ __forceinline__ void epilogue_row(const GemvArgs &a, float *y, int n, float s, float res) {
+__device__ __forceinline__ void epilogue_row(const GemvArgs &a, float *y, int n, float s, float res,
+                                             long long racc = 0) {
   if constexpr (EPI == EPI_ADD) {
     y[n] = res + s;
+  } else if constexpr (EPI == EPI_ADDACC) {
+    y[n] = residual_acc(res, racc) + s;
+    a.acc[n] = 0;
   } else {
     y[n] = s + (a.bias ? a.bias[n] : 0.f);
   }
@@ -869,6 +889,10 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   static_assert(!LOOP || EPI == EPI_ARGMAX || EPI == EPI_STORE, "tile loop epilogues");
   static_assert(MR == 1 || EPI != EPI_ARGMAX, "argmax keys for one row");
   static_assert(EPI != EPI_ROPE || (MR == 1 && !LOOP && RT % 2 == 0), "RoPE rows in pairs");
+  static_assert(PRO != PRO_RMSACC || (MR == 1 && BW == 0 && !LOOP),
+                "pending update: one activation row, built by the row waves");
+  static_assert(EPI != EPI_ADDACC || (MR == 1 && !LOOP), "pending update: one activation row");
+  constexpr bool RMS = PRO == PRO_RMSNORM || PRO == PRO_RMSACC;
   constexpr int QB = BlockTraits<TYPE>::QB;
   constexpr int NV = QB / 16;
   constexpr bool PAIR = EPI == EPI_SWIGLU;
@@ -879,7 +903,9 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   // blocks a lane builds one after another (Q = 1 only).  With more than
   // four waves the blocks are not split: only wave 0 builds (MR = 1), its
   // activations requested first, while the others stream weight bytes.
-  constexpr int TB = T <= 256 ? T : 64;
+  // PRO_RMSACC also loads 8 bytes of pending update per element, so four
+  // waves share the build there (wave 0 alone would spill).
+  constexpr int TB = T <= 256 ? T : PRO == PRO_RMSACC ? 256 : 64;
   constexpr int Q = TB >= 8 * NB ? 8 : TB >= 4 * NB ? 4 : TB >= 2 * NB ? 2 : 1;
   constexpr int FPL = 8 / Q;
   constexpr int IT = (NB * Q + T - 1) / T;
@@ -893,7 +919,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   // RMSNorm: sums of x^2 of each 16-lane row of the builder waves, SSP per
   // activation row (a builder wave covers 64 / Q blocks of one row)
   constexpr int SSP = IB * Q * 4;
-  __shared__ float4 ssq[PRO == PRO_RMSNORM ? MR : 1][SSP / 4];
+  __shared__ float4 ssq[RMS ? MR : 1][SSP / 4];
   __shared__ uint64_t kred[WV];
   __shared__ float ssqb[BW > 0 ? BW : 1];  // BW > 0: sum of x^2 of each builder wave
 
@@ -981,6 +1007,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   //    issue order, so activations requested behind the weight stream would
   //    arrive only with it.  Loads are unconditional from clamped addresses.
   float4 xv[IT][FPL], nv[IT][FPL];
+  i64x2_t qv[PRO == PRO_RMSACC ? IT : 1][PRO == PRO_RMSACC ? 2 * FPL : 1];  // pending updates
   // whole waves hold segments or none (NB * Q is a multiple of 64); the
   // others skip the build: waiting for loads they do not need would hold
   // the barrier behind their weight bytes
@@ -997,7 +1024,12 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     for (int v = 0; v < FPL; ++v) {
       xv[it][v] = *reinterpret_cast<const float4 *>(xr + 4 * v);
       nv[it][v] = make_float4(1.f, 1.f, 1.f, 1.f);
-      if constexpr (PRO == PRO_RMSNORM) nv[it][v] = *reinterpret_cast<const float4 *>(wr + 4 * v);
+      if constexpr (RMS) nv[it][v] = *reinterpret_cast<const float4 *>(wr + 4 * v);
+    }
+    if constexpr (PRO == PRO_RMSACC) {
+      const long long *qr = a.acc + (ok ? (size_t)b * 32 + qd * FPL * 4 : 0);
+#pragma unroll
+      for (int v = 0; v < 2 * FPL; ++v) qv[it][v] = *reinterpret_cast<const i64x2_t *>(qr + 2 * v);
     }
   }
 
@@ -1008,14 +1040,17 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   //    compiler issues them back to back; nothing is computed from a loaded
   //    value before the weight bytes are requested.
   float res[MR];
+  long long racc = 0;  // EPI_ADDACC: the row's pending update
 #pragma unroll
   for (int m = 0; m < MR; ++m) res[m] = 0.f;
-  if constexpr (EPI == EPI_ADD) {
+  if constexpr (EPI == EPI_ADD || EPI == EPI_ADDACC) {
     const int r0 = rbase(blockIdx.x);
     const int rr = (lane % LPR) == 0 ? lane / LPR : RT;
 #pragma unroll
     for (int m = 0; m < MR; ++m)
       if (rr < RT && r0 + rr < N) res[m] = y[(size_t)(m < rows ? m : 0) * NO + r0 + rr];
+    if constexpr (EPI == EPI_ADDACC)
+      if (rr < RT && r0 + rr < N) racc = a.acc[r0 + rr];
   }
   // Q6_K: db holds the super-block's d, ex the lane's two int8 sub-block
   // scales (load_lane); both are used only in the dots.
@@ -1083,8 +1118,14 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     float mx = 0.f, nf = 0.f, sq = 0.f;
 #pragma unroll
     for (int v = 0; v < FPL; ++v) {
-      const float4 t = ok ? xv[it][v] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[it][v];
-      if constexpr (PRO == PRO_RMSNORM)
+      float4 t = ok ? xv[it][v] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 w = nv[it][v];
+      if constexpr (PRO == PRO_RMSACC) {
+        const i64x2_t q0 = qv[it][2 * v], q1 = qv[it][2 * v + 1];
+        t = make_float4(residual_acc(t.x, q0.x), residual_acc(t.y, q0.y), residual_acc(t.z, q1.x),
+                        residual_acc(t.w, q1.y));
+      }
+      if constexpr (RMS)
         sq = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, sq))));
       p[v] = make_float4(t.x * w.x, t.y * w.y, t.z * w.z, t.w * w.w);
       mx = fmaxf(mx, fmaxf(fmaxf(fabsf(p[v].x), fabsf(p[v].y)), fmaxf(fabsf(p[v].z), fabsf(p[v].w))));
@@ -1094,7 +1135,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
       mx = group_max<Q>(mx);
       nf = group_sum<Q>(nf);
     }
-    if constexpr (PRO == PRO_RMSNORM) {
+    if constexpr (RMS) {
       // sum over the 16-lane row (DPP only); lane 16r of the wave writes it
       sq = wave_sum<8>(ok ? sq : 0.f);
       if ((lane & 15) == 0) {
@@ -1158,7 +1199,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     inv[m] = 1.f;
-    if constexpr (PRO == PRO_RMSNORM) {
+    if constexpr (RMS) {
       float sm = 0.f;
       if constexpr (BW > 0) {
 #pragma unroll
@@ -1369,7 +1410,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
     if (n < N) {
 #pragma unroll
       for (int m = 0; m < MR; ++m)
-        if (m < rows) epilogue_row<EPI>(a, y + (size_t)m * NO, n, tot[m], res[m]);
+        if (m < rows) epilogue_row<EPI>(a, y + (size_t)m * NO, n, tot[m], res[m], racc);
       if constexpr (EPI == EPI_ARGMAX) key = argmax_key(tot[0], (unsigned)n);
     }
   }

@@ -81,6 +81,9 @@ struct pbx_gemv_args {
   float *kcache = nullptr, *vcache = nullptr;
   int qdim = 0, kvdim = 0, head_dim = 0;
   int pos0 = 0;
+  // the residual's pending update (2^-32 units) that the gate|up GEMV adds
+  // to its input and the down GEMV folds into the residual
+  long long *acc = nullptr;
 };
 
 struct pbx_ctx {

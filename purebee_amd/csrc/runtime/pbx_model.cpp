@@ -34,6 +34,11 @@ struct AttnArgsHost {  // AttnArgs in pbx_decode.hip
   int n_heads, n_kv_heads, head_dim;
   float scale;
   int max_seq;
+  // pbx_attention_o_*: o projection planes, pending update, residual row
+  const void *oqs = nullptr;
+  const void *odsc = nullptr;
+  long long *oacc = nullptr;
+  float *ox = nullptr;
 };
 
 struct AttnSplitArgsHost {  // AttnSplitArgs in pbx_decode.hip
@@ -80,6 +85,7 @@ struct Op {
   std::string name;
   std::string role;      // embed / qkv / attn / o / gate_up / down / lm_head / argmax
   double bytes = 0;      // algorithmic bytes per launch (attention: per cached position)
+  double fixed_bytes = 0;  // attention: bytes per launch on top (the fused o projection)
   dim3 grid, block;
   ArgKind kind;
   GemvArgsHost gemv;
@@ -135,6 +141,10 @@ struct pbx_model {
   unsigned global_mask = 0;
   float *kcache = nullptr, *vcache = nullptr, *rope = nullptr;
   float *x = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
+  // the residual's pending update [dim] (2^-32 fixed point) between the
+  // fused attention + o projection and the down GEMV of a layer; zero
+  // outside that span
+  long long *xacc = nullptr;
   uint64_t *partials = nullptr;
   int n_partials_cap = 0;
   bool gemv_int = true;  // integer-limb GEMV kernels where they apply
@@ -142,6 +152,9 @@ struct pbx_model {
   int attn_splits = 0;
   float *attn_part = nullptr;
   int attn_mode = 0;  // AttnMode
+  // rows of the o projection per workgroup / 256 in the fused attention +
+  // o projection (0: a separate o GEMV); PBX_ATTN_O=0|1|2|4 at creation
+  int attn_o_ipt = 1;
   int *state = nullptr;
   int *hist = nullptr;
   int hist_cap = 0;
@@ -335,8 +348,12 @@ static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const c
   op.kind = ARG_GEMV;
   std::string shape;
   int n_tiles = 0;
-  // qkvr (RoPE + cache append epilogue) is planned as qkv
-  const char *plan_mode = strcmp(mode, "qkvr") == 0 ? "qkv" : mode;
+  // qkvr (RoPE + cache append epilogue) is planned as qkv, gua (input x +
+  // pending update) as gu, adda (folds the update in) as add
+  const char *plan_mode = strcmp(mode, "qkvr") == 0 ? "qkv"
+                          : strcmp(mode, "gua") == 0 ? "gu"
+                          : strcmp(mode, "adda") == 0 ? "add"
+                                                      : mode;
   plan_gemv(c, m->gemv_int, plan_mode, role, w->type, (int)w->N, (int)w->B, &shape, &op.grid,
             &op.block, &n_tiles);
   if (w->B > 32 && (w->B + 63) / 64 > 8)
@@ -350,9 +367,13 @@ static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const c
   op.role = role;
   // weights + activation reads (+ up for SwiGLU, + norm weight) + output
   // (read and written for the residual epilogue)
+  // (+ the pending update: read by gua, read and cleared by adda)
   op.bytes = (double)w->N * pbx_type_row_bytes(w->type, w->K) + 4.0 * w->K * (X2 ? 2 : 1) +
              (normw ? 4.0 * w->K : 0.0) +
-             (strcmp(mode, "add") == 0 ? 8.0 * w->N : strcmp(mode, "gu") == 0 ? 2.0 * w->N : 4.0 * w->N);
+             (strcmp(plan_mode, "add") == 0 ? 8.0 * w->N
+              : strcmp(plan_mode, "gu") == 0 ? 2.0 * w->N
+                                             : 4.0 * w->N) +
+             (strcmp(mode, "gua") == 0 ? 8.0 * w->K : strcmp(mode, "adda") == 0 ? 16.0 * w->N : 0.0);
   if (n_tiles_out) *n_tiles_out = n_tiles;
   m->ops.push_back(op);
   return PBX_OK;
@@ -414,6 +435,33 @@ static int build_ops(pbx_model *m) {
   }
   hipFunction_t fheadc = pbx_kernel_by_name(c, "pbx_attention_head_c");
   if (cached && !fheadc) return pbx_fail(c, PBX_ELOAD, "model: kernel pbx_attention_head_c not found");
+  // The o projection fused into the cached attention (pbx_attention_o_c<IPT>,
+  // 256 * IPT output rows a workgroup): head_dim 64, Q4_0 o projection and
+  // gate|up / down GEMVs whose planned shapes have the pending-update
+  // variants (IPT from PBX_ATTN_O at model creation; 0 keeps the separate
+  // o GEMV).
+  int o_ipt = 0;
+  hipFunction_t fattno = nullptr;
+  if (cached && g.head_dim == 64 && m->layers[0].wo->type == PBX_TYPE_Q4_0 &&
+      m->layers[0].wo->B == 2 * g.n_heads) {
+    const int ipt = m->attn_o_ipt;
+    if ((ipt == 1 || ipt == 2 || ipt == 4) && g.dim % (256 * ipt) == 0) {
+      auto variant = [&](const pbx_weight *w, const char *plan_mode, const char *mode,
+                         const char *role) {
+        std::string shape;
+        dim3 gr, bl;
+        int nt;
+        plan_gemv(c, m->gemv_int, plan_mode, role, w->type, (int)w->N, (int)w->B, &shape, &gr,
+                  &bl, &nt);
+        return pbx_kernel_by_name(c, std::string("pbx_dk_") + type_tag(w->type) + "_" + shape +
+                                         "_" + mode) != nullptr;
+      };
+      fattno = pbx_kernel_by_name(c, "pbx_attention_o_c" + std::to_string(ipt));
+      if (fattno && variant(m->layers[0].wgu, "gu", "gua", "gate_up") &&
+          variant(m->layers[0].wd, "add", "adda", "down"))
+        o_ipt = ipt;
+    }
+  }
   for (int l = 0; l < g.n_layers; ++l) {
     Layer &L = m->layers[l];
     int rc;
@@ -435,7 +483,24 @@ static int build_ops(pbx_model *m) {
     a.role = "attn";
     a.bytes = 2.0 * 4.0 * m->kvdim;  // K and V of one cached position, all KV heads
     a.block = dim3(256);
-    if (cached) {
+    if (o_ipt) {
+      a.kind = ARG_ATTN;
+      a.name = "pbx_attention_o_c" + std::to_string(o_ipt);
+      a.f = fattno;
+      a.role = "attn_o";
+      a.grid = dim3(g.n_heads * (g.dim / (256 * o_ipt)));
+      a.block = dim3(512);
+      a.attn = AttnArgsHost{m->qkv, m->kcache + l * layer_kv, m->vcache + l * layer_kv, m->rope,
+                            m->attn, m->state, g.n_heads, g.n_kv_heads, g.head_dim,
+                            (float)(1.0 / sqrt((double)g.head_dim)), g.max_seq};
+      a.attn.oqs = L.wo->qs;
+      a.attn.odsc = L.wo->d;
+      a.attn.oacc = m->xacc;
+      a.attn.ox = m->x;
+      // the o projection's weights, its head outputs' update (read and written)
+      a.fixed_bytes = (double)L.wo->N * pbx_type_row_bytes(L.wo->type, L.wo->K) + 16.0 * g.dim;
+      m->ops.push_back(a);
+    } else if (cached) {
       a.kind = ARG_ATTN;
       a.name = "pbx_attention_head_c";
       a.f = fheadc;
@@ -485,6 +550,15 @@ static int build_ops(pbx_model *m) {
                             m->attn, m->state, g.n_heads, g.n_kv_heads, g.head_dim,
                             (float)(1.0 / sqrt((double)g.head_dim)), g.max_seq};
       m->ops.push_back(a);
+    }
+    if (o_ipt) {
+      if ((rc = add_gemv(m, L.wgu, "gua", "gate_up", m->x, nullptr, L.ffn_norm, m->gu, nullptr)))
+        return rc;
+      m->ops.back().gemv.acc = m->xacc;
+      if ((rc = add_gemv(m, L.wd, "adda", "down", m->gu, nullptr, nullptr, m->x, nullptr)))
+        return rc;
+      m->ops.back().gemv.acc = m->xacc;
+      continue;
     }
     if ((rc = add_gemv(m, L.wo, "add", "o", m->attn, nullptr, nullptr, m->x, nullptr))) return rc;
     if ((rc = add_gemv(m, L.wgu, "gu", "gate_up", m->x, nullptr, L.ffn_norm, m->gu, nullptr))) return rc;
@@ -681,7 +755,8 @@ static void model_release(pbx_model *m) {
   pbx_weight_release(m->embd);
   pbx_weight_release(m->output);
   for (void *p : {(void *)m->out_norm, (void *)m->kcache, (void *)m->vcache, (void *)m->rope,
-                  (void *)m->x, (void *)m->qkv, (void *)m->attn, (void *)m->gu, (void *)m->logits,
+                  (void *)m->x, (void *)m->xacc, (void *)m->qkv, (void *)m->attn, (void *)m->gu,
+                  (void *)m->logits,
                   (void *)m->partials, (void *)m->state, (void *)m->hist,
                   (void *)m->attn_part, m->head_lanes})
     if (p) hipFree(p);
@@ -782,6 +857,7 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
   if (!rc) rc = dalloc(m, (void **)&m->vcache, kv_bytes);
   if (!rc) rc = dalloc(m, (void **)&m->rope, (size_t)g.max_seq * g.head_dim * 4);
   if (!rc) rc = dalloc(m, (void **)&m->x, (size_t)g.dim * 4);
+  if (!rc) rc = dalloc(m, (void **)&m->xacc, (size_t)g.dim * 8);
   if (!rc) rc = dalloc(m, (void **)&m->qkv, (size_t)m->qkv_rows * 4);
   if (!rc) rc = dalloc(m, (void **)&m->attn, (size_t)g.dim * 4);
   if (!rc) rc = dalloc(m, (void **)&m->gu, (size_t)g.hidden_dim * 2 * 4);
@@ -795,6 +871,7 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
   // query heads per KV head): about 256 workgroups per layer, at most 64
   // splits, never more splits than positions.
   m->attn_mode = attention_mode(g);
+  if (const char *e = getenv("PBX_ATTN_O")) m->attn_o_ipt = atoi(e);
   if (!rc && m->attn_mode == ATTN_SPLIT) {
     m->attn_splits = std::min({64, g.max_seq, std::max(4, (256 + g.n_kv_heads - 1) / g.n_kv_heads)});
     rc = dalloc(m, (void **)&m->attn_part,
@@ -815,6 +892,7 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
         hipMemsetAsync(m->kcache, 0, kv_bytes, c->stream) != hipSuccess ||
         hipMemsetAsync(m->vcache, 0, kv_bytes, c->stream) != hipSuccess ||
         hipMemsetAsync(m->state, 0, 64, c->stream) != hipSuccess ||
+        hipMemsetAsync(m->xacc, 0, (size_t)g.dim * 8, c->stream) != hipSuccess ||
         hipStreamSynchronize(c->stream) != hipSuccess)
       rc = pbx_fail(c, PBX_EHIP, "pbx_model_create: initialisation copies failed");
   }
@@ -1622,6 +1700,7 @@ extern "C" int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int
       const Op &op = m->ops[i];
       bytes[i] += (op.kind == ARG_ATTN || op.kind == ARG_ATTN_SPLIT) ? op.bytes * (start_pos + s + 1)
                                                                       : op.bytes;
+      bytes[i] += op.fixed_bytes;
     }
   }
   if (!rc) {

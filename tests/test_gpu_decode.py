@@ -222,6 +222,44 @@ def test_attention_kernels_match_one_workgroup_per_head(ctx, monkeypatch, mode, 
     ref.close()
 
 
+@pytest.mark.parametrize("ipt", [1, 2, 4])
+def test_fused_attention_o_matches_separate_o(ctx, monkeypatch, ipt):
+    """Decode with the o projection fused into the cached head attention
+    (workgroup (head, part) adds W_o[rows, head] o_h for its 256 * ipt rows
+    into a 64-bit 2^-32 fixed-point update; the gate|up GEMV adds the update
+    to its input, the down GEMV folds it into the residual and clears it)
+    against the same model with the separate o GEMV and against the oracle,
+    over 100 positions (past the attention's two speculative 32-position
+    slots) on two layers."""
+    print(f"[case] fused attention + o, ipt {ipt}, 2048/8192, 32/8 heads, 100 positions",
+          flush=True)
+    cfg = tiny(TYPE_Q4_0, TYPE_Q4_0, dim=2048, hidden_dim=8192, n_layers=2, n_heads=32,
+               n_kv_heads=8, vocab_size=512, max_seq=256)
+    monkeypatch.setenv("PBX_ATTN_O", str(ipt))
+    fused, ref, cfg = make_pair(ctx, cfg, 101)
+    monkeypatch.setenv("PBX_ATTN_O", "0")
+    plain = synth.build(ctx, cfg, 101)
+    monkeypatch.delenv("PBX_ATTN_O")
+    toks = [int(t) for t in synth.random_tokens(102, 100, cfg["vocab_size"])]
+    worst = 0.0
+    for p, t in enumerate(toks):
+        a, _ = fused.forward([t], p)
+        b, _ = plain.forward([t], p)
+        worst = max(worst, float(np.abs(a - b).max()))
+    r = ref.forward(toks, 0)
+    err = float(np.abs(a - r).max())
+    kern = {k for _, k, _, _ in fused.profile(toks[-1], len(toks), 1)}
+    plain_kern = {k for _, k, _, _ in plain.profile(toks[-1], len(toks), 1)}
+    print(f"  fused vs separate max-abs {worst:.2e}, vs oracle {err:.2e}")
+    assert f"pbx_attention_o_c{ipt}" in kern and "pbx_dk_q4_i16x4b1p2_gua" in kern
+    assert "pbx_attention_head_c" in plain_kern
+    assert worst <= 1e-4
+    assert err <= LOGIT_TOL
+    fused.free()
+    plain.free()
+    ref.close()
+
+
 @pytest.mark.parametrize("wt,et,dim,hidden,vocab", [(TYPE_Q4_0, TYPE_Q4_0, 2048, 1024, 40000),
                                                     (TYPE_Q4_0, TYPE_Q6_K, 2048, 1024, 40000),
                                                     (TYPE_Q8_0, TYPE_Q8_0, 2048, 1024, 512),
