@@ -167,6 +167,13 @@ struct pbx_model {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   bool graph_tried = false, graph_ok = false;
+  // pbx_model_generate: graph_steps whole steps captured back to back in one
+  // graph (the steps chain through the device state), which saves the gap
+  // between graph launches; PBX_GRAPH_STEPS at creation (<= 1: off)
+  int graph_steps = 4;
+  hipGraph_t graph_k = nullptr;
+  hipGraphExec_t exec_k = nullptr;
+  bool graph_k_tried = false, graph_k_ok = false;
   // steps that stop after the first L < n_layers layers (forward with
   // maxLayers), one captured graph per L, made on first use
   struct PartGraph {
@@ -627,6 +634,11 @@ static void drop_graph(pbx_model *m) {
   m->exec = nullptr;
   m->graph = nullptr;
   m->graph_tried = m->graph_ok = false;
+  if (m->exec_k) hipGraphExecDestroy(m->exec_k);
+  if (m->graph_k) hipGraphDestroy(m->graph_k);
+  m->exec_k = nullptr;
+  m->graph_k = nullptr;
+  m->graph_k_tried = m->graph_k_ok = false;
   for (auto &p : m->part) {
     if (p.exec) hipGraphExecDestroy(p.exec);
     if (p.graph) hipGraphDestroy(p.graph);
@@ -653,11 +665,13 @@ static int enqueue_ops_layers(pbx_model *m, int L) {
 
 // Captures the step of the first L layers into a graph (false: capture
 // failed, the caller launches kernel by kernel).
-static bool capture_step(pbx_model *m, int L, hipGraph_t *graph, hipGraphExec_t *exec) {
+static bool capture_step(pbx_model *m, int L, hipGraph_t *graph, hipGraphExec_t *exec,
+                         int steps = 1) {
   bool ok = false;
   hipStream_t s = m->c->stream;
   if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-    int rc = enqueue_ops_layers(m, L);
+    int rc = PBX_OK;
+    for (int i = 0; i < steps && !rc; ++i) rc = enqueue_ops_layers(m, L);
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(s, &g);
     if (!rc && e == hipSuccess && g && hipGraphInstantiate(exec, g, nullptr, nullptr, 0) == hipSuccess) {
@@ -703,6 +717,29 @@ static int run_step_layers(pbx_model *m, int L) {
 }
 
 static int run_step(pbx_model *m) { return run_step_layers(m, m->cfg.n_layers); }
+
+// Up to `left` whole decode steps: graph_steps of them in one graph launch
+// when that graph is available, else one step.  *done: the steps enqueued.
+static int run_steps(pbx_model *m, int left, int *done) {
+  *done = 1;
+  if (m->graph_steps > 1 && left >= m->graph_steps && use_graphs()) {
+    if (!m->ops_ready) {
+      int rc = build_ops(m);
+      if (rc) return rc;
+    }
+    if (!m->graph_k_tried) {
+      m->graph_k_tried = true;
+      m->graph_k_ok = capture_step(m, m->cfg.n_layers, &m->graph_k, &m->exec_k, m->graph_steps);
+    }
+    if (m->graph_k_ok) {
+      if (hipGraphLaunch(m->exec_k, m->c->stream) != hipSuccess)
+        return pbx_fail(m->c, PBX_EHIP, "model: hipGraphLaunch failed");
+      *done = m->graph_steps;
+      return PBX_OK;
+    }
+  }
+  return run_step(m);
+}
 
 // Device state for a host-driven step; with `embed`, also the token's
 // embedding row into x (a step's argmax embeds the token it picks).
@@ -872,6 +909,7 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
   // splits, never more splits than positions.
   m->attn_mode = attention_mode(g);
   if (const char *e = getenv("PBX_ATTN_O")) m->attn_o_ipt = atoi(e);
+  if (const char *e = getenv("PBX_GRAPH_STEPS")) m->graph_steps = atoi(e);
   if (!rc && m->attn_mode == ATTN_SPLIT) {
     m->attn_splits = std::min({64, g.max_seq, std::max(4, (256 + g.n_kv_heads - 1) / g.n_kv_heads)});
     rc = dalloc(m, (void **)&m->attn_part,
@@ -1575,8 +1613,8 @@ extern "C" int pbx_model_generate(pbx_model *m, int32_t token, int start_pos, in
   if (hipSetDevice(c->device) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_generate: hipSetDevice failed");
   if ((rc = set_state(m, start_pos, token, 0, true))) return rc;
-  for (int i = 0; i < n_steps; ++i)
-    if ((rc = run_step(m))) return rc;
+  for (int i = 0, k = 0; i < n_steps; i += k)
+    if ((rc = run_steps(m, n_steps - i, &k))) return rc;
   if (hipMemcpyAsync(out_tokens, m->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost,
                      c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_generate: token copy failed");
