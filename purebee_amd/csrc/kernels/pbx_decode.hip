@@ -186,6 +186,14 @@ DK_INT_ROWS(PBX_Q4, q4, 8, 1, 4, 5, false, , PRO_NONE, EPI_ADD, add)  // LDS: 5 
 MR_K(1, 4, 1, PRO_RMSNORM, EPI_ROPE, qkvr)
 MR_K(1, 4, 1, PRO_NONE, EPI_ADD, add)
 MR_K(4, 1, 1, PRO_RMSNORM, EPI_SWIGLU, gu)
+// down with the K blocks split over XS workgroups (grid y): pbx_mr_q4_<RW>x<KS>b<IB>s<XS>_add
+#define MR_KX(RW, KS, IB, XS, PRO, EPI, MN)                                                  \
+  extern "C" __global__ void __launch_bounds__(RW * KS * 64)                                \
+      __attribute__((amdgpu_waves_per_eu(1, 1)))                                             \
+      pbx_mr_q4_##RW##x##KS##b##IB##s##XS##_##MN(GemvArgs a) {                               \
+    gemv_mr<RW, KS, IB, PRO, EPI, 5, false, XS>(a);                                          \
+  }
+MR_KX(4, 1, 4, 8, PRO_NONE, EPI_ADD, add)
 MR_K(1, 8, 4, PRO_NONE, EPI_ADD, add)
 
 DK_MODES_WIDE(PBX_F32, f32, 2)

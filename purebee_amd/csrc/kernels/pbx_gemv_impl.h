@@ -73,6 +73,9 @@ struct GemvArgs {
   int qdim, kvdim, head_dim;
   int pos0;             // EPI_ROPE with several activation rows: row m at pos0 + m
   long long *acc;       // PRO_RMSACC / EPI_ADDACC: pending update [N] (2^-32 units)
+  // gemv_mr with the K split over workgroups: one cell per output element
+  // [MR][N] (zero between launches)
+  unsigned long long *xcell;
 };
 
 namespace pbx {
@@ -1428,6 +1431,41 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
 }
 
 
+// The cross-workgroup combine of gemv_mr with XS > 1: every slice adds its
+// sum of an output element into the element's 64-bit cell (bits 0..55: the
+// sum of the slices' 2^-32 fixed-point values, each biased by 2^51 so the
+// field stays non-negative; bits 56..59: slices arrived; bits 60..63:
+// slices whose sum was not finite or not below 2^19 in magnitude).  The add
+// that brings the count to XS returns the whole sum: that lane stores
+// residual + sum (NaN when a slice was poisoned) and clears the cell.  One
+// atomic carries value and count, so no fence is needed, and integer
+// addition makes the result independent of the arrival order.
+template <int XS, int MR>
+__device__ __forceinline__ void mr_combine(const GemvArgs &a, bool has, int mcol, int n0,
+                                           const float (&acc)[4], const float (&res)[4]) {
+  static_assert(XS < 16, "4-bit counts");
+  if (!has) return;
+  const int N = a.N;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = n0 + i;
+    if (n >= N) continue;
+    const float p = acc[i];
+    const bool bad = !(fabsf(p) < 0x1p19f);
+    const unsigned long long c =
+        (1ull << 56) + (bad ? (1ull << 60) + (1ull << 51)
+                            : (unsigned long long)((1ll << 51) + (long long)rintf(p * 0x1p32f)));
+    unsigned long long *cell = a.xcell + (size_t)mcol * N + n;
+    const unsigned long long t =
+        __hip_atomic_fetch_add(cell, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + c;
+    if (((t >> 56) & 15u) != (unsigned)XS) continue;
+    __hip_atomic_store(cell, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const long long v = (long long)(t & ((1ull << 56) - 1)) - (long long)XS * (1ll << 51);
+    a.Y[(size_t)mcol * N + n] =
+        (t >> 60) ? __builtin_nanf("") : (float)fma((double)v, 0x1p-32, (double)res[i]);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Row-batched GEMV on int8 MFMAs: up to MR = 5 activation rows against one
 // pass over Q4_0 weights (K = 2048..8192), for the speculative verify and
@@ -1460,28 +1498,34 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
 // next tile's weights requested while one is multiplied.
 // EPI_ROPE: rows of q|k|v at positions pos0 + m (RoPE of q and k, k and v
 // written to the cache rows, q to Y).
+// XS > 1 (EPI_ADD): the K blocks are split over XS workgroups (blockIdx.y),
+// so a workgroup builds and reads only its slice of the activation rows
+// (they dominate a CU's bytes at K = 8192); the slices meet in mr_combine.
 // ---------------------------------------------------------------------------
 typedef int pbx_v4i __attribute__((ext_vector_type(4)));
 
-template <int RW, int KS, int IB, int PRO, int EPI, int MR, bool LOOP = false>
+template <int RW, int KS, int IB, int PRO, int EPI, int MR, bool LOOP = false, int XS = 1>
 __device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
   static_assert(MR >= 1 && 3 * MR <= 15, "three limb columns a row, 16 columns");
   static_assert(EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_SWIGLU || EPI == EPI_ROPE,
                 "epilogues");
   static_assert(!LOOP || (KS == 1 && EPI == EPI_STORE), "tile loop: one slice, stored rows");
-  static_assert((IB * 64) % (4 * KS) == 0, "whole 4-block steps a slice");
+  static_assert(XS == 1 || (EPI == EPI_ADD && PRO == PRO_NONE && !LOOP),
+                "K split over workgroups: residual add epilogue");
+  static_assert((IB * 64) % XS == 0 && (IB * 64 / XS) % (4 * KS) == 0, "whole 4-block steps a slice");
   constexpr int WV = RW * KS, T = WV * 64;
-  constexpr int NB = IB * 64;  // blocks a row (past B: unused)
+  constexpr int NB = IB * 64 / XS;  // blocks of the workgroup's K slice (past B: unused)
   constexpr bool PAIR = EPI == EPI_SWIGLU;
-  // lanes per (row, block) segment in the build and float4s each covers
-  constexpr int NSEG = MR * NB;
+  // build segments: a block of every activation row, Q lanes each (the
+  // block's RMSNorm weights are read once for all rows)
+  constexpr int NSEG = NB;
   // 8 lanes a block: each wave reads 1 KB contiguous per activation load
   // (one lane a block reads 64 cache lines per instruction, several times
   // slower for these sizes)
   constexpr int Q = 8;
   constexpr int FPL = 8 / Q;
   constexpr int IT = (NSEG * Q + T - 1) / T;
-  constexpr int CH = NB * Q / 64;       // wave-chunks a row (one row each)
+  constexpr int CH = NB * Q / 64;       // wave-chunks of the blocks
   constexpr int BSM = (NB + KS - 1) / KS;  // blocks a slice at most
   constexpr int NQ = (BSM + 3) / 4;        // 4-block loads a slice
   constexpr int NSC = (BSM + 31) / 32;     // 16-byte scale loads a lane
@@ -1494,7 +1538,10 @@ __device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
   __shared__ float4 wst_red[WV * 64 * NSLOT > RED ? WV * 64 * NSLOT : RED];
   __shared__ __attribute__((aligned(16))) uint2 wsc[WV][4][NSC * 32];  // row group, block
 
-  const int N = a.N, B = a.B, K = B * 32;
+  // BR blocks a weight row; B blocks (K activations) in this workgroup's
+  // K slice, starting at block gb0
+  const int N = a.N, BR = a.B, KR = BR * 32, B = BR / XS, K = B * 32;
+  const int gb0 = XS > 1 ? (int)blockIdx.y * B : 0;
   const int lane = threadIdx.x & 63, tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rw = wave % RW, ks = wave / RW;
@@ -1511,20 +1558,26 @@ __device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
   // the wave's K slice
   const int BS = (B + KS - 1) / KS, b0 = ks * BS, b1 = min(B, b0 + BS);
 
-  // 1. activation segments (row m, block b; Q lanes each), requested first
-  float4 xv[IT][FPL], nv[IT][FPL];
+  // 1. activation segments (block b of every row; Q lanes each), requested first
+  float4 xv[IT][MR][FPL], nv[IT][FPL];
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     const int sg = tid + T * it;
-    const int gb = sg / Q, m = gb / NB, b = gb % NB, qd = sg % Q;
-    const bool ok = m < rows && b < B;
-    const float *xr = a.X + (ok ? (size_t)m * K + (size_t)b * 32 + qd * FPL * 4 : 0);
-    const float *wr = a.normw + (ok ? (size_t)b * 32 + qd * FPL * 4 : 0);
+    const int b = sg / Q, qd = sg % Q;
+    if (b >= NB) continue;  // wave-uniform: whole waves hold segments or none
+    const bool okb = b < B;
+    const float *wr = a.normw + (okb ? (size_t)(gb0 + b) * 32 + qd * FPL * 4 : 0);
 #pragma unroll
     for (int v = 0; v < FPL; ++v) {
-      xv[it][v] = *reinterpret_cast<const float4 *>(xr + 4 * v);
       nv[it][v] = make_float4(1.f, 1.f, 1.f, 1.f);
       if constexpr (PRO == PRO_RMSNORM) nv[it][v] = *reinterpret_cast<const float4 *>(wr + 4 * v);
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const bool ok = m < rows && okb;
+      const float *xr = a.X + (ok ? (size_t)m * KR + (size_t)(gb0 + b) * 32 + qd * FPL * 4 : 0);
+#pragma unroll
+      for (int v = 0; v < FPL; ++v) xv[it][m][v] = *reinterpret_cast<const float4 *>(xr + 4 * v);
     }
   }
   // 2. the first tile's residuals (EPI_ADD), row scales and weights
@@ -1553,7 +1606,8 @@ __device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
     for (int sgi = 0; sgi < NSC; ++sgi) {
       const int b = b0 + 32 * sgi + 2 * col;  // even: the pair lies inside B
       // a vector load (a struct copy would go through private memory)
-      const u32x4_t v = *reinterpret_cast<const u32x4_t *>(a.dsc + dsc_index(rd, b + 1 < b1 ? b : b0, B));
+      const u32x4_t v =
+          *reinterpret_cast<const u32x4_t *>(a.dsc + dsc_index(rd, gb0 + (b + 1 < b1 ? b : b0), BR));
       wd[sgi] = make_uint4(v.x, v.y, v.z, v.w);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1561,7 +1615,7 @@ __device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int b = b0 + 4 * q + g;
-      wq[q] = ld_stream(a.qs + ((size_t)ra * B + (b < b1 ? b : b0)) * 16);
+      wq[q] = ld_stream(a.qs + ((size_t)ra * BR + gb0 + (b < b1 ? b : b0)) * 16);
     }
   };
   uint4 wdA[NSC], wdB[NSC];
@@ -1573,16 +1627,18 @@ __device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
 
   // 3. build: fixed point of each segment into the B operand slots
 #pragma unroll
-  for (int it = 0; it < IT; ++it) {
+  for (int it = 0; it < IT; ++it)
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
     const int sg = tid + T * it;
-    const int gb = sg / Q, m = gb / NB, b = gb % NB, qd = sg % Q;
-    if (m >= MR) continue;  // wave-uniform: whole waves hold segments or none
+    const int b = sg / Q, qd = sg % Q;
+    if (b >= NB) continue;  // wave-uniform
     const bool ok = m < rows && b < B;
     float4 p[FPL];
     float mx = 0.f, nf = 0.f, sq = 0.f;
 #pragma unroll
     for (int v = 0; v < FPL; ++v) {
-      const float4 x = ok ? xv[it][v] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[it][v];
+      const float4 x = ok ? xv[it][m][v] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[it][v];
       if constexpr (PRO == PRO_RMSNORM)
         sq = fmaf(x.x, x.x, fmaf(x.y, x.y, fmaf(x.z, x.z, fmaf(x.w, x.w, sq))));
       p[v] = make_float4(x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w);
@@ -1594,8 +1650,8 @@ __device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
       nf = group_sum<Q>(nf);
     }
     if constexpr (PRO == PRO_RMSNORM) {
-      sq = wave_sum(sq);  // the wave-chunk lies in one activation row
-      if (lane == 0) ssq[m][((tid + T * it) / 64) % CH] = sq;
+      sq = wave_sum(sq);  // row m over the wave's 8 blocks
+      if (lane == 0) ssq[m][(tid + T * it) / 64] = sq;
     }
     int e = 0;
     if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
@@ -1754,6 +1810,10 @@ __device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
   }
   const int r0 = tile_r0(t0);
   if (t0 >= n_tiles) return;
+  if constexpr (XS > 1) {
+    mr_combine<XS, MR>(a, lcol == 0 && mcol < rows, mcol, r0 + 4 * g, acc, res);
+    return;
+  }
   if constexpr (PAIR) {
     // tile rows 0..7 (lane groups 0, 1) are gate rows, 8..15 their up rows
     float up[4];
@@ -1802,6 +1862,7 @@ __device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
     if (n < N) a.Y[(size_t)mcol * NO + n] = EPI == EPI_ADD ? res[i] + acc[i] : acc[i];
   }
 }
+
 
 }  // namespace pbx
 

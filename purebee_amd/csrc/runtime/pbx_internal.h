@@ -84,6 +84,9 @@ struct pbx_gemv_args {
   // the residual's pending update (2^-32 units) that the gate|up GEMV adds
   // to its input and the down GEMV folds into the residual
   long long *acc = nullptr;
+  // rows GEMV with the K blocks split over workgroups: one 64-bit cell per
+  // output element (zero between launches)
+  unsigned long long *xcell = nullptr;
 };
 
 struct pbx_ctx {

@@ -190,6 +190,9 @@ struct pbx_model {
         *bh = nullptr, *btmp = nullptr, *blogits = nullptr;
   int *btok = nullptr, *bnext = nullptr;
   uint64_t *bkeys = nullptr;  // [logits_cap][64] partial argmax keys
+  // rows GEMV with the K blocks split over workgroups (the down projection):
+  // a 64-bit cell per output element [MR_MAX][dim] (zero between launches)
+  unsigned long long *mr_cell = nullptr;
   // fused batched layers: the fp16 activation pair of the next GEMM and the
   // split-K partials of the last one
   void *g16 = nullptr, *g16lo = nullptr;
@@ -799,7 +802,8 @@ static void model_release(pbx_model *m) {
     if (p) hipFree(p);
   for (void *p : {(void *)m->bx, (void *)m->bxn, (void *)m->bqkv, (void *)m->battn,
                   (void *)m->bgu, (void *)m->bh, (void *)m->btmp, (void *)m->blogits,
-                  (void *)m->btok, (void *)m->bnext, (void *)m->bkeys, m->g16, m->g16lo,
+                  (void *)m->btok, (void *)m->bnext, (void *)m->bkeys, (void *)m->mr_cell,
+                  m->g16, m->g16lo,
                   (void *)m->ginv, (void *)m->gpart})
     if (p) hipFree(p);
   m->magic = 0;
@@ -1061,9 +1065,17 @@ static int grow(pbx_model *m, void **p, size_t bytes) {
   return PBX_OK;
 }
 
+#define MR_MAX 5
+#define MR_XS 15  // K slices of the split rows GEMV at most (4-bit counts)
+
 static int ensure_batch(pbx_model *m, int rows, bool all_logits) {
   const pbx_model_config &g = m->cfg;
   int rc = PBX_OK;
+  if (!m->mr_cell) {
+    if ((rc = grow(m, (void **)&m->mr_cell, (size_t)MR_MAX * g.dim * 8))) return rc;
+    if (hipMemsetAsync(m->mr_cell, 0, (size_t)MR_MAX * g.dim * 8, m->c->stream) != hipSuccess)
+      return pbx_fail(m->c, PBX_EHIP, "model: clearing the split cells failed");
+  }
   if (rows > m->batch_cap) {
     const size_t R = (size_t)rows;
     const size_t tmp_cols = std::max({(size_t)g.dim, (size_t)m->qkv_rows, 2 * (size_t)g.hidden_dim});
@@ -1150,18 +1162,20 @@ static int launch_rows(pbx_model *m, const char *name, const pbx_weight *w, cons
   return PBX_OK;
 }
 
-// Row-batched GEMVs on int8 MFMAs (pbx_mr_q4_<RW>x<KS>b<IB>_<mode>, gemv_mr)
-// for 1..5 rows: RW 16-row weight tiles (8 gate + 8 up rows for gu) a
-// workgroup of RW x KS waves.  rope: q|k|v rows at positions start.. with
-// RoPE and the cache append (the KV caches of layer l).
-#define MR_MAX 5
+// Row-batched GEMVs on int8 MFMAs (pbx_mr_q4_<RW>x<KS>b<IB>[s<XS>]_<mode>,
+// gemv_mr) for 1..5 rows: RW 16-row weight tiles (8 gate + 8 up rows for gu)
+// a workgroup of RW x KS waves; XS > 1: the K blocks split over XS
+// workgroups (grid y, residual add only).  rope: q|k|v rows at positions
+// start.. with RoPE and the cache append (the KV caches of layer l).
 static int launch_mr(pbx_model *m, const char *name, const pbx_weight *w, const float *X,
                      const float *normw, float *Y, int n, int RW, int KS, int rope_layer = -1,
-                     int start = 0, bool loop = false) {
+                     int start = 0, bool loop = false, int XS = 1) {
   hipFunction_t f = pbx_kernel_by_name(m->c, name);
   if (!f) return pbx_fail(m->c, PBX_ELOAD, "model: kernel %s not found", name);
-  // the kernels take whole 64-block rows and whole 4-block steps a slice
-  if (w->type != PBX_TYPE_Q4_0 || w->B % 64 != 0 || w->B % (4 * KS) != 0 || n > MR_MAX)
+  // the kernels take whole 64-block rows and whole 4-block steps a slice;
+  // the split kernel's scratch holds MR_XS slices of dim rows
+  if (w->type != PBX_TYPE_Q4_0 || w->B % 64 != 0 || w->B % (4 * KS * XS) != 0 || n > MR_MAX ||
+      (XS > 1 && (XS > MR_XS || w->N > m->cfg.dim || !m->mr_cell)))
     return pbx_fail(m->c, PBX_EINVAL, "model: %s does not take this shape", name);
   const bool pair = strstr(name, "_gu") != nullptr;
   const int NO = pair ? (int)w->N / 2 : (int)w->N;
@@ -1178,11 +1192,12 @@ static int launch_mr(pbx_model *m, const char *name, const pbx_weight *w, const 
     g.head_dim = m->cfg.head_dim;
     g.pos0 = start;
   }
+  g.xcell = m->mr_cell;
   void *args[] = {&g};
   int grid = (tiles + RW - 1) / RW;
   if (loop) grid = std::min(grid, 2 * m->c->cu_count);  // tile loop: two workgroups a CU
-  return pbx_launch_fn(m->c, f, name, dim3((unsigned)grid), dim3(64 * RW * KS), args,
-                       m->c->stream);
+  return pbx_launch_fn(m->c, f, name, dim3((unsigned)grid, (unsigned)XS), dim3(64 * RW * KS),
+                       args, m->c->stream);
 }
 
 // Skinny Q4_0 MFMA kernels (pbx_sk_q4_*) for up to 8 rows: Y[r] (+)= W .
@@ -1438,7 +1453,8 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, i
     if (mr && (int)L.wd->B == 256) {
       if ((rc = launch_mr(m, "pbx_mr_q4_1x4b1_add", L.wo, m->battn, nullptr, m->bx, n, 1, 4)) ||
           (rc = launch_mr(m, "pbx_mr_q4_4x1b1_gu", L.wgu, m->bx, L.ffn_norm, m->bh, n, 4, 1)) ||
-          (rc = launch_mr(m, "pbx_mr_q4_1x8b4_add", L.wd, m->bh, nullptr, m->bx, n, 1, 8)))
+          (rc = launch_mr(m, "pbx_mr_q4_4x1b4s8_add", L.wd, m->bh, nullptr, m->bx, n, 4, 1, -1, 0,
+                          false, 8)))
         return rc;
       continue;
     }
