@@ -174,9 +174,10 @@ DK_INT_ROWS(PBX_Q4, q4, 8, 1, 4, 5, false, , PRO_NONE, EPI_ADD, add)  // LDS: 5 
 
 // Row-batched GEMVs on int8 MFMAs for 1..5 activation rows (gemv_mr):
 // pbx_mr_q4_<RW>x<KS>b<IB>_<mode>, RW 16-row tiles x KS K slices a workgroup.
-// One workgroup a CU is the plan (LDS), so a lane may hold up to 512
-// registers: the weight requests then never wait for registers that an
-// earlier load still has to fill.
+// One workgroup a CU is the plan (LDS), so a lane may hold as many
+// registers as the wave count allows: the weight requests then never wait
+// for registers that an earlier load still has to fill.  The verify uses
+// q|k|v 1x8, o 1x8 and gate|up 4x4; the other shapes are tuning options.
 #define MR_K(RW, KS, IB, PRO, EPI, MN)                                                       \
   extern "C" __global__ void __launch_bounds__(RW * KS * 64)                                \
       __attribute__((amdgpu_waves_per_eu(1, 1)))                                             \
@@ -186,7 +187,14 @@ DK_INT_ROWS(PBX_Q4, q4, 8, 1, 4, 5, false, , PRO_NONE, EPI_ADD, add)  // LDS: 5 
 MR_K(1, 4, 1, PRO_RMSNORM, EPI_ROPE, qkvr)
 MR_K(1, 4, 1, PRO_NONE, EPI_ADD, add)
 MR_K(4, 1, 1, PRO_RMSNORM, EPI_SWIGLU, gu)
-// down with the K blocks split over XS workgroups (grid y): pbx_mr_q4_<RW>x<KS>b<IB>s<XS>_add
+MR_K(4, 2, 1, PRO_RMSNORM, EPI_SWIGLU, gu)
+MR_K(1, 8, 1, PRO_RMSNORM, EPI_ROPE, qkvr)
+MR_K(1, 8, 1, PRO_NONE, EPI_ADD, add)
+MR_K(4, 4, 1, PRO_RMSNORM, EPI_SWIGLU, gu)
+MR_K(1, 16, 1, PRO_RMSNORM, EPI_ROPE, qkvr)
+MR_K(1, 16, 1, PRO_NONE, EPI_ADD, add)
+// down with the K blocks split over XS workgroups (grid y):
+// pbx_mr_q4_<RW>x<KS>b<IB>s<XS>_add (the verify uses 4x4b4s8)
 #define MR_KX(RW, KS, IB, XS, PRO, EPI, MN)                                                  \
   extern "C" __global__ void __launch_bounds__(RW * KS * 64)                                \
       __attribute__((amdgpu_waves_per_eu(1, 1)))                                             \
@@ -194,7 +202,8 @@ MR_K(4, 1, 1, PRO_RMSNORM, EPI_SWIGLU, gu)
     gemv_mr<RW, KS, IB, PRO, EPI, 5, false, XS>(a);                                          \
   }
 MR_KX(4, 1, 4, 8, PRO_NONE, EPI_ADD, add)
-MR_K(1, 8, 4, PRO_NONE, EPI_ADD, add)
+MR_KX(4, 2, 4, 8, PRO_NONE, EPI_ADD, add)
+MR_KX(4, 4, 4, 8, PRO_NONE, EPI_ADD, add)
 
 DK_MODES_WIDE(PBX_F32, f32, 2)
 DK_MODES_WIDE(PBX_F32, f32, 4)

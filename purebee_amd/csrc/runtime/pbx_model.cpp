@@ -1167,6 +1167,27 @@ static int launch_rows(pbx_model *m, const char *name, const pbx_weight *w, cons
 // a workgroup of RW x KS waves; XS > 1: the K blocks split over XS
 // workgroups (grid y, residual add only).  rope: q|k|v rows at positions
 // start.. with RoPE and the cache append (the KV caches of layer l).
+// Rows-kernel shape of a role (IB 64-block groups a row, K split over XS
+// workgroups); for tuning, PBX_MR_SHAPES="role=RWxKS,..." (roles qkv, o,
+// gate_up, down) picks another compiled shape.
+struct MrShape {
+  int rw, ks, ib, xs;
+  std::string name(const char *mode) const {
+    return "pbx_mr_q4_" + std::to_string(rw) + "x" + std::to_string(ks) + "b" +
+           std::to_string(ib) + (xs > 1 ? "s" + std::to_string(xs) : "") + "_" + mode;
+  }
+};
+static MrShape mr_shape(const char *role, int rw, int ks, int ib = 1, int xs = 1) {
+  MrShape sh{rw, ks, ib, xs};
+  const char *e = getenv("PBX_MR_SHAPES");
+  if (!e) return sh;
+  const std::string s(e), key = std::string(role) + "=";
+  const size_t p = s.find(key);
+  if (p != std::string::npos && (p == 0 || s[p - 1] == ','))
+    sscanf(s.c_str() + p + key.size(), "%dx%d", &sh.rw, &sh.ks);
+  return sh;
+}
+
 static int launch_mr(pbx_model *m, const char *name, const pbx_weight *w, const float *X,
                      const float *normw, float *Y, int n, int RW, int KS, int rope_layer = -1,
                      int start = 0, bool loop = false, int XS = 1) {
@@ -1409,8 +1430,9 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, i
     const bool mr = rows_int && n <= MR_MAX && (int)L.wqkv->B == 64 && g.head_dim <= 64 &&
                     g.head_dim % 2 == 0 && g.dim % 16 == 0 && m->kvdim % 16 == 0;
     if (mr) {
-      if ((rc = launch_mr(m, "pbx_mr_q4_1x4b1_qkvr", L.wqkv, m->bx, L.attn_norm, m->bqkv, n, 1, 4,
-                          l, start)))
+      const MrShape qs = mr_shape("qkv", 1, 8);
+      if ((rc = launch_mr(m, qs.name("qkvr").c_str(), L.wqkv, m->bx, L.attn_norm, m->bqkv, n,
+                          qs.rw, qs.ks, l, start)))
         return rc;
     } else if (rows_int) {
       if ((rc = launch_rows(m, "pbx_dk_q4_i8x2b1r8_qkv", L.wqkv, m->bx, L.attn_norm, m->bqkv, n,
@@ -1451,10 +1473,17 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, i
       if (rc) return rc;
     }
     if (mr && (int)L.wd->B == 256) {
-      if ((rc = launch_mr(m, "pbx_mr_q4_1x4b1_add", L.wo, m->battn, nullptr, m->bx, n, 1, 4)) ||
-          (rc = launch_mr(m, "pbx_mr_q4_4x1b1_gu", L.wgu, m->bx, L.ffn_norm, m->bh, n, 4, 1)) ||
-          (rc = launch_mr(m, "pbx_mr_q4_4x1b4s8_add", L.wd, m->bh, nullptr, m->bx, n, 4, 1, -1, 0,
-                          false, 8)))
+      // 8 or 16 waves a workgroup (K slices across waves): the dots of a wave
+      // wait on LDS round trips, so more waves hide them (verify M=5: 4 waves
+      // 0.757 ms, these 0.673)
+      const MrShape os = mr_shape("o", 1, 8), gs = mr_shape("gate_up", 4, 4),
+                    ds = mr_shape("down", 4, 4, 4, 8);
+      if ((rc = launch_mr(m, os.name("add").c_str(), L.wo, m->battn, nullptr, m->bx, n, os.rw,
+                          os.ks)) ||
+          (rc = launch_mr(m, gs.name("gu").c_str(), L.wgu, m->bx, L.ffn_norm, m->bh, n, gs.rw,
+                          gs.ks)) ||
+          (rc = launch_mr(m, ds.name("add").c_str(), L.wd, m->bh, nullptr, m->bx, n, ds.rw, ds.ks,
+                          -1, 0, false, ds.xs)))
         return rc;
       continue;
     }
