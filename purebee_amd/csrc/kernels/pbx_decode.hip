@@ -177,7 +177,8 @@ DK_INT_ROWS(PBX_Q4, q4, 8, 1, 4, 5, false, , PRO_NONE, EPI_ADD, add)  // LDS: 5 
 // One workgroup a CU is the plan (LDS), so a lane may hold as many
 // registers as the wave count allows: the weight requests then never wait
 // for registers that an earlier load still has to fill.  The verify uses
-// q|k|v 1x8, o 1x8 and gate|up 4x4; the other shapes are tuning options.
+// q|k|v 1x8, o 1x8, gate|up 4x4 and the LM head 8x1; the other shapes are
+// tuning options.
 #define MR_K(RW, KS, IB, PRO, EPI, MN)                                                       \
   extern "C" __global__ void __launch_bounds__(RW * KS * 64)                                \
       __attribute__((amdgpu_waves_per_eu(1, 1)))                                             \
@@ -193,6 +194,9 @@ MR_K(1, 8, 1, PRO_NONE, EPI_ADD, add)
 MR_K(4, 4, 1, PRO_RMSNORM, EPI_SWIGLU, gu)
 MR_K(1, 16, 1, PRO_RMSNORM, EPI_ROPE, qkvr)
 MR_K(1, 16, 1, PRO_NONE, EPI_ADD, add)
+// the verify's LM head (RMSNorm + logits of every row): 8x1, several workgroups a CU
+MR_K(8, 1, 1, PRO_RMSNORM, EPI_STORE, store)
+MR_K(4, 2, 1, PRO_RMSNORM, EPI_STORE, store)
 // down with the K blocks split over XS workgroups (grid y):
 // pbx_mr_q4_<RW>x<KS>b<IB>s<XS>_add (the verify uses 4x4b4s8)
 #define MR_KX(RW, KS, IB, XS, PRO, EPI, MN)                                                  \

@@ -1609,9 +1609,16 @@ extern "C" int pbx_model_forward_batch(pbx_model *m, const int32_t *tokens, int 
   if ((rc = batch_layers(m, tokens, n, start_pos, g.n_layers))) return rc;
   const pbx_weight *head = m->output ? m->output : m->embd;
   if (n <= ROWS_MAX && rows_int_ok(m)) {
-    // RMSNorm + LM head over the rows on the skinny MFMA kernel (66 us against
-    // 91 for the integer-limb tile loop at 5 rows)
-    if ((rc = launch_skinny(m, "pbx_sk_q4_store", head, m->bx, m->out_norm, m->blogits, n)))
+    // RMSNorm + LM head over the rows: a Q4_0 head at K = 2048 on the rows
+    // kernel, 8 tiles a workgroup (5 rows: 46 us against 64 on the skinny
+    // MFMA kernel, which takes the other heads)
+    const bool mr_head = head->type == PBX_TYPE_Q4_0 && head->B == 64 && n <= MR_MAX;
+    if (mr_head) {
+      const MrShape hs = mr_shape("lm_head", 8, 1);
+      if ((rc = launch_mr(m, hs.name("store").c_str(), head, m->bx, m->out_norm, m->blogits, n,
+                          hs.rw, hs.ks)))
+        return rc;
+    } else if ((rc = launch_skinny(m, "pbx_sk_q4_store", head, m->bx, m->out_norm, m->blogits, n)))
       return rc;
   } else {
     if ((rc = rmsnorm_rows(m, m->bx, m->out_norm, m->bxn, n))) return rc;
