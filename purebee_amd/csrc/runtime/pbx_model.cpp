@@ -189,6 +189,11 @@ struct pbx_model {
   float *bx = nullptr, *bxn = nullptr, *bqkv = nullptr, *battn = nullptr, *bgu = nullptr,
         *bh = nullptr, *btmp = nullptr, *blogits = nullptr;
   int *btok = nullptr, *bnext = nullptr;
+  // pinned staging of the rows' tokens and next tokens (batch_cap each): the
+  // uploads and read-backs of a verify are then asynchronous copies;
+  // tok_ev marks the last upload out of h_tok
+  int32_t *h_tok = nullptr, *h_next = nullptr;
+  hipEvent_t tok_ev = nullptr;
   uint64_t *bkeys = nullptr;  // [logits_cap][64] partial argmax keys
   // rows GEMV with the K blocks split over workgroups (the down projection):
   // a 64-bit cell per output element [MR_MAX][dim] (zero between launches)
@@ -794,6 +799,10 @@ static void model_release(pbx_model *m) {
   }
   pbx_weight_release(m->embd);
   pbx_weight_release(m->output);
+  if (m->tok_ev) hipEventSynchronize(m->tok_ev);
+  if (m->h_tok) hipHostFree(m->h_tok);
+  if (m->h_next) hipHostFree(m->h_next);
+  if (m->tok_ev) hipEventDestroy(m->tok_ev);
   for (void *p : {(void *)m->out_norm, (void *)m->kcache, (void *)m->vcache, (void *)m->rope,
                   (void *)m->x, (void *)m->xacc, (void *)m->qkv, (void *)m->attn, (void *)m->gu,
                   (void *)m->logits,
@@ -1089,6 +1098,17 @@ static int ensure_batch(pbx_model *m, int rows, bool all_logits) {
     if (!rc) rc = grow(m, (void **)&m->btmp, R * tmp_cols * 4);
     if (!rc) rc = grow(m, (void **)&m->btok, R * 4);
     if (!rc) rc = grow(m, (void **)&m->bnext, R * 4);
+    if (!rc && !m->tok_ev && hipEventCreateWithFlags(&m->tok_ev, hipEventDisableTiming) != hipSuccess)
+      rc = pbx_fail(m->c, PBX_EHIP, "model: event creation failed");
+    if (!rc) {
+      hipEventSynchronize(m->tok_ev);
+      if (m->h_tok) hipHostFree(m->h_tok);
+      if (m->h_next) hipHostFree(m->h_next);
+      m->h_tok = m->h_next = nullptr;
+      if (hipHostMalloc((void **)&m->h_tok, R * 4) != hipSuccess ||
+          hipHostMalloc((void **)&m->h_next, R * 4) != hipSuccess)
+        rc = pbx_fail(m->c, PBX_ENOMEM, "model: pinned token buffers failed");
+    }
     if (rc) {
       m->batch_cap = 0;
       return rc;
@@ -1347,7 +1367,13 @@ static int fused_residual_norm(pbx_model *m, const pbx_gemm_plan *p, int M, int 
 static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, int nl) {
   pbx_ctx *c = m->c;
   const pbx_model_config &g = m->cfg;
-  if (hipMemcpyAsync(m->btok, tokens, (size_t)n * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess)
+  // through the pinned buffer (once the previous upload out of it is done)
+  if (hipEventSynchronize(m->tok_ev) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "model: token staging wait failed");
+  memcpy(m->h_tok, tokens, (size_t)n * 4);
+  if (hipMemcpyAsync(m->btok, m->h_tok, (size_t)n * 4, hipMemcpyHostToDevice, c->stream) !=
+          hipSuccess ||
+      hipEventRecord(m->tok_ev, c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "model: token upload failed");
   int rc;
   {
@@ -1640,11 +1666,12 @@ extern "C" int pbx_model_forward_batch(pbx_model *m, const int32_t *tokens, int 
   if (logits && hipMemcpyAsync(logits, m->blogits, (size_t)n * g.vocab_size * 4,
                                hipMemcpyDeviceToHost, c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward_batch: logits copy failed");
-  if (next_tokens && hipMemcpyAsync(next_tokens, m->bnext, (size_t)n * 4, hipMemcpyDeviceToHost,
+  if (next_tokens && hipMemcpyAsync(m->h_next, m->bnext, (size_t)n * 4, hipMemcpyDeviceToHost,
                                     c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward_batch: token copy failed");
   if (hipStreamSynchronize(c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward_batch: forward failed on the device");
+  if (next_tokens) memcpy(next_tokens, m->h_next, (size_t)n * 4);
   return PBX_OK;
 }
 
