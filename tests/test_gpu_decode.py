@@ -260,6 +260,58 @@ def test_fused_attention_o_matches_separate_o(ctx, monkeypatch, ipt):
     ref.close()
 
 
+def test_non_finite_activation_propagates(ctx):
+    """A token whose embedding row holds a Q4_0 block with a +inf scale: the
+    reference's activations for it are then +-inf and NaN (inf * 0 for the
+    block's zero codes), so its logits and those of every later position
+    (whose attention reads its K/V) are NaN (llama.js:204-371).  The decode
+    step must give NaN there, through the attention with the o projection
+    fused (a non-finite product sets the residual element to NaN instead of
+    entering the fixed-point update), and so must the 5-row verify, through
+    the down projection split over K slices (a non-finite slice marks its
+    cell); the rows before the poisoned one stay finite and at the logit
+    tolerance."""
+    print("[case] non-finite embedding: decode step and 5-row verify", flush=True)
+    from purebee_amd.native import T_TOKEN_EMBD
+    cfg = tiny(TYPE_Q4_0, TYPE_Q4_0, dim=2048, hidden_dim=8192, n_layers=2, n_heads=32,
+               n_kv_heads=8, vocab_size=512, max_seq=64)
+    bad = 7
+    spec = synth.tensor_specs(cfg)[0]
+    assert spec[0] == T_TOKEN_EMBD
+    emb = np.array(synth.make_tensor(spec, 103, 0), np.uint8, copy=True)
+    row_bytes = (cfg["dim"] // 32) * 18
+    emb[bad * row_bytes: bad * row_bytes + 2] = np.frombuffer(np.uint16(0x7C00).tobytes(), np.uint8)
+    emb_f = oracle.dequant(TYPE_Q4_0, emb, cfg["vocab_size"] * cfg["dim"])
+    assert np.isinf(emb_f[bad * cfg["dim"]: (bad + 1) * cfg["dim"]]).any()
+    toks = [1, 2, bad, 3, 4]
+    for mode in ("decode", "verify"):
+        model, ref, cfg = make_pair(ctx, cfg, 103)
+        model.set_tensor(T_TOKEN_EMBD, -1, emb)
+        ref.set(T_TOKEN_EMBD, -1, emb_f)
+        r = [ref.forward([t], p) for p, t in enumerate(toks)]
+        if mode == "decode":
+            g = [model.forward([t], p)[0] for p, t in enumerate(toks)]
+        else:
+            lg, _ = model.forward_batch(toks, 0)
+            g = list(lg)
+        for p in range(len(toks)):
+            if p < 2:
+                # the LM head is the tied embedding: the poisoned token's own
+                # logit is non-finite in every row, the others are finite
+                keep = np.arange(cfg["vocab_size"]) != bad
+                assert not np.isfinite(r[p][bad]) and not np.isfinite(g[p][bad]), f"{mode} {p}"
+                assert np.isfinite(r[p][keep]).all(), f"oracle row {p}"
+                assert np.isfinite(g[p][keep]).all(), f"{mode} row {p}"
+                err = float(np.abs(g[p][keep] - r[p][keep]).max())
+                assert err <= LOGIT_TOL, f"{mode} row {p}: {err:.2e}"
+            else:
+                assert np.isnan(r[p]).all(), f"oracle row {p}"
+                assert np.isnan(g[p]).all(), f"{mode} row {p}: {np.isfinite(g[p]).sum()} finite"
+        print(f"  {mode}: rows 0-1 finite, rows 2-4 NaN")
+        model.free()
+        ref.close()
+
+
 @pytest.mark.parametrize("wt,et,dim,hidden,vocab", [(TYPE_Q4_0, TYPE_Q4_0, 2048, 1024, 40000),
                                                     (TYPE_Q4_0, TYPE_Q6_K, 2048, 1024, 40000),
                                                     (TYPE_Q8_0, TYPE_Q8_0, 2048, 1024, 512),
