@@ -160,13 +160,15 @@ def test_llama1b_verify_rows_equal_sequential(ctx):
 
 
 def test_row_batched_kernels_vs_oracle(ctx):
-    """The up-to-8-row verify kernels (skinny MFMA gate|up + SwiGLU and LM
-    head, integer-limb rows GEMVs for q|k|v, o and down, batched-row
-    attention) run for Q4_0 models with dim <= 2048, 6144 < hidden <= 8192
-    and a Q4_0 head.  A one-layer model of that shape with a small
-    vocabulary, after a 40-token prompt: forward_batch of n = 1, 5 and 8
-    rows, every row's logits against the oracle's forward at the same
-    position (llama.js:204-371, teacher-forced on the same tokens)."""
+    """The up-to-8-row verify kernels run for Q4_0 models with dim <= 2048,
+    6144 < hidden <= 8192 and a Q4_0 head: for 1..5 rows the int8-MFMA rows
+    kernels (q|k|v with RoPE and the cache append, o, gate|up + SwiGLU, down
+    split over K slices, the LM head) and the batched-row attention; for 6..8
+    rows the integer-limb rows GEMVs and the skinny MFMA kernels.  A
+    one-layer model of that shape with a small vocabulary, after a 40-token
+    prompt: forward_batch of n = 1, 5 and 8 rows, every row's logits against
+    the oracle's forward at the same position (llama.js:204-371,
+    teacher-forced on the same tokens)."""
     print("[case] 1-layer dim 2048 / hidden 8192 Q4_0 rows kernels vs oracle", flush=True)
     cfg = dict(dim=2048, hidden_dim=8192, n_layers=1, n_heads=32, n_kv_heads=8, vocab_size=4096,
                max_seq=128, weight_type=TYPE_Q4_0, embed_type=TYPE_Q4_0, rope_theta=500000.0)
