@@ -255,6 +255,10 @@ struct AttnArgs {
   const uint16_t *odsc;
   long long *oacc;
   float *ox;
+  // pbx_qkvr_attn_o_*: the q|k|v rows published by the same launch's GEMV
+  // workgroups ([qdim | kv_dim | kv_dim] cells, the epoch at [cell_n])
+  const unsigned long long *cells;
+  int cell_n, qdim;
 };
 
 // One workgroup per query head (llama.js:258-301 / llama-streaming.js:543-573):
@@ -639,6 +643,32 @@ __device__ __forceinline__ void head_chunk_c(const float *kb, const float *vb, i
   head_fold<J, false>(k, v, s0, pl, nc, qq, m, l, acc);
 }
 
+// The same while the newest position nc - 1 is still being written: its
+// cache row is requested like the others, and its k and v (kn, vn: the
+// lane's dims) replace the loaded ones.  `ready` runs between the requests
+// and the arithmetic (the fused kernel waits there for q, kn and vn).
+template <int J, class Ready>
+__device__ __forceinline__ void head_chunk_n(const float *kb, const float *vb, int kvdim, int dcol,
+                                             int s0, int pl, int nc, Ready &&ready,
+                                             const float4 &qq, const float4 &kn, const float4 &vn,
+                                             float &m, float &l, float4 &acc) {
+  float4 k[J], v[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    k[j] = *reinterpret_cast<const float4 *>(kb + (size_t)min(32 * (s0 + j) + pl, nc - 1) * kvdim + dcol);
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    v[j] = *reinterpret_cast<const float4 *>(vb + (size_t)min(32 * (s0 + j) + pl, nc - 1) * kvdim + dcol);
+  ready();
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    if (32 * (s0 + j) + pl == nc - 1) {
+      k[j] = kn;
+      v[j] = vn;
+    }
+  head_fold<J, false>(k, v, s0, pl, nc, qq, m, l, acc);
+}
+
 // Query head h and part s of workgroup column b (n_heads * parts columns).
 // Workgroups go to the 8 XCDs round robin (column b on XCD b % 8 while the
 // grid's x extent is a multiple of 8), each XCD with its own L2; with
@@ -669,13 +699,37 @@ __device__ __forceinline__ void xcd_head(int b, int n_heads, int &h, int &s) {
 // of them would leave the 64-bit range) sets the residual element to NaN.
 // The weight bytes are requested right after the first K/V slots, so they
 // stream in under the attention.
-template <bool SPEC, int IPT = 0>
-__device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const int pos_arg) {
+//
+// FUSED (pbx_qkvr_attn_o_*, after the q|k|v GEMV workgroups of the same
+// launch, workgroup column bid): q of the head and k, v of the newest
+// position are still being computed.  The workgroup requests every cached
+// position (the newest row too, whose loaded values it discards) and the o
+// projection's bytes, then three waves wait for the 3 x 64 published cells
+// (value bits tagged with the layer's epoch + 1; a cell that has not
+// arrived after PBX_CELL_SPIN polls gives NaN) and pass them on through LDS.
+#define PBX_CELL_SPIN (1 << 16)
+// Polls a published cell until it carries `tag` (NaN after PBX_CELL_SPIN
+// polls).  One load at a time: three in flight, one every ~200 ns, made the
+// decode step slower (353.3 against 349.0 us a token).
+__device__ __forceinline__ float poll_cell(const unsigned long long *cp, unsigned tag) {
+  unsigned long long v = __hip_atomic_load(cp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int it = 0; (unsigned)(v >> 32) != tag && it < PBX_CELL_SPIN; ++it) {
+    __builtin_amdgcn_s_sleep(1);
+    v = __hip_atomic_load(cp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return (unsigned)(v >> 32) == tag ? __uint_as_float((unsigned)v) : __builtin_nanf("");
+}
+
+template <bool SPEC, int IPT = 0, bool FUSED = false>
+__device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const int pos_arg,
+                                                      const int bid = -1) {
+  static_assert(!FUSED || (SPEC && IPT > 0), "fused: device position, head_dim 64");
   __shared__ float st_m[PBX_HA_WAVES], st_l[PBX_HA_WAVES];
   __shared__ __attribute__((aligned(16))) float st_acc[PBX_HA_WAVES][PBX_HA_MAX_HD];
   __shared__ float o_h[IPT > 0 ? 64 : 1], o_sum[2];
+  __shared__ __attribute__((aligned(16))) float nrow[FUSED ? 3 : 1][FUSED ? 64 : 4];
   int h, part;
-  xcd_head(blockIdx.x, a.n_heads, h, part);
+  xcd_head(bid < 0 ? (int)blockIdx.x : bid, a.n_heads, h, part);
   const int hd = a.head_dim, hd4 = hd / 4;
   const int Gq = a.n_heads / a.n_kv_heads, g = h / Gq;
   const int kvdim = a.n_kv_heads * hd;
@@ -686,7 +740,8 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
   const float *kb = a.kcache + (size_t)g * hd, *vb = a.vcache + (size_t)g * hd;
 
   float4 k0[SPEC ? PBX_HC_SPEC : 1], v0[SPEC ? PBX_HC_SPEC : 1];
-  if constexpr (SPEC) {
+  const int fpos = FUSED ? a.state[0] : 0;  // first: the requests below need it
+  if constexpr (SPEC && !FUSED) {
 #pragma unroll
     for (int j = 0; j < PBX_HC_SPEC; ++j)
       k0[j] = *reinterpret_cast<const float4 *>(kb + (size_t)min(32 * j + pl, a.max_seq - 1) * kvdim + dcol);
@@ -694,7 +749,8 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
     for (int j = 0; j < PBX_HC_SPEC; ++j)
       v0[j] = *reinterpret_cast<const float4 *>(vb + (size_t)min(32 * j + pl, a.max_seq - 1) * kvdim + dcol);
   }
-  const float4 qv = *reinterpret_cast<const float4 *>(a.qkv + (size_t)h * hd + dcol);
+  const float4 qv = FUSED ? make_float4(0.f, 0.f, 0.f, 0.f)
+                          : *reinterpret_cast<const float4 *>(a.qkv + (size_t)h * hd + dcol);
   // IPT > 0: the o projection's bytes of the workgroup's items (item j: row
   // 256 * IPT * part + j / 2, block 2h + j % 2; thread t holds items t + 512 i)
   uint4 wq[IPT > 0 ? IPT : 1];
@@ -709,7 +765,7 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
       wd[i] = a.odsc[dsc_index(row, blk, B)];
     }
   }
-  const int nc = (SPEC ? a.state[0] : pos_arg) + 1;  // positions 0..pos
+  const int nc = (FUSED ? fpos : SPEC ? a.state[0] : pos_arg) + 1;  // positions 0..pos
   const float c = a.scale * 1.44269504088896340736f;  // scale * log2 e
   float4 qq = dg < hd4 ? make_float4(qv.x * c, qv.y * c, qv.z * c, qv.w * c)
                        : make_float4(0.f, 0.f, 0.f, 0.f);  // repeats of the last dims
@@ -717,11 +773,47 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
   float m = -INFINITY, l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   int s0 = 0;
-  if constexpr (SPEC) {
+  if constexpr (FUSED) {
+    const unsigned tag = (unsigned)a.cells[a.cell_n] + 1u;
+    float4 kn = make_float4(0.f, 0.f, 0.f, 0.f), vn = kn;
+    auto ready = [&]() {
+      if (w < 3) {  // wave 0: q of head h; 1, 2: k, v of KV head g
+        nrow[w][lane] =
+            poll_cell(a.cells + (w == 0 ? h * hd : a.qdim + (w - 1) * kvdim + g * hd) + lane, tag);
+      }
+      lds_barrier();
+      const float4 q4 = *reinterpret_cast<const float4 *>(&nrow[0][dcol]);
+      qq = make_float4(q4.x * c, q4.y * c, q4.z * c, q4.w * c);
+      kn = *reinterpret_cast<const float4 *>(&nrow[1][dcol]);
+      vn = *reinterpret_cast<const float4 *>(&nrow[2][dcol]);
+    };
+    auto none = [] {};
+    bool first = true;
+    while (32 * s0 < nc) {
+      const int J = min(16, (nc - 32 * s0 + 31) / 32);
+      switch (J) {
+#define PBX_HEAD_CHUNK_N(n)                                                                \
+  case n:                                                                                  \
+    if (first)                                                                             \
+      head_chunk_n<n>(kb, vb, kvdim, dcol, s0, pl, nc, ready, qq, kn, vn, m, l, acc);      \
+    else                                                                                   \
+      head_chunk_n<n>(kb, vb, kvdim, dcol, s0, pl, nc, none, qq, kn, vn, m, l, acc);       \
+    break;
+        PBX_HEAD_CHUNK_N(1) PBX_HEAD_CHUNK_N(2) PBX_HEAD_CHUNK_N(3) PBX_HEAD_CHUNK_N(4)
+        PBX_HEAD_CHUNK_N(5) PBX_HEAD_CHUNK_N(6) PBX_HEAD_CHUNK_N(7) PBX_HEAD_CHUNK_N(8)
+        PBX_HEAD_CHUNK_N(9) PBX_HEAD_CHUNK_N(10) PBX_HEAD_CHUNK_N(11) PBX_HEAD_CHUNK_N(12)
+        PBX_HEAD_CHUNK_N(13) PBX_HEAD_CHUNK_N(14) PBX_HEAD_CHUNK_N(15) PBX_HEAD_CHUNK_N(16)
+#undef PBX_HEAD_CHUNK_N
+        default: break;
+      }
+      first = false;
+      s0 += J;
+    }
+  } else if constexpr (SPEC) {
     head_fold<PBX_HC_SPEC, true>(k0, v0, 0, pl, nc, qq, m, l, acc);
     s0 = PBX_HC_SPEC;
   }
-  while (32 * s0 < nc) {
+  while (!FUSED && 32 * s0 < nc) {
     const int J = min(16, (nc - 32 * s0 + 31) / 32);
     switch (J) {
 #define PBX_HEAD_CHUNK_C(n) \
@@ -826,6 +918,30 @@ PBX_ATTN_O(1)
 PBX_ATTN_O(2)
 PBX_ATTN_O(4)
 #undef PBX_ATTN_O
+
+// RMSNorm + q|k|v GEMV + RoPE + cache append (workgroups 0..np-1: 4 row
+// waves of RT rows and 4 builder waves, Q4_0, K = 32 * 64) and the attention
+// with the o projection (workgroups np.., as pbx_attention_o_c<IPT>) in one
+// launch: the GEMV publishes q, k and v row by row, and each attention
+// workgroup waits only for the 192 values of its head.  The GEMV
+// workgroups come first in the grid, so every XCD dispatches them before
+// any attention workgroup and none of them waits: the grid always drains.
+// np must be a multiple of 8 (the attention's XCD placement).  A CU holds
+// one of these workgroups (their registers), so the attention workgroups
+// request their K/V rows while the GEMV runs only where the grid fits the
+// CUs: Llama-3.2-1B's 96 GEMV (RT 8) + 128 attention (IPT 2) workgroups.
+#define PBX_QKVR_ATTN_O(WV, RT, BW, SUF, IPT)                                               \
+  extern "C" __global__ void __launch_bounds__(PBX_HA_WAVES * 64)                           \
+      pbx_qkvr_attn_o_r##RT##SUF##c##IPT(GemvArgs g, AttnArgs a, int np) {                  \
+    static_assert(WV + BW == PBX_HA_WAVES, "one workgroup size");                           \
+    if ((int)blockIdx.x < np)                                                               \
+      gemv_int<PBX_Q4, WV, RT, 1, PRO_RMSNORM, EPI_ROPE, false, 1, BW, RT>(g);              \
+    else                                                                                    \
+      attention_cached_body<true, IPT, true>(a, 0, (int)blockIdx.x - np);                   \
+  }
+PBX_QKVR_ATTN_O(4, 4, 4, , 1)
+PBX_QKVR_ATTN_O(4, 8, 4, , 2)
+#undef PBX_QKVR_ATTN_O
 
 // Batched rows (speculative verify, short batches; head_dim <= 64): workgroup
 // (head, row t) at position start + t, after pbx_rope_append_rows has rotated

@@ -74,7 +74,9 @@ struct GemvArgs {
   int pos0;             // EPI_ROPE with several activation rows: row m at pos0 + m
   long long *acc;       // PRO_RMSACC / EPI_ADDACC: pending update [N] (2^-32 units)
   // gemv_mr with the K split over workgroups: one cell per output element
-  // [MR][N] (zero between launches)
+  // [MR][N] (zero between launches).  gemv_int EPI_ROPE: N published rows
+  // and the layer's epoch at [N] (the fused q|k|v + attention kernel);
+  // EPI_ADDACC: that epoch, advanced once per launch
   unsigned long long *xcell;
 };
 
@@ -948,6 +950,15 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   const float *X = a.X + (size_t)blockIdx.y * MR * K;
   float *y = a.Y + (size_t)blockIdx.y * MR * NO;
   const int pos = EPI == EPI_ROPE ? a.state[0] : 0;
+  // EPI_ROPE with a.xcell: every output row is also published as a 64-bit
+  // cell, (epoch + 1) << 32 | value bits, by a relaxed device-scope store,
+  // for the attention workgroups of the same launch (no fence: each cell
+  // carries its own epoch, so no ordering between cells is needed)
+  unsigned pub_tag = 0;
+  if constexpr (EPI == EPI_ROPE)
+    if (a.xcell) pub_tag = (unsigned)a.xcell[N] + 1u;
+  if constexpr (EPI == EPI_ADDACC)
+    if (a.xcell && blockIdx.x == 0 && threadIdx.x == 0) a.xcell[0] += 1;
 
   if constexpr (BW > 0) {
     if (wave < 0) {
@@ -1390,8 +1401,14 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
         const float o = (n & 1) ? fmaf(pt, rp.y, t * rp.x) : fmaf(t, rp.x, -pt * rp.y);
         if (n < a.qdim) y[n] = o;
         else a.kcache[(size_t)pos * a.kvdim + (n - a.qdim)] = o;
+        if (pub_tag)
+          __hip_atomic_store(a.xcell + n, (unsigned long long)pub_tag << 32 | __float_as_uint(o),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       } else if (n < N) {
         a.vcache[(size_t)pos * a.kvdim + (n - a.qdim - a.kvdim)] = t;
+        if (pub_tag)
+          __hip_atomic_store(a.xcell + n, (unsigned long long)pub_tag << 32 | __float_as_uint(t),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
     return;

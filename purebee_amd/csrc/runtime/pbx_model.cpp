@@ -39,6 +39,9 @@ struct AttnArgsHost {  // AttnArgs in pbx_decode.hip
   const void *odsc = nullptr;
   long long *oacc = nullptr;
   float *ox = nullptr;
+  // pbx_qkvr_attn_o_*: the GEMV's published rows and their epoch at [cell_n]
+  const unsigned long long *cells = nullptr;
+  int cell_n = 0, qdim = 0;
 };
 
 struct AttnSplitArgsHost {  // AttnSplitArgs in pbx_decode.hip
@@ -77,7 +80,7 @@ struct ArgmaxArgsHost {  // ArgmaxArgs in pbx_decode.hip
   EmbedArgsHost emb;
 };
 
-enum ArgKind { ARG_GEMV, ARG_ATTN, ARG_ATTN_SPLIT, ARG_COMBINE, ARG_EMBED, ARG_ARGMAX };
+enum ArgKind { ARG_GEMV, ARG_ATTN, ARG_ATTN_SPLIT, ARG_COMBINE, ARG_EMBED, ARG_ARGMAX, ARG_FUSED };
 enum AttnMode { ATTN_HEAD, ATTN_SPLIT, ATTN_DECODE };
 
 struct Op {
@@ -94,6 +97,7 @@ struct Op {
   CombineArgsHost comb;
   EmbedArgsHost embed;
   ArgmaxArgsHost amax;
+  int np = 0;  // ARG_FUSED: GEMV workgroups before the attention's
 };
 
 struct Layer {
@@ -153,8 +157,14 @@ struct pbx_model {
   float *attn_part = nullptr;
   int attn_mode = 0;  // AttnMode
   // rows of the o projection per workgroup / 256 in the fused attention +
-  // o projection (0: a separate o GEMV); PBX_ATTN_O=0|1|2|4 at creation
-  int attn_o_ipt = 1;
+  // o projection (0: a separate o GEMV); PBX_ATTN_O=0|1|2|4 at creation,
+  // default (-1) 2 where the q|k|v GEMV joins the launch, else 1
+  int attn_o_ipt = -1;
+  // q|k|v GEMV and attention + o projection in one launch (PBX_QKV_ATTN=0 at
+  // creation: two launches); per layer, the GEMV's published rows and the
+  // layer's epoch ((qkv_rows + 64) cells, allocated with the first step)
+  bool qkv_attn = true;
+  unsigned long long *qa_cells = nullptr;
   int *state = nullptr;
   int *hist = nullptr;
   int hist_cap = 0;
@@ -457,9 +467,13 @@ static int build_ops(pbx_model *m) {
   // o GEMV).
   int o_ipt = 0;
   hipFunction_t fattno = nullptr;
+  // the q|k|v GEMV can join the launch: Q4_0 at K = 2048 in 32-row tiles
+  // (16-row with IPT 1), a multiple of 8 tiles
+  const bool qa_fit = m->qkv_attn && m->layers[0].wqkv->type == PBX_TYPE_Q4_0 &&
+                      m->layers[0].wqkv->B == 64 && m->qkv_rows % 256 == 0;
   if (cached && g.head_dim == 64 && m->layers[0].wo->type == PBX_TYPE_Q4_0 &&
       m->layers[0].wo->B == 2 * g.n_heads) {
-    const int ipt = m->attn_o_ipt;
+    const int ipt = m->attn_o_ipt >= 0 ? m->attn_o_ipt : qa_fit ? 2 : 1;
     if ((ipt == 1 || ipt == 2 || ipt == 4) && g.dim % (256 * ipt) == 0) {
       auto variant = [&](const pbx_weight *w, const char *plan_mode, const char *mode,
                          const char *role) {
@@ -477,10 +491,26 @@ static int build_ops(pbx_model *m) {
         o_ipt = ipt;
     }
   }
+  // The q|k|v GEMV and the attention + o projection in one launch
+  // (pbx_qkvr_attn_o_r<RT>c<IPT>: IPT 1 with 16-row GEMV tiles, IPT 2 with
+  // 32-row tiles).
+  hipFunction_t fqa = nullptr;
+  const size_t cell_stride = (size_t)m->qkv_rows + 64;
+  const int qa_rows = o_ipt == 2 ? 32 : 16;
+  const std::string qa_name = o_ipt == 2 ? "pbx_qkvr_attn_o_r8c2" : "pbx_qkvr_attn_o_r4c1";
+  if ((o_ipt == 1 || o_ipt == 2) && qa_fit) fqa = pbx_kernel_by_name(c, qa_name);
+  if (fqa && !m->qa_cells) {
+    const size_t cb = (size_t)g.n_layers * cell_stride * 8;
+    int rc = dalloc(m, (void **)&m->qa_cells, cb);
+    if (rc) return rc;
+    if (hipMemsetAsync(m->qa_cells, 0, cb, c->stream) != hipSuccess)
+      return pbx_fail(c, PBX_EHIP, "model: clearing the q|k|v cells failed");
+  }
   for (int l = 0; l < g.n_layers; ++l) {
     Layer &L = m->layers[l];
     int rc;
     m->layer_op[l] = m->ops.size();
+    unsigned long long *cells = fqa ? m->qa_cells + l * cell_stride : nullptr;
     if ((rc = add_gemv(m, L.wqkv, cached ? "qkvr" : "qkv", "qkv", m->x, nullptr, L.attn_norm,
                        m->qkv, nullptr)))
       return rc;
@@ -514,6 +544,24 @@ static int build_ops(pbx_model *m) {
       a.attn.ox = m->x;
       // the o projection's weights, its head outputs' update (read and written)
       a.fixed_bytes = (double)L.wo->N * pbx_type_row_bytes(L.wo->type, L.wo->K) + 16.0 * g.dim;
+      if (cells) {
+        // one launch: the q|k|v op's GEMV arguments, publishing into the
+        // layer's cells, and these attention arguments reading them
+        Op q = m->ops.back();
+        m->ops.pop_back();
+        a.kind = ARG_FUSED;
+        a.name = qa_name;
+        a.f = fqa;
+        a.role = "qkv_attn_o";
+        a.np = m->qkv_rows / qa_rows;
+        a.grid = dim3(a.np + a.grid.x);
+        a.gemv = q.gemv;
+        a.gemv.xcell = cells;
+        a.attn.cells = cells;
+        a.attn.cell_n = m->qkv_rows;
+        a.attn.qdim = g.dim;
+        a.fixed_bytes += q.bytes;
+      }
       m->ops.push_back(a);
     } else if (cached) {
       a.kind = ARG_ATTN;
@@ -573,6 +621,7 @@ static int build_ops(pbx_model *m) {
       if ((rc = add_gemv(m, L.wd, "adda", "down", m->gu, nullptr, nullptr, m->x, nullptr)))
         return rc;
       m->ops.back().gemv.acc = m->xacc;
+      if (cells) m->ops.back().gemv.xcell = cells + m->qkv_rows;  // advances the epoch
       continue;
     }
     if ((rc = add_gemv(m, L.wo, "add", "o", m->attn, nullptr, nullptr, m->x, nullptr))) return rc;
@@ -629,7 +678,8 @@ static int enqueue_op(pbx_model *m, Op &op, hipEvent_t t0 = nullptr, hipEvent_t 
     default: arg = &op.amax; break;
   }
   void *one[] = {arg};
-  void **args = op.kind == ARG_COMBINE ? comb : one;
+  void *fused[] = {&op.gemv, &op.attn, &op.np};
+  void **args = op.kind == ARG_COMBINE ? comb : op.kind == ARG_FUSED ? fused : one;
   if (t0)
     return pbx_launch_fn_timed(m->c, op.f, op.name.c_str(), op.grid, op.block, args, m->c->stream,
                                t0, t1);
@@ -807,7 +857,7 @@ static void model_release(pbx_model *m) {
                   (void *)m->x, (void *)m->xacc, (void *)m->qkv, (void *)m->attn, (void *)m->gu,
                   (void *)m->logits,
                   (void *)m->partials, (void *)m->state, (void *)m->hist,
-                  (void *)m->attn_part, m->head_lanes})
+                  (void *)m->attn_part, m->head_lanes, (void *)m->qa_cells})
     if (p) hipFree(p);
   for (void *p : {(void *)m->bx, (void *)m->bxn, (void *)m->bqkv, (void *)m->battn,
                   (void *)m->bgu, (void *)m->bh, (void *)m->btmp, (void *)m->blogits,
@@ -921,6 +971,7 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
   // query heads per KV head): about 256 workgroups per layer, at most 64
   // splits, never more splits than positions.
   m->attn_mode = attention_mode(g);
+  if (const char *e = getenv("PBX_QKV_ATTN")) m->qkv_attn = e[0] != '0';
   if (const char *e = getenv("PBX_ATTN_O")) m->attn_o_ipt = atoi(e);
   if (const char *e = getenv("PBX_GRAPH_STEPS")) m->graph_steps = atoi(e);
   if (!rc && m->attn_mode == ATTN_SPLIT) {
@@ -1815,8 +1866,9 @@ extern "C" int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int
       hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]);
       acc[i] += ms * 1e3;
       const Op &op = m->ops[i];
-      bytes[i] += (op.kind == ARG_ATTN || op.kind == ARG_ATTN_SPLIT) ? op.bytes * (start_pos + s + 1)
-                                                                      : op.bytes;
+      bytes[i] += (op.kind == ARG_ATTN || op.kind == ARG_ATTN_SPLIT || op.kind == ARG_FUSED)
+                      ? op.bytes * (start_pos + s + 1)
+                      : op.bytes;
       bytes[i] += op.fixed_bytes;
     }
   }

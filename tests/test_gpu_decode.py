@@ -222,24 +222,28 @@ def test_attention_kernels_match_one_workgroup_per_head(ctx, monkeypatch, mode, 
     ref.close()
 
 
-@pytest.mark.parametrize("ipt", [1, 2, 4])
-def test_fused_attention_o_matches_separate_o(ctx, monkeypatch, ipt):
+@pytest.mark.parametrize("ipt,qa", [(1, True), (2, True), (1, False), (2, False), (4, False)])
+def test_fused_attention_o_matches_separate_o(ctx, monkeypatch, ipt, qa):
     """Decode with the o projection fused into the cached head attention
     (workgroup (head, part) adds W_o[rows, head] o_h for its 256 * ipt rows
     into a 64-bit 2^-32 fixed-point update; the gate|up GEMV adds the update
     to its input, the down GEMV folds it into the residual and clears it)
     against the same model with the separate o GEMV and against the oracle,
     over 100 positions (past the attention's two speculative 32-position
-    slots) on two layers."""
-    print(f"[case] fused attention + o, ipt {ipt}, 2048/8192, 32/8 heads, 100 positions",
-          flush=True)
+    slots) on two layers.  qa: the q|k|v GEMV in the same launch
+    (pbx_qkvr_attn_o_c1: the attention workgroups wait for the GEMV's
+    epoch-tagged q, k and v cells of their head)."""
+    print(f"[case] fused attention + o, ipt {ipt}, q|k|v in the launch {qa}, 2048/8192, "
+          f"32/8 heads, 100 positions", flush=True)
     cfg = tiny(TYPE_Q4_0, TYPE_Q4_0, dim=2048, hidden_dim=8192, n_layers=2, n_heads=32,
                n_kv_heads=8, vocab_size=512, max_seq=256)
     monkeypatch.setenv("PBX_ATTN_O", str(ipt))
+    monkeypatch.setenv("PBX_QKV_ATTN", "1" if qa else "0")
     fused, ref, cfg = make_pair(ctx, cfg, 101)
     monkeypatch.setenv("PBX_ATTN_O", "0")
     plain = synth.build(ctx, cfg, 101)
     monkeypatch.delenv("PBX_ATTN_O")
+    monkeypatch.delenv("PBX_QKV_ATTN")
     toks = [int(t) for t in synth.random_tokens(102, 100, cfg["vocab_size"])]
     worst = 0.0
     for p, t in enumerate(toks):
@@ -251,13 +255,49 @@ def test_fused_attention_o_matches_separate_o(ctx, monkeypatch, ipt):
     kern = {k for _, k, _, _ in fused.profile(toks[-1], len(toks), 1)}
     plain_kern = {k for _, k, _, _ in plain.profile(toks[-1], len(toks), 1)}
     print(f"  fused vs separate max-abs {worst:.2e}, vs oracle {err:.2e}")
-    assert f"pbx_attention_o_c{ipt}" in kern and "pbx_dk_q4_i16x4b1p2_gua" in kern
+    assert (f"pbx_qkvr_attn_o_r{4 * ipt}c{ipt}" if qa else f"pbx_attention_o_c{ipt}") in kern
+    assert "pbx_dk_q4_i16x4b1p2_gua" in kern
     assert "pbx_attention_head_c" in plain_kern
     assert worst <= 1e-4
     assert err <= LOGIT_TOL
     fused.free()
     plain.free()
     ref.close()
+
+
+def test_fused_qkv_attention_long_context(ctx, monkeypatch):
+    """The q|k|v GEMV and the attention + o projection in one launch past
+    512 cached positions, where the newest position falls in the
+    attention's second 512-position chunk (its k and v come from the
+    GEMV's cells there too): a 1-layer model prefilled with 520 tokens,
+    then 12 decode steps, against the same model launching the two kernels
+    separately, and the greedy tokens of 16 on-device steps (4 per graph
+    launch) against it."""
+    print("[case] q|k|v + attention in one launch, 1 layer, positions 520..531", flush=True)
+    cfg = tiny(TYPE_Q4_0, TYPE_Q4_0, dim=2048, hidden_dim=8192, n_layers=1, n_heads=32,
+               n_kv_heads=8, vocab_size=512, max_seq=1024)
+    fused = synth.build(ctx, cfg, 111)
+    monkeypatch.setenv("PBX_QKV_ATTN", "0")
+    plain = synth.build(ctx, cfg, 111)
+    monkeypatch.delenv("PBX_QKV_ATTN")
+    toks = [int(t) for t in synth.random_tokens(112, 532, cfg["vocab_size"])]
+    fused.forward(toks[:520], 0, want_logits=False)
+    plain.forward(toks[:520], 0, want_logits=False)
+    worst = 0.0
+    for p in range(520, 532):
+        a, _ = fused.forward([toks[p]], p)
+        b, _ = plain.forward([toks[p]], p)
+        assert np.isfinite(a).all()
+        worst = max(worst, float(np.abs(a - b).max()))
+    ga = fused.generate(toks[-1], 531, 16)
+    gb = plain.generate(toks[-1], 531, 16)
+    kern = {k for _, k, _, _ in fused.profile(toks[-1], 531, 1)}
+    print(f"  max-abs {worst:.2e}; greedy {list(ga)} / {list(gb)}")
+    assert any(k.startswith("pbx_qkvr_attn_o_") for k in kern)
+    assert worst <= 1e-4
+    assert list(ga) == list(gb)
+    fused.free()
+    plain.free()
 
 
 def test_non_finite_activation_propagates(ctx):
