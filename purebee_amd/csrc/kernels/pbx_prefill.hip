@@ -564,11 +564,16 @@ pbx_add_inplace(float *y, const float *x, int64_t n) {
 }
 
 // Argmax of each row of logits [M][vocab] (first maximum wins,
-// llama.js:432-442), in two passes so a row is scanned by many workgroups:
-// workgroup (p, row) reduces columns [p*chunk, (p+1)*chunk) to one key,
-// then one wave per row reduces the P keys.
+// llama.js:432-442), each row scanned by P workgroups in one launch:
+// workgroup (p, row) reduces columns [p*chunk, (p+1)*chunk) to one key and
+// folds it into the row's cell cells[row * stride] by a device-scope atomic max, waits for that to
+// return, and only then counts itself in at cells[row * stride + 1]; the
+// workgroup that completes the count of P therefore reads the final
+// maximum (one more atomic, at the same coherence point), writes the row's
+// token and clears both cells for the next launch (zero before the first).
 extern "C" __global__ void __launch_bounds__(256)
-pbx_argmax_rows_partial(const float *logits, int vocab, int chunk, uint64_t *keys, int P) {
+pbx_argmax_rows(const float *logits, int vocab, int chunk, unsigned long long *cells, int stride,
+                int P, int *out) {
   __shared__ uint64_t red[4];
   const int row = blockIdx.y, p = blockIdx.x;
   const float *r = logits + (size_t)row * vocab;
@@ -584,16 +589,19 @@ pbx_argmax_rows_partial(const float *logits, int vocab, int chunk, uint64_t *key
   if (threadIdx.x == 0) {
     for (int w = 1; w < 4; ++w) best = red[w] > best ? red[w] : best;
     best = red[0] > best ? red[0] : best;
-    keys[(size_t)row * P + p] = best;
+    unsigned long long *c = cells + (size_t)row * stride;
+    const unsigned long long prev =
+        __hip_atomic_fetch_max(c, (unsigned long long)best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::"v"(prev) : "memory");  // the max has been applied
+    const unsigned long long n =
+        __hip_atomic_fetch_add(c + 1, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (n == (unsigned long long)(P - 1)) {
+      const unsigned long long k =
+          __hip_atomic_fetch_max(c, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      out[row] = k ? (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFu)) : 0;
+      __hip_atomic_store(c, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(c + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
-extern "C" __global__ void __launch_bounds__(64)
-pbx_argmax_rows_final(const uint64_t *keys, int P, int *out) {
-  const uint64_t *k = keys + (size_t)blockIdx.x * P;
-  uint64_t best = 0;
-  for (int i = threadIdx.x; i < P; i += 64) best = k[i] > best ? k[i] : best;
-  best = wave_max_u64(best);
-  if (threadIdx.x == 0)
-    out[blockIdx.x] = best ? (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFu)) : 0;
-}

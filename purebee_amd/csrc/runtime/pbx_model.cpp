@@ -198,13 +198,17 @@ struct pbx_model {
   int batch_cap = 0, logits_cap = 0;
   float *bx = nullptr, *bxn = nullptr, *bqkv = nullptr, *battn = nullptr, *bgu = nullptr,
         *bh = nullptr, *btmp = nullptr, *blogits = nullptr;
-  int *btok = nullptr, *bnext = nullptr;
-  // pinned staging of the rows' tokens and next tokens (batch_cap each): the
-  // uploads and read-backs of a verify are then asynchronous copies;
-  // tok_ev marks the last upload out of h_tok
+  int *bnext = nullptr;
+  // the rows' tokens and next tokens in coherent pinned host memory
+  // (batch_cap each), which the kernels read and write directly through
+  // their device addresses d_tok / d_next: a verify then needs no copy
+  // operation; tok_ev marks the last kernel that reads h_tok
   int32_t *h_tok = nullptr, *h_next = nullptr;
+  int32_t *d_tok = nullptr, *d_next = nullptr;
   hipEvent_t tok_ev = nullptr;
-  uint64_t *bkeys = nullptr;  // [logits_cap][64] partial argmax keys
+  // [logits_cap][64]: per row, the running maximum key and the count of
+  // pbx_argmax_rows (zero between launches)
+  uint64_t *bkeys = nullptr;
   // rows GEMV with the K blocks split over workgroups (the down projection):
   // a 64-bit cell per output element [MR_MAX][dim] (zero between launches)
   unsigned long long *mr_cell = nullptr;
@@ -861,7 +865,7 @@ static void model_release(pbx_model *m) {
     if (p) hipFree(p);
   for (void *p : {(void *)m->bx, (void *)m->bxn, (void *)m->bqkv, (void *)m->battn,
                   (void *)m->bgu, (void *)m->bh, (void *)m->btmp, (void *)m->blogits,
-                  (void *)m->btok, (void *)m->bnext, (void *)m->bkeys, (void *)m->mr_cell,
+                  (void *)m->bnext, (void *)m->bkeys, (void *)m->mr_cell,
                   m->g16, m->g16lo,
                   (void *)m->ginv, (void *)m->gpart})
     if (p) hipFree(p);
@@ -1147,7 +1151,6 @@ static int ensure_batch(pbx_model *m, int rows, bool all_logits) {
     if (!rc) rc = grow(m, (void **)&m->bh, R * g.hidden_dim * 4);
     // accumulating linears without an MFMA path go through a temporary
     if (!rc) rc = grow(m, (void **)&m->btmp, R * tmp_cols * 4);
-    if (!rc) rc = grow(m, (void **)&m->btok, R * 4);
     if (!rc) rc = grow(m, (void **)&m->bnext, R * 4);
     if (!rc && !m->tok_ev && hipEventCreateWithFlags(&m->tok_ev, hipEventDisableTiming) != hipSuccess)
       rc = pbx_fail(m->c, PBX_EHIP, "model: event creation failed");
@@ -1156,8 +1159,11 @@ static int ensure_batch(pbx_model *m, int rows, bool all_logits) {
       if (m->h_tok) hipHostFree(m->h_tok);
       if (m->h_next) hipHostFree(m->h_next);
       m->h_tok = m->h_next = nullptr;
-      if (hipHostMalloc((void **)&m->h_tok, R * 4) != hipSuccess ||
-          hipHostMalloc((void **)&m->h_next, R * 4) != hipSuccess)
+      const unsigned fl = hipHostMallocMapped | hipHostMallocCoherent;
+      if (hipHostMalloc((void **)&m->h_tok, R * 4, fl) != hipSuccess ||
+          hipHostMalloc((void **)&m->h_next, R * 4, fl) != hipSuccess ||
+          hipHostGetDevicePointer((void **)&m->d_tok, m->h_tok, 0) != hipSuccess ||
+          hipHostGetDevicePointer((void **)&m->d_next, m->h_next, 0) != hipSuccess)
         rc = pbx_fail(m->c, PBX_ENOMEM, "model: pinned token buffers failed");
     }
     if (rc) {
@@ -1171,6 +1177,11 @@ static int ensure_batch(pbx_model *m, int rows, bool all_logits) {
         (rc = grow(m, (void **)&m->bkeys, (size_t)rows * 64 * 8))) {
       m->logits_cap = 0;
       return rc;
+    }
+    // pbx_argmax_rows' cells start at zero (and each launch leaves them so)
+    if (hipMemsetAsync(m->bkeys, 0, (size_t)rows * 64 * 8, m->c->stream) != hipSuccess) {
+      m->logits_cap = 0;
+      return pbx_fail(m->c, PBX_EHIP, "model: clearing the argmax cells failed");
     }
     m->logits_cap = rows;
   }
@@ -1418,22 +1429,21 @@ static int fused_residual_norm(pbx_model *m, const pbx_gemm_plan *p, int M, int 
 static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, int nl) {
   pbx_ctx *c = m->c;
   const pbx_model_config &g = m->cfg;
-  // through the pinned buffer (once the previous upload out of it is done)
+  // the embedding kernel reads the tokens from the pinned buffer (once the
+  // previous kernel that read it is done)
   if (hipEventSynchronize(m->tok_ev) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "model: token staging wait failed");
   memcpy(m->h_tok, tokens, (size_t)n * 4);
-  if (hipMemcpyAsync(m->btok, m->h_tok, (size_t)n * 4, hipMemcpyHostToDevice, c->stream) !=
-          hipSuccess ||
-      hipEventRecord(m->tok_ev, c->stream) != hipSuccess)
-    return pbx_fail(c, PBX_EHIP, "model: token upload failed");
   int rc;
   {
     const void *qs = m->embd->qs, *dsc = m->embd->d, *msc = m->embd->m;
-    int *tok = m->btok;
+    int *tok = m->d_tok;
     float *x = m->bx;
     int type = kernel_type(m->embd->type), dim = g.dim, vocab = g.vocab_size;
     void *args[] = {(void *)&qs, (void *)&dsc, (void *)&msc, &tok, &x, &type, &dim, &vocab};
     if ((rc = launch_k(m, "pbx_embed_rows", dim3((g.dim + 255) / 256, n), dim3(256), args))) return rc;
+    if (hipEventRecord(m->tok_ev, c->stream) != hipSuccess)
+      return pbx_fail(c, PBX_EHIP, "model: token event failed");
   }
   const size_t layer_kv = (size_t)g.max_seq * m->kvdim;
   const bool rows_int = n <= ROWS_MAX && rows_int_ok(m);
@@ -1702,24 +1712,20 @@ extern "C" int pbx_model_forward_batch(pbx_model *m, const int32_t *tokens, int 
     if ((rc = linear_rows(m, head, m->bxn, n, m->blogits, false))) return rc;
   }
   {
-    // P partial keys per row (<= 64, the bkeys row stride), ~2048 columns each
+    // P workgroups per row, ~2048 columns each, meeting in the row's cells
     const float *lg = m->blogits;
     int vocab = g.vocab_size;
     int P = std::min(64, (g.vocab_size + 2047) / 2048);
     int chunk = (g.vocab_size + P - 1) / P;
-    uint64_t *keys = m->bkeys;
-    int *out = m->bnext;
-    void *a1[] = {(void *)&lg, &vocab, &chunk, &keys, &P};
-    if ((rc = launch_k(m, "pbx_argmax_rows_partial", dim3(P, n), dim3(256), a1))) return rc;
-    void *a2[] = {&keys, &P, &out};
-    if ((rc = launch_k(m, "pbx_argmax_rows_final", dim3(n), dim3(64), a2))) return rc;
+    unsigned long long *cells = (unsigned long long *)m->bkeys;
+    int stride = 64;
+    int *out = next_tokens ? m->d_next : m->bnext;  // straight into host memory
+    void *a1[] = {(void *)&lg, &vocab, &chunk, &cells, &stride, &P, &out};
+    if ((rc = launch_k(m, "pbx_argmax_rows", dim3(P, n), dim3(256), a1))) return rc;
   }
   if (logits && hipMemcpyAsync(logits, m->blogits, (size_t)n * g.vocab_size * 4,
                                hipMemcpyDeviceToHost, c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward_batch: logits copy failed");
-  if (next_tokens && hipMemcpyAsync(m->h_next, m->bnext, (size_t)n * 4, hipMemcpyDeviceToHost,
-                                    c->stream) != hipSuccess)
-    return pbx_fail(c, PBX_EHIP, "pbx_model_forward_batch: token copy failed");
   if (hipStreamSynchronize(c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward_batch: forward failed on the device");
   if (next_tokens) memcpy(next_tokens, m->h_next, (size_t)n * 4);
