@@ -338,20 +338,29 @@ pbx_attention_tiled(const float *qkv, const float *kcache, const float *vcache, 
     (L) = (_Float16)(x_ - (float)h_);            \
   } while (0)
 
-extern "C" __global__ void __launch_bounds__(256)
-pbx_attention_mfma(const float *qkv, const float *kcache, const float *vcache, float *out,
-                   int start, int n_rows, int n_heads, int n_kv_heads, int head_dim,
-                   float scale) {
+// KG > 1: KG groups of four waves share the workgroup's 64 queries and take
+// the 64-key stages round robin (group g: stages g, g + KG, ...), each with
+// its own LDS stage, so the longest tile (the last one: every key) runs in
+// 1/KG of the stage steps; the 2 KG states per query (key halves x groups)
+// merge through LDS at the end.  All groups run the same number of steps
+// (a group past the last key only keeps the barriers).
+template <int KG>
+__device__ __forceinline__ void attention_mfma_body(const float *qkv, const float *kcache,
+                                                    const float *vcache, float *out, int start,
+                                                    int n_rows, int n_heads, int n_kv_heads,
+                                                    int head_dim, float scale) {
   typedef _Float16 half8 __attribute__((ext_vector_type(8)));
   typedef _Float16 half2t __attribute__((ext_vector_type(2)));
   typedef _Float16 half4t __attribute__((ext_vector_type(4)));
   typedef float floatx16 __attribute__((ext_vector_type(16)));
-  __shared__ __attribute__((aligned(16))) _Float16 Kh[FA_KT * FA_KP], Kl[FA_KT * FA_KP];
-  __shared__ __attribute__((aligned(16))) _Float16 Vh[64 * FA_KP], Vl[64 * FA_KP];  // [dim][key]
+  __shared__ __attribute__((aligned(16))) _Float16 Ksh[KG][2][FA_KT * FA_KP];
+  __shared__ __attribute__((aligned(16))) _Float16 Vsh[KG][2][64 * FA_KP];  // [dim][key]
   const int h = blockIdx.x, t0 = blockIdx.y * 64, hd = head_dim, hd4 = hd / 4, nc = hd / 16;
   const int group = n_heads / n_kv_heads, kvh = h / group;
   const int dim = n_heads * hd, kvdim = n_kv_heads * hd, rs = dim + 2 * kvdim;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
+  const int kg = KG > 1 ? (int)(threadIdx.x >> 8) : 0;  // the wave's key group
+  _Float16 *Kh = Ksh[kg][0], *Kl = Ksh[kg][1], *Vh = Vsh[kg][0], *Vl = Vsh[kg][1];
   const int qg = wave & 1, kh = wave >> 1, lq = lane & 31, hh = lane >> 5;
   const int nq = min(64, n_rows - t0);
   const int qrow = 32 * qg + lq;  // this lane's query within the tile
@@ -405,13 +414,15 @@ pbx_attention_mfma(const float *qkv, const float *kcache, const float *vcache, f
       vreg1[i] = ok && kp + 1 < nk ? *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + kp + 1) * kvdim + c4) : z4;
     }
   };
-  load_stage(0);
-  for (int k0 = 0; k0 <= last_key; k0 += FA_KT) {
+  if (kg * FA_KT <= last_key) load_stage(kg * FA_KT);
+  for (int step = 0; KG * FA_KT * step <= last_key; ++step) {
+    const int k0 = (KG * step + kg) * FA_KT;  // this group's stage
+    const bool live = k0 <= last_key;
     __syncthreads();  // the previous stage's reads are done
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int it = tid + 256 * i, key = it / hd4, c4 = 4 * (it % hd4);
-      if (it < FA_KT * hd4) {
+      if (live && it < FA_KT * hd4) {
         const float4 v = kreg[i];
         half4t hv, lv;
         SPLIT_F16(v.x, hv[0], lv[0]);
@@ -425,7 +436,7 @@ pbx_attention_mfma(const float *qkv, const float *kcache, const float *vcache, f
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int it = tid + 256 * i, kp = 2 * (it / hd4), c4 = 4 * (it % hd4);
-      if (it < (FA_KT / 2) * hd4) {
+      if (live && it < (FA_KT / 2) * hd4) {
         const float4 v0 = vreg0[i], v1 = vreg1[i];
 #define FA_PUTV(e, x0, x1)                                                  \
   do {                                                                      \
@@ -443,7 +454,8 @@ pbx_attention_mfma(const float *qkv, const float *kcache, const float *vcache, f
       }
     }
     __syncthreads();
-    if (k0 + FA_KT <= last_key) load_stage(k0 + FA_KT);
+    if (k0 + KG * FA_KT <= last_key) load_stage(k0 + KG * FA_KT);
+    if (!live) continue;
 
     // S^T for this wave's 32 keys (rows) x 32 queries (columns)
     const int kr = 32 * kh + lq;  // A row: key kr of the stage
@@ -506,11 +518,13 @@ pbx_attention_mfma(const float *qkv, const float *kcache, const float *vcache, f
     }
   }
 
-  // merge the two key halves of each query group: kh = 1 hands over through LDS
+  // merge the 2 KG key slices of each query group (key halves x groups):
+  // every slice but (kh 0, group 0) hands its state over through LDS
   __syncthreads();
-  float *mg = reinterpret_cast<float *>(Kh);  // [qg][lane][34]: acc (32), m, l
-  float *mine = mg + (qg * 64 + lane) * 34;
-  if (kh == 1) {
+  float *mg = reinterpret_cast<float *>(&Ksh[0][0][0]);  // [qg][slice - 1][lane][34]: acc, m, l
+  const int slice = 2 * kg + kh;
+  if (slice > 0) {
+    float *mine = mg + ((qg * (2 * KG - 1) + slice - 1) * 64 + lane) * 34;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       mine[r] = acc[0][r];
@@ -520,30 +534,58 @@ pbx_attention_mfma(const float *qkv, const float *kcache, const float *vcache, f
     mine[33] = l_run;
   }
   __syncthreads();
-  if (kh == 0 && qrow < nq) {
-    const float m1 = mine[32], l1 = mine[33];
-    const float M = fmaxf(m_run, m1);
+  if (slice == 0 && qrow < nq) {
+    float M = m_run;
+#pragma unroll
+    for (int j = 1; j < 2 * KG; ++j)
+      M = fmaxf(M, mg[((qg * (2 * KG - 1) + j - 1) * 64 + lane) * 34 + 32]);
     const float f0 = m_run == -INFINITY ? 0.f : expf(m_run - M);
-    const float f1 = m1 == -INFINITY ? 0.f : expf(m1 - M);
-    const float inv = 1.0f / (l_run * f0 + l1 * f1);
+    float den = l_run * f0;
+    floatx16 o0 = acc[0] * f0, o1 = acc[1] * f0;
+#pragma unroll
+    for (int j = 1; j < 2 * KG; ++j) {
+      const float *src = mg + ((qg * (2 * KG - 1) + j - 1) * 64 + lane) * 34;
+      const float mj = src[32];
+      const float fj = mj == -INFINITY ? 0.f : expf(mj - M);
+      den = fmaf(src[33], fj, den);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        o0[r] = fmaf(src[r], fj, o0[r]);
+        o1[r] = fmaf(src[16 + r], fj, o1[r]);
+      }
+    }
+    const float inv = 1.0f / den;
     float *o = out + (size_t)(t0 + qrow) * dim + (size_t)h * hd;
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d0 = 32 * dt + 8 * g4 + 4 * hh;
-        if (d0 < hd) {
-          float4 v;
-          v.x = (acc[dt][4 * g4 + 0] * f0 + mine[16 * dt + 4 * g4 + 0] * f1) * inv;
-          v.y = (acc[dt][4 * g4 + 1] * f0 + mine[16 * dt + 4 * g4 + 1] * f1) * inv;
-          v.z = (acc[dt][4 * g4 + 2] * f0 + mine[16 * dt + 4 * g4 + 2] * f1) * inv;
-          v.w = (acc[dt][4 * g4 + 3] * f0 + mine[16 * dt + 4 * g4 + 3] * f1) * inv;
-          *reinterpret_cast<float4 *>(o + d0) = v;
-        }
-      }
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d0 = 8 * g4 + 4 * hh;
+      if (d0 < hd)
+        *reinterpret_cast<float4 *>(o + d0) = make_float4(
+            o0[4 * g4] * inv, o0[4 * g4 + 1] * inv, o0[4 * g4 + 2] * inv, o0[4 * g4 + 3] * inv);
+      if (32 + d0 < hd)
+        *reinterpret_cast<float4 *>(o + 32 + d0) = make_float4(
+            o1[4 * g4] * inv, o1[4 * g4 + 1] * inv, o1[4 * g4 + 2] * inv, o1[4 * g4 + 3] * inv);
     }
   }
 }
+
+extern "C" __global__ void __launch_bounds__(256)
+pbx_attention_mfma(const float *qkv, const float *kcache, const float *vcache, float *out,
+                   int start, int n_rows, int n_heads, int n_kv_heads, int head_dim,
+                   float scale) {
+  attention_mfma_body<1>(qkv, kcache, vcache, out, start, n_rows, n_heads, n_kv_heads, head_dim,
+                         scale);
+}
+#define PBX_ATTN_MFMA_KG(KG)                                                                   \
+  extern "C" __global__ void __launch_bounds__(256 * KG)                                       \
+      pbx_attention_mfma_g##KG(const float *qkv, const float *kcache, const float *vcache,     \
+                               float *out, int start, int n_rows, int n_heads, int n_kv_heads, \
+                               int head_dim, float scale) {                                    \
+    attention_mfma_body<KG>(qkv, kcache, vcache, out, start, n_rows, n_heads, n_kv_heads,      \
+                            head_dim, scale);                                                  \
+  }
+PBX_ATTN_MFMA_KG(2)
+#undef PBX_ATTN_MFMA_KG
 
 // SwiGLU rows (llama.js:329-333): h[t][i] = silu(gate[t][i]) * up[t][i],
 // gate and up side by side in gu[t] = [gate | up].

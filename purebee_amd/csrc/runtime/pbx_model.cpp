@@ -1188,6 +1188,18 @@ static int ensure_batch(pbx_model *m, int rows, bool all_logits) {
   return PBX_OK;
 }
 
+// The causal MFMA attention of a batched forward: the key stages of a
+// workgroup split over two groups of four waves (PBX_PREFILL_ATTN_GROUPS=1:
+// one group, the 256-thread form)
+static bool prefill_attention_one_group() {
+  const char *e = getenv("PBX_PREFILL_ATTN_GROUPS");
+  return e && atoi(e) == 1;
+}
+static const char *prefill_attention_mfma() {
+  return prefill_attention_one_group() ? "pbx_attention_mfma" : "pbx_attention_mfma_g2";
+}
+static int prefill_attention_threads() { return prefill_attention_one_group() ? 256 : 512; }
+
 static int launch_k(pbx_model *m, const char *name, dim3 grid, dim3 block, void **args) {
   hipFunction_t f = pbx_kernel_by_name(m->c, name);
   if (!f) return pbx_fail(m->c, PBX_ELOAD, "model: kernel %s not found", name);
@@ -1470,8 +1482,10 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, i
         float scale = (float)(1.0 / sqrt((double)g.head_dim));
         if (g.head_dim <= 64 && n >= 16) {
           void *args[] = {&qkv, &kc, &vc, &out, &st, &rows, &nh, &nkv, &hd, &scale};
-          rc = launch_k(m, g.head_dim % 16 == 0 ? "pbx_attention_mfma" : "pbx_attention_tiled",
-                        dim3(g.n_heads, (n + 63) / 64), dim3(256), args);
+          const bool mf = g.head_dim % 16 == 0;
+          rc = launch_k(m, mf ? prefill_attention_mfma() : "pbx_attention_tiled",
+                        dim3(g.n_heads, (n + 63) / 64), dim3(mf ? prefill_attention_threads() : 256),
+                        args);
         } else {
           void *args[] = {&qkv, &kc, &vc, &out, &st, &nh, &nkv, &hd, &scale};
           if (g.head_dim <= 64)
@@ -1546,8 +1560,10 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, i
       if (g.head_dim <= 64 && n >= 16) {
         // MFMA kernel for head dims that are a multiple of 16, else fp32 FMAs
         void *args[] = {&qkv, &kc, &vc, &out, &st, &rows, &nh, &nkv, &hd, &scale};
-        rc = launch_k(m, g.head_dim % 16 == 0 ? "pbx_attention_mfma" : "pbx_attention_tiled",
-                      dim3(g.n_heads, (n + 63) / 64), dim3(256), args);
+        const bool mf = g.head_dim % 16 == 0;
+        rc = launch_k(m, mf ? prefill_attention_mfma() : "pbx_attention_tiled",
+                      dim3(g.n_heads, (n + 63) / 64), dim3(mf ? prefill_attention_threads() : 256),
+                      args);
       } else {
         void *args[] = {&qkv, &kc, &vc, &out, &st, &nh, &nkv, &hd, &scale};
         // head_dim <= 64: the decode kernel's flash layout per (head, row);

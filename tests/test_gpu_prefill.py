@@ -104,6 +104,34 @@ def test_batched_chunks_every_row_vs_oracle(ctx, n_heads, n_kv):
     ref.close()
 
 
+@pytest.mark.parametrize("start,n", [(0, 200), (37, 130), (0, 16)])
+def test_prefill_attention_key_groups(ctx, monkeypatch, start, n):
+    """The prefill attention with each workgroup's 64-key stages split over
+    two groups of four waves (pbx_attention_mfma_g2, the default) against
+    the one-group form (PBX_PREFILL_ATTN_GROUPS=1) on every row of a batched
+    forward, ragged last tiles and a non-zero start included (tiles whose
+    last stage falls to one group only), and against the oracle."""
+    print(f"[case] prefill attention key groups, start {start}, {n} rows", flush=True)
+    cfg = tiny(TYPE_Q8_0, TYPE_Q8_0, dim=512, hidden_dim=1024, n_heads=8, n_kv_heads=2,
+               max_seq=256)
+    model, ref, cfg = make_pair(ctx, cfg, 340 + start)
+    toks = [int(t) for t in synth.random_tokens(341 + start, start + n, cfg["vocab_size"])]
+    if start:
+        model.forward(toks[:start], 0, want_logits=False)
+    two, _ = model.forward_batch(toks[start:], start)
+    monkeypatch.setenv("PBX_PREFILL_ATTN_GROUPS", "1")
+    one, _ = model.forward_batch(toks[start:], start)
+    monkeypatch.delenv("PBX_PREFILL_ATTN_GROUPS")
+    r = ref.forward(toks, 0)
+    d = float(np.abs(two - one).max())
+    err = float(np.abs(two[-1] - r).max())
+    print(f"  two groups vs one max-abs {d:.2e}, last row vs oracle {err:.2e}")
+    assert d <= 1e-4
+    assert err <= LOGIT_TOL
+    model.free()
+    ref.close()
+
+
 def test_prefill_gqa_untied_head(ctx):
     print("[case] batched prefill, GQA 6/2, untied Q8_0 head, head_dim 48", flush=True)
     cfg = tiny(TYPE_Q8_0, TYPE_F32, dim=288, hidden_dim=768, n_heads=6, n_kv_heads=2,
