@@ -1628,9 +1628,10 @@ static int prefill_batched(pbx_model *m, const int32_t *tokens, int n, int start
   if (hipMemcpyAsync(m->x, m->bx + (size_t)(n - 1) * m->cfg.dim, (size_t)m->cfg.dim * 4,
                      hipMemcpyDeviceToDevice, m->c->stream) != hipSuccess)
     return pbx_fail(m->c, PBX_EHIP, "model: residual copy failed");
-  const size_t k = m->ops.size();
-  if ((rc = enqueue_op(m, m->ops[k - 2]))) return rc;  // lm_head
-  return enqueue_op(m, m->ops[k - 1]);                 // argmax
+  // the LM head and the argmax
+  for (size_t i = m->layer_op[m->cfg.n_layers]; i < m->ops.size(); ++i)
+    if ((rc = enqueue_op(m, m->ops[i]))) return rc;
+  return PBX_OK;
 }
 
 static bool batched_prefill_enabled() {
