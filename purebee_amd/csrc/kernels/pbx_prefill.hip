@@ -41,6 +41,22 @@ pbx_embed_rows(const uint8_t *qs, const uint16_t *dsc, const uint16_t *msc, cons
   x[(size_t)t * dim + i] = row_value(qs, dsc, msc, type, tok, i, dim);
 }
 
+// The same for at most 16 rows with the tokens passed by value (a short
+// verify: no memory read before the embedding).
+struct TokRows {
+  int t[16];
+};
+extern "C" __global__ void __launch_bounds__(256)
+pbx_embed_rows_arg(const uint8_t *qs, const uint16_t *dsc, const uint16_t *msc, TokRows toks,
+                   float *x, int type, int dim, int vocab) {
+  const int t = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= dim || t >= 16) return;
+  int tok = toks.t[t];
+  if (tok < 0 || tok >= vocab) tok = 0;
+  x[(size_t)t * dim + i] = row_value(qs, dsc, msc, type, tok, i, dim);
+}
+
 // RMSNorm of rows (engine.js:429-449): out[t] = x[t] * (1/rms) * w.
 extern "C" __global__ void __launch_bounds__(256)
 pbx_rmsnorm_rows(const float *x, const float *w, float *out, int dim, float eps) {

@@ -1441,13 +1441,25 @@ static int fused_residual_norm(pbx_model *m, const pbx_gemm_plan *p, int M, int 
 static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, int nl) {
   pbx_ctx *c = m->c;
   const pbx_model_config &g = m->cfg;
-  // the embedding kernel reads the tokens from the pinned buffer (once the
-  // previous kernel that read it is done)
-  if (hipEventSynchronize(m->tok_ev) != hipSuccess)
-    return pbx_fail(c, PBX_EHIP, "model: token staging wait failed");
-  memcpy(m->h_tok, tokens, (size_t)n * 4);
   int rc;
-  {
+  if (n <= 16) {
+    // a short batch: the tokens as a kernel argument
+    struct {
+      int32_t t[16];
+    } toks = {};
+    memcpy(toks.t, tokens, (size_t)n * 4);
+    const void *qs = m->embd->qs, *dsc = m->embd->d, *msc = m->embd->m;
+    float *x = m->bx;
+    int type = kernel_type(m->embd->type), dim = g.dim, vocab = g.vocab_size;
+    void *args[] = {(void *)&qs, (void *)&dsc, (void *)&msc, &toks, &x, &type, &dim, &vocab};
+    if ((rc = launch_k(m, "pbx_embed_rows_arg", dim3((g.dim + 255) / 256, n), dim3(256), args)))
+      return rc;
+  } else {
+    // the embedding kernel reads the tokens from the pinned buffer (once the
+    // previous kernel that read it is done)
+    if (hipEventSynchronize(m->tok_ev) != hipSuccess)
+      return pbx_fail(c, PBX_EHIP, "model: token staging wait failed");
+    memcpy(m->h_tok, tokens, (size_t)n * 4);
     const void *qs = m->embd->qs, *dsc = m->embd->d, *msc = m->embd->m;
     int *tok = m->d_tok;
     float *x = m->bx;
