@@ -179,11 +179,12 @@ struct pbx_model {
   bool graph_tried = false, graph_ok = false;
   // pbx_model_generate: graph_steps whole steps captured back to back in one
   // graph (the steps chain through the device state), which saves the gap
-  // between graph launches; PBX_GRAPH_STEPS at creation (<= 1: off)
-  int graph_steps = 4;
-  hipGraph_t graph_k = nullptr;
-  hipGraphExec_t exec_k = nullptr;
-  bool graph_k_tried = false, graph_k_ok = false;
+  // between graph launches, and a 4-step graph for shorter remainders (a
+  // speculative draft of 4); PBX_GRAPH_STEPS at creation (<= 1: off)
+  int graph_steps = 8;
+  hipGraph_t graph_k = nullptr, graph_k4 = nullptr;
+  hipGraphExec_t exec_k = nullptr, exec_k4 = nullptr;
+  bool graph_k_tried = false, graph_k_ok = false, graph_k4_tried = false, graph_k4_ok = false;
   // steps that stop after the first L < n_layers layers (forward with
   // maxLayers), one captured graph per L, made on first use
   struct PartGraph {
@@ -698,9 +699,11 @@ static void drop_graph(pbx_model *m) {
   m->graph_tried = m->graph_ok = false;
   if (m->exec_k) hipGraphExecDestroy(m->exec_k);
   if (m->graph_k) hipGraphDestroy(m->graph_k);
-  m->exec_k = nullptr;
-  m->graph_k = nullptr;
-  m->graph_k_tried = m->graph_k_ok = false;
+  if (m->exec_k4) hipGraphExecDestroy(m->exec_k4);
+  if (m->graph_k4) hipGraphDestroy(m->graph_k4);
+  m->exec_k = m->exec_k4 = nullptr;
+  m->graph_k = m->graph_k4 = nullptr;
+  m->graph_k_tried = m->graph_k_ok = m->graph_k4_tried = m->graph_k4_ok = false;
   for (auto &p : m->part) {
     if (p.exec) hipGraphExecDestroy(p.exec);
     if (p.graph) hipGraphDestroy(p.graph);
@@ -781,22 +784,34 @@ static int run_step_layers(pbx_model *m, int L) {
 static int run_step(pbx_model *m) { return run_step_layers(m, m->cfg.n_layers); }
 
 // Up to `left` whole decode steps: graph_steps of them in one graph launch
-// when that graph is available, else one step.  *done: the steps enqueued.
+// when that graph is available, else 4 in one launch, else one step.
+// *done: the steps enqueued.
 static int run_steps(pbx_model *m, int left, int *done) {
   *done = 1;
-  if (m->graph_steps > 1 && left >= m->graph_steps && use_graphs()) {
+  struct Multi {
+    int steps;
+    hipGraph_t *graph;
+    hipGraphExec_t *exec;
+    bool *tried, *ok;
+  } multi[2] = {
+      {m->graph_steps, &m->graph_k, &m->exec_k, &m->graph_k_tried, &m->graph_k_ok},
+      {4, &m->graph_k4, &m->exec_k4, &m->graph_k4_tried, &m->graph_k4_ok}};
+  for (int i = 0; i < 2; ++i) {
+    const Multi &g = multi[i];
+    if (g.steps <= 1 || left < g.steps || !use_graphs() || (i == 1 && m->graph_steps <= 4))
+      continue;
     if (!m->ops_ready) {
       int rc = build_ops(m);
       if (rc) return rc;
     }
-    if (!m->graph_k_tried) {
-      m->graph_k_tried = true;
-      m->graph_k_ok = capture_step(m, m->cfg.n_layers, &m->graph_k, &m->exec_k, m->graph_steps);
+    if (!*g.tried) {
+      *g.tried = true;
+      *g.ok = capture_step(m, m->cfg.n_layers, g.graph, g.exec, g.steps);
     }
-    if (m->graph_k_ok) {
-      if (hipGraphLaunch(m->exec_k, m->c->stream) != hipSuccess)
+    if (*g.ok) {
+      if (hipGraphLaunch(*g.exec, m->c->stream) != hipSuccess)
         return pbx_fail(m->c, PBX_EHIP, "model: hipGraphLaunch failed");
-      *done = m->graph_steps;
+      *done = g.steps;
       return PBX_OK;
     }
   }
