@@ -678,8 +678,8 @@ def main():
         print(json.dumps(res, indent=1))
         return
     if args.gpus != 1:
-        print("bench.py: this backend runs on one GPU; multi-GPU runs are not part of this "
-              "build (DESIGN.md describes how the path would shard)", file=sys.stderr)
+        print("bench.py: this backend runs on one GPU; runs over several GPUs are not "
+              "supported", file=sys.stderr)
         sys.exit(2)
     if args.workload == "decode" and PROMPT + args.steps > 1024:
         print("bench.py: --steps must keep the KV cache within 1024 positions", file=sys.stderr)
