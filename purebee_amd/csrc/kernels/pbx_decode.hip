@@ -96,6 +96,9 @@ DK_INT_GU(PBX_Q4, q4, 16, 4, 1)
 DK_INT_S(PBX_Q4, q4, 16, 4, 1, 0, 2, p2, PRO_RMSNORM, EPI_SWIGLU, gu)
 // after pbx_attention_o_*: the input is x + the pending update
 DK_INT_S(PBX_Q4, q4, 16, 4, 1, 0, 2, p2, PRO_RMSACC, EPI_SWIGLU, gua)
+// the same with 8 builder waves beside 8 row waves of 8 rows (4 requested
+// before the limb barrier): the default gate|up after the fused attention
+DK_INT_S(PBX_Q4, q4, 8, 8, 1, 8, 4, w8p4, PRO_RMSACC, EPI_SWIGLU, gua)
 DK_INT_GU(PBX_Q4, q4, 8, 4, 2)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 1)
 DK_INT_GU(PBX_Q8, q8, 8, 4, 2)

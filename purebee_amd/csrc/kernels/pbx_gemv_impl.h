@@ -894,8 +894,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   static_assert(!LOOP || EPI == EPI_ARGMAX || EPI == EPI_STORE, "tile loop epilogues");
   static_assert(MR == 1 || EPI != EPI_ARGMAX, "argmax keys for one row");
   static_assert(EPI != EPI_ROPE || (MR == 1 && !LOOP && RT % 2 == 0), "RoPE rows in pairs");
-  static_assert(PRO != PRO_RMSACC || (MR == 1 && BW == 0 && !LOOP),
-                "pending update: one activation row, built by the row waves");
+  static_assert(PRO != PRO_RMSACC || (MR == 1 && !LOOP), "pending update: one activation row");
   static_assert(EPI != EPI_ADDACC || (MR == 1 && !LOOP), "pending update: one activation row");
   constexpr bool RMS = PRO == PRO_RMSNORM || PRO == PRO_RMSACC;
   constexpr int QB = BlockTraits<TYPE>::QB;
@@ -967,21 +966,30 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
       constexpr int CPB = IB * 8 / BW;
       const int qd = lane & 7;
       float4 xv[CPB], nv[CPB];
+      i64x2_t qv[PRO == PRO_RMSACC ? CPB : 1][2];  // PRO_RMSACC: the pending update
 #pragma unroll
       for (int c = 0; c < CPB; ++c) {
         const int e0 = (wave_hw + BW * c) * 256 + lane * 4;
         const int ec = e0 < K ? e0 : 0;
         xv[c] = *reinterpret_cast<const float4 *>(X + ec);
         nv[c] = make_float4(1.f, 1.f, 1.f, 1.f);
-        if constexpr (PRO == PRO_RMSNORM) nv[c] = *reinterpret_cast<const float4 *>(a.normw + ec);
+        if constexpr (RMS) nv[c] = *reinterpret_cast<const float4 *>(a.normw + ec);
+        if constexpr (PRO == PRO_RMSACC) {
+          qv[c][0] = *reinterpret_cast<const i64x2_t *>(a.acc + ec);
+          qv[c][1] = *reinterpret_cast<const i64x2_t *>(a.acc + ec + 2);
+        }
       }
       float sq = 0.f;
 #pragma unroll
       for (int c = 0; c < CPB; ++c) {
         const int b = (wave_hw + BW * c) * 8 + (lane >> 3);
         const bool ok = b < B;
-        const float4 t = ok ? xv[c] : make_float4(0.f, 0.f, 0.f, 0.f), w = nv[c];
-        if constexpr (PRO == PRO_RMSNORM)
+        float4 t = ok ? xv[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 w = nv[c];
+        if constexpr (PRO == PRO_RMSACC)
+          t = make_float4(residual_acc(t.x, qv[c][0].x), residual_acc(t.y, qv[c][0].y),
+                          residual_acc(t.z, qv[c][1].x), residual_acc(t.w, qv[c][1].y));
+        if constexpr (RMS)
           sq = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, sq))));
         const float4 p = make_float4(t.x * w.x, t.y * w.y, t.z * w.z, t.w * w.w);
         float mx = fmaxf(fmaxf(fabsf(p.x), fabsf(p.y)), fmaxf(fabsf(p.z), fabsf(p.w)));
@@ -1006,7 +1014,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
           }
         }
       }
-      if constexpr (PRO == PRO_RMSNORM) {
+      if constexpr (RMS) {
         sq = wave_sum(sq);
         if (lane == 0) ssqb[wave_hw] = sq;
       }

@@ -289,14 +289,23 @@ static bool int_shape(bool enabled, const char *mode, const char *role, int type
   }
   if (type != PBX_TYPE_Q4_0 && type != PBX_TYPE_Q8_0) return false;
   if (int_override(role, sh)) return sh->bw > 0 || sh->ib <= sh->wv;
-  if (strcmp(mode, "gu") == 0) {
+  if (strcmp(mode, "gu") == 0 || strcmp(mode, "gua") == 0) {
     if (B > 128) return false;
     sh->rt = 4;
-    // 16 waves only for Q4_0 with one block per lane (register budget); their
-    // first two rows requested before the limb barrier
     if (type == PBX_TYPE_Q4_0 && sh->ib == 1 && N / 64 >= 256) {
-      sh->wv = 16;
-      sh->pre = 2;
+      if (mode[2] == 'a') {
+        // input x + pending update: 8 builder waves beside 8 row waves of 8
+        // rows, whose first four are requested before the limb barrier
+        sh->wv = 8;
+        sh->rt = 8;
+        sh->bw = 8;
+        sh->pre = 4;
+      } else {
+        // 16 waves only for Q4_0 with one block per lane (register budget);
+        // their first two rows requested before the limb barrier
+        sh->wv = 16;
+        sh->pre = 2;
+      }
     } else {
       sh->wv = 8;
     }
@@ -378,10 +387,9 @@ static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const c
   op.kind = ARG_GEMV;
   std::string shape;
   int n_tiles = 0;
-  // qkvr (RoPE + cache append epilogue) is planned as qkv, gua (input x +
-  // pending update) as gu, adda (folds the update in) as add
+  // qkvr (RoPE + cache append epilogue) is planned as qkv, adda (folds the
+  // pending update in) as add; gua (input x + pending update) has its own
   const char *plan_mode = strcmp(mode, "qkvr") == 0 ? "qkv"
-                          : strcmp(mode, "gua") == 0 ? "gu"
                           : strcmp(mode, "adda") == 0 ? "add"
                                                       : mode;
   plan_gemv(c, m->gemv_int, plan_mode, role, w->type, (int)w->N, (int)w->B, &shape, &op.grid,
@@ -400,9 +408,9 @@ static int add_gemv(pbx_model *m, const pbx_weight *w, const char *mode, const c
   // (+ the pending update: read by gua, read and cleared by adda)
   op.bytes = (double)w->N * pbx_type_row_bytes(w->type, w->K) + 4.0 * w->K * (X2 ? 2 : 1) +
              (normw ? 4.0 * w->K : 0.0) +
-             (strcmp(plan_mode, "add") == 0 ? 8.0 * w->N
-              : strcmp(plan_mode, "gu") == 0 ? 2.0 * w->N
-                                             : 4.0 * w->N) +
+             (strcmp(plan_mode, "add") == 0                                  ? 8.0 * w->N
+              : strcmp(plan_mode, "gu") == 0 || strcmp(plan_mode, "gua") == 0 ? 2.0 * w->N
+                                                                              : 4.0 * w->N) +
              (strcmp(mode, "gua") == 0 ? 8.0 * w->K : strcmp(mode, "adda") == 0 ? 16.0 * w->N : 0.0);
   if (n_tiles_out) *n_tiles_out = n_tiles;
   m->ops.push_back(op);
@@ -491,7 +499,7 @@ static int build_ops(pbx_model *m) {
                                          "_" + mode) != nullptr;
       };
       fattno = pbx_kernel_by_name(c, "pbx_attention_o_c" + std::to_string(ipt));
-      if (fattno && variant(m->layers[0].wgu, "gu", "gua", "gate_up") &&
+      if (fattno && variant(m->layers[0].wgu, "gua", "gua", "gate_up") &&
           variant(m->layers[0].wd, "add", "adda", "down"))
         o_ipt = ipt;
     }

@@ -256,7 +256,7 @@ def test_fused_attention_o_matches_separate_o(ctx, monkeypatch, ipt, qa):
     plain_kern = {k for _, k, _, _ in plain.profile(toks[-1], len(toks), 1)}
     print(f"  fused vs separate max-abs {worst:.2e}, vs oracle {err:.2e}")
     assert (f"pbx_qkvr_attn_o_r{4 * ipt}c{ipt}" if qa else f"pbx_attention_o_c{ipt}") in kern
-    assert "pbx_dk_q4_i16x4b1p2_gua" in kern
+    assert "pbx_dk_q4_i8x8b1w8p4_gua" in kern
     assert "pbx_attention_head_c" in plain_kern
     assert worst <= 1e-4
     assert err <= LOGIT_TOL
