@@ -114,6 +114,7 @@ DK_INT_ADD(PBX_Q4, q4, 4, 2, 2)
 DK_INT_ADD(PBX_Q4, q4, 4, 2, 4)
 DK_INT_S(PBX_Q4, q4, 4, 2, 4, 8, 2, w8, PRO_NONE, EPI_ADD, add)
 DK_INT_S(PBX_Q4, q4, 4, 2, 4, 8, 2, w8, PRO_NONE, EPI_ADDACC, adda)  // folds the update in
+DK_INT_S(PBX_Q4, q4, 4, 2, 4, 4, 2, w4, PRO_NONE, EPI_ADDACC, adda)
 DK_INT_S(PBX_Q4, q4, 4, 2, 4, 4, 2, w4, PRO_NONE, EPI_ADD, add)
 DK_INT_ADD(PBX_Q4, q4, 4, 1, 1)
 DK_INT_ADD(PBX_Q4, q4, 4, 1, 4)

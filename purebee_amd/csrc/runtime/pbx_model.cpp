@@ -319,7 +319,7 @@ static bool int_shape(bool enabled, const char *mode, const char *role, int type
   }
   if (strcmp(mode, "add") == 0) {
     sh->rt = 2;
-    if (sh->ib == 4) sh->bw = 8;  // K = 8192 (down): 8 builder waves
+    if (sh->ib == 4) sh->bw = 4;  // K = 8192 (down): 4 builder waves (8: +0.4 us a token)
     return sh->ib != 3;
   }
   if (strcmp(mode, "lmh") == 0) {  // K = 2048: 8-row waves with the tile loop
