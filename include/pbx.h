@@ -38,6 +38,9 @@ extern "C" {
 #define PBX_ENOTSUP  -5   /* shape or type not supported by any kernel       */
 #define PBX_ELOAD    -6   /* code object missing or not loadable (hipModuleLoad) */
 #define PBX_EIO      -7   /* a file could not be opened or mapped            */
+#define PBX_ETIMEOUT -8   /* a bounded device-side wait gave up: data that one
+                             workgroup publishes for another inside a launch
+                             never arrived; the call's results are invalid   */
 
 /* ---- weight types ----------------------------------------------------
  * GGML numbering, as gguf.js:30-33 (GGML_TYPE).  PBX_TYPE_Q8_REF is the
@@ -278,6 +281,14 @@ int pbx_model_info(const pbx_model *m, size_t *device_bytes, int *uses_graph);
 int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int n_steps,
                       double *op_us, double *op_bytes, int cap, int *n_ops);
 int pbx_model_op_name(const pbx_model *m, int i, char *buf, size_t cap);
+/* Test hook, no reference counterpart: makes the attention workgroups of
+ * layer `layer`'s joined q|k|v + attention launch wait for cells tagged
+ * `skew` epochs ahead (none ever are), giving up after `spin` polls (0: the
+ * kernel's default), so that the bounded wait's error path can be tested
+ * with every kernel still exiting normally; the call then fails with
+ * PBX_ETIMEOUT.  layer < 0 restores the normal launch.  Returns
+ * PBX_ENOTSUP when the model's step has no such launch. */
+int pbx_model_test_handoff(pbx_model *m, int layer, int skew, int spin);
 /* Measurement: the GEMV kernels of one role ("qkv", "o", "gate_up", "down",
  * "lm_head") launched back to back over every layer's weights, `reps`
  * passes between two HIP events on the model's stream; returns the mean

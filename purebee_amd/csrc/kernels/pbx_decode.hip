@@ -263,6 +263,11 @@ struct AttnArgs {
   // workgroups ([qdim | kv_dim | kv_dim] cells, the epoch at [cell_n])
   const unsigned long long *cells;
   int cell_n, qdim;
+  // pbx_qkvr_attn_o_*: the model's device status word (a wait that gives
+  // up ORs PBX_DEV_WAIT_TIMEOUT into it), the poll limit (0: PBX_CELL_SPIN)
+  // and a tag offset that only a test sets (the cells then never match)
+  int *status;
+  int spin, skew;
 };
 
 // One workgroup per query head (llama.js:258-301 / llama-streaming.js:543-573):
@@ -712,16 +717,24 @@ __device__ __forceinline__ void xcd_head(int b, int n_heads, int &h, int &s) {
 // (value bits tagged with the layer's epoch + 1; a cell that has not
 // arrived after PBX_CELL_SPIN polls gives NaN) and pass them on through LDS.
 #define PBX_CELL_SPIN (1 << 16)
-// Polls a published cell until it carries `tag` (NaN after PBX_CELL_SPIN
-// polls).  One load at a time: three in flight, one every ~200 ns, made the
-// decode step slower (353.3 against 349.0 us a token).
-__device__ __forceinline__ float poll_cell(const unsigned long long *cp, unsigned tag) {
+// Bit of the model's status word set by a bounded wait that gave up; the
+// host reads the word after the call's work and reports a timeout.
+#define PBX_DEV_WAIT_TIMEOUT 1
+// Polls a published cell until it carries `tag`.  After `spin` polls it
+// gives up: the value is NaN and PBX_DEV_WAIT_TIMEOUT goes into the status
+// word, so the host reports the call as failed instead of returning the
+// NaN results.  One load at a time: three in flight, one every ~200 ns,
+// made the decode step slower (353.3 against 349.0 us a token).
+__device__ __forceinline__ float poll_cell(const unsigned long long *cp, unsigned tag, int spin,
+                                           int *status) {
   unsigned long long v = __hip_atomic_load(cp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int it = 0; (unsigned)(v >> 32) != tag && it < PBX_CELL_SPIN; ++it) {
+  for (int it = 0; (unsigned)(v >> 32) != tag && it < spin; ++it) {
     __builtin_amdgcn_s_sleep(1);
     v = __hip_atomic_load(cp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  return (unsigned)(v >> 32) == tag ? __uint_as_float((unsigned)v) : __builtin_nanf("");
+  if ((unsigned)(v >> 32) == tag) return __uint_as_float((unsigned)v);
+  __hip_atomic_fetch_or(status, PBX_DEV_WAIT_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_nanf("");
 }
 
 template <bool SPEC, int IPT = 0, bool FUSED = false>
@@ -778,12 +791,14 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   int s0 = 0;
   if constexpr (FUSED) {
-    const unsigned tag = (unsigned)a.cells[a.cell_n] + 1u;
+    const unsigned tag = cell_tag(a.cells[a.cell_n]) + (unsigned)a.skew;
+    const int spin = a.spin > 0 ? a.spin : PBX_CELL_SPIN;
     float4 kn = make_float4(0.f, 0.f, 0.f, 0.f), vn = kn;
     auto ready = [&]() {
       if (w < 3) {  // wave 0: q of head h; 1, 2: k, v of KV head g
         nrow[w][lane] =
-            poll_cell(a.cells + (w == 0 ? h * hd : a.qdim + (w - 1) * kvdim + g * hd) + lane, tag);
+            poll_cell(a.cells + (w == 0 ? h * hd : a.qdim + (w - 1) * kvdim + g * hd) + lane, tag,
+                      spin, a.status);
       }
       lds_barrier();
       const float4 q4 = *reinterpret_cast<const float4 *>(&nrow[0][dcol]);

@@ -473,6 +473,15 @@ __device__ __forceinline__ float wave_transpose_reduce(float (&v)[R], int lane) 
   return wave_sum<(64 / R) / 2>(v[0]);
 }
 
+// The tag that a launch of epoch e publishes its cells with: never 0 (the
+// tag of cleared cells), and next_epoch skips the epoch whose tag would wrap
+// to 0, so consecutive launches always publish different tags.
+__device__ __forceinline__ unsigned cell_tag(unsigned long long e) { return (unsigned)e + 1u; }
+__device__ __forceinline__ unsigned long long next_epoch(unsigned long long e) {
+  const unsigned long long n = e + 1;
+  return cell_tag(n) == 0u ? n + 1 : n;
+}
+
 // x + q * 2^-32 rounded once: the residual row with its pending
 // fixed-point update (PRO_RMSACC and EPI_ADDACC form the same value).
 __device__ __forceinline__ float residual_acc(float x, long long q) {
@@ -955,9 +964,9 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   // carries its own epoch, so no ordering between cells is needed)
   unsigned pub_tag = 0;
   if constexpr (EPI == EPI_ROPE)
-    if (a.xcell) pub_tag = (unsigned)a.xcell[N] + 1u;
+    if (a.xcell) pub_tag = cell_tag(a.xcell[N]);
   if constexpr (EPI == EPI_ADDACC)
-    if (a.xcell && blockIdx.x == 0 && threadIdx.x == 0) a.xcell[0] += 1;
+    if (a.xcell && blockIdx.x == 0 && threadIdx.x == 0) a.xcell[0] = next_epoch(a.xcell[0]);
 
   if constexpr (BW > 0) {
     if (wave < 0) {

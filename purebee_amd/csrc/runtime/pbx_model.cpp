@@ -42,6 +42,10 @@ struct AttnArgsHost {  // AttnArgs in pbx_decode.hip
   // pbx_qkvr_attn_o_*: the GEMV's published rows and their epoch at [cell_n]
   const unsigned long long *cells = nullptr;
   int cell_n = 0, qdim = 0;
+  // the status word a bounded wait marks when it gives up, the poll limit
+  // (0: the kernel's default) and the test-only tag offset
+  int *status = nullptr;
+  int spin = 0, skew = 0;
 };
 
 struct AttnSplitArgsHost {  // AttnSplitArgs in pbx_decode.hip
@@ -165,7 +169,12 @@ struct pbx_model {
   // layer's epoch ((qkv_rows + 64) cells, allocated with the first step)
   bool qkv_attn = true;
   unsigned long long *qa_cells = nullptr;
+  // state[0] position, [1] token, [2] step, [3] status word (bits set by
+  // device-side waits that gave up; read and cleared by the host calls)
   int *state = nullptr;
+  // pbx_model_test_handoff: the fused launch of layer test_layer waits for
+  // tags offset by test_skew, with at most test_spin polls (0: default)
+  int test_layer = -1, test_skew = 0, test_spin = 0;
   int *hist = nullptr;
   int hist_cap = 0;
   std::vector<Op> ops;
@@ -573,6 +582,11 @@ static int build_ops(pbx_model *m) {
         a.attn.cells = cells;
         a.attn.cell_n = m->qkv_rows;
         a.attn.qdim = g.dim;
+        a.attn.status = m->state + 3;
+        if (l == m->test_layer) {
+          a.attn.skew = m->test_skew;
+          a.attn.spin = m->test_spin;
+        }
         a.fixed_bytes += q.bytes;
       }
       m->ops.push_back(a);
@@ -750,6 +764,8 @@ static bool capture_step(pbx_model *m, int L, hipGraph_t *graph, hipGraphExec_t 
     if (!rc && e == hipSuccess && g && hipGraphInstantiate(exec, g, nullptr, nullptr, 0) == hipSuccess) {
       *graph = g;
       ok = true;
+      // the executable's one-time device set-up now, not in its first launch
+      (void)hipGraphUpload(*exec, s);
     } else if (g) {
       hipGraphDestroy(g);
     }
@@ -852,6 +868,47 @@ static int kv_fill(pbx_model *m, int from) {
   const int64_t total = count * nl;
   return pbx_launch_fn(m->c, f, "pbx_kv_fill", dim3((unsigned)((total + 255) / 256)), dim3(256),
                        args, m->c->stream);
+}
+
+// After a call's work has been synchronised: st is the device state copied
+// with it.  A bounded device-side wait that gave up (a hand-off between the
+// workgroups of a launch whose data never arrived) marks the status word;
+// its results are then NaN, so the call fails with PBX_ETIMEOUT instead of
+// returning them.  The word is cleared for the next call.
+static int check_status(pbx_model *m, const int *st, const char *who) {
+  if (!st[3]) return PBX_OK;
+  if (hipMemsetAsync(m->state + 3, 0, 4, m->c->stream) != hipSuccess ||
+      hipStreamSynchronize(m->c->stream) != hipSuccess)
+    return pbx_fail(m->c, PBX_EHIP, "%s: clearing the device status failed", who);
+  return pbx_fail(m->c, PBX_ETIMEOUT,
+                  "%s: a device-side wait for data published inside a launch gave up "
+                  "(status 0x%x); the results of this call are invalid",
+                  who, (unsigned)st[3]);
+}
+
+// Captures every step graph pbx_model_generate replays (one step, the
+// multi-step graph and the 4-step one), so that no capture happens inside
+// a timed or latency-sensitive generate call.
+static int prepare_graphs(pbx_model *m) {
+  if (!use_graphs()) return PBX_OK;
+  if (!m->ops_ready) {
+    int rc = build_ops(m);
+    if (rc) return rc;
+  }
+  const int nl = m->cfg.n_layers;
+  if (!m->graph_tried) {
+    m->graph_tried = true;
+    m->graph_ok = capture_step(m, nl, &m->graph, &m->exec);
+  }
+  if (m->graph_steps > 1 && !m->graph_k_tried) {
+    m->graph_k_tried = true;
+    m->graph_k_ok = capture_step(m, nl, &m->graph_k, &m->exec_k, m->graph_steps);
+  }
+  if (m->graph_steps > 4 && !m->graph_k4_tried) {
+    m->graph_k4_tried = true;
+    m->graph_k4_ok = capture_step(m, nl, &m->graph_k4, &m->exec_k4, 4);
+  }
+  return PBX_OK;
 }
 
 static int dalloc(pbx_model *m, void **p, size_t bytes) {
@@ -992,6 +1049,8 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
   m->n_partials_cap = g.vocab_size + 256;  // at most one tile per row (+ small-kernel slack)
   if (!rc) rc = dalloc(m, (void **)&m->partials, (size_t)m->n_partials_cap * 8);
   if (!rc) rc = dalloc(m, (void **)&m->state, 64);
+  if (!rc && hipMemsetAsync(m->state, 0, 64, c->stream) != hipSuccess)
+    rc = pbx_fail(c, PBX_EHIP, "pbx_model_create: clearing the device state failed");
   m->hist_cap = g.max_seq;
   if (!rc) rc = dalloc(m, (void **)&m->hist, (size_t)m->hist_cap * 4);
   // Split-position attention when its tiles fit (head_dim <= 128, <= 16
@@ -1713,10 +1772,11 @@ extern "C" int pbx_model_forward_layers(pbx_model *m, const int32_t *tokens, int
   if (logits && hipMemcpyAsync(logits, m->logits, (size_t)g.vocab_size * 4,
                                hipMemcpyDeviceToHost, c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward: logits copy failed");
-  int st[3] = {0, 0, 0};
+  int st[4] = {0, 0, 0, 0};
   if (hipMemcpyAsync(st, m->state, sizeof st, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
       hipStreamSynchronize(c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_forward: step failed on the device");
+  if ((rc = check_status(m, st, "pbx_model_forward"))) return rc;
   if (next_token) *next_token = st[1];
   return PBX_OK;
 }
@@ -1800,6 +1860,7 @@ extern "C" int pbx_model_generate(pbx_model *m, int32_t token, int start_pos, in
   if (rc) return rc;
   if (hipSetDevice(c->device) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_generate: hipSetDevice failed");
+  if ((rc = prepare_graphs(m))) return rc;
   if ((rc = set_state(m, start_pos, token, 0, true))) return rc;
   for (int i = 0, k = 0; i < n_steps; i += k)
     if ((rc = run_steps(m, n_steps - i, &k))) return rc;
@@ -1809,9 +1870,11 @@ extern "C" int pbx_model_generate(pbx_model *m, int32_t token, int start_pos, in
   if (last_logits && hipMemcpyAsync(last_logits, m->logits, (size_t)g.vocab_size * 4,
                                     hipMemcpyDeviceToHost, c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_generate: logits copy failed");
-  if (hipStreamSynchronize(c->stream) != hipSuccess)
+  int st[4] = {0, 0, 0, 0};
+  if (hipMemcpyAsync(st, m->state, sizeof st, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_generate: step failed on the device");
-  return PBX_OK;
+  return check_status(m, st, "pbx_model_generate");
 }
 
 // The greedy chain of pbx_model_generate with every step stopping after the
@@ -1836,11 +1899,13 @@ int pbx_model_generate_layers(pbx_model *m, int32_t token, int start_pos, int n_
   if ((rc = set_state(m, start_pos, token, 0, true))) return rc;
   for (int i = 0; i < n_steps; ++i)
     if ((rc = run_step_layers(m, nl))) return rc;
+  int st[4] = {0, 0, 0, 0};
   if (hipMemcpyAsync(out_tokens, m->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost,
                      c->stream) != hipSuccess ||
+      hipMemcpyAsync(st, m->state, sizeof st, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
       hipStreamSynchronize(c->stream) != hipSuccess)
     return pbx_fail(c, PBX_EHIP, "pbx_model_generate: step failed on the device");
-  return PBX_OK;
+  return check_status(m, st, "pbx_model_generate");
 }
 
 extern "C" int pbx_model_reset_cache(pbx_model *m) {
@@ -1931,6 +1996,13 @@ extern "C" int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int
     }
   }
   if (!rc) {
+    int st[4] = {0, 0, 0, 0};
+    if (hipMemcpy(st, m->state, sizeof st, hipMemcpyDeviceToHost) != hipSuccess)
+      rc = pbx_fail(c, PBX_EHIP, "pbx_model_profile: state copy failed");
+    else
+      rc = check_status(m, st, "pbx_model_profile");
+  }
+  if (!rc) {
     const int k = std::min(n, cap);
     for (int i = 0; i < k; ++i) {
       op_us[i] = acc[i] / n_steps;
@@ -1949,6 +2021,26 @@ extern "C" int pbx_model_op_name(const pbx_model *m, int i, char *buf, size_t ca
     return pbx_fail(m->c, PBX_EINVAL, "pbx_model_op_name: op %d out of range", i);
   snprintf(buf, cap, "%s:%s", m->ops[i].role.c_str(), m->ops[i].name.c_str());
   return PBX_OK;
+}
+
+extern "C" int pbx_model_test_handoff(pbx_model *m, int layer, int skew, int spin) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_test_handoff: not a live model");
+  if (layer >= m->cfg.n_layers || spin < 0)
+    return pbx_fail(m->c, PBX_EINVAL, "pbx_model_test_handoff: layer %d / spin %d out of range",
+                    layer, spin);
+  m->test_layer = layer;
+  m->test_skew = skew;
+  m->test_spin = spin;
+  // the kernels' arguments change: rebuild them and every captured graph
+  drop_graph(m);
+  m->ops_ready = false;
+  int rc = check_complete(m);
+  if (rc || (rc = build_ops(m))) return rc;
+  for (const Op &op : m->ops)
+    if (op.kind == ARG_FUSED) return PBX_OK;
+  return layer < 0 ? PBX_OK
+                   : pbx_fail(m->c, PBX_ENOTSUP,
+                              "pbx_model_test_handoff: the step has no joined q|k|v + attention launch");
 }
 
 extern "C" int pbx_model_bench_role(pbx_model *m, const char *role, int reps,

@@ -20,7 +20,9 @@ TYPE_Q6_K = 14
 TYPE_Q8_REF = 100
 
 STATUS = {0: "PBX_OK", -1: "PBX_EINVAL", -2: "PBX_ENODEV", -3: "PBX_ENOMEM",
-          -4: "PBX_EHIP", -5: "PBX_ENOTSUP", -6: "PBX_ELOAD"}
+          -4: "PBX_EHIP", -5: "PBX_ENOTSUP", -6: "PBX_ELOAD", -7: "PBX_EIO",
+          -8: "PBX_ETIMEOUT"}
+ETIMEOUT = -8
 
 # Every entry point declared in include/pbx.h.
 EXPORTS = (
@@ -35,7 +37,7 @@ EXPORTS = (
     "pbx_bench_linear_graph",
     "pbx_model_create", "pbx_model_free", "pbx_model_set_tensor", "pbx_model_forward",
     "pbx_model_forward_batch", "pbx_model_generate", "pbx_model_reset_cache", "pbx_model_rollback", "pbx_model_info",
-    "pbx_model_profile", "pbx_model_op_name", "pbx_model_bench_role",
+    "pbx_model_profile", "pbx_model_op_name", "pbx_model_bench_role", "pbx_model_test_handoff",
     "pbx_speculative_generate", "pbx_model_forward_layers", "pbx_self_speculative_generate",
     "pbx_gguf_open", "pbx_gguf_close", "pbx_gguf_info", "pbx_gguf_tensor_info",
     "pbx_gguf_find_tensor", "pbx_gguf_get_int", "pbx_gguf_get_float", "pbx_gguf_get_string",
@@ -165,6 +167,7 @@ def load_library():
         "pbx_model_generate": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int, ctypes.c_int, _vp, _vp]),
         "pbx_model_reset_cache": (ctypes.c_int, [_vp]),
         "pbx_model_rollback": (ctypes.c_int, [_vp, ctypes.c_int]),
+        "pbx_model_test_handoff": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
         "pbx_model_info": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_size_t),
                                           ctypes.POINTER(ctypes.c_int)]),
         "pbx_model_profile": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int, ctypes.c_int,
@@ -545,6 +548,12 @@ class Model:
 
     def rollback(self, pos):
         self._mcall("pbx_model_rollback", pos)
+
+    def test_handoff(self, layer, skew, spin=0):
+        """Test hook: the joined q|k|v + attention launch of `layer` waits
+        for cells that never arrive (tag offset `skew`), giving up after
+        `spin` polls; layer < 0 restores the normal launch."""
+        self._mcall("pbx_model_test_handoff", layer, skew, spin)
 
     def info(self):
         b, g = ctypes.c_size_t(), ctypes.c_int()

@@ -352,6 +352,43 @@ def test_non_finite_activation_propagates(ctx):
         ref.close()
 
 
+def test_handoff_wait_timeout_is_reported(ctx):
+    """The bounded wait of the joined q|k|v + attention launch: when the
+    cells it waits for never carry its tag (forced from the host by the test
+    hook, which offsets the tag the attention workgroups expect and caps
+    their polls at 64), every kernel still exits, and forward, generate and
+    the layer-limited forward fail with PBX_ETIMEOUT instead of returning
+    NaN logits or tokens picked from them.  With the hook removed the same
+    positions give the logits of an untouched run again, bit for bit."""
+    print("[case] forced hand-off timeout: forward / generate report PBX_ETIMEOUT", flush=True)
+    from purebee_amd.native import ETIMEOUT
+    cfg = tiny(TYPE_Q4_0, TYPE_Q4_0, dim=2048, hidden_dim=8192, n_layers=2, n_heads=32,
+               n_kv_heads=8, vocab_size=512, max_seq=64)
+    model = synth.build(ctx, cfg, 121)
+    toks = [int(t) for t in synth.random_tokens(122, 6, cfg["vocab_size"])]
+    good = [model.forward([t], p)[0] for p, t in enumerate(toks)]
+    kern = {k for _, k, _, _ in model.profile(toks[-1], len(toks), 1)}
+    assert any(k.startswith("pbx_qkvr_attn_o_") for k in kern)
+    model.rollback(4)
+    model.test_handoff(1, 1, 64)
+    with pytest.raises(PbxError) as e:
+        model.forward([toks[4]], 4)
+    assert e.value.code == ETIMEOUT and "gave up" in str(e.value)
+    with pytest.raises(PbxError) as e:
+        model.generate(toks[4], 4, 3)
+    assert e.value.code == ETIMEOUT
+    # only layer 1 waits: a forward through the first layer alone succeeds
+    model.rollback(4)
+    lg, _ = model.forward([toks[4]], 4, max_layers=1)
+    assert np.isfinite(lg).all()
+    model.test_handoff(-1, 0, 0)
+    model.rollback(4)
+    again = [model.forward([t], 4 + i)[0] for i, t in enumerate(toks[4:])]
+    assert np.array_equal(again[0], good[4]) and np.array_equal(again[1], good[5])
+    print("  timeouts reported; normal launch restored bit for bit")
+    model.free()
+
+
 @pytest.mark.parametrize("wt,et,dim,hidden,vocab", [(TYPE_Q4_0, TYPE_Q4_0, 2048, 1024, 40000),
                                                     (TYPE_Q4_0, TYPE_Q6_K, 2048, 1024, 40000),
                                                     (TYPE_Q8_0, TYPE_Q8_0, 2048, 1024, 512),
