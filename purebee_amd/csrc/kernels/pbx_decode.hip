@@ -962,6 +962,174 @@ PBX_QKVR_ATTN_O(4, 4, 4, , 1)
 PBX_QKVR_ATTN_O(4, 8, 4, , 2)
 #undef PBX_QKVR_ATTN_O
 
+// ---------------------------------------------------------------------------
+// The FFN of a layer in one launch (llama-streaming.js:583-606: RMSNorm,
+// w1/w3, silu(g) * u, w2 and the residual), for dim 2048, hidden 8192 and
+// Q4_0 (Llama-3.2-1B): 256 workgroups of 8 builder and 8 row waves.
+//
+// Gate|up: workgroup j is the integer-limb GEMV of gate rows and up rows
+// [32 j, 32 j + 32) (the builders form the limbs of RMSNorm(x + update), the
+// row waves stream 8 rows each) and publishes its 32 outputs h as 64-bit
+// cells, (epoch + 1) << 32 | value bits, by relaxed device-scope stores.
+//
+// Down: the 256 blocks of K are split into 8 slices of 32 blocks (1024
+// values of h, the outputs of workgroups [32 s, 32 s + 32)), the 2048 rows
+// into 32 tiles of 64; workgroup j takes slice s = j / 32 and tile j % 32,
+// so the workgroups that produce a slice also consume it.  Builder thread t
+// takes row 64 tile + t / 8 and the slice's blocks t % 8 + 8 i (i < 4): it
+// requests those W_down bytes as soon as the limbs of gate|up are built (a
+// row's 8 lanes read 128 contiguous bytes per block step).  Once the
+// workgroup's own outputs are out, 256 builder threads poll 4 consecutive
+// cells each until the slice's 1024 values carry the launch's tag, and turn
+// them into the same per-block 22-bit fixed point as the GEMV inputs (three
+// int8 limbs in LDS, read by 8 lanes at consecutive blocks: no bank
+// conflicts); the dots are v_dot4 over the nibble codes (the first form,
+// fp32 FMAs with 8 lanes a row at blocks 4 apart, spent 3.6 us in
+// conflicted LDS reads).  The 8 slices of a row meet in the row's count
+// cell (as the verify's split down projection: value biased by 2^51 in
+// 2^-32 units plus a count, no fence, independent of the arrival order),
+// and the add that completes the count stores x + update + sum into the
+// next residual row and clears the cell.  The cell waits are bounded like
+// the attention's: after `spin` polls the values are NaN and the status
+// word is marked.
+// ---------------------------------------------------------------------------
+struct FfnArgs {
+  const uint8_t *qs;          // W_down qs plane: 2048 rows of 256 blocks
+  const uint16_t *dsc;        // its scale plane
+  const float *x;             // the layer's residual row (the gate|up input)
+  const long long *acc;       // its pending attention update (2^-32 units)
+  unsigned long long *cell;   // [2048] count cells (zero between launches)
+  float *xout;                // the next residual row
+  unsigned long long *qepoch; // the layer's q|k|v epoch: advanced here
+  int *status;
+  int spin;
+};
+
+#define PBX_FFN_SLICES 8
+
+extern "C" __global__ void __launch_bounds__(1024) pbx_ffn_q4_d2048_h8192(GemvArgs g, FfnArgs f) {
+  constexpr int HID = 8192, KB = HID / 32, S = PBX_FFN_SLICES, SB = KB / S;  // 32 blocks a slice
+  constexpr int TILES = 256 / S;  // 32 tiles of 64 rows
+  // limb words 4q..4q+3 of slice block b at hl[L][q][b]; the block's exact
+  // sum of codes and its 2^(e_b - 21) (NaN: a non-finite value)
+  __shared__ int4 hl[3][2][SB];
+  __shared__ int hsum[SB];
+  __shared__ float hscale[SB];
+  const int j = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const int sl = j / TILES, tile = j % TILES;
+  const bool bld = tid < 512;  // the builder waves (gemv_int's first BW = 8 waves)
+  // no other workgroup reads the q|k|v epoch in this launch
+  if (j == 0 && tid == 0) *f.qepoch = next_epoch(*f.qepoch);
+  const unsigned tag = cell_tag(g.xcell[HID]);
+  gemv_int<PBX_Q4, 8, 8, 1, PRO_RMSACC, EPI_SWIGLU, false, 1, 8, 4>(g);
+
+  const int row = tile * 64 + ((tid & 511) >> 3), g8 = tid & 7, b0 = sl * SB + g8;
+  uint4 wq[4];
+  unsigned wd[4];
+  float xr = 0.f;
+  long long ar = 0;
+  if (bld) {
+    if (g8 == 0) {
+      xr = f.x[row];
+      ar = f.acc[row];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wd[i] = f.dsc[dsc_index(row, b0 + 8 * i, KB)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wq[i] = ld_stream(f.qs + ((size_t)row * KB + b0 + 8 * i) * 16);
+  }
+  lds_barrier();  // the workgroup's own gate|up outputs are published
+  if (tid < 256) {
+    // cells 4t .. 4t + 3 of the slice: float4 t % 8 of slice block t / 8
+    const unsigned long long *cp = g.xcell + sl * SB * 32 + 4 * tid;
+    unsigned long long v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = __hip_atomic_load(cp + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int spin = f.spin > 0 ? f.spin : PBX_CELL_SPIN;
+    auto missing = [&]() {
+      return (unsigned)(v[0] >> 32) != tag || (unsigned)(v[1] >> 32) != tag ||
+             (unsigned)(v[2] >> 32) != tag || (unsigned)(v[3] >> 32) != tag;
+    };
+    for (int it = 0; missing() && it < spin; ++it) {
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if ((unsigned)(v[k] >> 32) != tag)
+          v[k] = __hip_atomic_load(cp + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const bool ok = !missing();
+    if (!ok)
+      __hip_atomic_fetch_or(f.status, PBX_DEV_WAIT_TIMEOUT, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    const float4 p = ok ? make_float4(__uint_as_float((unsigned)v[0]), __uint_as_float((unsigned)v[1]),
+                                      __uint_as_float((unsigned)v[2]), __uint_as_float((unsigned)v[3]))
+                        : make_float4(NAN, NAN, NAN, NAN);
+    // the block's fixed point, as the GEMV builders form it (no norm weight)
+    const int qd = tid & 7, b = tid >> 3;
+    float mx = fmaxf(fmaxf(fabsf(p.x), fabsf(p.y)), fmaxf(fabsf(p.z), fabsf(p.w)));
+    float nf = fmaf(p.x, 0.f, fmaf(p.y, 0.f, fmaf(p.z, 0.f, p.w * 0.f)));
+    mx = group_max<8>(mx);
+    nf = group_sum<8>(nf);
+    int e = 0;
+    if (mx > 0.f && mx < INFINITY) frexpf(mx, &e);
+    e = max(e, -100);
+    int w0, w1, w2, sv;
+    limb_words(p, ldexpf(1.f, 21 - e), w0, w1, w2, sv);
+    const int st = group_isum<8>(sv);
+    reinterpret_cast<int *>(&hl[0][qd >> 2][b])[qd & 3] = w0;
+    reinterpret_cast<int *>(&hl[1][qd >> 2][b])[qd & 3] = w1;
+    reinterpret_cast<int *>(&hl[2][qd >> 2][b])[qd & 3] = w2;
+    if (qd == 0) {
+      hsum[b] = st;
+      hscale[b] = ldexpf(1.f, e - 21) + nf;
+    }
+  }
+  lds_barrier();
+  if (!bld) return;
+  // the row's dots over its 4 blocks: exact int32 per limb, then the block's
+  // scale and d (Q4_0's -8 offset: one 8 * sum(x_q) correction)
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int b = g8 + 8 * i;
+    int xl[3][8];
+#pragma unroll
+    for (int L = 0; L < 3; ++L) {
+      const int4 t0 = hl[L][0][b], t1 = hl[L][1][b];
+      xl[L][0] = t0.x; xl[L][1] = t0.y; xl[L][2] = t0.z; xl[L][3] = t0.w;
+      xl[L][4] = t1.x; xl[L][5] = t1.y; xl[L][6] = t1.z; xl[L][7] = t1.w;
+    }
+    const unsigned w4[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+    int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int lo = (int)(w4[k] & 0x0F0F0F0Fu), hi = (int)((w4[k] >> 4) & 0x0F0F0F0Fu);
+      s0 = sdot4(lo, xl[0][k], s0); s0 = sdot4(hi, xl[0][4 + k], s0);
+      s1 = sdot4(lo, xl[1][k], s1); s1 = sdot4(hi, xl[1][4 + k], s1);
+      s2 = sdot4(lo, xl[2][k], s2); s2 = sdot4(hi, xl[2][4 + k], s2);
+    }
+    const float c0 = hscale[b];
+    const float fb = fmaf((float)s2, 65536.f * c0,
+                          fmaf((float)s1, 256.f * c0, fmaf((float)s0, c0, -8.f * (float)hsum[b] * c0)));
+    acc = fmaf(fb, f16_bits_to_f32(wd[i]), acc);
+  }
+  acc += __shfl_xor(acc, 1, 64);
+  acc += __shfl_xor(acc, 2, 64);
+  acc += __shfl_xor(acc, 4, 64);
+  if (g8 != 0) return;
+  const bool bad = !(fabsf(acc) < 0x1p19f);
+  const unsigned long long c =
+      (1ull << 56) + (bad ? (1ull << 60) + (1ull << 51)
+                          : (unsigned long long)((1ll << 51) + (long long)rintf(acc * 0x1p32f)));
+  const unsigned long long t =
+      __hip_atomic_fetch_add(f.cell + row, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + c;
+  if (((t >> 56) & 15u) != (unsigned)S) return;
+  __hip_atomic_store(f.cell + row, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const long long v = (long long)(t & ((1ull << 56) - 1)) - (long long)S * (1ll << 51);
+  f.xout[row] = (t >> 60) ? __builtin_nanf("")
+                          : (float)fma((double)v, 0x1p-32, (double)residual_acc(xr, ar));
+}
+
 // Batched rows (speculative verify, short batches; head_dim <= 64): workgroup
 // (head, row t) at position start + t, after pbx_rope_append_rows has rotated
 // q and k of every row and appended k and v; the arguments of
@@ -1219,11 +1387,18 @@ struct ArgmaxArgs {
   int n_partials;
   int hist_cap;
   EmbedArgs emb;  // the embedding table and x
+  // the joined FFN's pending attention updates, cleared for the next step
+  // (clr_n 64-bit words; null: none)
+  long long *clr;
+  int clr_n;
 };
 
 extern "C" __global__ void __launch_bounds__(1024) pbx_argmax_final(ArgmaxArgs a) {
   __shared__ uint64_t red[16];
   __shared__ int tok_sh;
+  if (a.clr)
+    for (int i = threadIdx.x; 2 * i < a.clr_n; i += blockDim.x)
+      reinterpret_cast<i64x2_t *>(a.clr)[i] = i64x2_t{0, 0};
   uint64_t best = 0;
   for (int i = threadIdx.x; i < a.n_partials; i += blockDim.x) {
     const uint64_t k = a.partials[i];

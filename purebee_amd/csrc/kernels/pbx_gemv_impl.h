@@ -76,8 +76,16 @@ struct GemvArgs {
   // gemv_mr with the K split over workgroups: one cell per output element
   // [MR][N] (zero between launches).  gemv_int EPI_ROPE: N published rows
   // and the layer's epoch at [N] (the fused q|k|v + attention kernel);
-  // EPI_ADDACC: that epoch, advanced once per launch
+  // EPI_ADDACC: that epoch, advanced once per launch.  EPI_SWIGLU: N / 2
+  // published outputs and their epoch at [N / 2] (the joined FFN launch)
   unsigned long long *xcell;
+  // builder waves (BW > 0): clr_n 64-bit words of clr zeroed by the grid's
+  // builder threads after their build; adv: an epoch that thread 0 of
+  // workgroup 0 advances (both only for buffers no one else touches in the
+  // launch)
+  long long *clr;
+  int clr_n;
+  unsigned long long *adv;
 };
 
 namespace pbx {
@@ -965,6 +973,10 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   unsigned pub_tag = 0;
   if constexpr (EPI == EPI_ROPE)
     if (a.xcell) pub_tag = cell_tag(a.xcell[N]);
+  if constexpr (EPI == EPI_SWIGLU)
+    if (a.xcell) pub_tag = cell_tag(a.xcell[N / 2]);
+  if constexpr (BW > 0)
+    if (a.adv && blockIdx.x == 0 && threadIdx.x == 0) *a.adv = next_epoch(*a.adv);
   if constexpr (EPI == EPI_ADDACC)
     if (a.xcell && blockIdx.x == 0 && threadIdx.x == 0) a.xcell[0] = next_epoch(a.xcell[0]);
 
@@ -1028,6 +1040,10 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
         if (lane == 0) ssqb[wave_hw] = sq;
       }
       lds_barrier();
+      if (a.clr) {
+        const int gi = (int)blockIdx.x * (BW * 64) + tid;
+        if (2 * gi < a.clr_n) reinterpret_cast<i64x2_t *>(a.clr)[gi] = i64x2_t{0, 0};
+      }
       return;
     }
   }
@@ -1436,7 +1452,13 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
       const float up = __shfl_xor(tot[m], 32, 64);
       if (m < rows && lane < 32 && (lane % LPR) == 0) {
         const int n = r0 + row;
-        if (n < NO) y[(size_t)m * NO + n] = silu(tot[m]) * up;
+        if (n < NO) {
+          const float h = silu(tot[m]) * up;
+          y[(size_t)m * NO + n] = h;
+          if (pub_tag)  // the joined FFN launch: the down slices wait for it
+            __hip_atomic_store(a.xcell + n, (unsigned long long)pub_tag << 32 | __float_as_uint(h),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
     return;

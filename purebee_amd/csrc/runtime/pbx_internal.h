@@ -87,6 +87,11 @@ struct pbx_gemv_args {
   // rows GEMV with the K blocks split over workgroups: one 64-bit cell per
   // output element (zero between launches)
   unsigned long long *xcell = nullptr;
+  // builder waves: clr_n 64-bit words of clr zeroed by the launch; adv: an
+  // epoch advanced once by the launch
+  long long *clr = nullptr;
+  int clr_n = 0;
+  unsigned long long *adv = nullptr;
 };
 
 struct pbx_ctx {

@@ -82,9 +82,25 @@ struct ArgmaxArgsHost {  // ArgmaxArgs in pbx_decode.hip
   int n_partials;
   int hist_cap;
   EmbedArgsHost emb;
+  long long *clr = nullptr;
+  int clr_n = 0;
 };
 
-enum ArgKind { ARG_GEMV, ARG_ATTN, ARG_ATTN_SPLIT, ARG_COMBINE, ARG_EMBED, ARG_ARGMAX, ARG_FUSED };
+struct FfnArgsHost {  // FfnArgs in pbx_decode.hip
+  const void *qs = nullptr;
+  const void *dsc = nullptr;
+  const float *x = nullptr;
+  const long long *acc = nullptr;
+  unsigned long long *cell = nullptr;
+  float *xout = nullptr;
+  unsigned long long *qepoch = nullptr;
+  int *status = nullptr;
+  int spin = 0;
+};
+
+enum ArgKind {
+  ARG_GEMV, ARG_ATTN, ARG_ATTN_SPLIT, ARG_COMBINE, ARG_EMBED, ARG_ARGMAX, ARG_FUSED, ARG_FFN
+};
 enum AttnMode { ATTN_HEAD, ATTN_SPLIT, ATTN_DECODE };
 
 struct Op {
@@ -101,6 +117,7 @@ struct Op {
   CombineArgsHost comb;
   EmbedArgsHost embed;
   ArgmaxArgsHost amax;
+  FfnArgsHost ffn;  // ARG_FFN: the down projection's arguments (gemv: gate|up)
   int np = 0;  // ARG_FUSED: GEMV workgroups before the attention's
 };
 
@@ -151,8 +168,18 @@ struct pbx_model {
   float *x = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
   // the residual's pending update [dim] (2^-32 fixed point) between the
   // fused attention + o projection and the down GEMV of a layer; zero
-  // outside that span
+  // outside that span.  With the joined FFN launch: [2][dim], layer l
+  // accumulating into [l % 2] while the launch of layer l clears the other
+  // (and the step's argmax both)
   long long *xacc = nullptr;
+  // joined FFN launch (dim 2048, hidden 8192, Q4_0; PBX_FFN=0 at creation:
+  // separate gate|up and down): the residual rows alternate between x
+  // (even layers' input) and x2, the down slices meet in ffn_cell [dim]
+  // (zero between launches), and each layer publishes its SwiGLU outputs
+  // in h_cells [n_layers][hidden + 64] (their epoch at [hidden])
+  bool ffn_join = true, ffn_joined = false;
+  float *x2 = nullptr;
+  unsigned long long *ffn_cell = nullptr, *h_cells = nullptr;
   uint64_t *partials = nullptr;
   int n_partials_cap = 0;
   bool gemv_int = true;  // integer-limb GEMV kernels where they apply
@@ -528,12 +555,39 @@ static int build_ops(pbx_model *m) {
     if (hipMemsetAsync(m->qa_cells, 0, cb, c->stream) != hipSuccess)
       return pbx_fail(c, PBX_EHIP, "model: clearing the q|k|v cells failed");
   }
+  // The FFN in one launch (pbx_ffn_q4_d2048_h8192): Llama-3.2-1B's shapes
+  // with Q4_0 layers, after the joined q|k|v + attention launch (whose epoch
+  // and pending-update scheme it continues).
+  hipFunction_t fffn = nullptr;
+  // Its slices wait for each other's gate|up outputs, so all 256 workgroups
+  // (one a CU) must be resident at once: only on parts with >= 256 CUs.
+  if (fqa && m->ffn_join && c->cu_count >= 256 && g.dim == 2048 && g.hidden_dim == 8192 &&
+      o_ipt == 2 &&
+      m->layers[0].wgu->type == PBX_TYPE_Q4_0 && m->layers[0].wd->type == PBX_TYPE_Q4_0)
+    fffn = pbx_kernel_by_name(c, "pbx_ffn_q4_d2048_h8192");
+  const size_t h_stride = (size_t)g.hidden_dim + 64;
+  if (fffn && !m->x2) {
+    const size_t hb = (size_t)g.n_layers * h_stride * 8;
+    int rc;
+    if ((rc = dalloc(m, (void **)&m->x2, (size_t)g.dim * 4)) ||
+        (rc = dalloc(m, (void **)&m->ffn_cell, (size_t)g.dim * 8)) ||
+        (rc = dalloc(m, (void **)&m->h_cells, hb)))
+      return rc;
+    if (hipMemsetAsync(m->ffn_cell, 0, (size_t)g.dim * 8, c->stream) != hipSuccess ||
+        hipMemsetAsync(m->h_cells, 0, hb, c->stream) != hipSuccess)
+      return pbx_fail(c, PBX_EHIP, "model: clearing the FFN cells failed");
+  }
   for (int l = 0; l < g.n_layers; ++l) {
     Layer &L = m->layers[l];
     int rc;
     m->layer_op[l] = m->ops.size();
     unsigned long long *cells = fqa ? m->qa_cells + l * cell_stride : nullptr;
-    if ((rc = add_gemv(m, L.wqkv, cached ? "qkvr" : "qkv", "qkv", m->x, nullptr, L.attn_norm,
+    // joined FFN: layer l reads its residual row from x (even l) or x2 and
+    // accumulates the attention's update in xacc[l % 2]
+    const int par = fffn ? l & 1 : 0;
+    float *xin = par ? m->x2 : m->x;
+    long long *acc_l = m->xacc + (size_t)par * g.dim;
+    if ((rc = add_gemv(m, L.wqkv, cached ? "qkvr" : "qkv", "qkv", xin, nullptr, L.attn_norm,
                        m->qkv, nullptr)))
       return rc;
     if (cached) {
@@ -562,8 +616,8 @@ static int build_ops(pbx_model *m) {
                             (float)(1.0 / sqrt((double)g.head_dim)), g.max_seq};
       a.attn.oqs = L.wo->qs;
       a.attn.odsc = L.wo->d;
-      a.attn.oacc = m->xacc;
-      a.attn.ox = m->x;
+      a.attn.oacc = acc_l;
+      a.attn.ox = xin;
       // the o projection's weights, its head outputs' update (read and written)
       a.fixed_bytes = (double)L.wo->N * pbx_type_row_bytes(L.wo->type, L.wo->K) + 16.0 * g.dim;
       if (cells) {
@@ -586,6 +640,14 @@ static int build_ops(pbx_model *m) {
         if (l == m->test_layer) {
           a.attn.skew = m->test_skew;
           a.attn.spin = m->test_spin;
+        }
+        if (fffn) {
+          // the other pending update (the previous layer's, read by its FFN
+          // launch) is cleared for the next layer; the FFN's cell epoch
+          // advances (no FFN launch runs meanwhile)
+          a.gemv.clr = m->xacc + (size_t)(1 - par) * g.dim;
+          a.gemv.clr_n = g.dim;
+          a.gemv.adv = m->h_cells + l * h_stride + g.hidden_dim;
         }
         a.fixed_bytes += q.bytes;
       }
@@ -641,6 +703,37 @@ static int build_ops(pbx_model *m) {
                             (float)(1.0 / sqrt((double)g.head_dim)), g.max_seq};
       m->ops.push_back(a);
     }
+    if (fffn) {
+      // gate|up (the integer-limb GEMV with the pending update, publishing
+      // its outputs) and the down slices in one launch
+      if ((rc = add_gemv(m, L.wgu, "gua", "gate_up", xin, nullptr, L.ffn_norm, m->gu, nullptr)))
+        return rc;
+      Op f = m->ops.back();
+      m->ops.pop_back();
+      if (f.name != "pbx_dk_q4_i8x8b1w8p4_gua" || f.grid.x != 256 || f.block.x != 1024)
+        return pbx_fail(c, PBX_ENOTSUP, "model: joined FFN needs the 8x8 gate|up shape, got %s",
+                        f.name.c_str());
+      f.kind = ARG_FFN;
+      f.name = "pbx_ffn_q4_d2048_h8192";
+      f.f = fffn;
+      f.role = "ffn";
+      f.gemv.acc = acc_l;
+      f.gemv.xcell = m->h_cells + l * h_stride;
+      f.ffn.qs = L.wd->qs;
+      f.ffn.dsc = L.wd->d;
+      f.ffn.x = xin;
+      f.ffn.acc = acc_l;
+      f.ffn.cell = m->ffn_cell;
+      f.ffn.xout = par ? m->x : m->x2;
+      f.ffn.qepoch = cells + m->qkv_rows;
+      f.ffn.status = m->state + 3;
+      // gate|up's bytes, then W_down, its input h (read as 8-byte cells, each
+      // slice once) and the residual row: x, the update, the next row
+      f.bytes += (double)L.wd->N * pbx_type_row_bytes(L.wd->type, L.wd->K) +
+                 8.0 * g.hidden_dim + 16.0 * g.dim;
+      m->ops.push_back(f);
+      continue;
+    }
     if (o_ipt) {
       if ((rc = add_gemv(m, L.wgu, "gua", "gate_up", m->x, nullptr, L.ffn_norm, m->gu, nullptr)))
         return rc;
@@ -658,7 +751,8 @@ static int build_ops(pbx_model *m) {
   int n_tiles = 0;
   const pbx_weight *head = m->output ? m->output : m->embd;
   m->layer_op[g.n_layers] = m->ops.size();
-  int rc = add_gemv(m, head, "lmh", "lm_head", m->x, nullptr, m->out_norm, m->logits, &n_tiles);
+  int rc = add_gemv(m, head, "lmh", "lm_head", fffn && (g.n_layers & 1) ? m->x2 : m->x, nullptr,
+                    m->out_norm, m->logits, &n_tiles);
   if (rc) return rc;
   if (m->ops.back().name.rfind("pbx_dk_q6k_i", 0) == 0) {
     // Q6_K head on the integer-limb kernel: the same kernel on the
@@ -686,6 +780,11 @@ static int build_ops(pbx_model *m) {
   am.role = "argmax";  // + the next step's embedding
   am.bytes = 8.0 * n_tiles;
   am.amax = ArgmaxArgsHost{m->partials, m->state, m->hist, n_tiles, m->hist_cap, e.embed};
+  if (fffn) {
+    am.amax.clr = m->xacc;  // both pending updates zero at the next step's start
+    am.amax.clr_n = 2 * g.dim;
+  }
+  m->ffn_joined = fffn != nullptr;
   am.bytes += (double)pbx_type_row_bytes(m->embd->type, g.dim) + 4.0 * g.dim;
   m->ops.push_back(am);
   m->ops_ready = true;
@@ -706,7 +805,11 @@ static int enqueue_op(pbx_model *m, Op &op, hipEvent_t t0 = nullptr, hipEvent_t 
   }
   void *one[] = {arg};
   void *fused[] = {&op.gemv, &op.attn, &op.np};
-  void **args = op.kind == ARG_COMBINE ? comb : op.kind == ARG_FUSED ? fused : one;
+  void *ffn[] = {&op.gemv, &op.ffn};
+  void **args = op.kind == ARG_COMBINE ? comb
+                : op.kind == ARG_FUSED ? fused
+                : op.kind == ARG_FFN   ? ffn
+                                       : one;
   if (t0)
     return pbx_launch_fn_timed(m->c, op.f, op.name.c_str(), op.grid, op.block, args, m->c->stream,
                                t0, t1);
@@ -744,7 +847,16 @@ static int enqueue_ops_layers(pbx_model *m, int L) {
   const size_t stop = m->layer_op[L], head = m->layer_op[m->cfg.n_layers];
   for (size_t i = 0; i < m->ops.size(); ++i) {
     if (i >= stop && i < head) continue;
-    int rc = enqueue_op(m, m->ops[i]);
+    int rc;
+    if (i == head && m->ffn_joined && L < m->cfg.n_layers) {
+      // the joined FFN alternates the residual rows: after L layers the
+      // head reads x (L even) or x2
+      Op h = m->ops[i];
+      h.gemv.X = (L & 1) ? m->x2 : m->x;
+      rc = enqueue_op(m, h);
+    } else {
+      rc = enqueue_op(m, m->ops[i]);
+    }
     if (rc) return rc;
   }
   return PBX_OK;
@@ -941,7 +1053,8 @@ static void model_release(pbx_model *m) {
                   (void *)m->x, (void *)m->xacc, (void *)m->qkv, (void *)m->attn, (void *)m->gu,
                   (void *)m->logits,
                   (void *)m->partials, (void *)m->state, (void *)m->hist,
-                  (void *)m->attn_part, m->head_lanes, (void *)m->qa_cells})
+                  (void *)m->attn_part, m->head_lanes, (void *)m->qa_cells, (void *)m->x2,
+                  (void *)m->ffn_cell, (void *)m->h_cells})
     if (p) hipFree(p);
   for (void *p : {(void *)m->bx, (void *)m->bxn, (void *)m->bqkv, (void *)m->battn,
                   (void *)m->bgu, (void *)m->bh, (void *)m->btmp, (void *)m->blogits,
@@ -1041,7 +1154,9 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
   if (!rc) rc = dalloc(m, (void **)&m->vcache, kv_bytes);
   if (!rc) rc = dalloc(m, (void **)&m->rope, (size_t)g.max_seq * g.head_dim * 4);
   if (!rc) rc = dalloc(m, (void **)&m->x, (size_t)g.dim * 4);
-  if (!rc) rc = dalloc(m, (void **)&m->xacc, (size_t)g.dim * 8);
+  if (!rc) rc = dalloc(m, (void **)&m->xacc, (size_t)g.dim * 16);
+  if (!rc && hipMemsetAsync(m->xacc, 0, (size_t)g.dim * 16, c->stream) != hipSuccess)
+    rc = pbx_fail(c, PBX_EHIP, "pbx_model_create: clearing the pending update failed");
   if (!rc) rc = dalloc(m, (void **)&m->qkv, (size_t)m->qkv_rows * 4);
   if (!rc) rc = dalloc(m, (void **)&m->attn, (size_t)g.dim * 4);
   if (!rc) rc = dalloc(m, (void **)&m->gu, (size_t)g.hidden_dim * 2 * 4);
@@ -1060,6 +1175,7 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
   if (const char *e = getenv("PBX_QKV_ATTN")) m->qkv_attn = e[0] != '0';
   if (const char *e = getenv("PBX_ATTN_O")) m->attn_o_ipt = atoi(e);
   if (const char *e = getenv("PBX_GRAPH_STEPS")) m->graph_steps = atoi(e);
+  if (const char *e = getenv("PBX_FFN")) m->ffn_join = e[0] != '0';
   if (!rc && m->attn_mode == ATTN_SPLIT) {
     m->attn_splits = std::min({64, g.max_seq, std::max(4, (256 + g.n_kv_heads - 1) / g.n_kv_heads)});
     rc = dalloc(m, (void **)&m->attn_part,
@@ -1080,7 +1196,7 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
         hipMemsetAsync(m->kcache, 0, kv_bytes, c->stream) != hipSuccess ||
         hipMemsetAsync(m->vcache, 0, kv_bytes, c->stream) != hipSuccess ||
         hipMemsetAsync(m->state, 0, 64, c->stream) != hipSuccess ||
-        hipMemsetAsync(m->xacc, 0, (size_t)g.dim * 8, c->stream) != hipSuccess ||
+        hipMemsetAsync(m->xacc, 0, (size_t)g.dim * 16, c->stream) != hipSuccess ||
         hipStreamSynchronize(c->stream) != hipSuccess)
       rc = pbx_fail(c, PBX_EHIP, "pbx_model_create: initialisation copies failed");
   }
@@ -1722,9 +1838,12 @@ static int prefill_batched(pbx_model *m, const int32_t *tokens, int n, int start
   if (hipMemcpyAsync(m->x, m->bx + (size_t)(n - 1) * m->cfg.dim, (size_t)m->cfg.dim * 4,
                      hipMemcpyDeviceToDevice, m->c->stream) != hipSuccess)
     return pbx_fail(m->c, PBX_EHIP, "model: residual copy failed");
-  // the LM head and the argmax
-  for (size_t i = m->layer_op[m->cfg.n_layers]; i < m->ops.size(); ++i)
-    if ((rc = enqueue_op(m, m->ops[i]))) return rc;
+  // the LM head (on x, where the last row now is) and the argmax
+  for (size_t i = m->layer_op[m->cfg.n_layers]; i < m->ops.size(); ++i) {
+    Op op = m->ops[i];
+    if (i == m->layer_op[m->cfg.n_layers]) op.gemv.X = m->x;
+    if ((rc = enqueue_op(m, op))) return rc;
+  }
   return PBX_OK;
 }
 
