@@ -132,6 +132,15 @@ int pbx_linear_dev(pbx_ctx *ctx, const pbx_weight *W, const float *dX,
 #define PBX_NOALLOC_WORKSPACE_BYTES (64u << 20)
 int pbx_linear_dev_noalloc(pbx_ctx *ctx, const pbx_weight *W, const float *dX, int64_t M,
                            const float *dBias, float *dY);
+/* Introspection for the two above, no reference counterpart (tests and
+ * capacity planning): *grown_bytes = device workspace the allocating entry
+ * points of this context have allocated so far (the noalloc one never adds
+ * to it), *static_bytes = the static workspace of the noalloc one (0 when
+ * it is unavailable); pbx_ctx_stream = the context's HIP stream (a
+ * hipStream_t), on which every enqueueing entry point works, for callers
+ * that capture that work into a graph or order their own work after it. */
+int   pbx_workspace_info(const pbx_ctx *ctx, size_t *grown_bytes, size_t *static_bytes);
+void *pbx_ctx_stream(const pbx_ctx *ctx);
 
 /* Exact dequantisation of a resident weight to fp32, row-major [N,K]
  * (for PBX_TYPE_Q8_REF: [K,N], the reference's own orientation).

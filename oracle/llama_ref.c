@@ -111,16 +111,41 @@ static void rmsnorm(const float *x, const float *w, int S, int D, double eps, fl
   }
 }
 
-/* LINEAR without bias: out[s][n] = sum_k x[s][k] * W[n][k] */
+/* LINEAR without bias: out[s][n] = sum_k x[s][k] * W[n][k], each sum in k
+ * order in double.  Four weight rows share the loop over k (four
+ * independent sums, so the double adds do not wait on each other) and the
+ * rows s run inside the loop over n, so a weight row is read from memory
+ * once for all of them; every sum is the same as the one-at-a-time loop's. */
 static void linear(const float *x, int S, int K, const float *W, int N, float *out) {
-  for (int s = 0; s < S; ++s) {
-    const float *xs = x + (size_t)s * K;
 #pragma omp parallel for schedule(static)
-    for (int n = 0; n < N; ++n) {
-      const float *w = W + (size_t)n * K;
-      double acc = 0;
-      for (int k = 0; k < K; ++k) acc += (double)xs[k] * w[k];
-      out[(size_t)s * N + n] = (float)acc;
+  for (int n0 = 0; n0 < N; n0 += 4) {
+    const int nn = N - n0 < 4 ? N - n0 : 4;
+    const float *w0 = W + (size_t)n0 * K;
+    for (int s = 0; s < S; ++s) {
+      const float *xs = x + (size_t)s * K;
+      if (nn == 4) {
+        const float *w1 = w0 + K, *w2 = w1 + K, *w3 = w2 + K;
+        double a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+        for (int k = 0; k < K; ++k) {
+          const double xv = xs[k];
+          a0 += xv * w0[k];
+          a1 += xv * w1[k];
+          a2 += xv * w2[k];
+          a3 += xv * w3[k];
+        }
+        float *o = out + (size_t)s * N + n0;
+        o[0] = (float)a0;
+        o[1] = (float)a1;
+        o[2] = (float)a2;
+        o[3] = (float)a3;
+      } else {
+        for (int i = 0; i < nn; ++i) {
+          const float *w = w0 + (size_t)i * K;
+          double acc = 0;
+          for (int k = 0; k < K; ++k) acc += (double)xs[k] * w[k];
+          out[(size_t)s * N + n0 + i] = (float)acc;
+        }
+      }
     }
   }
 }

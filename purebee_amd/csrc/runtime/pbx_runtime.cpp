@@ -652,6 +652,15 @@ extern "C" int pbx_linear_dev_noalloc(pbx_ctx *c, const pbx_weight *w, const flo
   return pbx_linear_enqueue(c, w, dX, M, dBias, dY, c->stream, &ws);
 }
 
+extern "C" int pbx_workspace_info(const pbx_ctx *c, size_t *grown_bytes, size_t *static_bytes) {
+  if (!c) return pbx_fail(nullptr, PBX_EINVAL, "pbx_workspace_info: ctx is NULL");
+  if (grown_bytes) *grown_bytes = c->d_gemm_cap;
+  if (static_bytes) *static_bytes = c->scratch ? c->scratch_bytes : 0;
+  return PBX_OK;
+}
+
+extern "C" void *pbx_ctx_stream(const pbx_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
 extern "C" int pbx_linear(pbx_ctx *c, const pbx_weight *w, const float *X, int64_t M,
                           const float *bias, float *Y) {
   int rc = check_linear_args(c, w, X, M, Y, "pbx_linear");

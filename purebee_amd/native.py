@@ -23,12 +23,14 @@ STATUS = {0: "PBX_OK", -1: "PBX_EINVAL", -2: "PBX_ENODEV", -3: "PBX_ENOMEM",
           -4: "PBX_EHIP", -5: "PBX_ENOTSUP", -6: "PBX_ELOAD", -7: "PBX_EIO",
           -8: "PBX_ETIMEOUT"}
 ETIMEOUT = -8
+NOALLOC_WORKSPACE_BYTES = 64 << 20  # PBX_NOALLOC_WORKSPACE_BYTES
 
 # Every entry point declared in include/pbx.h.
 EXPORTS = (
     "pbx_init", "pbx_shutdown", "pbx_last_error", "pbx_device_info",
     "pbx_weight_upload", "pbx_weight_upload_q8ref", "pbx_weight_free", "pbx_weight_info",
-    "pbx_linear", "pbx_linear_dev", "pbx_linear_dev_noalloc", "pbx_dequant", "pbx_dequant_dev",
+    "pbx_linear", "pbx_linear_dev", "pbx_linear_dev_noalloc", "pbx_workspace_info",
+    "pbx_ctx_stream", "pbx_dequant", "pbx_dequant_dev",
     "pbx_quantize_q8_0", "pbx_quantize_q4_0", "pbx_quantize_q4_1", "pbx_quantize_q6_k",
     "pbx_quantize_q8_ref",
     "pbx_synth_normal",
@@ -113,6 +115,8 @@ def load_library():
         "pbx_linear": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
         "pbx_linear_dev": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
         "pbx_linear_dev_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
+        "pbx_workspace_info": (ctypes.c_int, [_vp, _vp, _vp]),
+        "pbx_ctx_stream": (_vp, [_vp]),
         "pbx_dequant": (ctypes.c_int, [_vp, _vp, _vp]),
         "pbx_dequant_dev": (ctypes.c_int, [_vp, _vp, _vp]),
         "pbx_quantize_q8_0": (ctypes.c_int, [_f32p, _i64, _i64, _u8p]),
@@ -364,6 +368,17 @@ class Context:
     def linear_dev_noalloc(self, w, dX, M, dY, dBias=None):
         """pbx_linear_dev_noalloc: the same result, no device allocation."""
         self._call("pbx_linear_dev_noalloc", self._p, w.ptr, dX, M, dBias, dY)
+
+    def workspace_info(self):
+        """(bytes of workspace the allocating entry points grew, bytes of the
+        static no-allocation workspace)."""
+        g, st = ctypes.c_size_t(), ctypes.c_size_t()
+        self._call("pbx_workspace_info", self._p, ctypes.byref(g), ctypes.byref(st))
+        return g.value, st.value
+
+    def stream(self):
+        """The context's hipStream_t, as an integer handle."""
+        return self.L.pbx_ctx_stream(self._p)
 
     def dequant(self, w):
         shape = (w.K, w.N) if w.type == TYPE_Q8_REF else (w.N, w.K)

@@ -51,12 +51,13 @@ def tensor_specs(cfg):
     return specs
 
 
-def make_tensor(spec, base_seed, index):
-    """Bytes of one tensor as the loaders hand them over (GGUF blocks or f32)."""
+def make_tensor(spec, base_seed, index, std=WEIGHT_STD):
+    """Bytes of one tensor as the loaders hand them over (GGUF blocks or f32);
+    matrices are drawn from N(0, std)."""
     tid, layer, N, K, t = spec
     if tid in (T_OUTPUT_NORM, T_ATTN_NORM, T_FFN_NORM):
         return np.ones(K, np.float32)
-    w = native.synth_normal(base_seed + index, N * K, 0.0, WEIGHT_STD).reshape(N, K)
+    w = native.synth_normal(base_seed + index, N * K, 0.0, std).reshape(N, K)
     if t == TYPE_F32:
         return w
     return {TYPE_Q4_0: native.quantize_q4_0, TYPE_Q4_1: native.quantize_q4_1,
@@ -65,16 +66,18 @@ def make_tensor(spec, base_seed, index):
 
 
 def build(ctx, cfg, seed=1000, keep=None):
-    """Create a Model of config `cfg` (a CONFIGS key or a dict) and load seeded
-    weights; keep(spec, data) sees every tensor (for oracles / CPU baselines)."""
+    """Create a Model of config `cfg` (a CONFIGS key or a dict; "weight_std"
+    overrides the 0.02 of the matrices) and load seeded weights;
+    keep(spec, data) sees every tensor (for oracles / CPU baselines)."""
     if isinstance(cfg, str):
         cfg = CONFIGS[cfg]
     m = Model(ctx, cfg["dim"], cfg["hidden_dim"], cfg["n_layers"], cfg["n_heads"],
               cfg["n_kv_heads"], cfg["vocab_size"], cfg["max_seq"], cfg["weight_type"],
               cfg["embed_type"], cfg.get("output_type", -1), cfg.get("head_dim"),
               cfg.get("rms_eps", 1e-5), cfg.get("rope_theta", 10000.0))
+    std = cfg.get("weight_std", WEIGHT_STD)
     for i, spec in enumerate(tensor_specs(cfg)):
-        data = make_tensor(spec, seed, i)
+        data = make_tensor(spec, seed, i, std)
         m.set_tensor(spec[0], spec[1], data)
         if keep is not None:
             keep(spec, data)

@@ -68,19 +68,22 @@ def test_untied_head_and_small_head_dim(ctx):
 
 
 def test_stories15m_shape(ctx):
-    """config: stories15M-shaped, Q8_0 layers, f32 embedding / LM head."""
-    print("[case] stories15m 16-token prompt + 64 greedy", flush=True)
-    exact, ties, e1, e2 = run_prompt_then_greedy(ctx, "stories15m", 16, 64, seed=1000)
+    """config: stories15M-shaped, Q8_0 layers, f32 embedding / LM head, at its
+    workload's full length: a 16-token prompt, then 128 greedy steps, every
+    step's choice walked through the oracle."""
+    print("[case] stories15m 16-token prompt + 128 greedy", flush=True)
+    exact, ties, e1, e2 = run_prompt_then_greedy(ctx, "stories15m", 16, 128, seed=1000)
     print(f"  exact={exact} ties={ties} prefill_err={e1:.1e} final_err={e2:.1e}")
-    assert exact >= 62
+    assert exact >= 126
 
 
 def test_smollm2_shape(ctx):
-    """config: SmolLM2-135M-shaped, GQA 9/3, tied Q8_0 embedding."""
-    print("[case] smollm2 32-token prompt + 64 greedy", flush=True)
-    exact, ties, e1, e2 = run_prompt_then_greedy(ctx, "smollm2_135m", 32, 64, seed=2000)
+    """config: SmolLM2-135M-shaped, GQA 9/3, tied Q8_0 embedding, at its
+    workload's full length: a 32-token prompt, then 256 greedy steps."""
+    print("[case] smollm2 32-token prompt + 256 greedy", flush=True)
+    exact, ties, e1, e2 = run_prompt_then_greedy(ctx, "smollm2_135m", 32, 256, seed=2000)
     print(f"  exact={exact} ties={ties} prefill_err={e1:.1e} final_err={e2:.1e}")
-    assert exact >= 62
+    assert exact >= 252
 
 
 def test_llama1b_shape(ctx):
@@ -89,50 +92,6 @@ def test_llama1b_shape(ctx):
     exact, ties, e1, e2 = run_prompt_then_greedy(ctx, "llama32_1b", 8, 16, seed=3000)
     print(f"  exact={exact} ties={ties} prefill_err={e1:.1e} final_err={e2:.1e}")
     assert exact >= 15
-
-
-def test_llama1b_prompt128_greedy64_every_step(ctx):
-    """Llama-3.2-1B-shaped Q4_0 decode at its workload's length: a 128-token
-    random prompt through the batched prefill, then 64 greedy steps replayed
-    from the captured step (llama.js:452-505).  The GPU's tokens are then fed
-    again one at a time from position 128 and every step's logits are
-    compared with the oracle's teacher-forced forward (llama.js:204-371) at
-    the logit tolerance; every greedy choice must be the oracle's argmax or
-    a tie below that tolerance."""
-    print("[case] llama32_1b 128-token prompt + 64 greedy, logits every step", flush=True)
-    model, ref, cfg = make_pair(ctx, "llama32_1b", 3300)
-    n_prompt, n_gen = 128, 64
-    prompt = synth.random_tokens(3301, n_prompt, cfg["vocab_size"])
-    ref_logits = ref.forward(prompt, 0)
-    logits, nxt = model.forward(prompt, 0)
-    worst = float(np.abs(logits - ref_logits).max())
-    assert worst <= LOGIT_TOL, f"prefill logits max-abs {worst:.2e}"
-    first = oracle.argmax(ref_logits)
-    if nxt != first:
-        assert ref_logits[first] - ref_logits[nxt] < LOGIT_TOL
-    toks = model.generate(nxt, n_prompt, n_gen)
-    # teacher-forced replay of the same tokens: positions 128 .. 191
-    model.rollback(n_prompt)
-    feed = [nxt] + [int(t) for t in toks[:-1]]
-    exact, ties = 0, 0
-    for i, tok in enumerate(feed):
-        g, gnext = model.forward([tok], n_prompt + i)
-        r = ref.forward([tok], n_prompt + i)
-        err = float(np.abs(g - r).max())
-        worst = max(worst, err)
-        assert err <= LOGIT_TOL, f"step {i}: logits max-abs {err:.2e}"
-        assert gnext == int(toks[i]), f"step {i}: replay chose {gnext}, generate chose {toks[i]}"
-        best = oracle.argmax(r)
-        if gnext == best:
-            exact += 1
-        else:
-            gap = float(r[best] - r[gnext])
-            assert gap < LOGIT_TOL, f"step {i}: GPU {gnext} vs oracle {best}, gap {gap:.3e}"
-            ties += 1
-    print(f"  exact={exact} ties={ties} worst logits max-abs={worst:.1e}")
-    assert exact >= n_gen - 2
-    model.free()
-    ref.close()
 
 
 def test_llama1b_shape_q4_1(ctx):

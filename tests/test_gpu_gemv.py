@@ -267,6 +267,9 @@ def test_bias_and_multi_row(ctx, t):
     (8192, 4096, 2, True),     # 8 x 4, two groups
     (1000, 3104, 3, False),    # B = 97: the second group's lanes past B masked
     (2048, 8192, 1, True),     # 4 x 2, four groups
+    (2048, 7168, 1, True),     # builder-wave kernel with B = 224: its last chunk's
+    (2048, 7168, 3, False),    #   blocks past B masked (limbs and scales unwritten)
+    (4096, 6400, 2, True),     # B = 200
     (70000, 2048, 1, False),   # tall, no bias: the tile loop (512 workgroups)
     (70000, 2048, 2, True),    # tall with bias: one tile a workgroup
 ])

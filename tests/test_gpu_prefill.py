@@ -433,6 +433,90 @@ def test_self_speculative_equals_greedy(ctx, batched):
     model.free()
 
 
+def _spec_replay(ref, prompt, max_tokens, draft_layers, draft_count):
+    """SelfSpeculativeDecoder.generate (speculative.js:58-204) in greedy mode
+    over the oracle: draft with forward([t], pos, {maxLayers}) and argmax,
+    roll the cache back, verify one token at a time with the full model,
+    accept the agreeing prefix, take the verifier's token at the first
+    disagreement (rolling back past it) or a bonus token.  Returns the
+    generated tokens, the stats the reference counts and the smallest
+    top-2 logit gap of any decision (a near-tie could flip on the GPU)."""
+    ref.rollback(0)
+    out, pos, gaps = list(prompt), len(prompt), []
+
+    def pick(logits):
+        srt = np.sort(logits)
+        gaps.append(float(srt[-1] - srt[-2]))
+        return oracle.argmax(logits)
+
+    nxt = pick(ref.forward(prompt, 0))
+    out.append(nxt)
+    generated, rounds, drafted, accepted_all = 1, 0, 0, 0
+    while generated < max_tokens:
+        draft, dpos = [nxt], pos
+        for d in range(draft_count):
+            if generated + d >= max_tokens:
+                break
+            draft.append(pick(ref.forward([draft[-1]], dpos, max_layers=draft_layers)))
+            dpos += 1
+        nd = len(draft) - 1
+        if nd == 0:
+            break
+        drafted += nd
+        rounds += 1
+        ref.rollback(pos)
+        acc = 0
+        for d in range(nd):
+            vp = pick(ref.forward([draft[d]], pos + d))
+            out.append(vp)
+            generated += 1
+            if vp == draft[d + 1]:
+                acc += 1
+            else:
+                ref.rollback(pos + d + 2)
+                break
+        if acc == nd:
+            b = pick(ref.forward([draft[-1]], pos + nd))
+            out.append(b)
+            generated += 1
+            pos += nd + 1
+            nxt = b
+        else:
+            pos += acc + 1
+            nxt = out[-1]
+        accepted_all += acc
+    return out[len(prompt):], dict(rounds=rounds, drafted=drafted, accepted=accepted_all), min(gaps)
+
+
+@pytest.mark.parametrize("batched", [True, False])
+def test_self_speculative_stats_match_reference_replay(ctx, batched):
+    """The self-draft statistics, not just the tokens: the GPU's
+    self-speculative run (draft = the first 2 of 4 layers, 4 drafts a
+    round) against a replay of speculative.js:58-204 over the oracle with
+    the same weights.  Rounds, drafted and accepted counts (the reference's
+    acceptanceRate) and every emitted token are equal; a wrong draft chain
+    (layer limit, cache left stale by a rollback) changes them even where
+    the greedy output stays the same.  Weights N(0, 0.05): with 0.02 the
+    layers barely move the residual stream and every draft is accepted;
+    here 28 of 47 are, over 12 rounds (the replay's smallest top-2 gap is
+    1.9e-2, far above the logit tolerance)."""
+    print(f"[case] self-speculative stats vs oracle replay batched={batched}", flush=True)
+    tcfg = tiny(TYPE_Q4_0, TYPE_Q4_0, n_layers=4, max_seq=200, weight_std=0.05)
+    model, ref, tcfg = make_pair(ctx, tcfg, 440)
+    prompt = [int(t) for t in synth.random_tokens(441, 16, tcfg["vocab_size"])]
+    n_gen = 40
+    want, want_st, gap = _spec_replay(ref, prompt, n_gen, 2, 4)
+    out, st = self_speculative_generate(model, prompt, n_gen, draft_layers=2, draft_count=4,
+                                        eos_ids=(), batched_verify=batched)
+    got = {k: st[k] for k in ("rounds", "drafted", "accepted")}
+    print(f"  GPU {got} vs replay {want_st}; smallest decision gap {gap:.2e}")
+    assert gap > LOGIT_TOL, "a near-tie decision: pick another seed"
+    assert list(out) == want
+    assert got == want_st
+    model.free()
+    ref.close()
+
+
 def test_speculative_errors(ctx):
     print("[case] speculative errors", flush=True)
     cfg = tiny(TYPE_Q4_0, TYPE_Q4_0, max_seq=64)

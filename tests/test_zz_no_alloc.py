@@ -62,3 +62,64 @@ def test_noalloc_rejects_shapes_beyond_the_workspace(ctx):
     with pytest.raises(pb.PbxError, match="workspace"):
         ctx.linear_dev_noalloc(w, dx.ptr, M, dy.ptr)
     dx.free(), dy.free(), w.free()
+
+
+def test_noalloc_allocates_nothing_and_captures(ctx):
+    """On a fresh context, the no-allocation entry point goes first, on a
+    split-K MFMA GEMM shape (fp16 activation pair, row scales and partials
+    all in the static workspace): the context's grown workspace stays 0.
+    The same call is then captured into a HIP graph in global capture mode
+    (which fails if anything in it allocates or synchronises) and the graph
+    replayed three times, with the program's own work and synchronisations
+    between the replays; every replay equals the eager result bit for bit.
+    pbx_linear_dev afterwards gives the same result and does grow its
+    workspace."""
+    print("[case] noalloc on a fresh context: no growth, global-mode graph capture", flush=True)
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipStreamBeginCapture.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipGraphInstantiate.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
+    hip.hipGraphLaunch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipGraphExecDestroy.argtypes = [ctypes.c_void_p]
+    hip.hipGraphDestroy.argtypes = [ctypes.c_void_p]
+    N, K, M = 2048, 2048, 64
+    W = synth_matrix(91, N, K)
+    raw = oracle.quantize_q4_0(W)
+    with pb.Context(0) as fresh:
+        assert fresh.workspace_info()[0] == 0
+        w = fresh.upload(pb.TYPE_Q4_0, N, K, raw)
+        X = pb.synth_normal(92, M * K).reshape(M, K)
+        dx = fresh.alloc(M * K * 4).upload(X)
+        dy = [fresh.alloc(M * N * 4) for _ in range(3)]
+        fresh.linear_dev_noalloc(w, dx.ptr, M, dy[0].ptr)
+        fresh.sync()
+        grown, static = fresh.workspace_info()
+        assert grown == 0 and static == pb.native.NOALLOC_WORKSPACE_BYTES, (grown, static)
+        eager = dy[0].download(np.float32, M * N)
+        ref = oracle.matvec(pb.TYPE_Q4_0, X[M - 1], raw, N, K)
+        assert rel_l2(eager.reshape(M, N)[M - 1], ref) < 1e-3
+        stream = ctypes.c_void_p(fresh.stream())
+        assert hip.hipStreamBeginCapture(stream, 0) == 0  # hipStreamCaptureModeGlobal
+        fresh.linear_dev_noalloc(w, dx.ptr, M, dy[1].ptr)
+        graph, gexec = ctypes.c_void_p(), ctypes.c_void_p()
+        assert hip.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(gexec), graph, None, None, 0) == 0
+        for rep in range(3):
+            dy[1].upload(np.full(M * N, np.nan, np.float32))
+            assert hip.hipGraphLaunch(gexec, stream) == 0
+            fresh.sync()
+            got = dy[1].download(np.float32, M * N)
+            assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), rep
+            fresh.linear_dev_noalloc(w, dx.ptr, 3, dy[2].ptr)  # eager work between replays
+            fresh.sync()
+        hip.hipGraphExecDestroy(gexec)
+        hip.hipGraphDestroy(graph)
+        assert fresh.workspace_info()[0] == 0
+        fresh.linear_dev(w, dx.ptr, M, dy[2].ptr)
+        fresh.sync()
+        assert np.array_equal(dy[2].download(np.float32, M * N).view(np.uint32), eager.view(np.uint32))
+        assert fresh.workspace_info()[0] > 0
+        for b in (dx, *dy):
+            b.free()
+        w.free()
