@@ -273,6 +273,15 @@ int pbx_model_forward_batch(pbx_model *m, const int32_t *tokens, int n_tokens,
  * out_tokens[i] is the token chosen by step i. */
 int pbx_model_generate(pbx_model *m, int32_t token, int start_pos, int n_steps,
                        int32_t *out_tokens, float *last_logits);
+/* The same loop stopping at the first token in eos_ids[0..n_eos), as
+ * llama.js:475-489 stops at eosId (`if (nextToken === eosId) break`):
+ * out_tokens receives the *n_out <= max_steps chosen tokens, the EOS last if
+ * one was chosen, and the cache holds no row past the position that fed it.
+ * Steps run in chunks of whole graph launches, the chunk's tokens checked
+ * on the host after each. */
+int pbx_model_generate_eos(pbx_model *m, int32_t token, int start_pos, int max_steps,
+                           const int32_t *eos_ids, int n_eos, int32_t *out_tokens,
+                           int *n_out);
 /* resetCache / rollbackCache (llama-streaming.js:828-862): zero cache
  * positions >= pos of every layer. */
 int pbx_model_reset_cache(pbx_model *m);

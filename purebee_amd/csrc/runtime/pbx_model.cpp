@@ -1996,6 +1996,63 @@ extern "C" int pbx_model_generate(pbx_model *m, int32_t token, int start_pos, in
   return check_status(m, st, "pbx_model_generate");
 }
 
+extern "C" int pbx_model_generate_eos(pbx_model *m, int32_t token, int start_pos, int max_steps,
+                                      const int32_t *eos_ids, int n_eos, int32_t *out_tokens,
+                                      int *n_out) {
+  if (!model_ok(m)) return pbx_fail(nullptr, PBX_EINVAL, "pbx_model_generate_eos: not a live model");
+  pbx_ctx *c = m->c;
+  const pbx_model_config &g = m->cfg;
+  if (max_steps <= 0 || !out_tokens || !n_out || n_eos < 0 || (n_eos > 0 && !eos_ids))
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_generate_eos: bad arguments");
+  if (token < 0 || token >= g.vocab_size)
+    return pbx_fail(c, PBX_EINVAL, "pbx_model_generate_eos: token %d out of range", token);
+  if (start_pos < 0 || (int64_t)start_pos + max_steps > g.max_seq)
+    return pbx_fail(c, PBX_EINVAL,
+                    "pbx_model_generate_eos: positions [%d, %lld) exceed max_seq %d", start_pos,
+                    (long long)start_pos + max_steps, g.max_seq);
+  *n_out = 0;
+  int rc = check_complete(m);
+  if (rc) return rc;
+  if (hipSetDevice(c->device) != hipSuccess)
+    return pbx_fail(c, PBX_EHIP, "pbx_model_generate_eos: hipSetDevice failed");
+  if ((rc = prepare_graphs(m))) return rc;
+  if ((rc = set_state(m, start_pos, token, 0, true))) return rc;
+  // chunks of whole graph launches; after each, the chunk's tokens come back
+  // and the loop stops at the first EOS, as llama.js:475-489 does
+  const int chunk = std::max(1, m->graph_steps);
+  int done = 0;
+  while (done < max_steps) {
+    const int want = std::min(chunk, max_steps - done);
+    for (int i = 0, k = 0; i < want; i += k)
+      if ((rc = run_steps(m, want - i, &k))) return rc;
+    int st[4] = {0, 0, 0, 0};
+    if (hipMemcpyAsync(out_tokens + done, m->hist + done, (size_t)want * 4, hipMemcpyDeviceToHost,
+                       c->stream) != hipSuccess ||
+        hipMemcpyAsync(st, m->state, sizeof st, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+      return pbx_fail(c, PBX_EHIP, "pbx_model_generate_eos: step failed on the device");
+    if ((rc = check_status(m, st, "pbx_model_generate_eos"))) return rc;
+    for (int i = 0; i < want; ++i) {
+      const int32_t t = out_tokens[done + i];
+      bool eos = false;
+      for (int e = 0; e < n_eos; ++e) eos |= t == eos_ids[e];
+      if (!eos) continue;
+      // step done + i chose EOS; the steps after it fed tokens the
+      // reference never feeds: drop their cache rows
+      *n_out = done + i + 1;
+      const int stop = start_pos + done + i + 1;
+      if (stop < start_pos + done + want && (rc = pbx_model_clear_range(m, stop, start_pos + done + want)))
+        return rc;
+      if (hipStreamSynchronize(c->stream) != hipSuccess)
+        return pbx_fail(c, PBX_EHIP, "pbx_model_generate_eos: device failure");
+      return PBX_OK;
+    }
+    done += want;
+  }
+  *n_out = done;
+  return PBX_OK;
+}
+
 // The greedy chain of pbx_model_generate with every step stopping after the
 // first max_layers layers: the self-speculative draft (speculative.js:96-111,
 // forward([t], pos, {maxLayers}) then argmax, repeated), replayed on the

@@ -8,6 +8,10 @@
  *   tensorMulAddQ8(x[M,K], Wq, b|null, outName)    engine.js:259-269 (matmul_q8)
  *   cacheWeight(tensor)                             engine.js:39-42
  *   initWasm()                                      engine.js:28-31
+ *   wasmStats                                       engine.js:44-46
+ * and resetWeights(), the release the streaming runtime gets from
+ * wasmSimd.resetWeights (wasm-simd.js:511-513): cached f32 weights belong to
+ * hip-simd.js, the module that replaces wasm-simd.js.
  * Weights keep the reference's [K,N] orientation at this seam; they are
  * transposed once to the C ABI's [N,K] when made resident.  Results are
  * Tensor objects built with the input tensor's own class, so the reference's
@@ -19,8 +23,8 @@
 'use strict';
 
 const hipq = require('./hip-q4');
+const hipSimd = require('./hip-simd');
 
-const F32 = 0;
 
 class PlainTensor {
   constructor(name, shape, data) {
@@ -41,15 +45,6 @@ function makeTensor(like, name, shape, data) {
   return new PlainTensor(name, shape, data);
 }
 
-function transposeKN(data, K, N) {
-  const out = new Float32Array(K * N);
-  for (let k = 0; k < K; k++) {
-    const row = k * N;
-    for (let n = 0; n < N; n++) out[n * K + k] = data[row + n];
-  }
-  return out;
-}
-
 class HipEngine {
   constructor(options) {
     const opts = options || {};
@@ -59,9 +54,9 @@ class HipEngine {
     this._flops = 0;
   }
 
-  /** engine.js:28-31 -- returns true when the GPU backend is usable. */
+  /** engine.js:28-31 -- true when the GPU backend passed its self-tests. */
   initWasm() {
-    this._ready = hipq.init(this._device);
+    this._ready = hipSimd.init(this._device);
     return this._ready;
   }
 
@@ -72,24 +67,30 @@ class HipEngine {
     return hipq.addon;
   }
 
-  /** engine.js:39-42: make a [K,N] f32 weight resident; sets tensor._hipW. */
+  /**
+   * engine.js:39-42: make a [K,N] f32 weight resident.  The block belongs to
+   * the f32 matmul module (hip-simd.js): resetWeights() releases it, as the
+   * streaming runtime's per-layer wasmSimd.resetWeights() does
+   * (llama-streaming.js:367-380), and the next cacheWeight makes it again.
+   */
   cacheWeight(tensor) {
-    const addon = this._addon();
-    if (tensor._hipW) return;
-    const K = tensor.shape[0], N = tensor.shape[1];
-    tensor._hipW = addon.upload(F32, N, K, transposeKN(tensor.data, K, N));
+    this._addon();
+    if (tensor._hipW !== undefined && hipSimd.isLive(tensor._hipW)) return;
+    tensor._hipW = hipSimd.allocWeights(tensor.data, tensor.shape[0], tensor.shape[1]);
   }
 
-  _f32Handle(W) {
-    if (W._hipW) return { h: W._hipW, temp: false };
-    const K = W.shape[0], N = W.shape[1];
-    return { h: this._addon().upload(F32, N, K, transposeKN(W.data, K, N)), temp: true };
+  /** wasm-simd.js:511-513 through this engine: every cached weight released. */
+  resetWeights() {
+    hipSimd.resetWeights();
   }
 
-  _run(x, h, M, N, bias, outName, like) {
-    const addon = this._addon();
-    const y = addon.linear(h, x.data, M, bias ? bias.data : null);
-    return makeTensor(like, outName, [M, N], y);
+  /** engine.js:44-46 */
+  get wasmStats() {
+    return this._ready ? hipSimd.getStats() : null;
+  }
+
+  _cached(W) {
+    return W._hipW !== undefined && hipSimd.isLive(W._hipW);
   }
 
   /** engine.js:119-167 */
@@ -97,14 +98,13 @@ class HipEngine {
     const M = A.shape[0], K = A.shape[1];
     const K2 = B.shape[0], N = B.shape[1];
     if (K !== K2) throw new Error(`TENSOR_MUL: dimension mismatch A[${M},${K}] x B[${K2},${N}]`);
-    const r = this._f32Handle(B);
-    try {
-      this._opCount++;
-      this._flops += M * N * K * 2;
-      return this._run(A, r.h, M, N, null, outName || 'matmul_out', A);
-    } finally {
-      if (r.temp) this._addon().free(r.h);
-    }
+    this._addon();
+    const out = new Float32Array(M * N);
+    if (this._cached(B)) hipSimd.matmulCached(A.data, M, K, B._hipW, N, null, out);
+    else hipSimd.matmul_general(A.data, M, K, B.data, N, out);
+    this._opCount++;
+    this._flops += M * N * K * 2;
+    return makeTensor(A, outName || 'matmul_out', [M, N], out);
   }
 
   /** engine.js:180-244 */
@@ -112,14 +112,23 @@ class HipEngine {
     const M = x.shape[0], K = x.shape[1];
     const K2 = W.shape[0], N = W.shape[1];
     if (K !== K2) throw new Error('TENSOR_MUL_ADD: dimension mismatch');
-    const r = this._f32Handle(W);
-    try {
-      this._opCount++;
-      this._flops += M * N * K * 2 + (b ? M * N : 0);
-      return this._run(x, r.h, M, N, b, outName || 'linear_out', x);
-    } finally {
-      if (r.temp) this._addon().free(r.h);
+    const addon = this._addon();
+    const out = new Float32Array(M * N);
+    if (this._cached(W)) {
+      hipSimd.matmulCached(x.data, M, K, W._hipW, N, b ? b.data : null, out);
+    } else {
+      // one pass with the bias in the epilogue (the reference adds it after
+      // its general matmul, engine.js:205-214: the same sums)
+      const h = hipSimd.uploadKN(W.data, K, N);
+      try {
+        out.set(hipSimd.linearKN(h, x.data, M, K, b ? b.data : null));
+      } finally {
+        addon.free(h);
+      }
     }
+    this._opCount++;
+    this._flops += M * N * K * 2 + (b ? M * N : 0);
+    return makeTensor(x, outName || 'linear_out', [M, N], out);
   }
 
   /**
@@ -135,7 +144,8 @@ class HipEngine {
     if (!Wq._hipW) Wq._hipW = addon.uploadQ8Ref(K, N, Wq.data, Wq.scales);
     this._opCount++;
     this._flops += M * N * K * 2 + (b ? M * N : 0);
-    return this._run(x, Wq._hipW, M, N, b, outName || 'linear_q8_out', x);
+    const y = addon.linear(Wq._hipW, x.data, M, b ? b.data : null);
+    return makeTensor(x, outName || 'linear_q8_out', [M, N], y);
   }
 
   get stats() {

@@ -34,8 +34,10 @@ function loadAddon() {
 }
 
 /**
- * Initialise the GPU backend. Synchronous, like wasm-q4.js:647-668.
- * @returns {boolean} true if the HIP kernels are available
+ * Initialise the GPU backend. Synchronous, like wasm-q4.js:647-668: the
+ * addon and device, then the module's known-answer test
+ * (wasm-q4.js:673-704) on the GPU; false when either fails.
+ * @returns {boolean} true if the HIP kernels are available and correct
  */
 function init(device) {
   if (_supported) return true;
@@ -46,8 +48,42 @@ function init(device) {
   } catch (e) {
     _supported = false;
     _initError = e;
+    return false;
+  }
+  let ok = false;
+  try {
+    ok = selfTest();
+  } catch (e) {
+    _initError = e;
+  }
+  if (!ok) {
+    _supported = false;
+    if (!_initError) _initError = new Error('Q4_0 self-test failed');
   }
   return _supported;
+}
+
+/**
+ * wasm-q4.js:673-704: two Q4_0 rows of one block against x = 1: scale 1 with
+ * every code 9 gives 32, scale 2 with every code 10 gives 128.  Its bytes are
+ * uploaded once and freed after the check (no resident cache entry).
+ */
+function selfTest() {
+  const K = 32, N = 2;
+  const x = new Float32Array(K).fill(1.0);
+  const raw = new Uint8Array(36);
+  raw[0] = 0x00; raw[1] = 0x3C;  // fp16 1.0
+  for (let j = 2; j < 18; j++) raw[j] = 0x99;
+  raw[18] = 0x00; raw[19] = 0x40;  // fp16 2.0
+  for (let j = 20; j < 36; j++) raw[j] = 0xAA;
+  const h = addon.upload(GGML_TYPE.Q4_0, N, K, raw);
+  let r;
+  try {
+    r = addon.linear(h, x, 1, null);
+  } finally {
+    addon.free(h);
+  }
+  return Math.abs(r[0] - 32.0) < 0.1 && Math.abs(r[1] - 128.0) < 0.1;
 }
 
 function ensure() {
@@ -163,6 +199,7 @@ function lmHeadQuant(hidden, rawBuf, type, vocabSize, dim) {
 
 module.exports = {
   init,
+  selfTest,
   q4_0_matvec,
   q4_1_matvec,
   q8_0_matvec,

@@ -165,8 +165,9 @@ class HipLlamaRuntime {
 
   /**
    * llama.js:452-505.  Greedy: prefill, then the decode loop on the GPU (the
-   * argmax of each step feeds the next without returning to the host);
-   * tokens after the first eosId are dropped as the reference stops there.
+   * argmax of each step feeds the next without returning to the host, the
+   * tokens checked for eosId after every graph launch of 8 steps); it stops
+   * at the first eosId as the reference does, leaving no cache row past it.
    * Otherwise each step's logits come back and sample() picks the token.
    */
   generate(promptTokens, maxTokens = 50, opts = {}) {
@@ -182,12 +183,13 @@ class HipLlamaRuntime {
     let generated = 1;
     const t1 = Date.now();
     if (first !== eosId && maxTokens > 1) {
-      const rest = addon.modelGenerate(this._model, first, promptTokens.length, maxTokens - 1);
+      // the device loop stops at the first EOS too (no steps past it)
+      const rest = addon.modelGenerate(this._model, first, promptTokens.length, maxTokens - 1,
+        eosId);
       for (let i = 0; i < rest.length; i++) {
         all.push(rest[i]);
         generated++;
         if (opts.onToken) opts.onToken(rest[i], i + 1);
-        if (rest[i] === eosId) break;
       }
     }
     const decodeTime = Date.now() - t1;

@@ -511,21 +511,35 @@ napi_value ModelForwardBatch(napi_env env, napi_callback_info info) {
   return o;
 }
 
-// modelGenerate(model, token, startPos, nSteps) -> Int32Array [nSteps]
+// modelGenerate(model, token, startPos, nSteps[, eosId]) -> Int32Array:
+// nSteps tokens, or with eosId the tokens up to and including the first EOS
 napi_value ModelGenerate(napi_env env, napi_callback_info info) {
   if (!need_ctx(env)) return nullptr;
-  napi_value argv[4];
-  get_args(env, info, 4, argv);
+  napi_value argv[5];
+  get_args(env, info, 5, argv);
   ModelRef *r = get_model(env, argv[0]);
-  int64_t tok, start, n;
+  int64_t tok, start, n, eos = -1;
   if (!r || !get_i64(env, argv[1], &tok) || !get_i64(env, argv[2], &start) ||
-      !get_i64(env, argv[3], &n) || n <= 0 || n > r->max_seq)
-    return throw_msg(env, "modelGenerate(model, token, startPos, nSteps): bad arguments");
-  int32_t *out;
-  napi_value arr = new_i32(env, (size_t)n, &out);
-  if (!arr) return throw_msg(env, "modelGenerate: out of memory");
-  int rc = pbx_model_generate(r->m, (int32_t)tok, (int)start, (int)n, out, nullptr);
+      !get_i64(env, argv[3], &n) || n <= 0 || n > r->max_seq ||
+      (!is_nullish(env, argv[4]) && !get_i64(env, argv[4], &eos)))
+    return throw_msg(env, "modelGenerate(model, token, startPos, nSteps[, eosId]): bad arguments");
+  if (eos < 0) {
+    int32_t *out;
+    napi_value arr = new_i32(env, (size_t)n, &out);
+    if (!arr) return throw_msg(env, "modelGenerate: out of memory");
+    int rc = pbx_model_generate(r->m, (int32_t)tok, (int)start, (int)n, out, nullptr);
+    if (rc) return throw_pbx(env, rc, "modelGenerate");
+    return arr;
+  }
+  std::vector<int32_t> buf((size_t)n);
+  const int32_t e = (int32_t)eos;
+  int got = 0;
+  int rc = pbx_model_generate_eos(r->m, (int32_t)tok, (int)start, (int)n, &e, 1, buf.data(), &got);
   if (rc) return throw_pbx(env, rc, "modelGenerate");
+  int32_t *out;
+  napi_value arr = new_i32(env, (size_t)got, &out);
+  if (!arr) return throw_msg(env, "modelGenerate: out of memory");
+  for (int i = 0; i < got; ++i) out[i] = buf[i];
   return arr;
 }
 

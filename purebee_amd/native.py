@@ -38,7 +38,7 @@ EXPORTS = (
     "pbx_dev_copy", "pbx_sync", "pbx_timer_start", "pbx_timer_stop", "pbx_bench_linear",
     "pbx_bench_linear_graph",
     "pbx_model_create", "pbx_model_free", "pbx_model_set_tensor", "pbx_model_forward",
-    "pbx_model_forward_batch", "pbx_model_generate", "pbx_model_reset_cache", "pbx_model_rollback", "pbx_model_info",
+    "pbx_model_forward_batch", "pbx_model_generate", "pbx_model_generate_eos", "pbx_model_reset_cache", "pbx_model_rollback", "pbx_model_info",
     "pbx_model_profile", "pbx_model_op_name", "pbx_model_bench_role", "pbx_model_test_handoff",
     "pbx_speculative_generate", "pbx_model_forward_layers", "pbx_self_speculative_generate",
     "pbx_gguf_open", "pbx_gguf_close", "pbx_gguf_info", "pbx_gguf_tensor_info",
@@ -169,6 +169,8 @@ def load_library():
                                                          ctypes.POINTER(ctypes.c_int),
                                                          ctypes.POINTER(SpecStats)]),
         "pbx_model_generate": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+        "pbx_model_generate_eos": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int, ctypes.c_int,
+                                                  _vp, ctypes.c_int, _vp, _vp]),
         "pbx_model_reset_cache": (ctypes.c_int, [_vp]),
         "pbx_model_rollback": (ctypes.c_int, [_vp, ctypes.c_int]),
         "pbx_model_test_handoff": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
@@ -557,6 +559,17 @@ class Model:
         self._mcall("pbx_model_generate", int(token), start_pos, n_steps, out.ctypes.data,
                     None if logits is None else logits.ctypes.data)
         return (out, logits) if want_logits else out
+
+    def generate_until(self, token, start_pos, max_steps, eos_ids):
+        """pbx_model_generate_eos: greedy steps stopping at the first token in
+        eos_ids (returned last)."""
+        eos = np.ascontiguousarray(eos_ids, np.int32)
+        out = np.empty(max_steps, np.int32)
+        n = ctypes.c_int()
+        self._mcall("pbx_model_generate_eos", int(token), start_pos, max_steps,
+                    eos.ctypes.data if len(eos) else None, len(eos), out.ctypes.data,
+                    ctypes.byref(n))
+        return out[:n.value]
 
     def reset_cache(self):
         self._mcall("pbx_model_reset_cache")

@@ -150,6 +150,80 @@ console.log(JSON.stringify(hip.stats));
     assert rel_l2(yq, refq) <= 1e-3
 
 
+def test_simd_module_init_and_streaming_weight_cycle(tmp_path):
+    """js/hip-simd.js, the wasm-simd.js surface (wasm-simd.js:527-535), and
+    the init contracts, driven as their callers drive them:
+    * hip-q4 init() runs the wasm-q4.js:673-704 KAT on the GPU (wasm-q4.js
+      647-668) and hip-simd init() the wasm-simd.js:365-385 one;
+    * allocWeights + matmulCached (x W + bias) and matmul_general against
+      numpy in double;
+    * llama-streaming.js:367-392 per layer: resetWeights(), allocWeights of
+      the embedding again, engine.cacheWeight of the layer's weights, LINEAR
+      through tensorMulAdd -- the device memory held stays one layer's
+      weights (resetWeights frees them), getStats reads as the reference's,
+      and a pointer from before a reset is refused."""
+    print("[case] js hip-simd surface, init KATs, streaming weight cycle", flush=True)
+    K, N, M = 512, 384, 3
+    rng = np.random.default_rng(7)
+    ws = [rng.normal(0, 0.05, (K, N)).astype(np.float32) for _ in range(4)]
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    bias = rng.normal(0, 1, N).astype(np.float32)
+    for i, w in enumerate(ws):
+        w.tofile(tmp_path / f"w{i}.bin")
+    x.tofile(tmp_path / "x.bin")
+    bias.tofile(tmp_path / "b.bin")
+    out = run_node(tmp_path, f"""
+const simd = require({os.path.join(JS, 'hip-simd.js')!r});
+const q = require({os.path.join(JS, 'hip-q4.js')!r});
+const eng = require({os.path.join(JS, 'engine-hip.js')!r});
+const K = meta.K, N = meta.N, M = meta.M;
+const W = [0, 1, 2, 3].map(i => rd('w' + i + '.bin', Float32Array));
+const x = rd('x.bin', Float32Array), b = rd('b.bin', Float32Array);
+const okq = q.init(), kat = q.selfTest(), ok = simd.init();
+const st0 = simd.getStats();
+const p = simd.allocWeights(W[0]);
+const c1 = new Float32Array(M * N); simd.matmulCached(x, M, K, p, N, b, c1); wr('cached.bin', c1);
+const c2 = new Float32Array(M * N); simd.matmul_general(x, M, K, W[0], N, c2); wr('general.bin', c2);
+const st1 = simd.getStats();
+const hip = new eng.HipEngine();
+hip.initWasm();
+const emb = {{ name: 'token_embedding', shape: [K, N], data: W[0] }};
+const res = [];
+for (let l = 1; l <= 3; l++) {{
+  simd.resetWeights();
+  emb._wasmPtr = simd.allocWeights(emb.data);
+  const t = {{ name: 'layer.w', shape: [K, N], data: W[l] }};
+  hip.cacheWeight(t);
+  const y = hip.tensorMulAdd({{ shape: [M, K], data: x }}, t, {{ data: b }}, 'y');
+  wr('layer' + l + '.bin', y.data);
+  res.push(parseFloat(simd.getStats().residentMB));
+}}
+let stale = false;
+const old = emb._wasmPtr;
+simd.resetWeights();
+try {{ simd.matmulCached(x, M, K, old, N, null, c1); }} catch (e) {{ stale = /not a live/.test(e.message); }}
+console.log(JSON.stringify({{ okq, kat, ok, st0, st1, res, stale, final: simd.getStats(), wasm: hip.wasmStats }}));
+""", {"K": K, "N": N, "M": M})
+    r = json.loads(out.strip().splitlines()[-1])
+    assert r["okq"] and r["kat"] and r["ok"]
+    assert r["st0"]["weightsMB"] == "0.0" and r["st0"]["scratchMB"] == "4.0"
+    assert r["st1"]["weightsMB"] == f"{K * N * 4 / 2**20:.1f}"
+    want = x.astype(np.float64) @ ws[0].astype(np.float64)
+    got_c = np.fromfile(tmp_path / "cached.bin", np.float32).reshape(M, N)
+    got_g = np.fromfile(tmp_path / "general.bin", np.float32).reshape(M, N)
+    assert rel_l2(got_c.ravel(), (want + bias).ravel()) <= 1e-5
+    assert rel_l2(got_g.ravel(), want.ravel()) <= 1e-5
+    for l in (1, 2, 3):
+        y = np.fromfile(tmp_path / f"layer{l}.bin", np.float32).reshape(M, N)
+        ref = x.astype(np.float64) @ ws[l].astype(np.float64) + bias
+        assert rel_l2(y.ravel(), ref.ravel()) <= 1e-5
+    # each layer: the layer weight resident, the embedding's copy deferred
+    assert max(r["res"]) <= K * N * 4 / 2**20 + 0.1, r["res"]
+    assert r["stale"]
+    assert r["final"]["residentMB"] == "0.0" and r["final"]["weightsMB"] == "0.0"
+    assert r["wasm"]["supported"]
+
+
 def test_llama_runtime_and_speculative_decoder(ctx, tmp_path):
     """HipLlamaRuntime loaded tensor by tensor under GGUF names: forward
     logits and greedy tokens match the same weights through the C ABI, and
@@ -194,6 +268,7 @@ const rt = mk();
 const logits = rt.forward(meta.prompt, 0);
 wr('logits.bin', logits);
 const gen = rt.generate(meta.prompt, 20, {{ greedy: true, eosId: -1 }});
+const genEos = rt.generate(meta.prompt, 20, {{ greedy: true, eosId: meta.eos }});
 rt.rollbackCache(5);
 const all = rt.forwardAll(meta.prompt.slice(5), 5);
 wr('all.bin', all.logits);
@@ -201,15 +276,19 @@ const dr = mk();
 const sd = new HipSpeculativeDecoder(rt, dr, {{ draftCount: 4 }});
 const sp = sd.generate(meta.prompt, 20, {{ eosIds: [] }});
 const sampled = rt.generate(meta.prompt, 4, {{ eosId: -1 }}).tokens.slice(meta.prompt.length);
-console.log(JSON.stringify({{ gen: gen.tokens.slice(meta.prompt.length), spec: sp.tokens.slice(meta.prompt.length),
+console.log(JSON.stringify({{ gen: gen.tokens.slice(meta.prompt.length), genEos: genEos.tokens.slice(meta.prompt.length),
+  genEosCount: genEos.generated, spec: sp.tokens.slice(meta.prompt.length),
   acc: sp.acceptanceRate, sampled, argmax: rt.argmax(logits) }}));
 rt.free(); dr.free();
-""", {"cfg": cfg, "files": files, "prompt": prompt})
+""", {"cfg": cfg, "files": files, "prompt": prompt, "eos": greedy[6]})
     res = json.loads(out.strip().splitlines()[-1])
     lj = np.fromfile(tmp_path / "logits.bin", np.float32)
     assert float(np.abs(lj - logits).max()) <= 2e-3
     assert res["argmax"] == int(np.argmax(lj))
     assert res["gen"] == greedy
+    # llama.js:475-489: the loop stops at the first EOS, which is the last token
+    stop = greedy.index(greedy[6]) + 1
+    assert res["genEos"] == greedy[:stop] and res["genEosCount"] == stop
     assert res["spec"][:20] == greedy
     assert len(res["sampled"]) == 4 and all(0 <= t < cfg["vocab_size"] for t in res["sampled"])
     allj = np.fromfile(tmp_path / "all.bin", np.float32).reshape(-1, cfg["vocab_size"])
