@@ -15,6 +15,9 @@ q/k/v/o/gate/up/down + LM head) through the plain instruction.
 Workload "m-gt-1": only the M>1 measurements of the default line (batched
 512-token prefill, the MFMA GEMM at M=512, M=5 verify, speculative decoding).
 
+Workload "small": only the stories15M-shaped (16-token prompt + 128 steps)
+and SmolLM2-135M-shaped (32 + 256) Q8_0 decode legs of the default line.
+
 Prints one JSON line: the bench contract plus `roofline` (the kernel with the
 largest share of a step: its algorithmic bytes over its mean execution time
 inside decode steps, from HIP events that the kernel's own dispatch stamps),
@@ -104,6 +107,126 @@ def cpu_baseline(host, cfg, seconds):
             "sample": f"{n} decode tokens of Q4_0 matvec work (16 layers x 7 matvecs, "
                       f"{threads} threads) + single-threaded f32 LM head, {dt:.1f}s; "
                       f"t1_value: {n1} tokens on 1 thread, {dt1:.1f}s"}
+
+
+def cpu_matvec_shapes(host_threads_n):
+    """The restated reference CPU kernel (wasm-q4.js:118-267 in SSE, the
+    thread-pool.js:174-227 row split, the per-call copy) on each Llama-1B
+    Q4_0 matvec shape: median of 10 calls after 3 warm-ups, GB/s of the
+    algorithmic bytes (weights + x + y)."""
+    import oracle
+    pool = oracle.CpuPool(host_threads_n)
+    res = {}
+    for name, N, K in (("q_o", 2048, 2048), ("k_v", 512, 2048), ("gate_up", 8192, 2048),
+                       ("down", 2048, 8192), ("lm_head", 128256, 2048)):
+        raw = oracle.quantize_q4_0(oracle.synth_normal(70 + N + K, N * K, 0.0, 0.02).reshape(N, K))
+        x = np.random.default_rng(K).normal(0, 1, K).astype(np.float32)
+        out = np.empty(N, np.float32)
+        ts = []
+        for i in range(13):
+            t0 = time.perf_counter()
+            pool.q4_0_matvec(x, raw, N, K, out)
+            ts.append(time.perf_counter() - t0)
+        t = sorted(ts[3:])[5]
+        by = q4_bytes(N, K) + 4 * (N + K)
+        res[name] = {"N": N, "K": K, "us": round(t * 1e6, 1), "GBps": round(by / t / 1e9, 3)}
+    pool.close()
+    log("cpu matvec shapes (" + str(host_threads_n) + " threads): " +
+        ", ".join(f"{k} {v['GBps']:.2f} GB/s" for k, v in res.items()))
+    return {"threads": host_threads_n, "kind": "port", "shapes": res}
+
+
+def cpu_stories_decode(seconds):
+    """Config 1's path in the reference, restated: per token, 6 layers x 7
+    matmul_q8 calls (quantize.js:224-266 on QuantizedTensor [K,N], as LINEAR
+    -> tensorMulAddQ8 runs them, engine.js:259-269) and the f32 LM head over
+    the 32000 x 288 embedding (llama.js:353-367), on one thread as the
+    reference's main JS thread runs them.  Attention and norms (a small
+    share of its time) are left out of the sample."""
+    import oracle
+    d, h, L, V = 288, 768, 6, 32000
+    rng = np.random.default_rng(5)
+    mats = []
+    for K, N in ((d, d), (d, d), (d, d), (d, d), (d, h), (d, h), (h, d)):
+        q, sc = oracle.quantize_q8_ref(rng.normal(0, 0.02, (K, N)).astype(np.float32))
+        mats.append((K, N, q, sc))
+    emb = rng.normal(0, 0.02, V * d).astype(np.float32)
+    xs = {K: rng.normal(0, 1, (1, K)).astype(np.float32) for K in (d, h)}
+
+    def one_token():
+        for _ in range(L):
+            for K, N, q, sc in mats:
+                oracle.matmul_q8_ref(xs[K], q, sc, N)
+        oracle.cpu_lm_head(xs[d][0], emb, V, d)
+
+    one_token()
+    t0 = time.perf_counter()
+    one_token()
+    per = time.perf_counter() - t0
+    n = max(3, min(2000, int(seconds / max(per, 1e-4))))
+    t0 = time.perf_counter()
+    for _ in range(n):
+        one_token()
+    dt = time.perf_counter() - t0
+    log(f"cpu stories15M q8 decode (restated llama.js path, 1 thread): {n / dt:.1f} tok/s")
+    return {"value": round(n / dt, 2), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"{n} decode tokens: 6 layers x 7 matmul_q8 (M=1) + f32 LM head 32000x288, "
+                      f"{dt:.1f}s"}
+
+
+def run_small_decode(pb, synth, name, n_prompt, n_gen):
+    """Configs 1 and 3: greedy decode of n_gen tokens after a random
+    n_prompt-token prompt, timed over the whole generate call (HIP events on
+    the model's stream), plus the per-kernel times of 16 steps launched
+    kernel by kernel and the roofline of the step's largest kernel."""
+    cfg = synth.CONFIGS[name]
+    ctx = pb.Context(0)
+    model = synth.build(ctx, cfg, seed=1000)
+    prompt = synth.random_tokens(7, n_prompt, cfg["vocab_size"])
+    model.forward(prompt, 0, want_logits=False)
+    model.reset_cache()
+    t0 = time.perf_counter()
+    _, nxt = model.forward(prompt, 0, want_logits=False)
+    prefill_s = time.perf_counter() - t0
+    model.generate(nxt, n_prompt, 16)
+    model.rollback(n_prompt)
+    ctx.sync()
+    ctx.timer_start()
+    model.generate(nxt, n_prompt, n_gen)
+    ms = ctx.timer_stop() / n_gen
+    model.rollback(n_prompt)
+    prof = model.profile(nxt, n_prompt, 16)
+    roles = {}
+    for role, kern, us, by in prof:
+        r = roles.setdefault(role, {"kernel": kern, "launches_per_step": 0, "us_per_step": 0.0,
+                                    "bytes_per_step": 0.0})
+        r["launches_per_step"] += 1
+        r["us_per_step"] += us
+        r["bytes_per_step"] += by
+    for r in roles.values():
+        r["us_per_launch_in_step"] = round(r["us_per_step"] / r["launches_per_step"], 3)
+        r["GBps"] = round(r["bytes_per_step"] / r["us_per_step"] / 1e3, 1) if r["us_per_step"] else 0.0
+        r["us_per_step"] = round(r["us_per_step"], 2)
+        r["bytes_per_step"] = round(r["bytes_per_step"])
+    dom_name, dom = max(roles.items(), key=lambda kv: kv[1]["us_per_step"])
+    gbps = dom["bytes_per_step"] / dom["us_per_step"] / 1e3
+    step_bytes = sum(r["bytes_per_step"] for r in roles.values())
+    log(f"{name}: decode {n_gen} steps (KV {n_prompt}->{n_prompt + n_gen}) {ms * 1e3:.1f} us/token, "
+        f"{1e3 / ms:.1f} tok/s; largest kernel {dom_name} ({dom['kernel']}) "
+        f"{dom['us_per_launch_in_step']:.2f} us a launch, {gbps:.0f} GB/s")
+    out = {"workload": f"{name}-shaped {'q8_0'} greedy decode, batch 1, {n_prompt}-token prompt "
+                       f"then {n_gen} steps",
+           "tok_per_s": round(1e3 / ms, 2), "ms_per_token": round(ms, 5),
+           "prefill_ms": round(prefill_s * 1e3, 3), "bytes_per_step": step_bytes,
+           "effective_GBps": round(step_bytes / ms / 1e6, 1),
+           "roofline": {"bound": "hbm", "kernel": f"{dom['kernel']} ({dom_name})",
+                        "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbps / HBM_PEAK_GBS, 4),
+                        "us_per_launch": dom["us_per_launch_in_step"]},
+           "kernels": roles}
+    model.free()
+    ctx.close()
+    return out
 
 
 COPY_BYTES = 256 << 20
@@ -309,6 +432,13 @@ def run_decode(args, pb, synth):
         log("timing the restated reference CPU path ...")
         cpu = cpu_baseline(host, cfg, args.cpu_seconds)
         log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
+        cpu["matvec_shapes"] = cpu_matvec_shapes(cpu["cores"])
+    small = None
+    if not args.no_small_configs:
+        small = {"stories15m": run_small_decode(pb, synth, "stories15m", 16, 128),
+                 "smollm2_135m": run_small_decode(pb, synth, "smollm2_135m", 32, 256)}
+        if not args.no_cpu_baseline:
+            small["stories15m"]["cpu_baseline"] = cpu_stories_decode(args.cpu_seconds * 0.5)
     out = {
         "metric": METRIC,
         "value": round(1e3 / ms_per_step, 2),
@@ -346,6 +476,7 @@ def run_decode(args, pb, synth):
         "matvec_shapes": matvec_shapes,
         "m_gt_1": m_gt_1,
         "next_rows": next_rows,
+        "small_configs": small,
         "cpu_baseline": cpu,
     }
     model.free()
@@ -686,12 +817,14 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--workload", choices=("decode", "matvec", "pmc-probe", "m-gt-1"),
+    ap.add_argument("--workload", choices=("decode", "matvec", "pmc-probe", "m-gt-1", "small"),
                     default="decode")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-m-gt-1", action="store_true",
                     help="skip the prefill / verify / speculative measurements")
+    ap.add_argument("--no-small-configs", action="store_true",
+                    help="skip the stories15M and SmolLM2 decode legs")
     ap.add_argument("--no-matvec-shapes", action="store_true",
                     help="skip the isolated matvec shapes (their timing captures HIP graphs, "
                          "which rocprofv3's kernel tracer can fault on)")
@@ -714,6 +847,12 @@ def main():
     from purebee_amd import synth
     if args.workload == "pmc-probe":
         run_pmc_probe(args, pb, synth)
+        return
+    if args.workload == "small":
+        res = {"stories15m": run_small_decode(pb, synth, "stories15m", 16, 128),
+               "smollm2_135m": run_small_decode(pb, synth, "smollm2_135m", 32, 256)}
+        print(json.dumps({"workload": "stories15M and SmolLM2-shaped q8_0 decode",
+                          "small_configs": res}), flush=True)
         return
     if args.workload == "m-gt-1":
         cfg = synth.CONFIGS["llama32_1b"]
