@@ -268,6 +268,11 @@ struct AttnArgs {
   // and a tag offset that only a test sets (the cells then never match)
   int *status;
   int spin, skew;
+  // the small-model step (pbx_small_step_q8): the tag comes from *epoch
+  // instead of cells[cell_n], and the head's output is published as cells
+  // (tag << 32 | value bits) at ocells + h * head_dim instead of stored
+  const unsigned long long *epoch;
+  unsigned long long *ocells;
 };
 
 // One workgroup per query head (llama.js:258-301 / llama-streaming.js:543-573):
@@ -737,10 +742,13 @@ __device__ __forceinline__ float poll_cell(const unsigned long long *cp, unsigne
   return __builtin_nanf("");
 }
 
-template <bool SPEC, int IPT = 0, bool FUSED = false>
+// MAXJ: position slots a wave keeps in flight (16 slots of K and V are
+// 128 registers a lane; a caller with less room passes fewer).
+template <bool SPEC, int IPT = 0, bool FUSED = false, int MAXJ = 16>
 __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const int pos_arg,
                                                       const int bid = -1) {
-  static_assert(!FUSED || (SPEC && IPT > 0), "fused: device position, head_dim 64");
+  static_assert(MAXJ >= 1 && MAXJ <= 16, "1..16 slots");
+  static_assert(!FUSED || SPEC, "fused: device position");
   __shared__ float st_m[PBX_HA_WAVES], st_l[PBX_HA_WAVES];
   __shared__ __attribute__((aligned(16))) float st_acc[PBX_HA_WAVES][PBX_HA_MAX_HD];
   __shared__ float o_h[IPT > 0 ? 64 : 1], o_sum[2];
@@ -790,33 +798,40 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
   float m = -INFINITY, l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   int s0 = 0;
+  unsigned tag = 0;
   if constexpr (FUSED) {
-    const unsigned tag = cell_tag(a.cells[a.cell_n]) + (unsigned)a.skew;
+    tag = cell_tag(a.epoch ? *a.epoch : a.cells[a.cell_n]) + (unsigned)a.skew;
     const int spin = a.spin > 0 ? a.spin : PBX_CELL_SPIN;
     float4 kn = make_float4(0.f, 0.f, 0.f, 0.f), vn = kn;
     auto ready = [&]() {
       if (w < 3) {  // wave 0: q of head h; 1, 2: k, v of KV head g
         nrow[w][lane] =
-            poll_cell(a.cells + (w == 0 ? h * hd : a.qdim + (w - 1) * kvdim + g * hd) + lane, tag,
-                      spin, a.status);
+            lane < hd ? poll_cell(a.cells + (w == 0 ? h * hd : a.qdim + (w - 1) * kvdim + g * hd) +
+                                      lane,
+                                  tag, spin, a.status)
+                      : 0.f;
       }
       lds_barrier();
       const float4 q4 = *reinterpret_cast<const float4 *>(&nrow[0][dcol]);
-      qq = make_float4(q4.x * c, q4.y * c, q4.z * c, q4.w * c);
+      // lanes past head_dim / 4 repeat the last dims: their q stays 0
+      qq = dg < hd4 ? make_float4(q4.x * c, q4.y * c, q4.z * c, q4.w * c)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
       kn = *reinterpret_cast<const float4 *>(&nrow[1][dcol]);
       vn = *reinterpret_cast<const float4 *>(&nrow[2][dcol]);
     };
     auto none = [] {};
     bool first = true;
     while (32 * s0 < nc) {
-      const int J = min(16, (nc - 32 * s0 + 31) / 32);
+      const int J = min(MAXJ, (nc - 32 * s0 + 31) / 32);
       switch (J) {
 #define PBX_HEAD_CHUNK_N(n)                                                                \
   case n:                                                                                  \
-    if (first)                                                                             \
-      head_chunk_n<n>(kb, vb, kvdim, dcol, s0, pl, nc, ready, qq, kn, vn, m, l, acc);      \
-    else                                                                                   \
-      head_chunk_n<n>(kb, vb, kvdim, dcol, s0, pl, nc, none, qq, kn, vn, m, l, acc);       \
+    if constexpr (n <= MAXJ) {                                                             \
+      if (first)                                                                           \
+        head_chunk_n<n>(kb, vb, kvdim, dcol, s0, pl, nc, ready, qq, kn, vn, m, l, acc);    \
+      else                                                                                 \
+        head_chunk_n<n>(kb, vb, kvdim, dcol, s0, pl, nc, none, qq, kn, vn, m, l, acc);     \
+    }                                                                                      \
     break;
         PBX_HEAD_CHUNK_N(1) PBX_HEAD_CHUNK_N(2) PBX_HEAD_CHUNK_N(3) PBX_HEAD_CHUNK_N(4)
         PBX_HEAD_CHUNK_N(5) PBX_HEAD_CHUNK_N(6) PBX_HEAD_CHUNK_N(7) PBX_HEAD_CHUNK_N(8)
@@ -880,7 +895,15 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
       num = fmaf(__shfl(e, i, 64), st_acc[i][lane], num);
     const float dn = __shfl(den, 0, 64);
     if constexpr (IPT == 0) {
-      if (lane < hd) a.out[(size_t)h * hd + lane] = num / dn;
+      if (lane < hd) {
+        const float o = num / dn;
+        if (FUSED && a.ocells)  // published with the launch's own tag (no test offset)
+          __hip_atomic_store(a.ocells + (size_t)h * hd + lane,
+                             (unsigned long long)(tag - (unsigned)a.skew) << 32 | __float_as_uint(o),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          a.out[(size_t)h * hd + lane] = o;
+      }
     } else {
       const float o = num / dn;  // head_dim 64: every lane
       o_h[lane] = o;
@@ -1128,6 +1151,339 @@ extern "C" __global__ void __launch_bounds__(1024) pbx_ffn_q4_d2048_h8192(GemvAr
   const long long v = (long long)(t & ((1ull << 56) - 1)) - (long long)S * (1ll << 51);
   f.xout[row] = (t >> 60) ? __builtin_nanf("")
                           : (float)fma((double)v, 0x1p-32, (double)residual_acc(xr, ar));
+}
+
+// ---------------------------------------------------------------------------
+// Small models: every layer of a decode step in one launch.
+//
+// For Q8_0 layers with dim <= 1024, hidden <= 4096 and head_dim <= 64
+// (stories15M- and SmolLM2-135M-shaped models) each GEMV of a layer moves
+// 0.1-2 MB: as separate launches every one of them sits on the ~5 us floor
+// of a launch (dispatch, the activation round trip, one weight round trip),
+// five a layer.  Here G workgroups of 512 threads (one a CU, all resident:
+// the host keeps G <= the CU count) run all the layers of the step; the
+// phases of a layer hand their outputs on as 64-bit cells, (tag << 32) |
+// value bits, written by relaxed device-scope stores, and the next phase's
+// workgroups poll the cells they need (bounded like the joined Llama
+// launches: after `spin` polls a value is NaN and the status word is
+// marked).  Layer l, workgroup j:
+//   1. RMSNorm(x) (x: the step's row for l = 0, else the cells layer l - 1
+//      published), the q|k|v rows [rq j, rq j + rq) (even: RoPE pairs), RoPE
+//      of q and k, k and v appended at the position, all three published;
+//   2. j < n_heads: the attention of query head j (the decode attention
+//      body, which waits for q of its head and k, v of its KV head and reads
+//      the older positions from the cache), o_h published;
+//   3. the o projection's rows [ro j, ..) + the residual, published (x1);
+//   4. RMSNorm(x1), the gate|up columns [rg j, ..): silu(g) * u published;
+//   5. the down projection's rows [rd j, ..) + x1, published as layer
+//      l + 1's input (the last layer stores it to x for the LM head).
+// A task is one 32-block of one weight row (32 bytes of codes and its fp16
+// scale): thread t takes tasks t, t + 512, ... of a GEMV; the partial dots
+// meet in LDS, 8 threads a row.  The q|k|v bytes are requested when the
+// layer starts, the others when the attention is done, so they arrive
+// under the hand-offs.  Cells are written once a step with the step's tag,
+// cell_tag(*epoch); the last workgroup to finish advances *epoch.
+// ---------------------------------------------------------------------------
+#define PBX_SM_T (PBX_HA_WAVES * 64)  // threads a workgroup (the attention body's)
+#define PBX_SM_MAXD 1024
+#define PBX_SM_MAXH 4096
+#define PBX_SM_SQ 2  // task slots a thread: q|k|v, o, gate|up, down
+#define PBX_SM_SO 1
+#define PBX_SM_SG 4
+#define PBX_SM_SD 2
+#define PBX_SM_MAXR 256  // rows of one GEMV a workgroup
+// GEMV activations in LDS: 32-value block b at 36 b (4 floats of padding):
+// the 16-byte reads of 16 lanes at consecutive blocks then cover all 64
+// banks once (at 32 floats a block they would meet in 8 of them).
+#define PBX_SM_BLK 36
+__device__ __forceinline__ int sm_pad(int i) { return (i >> 5) * PBX_SM_BLK + (i & 31); }
+
+struct SmallLayer {
+  const uint8_t *qkv_qs, *o_qs, *gu_qs, *d_qs;
+  const uint16_t *qkv_d, *o_d, *gu_d, *d_d;
+  const float *attn_norm, *ffn_norm;
+};
+
+struct SmallArgs {
+  const SmallLayer *layers;   // [n_layers] in device memory
+  AttnArgs at;                // layer 0's cache rows, the heads, state, status and poll limit
+  long long layer_kv;         // cache floats of one layer
+  unsigned long long *cells;  // layer l: cell_stride cells [q|k|v | o_h | x1 | h | next x]
+  long long cell_stride;
+  unsigned long long *epoch;  // the step's tag is cell_tag(*epoch)
+  unsigned *done;             // workgroups finished (zero between launches)
+  float *x;                   // layer 0's input; the last layer's output
+  int n_layers, dim, hidden, qkv_rows;
+  float eps;
+  int rq, ro, rg, rd;         // rows (rg: gate|up columns) a workgroup
+  int test_layer, skew;       // test hook: that layer's waits expect tag + skew
+};
+
+// One task slot: 32 codes, the block's scale bits (0 for an empty slot).
+struct SmSlot {
+  uint4 a, b;
+  unsigned d;
+};
+
+// Task t of a GEMV with B blocks a row; row_of maps the workgroup's row
+// index to the weight row.  Loads are unconditional (an empty slot reads
+// the first task's bytes and gets a zero scale).
+template <class RowOf>
+__device__ __forceinline__ SmSlot sm_load(const uint8_t *qs, const uint16_t *dsc, int B, int ntask,
+                                          int t, RowOf row_of) {
+  const bool ok = t < ntask;
+  const int tt = ok ? t : 0;
+  const int r = row_of(tt / B), b = tt % B;
+  SmSlot s;
+  const uint8_t *src = qs + ((size_t)r * B + b) * 32;
+  s.a = ld_stream(src);
+  s.b = ld_stream(src + 16);
+  s.d = dsc[dsc_index(r, b, B)] & (ok ? 0xFFFFu : 0u);
+  return s;
+}
+
+// The slot's partial dot with the activations of its block (LDS).
+__device__ __forceinline__ float sm_dot(const SmSlot &s, const float *xb) {
+  float xr[32];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const float4 f = *reinterpret_cast<const float4 *>(xb + 4 * v);
+    xr[4 * v] = f.x;
+    xr[4 * v + 1] = f.y;
+    xr[4 * v + 2] = f.z;
+    xr[4 * v + 3] = f.w;
+  }
+  float xs = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) xs += xr[i];
+  return (dot_q8(s.a, s.b, xr) - 128.f * xs) * f16_bits_to_f32(s.d);
+}
+
+// Partial dots of S slots into part[task] (then a barrier); act holds the
+// activations in the padded layout (sm_pad).
+template <int S>
+__device__ __forceinline__ void sm_dots(const SmSlot (&sl)[S], int B, int ntask, const float *act,
+                                        float *part) {
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int t = (int)threadIdx.x + PBX_SM_T * i;
+    if (t < ntask) part[t] = sm_dot(sl[i], act + (size_t)(t % B) * PBX_SM_BLK);
+  }
+  __syncthreads();
+}
+
+// Sum of row i's B partials (8 threads a row: threads 8i .. 8i + 7 all
+// return it).
+__device__ __forceinline__ float sm_row(const float *part, int i, int B) {
+  const int sub = threadIdx.x & 7;
+  float v = 0.f;
+  for (int b = sub; b < B; b += 8) v += part[i * B + b];
+  return group_sum<8>(v);
+}
+
+__device__ __forceinline__ void sm_publish(unsigned long long *cell, unsigned tag, float v) {
+  __hip_atomic_store(cell, (unsigned long long)tag << 32 | __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// n published cells (n <= P * 512) into dst (LDS; PAD: the padded GEMV
+// layout), polled until they carry tag; after `spin` polls the missing ones
+// are NaN and the status word is marked.  The values are written after a
+// barrier (dst may still be read before) and a barrier follows.
+template <int P, bool PAD>
+__device__ __forceinline__ void sm_poll(const unsigned long long *cells, int n, unsigned tag,
+                                        int spin, int *status, float *dst) {
+  const int tid = threadIdx.x;
+  unsigned long long v[P];
+#pragma unroll
+  for (int k = 0; k < P; ++k) {
+    const int i = tid + PBX_SM_T * k;
+    v[k] = i < n ? __hip_atomic_load(cells + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                 : (unsigned long long)tag << 32;
+  }
+  auto missing = [&]() {
+    bool r = false;
+#pragma unroll
+    for (int k = 0; k < P; ++k) r |= (unsigned)(v[k] >> 32) != tag;
+    return r;
+  };
+  for (int it = 0; missing() && it < spin; ++it) {
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int k = 0; k < P; ++k)
+      if ((unsigned)(v[k] >> 32) != tag)
+        v[k] = __hip_atomic_load(cells + tid + PBX_SM_T * k, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (missing())
+    __hip_atomic_fetch_or(status, PBX_DEV_WAIT_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < P; ++k) {
+    const int i = tid + PBX_SM_T * k;
+    if (i < n)
+      dst[PAD ? sm_pad(i) : i] =
+          (unsigned)(v[k] >> 32) == tag ? __uint_as_float((unsigned)v[k]) : __builtin_nanf("");
+  }
+  __syncthreads();
+}
+
+// out = x * (1 / rms(x)) * w over n values in LDS (llama.js's RMSNorm; w
+// from memory, requested by the caller); out in the padded layout.
+__device__ __forceinline__ void sm_rmsnorm(const float *x, const float (&w)[2], float *out, int n,
+                                           float eps, float *red) {
+  const int tid = threadIdx.x;
+  float ss = 0.f;
+  for (int i = tid; i < n; i += PBX_SM_T) ss = fmaf(x[i], x[i], ss);
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w8 = 0; w8 < PBX_HA_WAVES; ++w8) tot += red[w8];
+  const float inv = 1.0f / sqrtf(tot / (float)n + eps);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = tid + PBX_SM_T * k;
+    if (i < n) out[sm_pad(i)] = x[i] * inv * w[k];
+  }
+  __syncthreads();
+}
+
+extern "C" __global__ void __launch_bounds__(PBX_SM_T) pbx_small_step_q8(SmallArgs a) {
+  __shared__ __attribute__((aligned(16))) float xin[PBX_SM_MAXD];  // the layer's residual row
+  // a GEMV's activations (padded layout)
+  __shared__ __attribute__((aligned(16))) float act[PBX_SM_MAXH / 32 * PBX_SM_BLK];
+  __shared__ float part[PBX_SM_T * PBX_SM_SG];                      // partial dots
+  __shared__ float rowv[PBX_SM_MAXR];                               // gate|up row sums
+  __shared__ float red[PBX_HA_WAVES];
+  const int j = blockIdx.x, tid = threadIdx.x;
+  const int dim = a.dim, hidden = a.hidden, qr = a.qkv_rows;
+  const int B = dim / 32, BH = hidden / 32;
+  const int kvdim = a.at.n_kv_heads * a.at.head_dim, hd = a.at.head_dim;
+  const int pos = a.at.state[0];
+  const unsigned tag0 = cell_tag(*a.epoch);
+  const int spin = a.at.spin > 0 ? a.at.spin : PBX_CELL_SPIN;
+  int *status = a.at.status;
+  // the workgroup's rows of each GEMV
+  const int q0 = j * a.rq, nq = max(0, min(a.rq, qr - q0));
+  const int o0 = j * a.ro, no = max(0, min(a.ro, dim - o0));
+  const int c0 = j * a.rg, ng = max(0, min(a.rg, hidden - c0));
+  const int d0 = j * a.rd, nd = max(0, min(a.rd, dim - d0));
+
+  for (int l = 0; l < a.n_layers; ++l) {
+    const SmallLayer L = a.layers[l];
+    unsigned long long *cq = a.cells + (size_t)l * a.cell_stride;
+    unsigned long long *co = cq + qr, *cx1 = co + dim, *ch = cx1 + dim, *cn = ch + hidden;
+    // cells are published with the step's tag; the test hook's layer waits
+    // for another one (its waits give up, every workgroup still finishes)
+    const unsigned tag = tag0, want = tag0 + (l == a.test_layer ? (unsigned)a.skew : 0u);
+    // 1. the q|k|v bytes and the norm weights, then the layer's input row
+    SmSlot sq[PBX_SM_SQ];
+#pragma unroll
+    for (int i = 0; i < PBX_SM_SQ; ++i)
+      sq[i] = sm_load(L.qkv_qs, L.qkv_d, B, nq * B, tid + PBX_SM_T * i,
+                      [&](int r) { return min(q0 + r, qr - 1); });
+    float nw[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) nw[k] = L.attn_norm[min(tid + PBX_SM_T * k, dim - 1)];
+    if (l == 0) {
+      __syncthreads();
+      for (int i = tid; i < dim; i += PBX_SM_T) xin[i] = a.x[i];
+      __syncthreads();
+    } else {
+      // the next-x cells of layer l - 1 (its cn)
+      const unsigned long long *prev = cq - a.cell_stride + qr + 2 * dim + hidden;
+      sm_poll<2, false>(prev, dim, want, spin, status, xin);
+    }
+    sm_rmsnorm(xin, nw, act, dim, a.eps, red);
+    sm_dots(sq, B, nq * B, act, part);
+    for (int i = tid >> 3; i < ((nq + 7) & ~7); i += PBX_SM_T / 8) {
+      // rows 2i', 2i' + 1 sit in adjacent 8-thread groups of one wave
+      const float v = i < nq ? sm_row(part, i, B) : 0.f;
+      const float pv = __shfl_xor(v, 8, 64);
+      if (i < nq && (tid & 7) == 0) {
+        const int n = q0 + i;
+        float o = v;
+        if (n < dim + kvdim) {
+          const float2 cs =
+              *reinterpret_cast<const float2 *>(a.at.rope + (size_t)pos * hd + ((n & ~1) % hd));
+          o = (n & 1) ? fmaf(pv, cs.y, v * cs.x) : fmaf(v, cs.x, -pv * cs.y);
+          if (n >= dim) a.at.kcache[(size_t)l * a.layer_kv + (size_t)pos * kvdim + (n - dim)] = o;
+        } else {
+          a.at.vcache[(size_t)l * a.layer_kv + (size_t)pos * kvdim + (n - dim - kvdim)] = o;
+        }
+        sm_publish(cq + n, tag, o);
+      }
+    }
+    // 2. attention of query head j
+    if (j < a.at.n_heads) {
+      AttnArgs at = a.at;
+      at.kcache += (size_t)l * a.layer_kv;
+      at.vcache += (size_t)l * a.layer_kv;
+      at.cells = cq;
+      at.qdim = dim;
+      at.epoch = a.epoch;
+      at.ocells = co;
+      at.skew = l == a.test_layer ? a.skew : 0;
+      attention_cached_body<true, 0, true, 8>(at, 0, j);
+    }
+    // 3. o projection + residual
+    SmSlot so[PBX_SM_SO];
+#pragma unroll
+    for (int i = 0; i < PBX_SM_SO; ++i)
+      so[i] = sm_load(L.o_qs, L.o_d, B, no * B, tid + PBX_SM_T * i,
+                      [&](int r) { return min(o0 + r, dim - 1); });
+    SmSlot sg[PBX_SM_SG];
+#pragma unroll
+    for (int i = 0; i < PBX_SM_SG; ++i)
+      sg[i] = sm_load(L.gu_qs, L.gu_d, B, 2 * ng * B, tid + PBX_SM_T * i,
+                      [&](int r) { return min(r < ng ? c0 + r : hidden + c0 + r - ng, 2 * hidden - 1); });
+    SmSlot sd[PBX_SM_SD];
+#pragma unroll
+    for (int i = 0; i < PBX_SM_SD; ++i)
+      sd[i] = sm_load(L.d_qs, L.d_d, BH, nd * BH, tid + PBX_SM_T * i,
+                      [&](int r) { return min(d0 + r, dim - 1); });
+#pragma unroll
+    for (int k = 0; k < 2; ++k) nw[k] = L.ffn_norm[min(tid + PBX_SM_T * k, dim - 1)];
+    sm_poll<2, true>(co, dim, want, spin, status, act);
+    sm_dots(so, B, no * B, act, part);
+    for (int i = tid >> 3; i < no; i += PBX_SM_T / 8) {
+      const float v = sm_row(part, i, B);
+      if ((tid & 7) == 0) sm_publish(cx1 + o0 + i, tag, xin[o0 + i] + v);
+    }
+    // 4. RMSNorm + gate|up + SwiGLU
+    sm_poll<2, false>(cx1, dim, want, spin, status, xin);
+    sm_rmsnorm(xin, nw, act, dim, a.eps, red);
+    sm_dots(sg, B, 2 * ng * B, act, part);
+    for (int i = tid >> 3; i < 2 * ng; i += PBX_SM_T / 8) {
+      const float v = sm_row(part, i, B);
+      if ((tid & 7) == 0) rowv[i] = v;
+    }
+    __syncthreads();
+    for (int i = tid; i < ng; i += PBX_SM_T) sm_publish(ch + c0 + i, tag, silu(rowv[i]) * rowv[ng + i]);
+    // 5. down + residual
+    sm_poll<PBX_SM_MAXH / PBX_SM_T, true>(ch, hidden, want, spin, status, act);
+    sm_dots(sd, BH, nd * BH, act, part);
+    for (int i = tid >> 3; i < nd; i += PBX_SM_T / 8) {
+      const float v = sm_row(part, i, BH);
+      if ((tid & 7) == 0) {
+        const float xo = xin[d0 + i] + v;
+        if (l + 1 == a.n_layers) a.x[d0 + i] = xo;
+        else sm_publish(cn + d0 + i, tag, xo);
+      }
+    }
+  }
+  // the last workgroup out advances the step's epoch (every workgroup read
+  // it when it started)
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned d = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d + 1 == gridDim.x) {
+      __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.epoch, next_epoch(*a.epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // Batched rows (speculative verify, short batches; head_dim <= 64): workgroup

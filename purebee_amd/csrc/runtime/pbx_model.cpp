@@ -46,6 +46,9 @@ struct AttnArgsHost {  // AttnArgs in pbx_decode.hip
   // (0: the kernel's default) and the test-only tag offset
   int *status = nullptr;
   int spin = 0, skew = 0;
+  // the small-model step: the tag's epoch and the published head outputs
+  const unsigned long long *epoch = nullptr;
+  unsigned long long *ocells = nullptr;
 };
 
 struct AttnSplitArgsHost {  // AttnSplitArgs in pbx_decode.hip
@@ -98,8 +101,30 @@ struct FfnArgsHost {  // FfnArgs in pbx_decode.hip
   int spin = 0;
 };
 
+struct SmallLayerHost {  // SmallLayer in pbx_decode.hip
+  const void *qkv_qs, *o_qs, *gu_qs, *d_qs;
+  const void *qkv_d, *o_d, *gu_d, *d_d;
+  const float *attn_norm, *ffn_norm;
+};
+
+struct SmallArgsHost {  // SmallArgs in pbx_decode.hip
+  const SmallLayerHost *layers = nullptr;
+  AttnArgsHost at{};
+  long long layer_kv = 0;
+  unsigned long long *cells = nullptr;
+  long long cell_stride = 0;
+  unsigned long long *epoch = nullptr;
+  unsigned *done = nullptr;
+  float *x = nullptr;
+  int n_layers = 0, dim = 0, hidden = 0, qkv_rows = 0;
+  float eps = 0.f;
+  int rq = 0, ro = 0, rg = 0, rd = 0;
+  int test_layer = -1, skew = 0;
+};
+
 enum ArgKind {
-  ARG_GEMV, ARG_ATTN, ARG_ATTN_SPLIT, ARG_COMBINE, ARG_EMBED, ARG_ARGMAX, ARG_FUSED, ARG_FFN
+  ARG_GEMV, ARG_ATTN, ARG_ATTN_SPLIT, ARG_COMBINE, ARG_EMBED, ARG_ARGMAX, ARG_FUSED, ARG_FFN,
+  ARG_SMALL
 };
 enum AttnMode { ATTN_HEAD, ATTN_SPLIT, ATTN_DECODE };
 
@@ -118,6 +143,7 @@ struct Op {
   EmbedArgsHost embed;
   ArgmaxArgsHost amax;
   FfnArgsHost ffn;  // ARG_FFN: the down projection's arguments (gemv: gate|up)
+  SmallArgsHost small;  // ARG_SMALL: every layer of the step in one launch
   int np = 0;  // ARG_FUSED: GEMV workgroups before the attention's
 };
 
@@ -180,6 +206,12 @@ struct pbx_model {
   bool ffn_join = true, ffn_joined = false;
   float *x2 = nullptr;
   unsigned long long *ffn_cell = nullptr, *h_cells = nullptr;
+  // small models (pbx_small_step_q8; PBX_SMALL_STEP=0 at creation: a launch
+  // per GEMV and attention): ops[0] runs every layer of the step; its layer
+  // table, per-layer cells, the step epoch and the finished-workgroup count
+  bool small_ok = true, small_step = false;
+  SmallLayerHost *small_layers = nullptr;
+  unsigned long long *small_cells = nullptr, *small_sync = nullptr;
   uint64_t *partials = nullptr;
   int n_partials_cap = 0;
   bool gemv_int = true;  // integer-limb GEMV kernels where they apply
@@ -467,6 +499,123 @@ static int pack_head_lanes(pbx_model *m) {
   const int64_t total = (int64_t)N * B;
   return pbx_launch_fn(m->c, f, "pbx_pack_q6_k_lanes", dim3((unsigned)((total + 255) / 256)),
                        dim3(256), args, m->c->stream);
+}
+
+// Small models (pbx_small_step_q8: Q8_0 layers, dim <= 1024, hidden <=
+// 4096, head_dim <= 64): the per-layer ops give way to one op that runs
+// every layer of the step in G workgroups (ops[0]); the LM head and the
+// argmax follow as before.  G starts at dim / 6 rounded up to a multiple of
+// 8, at least 32 (measured: stories15M's dim 288 ran 109-110 us a token at
+// 32-64 workgroups, SmolLM2's dim 576 435.6 at 96 against 463.5 at 64 and
+// 441.3 at 128), and grows until the per-workgroup rows fit the kernel's
+// task slots; it stays at or below the CU count (every workgroup must be
+// resident) and at or above the query head count.  PBX_SMALL_WGS sets the
+// start.
+static int plan_small_step(pbx_model *m) {
+  m->small_step = false;
+  const pbx_model_config &g = m->cfg;
+  pbx_ctx *c = m->c;
+  const int nl = g.n_layers, hd = g.head_dim, kvdim = m->kvdim;
+  if (!m->small_ok || nl < 1 || g.dim % 32 || g.hidden_dim % 32 || g.dim > 1024 ||
+      g.hidden_dim > 4096 || hd > 64 || hd % 4 || g.n_heads % g.n_kv_heads ||
+      m->qkv_rows != g.dim + 2 * kvdim)
+    return PBX_OK;
+  const int B = g.dim / 32, BH = g.hidden_dim / 32;
+  for (int l = 0; l < nl; ++l) {
+    const Layer &L = m->layers[l];
+    const pbx_weight *w[4] = {L.wqkv, L.wo, L.wgu, L.wd};
+    const int64_t rows[4] = {m->qkv_rows, g.dim, 2 * (int64_t)g.hidden_dim, g.dim};
+    const int64_t blocks[4] = {B, B, B, BH};
+    for (int k = 0; k < 4; ++k)
+      if (w[k]->type != PBX_TYPE_Q8_0 || w[k]->N != rows[k] || w[k]->B != blocks[k]) return PBX_OK;
+  }
+  hipFunction_t f = pbx_kernel_by_name(c, "pbx_small_step_q8");
+  if (!f) return PBX_OK;
+  int G = 0, rq = 0, ro = 0, rg = 0, rd = 0;
+  int g0 = std::max(32, (g.dim / 6 + 7) / 8 * 8);
+  if (const char *e = getenv("PBX_SMALL_WGS")) g0 = std::max(8, atoi(e));
+  for (int cand = g0; cand <= c->cu_count; cand += 8) {
+    rq = 2 * ((m->qkv_rows + 2 * cand - 1) / (2 * cand));
+    ro = (g.dim + cand - 1) / cand;
+    rg = (g.hidden_dim + cand - 1) / cand;
+    rd = (g.dim + cand - 1) / cand;
+    // task slots a thread of 512: q|k|v 2, o 1, gate|up 4 (<= 256 rows), down 2
+    if (cand >= g.n_heads && rq * B <= 1024 && ro * B <= 512 && 2 * rg * B <= 2048 &&
+        2 * rg <= 256 && rd * BH <= 1024) {
+      G = cand;
+      break;
+    }
+  }
+  if (!G) return PBX_OK;
+  const long long stride = ((long long)m->qkv_rows + 3LL * g.dim + g.hidden_dim + 63) / 64 * 64;
+  int rc;
+  if (!m->small_layers) {
+    std::vector<SmallLayerHost> tab(nl);
+    for (int l = 0; l < nl; ++l) {
+      const Layer &L = m->layers[l];
+      tab[l] = SmallLayerHost{L.wqkv->qs, L.wo->qs, L.wgu->qs, L.wd->qs, L.wqkv->d, L.wo->d,
+                              L.wgu->d,   L.wd->d, L.attn_norm, L.ffn_norm};
+    }
+    const size_t cb = (size_t)nl * stride * 8;
+    if ((rc = dalloc(m, (void **)&m->small_layers, tab.size() * sizeof(SmallLayerHost))) ||
+        (rc = dalloc(m, (void **)&m->small_cells, cb)) ||
+        (rc = dalloc(m, (void **)&m->small_sync, 64)))
+      return rc;
+    // tag 0 (cleared cells) is never published; epoch 0, no workgroup done
+    if (hipMemcpy(m->small_layers, tab.data(), tab.size() * sizeof(SmallLayerHost),
+                  hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemsetAsync(m->small_cells, 0, cb, c->stream) != hipSuccess ||
+        hipMemsetAsync(m->small_sync, 0, 64, c->stream) != hipSuccess)
+      return pbx_fail(c, PBX_EHIP, "model: small-step set-up failed");
+  }
+  Op s;
+  s.kind = ARG_SMALL;
+  s.name = "pbx_small_step_q8";
+  s.f = f;
+  s.role = "layers";
+  s.grid = dim3(G);
+  s.block = dim3(512);
+  SmallArgsHost &a = s.small;
+  a.layers = m->small_layers;
+  a.at = AttnArgsHost{nullptr, m->kcache, m->vcache, m->rope, nullptr, m->state, g.n_heads,
+                      g.n_kv_heads, hd, (float)(1.0 / sqrt((double)hd)), g.max_seq};
+  a.at.status = m->state + 3;
+  a.at.spin = m->test_layer >= 0 ? m->test_spin : 0;
+  a.layer_kv = (long long)g.max_seq * kvdim;
+  a.cells = m->small_cells;
+  a.cell_stride = stride;
+  a.epoch = m->small_sync;
+  a.done = reinterpret_cast<unsigned *>(m->small_sync + 1);
+  a.x = m->x;
+  a.n_layers = nl;
+  a.dim = g.dim;
+  a.hidden = g.hidden_dim;
+  a.qkv_rows = m->qkv_rows;
+  a.eps = g.rms_eps;
+  a.rq = rq;
+  a.ro = ro;
+  a.rg = rg;
+  a.rd = rd;
+  a.test_layer = m->test_layer;
+  a.skew = m->test_skew;
+  // K and V of one cached position in every layer; every layer's weights,
+  // norms and its cells (written once, read by every workgroup)
+  s.bytes = 8.0 * kvdim * nl;
+  for (int l = 0; l < nl; ++l) {
+    const Layer &L = m->layers[l];
+    for (const pbx_weight *w : {L.wqkv, L.wo, L.wgu, L.wd})
+      s.fixed_bytes += (double)w->N * pbx_type_row_bytes(w->type, w->K);
+    s.fixed_bytes += 8.0 * g.dim;
+  }
+  const size_t head = m->layer_op[nl];
+  std::vector<Op> ops;
+  ops.push_back(s);
+  ops.insert(ops.end(), m->ops.begin() + head, m->ops.end());
+  m->ops.swap(ops);
+  for (int l = 0; l < nl; ++l) m->layer_op[l] = 0;
+  m->layer_op[nl] = 1;
+  m->small_step = true;
+  return PBX_OK;
 }
 
 static int build_ops(pbx_model *m) {
@@ -787,6 +936,7 @@ static int build_ops(pbx_model *m) {
   m->ffn_joined = fffn != nullptr;
   am.bytes += (double)pbx_type_row_bytes(m->embd->type, g.dim) + 4.0 * g.dim;
   m->ops.push_back(am);
+  if ((rc = plan_small_step(m))) return rc;
   m->ops_ready = true;
   return PBX_OK;
 }
@@ -801,6 +951,7 @@ static int enqueue_op(pbx_model *m, Op &op, hipEvent_t t0 = nullptr, hipEvent_t 
     case ARG_ATTN: arg = &op.attn; break;
     case ARG_ATTN_SPLIT: arg = &op.split; break;
     case ARG_EMBED: arg = &op.embed; break;
+    case ARG_SMALL: arg = &op.small; break;
     default: arg = &op.amax; break;
   }
   void *one[] = {arg};
@@ -845,6 +996,17 @@ static bool use_graphs() {
 // then the LM head and the argmax.
 static int enqueue_ops_layers(pbx_model *m, int L) {
   const size_t stop = m->layer_op[L], head = m->layer_op[m->cfg.n_layers];
+  if (m->small_step) {
+    // ops[0] runs the layers (the first L of them), then the head's ops
+    int rc = PBX_OK;
+    if (L > 0) {
+      Op s = m->ops[0];
+      s.small.n_layers = L;
+      rc = enqueue_op(m, s);
+    }
+    for (size_t i = 1; i < m->ops.size() && !rc; ++i) rc = enqueue_op(m, m->ops[i]);
+    return rc;
+  }
   for (size_t i = 0; i < m->ops.size(); ++i) {
     if (i >= stop && i < head) continue;
     int rc;
@@ -1054,7 +1216,8 @@ static void model_release(pbx_model *m) {
                   (void *)m->logits,
                   (void *)m->partials, (void *)m->state, (void *)m->hist,
                   (void *)m->attn_part, m->head_lanes, (void *)m->qa_cells, (void *)m->x2,
-                  (void *)m->ffn_cell, (void *)m->h_cells})
+                  (void *)m->ffn_cell, (void *)m->h_cells, (void *)m->small_layers,
+                  (void *)m->small_cells, (void *)m->small_sync})
     if (p) hipFree(p);
   for (void *p : {(void *)m->bx, (void *)m->bxn, (void *)m->bqkv, (void *)m->battn,
                   (void *)m->bgu, (void *)m->bh, (void *)m->btmp, (void *)m->blogits,
@@ -1176,6 +1339,7 @@ extern "C" int pbx_model_create(pbx_ctx *c, const pbx_model_config *cfg, pbx_mod
   if (const char *e = getenv("PBX_ATTN_O")) m->attn_o_ipt = atoi(e);
   if (const char *e = getenv("PBX_GRAPH_STEPS")) m->graph_steps = atoi(e);
   if (const char *e = getenv("PBX_FFN")) m->ffn_join = e[0] != '0';
+  if (const char *e = getenv("PBX_SMALL_STEP")) m->small_ok = e[0] != '0';
   if (!rc && m->attn_mode == ATTN_SPLIT) {
     m->attn_splits = std::min({64, g.max_seq, std::max(4, (256 + g.n_kv_heads - 1) / g.n_kv_heads)});
     rc = dalloc(m, (void **)&m->attn_part,
@@ -2165,7 +2329,8 @@ extern "C" int pbx_model_profile(pbx_model *m, int32_t token, int start_pos, int
       hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]);
       acc[i] += ms * 1e3;
       const Op &op = m->ops[i];
-      bytes[i] += (op.kind == ARG_ATTN || op.kind == ARG_ATTN_SPLIT || op.kind == ARG_FUSED)
+      bytes[i] += (op.kind == ARG_ATTN || op.kind == ARG_ATTN_SPLIT || op.kind == ARG_FUSED ||
+                   op.kind == ARG_SMALL)
                       ? op.bytes * (start_pos + s + 1)
                       : op.bytes;
       bytes[i] += op.fixed_bytes;
@@ -2213,7 +2378,7 @@ extern "C" int pbx_model_test_handoff(pbx_model *m, int layer, int skew, int spi
   int rc = check_complete(m);
   if (rc || (rc = build_ops(m))) return rc;
   for (const Op &op : m->ops)
-    if (op.kind == ARG_FUSED) return PBX_OK;
+    if (op.kind == ARG_FUSED || op.kind == ARG_SMALL) return PBX_OK;
   return layer < 0 ? PBX_OK
                    : pbx_fail(m->c, PBX_ENOTSUP,
                               "pbx_model_test_handoff: the step has no joined q|k|v + attention launch");

@@ -351,6 +351,76 @@ def test_handoff_wait_timeout_is_reported(ctx):
     model.free()
 
 
+def test_small_step_matches_per_layer_launches(ctx, monkeypatch):
+    """Small Q8_0 models run every layer of a decode step in one launch
+    (pbx_small_step_q8: the phases of a layer hand their outputs on through
+    tagged cells).  stories15M-shaped, after a 16-token prompt: the step's
+    kernels are that launch, the LM head and the argmax; 24 greedy steps give
+    the tokens of the per-layer launches (a model made with PBX_SMALL_STEP=0)
+    and the last step's logits agree within 5e-4 (the dot products are summed
+    in another order); a forward through the first 3 layers
+    (llama-streaming.js maxLayers) agrees as well."""
+    print("[case] stories15m small-step launch vs per-layer launches", flush=True)
+    cfg = synth.CONFIGS["stories15m"]
+    small = synth.build(ctx, cfg, 1300)
+    monkeypatch.setenv("PBX_SMALL_STEP", "0")
+    per = synth.build(ctx, cfg, 1300)
+    monkeypatch.delenv("PBX_SMALL_STEP")
+    prompt = [int(t) for t in synth.random_tokens(1301, 16, cfg["vocab_size"])]
+    _, n1 = small.forward(prompt, 0)
+    _, n2 = per.forward(prompt, 0)
+    assert n1 == n2
+    kern = [k for _, k, _, _ in small.profile(n1, 16, 1)]
+    assert kern[0] == "pbx_small_step_q8" and len(kern) == 3, kern
+    assert "pbx_small_step_q8" not in [k for _, k, _, _ in per.profile(n2, 16, 1)]
+    small.rollback(16)
+    per.rollback(16)
+    t1, l1 = small.generate(n1, 16, 24, want_logits=True)
+    t2, l2 = per.generate(n2, 16, 24, want_logits=True)
+    err = float(np.abs(np.asarray(l1) - np.asarray(l2)).max())
+    print(f"  24 steps: max-abs logit difference {err:.2e}")
+    assert list(t1) == list(t2) and err <= 5e-4
+    a, _ = small.forward([int(t1[-1])], 40, max_layers=3)
+    b, _ = per.forward([int(t2[-1])], 40, max_layers=3)
+    err3 = float(np.abs(a - b).max())
+    print(f"  3 of 6 layers: {err3:.2e}")
+    assert err3 <= 5e-4
+    small.free()
+    per.free()
+
+
+def test_small_step_wait_timeout_is_reported(ctx):
+    """The bounded waits of the small-model step: with the test hook skewing
+    the tag that layer 1's waits expect (64 polls each), every workgroup still
+    finishes and forward and generate fail with PBX_ETIMEOUT; a forward
+    through layer 0 alone succeeds, and without the hook the logits are those
+    of an untouched run, bit for bit."""
+    print("[case] small-step forced wait timeout", flush=True)
+    from purebee_amd.native import ETIMEOUT
+    cfg = tiny(TYPE_Q8_0, TYPE_Q8_0, n_layers=2)
+    model = synth.build(ctx, cfg, 131)
+    toks = [int(t) for t in synth.random_tokens(132, 6, cfg["vocab_size"])]
+    good = [model.forward([t], p)[0] for p, t in enumerate(toks)]
+    assert "pbx_small_step_q8" in {k for _, k, _, _ in model.profile(toks[-1], len(toks), 1)}
+    model.rollback(4)
+    model.test_handoff(1, 1, 64)
+    with pytest.raises(PbxError) as e:
+        model.forward([toks[4]], 4)
+    assert e.value.code == ETIMEOUT and "gave up" in str(e.value)
+    with pytest.raises(PbxError) as e:
+        model.generate(toks[4], 4, 3)
+    assert e.value.code == ETIMEOUT
+    model.rollback(4)
+    lg, _ = model.forward([toks[4]], 4, max_layers=1)
+    assert np.isfinite(lg).all()
+    model.test_handoff(-1, 0, 0)
+    model.rollback(4)
+    again = [model.forward([t], 4 + i)[0] for i, t in enumerate(toks[4:])]
+    assert np.array_equal(again[0], good[4]) and np.array_equal(again[1], good[5])
+    print("  timeouts reported; normal launch restored bit for bit")
+    model.free()
+
+
 @pytest.mark.parametrize("wt,et,dim,hidden,vocab", [(TYPE_Q4_0, TYPE_Q4_0, 2048, 1024, 40000),
                                                     (TYPE_Q4_0, TYPE_Q6_K, 2048, 1024, 40000),
                                                     (TYPE_Q8_0, TYPE_Q8_0, 2048, 1024, 512),
