@@ -216,6 +216,15 @@ MR_KX(4, 4, 4, 8, PRO_NONE, EPI_ADD, add)
 DK_MODES_WIDE(PBX_F32, f32, 2)
 DK_MODES_WIDE(PBX_F32, f32, 4)
 DK_MODES_SMALL(PBX_F32, f32, 2)
+// f32 LM heads with K = 32 BT <= 512: pbx_dk_f32_t<BT>_lmh (8 lanes a row)
+#define DK_TALL_F32(BT)                                                                     \
+  extern "C" __global__ void __launch_bounds__(256) pbx_dk_f32_t##BT##_lmh(GemvArgs a) {    \
+    gemv_tall_f32_lmh<BT, 2>(a);                                                           \
+  }
+DK_TALL_F32(8)
+DK_TALL_F32(9)
+DK_TALL_F32(12)
+DK_TALL_F32(16)
 
 // ---------------------------------------------------------------------------
 // Block reductions for 256-thread workgroups.

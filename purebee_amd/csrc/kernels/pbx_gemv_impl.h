@@ -805,6 +805,78 @@ __device__ __forceinline__ void gemv_small(const GemvArgs &a) {
 }
 
 // ---------------------------------------------------------------------------
+// RMSNorm + f32 LM head with K = 32 BT (BT <= 16 blocks, the stories15M
+// head: 32000 x 288 f32, llama.js:353-367) and argmax partials.  Eight
+// lanes a row: lane (r, q) of a wave takes float4 columns q + 8 i (i < BT)
+// of row r of each of P passes of 8 rows, so one load instruction of a wave
+// reads eight whole 128-byte row segments (gemv_small's lane-per-block
+// mapping touches 64 lines an instruction: 1.2 TB/s on this head).  The
+// lane's 4 BT activations, normalised, stay in registers for every row.
+// Workgroup: 4 waves x 8 P rows; one argmax key per wave.
+// ---------------------------------------------------------------------------
+template <int BT, int P>
+__device__ __forceinline__ void gemv_tall_f32_lmh(const GemvArgs &a) {
+  static_assert(BT >= 1 && BT <= 16, "K <= 512");
+  const int N = a.N, K = BT * 32, F = K / 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r8 = lane >> 3, q = lane & 7;
+  const float4 *X4 = reinterpret_cast<const float4 *>(a.X);
+  const float4 *W4 = reinterpret_cast<const float4 *>(a.normw);
+  const float4 *M4 = reinterpret_cast<const float4 *>(a.qs);
+  float4 xv[BT], wv[BT];
+#pragma unroll
+  for (int i = 0; i < BT; ++i) {
+    xv[i] = X4[q + 8 * i];
+    wv[i] = W4[q + 8 * i];
+  }
+  const int r0 = ((int)blockIdx.x * 4 + wave) * 8 * P;
+  float4 m[P][BT];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int row = r0 + 8 * p + r8;
+    const size_t base = (size_t)(row < N ? row : 0) * F + q;
+#pragma unroll
+    for (int i = 0; i < BT; ++i) {
+      const uint4 u = ld_stream(M4 + base + 8 * i);
+      m[p][i] = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                            __uint_as_float(u.w));
+    }
+  }
+  // RMSNorm: the lanes of row slot 0 hold every column once
+  float ss = 0.f;
+  if (r8 == 0) {
+#pragma unroll
+    for (int i = 0; i < BT; ++i)
+      ss = fmaf(xv[i].x, xv[i].x, fmaf(xv[i].y, xv[i].y, fmaf(xv[i].z, xv[i].z, fmaf(xv[i].w, xv[i].w, ss))));
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+#pragma unroll
+  for (int i = 0; i < BT; ++i)
+    xv[i] = make_float4(xv[i].x * inv * wv[i].x, xv[i].y * inv * wv[i].y, xv[i].z * inv * wv[i].z,
+                        xv[i].w * inv * wv[i].w);
+  uint64_t key = 0;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < BT; ++i) {
+      float &s = (i & 1) ? s1 : s0;
+      s = fmaf(xv[i].x, m[p][i].x, fmaf(xv[i].y, m[p][i].y, fmaf(xv[i].z, m[p][i].z, fmaf(xv[i].w, m[p][i].w, s))));
+    }
+    const float t = wave_sum<4>(s0 + s1);  // the row's 8 lanes
+    const int row = r0 + 8 * p + r8;
+    if (q == 0 && row < N) {
+      a.Y[row] = t;
+      const uint64_t k = argmax_key(t, (unsigned)row);
+      key = k > key ? k : key;
+    }
+  }
+  key = wave_max_u64(key);
+  if (lane == 0) a.partials[blockIdx.x * 4 + wave] = key;
+}
+
+// ---------------------------------------------------------------------------
 // Integer-limb GEMV for Q4_0 / Q8_0 (and Q6_K heads) with K >= 2048 (decode).
 // The workgroup first turns the activation row(s) into fixed point, one
 // power-of-two scale per 32-element block:

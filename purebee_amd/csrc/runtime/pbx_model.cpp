@@ -422,6 +422,15 @@ static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, const char *rol
     return;
   }
   const bool q4 = type == PBX_TYPE_Q4_0 || type == PBX_TYPE_Q4_1;
+  if (type == PBX_TYPE_F32 && strcmp(mode, "lmh") == 0 &&
+      (B == 8 || B == 9 || B == 12 || B == 16)) {
+    // f32 head with K <= 512 (stories15M): 8 lanes a row, 64 rows a workgroup
+    *shape = "t" + std::to_string(B);
+    *grid = dim3((N + 63) / 64);
+    *block = dim3(256);
+    *n_tiles = (int)grid->x * 4;
+    return;
+  }
   if (B <= 32) {
     const int P = q4 ? 8 : type == PBX_TYPE_F32 ? 2 : 4;
     const int T = P * (64 / B);
