@@ -225,6 +225,17 @@ DK_TALL_F32(8)
 DK_TALL_F32(9)
 DK_TALL_F32(12)
 DK_TALL_F32(16)
+// Q8_0 LM heads with K = 32 BT <= 768: pbx_dk_q8_t<BT>_lmh (8 lanes a row)
+#define DK_TALL_Q8(BT)                                                                      \
+  extern "C" __global__ void __launch_bounds__(256) pbx_dk_q8_t##BT##_lmh(GemvArgs a) {     \
+    gemv_tall_q8_lmh<BT, 2>(a);                                                            \
+  }
+DK_TALL_Q8(8)
+DK_TALL_Q8(9)
+DK_TALL_Q8(12)
+DK_TALL_Q8(16)
+DK_TALL_Q8(18)
+DK_TALL_Q8(24)
 
 // ---------------------------------------------------------------------------
 // Block reductions for 256-thread workgroups.

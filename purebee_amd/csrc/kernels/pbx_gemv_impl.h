@@ -877,6 +877,102 @@ __device__ __forceinline__ void gemv_tall_f32_lmh(const GemvArgs &a) {
 }
 
 // ---------------------------------------------------------------------------
+// RMSNorm + Q8_0 LM head with K = 32 BT (BT <= 24 blocks: SmolLM2-135M's
+// tied 49152 x 576 head) and argmax partials.  A row's codes are 2 BT
+// 16-byte chunks (half a block each); eight lanes a row, lane (r, q)
+// taking chunks q + 8 i, so a wave's load instruction reads eight 128-byte
+// row segments.  The normalised activations are built once per workgroup
+// in LDS; a lane keeps the 16 values of each of its chunks in registers and
+// their sum (the codes enter as unsigned bytes, code + 128, and 128 sum(x)
+// comes off).  Workgroup: 4 waves x 8 P rows; one argmax key per wave.
+// ---------------------------------------------------------------------------
+template <int BT, int P>
+__device__ __forceinline__ void gemv_tall_q8_lmh(const GemvArgs &a) {
+  static_assert(BT >= 1 && BT <= 24, "K <= 768");
+  constexpr int K = BT * 32, NCH = 2 * BT, NC = (NCH + 7) / 8;
+  __shared__ __attribute__((aligned(16))) float xs_l[K];
+  __shared__ float red[4];
+  const int N = a.N, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int r8 = lane >> 3, q = lane & 7;
+  const int r0 = ((int)blockIdx.x * 4 + wave) * 8 * P;
+  // codes and scales first (clamped: rows past N read row 0, chunks past
+  // the row read chunk q and get a zero scale)
+  uint4 m[P][NC];
+  unsigned dbits[P][NC];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int row = r0 + 8 * p + r8, rr = row < N ? row : 0;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = q + 8 * i, cc = c < NCH ? c : q;
+      dbits[p][i] = a.dsc[dsc_index(rr, cc >> 1, BT)] & (c < NCH ? 0xFFFFu : 0u);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int row = r0 + 8 * p + r8, rr = row < N ? row : 0;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = q + 8 * i, cc = c < NCH ? c : q;
+      m[p][i] = ld_stream(a.qs + ((size_t)rr * NCH + cc) * 16);
+    }
+  }
+  // RMSNorm of the activation row into LDS
+  float ss = 0.f;
+  for (int k = tid; k < K; k += 256) ss = fmaf(a.X[k], a.X[k], ss);
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + a.eps);
+  for (int k = tid; k < K; k += 256) xs_l[k] = a.X[k] * inv * a.normw[k];
+  __syncthreads();
+  float xr[NC][16], xsum[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = q + 8 * i, cc = c < NCH ? c : q;
+    xsum[i] = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float4 f = *reinterpret_cast<const float4 *>(&xs_l[16 * cc + 4 * v]);
+      xr[i][4 * v] = f.x;
+      xr[i][4 * v + 1] = f.y;
+      xr[i][4 * v + 2] = f.z;
+      xr[i][4 * v + 3] = f.w;
+      xsum[i] += (f.x + f.y) + (f.z + f.w);
+    }
+  }
+  uint64_t key = 0;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const unsigned w[4] = {m[p][i].x ^ 0x80808080u, m[p][i].y ^ 0x80808080u,
+                             m[p][i].z ^ 0x80808080u, m[p][i].w ^ 0x80808080u};
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s = fmaf(xr[i][4 * j + 0], (float)(w[j] & 0xFFu), s);
+        s = fmaf(xr[i][4 * j + 1], (float)((w[j] >> 8) & 0xFFu), s);
+        s = fmaf(xr[i][4 * j + 2], (float)((w[j] >> 16) & 0xFFu), s);
+        s = fmaf(xr[i][4 * j + 3], (float)(w[j] >> 24), s);
+      }
+      acc = fmaf(fmaf(-128.f, xsum[i], s), f16_bits_to_f32(dbits[p][i]), acc);
+    }
+    const float t = wave_sum<4>(acc);  // the row's 8 lanes
+    const int row = r0 + 8 * p + r8;
+    if (q == 0 && row < N) {
+      a.Y[row] = t;
+      const uint64_t k = argmax_key(t, (unsigned)row);
+      key = k > key ? k : key;
+    }
+  }
+  key = wave_max_u64(key);
+  if (lane == 0) a.partials[blockIdx.x * 4 + wave] = key;
+}
+
+// ---------------------------------------------------------------------------
 // Integer-limb GEMV for Q4_0 / Q8_0 (and Q6_K heads) with K >= 2048 (decode).
 // The workgroup first turns the activation row(s) into fixed point, one
 // power-of-two scale per 32-element block:

@@ -422,9 +422,11 @@ static void plan_gemv(pbx_ctx *c, bool int_ok, const char *mode, const char *rol
     return;
   }
   const bool q4 = type == PBX_TYPE_Q4_0 || type == PBX_TYPE_Q4_1;
-  if (type == PBX_TYPE_F32 && strcmp(mode, "lmh") == 0 &&
-      (B == 8 || B == 9 || B == 12 || B == 16)) {
-    // f32 head with K <= 512 (stories15M): 8 lanes a row, 64 rows a workgroup
+  if (strcmp(mode, "lmh") == 0 &&
+      ((type == PBX_TYPE_F32 && (B == 8 || B == 9 || B == 12 || B == 16)) ||
+       (type == PBX_TYPE_Q8_0 && (B == 8 || B == 9 || B == 12 || B == 16 || B == 18 || B == 24)))) {
+    // f32 / Q8_0 heads with small K (stories15M, SmolLM2-135M): 8 lanes a
+    // row, 64 rows a workgroup
     *shape = "t" + std::to_string(B);
     *grid = dim3((N + 63) / 64);
     *block = dim3(256);
