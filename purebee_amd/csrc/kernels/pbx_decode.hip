@@ -1211,7 +1211,7 @@ extern "C" __global__ void __launch_bounds__(1024) pbx_ffn_q4_d2048_h8192(GemvAr
 #define PBX_SM_SO 1
 #define PBX_SM_SG 4
 #define PBX_SM_SD 2
-#define PBX_SM_MAXR 256  // rows of one GEMV a workgroup
+#define PBX_SM_MAXR 256  // gate|up rows a workgroup (the host keeps them to this)
 // GEMV activations in LDS: 32-value block b at 36 b (4 floats of padding):
 // the 16-byte reads of 16 lanes at consecutive blocks then cover all 64
 // banks once (at 32 floats a block they would meet in 8 of them).
@@ -1306,13 +1306,12 @@ __device__ __forceinline__ void sm_publish(unsigned long long *cell, unsigned ta
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// n published cells (n <= P * 512) into dst (LDS; PAD: the padded GEMV
-// layout), polled until they carry tag; after `spin` polls the missing ones
-// are NaN and the status word is marked.  The values are written after a
-// barrier (dst may still be read before) and a barrier follows.
-template <int P, bool PAD>
+// The values of n published cells (n <= P * 512; thread t: cells t,
+// t + 512, ...), polled until they carry tag; after `spin` polls the missing
+// ones are NaN and the status word is marked.
+template <int P>
 __device__ __forceinline__ void sm_poll(const unsigned long long *cells, int n, unsigned tag,
-                                        int spin, int *status, float *dst) {
+                                        int spin, int *status, float (&val)[P]) {
   const int tid = threadIdx.x;
   unsigned long long v[P];
 #pragma unroll
@@ -1337,37 +1336,49 @@ __device__ __forceinline__ void sm_poll(const unsigned long long *cells, int n, 
   }
   if (missing())
     __hip_atomic_fetch_or(status, PBX_DEV_WAIT_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int k = 0; k < P; ++k)
+    val[k] = (unsigned)(v[k] >> 32) == tag ? __uint_as_float((unsigned)v[k]) : __builtin_nanf("");
+}
+
+// val (thread t: elements t, t + 512, ...) into dst in the padded GEMV
+// layout, between two barriers (dst may still be read before).
+template <int P>
+__device__ __forceinline__ void sm_store(const float (&val)[P], int n, float *dst) {
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < P; ++k) {
-    const int i = tid + PBX_SM_T * k;
-    if (i < n)
-      dst[PAD ? sm_pad(i) : i] =
-          (unsigned)(v[k] >> 32) == tag ? __uint_as_float((unsigned)v[k]) : __builtin_nanf("");
+    const int i = (int)threadIdx.x + PBX_SM_T * k;
+    if (i < n) dst[sm_pad(i)] = val[k];
   }
   __syncthreads();
 }
 
-// out = x * (1 / rms(x)) * w over n values in LDS (llama.js's RMSNorm; w
-// from memory, requested by the caller); out in the padded layout.
-__device__ __forceinline__ void sm_rmsnorm(const float *x, const float (&w)[2], float *out, int n,
-                                           float eps, float *red) {
+// A layer's residual row (val) into xin, x * w into act (padded) and
+// 1 / rms(x) returned: llama.js's RMSNorm with 1/rms applied to the finished
+// dot products (the dot is linear in x), so one pass and the barriers the
+// store needs anyway.
+__device__ __forceinline__ float sm_store_norm(const float (&val)[2], const float (&w)[2], int n,
+                                               float eps, float *xin, float *act, float *red) {
   const int tid = threadIdx.x;
+  __syncthreads();
   float ss = 0.f;
-  for (int i = tid; i < n; i += PBX_SM_T) ss = fmaf(x[i], x[i], ss);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = tid + PBX_SM_T * k;
+    if (i < n) {
+      xin[i] = val[k];
+      act[sm_pad(i)] = val[k] * w[k];
+      ss = fmaf(val[k], val[k], ss);
+    }
+  }
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   float tot = 0.f;
 #pragma unroll
   for (int w8 = 0; w8 < PBX_HA_WAVES; ++w8) tot += red[w8];
-  const float inv = 1.0f / sqrtf(tot / (float)n + eps);
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int i = tid + PBX_SM_T * k;
-    if (i < n) out[sm_pad(i)] = x[i] * inv * w[k];
-  }
-  __syncthreads();
+  return 1.0f / sqrtf(tot / (float)n + eps);
 }
 
 extern "C" __global__ void __launch_bounds__(PBX_SM_T) pbx_small_step_q8(SmallArgs a) {
@@ -1375,7 +1386,6 @@ extern "C" __global__ void __launch_bounds__(PBX_SM_T) pbx_small_step_q8(SmallAr
   // a GEMV's activations (padded layout)
   __shared__ __attribute__((aligned(16))) float act[PBX_SM_MAXH / 32 * PBX_SM_BLK];
   __shared__ float part[PBX_SM_T * PBX_SM_SG];                      // partial dots
-  __shared__ float rowv[PBX_SM_MAXR];                               // gate|up row sums
   __shared__ float red[PBX_HA_WAVES];
   const int j = blockIdx.x, tid = threadIdx.x;
   const int dim = a.dim, hidden = a.hidden, qr = a.qkv_rows;
@@ -1407,20 +1417,19 @@ extern "C" __global__ void __launch_bounds__(PBX_SM_T) pbx_small_step_q8(SmallAr
     float nw[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) nw[k] = L.attn_norm[min(tid + PBX_SM_T * k, dim - 1)];
+    float xv[2];
     if (l == 0) {
-      __syncthreads();
-      for (int i = tid; i < dim; i += PBX_SM_T) xin[i] = a.x[i];
-      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 2; ++k) xv[k] = a.x[min(tid + PBX_SM_T * k, dim - 1)];
     } else {
       // the next-x cells of layer l - 1 (its cn)
-      const unsigned long long *prev = cq - a.cell_stride + qr + 2 * dim + hidden;
-      sm_poll<2, false>(prev, dim, want, spin, status, xin);
+      sm_poll(cq - a.cell_stride + qr + 2 * dim + hidden, dim, want, spin, status, xv);
     }
-    sm_rmsnorm(xin, nw, act, dim, a.eps, red);
+    float inv = sm_store_norm(xv, nw, dim, a.eps, xin, act, red);
     sm_dots(sq, B, nq * B, act, part);
     for (int i = tid >> 3; i < ((nq + 7) & ~7); i += PBX_SM_T / 8) {
       // rows 2i', 2i' + 1 sit in adjacent 8-thread groups of one wave
-      const float v = i < nq ? sm_row(part, i, B) : 0.f;
+      const float v = (i < nq ? sm_row(part, i, B) : 0.f) * inv;
       const float pv = __shfl_xor(v, 8, 64);
       if (i < nq && (tid & 7) == 0) {
         const int n = q0 + i;
@@ -1454,11 +1463,13 @@ extern "C" __global__ void __launch_bounds__(PBX_SM_T) pbx_small_step_q8(SmallAr
     for (int i = 0; i < PBX_SM_SO; ++i)
       so[i] = sm_load(L.o_qs, L.o_d, B, no * B, tid + PBX_SM_T * i,
                       [&](int r) { return min(o0 + r, dim - 1); });
+    // gate|up rows interleaved: local row 2c is gate column c0 + c, 2c + 1 its up row
     SmSlot sg[PBX_SM_SG];
 #pragma unroll
     for (int i = 0; i < PBX_SM_SG; ++i)
-      sg[i] = sm_load(L.gu_qs, L.gu_d, B, 2 * ng * B, tid + PBX_SM_T * i,
-                      [&](int r) { return min(r < ng ? c0 + r : hidden + c0 + r - ng, 2 * hidden - 1); });
+      sg[i] = sm_load(L.gu_qs, L.gu_d, B, 2 * ng * B, tid + PBX_SM_T * i, [&](int r) {
+        return min((r & 1) ? hidden + c0 + (r >> 1) : c0 + (r >> 1), 2 * hidden - 1);
+      });
     SmSlot sd[PBX_SM_SD];
 #pragma unroll
     for (int i = 0; i < PBX_SM_SD; ++i)
@@ -1466,24 +1477,27 @@ extern "C" __global__ void __launch_bounds__(PBX_SM_T) pbx_small_step_q8(SmallAr
                       [&](int r) { return min(d0 + r, dim - 1); });
 #pragma unroll
     for (int k = 0; k < 2; ++k) nw[k] = L.ffn_norm[min(tid + PBX_SM_T * k, dim - 1)];
-    sm_poll<2, true>(co, dim, want, spin, status, act);
+    sm_poll(co, dim, want, spin, status, xv);
+    sm_store(xv, dim, act);
     sm_dots(so, B, no * B, act, part);
     for (int i = tid >> 3; i < no; i += PBX_SM_T / 8) {
       const float v = sm_row(part, i, B);
       if ((tid & 7) == 0) sm_publish(cx1 + o0 + i, tag, xin[o0 + i] + v);
     }
-    // 4. RMSNorm + gate|up + SwiGLU
-    sm_poll<2, false>(cx1, dim, want, spin, status, xin);
-    sm_rmsnorm(xin, nw, act, dim, a.eps, red);
+    // 4. RMSNorm + gate|up + SwiGLU (gate and up rows in adjacent 8-thread groups)
+    sm_poll(cx1, dim, want, spin, status, xv);
+    inv = sm_store_norm(xv, nw, dim, a.eps, xin, act, red);
     sm_dots(sg, B, 2 * ng * B, act, part);
-    for (int i = tid >> 3; i < 2 * ng; i += PBX_SM_T / 8) {
-      const float v = sm_row(part, i, B);
-      if ((tid & 7) == 0) rowv[i] = v;
+    for (int i = tid >> 3; i < ((2 * ng + 7) & ~7); i += PBX_SM_T / 8) {
+      const float v = (i < 2 * ng ? sm_row(part, i, B) : 0.f) * inv;
+      const float up = __shfl_xor(v, 8, 64);
+      if (i < 2 * ng && (i & 1) == 0 && (tid & 7) == 0)
+        sm_publish(ch + c0 + (i >> 1), tag, silu(v) * up);
     }
-    __syncthreads();
-    for (int i = tid; i < ng; i += PBX_SM_T) sm_publish(ch + c0 + i, tag, silu(rowv[i]) * rowv[ng + i]);
     // 5. down + residual
-    sm_poll<PBX_SM_MAXH / PBX_SM_T, true>(ch, hidden, want, spin, status, act);
+    float hv[PBX_SM_MAXH / PBX_SM_T];
+    sm_poll(ch, hidden, want, spin, status, hv);
+    sm_store(hv, hidden, act);
     sm_dots(sd, BH, nd * BH, act, part);
     for (int i = tid >> 3; i < nd; i += PBX_SM_T / 8) {
       const float v = sm_row(part, i, BH);
