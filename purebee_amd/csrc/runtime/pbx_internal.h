@@ -115,6 +115,11 @@ struct pbx_ctx {
   size_t d_stage_cap[2] = {0, 0};
   void *h_io = nullptr;
   size_t h_io_cap = 0;
+  // pbx_linear with M < 4: x is read from coherent pinned memory by a copy
+  // kernel (h_x, device address d_hx) and the GEMV stores y straight into
+  // h_y (device address d_hy): no copy operation
+  void *h_x = nullptr, *d_hx = nullptr, *h_y = nullptr, *d_hy = nullptr;
+  size_t h_x_cap = 0, h_y_cap = 0;
   void *h_stage[2] = {nullptr, nullptr};
   size_t h_stage_cap[2] = {0, 0};
   void *models = nullptr;  // decode-step models owned by this context

@@ -157,7 +157,7 @@ extern "C" void pbx_shutdown(pbx_ctx *c) {
   pbx_model_release_all(c);
   for (void *p : {c->d_x, c->d_y, c->d_b, c->d_gemm, c->d_stage[0], c->d_stage[1]})
     if (p) hipFree(p);
-  for (void *p : {c->h_io, c->h_stage[0], c->h_stage[1]})
+  for (void *p : {c->h_io, c->h_x, c->h_y, c->h_stage[0], c->h_stage[1]})
     if (p) hipHostFree(p);
   hipEventDestroy(c->ev0);
   hipEventDestroy(c->ev1);
@@ -661,6 +661,26 @@ extern "C" int pbx_workspace_info(const pbx_ctx *c, size_t *grown_bytes, size_t 
 
 extern "C" void *pbx_ctx_stream(const pbx_ctx *c) { return c ? (void *)c->stream : nullptr; }
 
+// Coherent pinned memory of at least `need` bytes with a device address.
+static int ensure_mapped(pbx_ctx *c, void **h, void **d, size_t *cap, size_t need) {
+  if (*cap >= need) return PBX_OK;
+  if (*h) {
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    hipHostFree(*h);
+    *h = *d = nullptr;
+    *cap = 0;
+  }
+  const size_t sz = std::max<size_t>(need, 1 << 16);
+  if (hipHostMalloc(h, sz, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+      hipHostGetDevicePointer(d, *h, 0) != hipSuccess) {
+    if (*h) hipHostFree(*h);
+    *h = *d = nullptr;
+    return pbx_fail(c, PBX_ENOMEM, "hipHostMalloc(%zu, mapped) failed", sz);
+  }
+  *cap = sz;
+  return PBX_OK;
+}
+
 extern "C" int pbx_linear(pbx_ctx *c, const pbx_weight *w, const float *X, int64_t M,
                           const float *bias, float *Y) {
   int rc = check_linear_args(c, w, X, M, Y, "pbx_linear");
@@ -668,9 +688,37 @@ extern "C" int pbx_linear(pbx_ctx *c, const pbx_weight *w, const float *X, int64
   HIPCHK(c, hipSetDevice(c->device));
   const size_t xb = (size_t)M * w->K * 4, yb = (size_t)M * w->N * 4;
   const size_t bb = bias ? (size_t)w->N * 4 : 0;
-  if ((rc = pbx_ensure_dev(c, &c->d_x, &c->d_x_cap, xb))) return rc;
-  if ((rc = pbx_ensure_dev(c, &c->d_y, &c->d_y_cap, yb))) return rc;
+  // M < 4 (the GEMVs): x and the bias are read from coherent pinned memory
+  // by a copy kernel and y goes straight into coherent pinned memory, so a
+  // call is two launches and a synchronisation, no copy operation (the
+  // synchronous per-matmul seam of llama-streaming.js pays each operation's
+  // latency on every call: 24.3 us a call with the three copies)
+  const bool direct = M < PBX_GEMM_MIN_M && w->type != PBX_TYPE_Q8_REF;
+  // the bias follows x (whole 128-byte blocks) in 16-byte units
+  const size_t bpad = (bb + 15) / 16 * 16;
+  if ((rc = pbx_ensure_dev(c, &c->d_x, &c->d_x_cap, xb + bpad))) return rc;
   if (bias && (rc = pbx_ensure_dev(c, &c->d_b, &c->d_b_cap, bb))) return rc;
+  if (direct) {
+    if ((rc = ensure_mapped(c, &c->h_x, &c->d_hx, &c->h_x_cap, xb + bpad)) ||
+        (rc = ensure_mapped(c, &c->h_y, &c->d_hy, &c->h_y_cap, yb)))
+      return rc;
+    memcpy(c->h_x, X, xb);
+    if (bias) memcpy((char *)c->h_x + xb, bias, bb);
+    const void *src = c->d_hx;
+    void *dst = c->d_x;
+    const int64_t n16 = (int64_t)(xb + bpad) / 16;
+    void *args[] = {(void *)&src, &dst, (void *)&n16};
+    if ((rc = pbx_launch(c, PBX_K_COPY16, dim3((unsigned)((n16 + 255) / 256)), dim3(256), args)))
+      return rc;
+    if ((rc = pbx_linear_enqueue(c, w, (const float *)c->d_x, M,
+                                 bias ? (const float *)((char *)c->d_x + xb) : nullptr,
+                                 (float *)c->d_hy, c->stream)))
+      return rc;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    memcpy(Y, c->h_y, yb);
+    return PBX_OK;
+  }
+  if ((rc = pbx_ensure_dev(c, &c->d_y, &c->d_y_cap, yb))) return rc;
   if ((rc = pbx_ensure_pinned(c, &c->h_io, &c->h_io_cap, std::max(xb + bb, yb)))) return rc;
   memcpy(c->h_io, X, xb);
   if (bias) memcpy((char *)c->h_io + xb, bias, bb);
