@@ -884,19 +884,13 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
 
   // merge in two levels: the wave's 4 rows (same dims, 16 lanes apart) in
   // registers, then the 8 wave states through LDS in one wave
-  float mw = fmaxf(m, __shfl_xor(m, 16, 64));
-  mw = fmaxf(mw, __shfl_xor(mw, 32, 64));  // finite for wave 0 (position 0)
+  const float mw = pair_max<32>(pair_max<16>(m));  // finite for wave 0 (position 0)
   const float er = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mw);
-  float lw = l * er;
-  float4 aw = make_float4(acc.x * er, acc.y * er, acc.z * er, acc.w * er);
-#pragma unroll
-  for (int off = 16; off <= 32; off *= 2) {
-    lw += __shfl_xor(lw, off, 64);
-    aw.x += __shfl_xor(aw.x, off, 64);
-    aw.y += __shfl_xor(aw.y, off, 64);
-    aw.z += __shfl_xor(aw.z, off, 64);
-    aw.w += __shfl_xor(aw.w, off, 64);
-  }
+  const float lw = pair_sum<32>(pair_sum<16>(l * er));
+  const float4 aw = make_float4(pair_sum<32>(pair_sum<16>(acc.x * er)),
+                                pair_sum<32>(pair_sum<16>(acc.y * er)),
+                                pair_sum<32>(pair_sum<16>(acc.z * er)),
+                                pair_sum<32>(pair_sum<16>(acc.w * er)));
   if (lane == 0) {
     st_m[w] = mw;
     st_l[w] = lw;
@@ -909,11 +903,12 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
     const float M = wave_max<4>(mi);  // lanes 0..7 hold the states
     const float e = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - M);
     const float den = wave_sum<4>(e * li);
+    // readlane moves 32-bit integers: the floats travel as their bits
     float num = 0.f;
 #pragma unroll
     for (int i = 0; i < PBX_HA_WAVES; ++i)
-      num = fmaf(__shfl(e, i, 64), st_acc[i][lane], num);
-    const float dn = __shfl(den, 0, 64);
+      num = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), i)), st_acc[i][lane], num);
+    const float dn = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(den), 0));
     if constexpr (IPT == 0) {
       if (lane < hd) {
         const float o = num / dn;
@@ -952,7 +947,7 @@ __device__ __forceinline__ void attention_cached_body(const AttnArgs &a, const i
         }
       }
       float p = fmaf(-8.f, o_sum[hb], t) * f16_bits_to_f32(wd[i]);
-      p += __shfl_xor(p, 1, 64);  // the row's other block: the adjacent lane
+      p += lane_partner<1>(p);  // the row's other block: the adjacent lane
       if (hb == 0) {
         if (fabsf(p) < 0x1p26f)
           atomicAdd(reinterpret_cast<unsigned long long *>(a.oacc) + row,
@@ -1156,9 +1151,7 @@ extern "C" __global__ void __launch_bounds__(1024) pbx_ffn_q4_d2048_h8192(GemvAr
                           fmaf((float)s1, 256.f * c0, fmaf((float)s0, c0, -8.f * (float)hsum[b] * c0)));
     acc = fmaf(fb, f16_bits_to_f32(wd[i]), acc);
   }
-  acc += __shfl_xor(acc, 1, 64);
-  acc += __shfl_xor(acc, 2, 64);
-  acc += __shfl_xor(acc, 4, 64);
+  acc = group_sum<8>(acc);
   if (g8 != 0) return;
   const bool bad = !(fabsf(acc) < 0x1p19f);
   const unsigned long long c =
@@ -1430,7 +1423,7 @@ extern "C" __global__ void __launch_bounds__(PBX_SM_T) pbx_small_step_q8(SmallAr
     for (int i = tid >> 3; i < ((nq + 7) & ~7); i += PBX_SM_T / 8) {
       // rows 2i', 2i' + 1 sit in adjacent 8-thread groups of one wave
       const float v = (i < nq ? sm_row(part, i, B) : 0.f) * inv;
-      const float pv = __shfl_xor(v, 8, 64);
+      const float pv = lane_partner<8>(v);
       if (i < nq && (tid & 7) == 0) {
         const int n = q0 + i;
         float o = v;
@@ -1490,7 +1483,7 @@ extern "C" __global__ void __launch_bounds__(PBX_SM_T) pbx_small_step_q8(SmallAr
     sm_dots(sg, B, 2 * ng * B, act, part);
     for (int i = tid >> 3; i < ((2 * ng + 7) & ~7); i += PBX_SM_T / 8) {
       const float v = (i < 2 * ng ? sm_row(part, i, B) : 0.f) * inv;
-      const float up = __shfl_xor(v, 8, 64);
+      const float up = lane_partner<8>(v);
       if (i < 2 * ng && (i & 1) == 0 && (tid & 7) == 0)
         sm_publish(ch + c0 + (i >> 1), tag, silu(v) * up);
     }

@@ -350,30 +350,77 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Distances 16 and 32 by gfx950's lane swaps (VALU, no LDS round trip):
+// v_permlane32_swap of (v, v) leaves the lower half of v in both halves of
+// the first result and the upper half in both halves of the second;
+// v_permlane16_swap does the same for the even and odd 16-lane rows.  So
+// the first result holds v on lanes with bit OFF clear and the partner's
+// value on the others, the second the reverse.
+template <int OFF>
+__device__ __forceinline__ void lane_swap(float v, float &lo, float &hi) {
+  static_assert(OFF == 16 || OFF == 32, "row or half swap");
+  const unsigned b = __float_as_uint(v);
+  if constexpr (OFF == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+  }
+}
+
 // The value the butterfly partner at distance OFF holds.  Distances inside
 // a 16-lane row use DPP (a VALU operand modifier: no LDS round trip), with a
 // partner that differs in bit OFF and agrees in the bits above it:
 //   8 -> row_ror:8 (lane ^ 8), 4 -> row_half_mirror (lane ^ 7),
 //   2 -> quad_perm 3,2,1,0 (lane ^ 3), 1 -> quad_perm 1,0,3,2 (lane ^ 1).
-// 16 and 32 go through ds_bpermute.  The masks 32, 16, 8, 7, 3, 1 are
-// independent, so a butterfly over them sums all 64 lanes, and each stage's
-// partner agrees on the bits earlier stages split on, which the transposed
-// reductions rely on.  All 64 lanes must be active.
+// 16 and 32 use the lane swaps above (lane ^ 16, lane ^ 32).  The masks 32,
+// 16, 8, 7, 3, 1 are independent, so a butterfly over them sums all 64
+// lanes, and each stage's partner agrees on the bits earlier stages split
+// on, which the transposed reductions rely on.  All 64 lanes must be active.
 template <int OFF>
 __device__ __forceinline__ float lane_partner(float v) {
   if constexpr (OFF >= 16) {
-    return __shfl_xor(v, OFF, 64);
+    float lo, hi;
+    lane_swap<OFF>(v, lo, hi);
+    return (__lane_id() & OFF) ? lo : hi;
   } else {
     constexpr int ctrl = OFF == 8 ? 0x128 : OFF == 4 ? 0x141 : OFF == 2 ? 0x1B : 0xB1;
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false));
   }
 }
 
+// v + partner and max(v, partner) at distance OFF.  For 16 and 32 the two
+// swap results are v and the partner in some order on every lane: the sum
+// and the maximum are the same either way.
+template <int OFF>
+__device__ __forceinline__ float pair_sum(float v) {
+  if constexpr (OFF >= 16) {
+    float lo, hi;
+    lane_swap<OFF>(v, lo, hi);
+    return lo + hi;
+  } else {
+    return v + lane_partner<OFF>(v);
+  }
+}
+
+template <int OFF>
+__device__ __forceinline__ float pair_max(float v) {
+  if constexpr (OFF >= 16) {
+    float lo, hi;
+    lane_swap<OFF>(v, lo, hi);
+    return fmaxf(lo, hi);
+  } else {
+    return fmaxf(v, lane_partner<OFF>(v));
+  }
+}
+
 template <int OFF = 32>
 __device__ __forceinline__ float wave_sum(float v) {
   if constexpr (OFF >= 1) {
-    v += lane_partner<OFF>(v);
-    return wave_sum<OFF / 2>(v);
+    return wave_sum<OFF / 2>(pair_sum<OFF>(v));
   } else {
     return v;
   }
@@ -382,20 +429,29 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <int OFF = 32>
 __device__ __forceinline__ float wave_max(float v) {
   if constexpr (OFF >= 1) {
-    v = fmaxf(v, lane_partner<OFF>(v));
-    return wave_max<OFF / 2>(v);
+    return wave_max<OFF / 2>(pair_max<OFF>(v));
   } else {
     return v;
   }
 }
 
+// The partner's 64-bit value: both halves moved as bits (the lane moves
+// apply no arithmetic).
+template <int OFF>
+__device__ __forceinline__ uint64_t lane_partner_u64(uint64_t v) {
+  const unsigned lo = __float_as_uint(lane_partner<OFF>(__uint_as_float((unsigned)v)));
+  const unsigned hi = __float_as_uint(lane_partner<OFF>(__uint_as_float((unsigned)(v >> 32))));
+  return (uint64_t)hi << 32 | lo;
+}
+
+template <int OFF = 32>
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint64_t o = __shfl_xor(v, off, 64);
-    v = o > v ? o : v;
+  if constexpr (OFF >= 1) {
+    const uint64_t o = lane_partner_u64<OFF>(v);
+    return wave_max_u64<OFF / 2>(o > v ? o : v);
+  } else {
+    return v;
   }
-  return v;
 }
 
 // Order-preserving key for argmax: larger value -> larger key; equal values
@@ -622,7 +678,7 @@ __device__ __forceinline__ void gemv_wide(const GemvArgs &a) {
   if constexpr (PAIR) {
     // gate row i sits in lane i*lpr, its up row in lane i*lpr + 32
     if (nwaves == 1) {
-      const float up = __shfl_xor(tot, 32, 64);
+      const float up = lane_partner<32>(tot);
       if (lane < 32 && (lane % lanes_per_row) == 0) {
         const int n = r0 + row;
         if (n < NO) y[n] = silu(tot) * up;
@@ -1593,7 +1649,11 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   const int r0 = rbase(blockIdx.x);
   if constexpr (EPI == EPI_ROPE) {
     // rows 2i, 2i+1 sit LPR lanes apart after the transposed reduction
-    const float pt = __shfl_xor(tot[0], LPR, 64);
+    float pt;
+    if constexpr (LPR == 8 || LPR >= 16)
+      pt = lane_partner<LPR>(tot[0]);  // exact lane ^ LPR
+    else
+      pt = __shfl_xor(tot[0], LPR, 64);
     if ((lane % LPR) == 0) {
       const int n = r0 + row;
       const float t = tot[0];
@@ -1617,7 +1677,7 @@ __device__ __forceinline__ void gemv_int(const GemvArgs &a) {
   if constexpr (PAIR) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-      const float up = __shfl_xor(tot[m], 32, 64);
+      const float up = lane_partner<32>(tot[m]);
       if (m < rows && lane < 32 && (lane % LPR) == 0) {
         const int n = r0 + row;
         if (n < NO) {
@@ -2042,7 +2102,7 @@ __device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
     // tile rows 0..7 (lane groups 0, 1) are gate rows, 8..15 their up rows
     float up[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(acc[i], 32, 64);
+    for (int i = 0; i < 4; ++i) up[i] = lane_partner<32>(acc[i]);
     if (lcol == 0 && mcol < rows && g < 2) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {

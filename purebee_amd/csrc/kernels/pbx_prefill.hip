@@ -494,7 +494,7 @@ __device__ __forceinline__ void attention_mfma_body(const float *qkv, const floa
       if (kpos > qpos || kpos > last_key) s[r] = -INFINITY;
       mt = fmaxf(mt, s[r]);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    mt = pair_max<32>(mt);
     const float mn = fmaxf(m_run, mt);
     const float f = mn == -INFINITY ? 1.f : expf(m_run - mn);
     float ps = 0.f;
@@ -505,7 +505,7 @@ __device__ __forceinline__ void attention_mfma_body(const float *qkv, const floa
       ps += pr;
       SPLIT_F16(pr, Ph[r >> 3][r & 7], Pl[r >> 3][r & 7]);
     }
-    ps += __shfl_xor(ps, 32, 64);
+    ps = pair_sum<32>(ps);
     l_run = fmaf(l_run, f, ps);
     m_run = mn;
     // O^T += V^T . P^T over the 32 keys (two chunks of 16)
