@@ -2041,9 +2041,15 @@ __device__ __forceinline__ void gemv_mr(const GemvArgs &a) {
         acc[3] = fmaf(fmaf((float)d[u][3], c, -kk), f16_bits_to_f32(dw[u].y >> 16), acc[3]);
       }
     }
-    // limbs 0..2 of a row sit in columns 3m..3m+2 (adjacent lanes)
+    // limbs 0..2 of a row sit in columns 3m..3m+2 (adjacent lanes): DPP
+    // row_shl:1 and :2 read lanes +1 and +2 of the 16-lane row (column 3m
+    // <= 12 finds both inside it; the other lanes' sums are not used)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] += __shfl_down(acc[i], 1, 16) + __shfl_down(acc[i], 2, 16);
+    for (int i = 0; i < 4; ++i) {
+      const int v = __float_as_int(acc[i]);
+      acc[i] += __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x101, 0xF, 0xF, false)) +
+                __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x102, 0xF, 0xF, false));
+    }
   };
 
   float acc[4];
