@@ -51,7 +51,7 @@ def q4_bytes(N, K):
 
 def host_threads():
     """Threads for the CPU baseline: the CPUs this process may run on, at most
-    16 (a one-GPU box's share of its host)."""
+    16 (one GPU's share of the host CPUs of an 8-GPU node)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
