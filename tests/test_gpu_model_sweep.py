@@ -11,6 +11,7 @@ import pytest
 
 from purebee_amd import synth
 from purebee_amd.native import TYPE_F16, TYPE_F32, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q6_K, TYPE_Q8_0
+from tests.e2e_util import LOGIT_TOL, make_pair
 from tests.test_gpu_decode import run_prompt_then_greedy
 
 pytestmark = pytest.mark.gpu
@@ -54,3 +55,31 @@ def test_random_model_prefill_and_greedy(ctx, case):
     print(f"  exact={exact} ties={ties} prefill_err={e1:.1e} final_err={e2:.1e}", flush=True)
     assert exact + ties == n_gen
     assert exact >= n_gen - 2
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_random_model_batched_rows(ctx, case):
+    """The batched forward of 2-8 rows after a prompt (the speculative verify's
+    forward_batch: rows at positions P .. P + n - 1 attending to the cache and to
+    each other) against the oracle consuming the same tokens one at a time
+    (speculative.js:129-185 runs the target over the draft the same way)."""
+    cfg, n_prompt, n_gen = draw(100 + case)
+    rng = np.random.default_rng(5000 + case)
+    n = int(rng.integers(2, 9))
+    cfg["max_seq"] = n_prompt + n + 8
+    print(f"[case] batched rows {case}: {cfg} prompt {n_prompt} rows {n}", flush=True)
+    model, ref, cfg = make_pair(ctx, cfg, 4000 + case)
+    prompt = synth.random_tokens(4100 + case, n_prompt, cfg["vocab_size"])
+    ref.forward(prompt, 0)
+    model.forward(prompt, 0, want_logits=False)
+    rows = synth.random_tokens(4200 + case, n, cfg["vocab_size"])
+    logits, nxt = model.forward_batch(rows, n_prompt)
+    worst = 0.0
+    for i in range(n):
+        ref_l = ref.forward([int(rows[i])], n_prompt + i)
+        worst = max(worst, float(np.abs(logits[i] - ref_l).max()))
+        assert int(nxt[i]) == int(np.argmax(logits[i]))
+    print(f"  rows={n} worst logit max-abs {worst:.2e}", flush=True)
+    assert worst <= LOGIT_TOL
+    model.free()
+    ref.close()
