@@ -281,13 +281,14 @@ GEMM_KERNEL(pbx_gemm_f16_m2_n2, PBX_F16, 2, 2)
 // 8h..8h+7 (a lane reads its 8 code bytes once), the Q8_0 bytes 8h.. and
 // 16+8h.., the F16 halves likewise.  Each lane's 16 outputs share one column
 // (weight row), so the block scale is one value per lane.
-// Workgroup tile 128 (M) x 128 (N), four waves in 2 x 2, wave tile 64 x 64
-// (2 x 2 MFMA tiles).  A ring of NS LDS stages, each [hi/lo][128 rows][4
-// chunks of 8 halves] of activations, the 128 weight rows' code bytes (or
-// F16 weights) and their scales (and Q4_1 mins).  Per block every wave
-// issues the same number of DMA instructions (global_load_lds: lane i's bytes
-// land at the instruction's LDS base + size * i): four activation chunks and
-// its share of the weight data (DmaW), so one wait count fits every wave;
+// Workgroup tile MT (M, 128 or 64) x 128 (N), four waves in 2 x 2, wave tile
+// MT / 2 x 64 (MT / 64 x 2 MFMA tiles).  A ring of NS LDS stages, each
+// [hi/lo][MT rows][4 chunks of 8 halves] of activations, the 128 weight rows'
+// code bytes (or F16 weights) and their scales (and Q4_1 mins).  Per block
+// every wave issues the same number of DMA instructions (global_load_lds:
+// lane i's bytes land at the instruction's LDS base + size * i): MT / 32
+// activation chunks and its share of the weight data (DmaW), so one wait
+// count fits every wave;
 // the loads are issued from inline assembly with SGPR bases, so
 // the compiler adds no waits of its own, and no register load is in flight
 // across the block loop.  The chunks of activation row r are stored in the
@@ -331,40 +332,44 @@ template <int TYPE> struct DmaW {
   static constexpr int WD = TYPE == PBX_Q8 || TYPE == PBX_F16 ? 2 : 1;      // weight DMAs a wave
 };
 
-template <int TYPE, int NS>
+template <int TYPE, int NS, int MT = 128>
 __device__ __forceinline__ void gemm_dma(const GemmArgs &a) {
+  static_assert(MT == 128 || MT == 64, "M tile");
   typedef DmaW<TYPE> W;
-  constexpr int ASTAGE = 2 * 128 * 32 * 2;                        // bytes
+  constexpr int NA = MT / 64;                                     // activation chunks a wave and plane
+  constexpr int TT = MT / 64;                                     // 32-row MFMA tiles a wave
+  constexpr int PS = MT * 32 * 2;                                 // bytes of a stage's hi (or lo) plane
+  constexpr int ASTAGE = 2 * PS;                                  // bytes
   constexpr int STAGE = ASTAGE + W::CODES + 256 * W::NSC;         // bytes
-  constexpr int PER = 4 + W::WD;                                  // DMA instructions a wave and block
+  constexpr int PER = 2 * NA + W::WD;                             // DMA instructions a wave and block
   __shared__ __attribute__((aligned(1024))) uint8_t S[NS * STAGE];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR bases
   const int lr = lane & 31, h = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
   const int n0 = blockIdx.x * 128 + wn * 64;
-  const int mblk = blockIdx.y * 128;
-  const int m0 = wm * 64;
+  const int mblk = blockIdx.y * MT;
+  const int m0 = wm * (MT / 2);
   const int K = a.B * 32;
   const int per = (a.B + a.KS - 1) / a.KS;
   const int b0 = blockIdx.z * per;
   const int b1 = min(a.B, b0 + per);
   const floatx16 zero16 = {};
 
-  floatx16 acc[2][2];
+  floatx16 acc[TT][2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < TT; ++t)
 #pragma unroll
     for (int u = 0; u < 2; ++u) acc[t][u] = zero16;
 
   if (b0 < b1) {
-    // activation DMA i (i = 0..3) of this wave: plane i >> 1, LDS chunks
+    // activation DMA i (i < NA) of this wave and plane: LDS chunks
     // (4 i + wave) * 64 + lane; per-lane byte offset from the plane's tile base
-    unsigned avoff[2];
+    unsigned avoff[NA];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NA; ++i) {
       const int c = (4 * i + wave) * 64 + lane;  // plane 0 chunk (same offsets in plane 1)
-      const int r = (c & 511) >> 2, q = (c & 3) ^ a_swz(r);
+      const int r = c >> 2, q = (c & 3) ^ a_swz(r);
       avoff[i] = (unsigned)((r * K + q * 8) * 2);
     }
     const uint8_t *xhi = reinterpret_cast<const uint8_t *>(a.X16 + (size_t)mblk * K);
@@ -419,10 +424,11 @@ __device__ __forceinline__ void gemm_dma(const GemmArgs &a) {
     for (int k = 0; k < W::WD; ++k) ldw[k] = __builtin_amdgcn_readfirstlane(lbase + wl[k]);
     auto dma = [&](int b, int stage) {
       const unsigned so = stage * STAGE;
-      dma_to_lds_s<16>(xhi + b * 64, avoff[0], lds0 + so);
-      dma_to_lds_s<16>(xhi + b * 64, avoff[1], lds0 + so + 4096);
-      dma_to_lds_s<16>(xlo + b * 64, avoff[0], lds0 + so + 8192);
-      dma_to_lds_s<16>(xlo + b * 64, avoff[1], lds0 + so + 12288);
+#pragma unroll
+      for (int i = 0; i < NA; ++i) dma_to_lds_s<16>(xhi + b * 64, avoff[i], lds0 + so + 4096 * i);
+#pragma unroll
+      for (int i = 0; i < NA; ++i)
+        dma_to_lds_s<16>(xlo + b * 64, avoff[i], lds0 + so + PS + 4096 * i);
 #pragma unroll
       for (int k = 0; k < W::WD; ++k) {
         if (wsz[k] == 16)
@@ -433,9 +439,9 @@ __device__ __forceinline__ void gemm_dma(const GemmArgs &a) {
     };
     // this lane's read offsets in a stage
     const uint8_t *rbase = &S[0];
-    int aoff[2][2];
+    int aoff[TT][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < TT; ++t)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int r = m0 + 32 * t + lr;
@@ -481,11 +487,11 @@ __device__ __forceinline__ void gemm_dma(const GemmArgs &a) {
                                   : 0.f;
         }
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < TT; ++t) {
           const half8 Ah0 = *reinterpret_cast<const half8 *>(sb + aoff[t][0]);
           const half8 Ah1 = *reinterpret_cast<const half8 *>(sb + aoff[t][1]);
-          const half8 Al0 = *reinterpret_cast<const half8 *>(sb + 128 * 64 + aoff[t][0]);
-          const half8 Al1 = *reinterpret_cast<const half8 *>(sb + 128 * 64 + aoff[t][1]);
+          const half8 Al0 = *reinterpret_cast<const half8 *>(sb + PS + aoff[t][0]);
+          const half8 Al1 = *reinterpret_cast<const half8 *>(sb + PS + aoff[t][1]);
           floatx16 xs = zero16;
           if constexpr (TYPE == PBX_Q41) {
             // the block sums of the activation rows: the product with all-ones weights
@@ -523,7 +529,7 @@ __device__ __forceinline__ void gemm_dma(const GemmArgs &a) {
   }
 
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < TT; ++t)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int n = n0 + 32 * u + lr;
@@ -550,6 +556,13 @@ extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_big(GemmArgs a) { 
 extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q8_big(GemmArgs a) { gemm_dma<PBX_Q8, 3>(a); }
 extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q41_big(GemmArgs a) { gemm_dma<PBX_Q41, 3>(a); }
 extern "C" __global__ void __launch_bounds__(256) pbx_gemm_f16_big(GemmArgs a) { gemm_dma<PBX_F16, 3>(a); }
+// 64-row M tiles: twice the workgroups of the 128-row tile for the GEMMs
+// whose 128 x 128 grid leaves CUs idle (o, q|k|v and down at a 512-token
+// prompt), without a deeper K split
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_b64(GemmArgs a) { gemm_dma<PBX_Q4, 3, 64>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q8_b64(GemmArgs a) { gemm_dma<PBX_Q8, 3, 64>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q41_b64(GemmArgs a) { gemm_dma<PBX_Q41, 3, 64>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_f16_b64(GemmArgs a) { gemm_dma<PBX_F16, 3, 64>(a); }
 
 // Row scaling to fp16: one workgroup per (padded) row.  The scale is
 // 2^(15 - e) with 2^(e-1) <= max|x| < 2^e, so every scaled value is below

@@ -162,23 +162,42 @@ int pbx_gemm_make_plan(pbx_ctx *c, const pbx_weight *w, int M, pbx_gemm_plan *p)
   // Split K so the grid has about one workgroup (big) or eight waves
   // (small) per CU.
   int KS = 1;
+  int mt_rows = 128;
+  int mtl = mtiles;
   if (big) {
-    // about one workgroup per CU: a deeper split costs more in partial
-    // traffic and per-workgroup start-up than the extra occupancy returns
-    // (measured at M = 512 against 0.5, 0.75, 1.5, 2 and 3 per CU)
+    // 128 x 128 tiles where they give two workgroups a CU (the prefill's
+    // gate|up); otherwise 64-row M tiles (pbx_gemm_<type>_b64) with the K
+    // split to two workgroups a CU (PBX_GEMM_M64 = workgroups a CU, 0: the
+    // 128-row tiles at about one a CU).  512-token prefill: 4.34 against
+    // 4.48 ms (q|k|v 37.3 -> 32.2 us, o 25 -> 22.5 us; down unchanged);
+    // three or four a CU: 4.48 and 4.67 ms.  With 128-row tiles a deeper
+    // split costs more in partial traffic and per-workgroup start-up than
+    // the extra occupancy returns (measured against 0.5, 0.75, 1.5, 2 and 3
+    // per CU).
     const int wgs = nwg * mtiles;
-    if (wgs < c->cu_count) KS = std::min({B, 8, (c->cu_count + wgs - 1) / wgs});
+    const char *e = getenv("PBX_GEMM_M64");
+    const int per_cu = e ? atoi(e) : 2;
+    if (per_cu > 0 && wgs < per_cu * c->cu_count) {
+      mt_rows = 64;
+      mtl = Mpad / 64;
+      const int w64 = nwg * mtl;
+      if (w64 < per_cu * c->cu_count)
+        KS = std::min({B, 8, (per_cu * c->cu_count + w64 - 1) / w64});
+    } else if (wgs < c->cu_count) {
+      KS = std::min({B, 8, (c->cu_count + wgs - 1) / wgs});
+    }
   } else {
     const int waves = nwg * mtiles * 4;
     if (waves < 8 * c->cu_count) KS = std::min({B, 8, (8 * c->cu_count + waves - 1) / waves});
   }
   p->M = M;
   p->Mpad = Mpad;
-  p->mtiles = mtiles;
+  p->mtiles = mtl;
   p->nwg = nwg;
   p->KS = KS;
   p->name = std::string("pbx_gemm_") + gemm_tag(w->type) +
-            (big ? std::string("_big") : "_m" + std::to_string(MT) + "_n" + std::to_string(NT));
+            (big ? std::string(mt_rows == 64 ? "_b64" : "_big")
+                 : "_m" + std::to_string(MT) + "_n" + std::to_string(NT));
   return PBX_OK;
 }
 
