@@ -73,47 +73,50 @@ pbx_rmsnorm_rows(const float *x, const float *w, float *out, int dim, float eps)
 // RoPE of q and k in place for each row t (position start + t) and append of
 // k, v to the cache (llama.js:159-191, 243-255).  qkv rows: [dim | kv | kv].
 // With part, the rows are first the sum of the KS split-K partials
-// [KS][rows][dim + 2 kv] of the q|k|v GEMM (summed in split order).
+// [KS][rows][dim + 2 kv] of the q|k|v GEMM (summed in split order).  One pass
+// over float4 columns: a column holds the pairs (2p, 2p + 1) and (2p + 2,
+// 2p + 3) of one head (head_dim is a multiple of 4), rotated as the decode
+// GEMV's epilogue rotates them (the same fused multiply-adds), then stored to
+// the row and, for k and v, to the cache.
 extern "C" __global__ void __launch_bounds__(256)
 pbx_rope_append_rows(float *qkv, float *kcache, float *vcache, const float *rope, int start,
                      int n_heads, int n_kv_heads, int head_dim, const float *part, int KS) {
   const int t = blockIdx.x, pos = start + t;
   const int dim = n_heads * head_dim, kvdim = n_kv_heads * head_dim;
   const int rl = dim + 2 * kvdim;
-  float *row = qkv + (size_t)t * rl;
-  if (part) {
-    // float4 columns (rl is a multiple of 4); all partial loads of a column
-    // are issued before the sum (KS <= 8)
-    const size_t stride4 = (size_t)gridDim.x * rl / 4;
-    const float4 *pr = reinterpret_cast<const float4 *>(part + (size_t)t * rl);
-    for (int i = threadIdx.x; i < rl / 4; i += blockDim.x) {
+  float4 *row = reinterpret_cast<float4 *>(qkv + (size_t)t * rl);
+  const float *rp = rope + (size_t)pos * head_dim;
+  // all partial loads of a column are issued before the sum (KS <= 8)
+  const size_t stride4 = (size_t)gridDim.x * rl / 4;
+  const float4 *pr = part ? reinterpret_cast<const float4 *>(part + (size_t)t * rl) : nullptr;
+  for (int i = threadIdx.x; i < rl / 4; i += blockDim.x) {
+    float4 v;
+    if (pr) {
       float4 p[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) p[k] = k < KS ? pr[k * stride4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
-      float4 v = p[0];
+      v = p[0];
 #pragma unroll
       for (int k = 1; k < 8; ++k)
         if (k < KS) {
           v.x += p[k].x; v.y += p[k].y; v.z += p[k].z; v.w += p[k].w;
         }
-      reinterpret_cast<float4 *>(row)[i] = v;
+    } else {
+      v = row[i];
     }
-    __syncthreads();
-  }
-  const float *rp = rope + (size_t)pos * head_dim;
-  const int half = head_dim / 2;
-  for (int p = threadIdx.x; p < (n_heads + n_kv_heads) * half; p += blockDim.x) {
-    const int h = p / half, i = p % half;
-    float *v = h < n_heads ? row + h * head_dim + 2 * i : row + dim + (h - n_heads) * head_dim + 2 * i;
-    const float c = rp[2 * i], s = rp[2 * i + 1];
-    const float a0 = v[0], a1 = v[1];
-    v[0] = a0 * c - a1 * s;
-    v[1] = a0 * s + a1 * c;
-  }
-  __syncthreads();
-  for (int d = threadIdx.x; d < kvdim; d += blockDim.x) {
-    kcache[(size_t)pos * kvdim + d] = row[dim + d];
-    vcache[(size_t)pos * kvdim + d] = row[dim + kvdim + d];
+    const int e = 4 * i;
+    if (e < dim + kvdim) {
+      // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c) for both pairs of the column
+      const int j = (e < dim ? e : e - dim) % head_dim;
+      const float4 cs = *reinterpret_cast<const float4 *>(rp + j);  // c, s of pair j / 2, then j / 2 + 1
+      v = make_float4(fmaf(v.x, cs.x, -v.y * cs.y), fmaf(v.x, cs.y, v.y * cs.x),
+                      fmaf(v.z, cs.z, -v.w * cs.w), fmaf(v.z, cs.w, v.w * cs.z));
+    }
+    row[i] = v;
+    if (e >= dim + kvdim)
+      *reinterpret_cast<float4 *>(vcache + (size_t)pos * kvdim + (e - dim - kvdim)) = v;
+    else if (e >= dim)
+      *reinterpret_cast<float4 *>(kcache + (size_t)pos * kvdim + (e - dim)) = v;
   }
 }
 
