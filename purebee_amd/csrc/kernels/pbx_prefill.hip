@@ -372,14 +372,17 @@ __device__ __forceinline__ void attention_mfma_body(const float *qkv, const floa
   typedef _Float16 half2t __attribute__((ext_vector_type(2)));
   typedef _Float16 half4t __attribute__((ext_vector_type(4)));
   typedef float floatx16 __attribute__((ext_vector_type(16)));
-  __shared__ __attribute__((aligned(16))) _Float16 Ksh[KG][2][FA_KT * FA_KP];
-  __shared__ __attribute__((aligned(16))) _Float16 Vsh[KG][2][64 * FA_KP];  // [dim][key]
+  // each group's stage: K hi, K lo ([key][dim]), V^T hi, V^T lo ([dim][key]);
+  // one array, so the merge below may reuse all of it
+  __shared__ __attribute__((aligned(16))) _Float16 KVsh[KG][4][FA_KT * FA_KP];
+  static_assert(64 * FA_KP == FA_KT * FA_KP, "K and V^T stages of one size");
+  static_assert(2 * (2 * KG - 1) * 64 * 34 * 4 <= KG * 4 * FA_KT * FA_KP * 2, "merge fits the stages");
   const int h = blockIdx.x, t0 = blockIdx.y * 64, hd = head_dim, hd4 = hd / 4, nc = hd / 16;
   const int group = n_heads / n_kv_heads, kvh = h / group;
   const int dim = n_heads * hd, kvdim = n_kv_heads * hd, rs = dim + 2 * kvdim;
   const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
   const int kg = KG > 1 ? (int)(threadIdx.x >> 8) : 0;  // the wave's key group
-  _Float16 *Kh = Ksh[kg][0], *Kl = Ksh[kg][1], *Vh = Vsh[kg][0], *Vl = Vsh[kg][1];
+  _Float16 *Kh = KVsh[kg][0], *Kl = KVsh[kg][1], *Vh = KVsh[kg][2], *Vl = KVsh[kg][3];
   const int qg = wave & 1, kh = wave >> 1, lq = lane & 31, hh = lane >> 5;
   const int nq = min(64, n_rows - t0);
   const int qrow = 32 * qg + lq;  // this lane's query within the tile
@@ -540,7 +543,7 @@ __device__ __forceinline__ void attention_mfma_body(const float *qkv, const floa
   // merge the 2 KG key slices of each query group (key halves x groups):
   // every slice but (kh 0, group 0) hands its state over through LDS
   __syncthreads();
-  float *mg = reinterpret_cast<float *>(&Ksh[0][0][0]);  // [qg][slice - 1][lane][34]: acc, m, l
+  float *mg = reinterpret_cast<float *>(&KVsh[0][0][0]);  // [qg][slice - 1][lane][34]: acc, m, l
   const int slice = 2 * kg + kh;
   if (slice > 0) {
     float *mine = mg + ((qg * (2 * KG - 1) + slice - 1) * 64 + lane) * 34;
