@@ -15,6 +15,18 @@ from tests.e2e_util import LOGIT_TOL, check_greedy, make_pair
 
 pytestmark = pytest.mark.gpu
 
+# Switches that select other decode kernels at model creation; the tests
+# that check which kernels a step launches clear them first, so they hold
+# whatever the caller's environment selects.
+PATH_SWITCHES = ("PBX_FFN", "PBX_QKV_ATTN", "PBX_ATTN_O", "PBX_GEMV_INT", "PBX_SMALL_STEP")
+
+
+@pytest.fixture
+def default_paths(monkeypatch):
+    for k in PATH_SWITCHES:
+        monkeypatch.delenv(k, raising=False)
+    return monkeypatch
+
 
 def tiny(weight_type, embed_type, **kw):
     cfg = dict(dim=256, hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=1000,
@@ -182,7 +194,7 @@ def test_attention_kernels_match_one_workgroup_per_head(ctx, monkeypatch, mode, 
 
 
 @pytest.mark.parametrize("ipt,qa", [(1, True), (2, True), (1, False), (2, False), (4, False)])
-def test_fused_attention_o_matches_separate_o(ctx, monkeypatch, ipt, qa):
+def test_fused_attention_o_matches_separate_o(ctx, default_paths, ipt, qa):
     """Decode with the o projection fused into the cached head attention
     (workgroup (head, part) adds W_o[rows, head] o_h for its 256 * ipt rows
     into a 64-bit 2^-32 fixed-point update; the gate|up GEMV adds the update
@@ -192,6 +204,7 @@ def test_fused_attention_o_matches_separate_o(ctx, monkeypatch, ipt, qa):
     slots) on two layers.  qa: the q|k|v GEMV in the same launch
     (pbx_qkvr_attn_o_c1: the attention workgroups wait for the GEMV's
     epoch-tagged q, k and v cells of their head)."""
+    monkeypatch = default_paths
     print(f"[case] fused attention + o, ipt {ipt}, q|k|v in the launch {qa}, 2048/8192, "
           f"32/8 heads, 100 positions", flush=True)
     cfg = tiny(TYPE_Q4_0, TYPE_Q4_0, dim=2048, hidden_dim=8192, n_layers=2, n_heads=32,
@@ -227,7 +240,7 @@ def test_fused_attention_o_matches_separate_o(ctx, monkeypatch, ipt, qa):
     ref.close()
 
 
-def test_fused_qkv_attention_long_context(ctx, monkeypatch):
+def test_fused_qkv_attention_long_context(ctx, default_paths):
     """The q|k|v GEMV and the attention + o projection in one launch past
     512 cached positions, where the newest position falls in the
     attention's second 512-position chunk (its k and v come from the
@@ -235,6 +248,7 @@ def test_fused_qkv_attention_long_context(ctx, monkeypatch):
     then 12 decode steps, against the same model launching the two kernels
     separately, and the greedy tokens of 13 on-device steps (an 8-step and a
     4-step graph launch, then one step) against it."""
+    monkeypatch = default_paths
     print("[case] q|k|v + attention in one launch, 1 layer, positions 520..531", flush=True)
     cfg = tiny(TYPE_Q4_0, TYPE_Q4_0, dim=2048, hidden_dim=8192, n_layers=1, n_heads=32,
                n_kv_heads=8, vocab_size=512, max_seq=1024)
@@ -314,7 +328,7 @@ def test_non_finite_activation_propagates(ctx):
         ref.close()
 
 
-def test_handoff_wait_timeout_is_reported(ctx):
+def test_handoff_wait_timeout_is_reported(ctx, default_paths):
     """The bounded wait of the joined q|k|v + attention launch: when the
     cells it waits for never carry its tag (forced from the host by the test
     hook, which offsets the tag the attention workgroups expect and caps
@@ -351,7 +365,7 @@ def test_handoff_wait_timeout_is_reported(ctx):
     model.free()
 
 
-def test_small_step_matches_per_layer_launches(ctx, monkeypatch):
+def test_small_step_matches_per_layer_launches(ctx, default_paths):
     """Small Q8_0 models run every layer of a decode step in one launch
     (pbx_small_step_q8: the phases of a layer hand their outputs on through
     tagged cells).  stories15M-shaped, after a 16-token prompt: the step's
@@ -360,6 +374,7 @@ def test_small_step_matches_per_layer_launches(ctx, monkeypatch):
     and the last step's logits agree within 5e-4 (the dot products are summed
     in another order); a forward through the first 3 layers
     (llama-streaming.js maxLayers) agrees as well."""
+    monkeypatch = default_paths
     print("[case] stories15m small-step launch vs per-layer launches", flush=True)
     cfg = synth.CONFIGS["stories15m"]
     small = synth.build(ctx, cfg, 1300)
@@ -389,7 +404,7 @@ def test_small_step_matches_per_layer_launches(ctx, monkeypatch):
     per.free()
 
 
-def test_small_step_wait_timeout_is_reported(ctx):
+def test_small_step_wait_timeout_is_reported(ctx, default_paths):
     """The bounded waits of the small-model step: with the test hook skewing
     the tag that layer 1's waits expect (64 polls each), every workgroup still
     finishes and forward and generate fail with PBX_ETIMEOUT; a forward
