@@ -805,7 +805,9 @@ def run_matvec(args, pb, synth):
     return {"metric": METRIC, "value": round(1e3 / ms_per_step, 2), "unit": "tok/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "q4_0 weights; fp32 activations and accumulation",
+            "dtype": "q4_0 weights (int4 codes, fp16 block scales); each 32-element block of "
+                     "the input rounded to 22-bit fixed point (three int8 limbs, exact int32 "
+                     "dots); fp32 block combine and accumulation",
             "data": "synthetic: seeded N(0,0.02) weights quantised to Q4_0",
             "config": {"workload": "llama-3.2-1b-shaped q4_0 decode matvec pass only",
                        "bytes_per_step": step_bytes, "device": dev},
