@@ -377,8 +377,13 @@ extern "C" __global__ void __launch_bounds__(256) pbx_attention_decode(AttnArgs 
   float4 vp[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    // unconditional load from a clamped row (row 0 is always in the cache),
+    // the zero selected after it: a conditional load becomes a flat load of
+    // a selected address
     const int j = g + i * G;
-    vp[i] = (g < G && j < pos) ? vb[(size_t)j * stride4] : zero4;
+    const bool ok = g < G && j < pos;
+    const float4 t = vb[(size_t)(ok ? j : 0) * stride4];
+    vp[i] = ok ? t : zero4;
   }
   __syncthreads();
   float m = -INFINITY;
@@ -425,7 +430,8 @@ extern "C" __global__ void __launch_bounds__(256) pbx_attention_decode(AttnArgs 
       acc.z = fmaf(p3, v3.z, acc.z); acc.w = fmaf(p3, v3.w, acc.w);
     }
     for (; j < L; j += G) {
-      const float4 vv = (j < pos) ? vb[(size_t)j * stride4] : vnew;
+      const float4 t = vb[(size_t)(j < pos ? j : 0) * stride4];
+      const float4 vv = j < pos ? t : vnew;
       const float p = sc[j];
       acc.x = fmaf(p, vv.x, acc.x); acc.y = fmaf(p, vv.y, acc.y);
       acc.z = fmaf(p, vv.z, acc.z); acc.w = fmaf(p, vv.w, acc.w);
@@ -1248,10 +1254,10 @@ __device__ __forceinline__ SmSlot sm_load(const uint8_t *qs, const uint16_t *dsc
   const int tt = ok ? t : 0;
   const int r = row_of(tt / B), b = tt % B;
   SmSlot s;
-  const uint8_t *src = qs + ((size_t)r * B + b) * 32;
-  s.a = ld_stream(src);
-  s.b = ld_stream(src + 16);
-  s.d = dsc[dsc_index(r, b, B)] & (ok ? 0xFFFFu : 0u);
+  const uint8_t *src = qs + ((size_t)r * B + b) * 32;  // from the layer table: global loads
+  s.a = ld_stream_g(src);
+  s.b = ld_stream_g(src + 16);
+  s.d = *gmem(dsc + dsc_index(r, b, B)) & (ok ? 0xFFFFu : 0u);
   return s;
 }
 
@@ -1409,7 +1415,7 @@ extern "C" __global__ void __launch_bounds__(PBX_SM_T) pbx_small_step_q8(SmallAr
                       [&](int r) { return min(q0 + r, qr - 1); });
     float nw[2];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) nw[k] = L.attn_norm[min(tid + PBX_SM_T * k, dim - 1)];
+    for (int k = 0; k < 2; ++k) nw[k] = *gmem(L.attn_norm + min(tid + PBX_SM_T * k, dim - 1));
     float xv[2];
     if (l == 0) {
 #pragma unroll
@@ -1469,7 +1475,7 @@ extern "C" __global__ void __launch_bounds__(PBX_SM_T) pbx_small_step_q8(SmallAr
       sd[i] = sm_load(L.d_qs, L.d_d, BH, nd * BH, tid + PBX_SM_T * i,
                       [&](int r) { return min(d0 + r, dim - 1); });
 #pragma unroll
-    for (int k = 0; k < 2; ++k) nw[k] = L.ffn_norm[min(tid + PBX_SM_T * k, dim - 1)];
+    for (int k = 0; k < 2; ++k) nw[k] = *gmem(L.ffn_norm + min(tid + PBX_SM_T * k, dim - 1));
     sm_poll(co, dim, want, spin, status, xv);
     sm_store(xv, dim, act);
     sm_dots(so, B, no * B, act, part);

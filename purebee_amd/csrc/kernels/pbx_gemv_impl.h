@@ -100,6 +100,20 @@ __device__ __forceinline__ uint4 ld_stream(const void *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// A pointer the compiler cannot place (one read from memory, not a kernel
+// argument) as a global-memory pointer: loads through it are global loads.
+// Through the generic pointer they are flat loads, which also count against
+// the LDS wait counter, so every LDS wait after them waits for their data.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T *gmem(const T *p) {
+  return (const __attribute__((address_space(1))) T *)p;
+}
+
+__device__ __forceinline__ uint4 ld_stream_g(const void *p) {
+  const u32x4_t v = __builtin_nontemporal_load(gmem(reinterpret_cast<const u32x4_t *>(p)));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Scale plane: 4-row groups, [Npad/4][B][4] fp16, so the scales of 4
 // consecutive rows at one block are one 8-byte load and a tile of >= 4 rows
 // uses whole cache lines.

@@ -420,20 +420,31 @@ __device__ __forceinline__ void attention_mfma_body(const float *qkv, const floa
   // p = (tid + 256 i) / hd4 (< 32 key pairs), same column
   float4 kreg[4], vreg0[2], vreg1[2];
   const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  // Loads are unconditional from clamped addresses (key k0 is always in
+  // the cache), the zeros selected afterwards: a load under the condition
+  // compiles to a flat load from a selected address, the other choice a
+  // zero on the stack.
   auto load_stage = [&](int k0) {
     const int nk = min(FA_KT, last_key + 1 - k0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int it = tid + 256 * i, key = it / hd4, c4 = 4 * (it % hd4);
-      kreg[i] = (it < FA_KT * hd4 && key < nk)
-                    ? *reinterpret_cast<const float4 *>(kb + (size_t)(k0 + key) * kvdim + c4) : z4;
+      const bool ok = it < FA_KT * hd4 && key < nk;
+      const float4 v =
+          *reinterpret_cast<const float4 *>(kb + (size_t)(k0 + (ok ? key : 0)) * kvdim + (ok ? c4 : 0));
+      kreg[i] = ok ? v : z4;
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int it = tid + 256 * i, kp = 2 * (it / hd4), c4 = 4 * (it % hd4);
       const bool ok = it < (FA_KT / 2) * hd4;
-      vreg0[i] = ok && kp < nk ? *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + kp) * kvdim + c4) : z4;
-      vreg1[i] = ok && kp + 1 < nk ? *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + kp + 1) * kvdim + c4) : z4;
+      const bool ok0 = ok && kp < nk, ok1 = ok && kp + 1 < nk;
+      const float4 v0 =
+          *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + (ok0 ? kp : 0)) * kvdim + (ok0 ? c4 : 0));
+      const float4 v1 =
+          *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + (ok1 ? kp + 1 : 0)) * kvdim + (ok1 ? c4 : 0));
+      vreg0[i] = ok0 ? v0 : z4;
+      vreg1[i] = ok1 ? v1 : z4;
     }
   };
   if (kg * FA_KT <= last_key) load_stage(kg * FA_KT);
