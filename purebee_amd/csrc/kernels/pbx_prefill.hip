@@ -421,30 +421,34 @@ __device__ __forceinline__ void attention_mfma_body(const float *qkv, const floa
   float4 kreg[4], vreg0[2], vreg1[2];
   const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
   // Loads are unconditional from clamped addresses (key k0 is always in
-  // the cache), the zeros selected afterwards: a load under the condition
-  // compiles to a flat load from a selected address, the other choice a
-  // zero on the stack.
-  auto load_stage = [&](int k0) {
+  // the cache) and nothing reads the registers until the stage is stored
+  // to LDS, where the keys past the stage's end become zeros: a condition
+  // on the load (or a select right after it) makes the compiler wait for
+  // the data at once, and the next stage's loads no longer overlap this
+  // stage's arithmetic.
+  auto kv_ok = [&](int k0, int i, int which) -> bool {  // which: 0 K, 1 V row kp, 2 V row kp + 1
     const int nk = min(FA_KT, last_key + 1 - k0);
+    const int it = tid + 256 * i;
+    if (which == 0) return it < FA_KT * hd4 && it / hd4 < nk;
+    const int kp = 2 * (it / hd4) + (which - 1);
+    return it < (FA_KT / 2) * hd4 && kp < nk;
+  };
+  auto load_stage = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int it = tid + 256 * i, key = it / hd4, c4 = 4 * (it % hd4);
-      const bool ok = it < FA_KT * hd4 && key < nk;
-      const float4 v =
+      const bool ok = kv_ok(k0, i, 0);
+      kreg[i] =
           *reinterpret_cast<const float4 *>(kb + (size_t)(k0 + (ok ? key : 0)) * kvdim + (ok ? c4 : 0));
-      kreg[i] = ok ? v : z4;
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int it = tid + 256 * i, kp = 2 * (it / hd4), c4 = 4 * (it % hd4);
-      const bool ok = it < (FA_KT / 2) * hd4;
-      const bool ok0 = ok && kp < nk, ok1 = ok && kp + 1 < nk;
-      const float4 v0 =
+      const bool ok0 = kv_ok(k0, i, 1), ok1 = kv_ok(k0, i, 2);
+      vreg0[i] =
           *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + (ok0 ? kp : 0)) * kvdim + (ok0 ? c4 : 0));
-      const float4 v1 =
+      vreg1[i] =
           *reinterpret_cast<const float4 *>(vb + (size_t)(k0 + (ok1 ? kp + 1 : 0)) * kvdim + (ok1 ? c4 : 0));
-      vreg0[i] = ok0 ? v0 : z4;
-      vreg1[i] = ok1 ? v1 : z4;
     }
   };
   if (kg * FA_KT <= last_key) load_stage(kg * FA_KT);
@@ -456,7 +460,7 @@ __device__ __forceinline__ void attention_mfma_body(const float *qkv, const floa
     for (int i = 0; i < 4; ++i) {
       const int it = tid + 256 * i, key = it / hd4, c4 = 4 * (it % hd4);
       if (live && it < FA_KT * hd4) {
-        const float4 v = kreg[i];
+        const float4 v = kv_ok(k0, i, 0) ? kreg[i] : z4;
         half4t hv, lv;
         SPLIT_F16(v.x, hv[0], lv[0]);
         SPLIT_F16(v.y, hv[1], lv[1]);
@@ -470,7 +474,7 @@ __device__ __forceinline__ void attention_mfma_body(const float *qkv, const floa
     for (int i = 0; i < 2; ++i) {
       const int it = tid + 256 * i, kp = 2 * (it / hd4), c4 = 4 * (it % hd4);
       if (live && it < (FA_KT / 2) * hd4) {
-        const float4 v0 = vreg0[i], v1 = vreg1[i];
+        const float4 v0 = kv_ok(k0, i, 1) ? vreg0[i] : z4, v1 = kv_ok(k0, i, 2) ? vreg1[i] : z4;
 #define FA_PUTV(e, x0, x1)                                                  \
   do {                                                                      \
     half2t hv_, lv_;                                                        \
