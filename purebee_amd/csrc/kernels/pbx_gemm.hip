@@ -332,7 +332,14 @@ template <int TYPE> struct DmaW {
   static constexpr int WD = TYPE == PBX_Q8 || TYPE == PBX_F16 ? 2 : 1;      // weight DMAs a wave
 };
 
-template <int TYPE, int NS, int MT = 128>
+// SW: the gate|up weight of a Llama FFN (N / 2 gate rows, then N / 2 up
+// rows), with silu(gate) * up in the epilogue.  Workgroup x takes hidden
+// columns [64 x, 64 x + 64): tile rows 0-31 are their first 32 gate rows,
+// 32-63 the matching up rows, 64-127 the same for the next 32 columns, so a
+// wave's two 32-column subtiles (u = 0, 1) hold a gate and its up for one
+// lane's column; Y is [M][N / 2].  Needs N / 2 a multiple of 64 and no K
+// split.
+template <int TYPE, int NS, int MT = 128, bool SW = false>
 __device__ __forceinline__ void gemm_dma(const GemmArgs &a) {
   static_assert(MT == 128 || MT == 64, "M tile");
   typedef DmaW<TYPE> W;
@@ -386,19 +393,37 @@ __device__ __forceinline__ void gemm_dma(const GemmArgs &a) {
     unsigned wv[2], wl[2];
     int wstep[2], wsz[2];
     const size_t rowbytes = (size_t)a.B * W::CB;
+    // SW: the weight row of tile row i (the gate or up rows of the
+    // workgroup's hidden columns; relative to row 0)
+    auto sw_row = [&](int i) -> int {
+      const int c = i >> 5;
+      return ((c & 1) ? a.N / 2 : 0) + blockIdx.x * 64 + 32 * (c >> 1) + (i & 31);
+    };
     auto code_dma = [&](int k, int d) {
       const int per_row = W::CB / 16;
-      const int n = min(blockIdx.x * 128 + (1024 / W::CB) * d + lane / per_row, a.Npad - 1) - blockIdx.x * 128;
-      wb[k] = a.qs + (size_t)blockIdx.x * 128 * rowbytes;
-      wv[k] = (unsigned)(n * rowbytes + (lane % per_row) * 16);
+      const int i = (1024 / W::CB) * d + lane / per_row;  // tile row
+      if constexpr (SW) {
+        wb[k] = a.qs;
+        wv[k] = (unsigned)((size_t)sw_row(i) * rowbytes + (lane % per_row) * 16);
+      } else {
+        const int n = min(blockIdx.x * 128 + i, a.Npad - 1) - blockIdx.x * 128;
+        wb[k] = a.qs + (size_t)blockIdx.x * 128 * rowbytes;
+        wv[k] = (unsigned)(n * rowbytes + (lane % per_row) * 16);
+      }
       wl[k] = ASTAGE + d * 1024;
       wstep[k] = W::CB;
       wsz[k] = 16;
     };
     auto plane_dma = [&](int k, const uint16_t *plane, int which) {
-      const int g = min(blockIdx.x * 32 + (lane >> 1), a.Npad / 4 - 1) - blockIdx.x * 32;
-      wb[k] = reinterpret_cast<const uint8_t *>(plane) + (size_t)blockIdx.x * 32 * a.B * 8;
-      wv[k] = (unsigned)(g * a.B * 8 + (lane & 1) * 4);
+      if constexpr (SW) {
+        // four-row group lane >> 1 of the tile: four consecutive weight rows
+        wb[k] = reinterpret_cast<const uint8_t *>(plane);
+        wv[k] = (unsigned)((size_t)(sw_row(4 * (lane >> 1)) >> 2) * a.B * 8 + (lane & 1) * 4);
+      } else {
+        const int g = min(blockIdx.x * 32 + (lane >> 1), a.Npad / 4 - 1) - blockIdx.x * 32;
+        wb[k] = reinterpret_cast<const uint8_t *>(plane) + (size_t)blockIdx.x * 32 * a.B * 8;
+        wv[k] = (unsigned)(g * a.B * 8 + (lane & 1) * 4);
+      }
       wl[k] = ASTAGE + W::CODES + 256 * which;
       wstep[k] = 8;
       wsz[k] = 4;
@@ -528,6 +553,20 @@ __device__ __forceinline__ void gemm_dma(const GemmArgs &a) {
     wait_vm<0>();
   }
 
+  if constexpr (SW) {
+    const int NO = a.N / 2, c = blockIdx.x * 64 + 32 * wn + lr;  // the lane's hidden column
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = mblk + m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (m < a.M) {
+          const float iv = a.inv[m];
+          a.Y[(size_t)m * NO + c] = silu(acc[t][0][r] * iv) * (acc[t][1][r] * iv);
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < TT; ++t)
 #pragma unroll
@@ -563,6 +602,15 @@ extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_b64(GemmArgs a) { 
 extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q8_b64(GemmArgs a) { gemm_dma<PBX_Q8, 3, 64>(a); }
 extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q41_b64(GemmArgs a) { gemm_dma<PBX_Q41, 3, 64>(a); }
 extern "C" __global__ void __launch_bounds__(256) pbx_gemm_f16_b64(GemmArgs a) { gemm_dma<PBX_F16, 3, 64>(a); }
+// gate|up with silu(gate) * up in the epilogue (no K split; Y is [M][N / 2])
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_big_sw(GemmArgs a) { gemm_dma<PBX_Q4, 3, 128, true>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q8_big_sw(GemmArgs a) { gemm_dma<PBX_Q8, 3, 128, true>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q41_big_sw(GemmArgs a) { gemm_dma<PBX_Q41, 3, 128, true>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_f16_big_sw(GemmArgs a) { gemm_dma<PBX_F16, 3, 128, true>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q4_b64_sw(GemmArgs a) { gemm_dma<PBX_Q4, 3, 64, true>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q8_b64_sw(GemmArgs a) { gemm_dma<PBX_Q8, 3, 64, true>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_q41_b64_sw(GemmArgs a) { gemm_dma<PBX_Q41, 3, 64, true>(a); }
+extern "C" __global__ void __launch_bounds__(256) pbx_gemm_f16_b64_sw(GemmArgs a) { gemm_dma<PBX_F16, 3, 64, true>(a); }
 
 // Row scaling to fp16: one workgroup per (padded) row.  The scale is
 // 2^(15 - e) with 2^(e-1) <= max|x| < 2^e, so every scaled value is below

@@ -135,7 +135,7 @@ int launch_f32(pbx_ctx *c, const pbx_weight *w, const float *dX, int M, const fl
 
 }  // namespace
 
-int pbx_gemm_make_plan(pbx_ctx *c, const pbx_weight *w, int M, pbx_gemm_plan *p) {
+int pbx_gemm_make_plan(pbx_ctx *c, const pbx_weight *w, int M, pbx_gemm_plan *p, bool swiglu) {
   if (!gemm_tag(w->type) || w->type == PBX_TYPE_F32)
     return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: weight type %d has no fp16 MFMA path", w->type);
   if (M <= 0 || M > 65535) return pbx_fail(c, PBX_ENOTSUP, "pbx_gemm: M=%d out of range", M);
@@ -195,9 +195,17 @@ int pbx_gemm_make_plan(pbx_ctx *c, const pbx_weight *w, int M, pbx_gemm_plan *p)
   p->mtiles = mtl;
   p->nwg = nwg;
   p->KS = KS;
+  // gate|up with silu(gate) * up in the epilogue (M > 32 kernels, no K
+  // split, 64 hidden columns a workgroup, 32-bit weight offsets);
+  // PBX_GEMM_SWIGLU=0 keeps gate and up side by side
+  const char *sw_env = getenv("PBX_GEMM_SWIGLU");
+  p->swiglu = swiglu && big && KS == 1 && N % 128 == 0 &&
+              (double)N * pbx_type_row_bytes(w->type, w->K) < 4294967296.0 &&
+              !(sw_env && sw_env[0] == '0');
   p->name = std::string("pbx_gemm_") + gemm_tag(w->type) +
             (big ? std::string(mt_rows == 64 ? "_b64" : "_big")
-                 : "_m" + std::to_string(MT) + "_n" + std::to_string(NT));
+                 : "_m" + std::to_string(MT) + "_n" + std::to_string(NT)) +
+            (p->swiglu ? "_sw" : "");
   return PBX_OK;
 }
 

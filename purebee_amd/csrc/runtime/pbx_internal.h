@@ -177,8 +177,13 @@ int pbx_scratch_lookup(pbx_ctx *c);
 struct pbx_gemm_plan {
   int M = 0, Mpad = 0, mtiles = 0, nwg = 0, KS = 1;
   std::string name;
+  bool swiglu = false;  // the kernel stores silu(gate) * up: Y is [M][N / 2]
 };
-int pbx_gemm_make_plan(pbx_ctx *c, const pbx_weight *w, int M, pbx_gemm_plan *p);
+// swiglu: w is a gate|up weight (N / 2 gate rows, then the up rows) and the
+// caller takes silu(gate) * up where the shape allows it (p->swiglu says
+// whether it does; otherwise Y holds gate and up side by side)
+int pbx_gemm_make_plan(pbx_ctx *c, const pbx_weight *w, int M, pbx_gemm_plan *p,
+                       bool swiglu = false);
 int pbx_gemm_run(pbx_ctx *c, const pbx_weight *w, const pbx_gemm_plan &p, const void *x16,
                  const void *x16lo, const float *inv, const float *dBias, float *out,
                  int accumulate, hipStream_t stream);

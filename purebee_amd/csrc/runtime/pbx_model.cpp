@@ -1743,7 +1743,8 @@ static int fused_plans(pbx_model *m, int n, FusedPlans *P) {
   const Layer &L = m->layers[0];
   int rc;
   if ((rc = pbx_gemm_make_plan(c, L.wqkv, n, &P->qkv)) || (rc = pbx_gemm_make_plan(c, L.wo, n, &P->o)) ||
-      (rc = pbx_gemm_make_plan(c, L.wgu, n, &P->gu)) || (rc = pbx_gemm_make_plan(c, L.wd, n, &P->d)))
+      (rc = pbx_gemm_make_plan(c, L.wgu, n, &P->gu, true)) ||
+      (rc = pbx_gemm_make_plan(c, L.wd, n, &P->d)))
     return rc;
   const pbx_model_config &g = m->cfg;
   const size_t kmax = std::max(g.dim, g.hidden_dim);
@@ -1894,12 +1895,16 @@ static int batch_layers(pbx_model *m, const int32_t *tokens, int n, int start, i
         return rc;
       if (P.gu.KS > 1 && (rc = fused_reduce(m, P.gu, (int)L.wgu->N, m->bgu, false))) return rc;
       {
+        // the down GEMM's input: silu(gate) * up, from the gate|up GEMM's
+        // epilogue ([n][hidden]) or computed here from gate and up
         float *gu = m->bgu;
         void *x16 = m->g16, *x16lo = m->g16lo;
         float *inv = m->ginv;
         int M = n, hidden = g.hidden_dim;
         void *args[] = {&gu, &x16, &x16lo, &inv, &M, &hidden};
-        if ((rc = launch_k(m, "pbx_gemm_prep_swiglu", dim3(P.gu.Mpad), dim3(256), args))) return rc;
+        if ((rc = launch_k(m, P.gu.swiglu ? "pbx_gemm_prep_x" : "pbx_gemm_prep_swiglu",
+                           dim3(P.gu.Mpad), dim3(256), args)))
+          return rc;
       }
       if ((rc = fused_gemm(m, L.wd, P.d, m->bx, true)) ||
           (rc = fused_residual_norm(m, &P.d, n, P.d.Mpad, m->bx,

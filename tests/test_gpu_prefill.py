@@ -15,8 +15,8 @@ import pytest
 
 import oracle
 from purebee_amd import PbxError, synth
-from purebee_amd.native import (TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, self_speculative_generate,
-                                speculative_generate)
+from purebee_amd.native import (TYPE_F16, TYPE_F32, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q8_0,
+                                self_speculative_generate, speculative_generate)
 from tests.e2e_util import LOGIT_TOL, make_pair
 
 pytestmark = pytest.mark.gpu
@@ -534,3 +534,29 @@ def test_speculative_errors(ctx):
         a.forward_batch([1, 2], cfg["max_seq"] - 1)
     a.free()
     b.free()
+
+
+@pytest.mark.parametrize("wt", [TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_1, TYPE_F16])
+@pytest.mark.parametrize("n", [256, 512])
+def test_gate_up_swiglu_epilogue(ctx, monkeypatch, wt, n):
+    """The batched forward's gate|up GEMM with silu(gate) * up in its epilogue
+    (hidden 8192: 64-row tiles at 256 rows, 128-row tiles at 512, no K split)
+    gives bit-identical logits to the same GEMM storing gate and up for the
+    separate SwiGLU pass (PBX_GEMM_SWIGLU=0), and the oracle's logits within
+    the usual tolerance (llama.js:326-336)."""
+    cfg = dict(dim=512, hidden_dim=8192, n_layers=1, n_heads=8, n_kv_heads=2, vocab_size=512,
+               max_seq=n + 8, weight_type=wt, embed_type=TYPE_Q8_0, rope_theta=500000.0)
+    print(f"[case] swiglu epilogue wt={wt} n={n}", flush=True)
+    model, ref, cfg = make_pair(ctx, cfg, 7000 + wt)
+    prompt = [int(t) for t in synth.random_tokens(7100 + n, n, cfg["vocab_size"])]
+    monkeypatch.delenv("PBX_GEMM_SWIGLU", raising=False)
+    l_sw, _ = model.forward(prompt, 0)
+    monkeypatch.setenv("PBX_GEMM_SWIGLU", "0")
+    model.reset_cache()
+    l_sep, _ = model.forward(prompt, 0)
+    assert np.array_equal(l_sw, l_sep)
+    err = float(np.abs(l_sw - ref.forward(prompt, 0)).max())
+    print(f"  bit-identical to the separate pass; oracle max-abs {err:.2e}", flush=True)
+    assert err <= LOGIT_TOL
+    model.free()
+    ref.close()
