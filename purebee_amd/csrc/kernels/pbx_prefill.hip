@@ -346,7 +346,11 @@ pbx_attention_tiled(const float *qkv, const float *kcache, const float *vcache, 
 // (stored [dim][key] in LDS) follows.  The two key halves of a query group
 // merge their running max, sum and output through LDS at the end.
 #define FA_KT 64           // keys per LDS stage
-#define FA_KP (64 + 8)     // halves per K row (dims) and per V^T row (keys)
+#define FA_KP (64 + 8)     // halves per K row (dims)
+// halves per V^T row (keys): the stage writes rows 4 apart from 16 threads,
+// which a 72-half row puts on 4 bank groups and a 68-half row on 8 (still
+// 8-byte aligned for the operand reads, which stay conflict-free)
+#define FA_VP (64 + 4)
 
 // hi = fp16(x), lo = fp16(x - hi), assigned to H and L (vector elements allowed)
 #define SPLIT_F16(x, H, L)                       \
@@ -375,7 +379,7 @@ __device__ __forceinline__ void attention_mfma_body(const float *qkv, const floa
   // each group's stage: K hi, K lo ([key][dim]), V^T hi, V^T lo ([dim][key]);
   // one array, so the merge below may reuse all of it
   __shared__ __attribute__((aligned(16))) _Float16 KVsh[KG][4][FA_KT * FA_KP];
-  static_assert(64 * FA_KP == FA_KT * FA_KP, "K and V^T stages of one size");
+  static_assert(64 * FA_VP <= FA_KT * FA_KP, "the V^T stage fits a K stage's space");
   static_assert(2 * (2 * KG - 1) * 64 * 34 * 4 <= KG * 4 * FA_KT * FA_KP * 2, "merge fits the stages");
   const int h = blockIdx.x, t0 = blockIdx.y * 64, hd = head_dim, hd4 = hd / 4, nc = hd / 16;
   const int group = n_heads / n_kv_heads, kvh = h / group;
@@ -480,8 +484,8 @@ __device__ __forceinline__ void attention_mfma_body(const float *qkv, const floa
     half2t hv_, lv_;                                                        \
     SPLIT_F16(x0, hv_[0], lv_[0]);                                          \
     SPLIT_F16(x1, hv_[1], lv_[1]);                                          \
-    *reinterpret_cast<half2t *>(&Vh[(c4 + (e)) * FA_KP + kp]) = hv_;        \
-    *reinterpret_cast<half2t *>(&Vl[(c4 + (e)) * FA_KP + kp]) = lv_;        \
+    *reinterpret_cast<half2t *>(&Vh[(c4 + (e)) * FA_VP + kp]) = hv_;        \
+    *reinterpret_cast<half2t *>(&Vl[(c4 + (e)) * FA_VP + kp]) = lv_;        \
   } while (0)
         FA_PUTV(0, v0.x, v1.x);
         FA_PUTV(1, v0.y, v1.y);
@@ -534,7 +538,7 @@ __device__ __forceinline__ void attention_mfma_body(const float *qkv, const floa
     for (int dt = 0; dt < 2; ++dt) {
       if (32 * dt < hd) {
         acc[dt] *= f;
-        const int vr = (32 * dt + lq) * FA_KP + 32 * kh + 4 * hh;  // V^T row (dim), key base
+        const int vr = (32 * dt + lq) * FA_VP + 32 * kh + 4 * hh;  // V^T row (dim), key base
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
           half8 ah, al;
