@@ -537,10 +537,11 @@ def test_speculative_errors(ctx):
 
 
 @pytest.mark.parametrize("wt", [TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_1, TYPE_F16])
-@pytest.mark.parametrize("n", [256, 512])
+@pytest.mark.parametrize("n", [256, 300, 512])
 def test_gate_up_swiglu_epilogue(ctx, monkeypatch, wt, n):
     """The batched forward's gate|up GEMM with silu(gate) * up in its epilogue
-    (hidden 8192: 64-row tiles at 256 rows, 128-row tiles at 512, no K split)
+    (hidden 8192: 64-row tiles at 256 and 300 rows -- the last tile partly
+    padding --, 128-row tiles at 512, no K split)
     gives bit-identical logits to the same GEMM storing gate and up for the
     separate SwiGLU pass (PBX_GEMM_SWIGLU=0), and the oracle's logits within
     the usual tolerance (llama.js:326-336)."""
